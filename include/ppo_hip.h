@@ -1,0 +1,268 @@
+/*
+ * ppo_hip.h -- C ABI of the MI355X (gfx950) PPO update library (libppo_hip.so).
+ *
+ * Every entry point takes caller-owned DEVICE pointers, int64 sizes and a HIP stream (hipStream_t passed as an
+ * opaque pointer; NULL = the default stream), enqueues its kernels on that stream and returns without
+ * synchronising.  Return value: PPO_OK (0) or a negative status; ppo_last_error() then describes the failure
+ * (thread-local).  No entry point allocates device memory: scratch space is passed in by the caller, sized by the
+ * matching *_workspace_bytes() query.  All arithmetic is fp32 with fp64 accumulators where a reduction spans rows.
+ *
+ * The comment above each entry point names the upstream rsl_rl v5.5.2 code (file:line) whose arithmetic it
+ * replaces; the host side that calls these mirrors rsl_rl's PPO / RolloutStorage / MLPModel interface.
+ */
+#ifndef PPO_HIP_H_
+#define PPO_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ppo_stream_t; /* a hipStream_t */
+
+enum {
+  PPO_OK = 0,
+  PPO_EINVAL = -1,       /* bad argument: null pointer, negative or inconsistent size, workspace too small */
+  PPO_EHIP = -2,         /* the HIP runtime reported an error (launch failure, ...) */
+  PPO_EUNSUPPORTED = -3, /* shape or option outside what the kernels implement */
+};
+
+enum { PPO_ACT_NONE = 0, PPO_ACT_ELU = 1 };
+enum { PPO_STD_SCALAR = 0, PPO_STD_LOG = 1 };
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* ppo_last_error(void);
+/* ABI version of this header (bumped on any layout change of the structs below). */
+int ppo_abi_version(void);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * A1  GAE reverse-time scan.  Replaces the loop of rsl_rl/algorithms/ppo.py:175-188 (PPO.compute_returns).
+ * rewards, values, returns, advantages: [T, N] fp32 (time-major, row t*N+n); dones: [T, N] uint8;
+ * last_values: [N].  For t = T-1..0, in upstream's fp32 operation order (no contraction):
+ *   nt = 1 - done[t];  delta = (r[t] + (nt*gamma)*V[t+1]) - V[t];  adv = delta + ((nt*gamma)*lam)*adv;
+ *   ret[t] = adv + V[t]   (V[T] = last_values, adv starts at 0);   advantages = ret - V  (ppo.py:188).
+ * ------------------------------------------------------------------------------------------------------------------ */
+int ppo_gae(const float* rewards, const float* values, const uint8_t* dones, const float* last_values,
+            float* returns, float* advantages, int64_t num_steps, int64_t num_envs, float gamma, float lam,
+            ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * A2  Advantage normalisation.  Replaces rsl_rl/algorithms/ppo.py:189-191 (global) and :213-216 (per mini-batch):
+ *   out[i*out_stride] = (x[i*in_stride] - mean(x)) / (std_unbiased(x) + eps),  i < n.
+ * mean and the unbiased std are reduced in fp64 (two passes), rounded to fp32 like torch's mean()/std().
+ * n == 1 copies x unchanged (upstream skips the normalisation when numel() == 1).  in-place (out == x) allowed.
+ * ------------------------------------------------------------------------------------------------------------------ */
+size_t ppo_adv_normalize_workspace_bytes(int64_t n);
+int ppo_adv_normalize(const float* x, int64_t in_stride, float* out, int64_t out_stride, int64_t n, float eps,
+                      void* workspace, size_t workspace_bytes, ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * A5  Permutation gather into a packed row table.  Replaces the per-mini-batch fancy indexing of
+ * rsl_rl/storage/rollout_storage.py:232-259 (mini_batch_generator): because upstream draws ONE permutation per
+ * update and reuses it for every epoch, gathering the whole rollout once in permutation order makes mini-batch i
+ * the contiguous row range [i*B/M, (i+1)*B/M) of the table.
+ *   dst[j*dst_stride + seg.dst_col + c] = f(seg.src[perm[j]*seg.src_stride + c]),  c < seg.width,
+ * with f the identity, or the observation normaliser (x - mean[c]) / (std[c] + eps)
+ * (rsl_rl/modules/normalization.py:46-48) when seg.norm_mean != NULL.  Data moves bit-exactly.
+ * perm: int64 [rows], every entry in [0, src_rows).
+ * ------------------------------------------------------------------------------------------------------------------ */
+typedef struct ppo_gather_segment {
+  const float* src;       /* [src_rows, src_stride] */
+  int64_t src_stride;     /* floats */
+  int32_t width;          /* floats copied per row */
+  int32_t dst_col;        /* first destination column */
+  const float* norm_mean; /* [width] or NULL */
+  const float* norm_std;  /* [width] (required with norm_mean) */
+  float norm_eps;
+  int32_t reserved;
+} ppo_gather_segment;
+
+#define PPO_MAX_GATHER_SEGMENTS 16
+
+int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_rows, const ppo_gather_segment* segments,
+                    int32_t num_segments, float* dst, int64_t dst_stride, ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * A6  Linear layers of rsl_rl/modules/mlp.py:27-95 (nn.Linear + nn.ELU), forward and hand-written backward, as fp32
+ * MFMA GEMMs.  One call runs up to PPO_MAX_LINEAR_PROBLEMS independent problems (e.g. actor and critic) over the
+ * same number of rows in a single grouped launch.  Weights use torch's layout: w[out, in], row-major.
+ * ------------------------------------------------------------------------------------------------------------------ */
+#define PPO_MAX_LINEAR_PROBLEMS 8
+
+/* forward: z = x w^T + b; with PPO_ACT_ELU also h = elu(z) (alpha 1).  Replaces nn.Linear.forward / nn.ELU.forward.
+ * z (pre-activation) is kept for the backward; h may be NULL with PPO_ACT_NONE. */
+typedef struct ppo_linear_fwd_problem {
+  const float* x; int64_t ldx; /* [rows, in] */
+  const float* w;              /* [out, in] */
+  const float* b;              /* [out] */
+  float* z; int64_t ldz;       /* [rows, out] */
+  float* h; int64_t ldh;       /* [rows, out] or NULL */
+  int32_t in_features;
+  int32_t out_features;
+} ppo_linear_fwd_problem;
+
+int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t count, int64_t rows, int32_t activation,
+                   ppo_stream_t stream);
+
+/* backward to the layer input: dz_prev = (dz w) * act'(z_prev), act' of ELU = 1 if z > 0 else exp(z)
+ * (torch's elu_backward on the input).  z_prev == NULL means no activation (plain dx = dz w).
+ * Replaces autograd's mm backward + EluBackward (rsl_rl/algorithms/ppo.py:298). */
+typedef struct ppo_linear_bwd_dx_problem {
+  const float* dz; int64_t lddz;         /* [rows, out] */
+  const float* w;                        /* [out, in] */
+  const float* z_prev; int64_t ldz_prev; /* [rows, in] or NULL */
+  float* dz_prev; int64_t lddz_prev;     /* [rows, in] */
+  int32_t in_features;
+  int32_t out_features;
+} ppo_linear_bwd_dx_problem;
+
+int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, ppo_stream_t stream);
+
+/* backward to the parameters: dw = dz^T x, db = sum_rows dz, reduced over rows in fixed-order split-K partials
+ * (deterministic: no float atomics).  Replaces autograd's AddmmBackward for weight and bias. */
+typedef struct ppo_linear_bwd_dw_problem {
+  const float* dz; int64_t lddz; /* [rows, out] */
+  const float* x; int64_t ldx;   /* [rows, in] */
+  float* dw;                     /* [out, in] */
+  float* db;                     /* [out] */
+  int32_t in_features;
+  int32_t out_features;
+} ppo_linear_bwd_dw_problem;
+
+size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows);
+int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows, void* workspace,
+                      size_t workspace_bytes, ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * A7  Empirical observation normaliser, rsl_rl/modules/normalization.py:46-78.
+ * ppo_obs_normalize: y = (x - mean) / (std + eps) over [rows, width] (forward, :46-48).
+ * ppo_normalizer_update: batch moments of the concatenation of `num_segments` column blocks over `rows` rows
+ * (fp64, two-pass: mean then biased variance), then the running update of (_mean, _var, _std, count) in upstream's
+ * fp32 operation order (:58-78, single process).  state_mean/var/std: [dim]; count: one int64.
+ * ------------------------------------------------------------------------------------------------------------------ */
+int ppo_obs_normalize(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows, int32_t width,
+                      const float* mean, const float* std, float eps, ppo_stream_t stream);
+
+typedef struct ppo_column_block {
+  const float* src; /* [rows, stride] */
+  int64_t stride;
+  int32_t width;
+  int32_t reserved;
+} ppo_column_block;
+
+size_t ppo_normalizer_update_workspace_bytes(int64_t rows, int32_t dim);
+int ppo_normalizer_update(const ppo_column_block* blocks, int32_t num_blocks, int64_t rows, float* state_mean,
+                          float* state_var, float* state_std, int64_t* count, void* workspace,
+                          size_t workspace_bytes, ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * A8-A11  Gaussian policy head + PPO losses, forward and backward, rsl_rl/algorithms/ppo.py:226-285 with
+ * rsl_rl/modules/distribution.py:183-238 (state-independent std).  Per row r of a mini-batch of R rows:
+ *   std = clamp(std_param) (scalar) or exp(clamp(log_std_param)) (log);
+ *   logp = sum_a [-(a-mu)^2/(2 std^2) - log std - log sqrt(2 pi)];  ratio = exp(logp - old_logp);
+ *   L_pi = mean_r max(-adv ratio, -adv clamp(ratio, 1-clip, 1+clip));
+ *   L_v = mean_r max((V-R)^2, (V_old + clamp(V-V_old, -clip, clip) - R)^2)  (or mean (R-V)^2 unclipped);
+ *   entropy_r = sum_a [0.5 + 0.5 log(2 pi) + log std];  loss = L_pi + c_v L_v - c_e mean(entropy);
+ *   kl_r = sum_a 0.5 ((var_ratio + t1) - 1 - log var_ratio)  (torch's Normal/Normal KL, ppo.py:243).
+ * Backward follows torch autograd: max() splits ties 50/50, clamp() passes the gradient on the closed interval.
+ * Outputs d_mean [R, A] = dloss/dmu and d_value [R] = dloss/dV, plus per-block partial sums in `workspace`
+ * (surrogate, value loss, kl, and the per-action std-parameter gradient) reduced by ppo_loss_finalize.
+ * ------------------------------------------------------------------------------------------------------------------ */
+typedef struct ppo_loss_args {
+  int64_t rows;
+  int32_t num_actions;
+  int32_t std_type;         /* PPO_STD_SCALAR or PPO_STD_LOG */
+  const float* mean;        /* [rows, ld_mean] new actor output */
+  int64_t ld_mean;
+  const float* value;       /* [rows] at stride ld_value: new critic output */
+  int64_t ld_value;
+  const float* actions;     /* [rows, A] at row stride ld_batch */
+  const float* old_mean;    /* [rows, A] at row stride ld_batch */
+  const float* old_std;     /* [rows, A] at row stride ld_batch */
+  const float* old_logp;    /* [rows] at stride ld_batch */
+  const float* advantages;  /* [rows] at stride ld_batch */
+  const float* old_values;  /* [rows] at stride ld_batch */
+  const float* returns;     /* [rows] at stride ld_batch */
+  int64_t ld_batch;
+  const float* std_param;   /* [A] the distribution parameter (std_param or log_std_param) */
+  double std_lo, std_hi;    /* clamp range in the parameter's own space (log-space bounds for PPO_STD_LOG) */
+  double clip_param;        /* ratio clamp [(float)(1-clip), (float)(1+clip)], value clamp +-(float)clip */
+  double value_loss_coef;   /* used as fp32, like torch's Python-scalar multiply */
+  double entropy_coef;
+  int32_t use_clipped_value_loss;
+  int32_t reserved;
+  float* d_mean;            /* [rows, ld_dmean] */
+  int64_t ld_dmean;
+  float* d_value;           /* [rows] at stride ld_dvalue */
+  int64_t ld_dvalue;
+} ppo_loss_args;
+
+#define PPO_MAX_ACTIONS 64
+
+size_t ppo_loss_workspace_bytes(int64_t rows, int32_t num_actions);
+int ppo_gauss_ppo_loss(const ppo_loss_args* args, void* workspace, size_t workspace_bytes, ppo_stream_t stream);
+
+/* Device-resident optimisation state shared by ppo_loss_finalize and ppo_adam_step (fp64 like upstream's Python
+ * floats).  The host reads it back once per update. */
+typedef struct ppo_device_state {
+  double learning_rate;       /* upstream PPO.learning_rate (ppo.py:120, :253-256) */
+  double sum_value_loss;      /* sum over mini-batches of value_loss.item()        (ppo.py:317) */
+  double sum_surrogate_loss;  /*                         surrogate_loss.item()     (ppo.py:318) */
+  double sum_entropy;         /*                         entropy.mean().item()     (ppo.py:319) */
+  float last_kl_mean;
+  float last_value_loss;
+  float last_surrogate_loss;
+  float last_entropy;
+  float total_norm[4];        /* per parameter group, last step (clip_grad_norm_'s total_norm) */
+  float clip_coef[4];         /* per parameter group, last step */
+  int32_t num_minibatches;    /* mini-batches finalised since the state was reset */
+  int32_t reserved[3];
+} ppo_device_state;
+
+/* Reduces the loss partials of the last ppo_gauss_ppo_loss call (same rows / num_actions / workspace), writes the
+ * fp32 losses, applies the adaptive-KL learning-rate rule of ppo.py:240-266 when adaptive != 0
+ * (kl > 2 desired -> lr = max(1e-5, lr/1.5); 0 < kl < desired/2 -> lr = min(1e-2, lr*1.5); fp32 comparisons),
+ * accumulates the loss sums, and writes the std-parameter gradient d_std_param [A] (entropy term and clamp mask
+ * included).  trace, if not NULL, receives {kl_mean, lr, surrogate, value, entropy} (fp64) at
+ * trace[5*state->num_minibatches]. */
+int ppo_loss_finalize(const ppo_loss_args* args, const void* workspace, size_t workspace_bytes, float* d_std_param,
+                      ppo_device_state* state, int32_t adaptive, double desired_kl, double* trace,
+                      ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * Rollout-side Gaussian head for act() (rsl_rl/algorithms/ppo.py:124-135; rsl_rl/modules/distribution.py:183-232):
+ * std = clamp(std_param) or exp(clamp(log_std_param)); with noise != NULL, actions = noise * std + mean
+ * (torch.normal(mean, std) on a standard-normal draw); with noise == NULL the given actions are scored.
+ * logp [rows] (optional) = sum_a log N(actions; mean, std); std_out [rows, A] (optional) = std per row, the
+ * distribution_params[1] the rollout storage keeps.
+ * ------------------------------------------------------------------------------------------------------------------ */
+int ppo_gauss_sample(const float* mean, int64_t ld_mean, const float* std_param, int32_t std_type, double std_lo,
+                     double std_hi, const float* noise, int64_t ld_noise, float* actions, int64_t ld_actions,
+                     float* logp, float* std_out, int64_t ld_std, int64_t rows, int32_t num_actions,
+                     ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
+ * A12+A13  Per-group gradient-norm clipping (torch.nn.utils.clip_grad_norm_, called per model at ppo.py:309-310)
+ * fused with Adam (torch.optim.Adam single-tensor path, ppo.py:311) over ONE flat fp32 buffer per kind.
+ * Groups are contiguous ranges [group_begin[g], group_begin[g+1]) of the flat buffers.
+ *   total_g = ||grad[group g]||_2 (fp64);  coef_g = min(1, max_norm / (total_g + 1e-6));  g' = grad * coef_g;
+ *   m = m + (1-b1) (g' - m);  v = v b2 + ((1-b2) g') g';  denom = sqrt(v) / bc2_sqrt + eps;
+ *   p = p + ((-lr/bc1) m) / denom,   lr read from state->learning_rate,
+ * bc1 = 1 - b1^step and bc2_sqrt = (1 - b2^step)^0.5 computed by the caller in double exactly as torch does.
+ * grad is rewritten with the clipped values (upstream clips in place).
+ * ------------------------------------------------------------------------------------------------------------------ */
+#define PPO_MAX_PARAM_GROUPS 4
+
+size_t ppo_adam_workspace_bytes(int64_t num_params);
+int ppo_adam_step(float* params, float* grads, float* exp_avg, float* exp_avg_sq, const int64_t* group_begin,
+                  int32_t num_groups, double max_grad_norm, double beta1, double beta2, double eps, double bc1,
+                  double bc2_sqrt, ppo_device_state* state, void* workspace, size_t workspace_bytes,
+                  ppo_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PPO_HIP_H_ */

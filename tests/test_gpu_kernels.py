@@ -1,0 +1,395 @@
+"""GPU parity of every kernel of libppo_hip.so, called through the C ABI (tt_rsl_rl_amd.ops), against the oracle.
+
+Bars: bit-exact for data movement (gather) and for the GAE returns; 1e-6 relative for advantages and normaliser
+statistics; fp32-GEMM tolerance (relative Frobenius 2e-6 against float64) for the linear layers; 2e-6 for the loss
+gradients given identical network outputs; 1e-6 for Adam + clipping against torch.optim.Adam / clip_grad_norm_.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import ppo_ref as O
+from tests.parity import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from tt_rsl_rl_amd import _lib, ops
+
+    _lib.load()
+    return ops
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A1 / A2
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("T,N,p_done", [(24, 4096, 0.005), (7, 333, 0.3), (1, 1, 0.0), (24, 65536, 0.01)])
+def test_gae_matches_oracle(cuda, T, N, p_done):
+    ops = _ops()
+    g = torch.Generator().manual_seed(T * 1000 + N)
+    rewards = torch.randn(T, N, 1, generator=g) * 0.3
+    values = torch.randn(T, N, 1, generator=g)
+    dones = (torch.rand(T, N, 1, generator=g) < p_done).to(torch.uint8)
+    last = torch.randn(N, 1, generator=g)
+    ret_ref, adv_raw_ref = O.gae_returns(rewards, values, dones, last, 0.99, 0.95, normalize=False)
+    _, adv_ref = O.gae_returns(rewards, values, dones, last, 0.99, 0.95, normalize=True)
+    d = lambda t: t.to(cuda).contiguous()
+    ret, adv = torch.empty(T, N, 1, device=cuda), torch.empty(T, N, 1, device=cuda)
+    ops.gae(d(rewards), d(values), d(dones), d(last), ret, adv, 0.99, 0.95)
+    assert torch.equal(ret.cpu(), ret_ref), "GAE returns must be bit-exact"
+    assert torch.equal(adv.cpu(), adv_raw_ref), "returns - values must be bit-exact"
+    if T * N > 1:
+        ops.adv_normalize(adv, adv, T * N)
+        err = (adv.cpu() - adv_ref).abs().max().item()
+        assert err <= 1e-6 * max(1.0, adv_ref.abs().max().item()), err
+
+
+def test_adv_normalize_strided(cuda):
+    ops = _ops()
+    x = torch.randn(5000, 3)
+    out = torch.zeros(5000, 7)
+    xd, od = x.to(cuda), out.to(cuda)
+    ops.adv_normalize(xd[:, 1], od[:, 4], 5000, in_stride=3, out_stride=7)
+    col = x[:, 1]
+    ref = (col - col.mean()) / (col.std() + 1e-8)
+    assert rel_err(od[:, 4], ref) < 1e-6
+    assert torch.equal(od[:, :4].cpu(), out[:, :4]) and torch.equal(od[:, 5:].cpu(), out[:, 5:])
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A5 gather (+ fused normaliser)
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def test_gather_rows_bit_exact(cuda):
+    ops = _ops()
+    B = 98304
+    torch.manual_seed(3)
+    obs = torch.randn(B, 99)
+    act = torch.randn(B, 29)
+    logp = torch.randn(B, 1)
+    mean, std = torch.randn(1, 99), torch.rand(1, 99) + 0.5
+    perm = torch.randperm(B)
+    W = 140
+    dst = torch.full((B, W), float("nan"), device=cuda)
+    segs = [ops.Segment(obs.to(cuda), 0, mean.view(-1).to(cuda), std.view(-1).to(cuda), 1e-2),
+            ops.Segment(act.to(cuda), 100), ops.Segment(logp.to(cuda), 132)]
+    ops.gather_rows(perm.to(cuda), segs, dst)
+    out = dst.cpu()
+    norm = O.EmpiricalNormalization(99)
+    norm._mean.copy_(mean)
+    norm._std.copy_(std)
+    assert torch.equal(out[:, :99], norm(obs[perm])), "normalised gather must be bit-exact"
+    assert torch.equal(out[:, 100:129], act[perm])
+    assert torch.equal(out[:, 132:133], logp[perm])
+    assert torch.isnan(out[:, 99]).all() and torch.isnan(out[:, 129:132]).all(), "gather wrote outside its columns"
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A6 linear layers
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def _elu64(z):
+    return torch.where(z > 0, z, torch.expm1(z))
+
+
+@pytest.mark.parametrize("rows", [1, 77, 1000, 24576])
+def test_linear_fwd_grouped(cuda, rows):
+    ops = _ops()
+    torch.manual_seed(rows)
+    shapes = [(96, 512), (99, 512)] if rows != 77 else [(99, 29), (48, 1)]
+    probs, refs = [], []
+    for i, (fin, fout) in enumerate(shapes):
+        x = torch.randn(rows, fin + 5)[:, 2:2 + fin]  # strided view (ld = fin + 5)
+        w = torch.randn(fout, fin) / math.sqrt(fin)
+        b = torch.randn(fout)
+        xd = torch.randn(rows, fin + 5, device=cuda)
+        xd.copy_(torch.cat([torch.zeros(rows, 2), x, torch.zeros(rows, 3)], 1))
+        z, h = torch.empty(rows, fout, device=cuda), torch.empty(rows, fout, device=cuda)
+        probs.append((xd[:, 2:2 + fin], w.to(cuda), b.to(cuda), z, h))
+        z64 = x.double() @ w.double().t() + b.double()
+        refs.append((z, h, z64))
+    ops.linear_fwd(probs, rows, elu=True)
+    for z, h, z64 in refs:
+        assert rel_err(z, z64) < 2e-6
+        assert rel_err(h, _elu64(z64)) < 2e-6
+
+
+@pytest.mark.parametrize("rows,fin,fout,act", [(24576, 512, 256, True), (1000, 128, 29, True), (333, 256, 1, False)])
+def test_linear_bwd_dx(cuda, rows, fin, fout, act):
+    ops = _ops()
+    torch.manual_seed(fin + fout)
+    dz = torch.randn(rows, fout)
+    w = torch.randn(fout, fin) / math.sqrt(fout)
+    zp = torch.randn(rows, fin) if act else None
+    out = torch.empty(rows, fin, device=cuda)
+    ops.linear_bwd_dx([(dz.to(cuda), w.to(cuda), None if zp is None else zp.to(cuda), out)], rows)
+    ref = dz.double() @ w.double()
+    if act:
+        ref = ref * torch.where(zp.double() > 0, torch.ones_like(ref), torch.exp(zp.double()))
+    assert rel_err(out, ref) < 2e-6
+
+
+@pytest.mark.parametrize("rows", [24576, 1000, 5])
+def test_linear_bwd_dw_grouped(cuda, rows):
+    ops = _ops()
+    torch.manual_seed(rows + 1)
+    shapes = [(99, 512), (512, 256), (256, 128), (128, 29), (96, 512), (512, 256), (256, 128), (128, 1)]
+    probs, refs = [], []
+    for fin, fout in shapes:
+        dz = torch.randn(rows, fout) / rows
+        x = torch.randn(rows, fin)
+        dw = torch.full((fout, fin), float("nan"), device=cuda)
+        db = torch.full((fout,), float("nan"), device=cuda)
+        probs.append((dz.to(cuda), x.to(cuda), dw, db))
+        refs.append((dw, db, dz.double().t() @ x.double(), dz.double().sum(0), dz.double().abs().sum(0)))
+    ops.linear_bwd_dw(probs, rows)
+    for dw, db, rw, rb, rb_abs in refs:
+        assert rel_err(dw, rw) < 2e-6
+        # a bias gradient is a sum that can cancel: bound the error by the sum of |terms| (dot-product bound)
+        assert ((db.cpu().double() - rb).abs() / rb_abs).max().item() < 1e-6
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A8-A11 losses
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def _loss_case(rows, A, std_type, clipped, seed, ratio_spread=0.3):
+    g = torch.Generator().manual_seed(seed)
+    mean = torch.randn(rows, A, generator=g) * 0.5
+    if std_type == "log":
+        param = torch.randn(A, generator=g) * 0.3
+        std = torch.exp(param)
+    else:
+        param = torch.rand(A, generator=g) + 0.5
+        std = param.clone()
+    actions = mean + std * torch.randn(rows, A, generator=g)
+    old_mean = mean + ratio_spread * 0.1 * torch.randn(rows, A, generator=g)
+    old_std = std * (1 + 0.05 * torch.randn(A, generator=g)).abs()
+    old_std = old_std.expand(rows, A).contiguous()
+    old_logp = torch.distributions.Normal(old_mean, old_std).log_prob(actions).sum(-1) + ratio_spread * torch.randn(
+        rows, generator=g)
+    adv = torch.randn(rows, generator=g)
+    value = torch.randn(rows, generator=g)
+    old_value = value + 0.3 * torch.randn(rows, generator=g)
+    ret = value + torch.randn(rows, generator=g)
+    return dict(mean=mean, param=param, actions=actions, old_mean=old_mean, old_std=old_std, old_logp=old_logp,
+                adv=adv, value=value, old_value=old_value, ret=ret)
+
+
+def _oracle_loss(c, std_type, clipped, clip=0.2, cv=1.0, ce=0.01, dtype=torch.float32):
+    """The oracle's loss block (ppo_loss_terms + GaussianDistribution) with torch autograd, in `dtype`."""
+    c = {k: v.to(dtype) for k, v in c.items()}
+    dist = O.GaussianDistribution(c["mean"].shape[1], std_type=std_type).to(dtype)
+    with torch.no_grad():
+        (dist.std_param if std_type == "scalar" else dist.log_std_param).copy_(c["param"])
+    mean = c["mean"].clone().requires_grad_(True)
+    value = c["value"].clone().requires_grad_(True)
+    dist.update(mean)
+    logp = dist.log_prob(c["actions"])
+    entropy = dist.entropy
+    with torch.no_grad():
+        kl = dist.kl_divergence((c["old_mean"], c["old_std"]), dist.params).mean()
+    s, v, loss = O.ppo_loss_terms(logp, c["old_logp"].unsqueeze(-1), c["adv"].unsqueeze(-1), value, c["old_value"],
+                                  c["ret"], entropy, clip, clipped, cv, ce)
+    loss.backward()
+    p = dist.std_param if std_type == "scalar" else dist.log_std_param
+    return dict(surrogate=s.item(), value=v.item(), entropy=entropy.mean().item(), kl=kl.item(), d_mean=mean.grad,
+                d_value=value.grad, d_param=p.grad)
+
+
+@pytest.mark.parametrize("rows,A,std_type,clipped", [(24576, 29, "log", True), (1000, 12, "scalar", True),
+                                                     (77, 1, "log", False), (1, 3, "log", True)])
+def test_ppo_loss_matches_autograd(cuda, rows, A, std_type, clipped):
+    ops = _ops()
+    from tt_rsl_rl_amd import _lib as L
+
+    c = _loss_case(rows, A, std_type, clipped, seed=rows + A)
+    ref = _oracle_loss(c, std_type, clipped)  # fp32, upstream's own arithmetic
+    ref64 = _oracle_loss(c, std_type, clipped, dtype=torch.float64)  # the same formulas in fp64
+    W = 3 * A + 4
+    tab = torch.zeros(rows, W)
+    tab[:, 0:A], tab[:, A:2 * A], tab[:, 2 * A:3 * A] = c["actions"], c["old_mean"], c["old_std"]
+    tab[:, 3 * A], tab[:, 3 * A + 1], tab[:, 3 * A + 2], tab[:, 3 * A + 3] = c["old_logp"], c["adv"], c["old_value"], \
+        c["ret"]
+    tab = tab.to(cuda)
+    batch = {"ld": W, "actions": tab[:, 0], "old_mean": tab[:, A], "old_std": tab[:, 2 * A],
+             "old_logp": tab[:, 3 * A], "advantages": tab[:, 3 * A + 1], "old_values": tab[:, 3 * A + 2],
+             "returns": tab[:, 3 * A + 3]}
+    mean, value, param = c["mean"].to(cuda), c["value"].to(cuda), c["param"].to(cuda)
+    d_mean, d_value, d_param = torch.empty(rows, A, device=cuda), torch.empty(rows, device=cuda), torch.empty(A, device=cuda)
+    if std_type == "log":
+        lo, hi, st = math.log(1e-6), math.log(1e6), L.PPO_STD_LOG
+    else:
+        lo, hi, st = 1e-6, 1e6, L.PPO_STD_SCALAR
+    args = ops.make_loss_args(rows, mean, value, batch, param, st, lo, hi, 0.2, 1.0, 0.01, clipped, d_mean, d_value)
+    ws = torch.empty(ops.loss_workspace_bytes(rows, A), dtype=torch.uint8, device=cuda)
+    state = ops.new_device_state(1e-3, cuda)
+    trace = torch.zeros(5, dtype=torch.float64, device=cuda)
+    ops.ppo_loss(args, ws)
+    ops.ppo_loss_finalize(args, ws, d_param, state, True, 0.01, trace)
+    tr = trace.cpu().tolist()
+    assert abs(tr[2] - ref["surrogate"]) <= 2e-6 * max(1.0, abs(ref["surrogate"]))
+    assert abs(tr[3] - ref["value"]) <= 2e-6 * max(1.0, abs(ref["value"]))
+    assert abs(tr[4] - ref["entropy"]) <= 2e-6 * max(1.0, abs(ref["entropy"]))
+    assert abs(tr[0] - ref["kl"]) <= 1e-6 * max(1e-3, abs(ref["kl"])) + 1e-7
+    # gradients: within fp32 noise of the fp64 truth, and of upstream's fp32 autograd (2e-5, the loss-gradient bar)
+    for key, got in (("d_mean", d_mean), ("d_value", d_value), ("d_param", d_param)):
+        assert rel_err(got, ref64[key], 1e-12) < 1e-5, key
+        assert rel_err(got, ref[key], 1e-12) < 2e-5, key
+    lr_ref = O.adaptive_lr(torch.tensor(tr[0], dtype=torch.float32), 1e-3, 0.01)
+    assert tr[1] == lr_ref
+
+
+def test_kl_is_exactly_zero_for_identical_distributions(cuda):
+    ops = _ops()
+    from tt_rsl_rl_amd import _lib as L
+
+    from tt_rsl_rl_amd.models import GaussianDistribution
+
+    rows, A = 4096, 12
+    c = _loss_case(rows, A, "log", True, seed=5)
+    # the rollout's stored std is produced by the same device code as the update's (act() -> gauss_sample)
+    dist = GaussianDistribution(A, std_type="log").to(cuda)
+    with torch.no_grad():
+        dist.log_std_param.copy_(c["param"])
+    std_d = torch.empty(rows, A, device=cuda)
+    dist.sample_from(c["mean"].to(cuda), None, c["actions"].to(cuda), None, std_d)
+    std = std_d.cpu()
+    W = 3 * A + 4
+    tab = torch.zeros(rows, W)
+    tab[:, 0:A], tab[:, A:2 * A], tab[:, 2 * A:3 * A] = c["actions"], c["mean"], std
+    tab = tab.to(cuda)
+    batch = {"ld": W, "actions": tab[:, 0], "old_mean": tab[:, A], "old_std": tab[:, 2 * A],
+             "old_logp": tab[:, 3 * A], "advantages": tab[:, 3 * A + 1], "old_values": tab[:, 3 * A + 2],
+             "returns": tab[:, 3 * A + 3]}
+    mean = c["mean"].to(cuda)
+    value = torch.zeros(rows, device=cuda)
+    param = c["param"].to(cuda)
+    # the args struct holds raw pointers: every buffer it names must stay referenced until the kernels ran
+    d_mean, d_value, d_param = torch.empty(rows, A, device=cuda), torch.empty(rows, device=cuda), torch.empty(A, device=cuda)
+    args = ops.make_loss_args(rows, mean, value, batch, param, L.PPO_STD_LOG, math.log(1e-6), math.log(1e6), 0.2, 1.0,
+                              0.01, True, d_mean, d_value)
+    ws = torch.empty(ops.loss_workspace_bytes(rows, A), dtype=torch.uint8, device=cuda)
+    state = ops.new_device_state(1e-3, cuda)
+    trace = torch.zeros(5, dtype=torch.float64, device=cuda)
+    ops.ppo_loss(args, ws)
+    ops.ppo_loss_finalize(args, ws, d_param, state, True, 0.01, trace)
+    kl, lr = trace.cpu().tolist()[:2]
+    assert kl == 0.0 and lr == 1e-3, "KL(p||p) must round to exactly 0 so the LR is not raised (upstream S15-S17)"
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A12-A13 clip + Adam
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def test_adam_clip_matches_torch(cuda):
+    ops = _ops()
+    torch.manual_seed(11)
+    shapes_a = [(29,), (512, 96), (512,), (256, 512), (256,)]
+    shapes_c = [(512, 99), (512,), (1, 128), (1,)]
+    pa = [torch.nn.Parameter(torch.randn(s) * 0.1) for s in shapes_a]
+    pc = [torch.nn.Parameter(torch.randn(s) * 0.1) for s in shapes_c]
+    opt = torch.optim.Adam(pa + pc, lr=1e-3)
+    flat = torch.cat([p.detach().reshape(-1) for p in pa + pc]).to(cuda)
+    n_a = sum(p.numel() for p in pa)
+    grad = torch.zeros_like(flat)
+    m, v = torch.zeros_like(flat), torch.zeros_like(flat)
+    gb = torch.tensor([0, n_a, flat.numel()], dtype=torch.int64)
+    state = ops.new_device_state(1e-3, cuda)
+    ws = ops.Workspace(cuda)
+    lrs = [1e-3, 1e-3, 6.7e-4, 2e-3, 1e-5, 1e-2, 3e-3, 1e-3]
+    for step, lr in enumerate(lrs, start=1):
+        scale = 10.0 if step % 3 == 0 else 0.01  # both sides of the clip threshold
+        for p in pa + pc:
+            p.grad = torch.randn_like(p) * scale
+        grad.copy_(torch.cat([p.grad.reshape(-1) for p in pa + pc]).to(cuda))
+        for group in opt.param_groups:
+            group["lr"] = lr
+        torch.nn.utils.clip_grad_norm_(pa, 1.0)
+        torch.nn.utils.clip_grad_norm_(pc, 1.0)
+        opt.step()
+        ops.reset_device_state(state, lr)
+        ops.adam_step(flat, grad, m, v, gb, 1.0, 0.9, 0.999, 1e-8, 1 - 0.9 ** step, (1 - 0.999 ** step) ** 0.5,
+                      state, ws)
+        ref = torch.cat([p.detach().reshape(-1) for p in pa + pc])
+        assert rel_err(flat, ref) < 1e-6, step
+        ref_m = torch.cat([opt.state[p]["exp_avg"].reshape(-1) for p in pa + pc])
+        ref_v = torch.cat([opt.state[p]["exp_avg_sq"].reshape(-1) for p in pa + pc])
+        assert rel_err(m, ref_m) < 1e-6 and rel_err(v, ref_v) < 1e-6
+        ref_g = torch.cat([p.grad.reshape(-1) for p in pa + pc])
+        assert rel_err(grad, ref_g) < 1e-6, "clipped gradients are left in the gradient buffer like upstream"
+
+
+def test_adam_first_step_moves_by_lr(cuda):
+    """tests/algorithms/test_ppo.py:492-505: the first Adam step moves every parameter by lr."""
+    ops = _ops()
+    p = torch.randn(1000, device=cuda)
+    p0 = p.clone()
+    g = torch.ones(1000, device=cuda) * 1e-3
+    m, v = torch.zeros_like(p), torch.zeros_like(p)
+    state = ops.new_device_state(1e-3, cuda)
+    ops.adam_step(p, g, m, v, torch.tensor([0, 1000]), 1.0, 0.9, 0.999, 1e-8, 1 - 0.9, (1 - 0.999) ** 0.5, state,
+                  ops.Workspace(cuda))
+    assert torch.allclose((p0 - p).abs(), torch.full_like(p, 1e-3), atol=1e-6, rtol=0)
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A7 normaliser
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def test_normalizer_update_matches_oracle(cuda):
+    ops = _ops()
+    torch.manual_seed(2)
+    ref = O.EmpiricalNormalization(96 + 3)
+    ref.train()
+    mean, var, std = torch.zeros(99, device=cuda), torch.ones(99, device=cuda), torch.ones(99, device=cuda)
+    count = torch.zeros((), dtype=torch.int64, device=cuda)
+    ws = ops.Workspace(cuda)
+    for i, rows in enumerate([98304, 4096, 33, 98304]):
+        a = torch.randn(rows, 96) * (i + 1) + 3.0
+        b = torch.rand(rows, 3) * 2 - 1
+        ref.update(torch.cat([a, b], 1))
+        ops.normalizer_update([a.to(cuda), b.to(cuda)], mean, var, std, count, ws)
+        assert int(count) == int(ref.count)
+        assert rel_err(mean, ref._mean.view(-1)) < 1e-6
+        assert rel_err(var, ref._var.view(-1)) < 1e-6
+        assert rel_err(std, ref._std.view(-1)) < 1e-6
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# rollout-side Gaussian head
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def test_gauss_sample_and_log_prob(cuda):
+    _ops()
+    from tt_rsl_rl_amd.models import GaussianDistribution
+
+    torch.manual_seed(4)
+    dist = GaussianDistribution(29, init_std=0.7, std_type="log").to(cuda)
+    mean = torch.randn(4096, 29, device=cuda)
+    noise = torch.randn(4096, 29, device=cuda)
+    actions = torch.empty_like(mean)
+    logp = torch.empty(4096, device=cuda)
+    std = torch.empty_like(mean)
+    dist.sample_from(mean, noise, actions, logp, std)
+    sd = torch.exp(dist.log_std_param.detach().cpu())
+    assert rel_err(std, sd.expand(4096, 29)) < 1e-7
+    k_sd = std.cpu()
+    assert torch.equal(k_sd, k_sd[:1].expand(4096, 29)), "the std is state-independent: one value per action"
+    ref_a = noise.cpu() * k_sd + mean.cpu()  # torch.normal(mean, std): standard draw * std + mean
+    assert torch.equal(actions.cpu(), ref_a)
+    ref_lp = torch.distributions.Normal(mean.cpu(), k_sd).log_prob(ref_a).sum(-1)
+    assert rel_err(logp, ref_lp) < 1e-6

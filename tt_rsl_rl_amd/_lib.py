@@ -1,0 +1,162 @@
+"""ctypes binding of libppo_hip.so (the C ABI declared in include/ppo_hip.h).
+
+The product path calls these entry points only; there is no CPU fallback.  Loading fails loudly when the library
+is missing (build it with ``python -m tt_rsl_rl_amd.build``).  Status codes become Python exceptions the way
+upstream rsl_rl raises them: bad arguments -> ValueError, unsupported shapes -> NotImplementedError, HIP runtime
+failures -> RuntimeError.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libppo_hip.so"
+
+PPO_OK = 0
+PPO_EINVAL = -1
+PPO_EHIP = -2
+PPO_EUNSUPPORTED = -3
+PPO_ACT_NONE = 0
+PPO_ACT_ELU = 1
+PPO_STD_SCALAR = 0
+PPO_STD_LOG = 1
+MAX_GATHER_SEGMENTS = 16
+MAX_LINEAR_PROBLEMS = 8
+MAX_PARAM_GROUPS = 4
+MAX_ACTIONS = 64
+
+f32p = C.c_void_p  # device pointers are passed as plain addresses
+i64 = C.c_int64
+i32 = C.c_int32
+
+
+class GatherSegment(C.Structure):
+    _fields_ = [("src", C.c_void_p), ("src_stride", i64), ("width", i32), ("dst_col", i32),
+                ("norm_mean", C.c_void_p), ("norm_std", C.c_void_p), ("norm_eps", C.c_float), ("reserved", i32)]
+
+
+class LinearFwdProblem(C.Structure):
+    _fields_ = [("x", C.c_void_p), ("ldx", i64), ("w", C.c_void_p), ("b", C.c_void_p), ("z", C.c_void_p),
+                ("ldz", i64), ("h", C.c_void_p), ("ldh", i64), ("in_features", i32), ("out_features", i32)]
+
+
+class LinearBwdDxProblem(C.Structure):
+    _fields_ = [("dz", C.c_void_p), ("lddz", i64), ("w", C.c_void_p), ("z_prev", C.c_void_p), ("ldz_prev", i64),
+                ("dz_prev", C.c_void_p), ("lddz_prev", i64), ("in_features", i32), ("out_features", i32)]
+
+
+class LinearBwdDwProblem(C.Structure):
+    _fields_ = [("dz", C.c_void_p), ("lddz", i64), ("x", C.c_void_p), ("ldx", i64), ("dw", C.c_void_p),
+                ("db", C.c_void_p), ("in_features", i32), ("out_features", i32)]
+
+
+class ColumnBlock(C.Structure):
+    _fields_ = [("src", C.c_void_p), ("stride", i64), ("width", i32), ("reserved", i32)]
+
+
+class LossArgs(C.Structure):
+    _fields_ = [
+        ("rows", i64), ("num_actions", i32), ("std_type", i32),
+        ("mean", C.c_void_p), ("ld_mean", i64),
+        ("value", C.c_void_p), ("ld_value", i64),
+        ("actions", C.c_void_p), ("old_mean", C.c_void_p), ("old_std", C.c_void_p), ("old_logp", C.c_void_p),
+        ("advantages", C.c_void_p), ("old_values", C.c_void_p), ("returns", C.c_void_p), ("ld_batch", i64),
+        ("std_param", C.c_void_p), ("std_lo", C.c_double), ("std_hi", C.c_double),
+        ("clip_param", C.c_double), ("value_loss_coef", C.c_double), ("entropy_coef", C.c_double),
+        ("use_clipped_value_loss", i32), ("reserved", i32),
+        ("d_mean", C.c_void_p), ("ld_dmean", i64),
+        ("d_value", C.c_void_p), ("ld_dvalue", i64),
+    ]
+
+
+class DeviceState(C.Structure):
+    _fields_ = [("learning_rate", C.c_double), ("sum_value_loss", C.c_double),
+                ("sum_surrogate_loss", C.c_double), ("sum_entropy", C.c_double),
+                ("last_kl_mean", C.c_float), ("last_value_loss", C.c_float), ("last_surrogate_loss", C.c_float),
+                ("last_entropy", C.c_float), ("total_norm", C.c_float * 4), ("clip_coef", C.c_float * 4),
+                ("num_minibatches", i32), ("reserved", i32 * 3)]
+
+
+DEVICE_STATE_BYTES = C.sizeof(DeviceState)
+
+# (name, restype, argtypes)
+_SIGNATURES = [
+    ("ppo_last_error", C.c_char_p, []),
+    ("ppo_abi_version", C.c_int, []),
+    ("ppo_gae", C.c_int, [f32p, f32p, f32p, f32p, f32p, f32p, i64, i64, C.c_float, C.c_float, C.c_void_p]),
+    ("ppo_adv_normalize_workspace_bytes", C.c_size_t, [i64]),
+    ("ppo_adv_normalize", C.c_int, [f32p, i64, f32p, i64, i64, C.c_float, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("ppo_gather_rows", C.c_int, [C.c_void_p, i64, i64, C.POINTER(GatherSegment), i32, f32p, i64, C.c_void_p]),
+    ("ppo_linear_fwd", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, C.c_void_p]),
+    ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, C.c_void_p]),
+    ("ppo_linear_bwd_dw_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDwProblem), i32, i64]),
+    ("ppo_linear_bwd_dw", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("ppo_obs_normalize", C.c_int, [f32p, i64, f32p, i64, i64, i32, f32p, f32p, C.c_float, C.c_void_p]),
+    ("ppo_normalizer_update_workspace_bytes", C.c_size_t, [i64, i32]),
+    ("ppo_normalizer_update", C.c_int, [C.POINTER(ColumnBlock), i32, i64, f32p, f32p, f32p, C.c_void_p, C.c_void_p,
+                                        C.c_size_t, C.c_void_p]),
+    ("ppo_loss_workspace_bytes", C.c_size_t, [i64, i32]),
+    ("ppo_gauss_ppo_loss", C.c_int, [C.POINTER(LossArgs), C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("ppo_loss_finalize", C.c_int, [C.POINTER(LossArgs), C.c_void_p, C.c_size_t, f32p, C.c_void_p, i32, C.c_double,
+                                    C.c_void_p, C.c_void_p]),
+    ("ppo_gauss_sample", C.c_int, [f32p, i64, f32p, i32, C.c_double, C.c_double, f32p, i64, f32p, i64, f32p, f32p,
+                                   i64, i64, i32, C.c_void_p]),
+    ("ppo_adam_workspace_bytes", C.c_size_t, [i64]),
+    ("ppo_adam_step", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double, C.c_double,
+                                C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_size_t,
+                                C.c_void_p]),
+]
+
+EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
+ABI_VERSION = 1
+
+_lib: C.CDLL | None = None
+
+
+def load(path: str | os.PathLike | None = None) -> C.CDLL:
+    """Load libppo_hip.so (idempotent) and declare every entry point's signature."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"{p} is missing: build the HIP library first (python -m tt_rsl_rl_amd.build)")
+    lib = C.CDLL(str(p))
+    for name, res, args in _SIGNATURES:
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.ppo_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{p}: ABI version {lib.ppo_abi_version()} != {ABI_VERSION}; rebuild the library")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().ppo_last_error().decode(errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    if status == PPO_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if status == PPO_EINVAL:
+        raise ValueError(msg)
+    if status == PPO_EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+def call(name: str, *args) -> None:
+    """Call an int-returning entry point and raise on a non-zero status."""
+    check(getattr(load(), name)(*args), name)
+
+
+def array(struct_type, items):
+    arr = (struct_type * max(1, len(items)))()
+    for i, it in enumerate(items):
+        arr[i] = it
+    return arr

@@ -1,0 +1,301 @@
+// A8-A11: Gaussian policy head, clipped surrogate, clipped value loss, entropy bonus and the KL of the adaptive
+// learning-rate rule, forward and backward in one pass over the mini-batch
+// (rsl_rl/algorithms/ppo.py:226-285, rsl_rl/modules/distribution.py:183-238, torch's Normal / kl_divergence).
+//
+// One wavefront per 64 rows, one lane per row.  Each lane reads its row's A means / actions / old means / old
+// stds and five scalars, writes dloss/dmu [A] and dloss/dV, and contributes to per-block fp64 partial sums
+// (surrogate, value loss, KL, and the per-action dlogp/dlog(std) sums for the std-parameter gradient).  The
+// partials are reduced in a fixed order by a single-block finalize kernel, which also applies the adaptive-KL
+// learning-rate rule on the device, so the update loop never waits on the host.
+//
+// Gradients follow torch autograd's conventions: max() sends the gradient to the larger operand and splits it
+// 50/50 on a tie; clamp() passes it on the closed interval [lo, hi].
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ppo {
+namespace {
+
+constexpr int kLossThreads = 64;  // one wavefront per block
+constexpr int kFixedCols = 3;     // surrogate, value loss, kl
+
+// log(sqrt(2*pi)) and 0.5 + 0.5*log(2*pi) as the fp32 values torch subtracts / adds (Python doubles cast once).
+constexpr double kLogSqrt2Pi = 0.91893853320467274178;
+constexpr double kEntropyConst = 1.41893853320467274178;
+
+struct LossParams {
+  ppo_loss_args a;
+  float ratio_lo, ratio_hi, vclip_lo, vclip_hi;
+  float c_v, inv_rows_surr, inv_rows_value;
+  float std_lo, std_hi;
+};
+
+__device__ inline double wave_sum(double x) {
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_down(x, off, 64);
+  return x;
+}
+
+// std and its log exactly as torch builds them: clamp in the parameter's space, exp for the log form, then
+// Normal.log_prob / entropy take log(scale) of that std.
+__device__ inline void std_of(const LossParams& p, int a, float& sd, float& log_sd) {
+  std_from_param(p.a.std_param[a], p.a.std_type, p.std_lo, p.std_hi, sd, log_sd);
+}
+
+__global__ __launch_bounds__(kLossThreads) void ppo_loss_kernel(const LossParams p, double* __restrict__ partials) {
+  const ppo_loss_args& a = p.a;
+  const int A = a.num_actions;
+  const int cols = kFixedCols + A;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * kLossThreads + threadIdx.x;
+  const bool live = r < a.rows;
+  double* part = partials + static_cast<int64_t>(blockIdx.x) * cols;
+
+  __shared__ float s_std[PPO_MAX_ACTIONS], s_var[PPO_MAX_ACTIONS], s_log[PPO_MAX_ACTIONS];
+  for (int j = threadIdx.x; j < A; j += kLossThreads) {
+    float sd, lg;
+    std_of(p, j, sd, lg);
+    s_std[j] = sd;
+    s_var[j] = sd * sd;
+    s_log[j] = lg;
+  }
+  __syncthreads();
+
+  float g_logp = 0.0f, surr = 0.0f, vloss = 0.0f, kl = 0.0f;
+  if (live) {
+    const float* mu = a.mean + r * a.ld_mean;
+    const float* act = a.actions + r * a.ld_batch;
+    const float* omu = a.old_mean + r * a.ld_batch;
+    const float* osd = a.old_std + r * a.ld_batch;
+    const float c_lp = static_cast<float>(kLogSqrt2Pi);
+    double logp_acc = 0.0;  // the sum over actions in fp64: one rounding instead of A
+    for (int j = 0; j < A; ++j) {
+      const float d = act[j] - mu[j];
+      float t = -(d * d) / (2.0f * s_var[j]);
+      t = t - s_log[j];
+      t = t - c_lp;
+      logp_acc += static_cast<double>(t);
+      // torch kl_divergence(Normal(old), Normal(new)) = 0.5 * (var_ratio + t1 - 1 - log(var_ratio))
+      const float q = osd[j] / s_std[j];
+      const float vr = q * q;
+      const float e = (omu[j] - mu[j]) / s_std[j];
+      const float t1 = e * e;
+      kl += 0.5f * (((vr + t1) - 1.0f) - logf(vr));
+    }
+    const float logp = static_cast<float>(logp_acc);
+    const float old_logp = a.old_logp[r * a.ld_batch];
+    const float adv = a.advantages[r * a.ld_batch];
+    const float ratio = expf(logp - old_logp);
+    const float nadv = -adv;
+    const float s1 = nadv * ratio;
+    const float rc = fminf(fmaxf(ratio, p.ratio_lo), p.ratio_hi);
+    const float s2 = nadv * rc;
+    surr = fmaxf(s1, s2);
+    // d surrogate_loss / d ratio with torch's max / clamp conventions
+    const float gs = p.inv_rows_surr;
+    const float ga = s1 > s2 ? gs : (s1 == s2 ? gs * 0.5f : 0.0f);
+    const float gb = s2 > s1 ? gs : (s1 == s2 ? gs * 0.5f : 0.0f);
+    const bool in_clip = (ratio >= p.ratio_lo) && (ratio <= p.ratio_hi);
+    const float g_ratio = ga * nadv + (in_clip ? gb * nadv : 0.0f);
+    g_logp = g_ratio * ratio;
+
+    // value loss
+    const float v = a.value[r * a.ld_value];
+    const float v_old = a.old_values[r * a.ld_batch];
+    const float ret = a.returns[r * a.ld_batch];
+    const float gv = p.inv_rows_value;  // c_v / R
+    float dv;
+    if (a.use_clipped_value_loss) {
+      const float dvo = v - v_old;
+      const float dvc = fminf(fmaxf(dvo, p.vclip_lo), p.vclip_hi);
+      const float vc = v_old + dvc;
+      const float e1 = v - ret, e2 = vc - ret;
+      const float l1 = e1 * e1, l2 = e2 * e2;
+      vloss = fmaxf(l1, l2);
+      const float g1 = l1 > l2 ? gv : (l1 == l2 ? gv * 0.5f : 0.0f);
+      const float g2 = l2 > l1 ? gv : (l1 == l2 ? gv * 0.5f : 0.0f);
+      const bool in_vclip = (dvo >= p.vclip_lo) && (dvo <= p.vclip_hi);
+      dv = (g1 * 2.0f) * e1 + (in_vclip ? (g2 * 2.0f) * e2 : 0.0f);
+    } else {
+      const float e = ret - v;
+      vloss = e * e;
+      dv = -((gv * 2.0f) * e);
+    }
+    a.d_value[r * a.ld_dvalue] = dv;
+
+    float* dmu = a.d_mean + r * a.ld_dmean;
+    for (int j = 0; j < A; ++j) {
+      const float d = act[j] - mu[j];
+      dmu[j] = (g_logp * d) / s_var[j];
+    }
+  }
+
+  // block partials (fixed lane order -> deterministic)
+  const double ssum = wave_sum(live ? static_cast<double>(surr) : 0.0);
+  const double vsum = wave_sum(live ? static_cast<double>(vloss) : 0.0);
+  const double ksum = wave_sum(live ? static_cast<double>(kl) : 0.0);
+  if (threadIdx.x == 0) {
+    part[0] = ssum;
+    part[1] = vsum;
+    part[2] = ksum;
+  }
+  for (int j = 0; j < A; ++j) {
+    double c = 0.0;
+    if (live) {
+      const float d = a.actions[r * a.ld_batch + j] - a.mean[r * a.ld_mean + j];
+      // d logp / d log(std_j) = d^2 / var_j - 1
+      c = static_cast<double>(g_logp) * (static_cast<double>(d) * d / s_var[j] - 1.0);
+    }
+    c = wave_sum(c);
+    if (threadIdx.x == 0) part[kFixedCols + j] = c;
+  }
+}
+
+constexpr int kFinThreads = 256;
+
+__global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
+    const LossParams p, const double* __restrict__ partials, int nblocks, float* __restrict__ d_std_param,
+    ppo_device_state* __restrict__ state, int adaptive, float kl_hi, float kl_lo, double* __restrict__ trace) {
+  const int A = p.a.num_actions;
+  const int cols = kFixedCols + A;
+  __shared__ double s_red[kFinThreads / 64];
+  __shared__ double s_col[kFixedCols + PPO_MAX_ACTIONS];
+  // column sums: each thread strides the blocks in a fixed order, then a fixed wave/LDS tree
+  for (int c = 0; c < cols; ++c) {
+    double acc = 0.0;
+    for (int b = threadIdx.x; b < nblocks; b += kFinThreads) acc += partials[static_cast<int64_t>(b) * cols + c];
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double s = 0.0;
+      for (int w = 0; w < kFinThreads / 64; ++w) s += s_red[w];
+      s_col[c] = s;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double R = static_cast<double>(p.a.rows);
+    const float surrogate = static_cast<float>(s_col[0] / R);
+    const float value = static_cast<float>(s_col[1] / R);
+    const float kl_mean = static_cast<float>(s_col[2] / R);
+    double ent_acc = 0.0;  // every row's entropy is the same sum over actions; accumulate it in fp64
+    const float ec = static_cast<float>(kEntropyConst);
+    for (int j = 0; j < A; ++j) {
+      float sd, lg;
+      std_of(p, j, sd, lg);
+      ent_acc += static_cast<double>(ec + lg);
+    }
+    const float entropy = static_cast<float>(ent_acc);
+    double lr = state->learning_rate;
+    if (adaptive) {
+      if (kl_mean > kl_hi) {
+        lr = fmax(1e-5, lr / 1.5);
+      } else if (kl_mean < kl_lo && kl_mean > 0.0f) {
+        lr = fmin(1e-2, lr * 1.5);
+      }
+      state->learning_rate = lr;
+    }
+    state->sum_surrogate_loss += static_cast<double>(surrogate);
+    state->sum_value_loss += static_cast<double>(value);
+    state->sum_entropy += static_cast<double>(entropy);
+    state->last_kl_mean = kl_mean;
+    state->last_surrogate_loss = surrogate;
+    state->last_value_loss = value;
+    state->last_entropy = entropy;
+    if (trace != nullptr) {
+      double* t = trace + 5 * static_cast<int64_t>(state->num_minibatches);
+      t[0] = kl_mean;
+      t[1] = lr;
+      t[2] = surrogate;
+      t[3] = value;
+      t[4] = entropy;
+    }
+    state->num_minibatches += 1;
+  }
+  // std-parameter gradient: d/dlog(std) = sum_r g_logp (d^2/var - 1) - c_e (entropy), then the clamp mask and
+  // the chain rule of the parameterisation.
+  const float c_e = static_cast<float>(p.a.entropy_coef);
+  for (int j = threadIdx.x; j < A; j += kFinThreads) {
+    const float q = p.a.std_param[j];
+    const bool inside = (q >= p.std_lo) && (q <= p.std_hi);
+    float sd, lg;
+    std_of(p, j, sd, lg);
+    const double dlog = s_col[kFixedCols + j] - static_cast<double>(c_e);
+    double g = (p.a.std_type == PPO_STD_LOG) ? dlog : dlog / static_cast<double>(sd);
+    d_std_param[j] = inside ? static_cast<float>(g) : 0.0f;
+  }
+}
+
+int64_t loss_blocks(int64_t rows) { return ceil_div(rows, kLossThreads); }
+
+int make_params(const ppo_loss_args* args, LossParams& p, const char* who) {
+  PPO_REQUIRE(args != nullptr, "%s: null args", who);
+  const ppo_loss_args& a = *args;
+  PPO_REQUIRE(a.rows > 0 && a.rows <= (int64_t)INT32_MAX * kLossThreads, "%s: rows=%lld", who, (long long)a.rows);
+  PPO_REQUIRE(a.num_actions > 0 && a.num_actions <= PPO_MAX_ACTIONS, "%s: num_actions=%d outside [1, %d]", who,
+              a.num_actions, PPO_MAX_ACTIONS);
+  PPO_REQUIRE(a.std_type == PPO_STD_LOG || a.std_type == PPO_STD_SCALAR, "%s: std_type=%d", who, a.std_type);
+  PPO_REQUIRE(a.mean && a.value && a.actions && a.old_mean && a.old_std && a.old_logp && a.advantages &&
+                  a.old_values && a.returns && a.std_param && a.d_mean && a.d_value,
+              "%s: null pointer in args", who);
+  PPO_REQUIRE(a.ld_mean >= a.num_actions && a.ld_dmean >= a.num_actions && a.ld_batch >= 1 && a.ld_value >= 1 &&
+                  a.ld_dvalue >= 1,
+              "%s: bad leading dimension", who);
+  p.a = a;
+  p.ratio_lo = static_cast<float>(1.0 - a.clip_param);
+  p.ratio_hi = static_cast<float>(1.0 + a.clip_param);
+  p.vclip_lo = static_cast<float>(-a.clip_param);
+  p.vclip_hi = static_cast<float>(a.clip_param);
+  p.c_v = static_cast<float>(a.value_loss_coef);
+  const float rows_f = static_cast<float>(a.rows);
+  p.inv_rows_surr = 1.0f / rows_f;
+  p.inv_rows_value = p.c_v / rows_f;
+  p.std_lo = static_cast<float>(a.std_lo);
+  p.std_hi = static_cast<float>(a.std_hi);
+  return PPO_OK;
+}
+
+}  // namespace
+}  // namespace ppo
+
+using namespace ppo;
+
+extern "C" size_t ppo_loss_workspace_bytes(int64_t rows, int32_t num_actions) {
+  if (rows <= 0 || num_actions <= 0 || num_actions > PPO_MAX_ACTIONS) return 0;
+  return sizeof(double) * static_cast<size_t>(loss_blocks(rows)) * (kFixedCols + num_actions);
+}
+
+extern "C" int ppo_gauss_ppo_loss(const ppo_loss_args* args, void* workspace, size_t workspace_bytes,
+                                  ppo_stream_t stream) {
+  LossParams p{};
+  int rc = make_params(args, p, "ppo_gauss_ppo_loss");
+  if (rc != PPO_OK) return rc;
+  const size_t need = ppo_loss_workspace_bytes(args->rows, args->num_actions);
+  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_gauss_ppo_loss: workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  const int64_t blocks = loss_blocks(args->rows);
+  hipLaunchKernelGGL(ppo_loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kLossThreads), 0,
+                     static_cast<hipStream_t>(stream), p, static_cast<double*>(workspace));
+  return check_launch("ppo_loss_kernel");
+}
+
+extern "C" int ppo_loss_finalize(const ppo_loss_args* args, const void* workspace, size_t workspace_bytes,
+                                 float* d_std_param, ppo_device_state* state, int32_t adaptive, double desired_kl,
+                                 double* trace, ppo_stream_t stream) {
+  LossParams p{};
+  int rc = make_params(args, p, "ppo_loss_finalize");
+  if (rc != PPO_OK) return rc;
+  const size_t need = ppo_loss_workspace_bytes(args->rows, args->num_actions);
+  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_loss_finalize: workspace too small");
+  PPO_REQUIRE(d_std_param != nullptr && state != nullptr, "ppo_loss_finalize: null pointer");
+  const int64_t blocks = loss_blocks(args->rows);
+  PPO_REQUIRE(blocks <= INT32_MAX, "ppo_loss_finalize: too many rows");
+  // upstream compares the fp32 kl_mean with the Python floats desired_kl*2 and desired_kl/2, which torch rounds
+  // to fp32 before comparing.
+  const float kl_hi = static_cast<float>(desired_kl * 2.0);
+  const float kl_lo = static_cast<float>(desired_kl / 2.0);
+  hipLaunchKernelGGL(ppo_loss_finalize_kernel, dim3(1), dim3(kFinThreads), 0, static_cast<hipStream_t>(stream), p,
+                     static_cast<const double*>(workspace), static_cast<int>(blocks), d_std_param, state,
+                     adaptive ? 1 : 0, kl_hi, kl_lo, trace);
+  return check_launch("ppo_loss_finalize_kernel");
+}

@@ -1,0 +1,162 @@
+// A12 + A13: per-group gradient-norm clipping (torch.nn.utils.clip_grad_norm_, rsl_rl/algorithms/ppo.py:309-310)
+// fused with Adam (torch.optim.Adam, single-tensor path, ppo.py:311) over flat parameter / gradient / moment
+// buffers.  Two launches:
+//   1. sum of squares of the gradient, one fp64 partial per 4096-element chunk (chunks never straddle groups);
+//   2. every block re-reduces its group's partials in the same fixed order (so all blocks agree bit for bit),
+//      derives the clip coefficient and streams p, g, m, v once: 16 B read + 12 B written per parameter
+//      (+4 B rewriting the clipped gradient, which upstream leaves in .grad).
+// The element update follows torch's fp32 operation order with contraction disabled.
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace ppo {
+namespace {
+
+constexpr int kAdamThreads = 256;
+constexpr int kChunk = 4096;
+
+struct GroupTable {
+  int64_t begin[PPO_MAX_PARAM_GROUPS + 1];
+  int32_t first_chunk[PPO_MAX_PARAM_GROUPS + 1];
+  int32_t num_groups;
+};
+
+__device__ inline int group_of_chunk(const GroupTable& t, int chunk) {
+  int g = 0;
+#pragma unroll
+  for (int i = 1; i < PPO_MAX_PARAM_GROUPS; ++i)
+    if (i < t.num_groups && chunk >= t.first_chunk[i]) g = i;
+  return g;
+}
+
+__device__ inline double block_sum256(double x, double* red) {
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_down(x, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  double s = 0.0;
+  for (int w = 0; w < kAdamThreads / 64; ++w) s += red[w];
+  __syncthreads();
+  return s;  // same value in every thread
+}
+
+__global__ __launch_bounds__(kAdamThreads) void grad_sqnorm_kernel(const float* __restrict__ grads, GroupTable t,
+                                                                   double* __restrict__ partials) {
+  __shared__ double red[kAdamThreads / 64];
+  const int chunk = blockIdx.x;
+  const int g = group_of_chunk(t, chunk);
+  const int64_t lo = t.begin[g] + static_cast<int64_t>(chunk - t.first_chunk[g]) * kChunk;
+  const int64_t hi = min(lo + kChunk, t.begin[g + 1]);
+  double acc = 0.0;
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
+    const double v = grads[i];
+    acc += v * v;
+  }
+  const double s = block_sum256(acc, red);
+  if (threadIdx.x == 0) partials[chunk] = s;
+}
+
+struct AdamScalars {
+  float max_norm, w1, b2, c2, eps, bc2_sqrt;
+  double bc1;
+};
+
+__global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ params, float* __restrict__ grads,
+                                                            float* __restrict__ exp_avg,
+                                                            float* __restrict__ exp_avg_sq, GroupTable t,
+                                                            AdamScalars s, const double* __restrict__ partials,
+                                                            ppo_device_state* __restrict__ state) {
+  __shared__ double red[kAdamThreads / 64];
+  const int chunk = blockIdx.x;
+  const int g = group_of_chunk(t, chunk);
+  double acc = 0.0;
+  for (int c = t.first_chunk[g] + threadIdx.x; c < t.first_chunk[g + 1]; c += kAdamThreads) acc += partials[c];
+  const double sq = block_sum256(acc, red);
+  const float total = static_cast<float>(sqrt(sq));
+  const float coef = fminf(s.max_norm / (total + 1e-6f), 1.0f);
+  const double lr = state->learning_rate;
+  const float neg_step = static_cast<float>(-(lr / s.bc1));
+  if (chunk == t.first_chunk[g] && threadIdx.x == 0 && g < 4) {
+    state->total_norm[g] = total;
+    state->clip_coef[g] = coef;
+  }
+  const int64_t lo = t.begin[g] + static_cast<int64_t>(chunk - t.first_chunk[g]) * kChunk;
+  const int64_t hi = min(lo + kChunk, t.begin[g + 1]);
+  for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
+    const float gr = grads[i] * coef;
+    grads[i] = gr;
+    float m = exp_avg[i];
+    m = m + s.w1 * (gr - m);
+    float v = exp_avg_sq[i];
+    v = v * s.b2;
+    v = v + (s.c2 * gr) * gr;
+    const float denom = sqrtf(v) / s.bc2_sqrt + s.eps;
+    params[i] = params[i] + (neg_step * m) / denom;
+    exp_avg[i] = m;
+    exp_avg_sq[i] = v;
+  }
+}
+
+int build_table(const int64_t* group_begin, int num_groups, GroupTable& t, int& chunks) {
+  PPO_REQUIRE(group_begin != nullptr && num_groups >= 1 && num_groups <= PPO_MAX_PARAM_GROUPS,
+              "ppo_adam_step: num_groups=%d outside [1, %d]", num_groups, PPO_MAX_PARAM_GROUPS);
+  t = GroupTable{};
+  t.num_groups = num_groups;
+  int64_t c = 0;
+  for (int g = 0; g <= num_groups; ++g) {
+    t.begin[g] = group_begin[g];
+    if (g > 0) PPO_REQUIRE(group_begin[g] > group_begin[g - 1], "ppo_adam_step: group %d is empty", g - 1);
+  }
+  PPO_REQUIRE(group_begin[0] == 0, "ppo_adam_step: group_begin[0] must be 0");
+  for (int g = 0; g < num_groups; ++g) {
+    t.first_chunk[g] = static_cast<int32_t>(c);
+    c += ceil_div(group_begin[g + 1] - group_begin[g], kChunk);
+    PPO_REQUIRE(c < INT32_MAX, "ppo_adam_step: too many parameters");
+  }
+  t.first_chunk[num_groups] = static_cast<int32_t>(c);
+  for (int g = num_groups + 1; g <= PPO_MAX_PARAM_GROUPS; ++g) t.first_chunk[g] = INT32_MAX;
+  chunks = static_cast<int>(c);
+  return PPO_OK;
+}
+
+}  // namespace
+}  // namespace ppo
+
+using namespace ppo;
+
+extern "C" size_t ppo_adam_workspace_bytes(int64_t num_params) {
+  if (num_params <= 0) return 0;
+  return sizeof(double) * static_cast<size_t>(ceil_div(num_params, kChunk) + PPO_MAX_PARAM_GROUPS);
+}
+
+extern "C" int ppo_adam_step(float* params, float* grads, float* exp_avg, float* exp_avg_sq,
+                             const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1,
+                             double beta2, double eps, double bc1, double bc2_sqrt, ppo_device_state* state,
+                             void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
+  PPO_REQUIRE(params && grads && exp_avg && exp_avg_sq && state, "ppo_adam_step: null pointer");
+  GroupTable t;
+  int chunks = 0;
+  int rc = build_table(group_begin, num_groups, t, chunks);
+  if (rc != PPO_OK) return rc;
+  const size_t need = ppo_adam_workspace_bytes(group_begin[num_groups]);
+  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_adam_step: workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  PPO_REQUIRE(bc1 > 0.0 && bc2_sqrt > 0.0, "ppo_adam_step: bias corrections must be positive");
+  AdamScalars s;
+  // torch passes max_norm, 1 - beta1, beta2, 1 - beta2 and eps as Python doubles that the fp32 kernels round once
+  s.max_norm = static_cast<float>(max_grad_norm);
+  s.w1 = static_cast<float>(1.0 - beta1);
+  s.b2 = static_cast<float>(beta2);
+  s.c2 = static_cast<float>(1.0 - beta2);
+  s.eps = static_cast<float>(eps);
+  s.bc1 = bc1;
+  s.bc2_sqrt = static_cast<float>(bc2_sqrt);
+  double* partials = static_cast<double*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(grad_sqnorm_kernel, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, partials);
+  rc = check_launch("grad_sqnorm_kernel");
+  if (rc != PPO_OK) return rc;
+  hipLaunchKernelGGL(adam_kernel, dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg, exp_avg_sq, t, s,
+                     partials, state);
+  return check_launch("adam_kernel");
+}

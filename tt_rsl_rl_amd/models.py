@@ -1,0 +1,391 @@
+"""Actor / critic models with upstream rsl_rl's constructor signature, state_dict keys and parameter order.
+
+Mirrors rsl_rl/models/mlp_model.py:19-193, rsl_rl/modules/mlp.py:16-95, rsl_rl/modules/distribution.py:132-238
+and rsl_rl/modules/normalization.py:15-84.  Parameters are ordinary ``nn.Parameter`` objects (default
+``nn.Linear`` initialisation drawn from the global CPU generator in upstream's order, so a given seed yields
+upstream's initial weights); once the PPO plugin binds them they are views into flat device buffers.  The forward
+pass on the GPU runs the HIP kernels of libppo_hip.so; CPU tensors are rejected.
+"""
+
+from __future__ import annotations
+
+import copy
+from typing import Mapping
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from . import _lib as L
+from . import ops
+
+_ACTIVATIONS = {
+    "elu": nn.ELU, "selu": nn.SELU, "relu": nn.ReLU, "crelu": nn.CELU, "lrelu": nn.LeakyReLU, "tanh": nn.Tanh,
+    "sigmoid": nn.Sigmoid, "softplus": nn.Softplus, "gelu": nn.GELU, "swish": nn.SiLU, "mish": nn.Mish,
+    "identity": nn.Identity,
+}
+
+
+def resolve_nn_activation(name: str) -> nn.Module:
+    """rsl_rl/utils/utils.py:34-68."""
+    key = name.lower()
+    if key not in _ACTIVATIONS:
+        raise ValueError(f"Invalid activation function '{name}'. Valid activations are: {list(_ACTIVATIONS)}")
+    return _ACTIVATIONS[key]()
+
+
+def _require_gpu(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{what}: the tt_rsl_rl_amd models run on the GPU through libppo_hip.so only")
+
+
+class EmpiricalNormalization(nn.Module):
+    """rsl_rl/modules/normalization.py:15-84: buffers ``_mean``, ``_var``, ``_std`` [1, D] and ``count``."""
+
+    def __init__(self, shape, eps: float = 1e-2, until: int | None = None) -> None:
+        super().__init__()
+        self.eps = eps
+        self.until = until
+        self.register_buffer("_mean", torch.zeros(shape).unsqueeze(0))
+        self.register_buffer("_var", torch.ones(shape).unsqueeze(0))
+        self.register_buffer("_std", torch.ones(shape).unsqueeze(0))
+        self.register_buffer("count", torch.tensor(0, dtype=torch.long))
+        self._host_count = 0  # mirror of `count` for the `until` check without a device sync
+        self._ws = ops.Workspace()
+
+    @property
+    def mean(self) -> torch.Tensor:
+        return self._mean.squeeze(0).clone()
+
+    @property
+    def std(self) -> torch.Tensor:
+        return self._std.squeeze(0).clone()
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        super()._load_from_state_dict(*args, **kwargs)
+        self._host_count = int(self.count)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        _require_gpu(x, "EmpiricalNormalization.forward")
+        x = x.contiguous()
+        y = torch.empty_like(x)
+        ops.obs_normalize(x.view(-1, x.shape[-1]), y.view(-1, x.shape[-1]), self._mean.view(-1), self._std.view(-1),
+                          self.eps)
+        return y
+
+    def update_columns(self, columns: list[torch.Tensor]) -> None:
+        """normalization.py:51-78 on the concatenation of row-major column blocks (no concatenated copy)."""
+        if not self.training:
+            return
+        if self.until is not None and self._host_count >= self.until:
+            return
+        self._ws.device = columns[0].device
+        ops.normalizer_update(columns, self._mean.view(-1), self._var.view(-1), self._std.view(-1), self.count,
+                              self._ws)
+        self._host_count += columns[0].shape[0]
+
+    def update(self, x: torch.Tensor) -> None:
+        _require_gpu(x, "EmpiricalNormalization.update")
+        self.update_columns([x.reshape(-1, x.shape[-1])])
+
+    def inverse(self, y: torch.Tensor) -> torch.Tensor:
+        return y * (self._std + self.eps) + self._mean
+
+
+class GaussianDistribution(nn.Module):
+    """rsl_rl/modules/distribution.py:132-238 (state-independent std, ``scalar`` or ``log`` parameterisation)."""
+
+    def __init__(self, output_dim: int, init_std: float = 1.0, std_range=(1e-6, 1e6), std_type: str = "scalar",
+                 learn_std: bool = True) -> None:
+        super().__init__()
+        self.output_dim = output_dim
+        self.std_type = std_type
+        if std_type == "scalar":
+            self.std_param = nn.Parameter(init_std * torch.ones(output_dim), requires_grad=learn_std)
+        elif std_type == "log":
+            self.log_std_param = nn.Parameter(torch.log(init_std * torch.ones(output_dim)), requires_grad=learn_std)
+        else:
+            raise ValueError(f"Unknown standard deviation type: {std_type}. Should be 'scalar' or 'log'.")
+        self.std_range = list(std_range)
+        self.std_range[0] = max(self.std_range[0], 1e-6)
+        self.log_std_range = [float(np.log(self.std_range[0])), float(np.log(self.std_range[1]))]
+        self._mean: torch.Tensor | None = None
+        self._std: torch.Tensor | None = None
+
+    # parameter in its own space and the clamp bounds that go with it
+    @property
+    def param(self) -> nn.Parameter:
+        return self.std_param if self.std_type == "scalar" else self.log_std_param
+
+    @property
+    def kernel_std_type(self) -> int:
+        return L.PPO_STD_SCALAR if self.std_type == "scalar" else L.PPO_STD_LOG
+
+    @property
+    def param_range(self) -> tuple[float, float]:
+        r = self.std_range if self.std_type == "scalar" else self.log_std_range
+        return float(r[0]), float(r[1])
+
+    @property
+    def input_dim(self) -> int:
+        return self.output_dim
+
+    def init_mlp_weights(self, mlp: nn.Module) -> None:
+        pass
+
+    def sample_from(self, mean: torch.Tensor, noise: torch.Tensor | None, actions: torch.Tensor,
+                    logp: torch.Tensor | None, std_out: torch.Tensor | None) -> None:
+        lo, hi = self.param_range
+        L.call("ppo_gauss_sample", mean.data_ptr(), mean.stride(0), self.param.data_ptr(), self.kernel_std_type, lo, hi,
+               None if noise is None else noise.data_ptr(), 0 if noise is None else noise.stride(0),
+               actions.data_ptr(), actions.stride(0), None if logp is None else logp.data_ptr(),
+               None if std_out is None else std_out.data_ptr(), 0 if std_out is None else std_out.stride(0),
+               mean.shape[0], self.output_dim, torch.cuda.current_stream().cuda_stream)
+
+    def update(self, mean: torch.Tensor) -> None:
+        """Record the distribution of the last forward (the std broadcast per row, as upstream's Normal does)."""
+        self._mean = mean
+        std = torch.empty_like(mean)
+        scratch = torch.empty_like(mean)
+        self.sample_from(mean, torch.zeros_like(mean), scratch, None, std)
+        self._std = std
+
+    def sample(self) -> torch.Tensor:
+        noise = torch.randn_like(self._mean)
+        actions = torch.empty_like(self._mean)
+        self.sample_from(self._mean, noise, actions, None, None)
+        return actions
+
+    @property
+    def mean(self) -> torch.Tensor:
+        return self._mean
+
+    @property
+    def std(self) -> torch.Tensor:
+        return self._std
+
+    @property
+    def params(self) -> tuple[torch.Tensor, torch.Tensor]:
+        return (self._mean, self._std)
+
+    @property
+    def entropy(self) -> torch.Tensor:
+        # identical for every row: sum_a 0.5 + 0.5 log(2 pi) + log(std_a)
+        return (0.5 + 0.5 * np.log(2 * np.pi) + torch.log(self._std)).sum(dim=-1)
+
+    def log_prob(self, outputs: torch.Tensor) -> torch.Tensor:
+        outputs = outputs.contiguous()
+        logp = torch.empty(outputs.shape[0], device=outputs.device)
+        self.sample_from(self._mean, None, outputs.clone(), logp, None)
+        return logp
+
+    def deterministic_output(self, mlp_output: torch.Tensor) -> torch.Tensor:
+        return mlp_output
+
+
+class _ForwardBuffers:
+    """Grow-only activation buffers for rollout-side forwards (no per-call allocation in steady state)."""
+
+    def __init__(self) -> None:
+        self.rows = 0
+        self.bufs: list[torch.Tensor] = []
+
+    def get(self, rows: int, widths: list[int], device) -> list[torch.Tensor]:
+        if rows > self.rows or len(self.bufs) != len(widths) or self.bufs[0].device != torch.device(device):
+            cap = max(rows, self.rows)
+            self.bufs = [torch.empty(cap, w, device=device) for w in widths]
+            self.rows = cap
+        return [b[:rows] for b in self.bufs]
+
+
+class MLPModel(nn.Module):
+    """rsl_rl/models/mlp_model.py:19-193 (same signature; registration order normalizer, distribution, mlp)."""
+
+    is_recurrent: bool = False
+
+    def __init__(self, obs: Mapping, obs_groups: dict, obs_set: str, output_dim: int, hidden_dims=(256, 256, 256),
+                 activation: str = "elu", obs_normalization: bool = False, distribution_cfg: dict | None = None) -> None:
+        super().__init__()
+        self.obs_groups, self.obs_dim = self._get_obs_dim(obs, obs_groups, obs_set)
+        self.obs_normalization = obs_normalization
+        self.obs_normalizer = EmpiricalNormalization(self.obs_dim) if obs_normalization else nn.Identity()
+        if distribution_cfg is not None:
+            cfg = dict(distribution_cfg)
+            name = cfg.pop("class_name")
+            short = name.split(":")[-1].split(".")[-1] if isinstance(name, str) else name.__name__
+            if short != "GaussianDistribution":
+                raise NotImplementedError(f"distribution {name}: only GaussianDistribution is on the HIP path")
+            self.distribution: GaussianDistribution | None = GaussianDistribution(output_dim, **cfg)
+            mlp_out = self.distribution.input_dim
+        else:
+            self.distribution = None
+            mlp_out = output_dim
+        if activation.lower() != "elu":
+            raise NotImplementedError(f"activation '{activation}': the HIP MLP kernels implement ELU")
+        act = resolve_nn_activation(activation)
+        dims = [self._get_latent_dim() if d == -1 else d for d in hidden_dims]
+        layers: list[nn.Module] = [nn.Linear(self._get_latent_dim(), dims[0]), act]
+        for a, b in zip(dims[:-1], dims[1:]):
+            layers += [nn.Linear(a, b), act]
+        layers.append(nn.Linear(dims[-1], mlp_out))
+        self.mlp = nn.Sequential(*layers)
+        self.output_dim = mlp_out
+        self._fwd = _ForwardBuffers()
+
+    # -- structure ---------------------------------------------------------------------------------------------------
+    def _get_obs_dim(self, obs: Mapping, obs_groups: dict, obs_set: str) -> tuple[list[str], int]:
+        groups = list(obs_groups[obs_set])
+        dim = 0
+        for g in groups:
+            if len(obs[g].shape) != 2:
+                raise ValueError(f"The MLP model only supports 1D observations, got shape {obs[g].shape} for '{g}'.")
+            dim += obs[g].shape[-1]
+        return groups, dim
+
+    def _get_latent_dim(self) -> int:
+        return self.obs_dim
+
+    @property
+    def linears(self) -> list[nn.Linear]:
+        return [m for m in self.mlp if isinstance(m, nn.Linear)]
+
+    # -- forward on the GPU ------------------------------------------------------------------------------------------
+    def latent_into(self, obs: Mapping, out: torch.Tensor) -> None:
+        """Concatenate this model's observation groups into ``out`` [rows, obs_dim], normalised if enabled."""
+        col = 0
+        norm = self.obs_normalizer if self.obs_normalization else None
+        for g in self.obs_groups:
+            x = obs[g]
+            _require_gpu(x, "MLPModel.forward")
+            x = x.reshape(-1, x.shape[-1])
+            if x.stride(-1) != 1:
+                x = x.contiguous()
+            w = x.shape[1]
+            dst = out[:, col:col + w]
+            if norm is not None:
+                ops.obs_normalize(x, dst, norm._mean.view(-1)[col:col + w], norm._std.view(-1)[col:col + w], norm.eps)
+            else:
+                dst.copy_(x)
+            col += w
+
+    def mlp_forward(self, latent: torch.Tensor) -> torch.Tensor:
+        rows = latent.shape[0]
+        lin = self.linears
+        widths = [l.out_features for l in lin[:-1] for _ in (0, 1)] + [lin[-1].out_features]
+        bufs = self._fwd.get(rows, widths, latent.device)
+        x = latent
+        for i, l in enumerate(lin[:-1]):
+            z, h = bufs[2 * i], bufs[2 * i + 1]
+            ops.linear_fwd([(x, l.weight, l.bias, z, h)], rows, elu=True)
+            x = h
+        out = torch.empty(rows, lin[-1].out_features, device=latent.device)
+        ops.linear_fwd([(x, lin[-1].weight, lin[-1].bias, out, None)], rows, elu=False)
+        return out
+
+    def get_latent(self, obs: Mapping, masks=None, hidden_state=None) -> torch.Tensor:
+        first = obs[self.obs_groups[0]]
+        latent = torch.empty(first.shape[0], self.obs_dim, device=first.device)
+        self.latent_into(obs, latent)
+        return latent
+
+    def forward(self, obs: Mapping, masks=None, hidden_state=None, stochastic_output: bool = False) -> torch.Tensor:
+        if masks is not None:
+            raise NotImplementedError("padded (recurrent) batches are not supported by the MLP HIP path")
+        out = self.mlp_forward(self.get_latent(obs))
+        if self.distribution is not None:
+            if stochastic_output:
+                self.distribution.update(out)
+                return self.distribution.sample()
+            return self.distribution.deterministic_output(out)
+        return out
+
+    # -- upstream model API ------------------------------------------------------------------------------------------
+    def reset(self, dones=None, hidden_state=None) -> None:
+        pass
+
+    def get_hidden_state(self):
+        return None
+
+    def detach_hidden_state(self, dones=None) -> None:
+        pass
+
+    @property
+    def output_mean(self) -> torch.Tensor:
+        return self.distribution.mean
+
+    @property
+    def output_std(self) -> torch.Tensor:
+        return self.distribution.std
+
+    @property
+    def output_entropy(self) -> torch.Tensor:
+        return self.distribution.entropy
+
+    @property
+    def output_distribution_params(self) -> tuple[torch.Tensor, ...]:
+        return self.distribution.params
+
+    def get_output_log_prob(self, outputs: torch.Tensor) -> torch.Tensor:
+        return self.distribution.log_prob(outputs)
+
+    def get_kl_divergence(self, old_params, new_params) -> torch.Tensor:
+        (om, os_), (nm, ns) = old_params, new_params
+        r = (os_ / ns).pow(2)
+        t1 = ((om - nm) / ns).pow(2)
+        return (0.5 * (r + t1 - 1 - r.log())).sum(dim=-1)
+
+    def update_normalization(self, obs: Mapping) -> None:
+        if self.obs_normalization and self.obs_groups:
+            cols = []
+            for g in self.obs_groups:
+                x = obs[g]
+                cols.append(x.reshape(-1, x.shape[-1]))
+            self.obs_normalizer.update_columns(cols)
+
+    def as_jit(self) -> nn.Module:
+        """Export copy in plain torch modules (rsl_rl/models/mlp_model.py:196-218) -- export, not the hot path."""
+        return _ExportMLP(self)
+
+    def as_onnx(self) -> nn.Module:
+        return _ExportMLP(self)
+
+
+class _TorchNormalizer(nn.Module):
+    def __init__(self, norm: EmpiricalNormalization) -> None:
+        super().__init__()
+        self.eps = norm.eps
+        self.register_buffer("_mean", norm._mean.detach().clone().cpu())
+        self.register_buffer("_std", norm._std.detach().clone().cpu())
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return (x - self._mean) / (self._std + self.eps)
+
+
+class _ExportMLP(nn.Module):
+    """Deterministic export copy (mean output) with plain torch modules, for TorchScript / ONNX."""
+
+    is_recurrent = False
+
+    def __init__(self, model: MLPModel) -> None:
+        super().__init__()
+        self.obs_normalizer = _TorchNormalizer(model.obs_normalizer) if model.obs_normalization else nn.Identity()
+        self.mlp = copy.deepcopy(model.mlp).cpu()
+        self.input_size = model.obs_dim
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.mlp(self.obs_normalizer(x))
+
+    @torch.jit.export
+    def reset(self) -> None:
+        pass
+
+    def get_dummy_inputs(self) -> tuple[torch.Tensor]:
+        return (torch.zeros(1, self.input_size),)
+
+    @property
+    def input_names(self) -> list[str]:
+        return ["obs"]
+
+    @property
+    def output_names(self) -> list[str]:
+        return ["actions"]

@@ -1,0 +1,317 @@
+"""Tensor-level wrappers over the C ABI of libppo_hip.so.
+
+Each function validates its torch tensors (device, dtype, shape, strides), then calls the matching C entry point
+with raw device pointers and the current HIP stream.  Device memory and streams come from PyTorch; every
+arithmetic operation happens in the HIP kernels.  Nothing here falls back to torch or the CPU: tensors that are not
+on a GPU are rejected.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib as L
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dev(*tensors: torch.Tensor | None, dtype=torch.float32) -> None:
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("tt_rsl_rl_amd ops take GPU tensors only (no CPU path exists)")
+        if dtype is not None and t.dtype != dtype:
+            raise ValueError(f"expected {dtype}, got {t.dtype}")
+
+
+def _row_major(t: torch.Tensor, name: str) -> int:
+    """Leading dimension (floats) of a 2-D row-major view with unit column stride."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D view with unit column stride, got shape {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+    return max(t.stride(0), t.shape[1])
+
+
+class Workspace:
+    """Grow-only device scratch buffer (one per consumer), so steady-state calls allocate nothing."""
+
+    def __init__(self, device: torch.device | str | None = None) -> None:
+        self.device = device
+        self.buf: torch.Tensor | None = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        nbytes = max(int(nbytes), 256)
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device or "cuda")
+        return self.buf
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A1 / A2
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def gae(rewards, values, dones, last_values, returns, advantages, gamma: float, lam: float) -> None:
+    """rewards/values/returns/advantages: [T, N] (or [T, N, 1]) contiguous fp32; dones uint8 same shape."""
+    _dev(rewards, values, last_values, returns, advantages)
+    _dev(dones, dtype=torch.uint8)
+    T, N = rewards.shape[0], rewards.shape[1]
+    for t in (rewards, values, returns, advantages, dones):
+        if t.numel() != T * N or not t.is_contiguous():
+            raise ValueError("gae: every [T, N] input must be contiguous with T*N elements")
+    if last_values.numel() != N or not last_values.is_contiguous():
+        raise ValueError("gae: last_values must hold N contiguous values")
+    L.call("ppo_gae", _ptr(rewards), _ptr(values), _ptr(dones), _ptr(last_values), _ptr(returns), _ptr(advantages),
+           T, N, float(gamma), float(lam), _stream())
+
+
+def adv_normalize(x: torch.Tensor, out: torch.Tensor, n: int, in_stride: int = 1, out_stride: int = 1,
+                  eps: float = 1e-8, ws: Workspace | None = None) -> None:
+    _dev(x, out)
+    lib = L.load()
+    nbytes = lib.ppo_adv_normalize_workspace_bytes(n)
+    buf = (ws or Workspace(x.device)).get(nbytes)
+    L.call("ppo_adv_normalize", _ptr(x), in_stride, _ptr(out), out_stride, n, float(eps), buf.data_ptr(), buf.numel(),
+           _stream())
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A5 / A7 forward
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+@dataclass
+class Segment:
+    src: torch.Tensor          # [src_rows, >= width] row-major view
+    dst_col: int
+    norm_mean: torch.Tensor | None = None
+    norm_std: torch.Tensor | None = None
+    norm_eps: float = 0.0
+
+
+def gather_rows(perm: torch.Tensor, segments: list[Segment], dst: torch.Tensor) -> None:
+    """dst[j, seg.dst_col : +width] = f(seg.src[perm[j]])  (f = identity or the obs normaliser)."""
+    _dev(dst)
+    _dev(perm, dtype=torch.int64)
+    if not perm.is_contiguous() or perm.dim() != 1:
+        raise ValueError("perm must be a contiguous int64 vector")
+    ld_dst = _row_major(dst, "dst")
+    if dst.shape[0] < perm.numel():
+        raise ValueError("dst has fewer rows than perm")
+    segs = []
+    src_rows = None
+    for s in segments:
+        _dev(s.src, s.norm_mean, s.norm_std)
+        ld = _row_major(s.src, "segment src")
+        src_rows = s.src.shape[0] if src_rows is None else min(src_rows, s.src.shape[0])
+        if s.norm_mean is not None and (s.norm_mean.numel() < s.src.shape[1] or s.norm_std is None
+                                        or s.norm_std.numel() < s.src.shape[1]):
+            raise ValueError("normaliser statistics narrower than the segment")
+        segs.append(L.GatherSegment(s.src.data_ptr(), ld, s.src.shape[1], s.dst_col, _ptr(s.norm_mean),
+                                    _ptr(s.norm_std), float(s.norm_eps), 0))
+    L.call("ppo_gather_rows", perm.data_ptr(), perm.numel(), int(src_rows), L.array(L.GatherSegment, segs), len(segs),
+           dst.data_ptr(), ld_dst, _stream())
+
+
+def obs_normalize(x: torch.Tensor, y: torch.Tensor, mean: torch.Tensor, std: torch.Tensor, eps: float) -> None:
+    _dev(x, y, mean, std)
+    ldx, ldy = _row_major(x, "x"), _row_major(y, "y")
+    if x.shape != y.shape or mean.numel() < x.shape[1] or std.numel() < x.shape[1]:
+        raise ValueError("obs_normalize: shape mismatch")
+    L.call("ppo_obs_normalize", x.data_ptr(), ldx, y.data_ptr(), ldy, x.shape[0], x.shape[1], mean.data_ptr(),
+           std.data_ptr(), float(eps), _stream())
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A6
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def _check_weight(w: torch.Tensor, b: torch.Tensor | None) -> tuple[int, int]:
+    if w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("weight must be a contiguous [out, in] matrix")
+    out_f, in_f = w.shape
+    if b is not None and (b.numel() != out_f or not b.is_contiguous()):
+        raise ValueError("bias must be a contiguous [out] vector")
+    return out_f, in_f
+
+
+def linear_fwd(problems: list[tuple], rows: int, elu: bool) -> None:
+    """problems: (x [rows, in], w [out, in], b [out], z [rows, out], h [rows, out] or None)."""
+    items = []
+    for x, w, b, z, h in problems:
+        _dev(x, w, b, z, h)
+        out_f, in_f = _check_weight(w, b)
+        ldx, ldz = _row_major(x, "x"), _row_major(z, "z")
+        if x.shape[0] < rows or z.shape[0] < rows or x.shape[1] < in_f or z.shape[1] < out_f:
+            raise ValueError("linear_fwd: activation buffers too small")
+        ldh = 0
+        if h is not None:
+            ldh = _row_major(h, "h")
+            if h.shape[0] < rows or h.shape[1] < out_f:
+                raise ValueError("linear_fwd: h too small")
+        elif elu:
+            raise ValueError("linear_fwd: ELU needs an h buffer")
+        items.append(L.LinearFwdProblem(x.data_ptr(), ldx, w.data_ptr(), b.data_ptr(), z.data_ptr(), ldz, _ptr(h),
+                                        ldh, in_f, out_f))
+    L.call("ppo_linear_fwd", L.array(L.LinearFwdProblem, items), len(items), rows,
+           L.PPO_ACT_ELU if elu else L.PPO_ACT_NONE, _stream())
+
+
+def linear_bwd_dx(problems: list[tuple], rows: int) -> None:
+    """problems: (dz [rows, out], w [out, in], z_prev [rows, in] or None, dz_prev [rows, in])."""
+    items = []
+    for dz, w, z_prev, dz_prev in problems:
+        _dev(dz, w, z_prev, dz_prev)
+        out_f, in_f = _check_weight(w, None)
+        lddz, ldo = _row_major(dz, "dz"), _row_major(dz_prev, "dz_prev")
+        ldzp = _row_major(z_prev, "z_prev") if z_prev is not None else 0
+        if dz.shape[0] < rows or dz_prev.shape[0] < rows or dz.shape[1] < out_f or dz_prev.shape[1] < in_f:
+            raise ValueError("linear_bwd_dx: buffers too small")
+        if z_prev is not None and (z_prev.shape[0] < rows or z_prev.shape[1] < in_f):
+            raise ValueError("linear_bwd_dx: z_prev too small")
+        items.append(L.LinearBwdDxProblem(dz.data_ptr(), lddz, w.data_ptr(), _ptr(z_prev), ldzp, dz_prev.data_ptr(),
+                                          ldo, in_f, out_f))
+    L.call("ppo_linear_bwd_dx", L.array(L.LinearBwdDxProblem, items), len(items), rows, _stream())
+
+
+def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:
+    """problems: (dz [rows, out], x [rows, in], dw [out, in], db [out])."""
+    items = []
+    for dz, x, dw, db in problems:
+        _dev(dz, x, dw, db)
+        out_f, in_f = _check_weight(dw, db)
+        lddz, ldx = _row_major(dz, "dz"), _row_major(x, "x")
+        if dz.shape[0] < rows or x.shape[0] < rows or dz.shape[1] < out_f or x.shape[1] < in_f:
+            raise ValueError("linear_bwd_dw: buffers too small")
+        items.append(L.LinearBwdDwProblem(dz.data_ptr(), lddz, x.data_ptr(), ldx, dw.data_ptr(), db.data_ptr(), in_f,
+                                          out_f))
+    arr = L.array(L.LinearBwdDwProblem, items)
+    nbytes = L.load().ppo_linear_bwd_dw_workspace_bytes(arr, len(items), rows)
+    if nbytes == 0:
+        raise ValueError("linear_bwd_dw: invalid problem set")
+    buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
+    L.call("ppo_linear_bwd_dw", arr, len(items), rows, buf.data_ptr(), buf.numel(), _stream())
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A7 update
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def normalizer_update(columns: list[torch.Tensor], mean: torch.Tensor, var: torch.Tensor, std: torch.Tensor,
+                      count: torch.Tensor, ws: Workspace | None = None) -> None:
+    """columns: row-major [rows, width_i] views whose concatenation is the model latent."""
+    _dev(mean, var, std, *columns)
+    _dev(count, dtype=torch.int64)
+    rows = columns[0].shape[0]
+    blocks = []
+    for c in columns:
+        if c.shape[0] != rows:
+            raise ValueError("normalizer_update: column blocks disagree on rows")
+        blocks.append(L.ColumnBlock(c.data_ptr(), _row_major(c, "column block"), c.shape[1], 0))
+    dim = sum(c.shape[1] for c in columns)
+    if mean.numel() != dim or var.numel() != dim or std.numel() != dim:
+        raise ValueError("normalizer_update: statistics width != concatenated width")
+    for t in (mean, var, std, count):
+        if not t.is_contiguous():
+            raise ValueError("normalizer_update: statistics must be contiguous")
+    nbytes = L.load().ppo_normalizer_update_workspace_bytes(rows, dim)
+    buf = (ws or Workspace(mean.device)).get(nbytes)
+    L.call("ppo_normalizer_update", L.array(L.ColumnBlock, blocks), len(blocks), rows, mean.data_ptr(),
+           var.data_ptr(), std.data_ptr(), count.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A8-A11 losses, A12-A13 optimiser
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def new_device_state(learning_rate: float, device) -> torch.Tensor:
+    st = torch.zeros(L.DEVICE_STATE_BYTES, dtype=torch.uint8, device=device)
+    reset_device_state(st, learning_rate)
+    return st
+
+
+def reset_device_state(st: torch.Tensor, learning_rate: float) -> None:
+    host = L.DeviceState()
+    host.learning_rate = float(learning_rate)
+    raw = torch.frombuffer(bytearray(bytes(host)), dtype=torch.uint8)
+    st.copy_(raw)
+
+
+def read_device_state(st: torch.Tensor) -> L.DeviceState:
+    raw = st.cpu().numpy().tobytes()
+    return L.DeviceState.from_buffer_copy(raw)
+
+
+def make_loss_args(rows: int, mean: torch.Tensor, value: torch.Tensor, batch: dict, std_param: torch.Tensor,
+                   std_type: int, std_lo: float, std_hi: float, clip_param: float, value_loss_coef: float,
+                   entropy_coef: float, use_clipped_value_loss: bool, d_mean: torch.Tensor,
+                   d_value: torch.Tensor) -> L.LossArgs:
+    """batch: dict of row-major views sharing one row stride: actions/old_mean/old_std [rows, A] and
+    old_logp/advantages/old_values/returns [rows] (columns of the packed table)."""
+    A = std_param.numel()
+    ld_batch = batch["ld"]
+    return L.LossArgs(
+        rows=rows, num_actions=A, std_type=std_type,
+        mean=mean.data_ptr(), ld_mean=_row_major(mean, "mean"),
+        value=value.data_ptr(), ld_value=value.stride(0),
+        actions=batch["actions"].data_ptr(), old_mean=batch["old_mean"].data_ptr(),
+        old_std=batch["old_std"].data_ptr(), old_logp=batch["old_logp"].data_ptr(),
+        advantages=batch["advantages"].data_ptr(), old_values=batch["old_values"].data_ptr(),
+        returns=batch["returns"].data_ptr(), ld_batch=ld_batch,
+        std_param=std_param.data_ptr(), std_lo=float(std_lo), std_hi=float(std_hi),
+        clip_param=float(clip_param), value_loss_coef=float(value_loss_coef), entropy_coef=float(entropy_coef),
+        use_clipped_value_loss=1 if use_clipped_value_loss else 0, reserved=0,
+        d_mean=d_mean.data_ptr(), ld_dmean=_row_major(d_mean, "d_mean"),
+        d_value=d_value.data_ptr(), ld_dvalue=d_value.stride(0),
+    )
+
+
+def ppo_loss(args: L.LossArgs, ws: torch.Tensor) -> None:
+    L.call("ppo_gauss_ppo_loss", C_ref(args), ws.data_ptr(), ws.numel(), _stream())
+
+
+def ppo_loss_finalize(args: L.LossArgs, ws: torch.Tensor, d_std_param: torch.Tensor, state: torch.Tensor,
+                      adaptive: bool, desired_kl: float, trace: torch.Tensor | None) -> None:
+    L.call("ppo_loss_finalize", C_ref(args), ws.data_ptr(), ws.numel(), d_std_param.data_ptr(), state.data_ptr(),
+           1 if adaptive else 0, float(desired_kl if desired_kl is not None else 0.0), _ptr(trace), _stream())
+
+
+def loss_workspace_bytes(rows: int, num_actions: int) -> int:
+    return int(L.load().ppo_loss_workspace_bytes(rows, num_actions))
+
+
+def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max_grad_norm: float, beta1: float,
+              beta2: float, eps: float, bc1: float, bc2_sqrt: float, state: torch.Tensor, ws: Workspace) -> None:
+    _dev(params, grads, exp_avg, exp_avg_sq)
+    n = params.numel()
+    for t in (grads, exp_avg, exp_avg_sq):
+        if t.numel() != n or not t.is_contiguous():
+            raise ValueError("adam_step: flat buffers must be contiguous and equally long")
+    if group_begin.device.type != "cpu" or group_begin.dtype != torch.int64:
+        raise ValueError("adam_step: group_begin is a host int64 tensor")
+    groups = group_begin.numel() - 1
+    if int(group_begin[-1]) != n:
+        raise ValueError("adam_step: the groups must cover the flat buffer")
+    nbytes = L.load().ppo_adam_workspace_bytes(n)
+    buf = ws.get(nbytes)
+    L.call("ppo_adam_step", params.data_ptr(), grads.data_ptr(), exp_avg.data_ptr(), exp_avg_sq.data_ptr(),
+           group_begin.data_ptr(), groups, float(max_grad_norm), float(beta1), float(beta2), float(eps), float(bc1),
+           float(bc2_sqrt), state.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
+
+
+def C_ref(struct):
+    import ctypes
+
+    return ctypes.byref(struct)

@@ -1,0 +1,369 @@
+"""PPO plugin for upstream rsl_rl's OnPolicyRunner, running the update on MI355X through libppo_hip.so.
+
+Selected with ``cfg["algorithm"]["class_name"] = "tt_rsl_rl_amd.ppo:PPO"``; the runner then calls
+``PPO.construct_algorithm(obs, env, cfg, device)`` (upstream rsl_rl/algorithms/ppo.py:428-465) and the methods
+upstream's runner uses: train_mode / eval_mode / act / process_env_step / compute_returns / update /
+learning_rate / get_policy / save / load (rsl_rl/runners/on_policy_runner.py:39-169).
+
+Compatibility kept with upstream:
+  * constructor keywords and defaults (ppo.py:40-68); RND / symmetry / multi-GPU raise NotImplementedError;
+  * actor / critic / optimizer state_dict layouts: the models keep upstream's module names and parameter order,
+    and ``self.optimizer`` is a real ``torch.optim.Adam`` whose state tensors are views of the flat buffers the
+    kernels update, so ``save()`` / ``load()`` produce and accept upstream checkpoints;
+  * the permutation is ``torch.randperm`` on the host CPU generator, drawn once per update, so the mini-batch
+    indices are bit-identical to upstream's CPU run after the same ``torch.manual_seed``.
+"""
+
+from __future__ import annotations
+
+import copy
+import importlib
+import warnings
+from itertools import chain
+from typing import Mapping
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .engine import UpdateEngine
+from .models import MLPModel
+from .storage import RolloutStorage
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# class resolution (rsl_rl/utils/utils.py:99-189) -- simple names resolve inside this package
+# ----------------------------------------------------------------------------------------------------------------------
+
+def resolve_callable(name):
+    if callable(name):
+        return name
+    if not isinstance(name, str):
+        raise TypeError(f"Expected callable or string, got {type(name)}")
+    short = name.split(":")[-1].split(".")[-1]
+    local = {"PPO": PPO, "MLPModel": MLPModel, "RolloutStorage": RolloutStorage}
+    if ":" in name:
+        mod, attr = name.rsplit(":", 1)
+        if mod.split(".")[0] == "rsl_rl" and short in local:
+            return local[short]  # upstream's classes map onto their HIP counterparts
+        obj = importlib.import_module(mod)
+        for a in attr.split("."):
+            obj = getattr(obj, a)
+        return obj
+    if short in local:
+        return local[short]
+    if short == "RNNModel":
+        raise NotImplementedError("RNNModel (recurrent PPO) is not implemented on the HIP path yet")
+    raise ValueError(f"Could not resolve '{name}'. Use a qualified name like 'module.path:ClassName'.")
+
+
+def resolve_class(cfg: dict):
+    c = copy.deepcopy(cfg)
+    return resolve_callable(c.pop("class_name")), c
+
+
+def resolve_obs_groups(obs: Mapping, obs_groups: dict, default_sets: list[str]) -> dict:
+    """rsl_rl/utils/utils.py:192-287."""
+    if len(obs_groups) == 0:
+        warnings.warn("The observation configuration dictionary 'obs_groups' is empty and thus likely not configured.")
+    else:
+        for set_name, groups in obs_groups.items():
+            if len(groups) == 0:
+                raise ValueError(f"The '{set_name}' key in the 'obs_groups' dictionary can not be an empty list.")
+            for g in groups:
+                if g not in obs:
+                    raise ValueError(f"Observation '{g}' in observation set '{set_name}' not found in the observations "
+                                     f"from the environment. Available observations: {list(obs.keys())}")
+    for name in default_sets:
+        if name not in obs_groups:
+            if name in obs:
+                obs_groups[name] = [name]
+            elif "policy" in obs:
+                obs_groups[name] = ["policy"]
+            else:
+                raise ValueError(f"The observation configuration dictionary 'obs_groups' does not contain the '{name}'"
+                                 " key and no suitable observation could be found.")
+    return obs_groups
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# flat parameter buffers
+# ----------------------------------------------------------------------------------------------------------------------
+
+class FlatParams:
+    """Parameters, gradients and Adam moments of an ordered parameter list as views of four flat fp32 buffers."""
+
+    def __init__(self, groups: list[list[nn.Parameter]], device) -> None:
+        params = [p for g in groups for p in g]
+        n = sum(p.numel() for p in params)
+        self.param = torch.empty(n, device=device)
+        self.grad = torch.zeros(n, device=device)
+        self.exp_avg = torch.zeros(n, device=device)
+        self.exp_avg_sq = torch.zeros(n, device=device)
+        self.offsets: dict[int, tuple[int, int]] = {}
+        bounds = [0]
+        off = 0
+        with torch.no_grad():
+            for g in groups:
+                for p in g:
+                    k = p.numel()
+                    self.param[off:off + k].copy_(p.detach().reshape(-1))
+                    p.data = self.param[off:off + k].view(p.shape)
+                    p.grad = self.grad[off:off + k].view(p.shape)
+                    self.offsets[id(p)] = (off, k)
+                    off += k
+                bounds.append(off)
+        self.group_begin = torch.tensor(bounds, dtype=torch.int64)
+        self.params = params
+
+    def _view(self, buf: torch.Tensor, p: nn.Parameter) -> torch.Tensor:
+        off, k = self.offsets[id(p)]
+        return buf[off:off + k].view(p.shape)
+
+    def grad_view(self, p: nn.Parameter) -> torch.Tensor:
+        return self._view(self.grad, p)
+
+    def exp_avg_view(self, p: nn.Parameter) -> torch.Tensor:
+        return self._view(self.exp_avg, p)
+
+    def exp_avg_sq_view(self, p: nn.Parameter) -> torch.Tensor:
+        return self._view(self.exp_avg_sq, p)
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# the algorithm
+# ----------------------------------------------------------------------------------------------------------------------
+
+class PPO:
+    """Proximal Policy Optimization with the update on the GPU (upstream rsl_rl/algorithms/ppo.py:27-486)."""
+
+    actor: MLPModel
+    critic: MLPModel
+
+    def __init__(self, actor: MLPModel, critic: MLPModel, storage: RolloutStorage, num_learning_epochs: int = 5,
+                 num_mini_batches: int = 4, clip_param: float = 0.2, gamma: float = 0.99, lam: float = 0.95,
+                 value_loss_coef: float = 1.0, entropy_coef: float = 0.01, learning_rate: float = 0.001,
+                 max_grad_norm: float = 1.0, optimizer: str = "adam", use_clipped_value_loss: bool = True,
+                 schedule: str = "adaptive", desired_kl: float = 0.01,
+                 normalize_advantage_per_mini_batch: bool = False, use_mixed_precision: bool = False,
+                 device: str = "cuda", rnd_cfg: dict | None = None, symmetry_cfg: dict | None = None,
+                 multi_gpu_cfg: dict | None = None, grad_reduce_bucket_mb: float = 25,
+                 hip_cfg: dict | None = None) -> None:
+        if rnd_cfg:
+            raise NotImplementedError("RND is not on the HIP PPO path")
+        if symmetry_cfg:
+            raise NotImplementedError("symmetry augmentation is not on the HIP PPO path")
+        if multi_gpu_cfg is not None:
+            raise NotImplementedError("multi-GPU training is not implemented by the HIP PPO plugin (single GPU)")
+        if optimizer.lower() != "adam":
+            raise NotImplementedError(f"optimizer '{optimizer}': the fused update implements Adam")
+        if use_mixed_precision:
+            raise NotImplementedError("the HIP update computes in fp32; use_mixed_precision is not supported")
+        if actor.is_recurrent or critic.is_recurrent:
+            raise NotImplementedError("recurrent models are not on the HIP MLP path")
+        if actor.distribution is None:
+            raise ValueError("the actor needs a GaussianDistribution (distribution_cfg)")
+        if not actor.distribution.param.requires_grad:
+            raise NotImplementedError("learn_std=False is not supported by the fused update")
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("tt_rsl_rl_amd.ppo.PPO runs on a GPU device (no CPU path)")
+        self.hip_cfg = dict(hip_cfg or {})
+        self.is_multi_gpu = False
+        self.gpu_global_rank = 0
+        self.gpu_world_size = 1
+        self.grad_reduce_bucket_mb = grad_reduce_bucket_mb
+        self.rnd = None
+        self.symmetry = None
+
+        self.actor = actor.to(self.device)
+        self.critic = critic.to(self.device)
+        self._raw_actor = self.actor
+        self._raw_critic = self.critic
+
+        # upstream's optimizer parameter list: actor params then critic params, de-duplicated (ppo.py:100-102)
+        actor_params = list(dict.fromkeys(self.actor.parameters()))
+        critic_params = [p for p in dict.fromkeys(self.critic.parameters()) if p not in set(actor_params)]
+        self.flat = FlatParams([actor_params, critic_params], self.device)
+        self.optimizer = torch.optim.Adam(actor_params + critic_params, lr=learning_rate)
+        self.betas = tuple(self.optimizer.defaults["betas"])
+        self.adam_eps = float(self.optimizer.defaults["eps"])
+        self._opt_steps = 0
+
+        self.storage = storage
+        self.transition = RolloutStorage.Transition()
+        self.clip_param = clip_param
+        self.num_learning_epochs = num_learning_epochs
+        self.num_mini_batches = num_mini_batches
+        self.value_loss_coef = value_loss_coef
+        self.entropy_coef = entropy_coef
+        self.gamma = gamma
+        self.lam = lam
+        self.max_grad_norm = max_grad_norm
+        self.use_clipped_value_loss = use_clipped_value_loss
+        self.desired_kl = desired_kl
+        self.schedule = schedule
+        self.learning_rate = learning_rate
+        self.normalize_advantage_per_mini_batch = normalize_advantage_per_mini_batch
+        self.use_mixed_precision = use_mixed_precision
+        self.device_state = ops.new_device_state(learning_rate, self.device)
+        self._engine: UpdateEngine | None = None
+        self._adv_ws = ops.Workspace(self.device)
+        self.last_trace: list[dict] = []
+
+    # -- rollout side ------------------------------------------------------------------------------------------------
+    def act(self, obs: Mapping) -> torch.Tensor:
+        """ppo.py:124-135."""
+        self.transition.hidden_states = (self.actor.get_hidden_state(), self.critic.get_hidden_state())
+        self.transition.actions = self.actor(obs, stochastic_output=True).detach()
+        self.transition.values = self.critic(obs).detach()
+        self.transition.actions_log_prob = self.actor.get_output_log_prob(self.transition.actions).detach()
+        self.transition.distribution_params = tuple(p.detach() for p in self.actor.output_distribution_params)
+        self.transition.observations = obs
+        return self.transition.actions
+
+    def process_env_step(self, obs: Mapping, rewards: torch.Tensor, dones: torch.Tensor, extras: dict) -> None:
+        """ppo.py:137-164 (time-out bootstrap with the pre-step value V(s_t))."""
+        self.transition.rewards = rewards.clone()
+        self.transition.dones = dones
+        if "time_outs" in extras:
+            self.transition.rewards += self.gamma * torch.squeeze(
+                self.transition.values * extras["time_outs"].unsqueeze(1).to(self.device), 1)
+        self.storage.add_transition(self.transition)
+        self.transition.clear()
+        self.actor.reset(dones)
+        self.critic.reset(dones)
+
+    def compute_returns(self, obs: Mapping) -> None:
+        """ppo.py:166-191: bootstrap value, GAE scan and global advantage normalisation on the GPU."""
+        st = self.storage
+        last_values = self.critic(obs).detach().contiguous()
+        self.compute_returns_from(last_values)
+
+    def compute_returns_from(self, last_values: torch.Tensor) -> None:
+        st = self.storage
+        ops.gae(st.rewards, st.values, st.dones, last_values, st.returns, st.advantages, self.gamma, self.lam)
+        n = st.advantages.numel()
+        if not self.normalize_advantage_per_mini_batch and n > 1:
+            ops.adv_normalize(st.advantages, st.advantages, n, ws=self._adv_ws)
+
+    # -- learning side -----------------------------------------------------------------------------------------------
+    def _get_engine(self) -> UpdateEngine:
+        e = self._engine
+        if e is None or e.B != self.storage.batch_size or e.M != self.num_mini_batches:
+            self._engine = e = UpdateEngine(self)
+        return e
+
+    def update(self) -> dict[str, float]:
+        """ppo.py:193-358."""
+        st = self.storage
+        B = st.batch_size
+        if not 1 <= self.num_mini_batches <= B:
+            raise ValueError("num_mini_batches must be between 1 and the rollout batch size.")
+        if st.distribution_params is None:
+            raise RuntimeError("update() called before any transition was stored")
+        engine = self._get_engine()
+        ops.reset_device_state(self.device_state, self.learning_rate)
+        perm = torch.randperm(B).to(self.device, non_blocking=False)
+        steps = engine.run(perm, self._opt_steps)
+        self._opt_steps += steps
+
+        obs = st.observations
+        self.actor.update_normalization(obs)
+        self.critic.update_normalization(obs)
+
+        state = ops.read_device_state(self.device_state)  # the one host sync of the update
+        self.learning_rate = state.learning_rate
+        for group in self.optimizer.param_groups:
+            group["lr"] = self.learning_rate
+        self._sync_optimizer_state()
+        n = self.num_learning_epochs * self.num_mini_batches
+        trace = engine.trace.view(-1, 5).cpu().tolist()
+        self.last_trace = [dict(kl_mean=t[0], lr=t[1], surrogate=t[2], value=t[3], entropy=t[4]) for t in trace]
+        st.clear()
+        return {"value": state.sum_value_loss / n, "surrogate": state.sum_surrogate_loss / n,
+                "entropy": state.sum_entropy / n}
+
+    def _sync_optimizer_state(self) -> None:
+        """Expose the flat Adam moments through torch.optim.Adam's state (views, no copies)."""
+        step = torch.tensor(float(self._opt_steps))
+        for p in self.flat.params:
+            s = self.optimizer.state[p]
+            s["step"] = step.clone()
+            s["exp_avg"] = self.flat.exp_avg_view(p)
+            s["exp_avg_sq"] = self.flat.exp_avg_sq_view(p)
+
+    # -- bookkeeping -------------------------------------------------------------------------------------------------
+    def train_mode(self) -> None:
+        self.actor.train()
+        self.critic.train()
+
+    def eval_mode(self) -> None:
+        self.actor.eval()
+        self.critic.eval()
+
+    def save(self) -> dict:
+        """ppo.py:374-385."""
+        return {"actor_state_dict": self._raw_actor.state_dict(), "critic_state_dict": self._raw_critic.state_dict(),
+                "optimizer_state_dict": self.optimizer.state_dict()}
+
+    def load(self, loaded_dict: dict, load_cfg: dict | None, strict: bool) -> bool:
+        """ppo.py:387-411.  Loaded Adam moments are copied into the flat buffers the kernels update."""
+        if load_cfg is None:
+            load_cfg = {"actor": True, "critic": True, "optimizer": True, "iteration": True, "rnd": True}
+        if load_cfg.get("actor"):
+            self._raw_actor.load_state_dict(loaded_dict["actor_state_dict"], strict=strict)
+        if load_cfg.get("critic"):
+            self._raw_critic.load_state_dict(loaded_dict["critic_state_dict"], strict=strict)
+        if load_cfg.get("optimizer"):
+            self.optimizer.load_state_dict(loaded_dict["optimizer_state_dict"])
+            self.learning_rate = self.optimizer.param_groups[0]["lr"]
+            steps = 0
+            with torch.no_grad():
+                for p in self.flat.params:
+                    s = self.optimizer.state.get(p, {})
+                    if "exp_avg" in s:
+                        self.flat.exp_avg_view(p).copy_(s["exp_avg"])
+                        self.flat.exp_avg_sq_view(p).copy_(s["exp_avg_sq"])
+                        steps = max(steps, int(float(s["step"])))
+                    else:
+                        self.flat.exp_avg_view(p).zero_()
+                        self.flat.exp_avg_sq_view(p).zero_()
+            self._opt_steps = steps
+            if steps > 0:
+                self._sync_optimizer_state()
+        return load_cfg.get("iteration", False)
+
+    def get_policy(self) -> MLPModel:
+        return self._raw_actor
+
+    def compile(self, mode: str | None = None) -> None:
+        """Upstream wraps the models in torch.compile; the HIP path has its own kernels, so only None is accepted."""
+        if mode is not None:
+            raise NotImplementedError("torch_compile_mode is not applicable to the HIP PPO path")
+
+    def broadcast_parameters(self) -> None:
+        raise NotImplementedError("multi-GPU training is not implemented by the HIP PPO plugin")
+
+    def reduce_parameters(self) -> None:
+        raise NotImplementedError("multi-GPU training is not implemented by the HIP PPO plugin")
+
+    @staticmethod
+    def construct_algorithm(obs: Mapping, env, cfg: dict, device: str) -> "PPO":
+        """ppo.py:428-465 (actor then critic construction consumes the global RNG in upstream's order)."""
+        alg_class, alg_cfg = resolve_class(cfg["algorithm"])
+        actor_class, actor_cfg = resolve_class(cfg["actor"])
+        critic_class, critic_cfg = resolve_class(cfg["critic"])
+        if alg_cfg.get("rnd_cfg"):
+            raise NotImplementedError("RND is not on the HIP PPO path")
+        cfg["obs_groups"] = resolve_obs_groups(obs, cfg.get("obs_groups", {}), ["actor", "critic"])
+        alg_cfg.pop("share_cnn_encoders", None)
+        actor = actor_class(obs, cfg["obs_groups"], "actor", env.num_actions, **actor_cfg)
+        critic = critic_class(obs, cfg["obs_groups"], "critic", 1, **critic_cfg)
+        storage = RolloutStorage("rl", env.num_envs, cfg["num_steps_per_env"], obs, [env.num_actions], device)
+        alg = alg_class(actor, critic, storage, device=device, **alg_cfg, multi_gpu_cfg=cfg.get("multi_gpu"))
+        alg.compile(cfg.get("torch_compile_mode"))
+        return alg
+
+
+HipPPO = PPO
