@@ -1,0 +1,230 @@
+#!/usr/bin/env python3
+"""PPO update throughput on one MI355X: samples/s and ms per update (fwd + bwd + Adam over all epochs).
+
+Workload (default): the humanoid-scale update -- actor obs 96 -> [512, 256, 128] ELU -> 29 actions, critic obs 99
+-> [512, 256, 128] ELU -> 1, observation normalisation, 4096 envs x 24 steps, 5 epochs x 4 mini-batches.
+A synthetic rollout (obs ~ N(0,1), rewards ~ N(0, 0.2^2), dones ~ Bernoulli(0.01), actions sampled from the
+policy) is collected once with the plugin's own act() on the GPU, returns are computed, and then `--steps` updates
+are timed on the resident rollout (each update = one step; inputs already in HBM).
+
+Prints ONE JSON line.  Alongside the GPU figure it reports:
+  * roofline: the dominant kernel's algorithmic FLOP rate (HIP events on the launch stream, timed region) against
+    the fp32 MFMA peak, and the HBM traffic per launch measured with rocprofv3 counters (profiles/, else null);
+  * cpu_baseline: the CPU oracle's update() on this host's cores on the same workload (a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+from types import SimpleNamespace
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "PPO update samples/s (fwd+bwd+Adam) and ms/update at 4096 envs×24 steps, 1 GPU"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def _sample_obs(workload, n, device, gen):
+    import torch
+
+    out = {}
+    for name, (kind, width) in workload["obs"].items():
+        if kind == "normal":
+            out[name] = torch.randn(n, width, device=device, generator=gen)
+        else:
+            out[name] = torch.rand(n, width, device=device, generator=gen) * 2.0 - 1.0
+    return out
+
+
+def build_gpu_alg(workload, seed: int = 0):
+    """Construct the plugin the way upstream's runner does and collect one synthetic rollout on the GPU."""
+    import torch
+
+    from tt_rsl_rl_amd import workloads as W
+    from tt_rsl_rl_amd.ppo import PPO
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(seed)
+    cfg = W.train_cfg(workload)
+    env = SimpleNamespace(num_envs=workload["num_envs"], num_actions=workload["num_actions"])
+    n = workload["num_envs"]
+    obs0 = {k: torch.zeros(n, w) for k, (_, w) in workload["obs"].items()}
+    alg = PPO.construct_algorithm(obs0, env, cfg, str(dev))
+    alg.train_mode()
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    with torch.inference_mode():
+        obs = _sample_obs(workload, n, dev, gen)
+        for _ in range(workload["steps"]):
+            alg.act(obs)
+            rewards = workload["reward_std"] * torch.randn(n, device=dev, generator=gen)
+            dones = (torch.rand(n, device=dev, generator=gen) < workload["p_done"]).float()
+            obs = _sample_obs(workload, n, dev, gen)
+            alg.process_env_step(obs, rewards, dones, {})
+        alg.compute_returns(obs)
+    torch.cuda.synchronize()
+    return alg
+
+
+def phase_flops(workload, R: int) -> dict[str, float]:
+    """Algorithmic FLOPs of one launch of each GEMM phase (both models share a launch)."""
+    from tt_rsl_rl_amd import workloads as W
+
+    shapes = W.linear_shapes(workload)
+    nl = len(shapes[0])
+    out = {}
+    for i in range(nl):
+        out[f"fwd{i}"] = sum(2.0 * R * s[i][0] * s[i][1] for s in shapes)
+    for i in range(1, nl):
+        out[f"dx{i}"] = sum(2.0 * R * s[i][0] * s[i][1] for s in shapes)
+    out["dw"] = sum(2.0 * R * i_ * o_ for s in shapes for i_, o_ in s)
+    return out
+
+
+def load_traffic(kernel_phase: str):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter summary, if present."""
+    p = ROOT / "profiles" / "traffic_humanoid.json"
+    if not p.exists():
+        return None
+    try:
+        d = json.loads(p.read_text())
+        return d.get(kernel_phase)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(workload, reps: int) -> dict:
+    """The oracle (upstream's update restated in CPU torch) on this host's cores, same workload, same statistics."""
+    import torch
+
+    from oracle import rollout as R
+
+    threads = torch.get_num_threads()
+    ora, roll = R.generate(workload, seed=0)
+    ora.compute_returns(roll.last_obs)
+    times = []
+    for i in range(reps + 1):
+        ora.storage.step = ora.storage.num_transitions_per_env
+        torch.manual_seed(1)
+        t0 = time.perf_counter()
+        ora.update()
+        dt = time.perf_counter() - t0
+        if i > 0:
+            times.append(dt)
+    med = statistics.median(times)
+    B = workload["num_envs"] * workload["steps"]
+    return {"value": B / med, "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": f"oracle PPO.update (upstream restated in CPU torch) on the same workload, median of {reps} "
+                      f"after 1 warm-up, {threads} torch threads, cpu_count={os.cpu_count()}",
+            "ms_per_update": med * 1e3}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="humanoid")
+    ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-phase-events", action="store_true", help="do not record per-launch HIP events")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs the PPO update on ONE GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU data parallelism is not implemented)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from tt_rsl_rl_amd import workloads as W
+    from tt_rsl_rl_amd.engine import PhaseTimer
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    workload = W.WORKLOADS[args.workload]
+    if "rnn" in workload:
+        print("bench.py: recurrent workloads are not implemented", file=sys.stderr)
+        return 2
+    alg = build_gpu_alg(workload)
+    B = workload["num_envs"] * workload["steps"]
+    M = alg.num_mini_batches
+    R = B // M
+
+    def one_update():
+        alg.storage.step = alg.storage.num_transitions_per_env
+        torch.manual_seed(1)
+        return alg.update()
+
+    for _ in range(args.warmup):
+        one_update()
+    engine = alg._engine
+    timer = PhaseTimer()
+    timer.enabled = not args.no_phase_events
+    engine.timer = timer
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    per = []
+    for _ in range(args.steps):
+        s0 = time.perf_counter()
+        losses = one_update()
+        per.append(time.perf_counter() - s0)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    value = B / (elapsed / args.steps)
+
+    phases = timer.summary() if timer.enabled else {}
+    flops = phase_flops(workload, R)
+    total_ms = {k: n * t for k, (n, t) in phases.items()}
+    phase_report = {}
+    for k, (n, t) in phases.items():
+        entry = {"launches": n, "mean_ms": round(t, 5)}
+        if k in flops:
+            entry["tflops"] = round(flops[k] / (t * 1e-3) / 1e12, 2)
+        phase_report[k] = entry
+    gemm_phases = [k for k in phases if k in flops]
+    roofline = None
+    if gemm_phases:
+        dom = max(gemm_phases, key=lambda k: total_ms[k])
+        n, t = phases[dom]
+        ach = flops[dom] / (t * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": load_traffic(dom), "kernel": dom,
+                    "flops_per_launch": flops[dom], "mean_launch_ms": round(t, 5)}
+    gemm_total = W.gemm_flops_per_update(workload, alg.num_learning_epochs)
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {len(W.linear_shapes(workload)[0])}-layer actor/critic MLPs "
+                               f"{W.linear_shapes(workload)}, {workload['num_envs']} envs x {workload['steps']} steps, "
+                               f"{alg.num_learning_epochs} epochs x {M} mini-batches of {R} rows, "
+                               f"obs normalisation {workload['obs_normalization']}",
+                   "num_envs": workload["num_envs"], "steps_per_env": workload["steps"], "mini_batch_rows": R,
+                   "parallelism": "single GPU"},
+        "ms_per_update_median": round(statistics.median(per) * 1e3, 3),
+        "update_gemm_tflops": round(gemm_total / (ms * 1e-3) / 1e12, 2),
+        "update_gemm_mfma_frac": round(gemm_total / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "phases": phase_report,
+        "roofline": roofline,
+        "losses": losses,
+        "cpu_baseline": None,
+    }
+    if args.cpu_baseline == "on":
+        line["cpu_baseline"] = cpu_baseline(workload, args.cpu_reps)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

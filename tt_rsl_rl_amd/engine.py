@@ -55,11 +55,49 @@ class ModelBuffers:
         self.dz = [torch.empty(rows, w, device=device) for w in self.widths]
 
 
+class PhaseTimer:
+    """Optional instrumentation: HIP events (torch.cuda.Event on the launch stream) around named launches."""
+
+    def __init__(self) -> None:
+        self.events: dict[str, list[tuple[torch.cuda.Event, torch.cuda.Event]]] = {}
+        self._open: dict[str, torch.cuda.Event] = {}
+        self.enabled = True
+
+    def start(self, name: str) -> None:
+        if self.enabled:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            self._open[name] = e
+
+    def stop(self, name: str) -> None:
+        if self.enabled:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            self.events.setdefault(name, []).append((self._open.pop(name), e))
+
+    def reset(self) -> None:
+        self.events.clear()
+        self._open.clear()
+
+    def summary(self) -> dict[str, tuple[int, float]]:
+        """name -> (launches, mean milliseconds); call after a device synchronisation."""
+        return {k: (len(v), sum(a.elapsed_time(b) for a, b in v) / len(v)) for k, v in self.events.items()}
+
+
+class _NoTimer:
+    def start(self, name: str) -> None:
+        pass
+
+    def stop(self, name: str) -> None:
+        pass
+
+
 class UpdateEngine:
     """Owns the device workspaces of the update and runs it.  Rebuilt when the rollout shape changes."""
 
     def __init__(self, alg) -> None:
         self.alg = alg
+        self.timer = _NoTimer()
         self.device = alg.device
         st = alg.storage
         self.B = st.batch_size
@@ -123,12 +161,15 @@ class UpdateEngine:
             adv_col = lay.adv_mb
 
         # forward, actor and critic grouped layer by layer
+        tm = self.timer
         ins_a, ins_c = [xa], [xc]
         for i in range(nl):
             last = i == nl - 1
             probs = [(ins_a[-1], la[i].weight, la[i].bias, ba.z[i][:R], None if last else ba.h[i][:R]),
                      (ins_c[-1], lc[i].weight, lc[i].bias, bc.z[i][:R], None if last else bc.h[i][:R])]
+            tm.start(f"fwd{i}")
             ops.linear_fwd(probs, R, elu=not last)
+            tm.stop(f"fwd{i}")
             if not last:
                 ins_a.append(ba.h[i][:R])
                 ins_c.append(bc.h[i][:R])
@@ -142,33 +183,43 @@ class UpdateEngine:
         args = ops.make_loss_args(R, ba.z[-1][:R], bc.z[-1][:R, 0], batch, dist.param, dist.kernel_std_type, lo, hi,
                                   alg.clip_param, alg.value_loss_coef, alg.entropy_coef, alg.use_clipped_value_loss,
                                   ba.dz[-1][:R], bc.dz[-1][:R, 0])
+        tm.start("loss")
         ops.ppo_loss(args, self.loss_ws)
         adaptive = alg.desired_kl is not None and alg.schedule == "adaptive"
         ops.ppo_loss_finalize(args, self.loss_ws, alg.flat.grad_view(dist.param), alg.device_state, adaptive,
                               alg.desired_kl if alg.desired_kl is not None else 0.0, self.trace)
+        tm.stop("loss")
 
         # backward: input gradients down the chain (grouped), then every weight gradient in one launch
         for i in range(nl - 1, 0, -1):
+            tm.start(f"dx{i}")
             ops.linear_bwd_dx([(ba.dz[i][:R], la[i].weight, ba.z[i - 1][:R], ba.dz[i - 1][:R]),
                                (bc.dz[i][:R], lc[i].weight, bc.z[i - 1][:R], bc.dz[i - 1][:R])], R)
+            tm.stop(f"dx{i}")
         dw = []
         for model, buf, lins, x0 in ((actor, ba, la, xa), (critic, bc, lc, xc)):
             for i in range(nl):
                 x = x0 if i == 0 else buf.h[i - 1][:R]
                 dw.append((buf.dz[i][:R], x, alg.flat.grad_view(lins[i].weight), alg.flat.grad_view(lins[i].bias)))
+        tm.start("dw")
         ops.linear_bwd_dw(dw, R, self.dw_ws)
+        tm.stop("dw")
 
         # per-model clip + Adam over the flat buffers
         b1, b2 = alg.betas
         bc1 = 1 - b1 ** step
         bc2_sqrt = (1 - b2 ** step) ** 0.5
         f = alg.flat
+        tm.start("adam")
         ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin, alg.max_grad_norm, b1, b2, alg.adam_eps,
                       bc1, bc2_sqrt, alg.device_state, self.adam_ws)
+        tm.stop("adam")
 
     def run(self, perm: torch.Tensor, first_step: int) -> int:
         """All epochs x mini-batches.  Returns the number of optimiser steps taken."""
+        self.timer.start("gather")
         self.gather(perm)
+        self.timer.stop("gather")
         self.trace.zero_()
         step = first_step
         for _ in range(self.alg.num_learning_epochs):
