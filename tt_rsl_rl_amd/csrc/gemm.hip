@@ -1,24 +1,30 @@
 // A6 linear layers (rsl_rl/modules/mlp.py:27-95; autograd of nn.Linear / nn.ELU) as fp32 MFMA GEMMs for gfx950.
 //
-// One templated kernel computes C = A B over BM x BN output tiles with 256 threads (4 wavefronts in a 2 x 2
-// arrangement, each owning a (BM/2) x (BN/2) sub-tile of 32 x 32 v_mfma_f32_32x32x2f32 accumulators).  A and B are
-// staged through LDS in BK = 16 deep k-slabs stored k-major, so every MFMA operand fetch is one conflict-light
-// ds_read_b32 per lane; the next slab is prefetched into registers while the current one is multiplied.
-// A(m,k) and B(k,n) are read either k-contiguous or m/n-contiguous (template flags), which covers the three
-// products of a layer without transposing anything in memory:
-//   forward   z[r,o]  = sum_i x[r,i]  w[o,i]   A = x  (k-contig)      B = w  (k-contig)   epilogue +b, ELU
-//   input-grad dzp[r,i] = sum_o dz[r,o] w[o,i] A = dz (k-contig)      B = w  (n-contig)   epilogue * ELU'(z_prev)
-//   weight-grad dw[o,i] = sum_r dz[r,o] x[r,i] A = dz (m-contig)      B = x  (n-contig)   split-K partials
+// One templated kernel computes C = A B over BM x BN output tiles with 256 threads: 4 wavefronts in a 2 x 2
+// arrangement, each owning a (BM/2) x (BN/2) sub-tile of 32 x 32 v_mfma_f32_32x32x2f32 accumulators.  A and B are
+// staged through double-buffered LDS in BK-deep k-slabs stored k-major, so every MFMA operand fetch is one
+// ds_read_b32 per lane and each slab costs a single barrier; the next slab is fetched from global memory into
+// registers (float4 where the leading dimension allows, chosen per problem at launch) while the current one is
+// multiplied.  A(m,k) and B(k,n) are read either k-contiguous or m/n-contiguous (template flags), which covers the
+// three products of a layer without transposing anything in memory:
+//   forward     z[r,o]   = sum_i x[r,i]  w[o,i]   A = x  (k-contig)   B = w (k-contig)   epilogue +b, ELU
+//   input-grad  dzp[r,i] = sum_o dz[r,o] w[o,i]   A = dz (k-contig)   B = w (n-contig)   epilogue * ELU'(z_prev)
+//   weight-grad dw[o,i]  = sum_r dz[r,o] x[r,i]   A = dz (m-contig)   B = x (n-contig)   split-K partials
 // The weight-grad kernel also sums its A slab over k (blocks of the first n tile only), which yields the bias
-// gradient db[o] = sum_r dz[r,o] for free.  Split-K partials are reduced in a fixed order by a second kernel, so
-// the result is deterministic.  Several independent problems (actor and critic, or all layers of the weight-grad)
-// share one launch: the block index is mapped to (problem, split, tile) through per-problem block offsets.
+// gradient db[o] = sum_r dz[r,o] in fp64.  Split-K partials are reduced in a fixed order by a second kernel, so the
+// result is deterministic.  Several independent problems (actor and critic, or all layers of the weight-grad)
+// share one launch: the block index is mapped to (problem, split, tile) through per-problem block offsets, after
+// an XCD-aware permutation that places consecutive tiles (which share an A panel) on the same XCD / L2.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.hpp"
 
 namespace ppo {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_ELU = 1, EPI_ELU_GRAD = 2, EPI_STORE = 3, EPI_PARTIAL = 4 };
 
@@ -35,28 +41,125 @@ struct Problem {
   int32_t M, N, K;
   int32_t tiles_m, tiles_n, splits, k_chunk;
   int32_t block_begin;
+  int32_t a_vec, b_vec;    // float4 global loads along the contiguous dimension are valid for this problem
 };
 
 struct Group {
   Problem p[PPO_MAX_LINEAR_PROBLEMS];
   int32_t count;
+  int32_t xcd_remap;  // 1: permute block ids so each XCD gets a contiguous range of tiles
 };
 
 constexpr int kThreads = 256;
-constexpr int kBK = 16;
+constexpr int kXcds = 8;
 
-template <int BM, int BN, bool A_KMAJ, bool B_KMAJ, int EPI>
+// Blocks are dispatched round-robin over the XCDs; renumber them so that each XCD receives a contiguous range of
+// logical tiles (a bijection of [0, n)).
+__device__ inline int xcd_remap(int b, int n) {
+  const int q = n / kXcds, r = n % kXcds;
+  const int xcd = b % kXcds, slot = b / kXcds;
+  return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+}
+
+// Loads one BK-deep slab of a BM-wide (A) or BN-wide (B) operand into registers and stores it k-major into LDS.
+// KMAJ: element (x, k) at base[(x0 + x) * ld + k0 + k]; otherwise at base[(k0 + k) * ld + x0 + x].
+template <int BX, int BK, bool KMAJ, bool VEC>
+struct Slab {
+  static constexpr int kElems = BX * BK / kThreads;
+  static_assert(kElems % 4 == 0, "slab must give every thread a multiple of 4 elements");
+  float r[kElems];
+  int valid[kElems / 4];  // float4 path: leading elements of each vector inside the operand (the rest -> 0)
+
+  // Issues the loads only: nothing here consumes the loaded registers, so the wait for them lands in store(),
+  // after the MFMAs of the current slab.
+  __device__ inline void load(const float* __restrict__ base, int64_t ld, int x0, int X, int k0, int k_end) {
+    const int tid = threadIdx.x;
+    if (VEC) {
+#pragma unroll
+      for (int i = 0; i < kElems / 4; ++i) {
+        const int q = tid + kThreads * i;
+        int x, k;
+        if (KMAJ) {
+          x = q / (BK / 4);
+          k = (q % (BK / 4)) * 4;
+        } else {
+          k = q / (BX / 4);
+          x = (q % (BX / 4)) * 4;
+        }
+        const int gx = x0 + x, gk = k0 + k;
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        int n = 0;
+        if (KMAJ) {
+          if (gx < X && gk < k_end) {
+            v = *reinterpret_cast<const f32x4*>(base + gx * ld + gk);
+            n = min(4, k_end - gk);
+          }
+        } else {
+          if (gk < k_end && gx < X) {
+            v = *reinterpret_cast<const f32x4*>(base + gk * ld + gx);
+            n = min(4, X - gx);
+          }
+        }
+        valid[i] = n;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r[4 * i + j] = v[j];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kElems; ++i) {
+        const int q = tid + kThreads * i;
+        const int x = KMAJ ? q / BK : q % BX;
+        const int k = KMAJ ? q % BK : q / BX;
+        const int gx = x0 + x, gk = k0 + k;
+        float v = 0.0f;
+        if (gx < X && gk < k_end) v = KMAJ ? base[gx * ld + gk] : base[gk * ld + gx];
+        r[i] = v;
+      }
+    }
+  }
+
+  template <int LDS_W>
+  __device__ inline void store(float (*lds)[LDS_W]) {
+    const int tid = threadIdx.x;
+    if (VEC) {
+#pragma unroll
+      for (int i = 0; i < kElems / 4; ++i) {
+        const int q = tid + kThreads * i;
+        float e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = j < valid[i] ? r[4 * i + j] : 0.0f;
+        if (KMAJ) {
+          const int x = q / (BK / 4), k = (q % (BK / 4)) * 4;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) lds[k + j][x] = e[j];
+        } else {
+          const int k = q / (BX / 4), x = (q % (BX / 4)) * 4;
+          f32x4 v = {e[0], e[1], e[2], e[3]};
+          *reinterpret_cast<f32x4*>(&lds[k][x]) = v;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kElems; ++i) {
+        const int q = tid + kThreads * i;
+        const int x = KMAJ ? q / BK : q % BX;
+        const int k = KMAJ ? q % BK : q / BX;
+        lds[k][x] = r[i];
+      }
+    }
+  }
+};
+
+template <int BM, int BN, int BK, bool A_KMAJ, bool B_KMAJ, bool A_VEC, bool B_VEC, int EPI>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(const Group g) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int PAD = 4;
-  constexpr int A_LOADS = BM * kBK / kThreads;
-  constexpr int B_LOADS = BN * kBK / kThreads;
-  static_assert(TM >= 1 && TN >= 1 && A_LOADS >= 1 && B_LOADS >= 1, "tile too small");
-  __shared__ float As[kBK][BM + PAD];
-  __shared__ float Bs[kBK][BN + PAD];
+  static_assert(TM >= 1 && TN >= 1, "tile too small");
+  __shared__ __align__(16) float As[2][BK][BM + PAD];
+  __shared__ __align__(16) float Bs[2][BK][BN + PAD];
 
-  const int b = blockIdx.x;
+  const int b = g.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
   int pi = 0;
 #pragma unroll
   for (int i = 1; i < PPO_MAX_LINEAR_PROBLEMS; ++i) {
@@ -88,76 +191,49 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const Group g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  float ra[A_LOADS], rb[B_LOADS];
-  const float* __restrict__ Ap = P.A;
-  const float* __restrict__ Bp = P.B;
-  const int64_t lda = P.lda, ldb = P.ldb;
-
-  auto load_tiles = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const int idx = tid + kThreads * i;
-      const int m = A_KMAJ ? idx / kBK : idx % BM;
-      const int k = A_KMAJ ? idx % kBK : idx / BM;
-      const int gm = row0 + m, gk = k0 + k;
-      float v = 0.0f;
-      if (gm < M && gk < k_end) v = A_KMAJ ? Ap[gm * lda + gk] : Ap[gk * lda + gm];
-      ra[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = tid + kThreads * i;
-      const int n = B_KMAJ ? idx / kBK : idx % BN;
-      const int k = B_KMAJ ? idx % kBK : idx / BN;
-      const int gn = col0 + n, gk = k0 + k;
-      float v = 0.0f;
-      if (gn < N && gk < k_end) v = B_KMAJ ? Bp[gn * ldb + gk] : Bp[gk * ldb + gn];
-      rb[i] = v;
-    }
-  };
-  auto store_tiles = [&]() {
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      const int idx = tid + kThreads * i;
-      const int m = A_KMAJ ? idx / kBK : idx % BM;
-      const int k = A_KMAJ ? idx % kBK : idx / BM;
-      As[k][m] = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = tid + kThreads * i;
-      const int n = B_KMAJ ? idx / kBK : idx % BN;
-      const int k = B_KMAJ ? idx % kBK : idx / BN;
-      Bs[k][n] = rb[i];
-    }
-  };
-
+  Slab<BM, BK, A_KMAJ, A_VEC> sa;
+  Slab<BN, BK, B_KMAJ, B_VEC> sb;
   const bool do_colsum = (EPI == EPI_PARTIAL) && (P.colsum != nullptr) && (tn == 0);
   double colsum_acc = 0.0;
 
-  if (k_begin < k_end) load_tiles(k_begin);
-  for (int k0 = k_begin; k0 < k_end; k0 += kBK) {
-    __syncthreads();
-    store_tiles();
-    __syncthreads();
-    if (k0 + kBK < k_end) load_tiles(k0 + kBK);
+  const int nk = k_begin < k_end ? static_cast<int>(ceil_div(k_end - k_begin, BK)) : 0;
+  if (nk > 0) {
+    sa.load(P.A, P.lda, row0, M, k_begin, k_end);
+    sb.load(P.B, P.ldb, col0, N, k_begin, k_end);
+    sa.store(As[0]);
+    sb.store(Bs[0]);
+  }
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      const int k0 = k_begin + (kt + 1) * BK;
+      sa.load(P.A, P.lda, row0, M, k0, k_end);
+      sb.load(P.B, P.ldb, col0, N, k0, k_end);
+    }
     if (do_colsum && tid < BM) {
 #pragma unroll
-      for (int kk = 0; kk < kBK; ++kk) colsum_acc += static_cast<double>(As[kk][tid]);
+      for (int kk = 0; kk < BK; ++kk) colsum_acc += static_cast<double>(As[cur][kk][tid]);
     }
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += 2) {
+    for (int kk = 0; kk < BK; kk += 2) {
       const int k = kk + (lane >> 5);
       float a[TM], bv[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = As[k][wm * WM + i * 32 + (lane & 31)];
+      for (int i = 0; i < TM; ++i) a[i] = As[cur][k][wm * WM + i * 32 + (lane & 31)];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bv[j] = Bs[k][wn * WN + j * 32 + (lane & 31)];
+      for (int j = 0; j < TN; ++j) bv[j] = Bs[cur][k][wn * WN + j * 32 + (lane & 31)];
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], bv[j], acc[i][j], 0, 0, 0);
     }
+    if (more) {
+      sa.store(As[cur ^ 1]);
+      sb.store(Bs[cur ^ 1]);
+    }
+    __syncthreads();
   }
 
   // Epilogue.  MFMA 32x32 output layout: element v of lane l is row 8*(v/4) + 4*(l/32) + v%4, column l%32.
@@ -233,9 +309,10 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
   }
 }
 
-template <int BM, int BN, bool AK, bool BK_, int EPI>
+template <int BM, int BN, int BK, bool AK, bool BKM, int EPI>
 int launch(Group& g, int count, hipStream_t s, const char* name) {
   int blocks = 0;
+  bool avec = std::getenv("PPO_HIP_GEMM_SCALAR") == nullptr, bvec = avec;
   for (int i = 0; i < count; ++i) {
     Problem& p = g.p[i];
     p.tiles_m = static_cast<int>(ceil_div(p.M, BM));
@@ -244,16 +321,85 @@ int launch(Group& g, int count, hipStream_t s, const char* name) {
     const int64_t nb = static_cast<int64_t>(p.tiles_m) * p.tiles_n * p.splits;
     if (blocks + nb > INT32_MAX) return fail(PPO_EUNSUPPORTED, "%s: grid too large", name);
     blocks += static_cast<int>(nb);
+    avec = avec && p.a_vec;
+    bvec = bvec && p.b_vec;
   }
   g.count = count;
+  g.xcd_remap = std::getenv("PPO_HIP_NO_XCD_REMAP") == nullptr;
   for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) g.p[i].block_begin = INT32_MAX;
   if (blocks == 0) return PPO_OK;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, AK, BK_, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  // float4 global loads only when every problem of the launch allows them
+  if (avec && bvec) {
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else if (avec) {
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, true, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else if (bvec) {
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, false, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, false, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  }
   return check_launch(name);
 }
 
+// float4 loads along the contiguous dimension need a 16-byte aligned base, a leading dimension that is a multiple
+// of 4, and -- because a partial float4 at the end of a row is read whole and masked -- a leading dimension of at
+// least the contiguous extent rounded up to 4 (the caller's buffer holds rows x ld floats).
+bool vec_ok(const float* base, int64_t ld, int64_t contiguous_extent) {
+  return (reinterpret_cast<uintptr_t>(base) % 16 == 0) && ld % 4 == 0 && ld >= (contiguous_extent + 3) / 4 * 4;
+}
+
+// Tile of a launch: "PPO_HIP_GEMM_TILE" (e.g. "128x64k32") overrides the size-based choice (tuning aid).
+enum Tile { T128x128k32, T128x128k16, T128x64k32, T64x64k32, T256x128k16 };
+
+Tile pick_tile(Tile dflt) {
+  const char* e = std::getenv("PPO_HIP_GEMM_TILE");
+  if (e == nullptr) return dflt;
+  if (!std::strcmp(e, "128x128k32")) return T128x128k32;
+  if (!std::strcmp(e, "128x128k16")) return T128x128k16;
+  if (!std::strcmp(e, "128x64k32")) return T128x64k32;
+  if (!std::strcmp(e, "64x64k32")) return T64x64k32;
+  if (!std::strcmp(e, "256x128k16")) return T256x128k16;
+  return dflt;
+}
+
+template <bool AK, bool BKM, int EPI>
+int launch_tile(Tile t, Group& g, int count, hipStream_t s, const char* name) {
+  switch (t) {
+    case T128x128k16:
+      return launch<128, 128, 16, AK, BKM, EPI>(g, count, s, name);
+    case T128x64k32:
+      return launch<128, 64, 32, AK, BKM, EPI>(g, count, s, name);
+    case T64x64k32:
+      return launch<64, 64, 32, AK, BKM, EPI>(g, count, s, name);
+    case T256x128k16:
+      return launch<256, 128, 16, AK, BKM, EPI>(g, count, s, name);
+    default:
+      return launch<128, 128, 32, AK, BKM, EPI>(g, count, s, name);
+  }
+}
+
 // Split-K policy for the weight-grad: enough blocks to cover the chip (~4 per CU), slabs of at least 256 rows.
-constexpr int kDwBM = 64, kDwBN = 64;
+// Tile: "PPO_HIP_DW_TILE" overrides the default 128x128k32 (tuning aid).
+constexpr int kDwBK = 32;  // split-K chunks are multiples of the largest BK
+
+Tile dw_tile() {
+  const char* e = std::getenv("PPO_HIP_DW_TILE");
+  if (e == nullptr) return T128x128k16;
+  if (!std::strcmp(e, "128x128k32")) return T128x128k32;
+  if (!std::strcmp(e, "128x64k32")) return T128x64k32;
+  if (!std::strcmp(e, "64x64k32")) return T64x64k32;
+  if (!std::strcmp(e, "256x128k16")) return T256x128k16;
+  return T128x128k16;
+}
+
+void tile_dims(Tile t, int& bm, int& bn) {
+  switch (t) {
+    case T128x64k32: bm = 128; bn = 64; break;
+    case T64x64k32: bm = 64; bn = 64; break;
+    case T256x128k16: bm = 256; bn = 128; break;
+    default: bm = 128; bn = 128; break;
+  }
+}
 
 int dw_splits(int64_t tiles, int64_t rows) {
   const int64_t target = 1024;
@@ -267,19 +413,21 @@ struct DwPlan {
   int splits[PPO_MAX_LINEAR_PROBLEMS];
   int k_chunk[PPO_MAX_LINEAR_PROBLEMS];
   size_t partial_off[PPO_MAX_LINEAR_PROBLEMS];  // floats
-  size_t colsum_off[PPO_MAX_LINEAR_PROBLEMS];  // floats (8-byte aligned: holds doubles)
+  size_t colsum_off[PPO_MAX_LINEAR_PROBLEMS];   // floats (8-byte aligned: holds doubles)
   size_t total_floats;
 };
 
 DwPlan plan_dw(const ppo_linear_bwd_dw_problem* probs, int count, int64_t rows) {
   DwPlan plan{};
+  int bm, bn;
+  tile_dims(dw_tile(), bm, bn);
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i)
-    tiles += ceil_div(probs[i].out_features, kDwBM) * ceil_div(probs[i].in_features, kDwBN);
+    tiles += ceil_div(probs[i].out_features, bm) * ceil_div(probs[i].in_features, bn);
   const int s = dw_splits(tiles, rows);
   size_t off = 0;
   for (int i = 0; i < count; ++i) {
-    const int64_t chunk = ceil_div(ceil_div(rows, s), kBK) * kBK;
+    const int64_t chunk = ceil_div(ceil_div(rows, s), kDwBK) * kDwBK;
     const int splits = static_cast<int>(ceil_div(rows, chunk));
     plan.splits[i] = splits;
     plan.k_chunk[i] = static_cast<int>(chunk);
@@ -324,15 +472,16 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
     p.vec = q.b;
     p.M = static_cast<int>(rows); p.N = q.out_features; p.K = q.in_features;
     p.splits = 1; p.k_chunk = q.in_features;
+    p.a_vec = vec_ok(q.x, q.ldx, q.in_features);
+    p.b_vec = vec_ok(q.w, q.in_features, q.in_features);
     max_n = std::max(max_n, q.out_features);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (activation == PPO_ACT_ELU) {
-    if (max_n <= 64) return launch<128, 64, true, true, EPI_BIAS_ELU>(g, count, s, "linear_fwd_elu");
-    return launch<128, 128, true, true, EPI_BIAS_ELU>(g, count, s, "linear_fwd_elu");
-  }
-  if (max_n <= 64) return launch<128, 64, true, true, EPI_BIAS>(g, count, s, "linear_fwd");
-  return launch<128, 128, true, true, EPI_BIAS>(g, count, s, "linear_fwd");
+  // measured on MI355X for 24576-row mini-batches: wide outputs like 128x128 tiles, 128..256-wide outputs 128x64,
+  // narrow output layers 64x64
+  const Tile t = pick_tile(max_n > 256 ? T128x128k16 : (max_n > 64 ? T128x64k32 : T64x64k32));
+  if (activation == PPO_ACT_ELU) return launch_tile<true, true, EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_elu");
+  return launch_tile<true, true, EPI_BIAS>(t, g, count, s, "linear_fwd");
 }
 
 extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
@@ -358,16 +507,16 @@ extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int3
     p.aux = q.z_prev; p.ldaux = q.ldz_prev;
     p.M = static_cast<int>(rows); p.N = q.in_features; p.K = q.out_features;
     p.splits = 1; p.k_chunk = q.out_features;
+    p.a_vec = vec_ok(q.dz, q.lddz, q.out_features);
+    p.b_vec = vec_ok(q.w, q.in_features, q.in_features);
     max_n = std::max(max_n, q.in_features);
   }
   PPO_REQUIRE(!(any_act && any_plain), "ppo_linear_bwd_dx: mix of activation and plain problems in one call");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (any_act) {
-    if (max_n <= 64) return launch<128, 64, true, false, EPI_ELU_GRAD>(g, count, s, "linear_bwd_dx_elu");
-    return launch<128, 128, true, false, EPI_ELU_GRAD>(g, count, s, "linear_bwd_dx_elu");
-  }
-  if (max_n <= 64) return launch<128, 64, true, false, EPI_STORE>(g, count, s, "linear_bwd_dx");
-  return launch<128, 128, true, false, EPI_STORE>(g, count, s, "linear_bwd_dx");
+  // measured on MI355X: 64x64 tiles for every input-grad shape of the [512, 256, 128] MLPs
+  const Tile t = pick_tile(T64x64k32);
+  if (any_act) return launch_tile<true, false, EPI_ELU_GRAD>(t, g, count, s, "linear_bwd_dx_elu");
+  return launch_tile<true, false, EPI_STORE>(t, g, count, s, "linear_bwd_dx");
 }
 
 extern "C" size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_problem* problems, int32_t count,
@@ -393,6 +542,7 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total_floats * sizeof(float),
               "ppo_linear_bwd_dw: workspace too small (%zu < %zu)", workspace_bytes,
               plan.total_floats * sizeof(float));
+  PPO_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "ppo_linear_bwd_dw: workspace must be 16-byte aligned");
   float* ws = static_cast<float*>(workspace);
   Group g{};
   ReduceGroup rg{};
@@ -407,6 +557,8 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     p.colsum = reinterpret_cast<double*>(ws + plan.colsum_off[i]);
     p.M = q.out_features; p.N = q.in_features; p.K = static_cast<int>(rows);
     p.splits = plan.splits[i]; p.k_chunk = plan.k_chunk[i];
+    p.a_vec = vec_ok(q.dz, q.lddz, q.out_features);
+    p.b_vec = vec_ok(q.x, q.ldx, q.in_features);
     ReduceItem& r = rg.it[i];
     r.partial = p.C; r.colsum = p.colsum; r.dw = q.dw; r.db = q.db;
     r.out = q.out_features; r.in = q.in_features; r.splits = plan.splits[i];
@@ -417,7 +569,7 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   rg.count = count;
   rg.total = total;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = launch<kDwBM, kDwBN, false, false, EPI_PARTIAL>(g, count, s, "linear_bwd_dw");
+  int rc = launch_tile<false, false, EPI_PARTIAL>(dw_tile(), g, count, s, "linear_bwd_dw");
   if (rc != PPO_OK) return rc;
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 4096);
   hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);

@@ -2,11 +2,11 @@
 // learning-rate rule, forward and backward in one pass over the mini-batch
 // (rsl_rl/algorithms/ppo.py:226-285, rsl_rl/modules/distribution.py:183-238, torch's Normal / kl_divergence).
 //
-// One wavefront per 64 rows, one lane per row.  Each lane reads its row's A means / actions / old means / old
-// stds and five scalars, writes dloss/dmu [A] and dloss/dV, and contributes to per-block fp64 partial sums
-// (surrogate, value loss, KL, and the per-action dlogp/dlog(std) sums for the std-parameter gradient).  The
-// partials are reduced in a fixed order by a single-block finalize kernel, which also applies the adaptive-KL
-// learning-rate rule on the device, so the update loop never waits on the host.
+// The loss kernel writes dloss/dmu [R, A] and dloss/dV [R] and per-block fp64 partial sums (surrogate, value loss,
+// KL, and the per-action dlogp/dlog(std) sums for the std-parameter gradient).  The partials are reduced in a
+// fixed order by a single-block finalize kernel, which also applies the adaptive-KL learning-rate rule on the
+// device, so the update loop never waits on the host.  HBM-bound: per row 5 A-wide fp32 runs (mean, actions,
+// old mean, old std in; dloss/dmu out) and 6 scalars.
 //
 // Gradients follow torch autograd's conventions: max() sends the gradient to the larger operand and splits it
 // 50/50 on a tie; clamp() passes it on the closed interval [lo, hi].
@@ -17,7 +17,7 @@
 namespace ppo {
 namespace {
 
-constexpr int kLossThreads = 64;  // one wavefront per block
+constexpr int kLossThreads = 256;
 constexpr int kFixedCols = 3;     // surrogate, value loss, kl
 
 // log(sqrt(2*pi)) and 0.5 + 0.5*log(2*pi) as the fp32 values torch subtracts / adds (Python doubles cast once).
@@ -42,46 +42,58 @@ __device__ inline void std_of(const LossParams& p, int a, float& sd, float& log_
   std_from_param(p.a.std_param[a], p.a.std_type, p.std_lo, p.std_hi, sd, log_sd);
 }
 
+// Each group of L lanes (L = 32 for A <= 32, else 64) owns one row at a time, lane a <-> action a, so the A-wide
+// row segments are read as one coalesced run.  The per-row log-prob is a butterfly sum over the group in fp64; the
+// row scalars (advantage, returns, ...) are broadcast loads.  Every lane keeps fp64 running sums of its own action's
+// std-gradient and KL terms across the rows it visits, so no per-action reduction is needed until the block ends.
+template <int L>
 __global__ __launch_bounds__(kLossThreads) void ppo_loss_kernel(const LossParams p, double* __restrict__ partials) {
+  constexpr int kGroups = kLossThreads / L;  // rows in flight per block
   const ppo_loss_args& a = p.a;
   const int A = a.num_actions;
   const int cols = kFixedCols + A;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * kLossThreads + threadIdx.x;
-  const bool live = r < a.rows;
-  double* part = partials + static_cast<int64_t>(blockIdx.x) * cols;
+  const int lane = threadIdx.x & 63;
+  const int j = threadIdx.x % L;             // action of this lane
+  const int grp = threadIdx.x / L;           // row slot of this lane
+  const bool act_lane = j < A;
 
   __shared__ float s_std[PPO_MAX_ACTIONS], s_var[PPO_MAX_ACTIONS], s_log[PPO_MAX_ACTIONS];
-  for (int j = threadIdx.x; j < A; j += kLossThreads) {
+  __shared__ double s_red[kLossThreads / 64][kFixedCols + PPO_MAX_ACTIONS];
+  for (int q = threadIdx.x; q < A; q += kLossThreads) {
     float sd, lg;
-    std_of(p, j, sd, lg);
-    s_std[j] = sd;
-    s_var[j] = sd * sd;
-    s_log[j] = lg;
+    std_of(p, q, sd, lg);
+    s_std[q] = sd;
+    s_var[q] = sd * sd;
+    s_log[q] = lg;
   }
   __syncthreads();
+  const float sd = act_lane ? s_std[j] : 1.0f;
+  const float var = act_lane ? s_var[j] : 1.0f;
+  const float lg = act_lane ? s_log[j] : 0.0f;
+  const float c_lp = static_cast<float>(kLogSqrt2Pi);
 
-  float g_logp = 0.0f, surr = 0.0f, vloss = 0.0f, kl = 0.0f;
-  if (live) {
-    const float* mu = a.mean + r * a.ld_mean;
-    const float* act = a.actions + r * a.ld_batch;
-    const float* omu = a.old_mean + r * a.ld_batch;
-    const float* osd = a.old_std + r * a.ld_batch;
-    const float c_lp = static_cast<float>(kLogSqrt2Pi);
-    double logp_acc = 0.0;  // the sum over actions in fp64: one rounding instead of A
-    for (int j = 0; j < A; ++j) {
-      const float d = act[j] - mu[j];
-      float t = -(d * d) / (2.0f * s_var[j]);
-      t = t - s_log[j];
+  double acc_surr = 0.0, acc_val = 0.0, acc_kl = 0.0, acc_dstd = 0.0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kGroups;
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * kGroups + grp; r < a.rows; r += stride) {
+    float d = 0.0f;
+    double t_acc = 0.0;
+    if (act_lane) {
+      const float mu = a.mean[r * a.ld_mean + j];
+      d = a.actions[r * a.ld_batch + j] - mu;
+      float t = -(d * d) / (2.0f * var);
+      t = t - lg;
       t = t - c_lp;
-      logp_acc += static_cast<double>(t);
+      t_acc = static_cast<double>(t);
       // torch kl_divergence(Normal(old), Normal(new)) = 0.5 * (var_ratio + t1 - 1 - log(var_ratio))
-      const float q = osd[j] / s_std[j];
+      const float q = a.old_std[r * a.ld_batch + j] / sd;
       const float vr = q * q;
-      const float e = (omu[j] - mu[j]) / s_std[j];
+      const float e = (a.old_mean[r * a.ld_batch + j] - mu) / sd;
       const float t1 = e * e;
-      kl += 0.5f * (((vr + t1) - 1.0f) - logf(vr));
+      acc_kl += static_cast<double>(0.5f * (((vr + t1) - 1.0f) - logf(vr)));
     }
-    const float logp = static_cast<float>(logp_acc);
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) t_acc += __shfl_xor(t_acc, off, 64);
+    const float logp = static_cast<float>(t_acc);
     const float old_logp = a.old_logp[r * a.ld_batch];
     const float adv = a.advantages[r * a.ld_batch];
     const float ratio = expf(logp - old_logp);
@@ -89,64 +101,66 @@ __global__ __launch_bounds__(kLossThreads) void ppo_loss_kernel(const LossParams
     const float s1 = nadv * ratio;
     const float rc = fminf(fmaxf(ratio, p.ratio_lo), p.ratio_hi);
     const float s2 = nadv * rc;
-    surr = fmaxf(s1, s2);
     // d surrogate_loss / d ratio with torch's max / clamp conventions
     const float gs = p.inv_rows_surr;
     const float ga = s1 > s2 ? gs : (s1 == s2 ? gs * 0.5f : 0.0f);
     const float gb = s2 > s1 ? gs : (s1 == s2 ? gs * 0.5f : 0.0f);
     const bool in_clip = (ratio >= p.ratio_lo) && (ratio <= p.ratio_hi);
     const float g_ratio = ga * nadv + (in_clip ? gb * nadv : 0.0f);
-    g_logp = g_ratio * ratio;
-
-    // value loss
-    const float v = a.value[r * a.ld_value];
-    const float v_old = a.old_values[r * a.ld_batch];
-    const float ret = a.returns[r * a.ld_batch];
-    const float gv = p.inv_rows_value;  // c_v / R
-    float dv;
-    if (a.use_clipped_value_loss) {
-      const float dvo = v - v_old;
-      const float dvc = fminf(fmaxf(dvo, p.vclip_lo), p.vclip_hi);
-      const float vc = v_old + dvc;
-      const float e1 = v - ret, e2 = vc - ret;
-      const float l1 = e1 * e1, l2 = e2 * e2;
-      vloss = fmaxf(l1, l2);
-      const float g1 = l1 > l2 ? gv : (l1 == l2 ? gv * 0.5f : 0.0f);
-      const float g2 = l2 > l1 ? gv : (l1 == l2 ? gv * 0.5f : 0.0f);
-      const bool in_vclip = (dvo >= p.vclip_lo) && (dvo <= p.vclip_hi);
-      dv = (g1 * 2.0f) * e1 + (in_vclip ? (g2 * 2.0f) * e2 : 0.0f);
-    } else {
-      const float e = ret - v;
-      vloss = e * e;
-      dv = -((gv * 2.0f) * e);
-    }
-    a.d_value[r * a.ld_dvalue] = dv;
-
-    float* dmu = a.d_mean + r * a.ld_dmean;
-    for (int j = 0; j < A; ++j) {
-      const float d = act[j] - mu[j];
-      dmu[j] = (g_logp * d) / s_var[j];
-    }
-  }
-
-  // block partials (fixed lane order -> deterministic)
-  const double ssum = wave_sum(live ? static_cast<double>(surr) : 0.0);
-  const double vsum = wave_sum(live ? static_cast<double>(vloss) : 0.0);
-  const double ksum = wave_sum(live ? static_cast<double>(kl) : 0.0);
-  if (threadIdx.x == 0) {
-    part[0] = ssum;
-    part[1] = vsum;
-    part[2] = ksum;
-  }
-  for (int j = 0; j < A; ++j) {
-    double c = 0.0;
-    if (live) {
-      const float d = a.actions[r * a.ld_batch + j] - a.mean[r * a.ld_mean + j];
+    const float g_logp = g_ratio * ratio;
+    if (act_lane) {
+      a.d_mean[r * a.ld_dmean + j] = (g_logp * d) / var;
       // d logp / d log(std_j) = d^2 / var_j - 1
-      c = static_cast<double>(g_logp) * (static_cast<double>(d) * d / s_var[j] - 1.0);
+      acc_dstd += static_cast<double>(g_logp) * (static_cast<double>(d) * d / var - 1.0);
     }
-    c = wave_sum(c);
-    if (threadIdx.x == 0) part[kFixedCols + j] = c;
+    if (j == 0) {
+      const float v = a.value[r * a.ld_value];
+      const float v_old = a.old_values[r * a.ld_batch];
+      const float ret = a.returns[r * a.ld_batch];
+      const float gv = p.inv_rows_value;  // c_v / R
+      float dv, vloss;
+      if (a.use_clipped_value_loss) {
+        const float dvo = v - v_old;
+        const float dvc = fminf(fmaxf(dvo, p.vclip_lo), p.vclip_hi);
+        const float vc = v_old + dvc;
+        const float e1 = v - ret, e2 = vc - ret;
+        const float l1 = e1 * e1, l2 = e2 * e2;
+        vloss = fmaxf(l1, l2);
+        const float g1 = l1 > l2 ? gv : (l1 == l2 ? gv * 0.5f : 0.0f);
+        const float g2 = l2 > l1 ? gv : (l1 == l2 ? gv * 0.5f : 0.0f);
+        const bool in_vclip = (dvo >= p.vclip_lo) && (dvo <= p.vclip_hi);
+        dv = (g1 * 2.0f) * e1 + (in_vclip ? (g2 * 2.0f) * e2 : 0.0f);
+      } else {
+        const float e = ret - v;
+        vloss = e * e;
+        dv = -((gv * 2.0f) * e);
+      }
+      a.d_value[r * a.ld_dvalue] = dv;
+      acc_surr += static_cast<double>(fmaxf(s1, s2));
+      acc_val += static_cast<double>(vloss);
+    }
+  }
+
+  // block partials in a fixed order: fold the row groups of each wavefront, then the wavefronts through LDS
+  const int wave = threadIdx.x >> 6;
+  acc_kl = wave_sum(acc_kl);                   // lane 0 holds the wave's KL sum
+  if (L == 32) {
+    acc_dstd += __shfl_xor(acc_dstd, 32, 64);  // lanes j and j + 32 hold the same action
+    acc_surr += __shfl_xor(acc_surr, 32, 64);
+    acc_val += __shfl_xor(acc_val, 32, 64);
+  }
+  if (lane == 0) {
+    s_red[wave][0] = acc_surr;
+    s_red[wave][1] = acc_val;
+    s_red[wave][2] = acc_kl;
+  }
+  if (lane < A && lane < L) s_red[wave][kFixedCols + lane] = acc_dstd;
+  __syncthreads();
+  double* part = partials + static_cast<int64_t>(blockIdx.x) * cols;
+  for (int c = threadIdx.x; c < cols; c += kLossThreads) {
+    double sum = 0.0;
+    for (int w = 0; w < kLossThreads / 64; ++w) sum += s_red[w][c];
+    part[c] = sum;
   }
 }
 
@@ -157,22 +171,16 @@ __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
     ppo_device_state* __restrict__ state, int adaptive, float kl_hi, float kl_lo, double* __restrict__ trace) {
   const int A = p.a.num_actions;
   const int cols = kFixedCols + A;
-  __shared__ double s_red[kFinThreads / 64];
   __shared__ double s_col[kFixedCols + PPO_MAX_ACTIONS];
-  // column sums: each thread strides the blocks in a fixed order, then a fixed wave/LDS tree
-  for (int c = 0; c < cols; ++c) {
+  // column sums: wavefront w owns columns w, w + 4, ...; its lanes stride the block partials in a fixed order
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (int c = wave; c < cols; c += kFinThreads / 64) {
     double acc = 0.0;
-    for (int b = threadIdx.x; b < nblocks; b += kFinThreads) acc += partials[static_cast<int64_t>(b) * cols + c];
+    for (int b = lane; b < nblocks; b += 64) acc += partials[static_cast<int64_t>(b) * cols + c];
     acc = wave_sum(acc);
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      double s = 0.0;
-      for (int w = 0; w < kFinThreads / 64; ++w) s += s_red[w];
-      s_col[c] = s;
-    }
-    __syncthreads();
+    if (lane == 0) s_col[c] = acc;
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
     const double R = static_cast<double>(p.a.rows);
     const float surrogate = static_cast<float>(s_col[0] / R);
@@ -226,7 +234,12 @@ __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
   }
 }
 
-int64_t loss_blocks(int64_t rows) { return ceil_div(rows, kLossThreads); }
+int lanes_per_row(int num_actions) { return num_actions <= 32 ? 32 : 64; }
+
+int64_t loss_blocks(int64_t rows, int num_actions) {
+  const int groups = kLossThreads / lanes_per_row(num_actions);
+  return std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(rows, groups)));
+}
 
 int make_params(const ppo_loss_args* args, LossParams& p, const char* who) {
   PPO_REQUIRE(args != nullptr, "%s: null args", who);
@@ -262,7 +275,7 @@ using namespace ppo;
 
 extern "C" size_t ppo_loss_workspace_bytes(int64_t rows, int32_t num_actions) {
   if (rows <= 0 || num_actions <= 0 || num_actions > PPO_MAX_ACTIONS) return 0;
-  return sizeof(double) * static_cast<size_t>(loss_blocks(rows)) * (kFixedCols + num_actions);
+  return sizeof(double) * static_cast<size_t>(loss_blocks(rows, num_actions)) * (kFixedCols + num_actions);
 }
 
 extern "C" int ppo_gauss_ppo_loss(const ppo_loss_args* args, void* workspace, size_t workspace_bytes,
@@ -273,9 +286,14 @@ extern "C" int ppo_gauss_ppo_loss(const ppo_loss_args* args, void* workspace, si
   const size_t need = ppo_loss_workspace_bytes(args->rows, args->num_actions);
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_gauss_ppo_loss: workspace too small (%zu < %zu)",
               workspace_bytes, need);
-  const int64_t blocks = loss_blocks(args->rows);
-  hipLaunchKernelGGL(ppo_loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kLossThreads), 0,
-                     static_cast<hipStream_t>(stream), p, static_cast<double*>(workspace));
+  const int64_t blocks = loss_blocks(args->rows, args->num_actions);
+  if (lanes_per_row(args->num_actions) == 32) {
+    hipLaunchKernelGGL(ppo_loss_kernel<32>, dim3(static_cast<unsigned>(blocks)), dim3(kLossThreads), 0,
+                       static_cast<hipStream_t>(stream), p, static_cast<double*>(workspace));
+  } else {
+    hipLaunchKernelGGL(ppo_loss_kernel<64>, dim3(static_cast<unsigned>(blocks)), dim3(kLossThreads), 0,
+                       static_cast<hipStream_t>(stream), p, static_cast<double*>(workspace));
+  }
   return check_launch("ppo_loss_kernel");
 }
 
@@ -288,8 +306,7 @@ extern "C" int ppo_loss_finalize(const ppo_loss_args* args, const void* workspac
   const size_t need = ppo_loss_workspace_bytes(args->rows, args->num_actions);
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_loss_finalize: workspace too small");
   PPO_REQUIRE(d_std_param != nullptr && state != nullptr, "ppo_loss_finalize: null pointer");
-  const int64_t blocks = loss_blocks(args->rows);
-  PPO_REQUIRE(blocks <= INT32_MAX, "ppo_loss_finalize: too many rows");
+  const int64_t blocks = loss_blocks(args->rows, args->num_actions);
   // upstream compares the fp32 kl_mean with the Python floats desired_kl*2 and desired_kl/2, which torch rounds
   // to fp32 before comparing.
   const float kl_hi = static_cast<float>(desired_kl * 2.0);

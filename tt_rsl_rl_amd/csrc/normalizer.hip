@@ -1,9 +1,10 @@
 // A7: EmpiricalNormalization.update (rsl_rl/modules/normalization.py:51-78, single process) over the rollout's
 // stored observations, once per update after the epochs (rsl_rl/algorithms/ppo.py:327-330).
 //
-// Batch moments are reduced in fp64 and two passes (mean, then the biased variance around it), column-parallel:
-// each block owns a slab of rows, each thread a column, so every row is one coalesced read.  Partials are summed
-// in a fixed order.  The running-statistics update then replays torch's fp32 operation order on [dim] vectors.
+// Batch moments are reduced in fp64 and two passes (mean, then the biased variance around it): blocks own
+// (64-column tile, row slab) pairs, a wavefront reads 64 consecutive columns of a row (one coalesced 256 B access),
+// and the slab partials are summed by one block per column in a fixed order (deterministic).  The
+// running-statistics update then replays torch's fp32 operation order on [dim] vectors.
 #include "common.hpp"
 
 #pragma clang fp contract(off)
@@ -12,7 +13,8 @@ namespace ppo {
 namespace {
 
 constexpr int kNormThreads = 256;
-constexpr int kRowsPerSlab = 128;
+constexpr int kColTile = 64;     // one wavefront covers 64 consecutive columns
+constexpr int kMaxSlabs = 256;   // row slabs (blocks along the rows)
 constexpr int kMaxBlocks = PPO_MAX_GATHER_SEGMENTS;
 
 struct Blocks {
@@ -22,24 +24,26 @@ struct Blocks {
   int32_t dim;
 };
 
-__device__ inline float load_col(const Blocks& bl, int64_t r, int c) {
-  int i = 0;
-  for (int k = 1; k < kMaxBlocks; ++k)
-    if (k < bl.count && c >= bl.col_begin[k]) i = k;
-  return bl.b[i].src[r * bl.b[i].stride + (c - bl.col_begin[i])];
-}
-
-// pass 0: partial column sums; pass 1: partial sums of (x - mean)^2 (mean from stats[0..dim)).
-__global__ __launch_bounds__(kNormThreads) void moments_kernel(const Blocks bl, int64_t rows, int pass,
-                                                               const double* __restrict__ stats,
+// pass 0: per-slab column sums; pass 1: per-slab sums of (x - mean)^2 (mean from stats[0..dim)).
+// grid = (column tiles, slabs); lane = column inside the tile, wave w takes rows r0 + w, r0 + w + 4, ...
+__global__ __launch_bounds__(kNormThreads) void moments_kernel(const Blocks bl, int64_t rows, int64_t slab_rows,
+                                                               int pass, const double* __restrict__ stats,
                                                                double* __restrict__ partials) {
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kRowsPerSlab;
-  const int64_t r1 = min(rows, r0 + kRowsPerSlab);
-  for (int c = threadIdx.x; c < bl.dim; c += kNormThreads) {
+  __shared__ double red[kNormThreads / 64][kColTile];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * kColTile + lane;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * slab_rows;
+  const int64_t r1 = min(rows, r0 + slab_rows);
+  double acc = 0.0;
+  if (c < bl.dim) {
+    int i = 0;
+    for (int k = 1; k < kMaxBlocks; ++k)
+      if (k < bl.count && c >= bl.col_begin[k]) i = k;
+    const float* src = bl.b[i].src + (c - bl.col_begin[i]);
+    const int64_t stride = bl.b[i].stride;
     const double mu = pass ? stats[c] : 0.0;
-    double acc = 0.0;
-    for (int64_t r = r0; r < r1; ++r) {
-      const double v = load_col(bl, r, c);
+    for (int64_t r = r0 + wave; r < r1; r += kNormThreads / 64) {
+      const double v = src[r * stride];
       if (pass == 0) {
         acc += v;
       } else {
@@ -47,16 +51,29 @@ __global__ __launch_bounds__(kNormThreads) void moments_kernel(const Blocks bl, 
         acc += d * d;
       }
     }
-    partials[static_cast<int64_t>(blockIdx.x) * bl.dim + c] = acc;
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && c < bl.dim) {
+    double s = 0.0;
+    for (int w = 0; w < kNormThreads / 64; ++w) s += red[w][lane];
+    partials[static_cast<int64_t>(blockIdx.y) * bl.dim + c] = s;
   }
 }
 
-// Fixed-order column reduction of the slab partials: stats[c] = sum / rows (pass 0 -> mean, pass 1 -> var).
+// One block per column: fixed-order strided sums over the slab partials, then a fixed tree -> sum / rows.
 __global__ __launch_bounds__(kNormThreads) void moments_reduce_kernel(const double* __restrict__ partials, int slabs,
                                                                       int dim, int64_t rows, double* __restrict__ out) {
-  for (int c = blockIdx.x * kNormThreads + threadIdx.x; c < dim; c += gridDim.x * kNormThreads) {
+  __shared__ double red[kNormThreads / 64];
+  const int c = blockIdx.x;
+  double acc = 0.0;
+  for (int k = threadIdx.x; k < slabs; k += kNormThreads) acc += partials[static_cast<int64_t>(k) * dim + c];
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
     double s = 0.0;
-    for (int k = 0; k < slabs; ++k) s += partials[static_cast<int64_t>(k) * dim + c];
+    for (int w = 0; w < kNormThreads / 64; ++w) s += red[w];
     out[c] = s / static_cast<double>(rows);
   }
 }
@@ -88,13 +105,15 @@ __global__ __launch_bounds__(kNormThreads) void running_update_kernel(const doub
 }
 
 struct NormPlan {
-  int64_t slabs;
+  int64_t slabs, slab_rows;
   size_t partial_off, mean_off, var_off, total;  // doubles
 };
 
 NormPlan plan_norm(int64_t rows, int dim) {
   NormPlan p;
-  p.slabs = ceil_div(rows, kRowsPerSlab);
+  p.slabs = std::min<int64_t>(kMaxSlabs, ceil_div(rows, 64));
+  p.slab_rows = ceil_div(rows, p.slabs);
+  p.slabs = ceil_div(rows, p.slab_rows);
   p.partial_off = 0;
   p.mean_off = static_cast<size_t>(p.slabs) * dim;
   p.var_off = p.mean_off + dim;
@@ -140,13 +159,11 @@ extern "C" int ppo_normalizer_update(const ppo_column_block* blocks, int32_t num
   double* bvar = ws + plan.var_off;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int slabs = static_cast<int>(plan.slabs);
-  const int rblocks = static_cast<int>(ceil_div(dim, kNormThreads));
-  hipLaunchKernelGGL(moments_kernel, dim3(slabs), dim3(kNormThreads), 0, s, bl, rows, 0, bmean, partials);
-  hipLaunchKernelGGL(moments_reduce_kernel, dim3(rblocks), dim3(kNormThreads), 0, s, partials, slabs, dim, rows,
-                     bmean);
-  hipLaunchKernelGGL(moments_kernel, dim3(slabs), dim3(kNormThreads), 0, s, bl, rows, 1, bmean, partials);
-  hipLaunchKernelGGL(moments_reduce_kernel, dim3(rblocks), dim3(kNormThreads), 0, s, partials, slabs, dim, rows,
-                     bvar);
+  const dim3 grid(static_cast<unsigned>(ceil_div(dim, kColTile)), static_cast<unsigned>(slabs));
+  hipLaunchKernelGGL(moments_kernel, grid, dim3(kNormThreads), 0, s, bl, rows, plan.slab_rows, 0, bmean, partials);
+  hipLaunchKernelGGL(moments_reduce_kernel, dim3(dim), dim3(kNormThreads), 0, s, partials, slabs, dim, rows, bmean);
+  hipLaunchKernelGGL(moments_kernel, grid, dim3(kNormThreads), 0, s, bl, rows, plan.slab_rows, 1, bmean, partials);
+  hipLaunchKernelGGL(moments_reduce_kernel, dim3(dim), dim3(kNormThreads), 0, s, partials, slabs, dim, rows, bvar);
   hipLaunchKernelGGL(running_update_kernel, dim3(1), dim3(kNormThreads), 0, s, bmean, bvar, dim, rows, state_mean,
                      state_var, state_std, count);
   return check_launch("normalizer_update");
