@@ -135,7 +135,20 @@ def main() -> int:
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-phase-events", action="store_true", help="do not record per-launch HIP events")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        n = args.copy_calibration * (1 << 20) // 4
+        x = torch.ones(n, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 4 * n}))
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py: this build runs the PPO update on ONE GPU; --gpus {args.gpus} is not supported "

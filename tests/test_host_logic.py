@@ -1,0 +1,111 @@
+"""Host-side logic of the plugin, without a GPU: drop-in construction, initial weights and state_dict layout equal
+upstream's (through the oracle), class resolution, rejected options, the packed-table layout and the workload table.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import pytest
+import torch
+
+from oracle import rollout as R
+from tt_rsl_rl_amd import workloads as W
+from tt_rsl_rl_amd.engine import TableLayout
+from tt_rsl_rl_amd.models import MLPModel
+from tt_rsl_rl_amd.ppo import PPO, resolve_callable
+
+
+def test_workload_table_matches_the_oracle_copy():
+    assert W.WORKLOADS == R.WORKLOADS
+    assert W.ALGORITHM == R.DEFAULT_ALGORITHM
+
+
+@pytest.mark.parametrize("name", ["flat48", "humanoid", "rough235"])
+def test_initial_weights_and_state_dict_layout_equal_upstream(name):
+    """Same seed -> same default nn.Linear init as upstream (actor then critic), same keys, same parameter order."""
+    w = R.scaled(R.WORKLOADS[name], num_envs=8)
+    ora = R.make_oracle(w, seed=3)
+    torch.manual_seed(3)
+    cfg = W.train_cfg(w)
+    obs = R.zero_obs(w)
+    kw = lambda c: {k: v for k, v in c.items() if k != "class_name"}
+    actor = MLPModel(obs, cfg["obs_groups"], "actor", w["num_actions"], **kw(cfg["actor"]))
+    critic = MLPModel(obs, cfg["obs_groups"], "critic", 1, **kw(cfg["critic"]))
+    for mine, ref in ((actor, ora.actor), (critic, ora.critic)):
+        sd, rd = mine.state_dict(), ref.state_dict()
+        assert list(sd) == list(rd)
+        for k in sd:
+            assert torch.equal(sd[k], rd[k]), k
+        assert [n for n, _ in mine.named_parameters()] == [n for n, _ in ref.named_parameters()]
+
+
+def test_class_resolution_maps_upstream_names():
+    assert resolve_callable("MLPModel") is MLPModel
+    assert resolve_callable("rsl_rl.models:MLPModel") is MLPModel
+    assert resolve_callable("rsl_rl.algorithms:PPO") is PPO
+    assert resolve_callable("tt_rsl_rl_amd.ppo:PPO") is PPO
+    with pytest.raises(NotImplementedError):
+        resolve_callable("RNNModel")
+    with pytest.raises(ValueError):
+        resolve_callable("NoSuchClass")
+
+
+def _models(w):
+    cfg = W.train_cfg(w)
+    obs = R.zero_obs(w)
+    kw = lambda c: {k: v for k, v in c.items() if k != "class_name"}
+    return (MLPModel(obs, cfg["obs_groups"], "actor", w["num_actions"], **kw(cfg["actor"])),
+            MLPModel(obs, cfg["obs_groups"], "critic", 1, **kw(cfg["critic"])))
+
+
+@pytest.mark.parametrize("kwargs, exc", [
+    ({"device": "cpu"}, RuntimeError),
+    ({"device": "cuda", "rnd_cfg": {"weight": 1.0}}, NotImplementedError),
+    ({"device": "cuda", "symmetry_cfg": {"use_data_augmentation": True}}, NotImplementedError),
+    ({"device": "cuda", "multi_gpu_cfg": {"global_rank": 0, "world_size": 2}}, NotImplementedError),
+    ({"device": "cuda", "optimizer": "sgd"}, NotImplementedError),
+    ({"device": "cuda", "use_mixed_precision": True}, NotImplementedError),
+])
+def test_unsupported_options_are_rejected_before_touching_the_gpu(kwargs, exc):
+    w = R.scaled(R.WORKLOADS["flat48"], num_envs=8)
+    actor, critic = _models(w)
+    with pytest.raises(exc):
+        PPO(actor, critic, None, **kwargs)
+
+
+def test_non_elu_activation_is_rejected():
+    w = R.scaled(R.WORKLOADS["flat48"], num_envs=8)
+    cfg = W.train_cfg(w)
+    with pytest.raises(NotImplementedError):
+        MLPModel(R.zero_obs(w), cfg["obs_groups"], "critic", 1, hidden_dims=[8], activation="tanh")
+
+
+@pytest.mark.parametrize("da, dc, a", [(96, 99, 29), (48, 48, 12), (235, 235, 12), (3, 5, 1)])
+def test_table_layout_is_aligned_and_disjoint(da, dc, a):
+    lay = TableLayout(da, dc, a)
+    spans = [(lay.xa, da), (lay.xc, dc), (lay.actions, a), (lay.old_mean, a), (lay.old_std, a),
+             (lay.old_logp, 1), (lay.adv, 1), (lay.old_values, 1), (lay.returns, 1), (lay.adv_mb, 1)]
+    for start, _ in spans[:5]:
+        assert start % 4 == 0
+    ends = sorted((s, s + n) for s, n in spans)
+    for (s0, e0), (s1, e1) in zip(ends, ends[1:]):
+        assert e0 <= s1, "columns overlap"
+    assert lay.width % 4 == 0 and lay.width >= ends[-1][1]
+
+
+def test_gemm_flop_counts():
+    """Algorithmic FLOPs per update (fwd + input-grad (not for layer 0) + weight-grad, 5 epochs)."""
+    assert W.gemm_flops_per_update(W.WORKLOADS["flat48"]) == pytest.approx(1.06791174144e12)
+    assert W.gemm_flops_per_update(W.WORKLOADS["humanoid"]) == pytest.approx(1.1739856896e12)
+    assert W.gemm_flops_per_update(W.WORKLOADS["rough235"]) == pytest.approx(1.44439246848e12)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    res = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert res.returncode != 0 and "ONE GPU" in res.stderr

@@ -1,0 +1,103 @@
+"""The C ABI without a GPU: libppo_hip.so loads, exports every entry point include/ppo_hip.h declares, the ctypes
+binding declares exactly those, the struct layouts agree with the C compiler's, and argument validation reports
+errors (these calls return before any HIP call, so no GPU is touched)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "ppo_hip.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|size_t|const char\*)\s+(ppo_\w+)\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    from tt_rsl_rl_amd import _lib
+
+    lib = _lib.load()
+    declared = _declared()
+    assert len(declared) >= 19
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in ppo_hip.h but not exported"
+    assert sorted(_lib.EXPORTED_SYMBOLS) == declared, "ctypes signatures must cover exactly the header"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    exported = sorted(set(re.findall(r" T (ppo_\w+)$", out, flags=re.M)))
+    assert exported == declared, "the library exports nothing beyond the header"
+
+
+STRUCTS = {
+    "ppo_gather_segment": ("GatherSegment", ["src", "src_stride", "width", "dst_col", "norm_mean", "norm_std",
+                                             "norm_eps"]),
+    "ppo_linear_fwd_problem": ("LinearFwdProblem", ["x", "ldx", "w", "b", "z", "ldz", "h", "ldh", "in_features",
+                                                    "out_features"]),
+    "ppo_linear_bwd_dx_problem": ("LinearBwdDxProblem", ["dz", "lddz", "w", "z_prev", "ldz_prev", "dz_prev",
+                                                         "lddz_prev", "in_features", "out_features"]),
+    "ppo_linear_bwd_dw_problem": ("LinearBwdDwProblem", ["dz", "lddz", "x", "ldx", "dw", "db", "in_features",
+                                                         "out_features"]),
+    "ppo_column_block": ("ColumnBlock", ["src", "stride", "width"]),
+    "ppo_loss_args": ("LossArgs", ["rows", "num_actions", "std_type", "mean", "ld_mean", "value", "ld_value",
+                                   "actions", "old_mean", "old_std", "old_logp", "advantages", "old_values", "returns",
+                                   "ld_batch", "std_param", "std_lo", "std_hi", "clip_param", "value_loss_coef",
+                                   "entropy_coef", "use_clipped_value_loss", "d_mean", "ld_dmean", "d_value",
+                                   "ld_dvalue"]),
+    "ppo_device_state": ("DeviceState", ["learning_rate", "sum_value_loss", "sum_surrogate_loss", "sum_entropy",
+                                         "last_kl_mean", "last_value_loss", "last_surrogate_loss", "last_entropy",
+                                         "total_norm", "clip_coef", "num_minibatches"]),
+}
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_struct_layouts_match_the_c_compiler(tmp_path):
+    from tt_rsl_rl_amd import _lib
+
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, (_, fields) in STRUCTS.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f in fields:
+            lines.append(f'  printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        k, v = line.rsplit(" ", 1)
+        got[k] = int(v)
+    for cname, (pyname, fields) in STRUCTS.items():
+        cls = getattr(_lib, pyname)
+        assert got[f"{cname} size"] == ctypes.sizeof(cls), cname
+        for f in fields:
+            assert got[f"{cname}.{f}"] == getattr(cls, f).offset, f"{cname}.{f}"
+
+
+def test_argument_validation_reports_errors_without_a_gpu():
+    from tt_rsl_rl_amd import _lib
+
+    lib = _lib.load()
+    assert lib.ppo_gae(None, None, None, None, None, None, 24, 4096, 0.99, 0.95, None) == _lib.PPO_EINVAL
+    assert "null pointer" in _lib.last_error()
+    with pytest.raises(ValueError, match="num_steps"):
+        _lib.call("ppo_gae", 8, 8, 8, 8, 8, 8, 0, 4096, 0.99, 0.95, None)
+    with pytest.raises(ValueError, match="count"):
+        _lib.call("ppo_linear_fwd", None, 0, 10, 1, None)
+    with pytest.raises(ValueError, match="num_actions"):
+        args = _lib.LossArgs(rows=10, num_actions=65)
+        _lib.call("ppo_gauss_ppo_loss", ctypes.byref(args), None, 0, None)
+    # workspace queries are pure host arithmetic
+    assert lib.ppo_adv_normalize_workspace_bytes(98304) > 0
+    assert lib.ppo_loss_workspace_bytes(24576, 29) > 0
+    assert lib.ppo_loss_workspace_bytes(24576, 65) == 0
+    assert lib.ppo_adam_workspace_bytes(433211) >= 8 * (433211 // 4096)
+    probs = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512)])
+    assert lib.ppo_linear_bwd_dw_workspace_bytes(probs, 1, 24576) >= 4 * 512 * 96

@@ -156,11 +156,11 @@ __global__ __launch_bounds__(kLossThreads) void ppo_loss_kernel(const LossParams
   }
   if (lane < A && lane < L) s_red[wave][kFixedCols + lane] = acc_dstd;
   __syncthreads();
-  double* part = partials + static_cast<int64_t>(blockIdx.x) * cols;
+  // column-major partials [cols][blocks]: the finalize reads each column as one contiguous run
   for (int c = threadIdx.x; c < cols; c += kLossThreads) {
     double sum = 0.0;
     for (int w = 0; w < kLossThreads / 64; ++w) sum += s_red[w][c];
-    part[c] = sum;
+    partials[static_cast<int64_t>(c) * gridDim.x + blockIdx.x] = sum;
   }
 }
 
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int c = wave; c < cols; c += kFinThreads / 64) {
     double acc = 0.0;
-    for (int b = lane; b < nblocks; b += 64) acc += partials[static_cast<int64_t>(b) * cols + c];
+    for (int b = lane; b < nblocks; b += 64) acc += partials[static_cast<int64_t>(c) * nblocks + b];
     acc = wave_sum(acc);
     if (lane == 0) s_col[c] = acc;
   }

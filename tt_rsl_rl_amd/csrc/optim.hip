@@ -1,7 +1,7 @@
 // A12 + A13: per-group gradient-norm clipping (torch.nn.utils.clip_grad_norm_, rsl_rl/algorithms/ppo.py:309-310)
 // fused with Adam (torch.optim.Adam, single-tensor path, ppo.py:311) over flat parameter / gradient / moment
 // buffers.  Two launches:
-//   1. sum of squares of the gradient, one fp64 partial per 4096-element chunk (chunks never straddle groups);
+//   1. sum of squares of the gradient, one fp64 partial per 1024-element chunk (chunks never straddle groups);
 //   2. every block re-reduces its group's partials in the same fixed order (so all blocks agree bit for bit),
 //      derives the clip coefficient and streams p, g, m, v once: 16 B read + 12 B written per parameter
 //      (+4 B rewriting the clipped gradient, which upstream leaves in .grad).
@@ -14,7 +14,7 @@ namespace ppo {
 namespace {
 
 constexpr int kAdamThreads = 256;
-constexpr int kChunk = 4096;
+constexpr int kChunk = 1024;  // ~420 blocks for the humanoid models: every CU busy
 
 struct GroupTable {
   int64_t begin[PPO_MAX_PARAM_GROUPS + 1];
