@@ -108,6 +108,7 @@ int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t count, int64_
 
 /* backward to the layer input: dz_prev = (dz w) * act'(z_prev), act' of ELU = 1 if z > 0 else exp(z)
  * (torch's elu_backward on the input).  z_prev == NULL means no activation (plain dx = dz w).
+ * The workspace (ppo_linear_bwd_dx_workspace_bytes, 16-byte aligned) receives w^T of every problem.
  * Replaces autograd's mm backward + EluBackward (rsl_rl/algorithms/ppo.py:298). */
 typedef struct ppo_linear_bwd_dx_problem {
   const float* dz; int64_t lddz;         /* [rows, out] */
@@ -118,7 +119,9 @@ typedef struct ppo_linear_bwd_dx_problem {
   int32_t out_features;
 } ppo_linear_bwd_dx_problem;
 
-int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, ppo_stream_t stream);
+size_t ppo_linear_bwd_dx_workspace_bytes(const ppo_linear_bwd_dx_problem* problems, int32_t count);
+int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, void* workspace,
+                      size_t workspace_bytes, ppo_stream_t stream);
 
 /* backward to the parameters: dw = dz^T x, db = sum_rows dz, reduced over rows in fixed-order split-K partials
  * (deterministic: no float atomics).  Replaces autograd's AddmmBackward for weight and bias. */

@@ -620,6 +620,9 @@ class PPO:
         self.use_mixed_precision = use_mixed_precision
         # per-mini-batch diagnostics (not upstream): kl_mean, lr after the rule, the three losses, batch indices
         self.trace: list[dict] = []
+        # per-mini-batch state hook (not upstream): called as recorder("pre", self) before a mini-batch's forward
+        # pass and recorder("post", self) after its optimiser step; tests use it to snapshot the training state
+        self.recorder = None
         # hook to replace the KL (upstream's tests monkeypatch actor.get_kl_divergence the same way)
 
     # -- rollout side ------------------------------------------------------------------------------------------------
@@ -668,6 +671,8 @@ class PPO:
         else:
             generator = self.storage.mini_batch_generator(self.num_mini_batches, self.num_learning_epochs)
         for batch in generator:
+            if self.recorder is not None:
+                self.recorder("pre", self)
             if self.normalize_advantage_per_mini_batch and batch.advantages.numel() > 1:
                 with torch.no_grad():
                     batch.advantages = (batch.advantages - batch.advantages.mean()) / (batch.advantages.std() + 1e-8)
@@ -695,12 +700,18 @@ class PPO:
             nn.utils.clip_grad_norm_(self.actor.parameters(), self.max_grad_norm)
             nn.utils.clip_grad_norm_(self.critic.parameters(), self.max_grad_norm)
             self.optimizer.step()
+            if self.recorder is not None:
+                self.recorder("post", self)
+            with torch.no_grad():  # diagnostic: distance of the nearest ratio to a clip boundary (not upstream)
+                ratio = torch.exp(logp.detach() - batch.old_actions_log_prob.squeeze(-1)).double()
+                margin = torch.minimum((ratio - (1.0 + self.clip_param)).abs(),
+                                       (ratio - (1.0 - self.clip_param)).abs()).min().item()
             v, s, e = value_loss.item(), surrogate_loss.item(), entropy.mean().item()
             mean_value_loss += v
             mean_surrogate_loss += s
             mean_entropy += e
             self.trace.append({"kl_mean": kl_value, "lr": self.learning_rate, "value": v, "surrogate": s,
-                               "entropy": e, "indices": batch.indices})
+                               "entropy": e, "indices": batch.indices, "clip_margin": margin})
         obs = {k: v.flatten(0, 1) for k, v in self.storage.observations.items()}
         self.actor.update_normalization(obs)
         self.critic.update_normalization(obs)

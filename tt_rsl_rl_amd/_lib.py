@@ -90,7 +90,8 @@ _SIGNATURES = [
     ("ppo_adv_normalize", C.c_int, [f32p, i64, f32p, i64, i64, C.c_float, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("ppo_gather_rows", C.c_int, [C.c_void_p, i64, i64, C.POINTER(GatherSegment), i32, f32p, i64, C.c_void_p]),
     ("ppo_linear_fwd", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, C.c_void_p]),
-    ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, C.c_void_p]),
+    ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),
+    ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("ppo_linear_bwd_dw_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDwProblem), i32, i64]),
     ("ppo_linear_bwd_dw", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("ppo_obs_normalize", C.c_int, [f32p, i64, f32p, i64, i64, i32, f32p, f32p, C.c_float, C.c_void_p]),

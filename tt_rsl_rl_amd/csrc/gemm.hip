@@ -1,20 +1,26 @@
 // A6 linear layers (rsl_rl/modules/mlp.py:27-95; autograd of nn.Linear / nn.ELU) as fp32 MFMA GEMMs for gfx950.
 //
-// One templated kernel computes C = A B over BM x BN output tiles with 256 threads: 4 wavefronts in a 2 x 2
-// arrangement, each owning a (BM/2) x (BN/2) sub-tile of 32 x 32 v_mfma_f32_32x32x2f32 accumulators.  A and B are
-// staged through double-buffered LDS in BK-deep k-slabs stored k-major, so every MFMA operand fetch is one
-// ds_read_b32 per lane and each slab costs a single barrier; the next slab is fetched from global memory into
-// registers (float4 where the leading dimension allows, chosen per problem at launch) while the current one is
-// multiplied.  A(m,k) and B(k,n) are read either k-contiguous or m/n-contiguous (template flags), which covers the
-// three products of a layer without transposing anything in memory:
-//   forward     z[r,o]   = sum_i x[r,i]  w[o,i]   A = x  (k-contig)   B = w (k-contig)   epilogue +b, ELU
-//   input-grad  dzp[r,i] = sum_o dz[r,o] w[o,i]   A = dz (k-contig)   B = w (n-contig)   epilogue * ELU'(z_prev)
-//   weight-grad dw[o,i]  = sum_r dz[r,o] x[r,i]   A = dz (m-contig)   B = x (n-contig)   split-K partials
-// The weight-grad kernel also sums its A slab over k (blocks of the first n tile only), which yields the bias
-// gradient db[o] = sum_r dz[r,o] in fp64.  Split-K partials are reduced in a fixed order by a second kernel, so the
-// result is deterministic.  Several independent problems (actor and critic, or all layers of the weight-grad)
-// share one launch: the block index is mapped to (problem, split, tile) through per-problem block offsets, after
-// an XCD-aware permutation that places consecutive tiles (which share an A panel) on the same XCD / L2.
+// Two kernel families, both 256 threads = 4 wavefronts in a 2 x 2 arrangement over a BM x BN output tile, each
+// wave owning (BM/2) x (BN/2) of 32 x 32 v_mfma_f32_32x32x2f32 accumulators, both fed by gfx950's direct
+// global->LDS loads (global_load_lds_dwordx4 / _dword: no register staging, no ds_write) into a two-stage LDS ring
+// with one barrier per BK-deep k-slab:
+//
+//   NT  C[m,n] = sum_k A[m,k] B[n,k]        both operands k-contiguous in memory
+//       forward     z[r,o]   = sum_i x[r,i]  w[o,i]    A = x,  B = w           epilogue +b (ELU)
+//       input-grad  dzp[r,i] = sum_o dz[r,o] wt[i,o]   A = dz, B = w^T (copied) epilogue * ELU'(z_prev)
+//   TN  C[m,n] = sum_k A[k,m] B[k,n]        both operands m/n-contiguous ("k-major")
+//       weight-grad dw[o,i]  = sum_r dz[r,o] x[r,i]    split-K partials, fixed-order reduction, fp64 db
+//
+// NT tiles are stored row-per-m in LDS with BK floats per row and the 16-byte chunks of each row XOR-swizzled by
+// the row index, so a ds_read_b128 of 16 consecutive rows is bank-conflict free.  The k order inside a slab is
+// permuted so that one ds_read_b128 per operand and lane supplies four consecutive MFMA k-steps: at step s of
+// group g, lane half h contributes k = 8g + 4h + s for both operands (any bijection of k works if A and B agree).
+// TN tiles are stored k-major (row per k, BM or BN floats), and rows are interleaved across the two 32-wide MFMA
+// tiles of a wave (tile i takes m = 2*rho + i) so one ds_read_b64 feeds both tiles and the partial stores are
+// float2-wide.  Reads of rows past M or N are clamped into the operand (their results are discarded); the K tail
+// is loaded through a masked path with zeros.  Several independent problems (actor and critic, or all layers of
+// the weight-grad) share one launch: the block index maps to (problem, split, tile) through per-problem block
+// offsets, after an XCD-aware permutation that places consecutive tiles (which share an A panel) on one XCD / L2.
 #include <cstdlib>
 #include <cstring>
 
@@ -25,6 +31,7 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_ELU = 1, EPI_ELU_GRAD = 2, EPI_STORE = 3, EPI_PARTIAL = 4 };
 
@@ -35,13 +42,12 @@ struct Problem {
   float* C2;
   const float* vec;  // bias [N]
   const float* aux;  // ELU'-source z_prev [M, N]
-  double* colsum;    // [splits, M] row sums of A over each split's k range (fp64: bias grads cancel heavily)
+  double* colsum;    // [splits, M] sums of A over each split's k range (fp64: bias grads cancel heavily)
   int64_t lda, ldb, ldc, ldc2, ldaux;
   int64_t partial_stride;  // floats between split partials of C
   int32_t M, N, K;
   int32_t tiles_m, tiles_n, splits, k_chunk;
   int32_t block_begin;
-  int32_t a_vec, b_vec;    // float4 global loads along the contiguous dimension are valid for this problem
 };
 
 struct Group {
@@ -61,104 +67,11 @@ __device__ inline int xcd_remap(int b, int n) {
   return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
 }
 
-// Loads one BK-deep slab of a BM-wide (A) or BN-wide (B) operand into registers and stores it k-major into LDS.
-// KMAJ: element (x, k) at base[(x0 + x) * ld + k0 + k]; otherwise at base[(k0 + k) * ld + x0 + x].
-template <int BX, int BK, bool KMAJ, bool VEC>
-struct Slab {
-  static constexpr int kElems = BX * BK / kThreads;
-  static_assert(kElems % 4 == 0, "slab must give every thread a multiple of 4 elements");
-  float r[kElems];
-  int valid[kElems / 4];  // float4 path: leading elements of each vector inside the operand (the rest -> 0)
-
-  // Issues the loads only: nothing here consumes the loaded registers, so the wait for them lands in store(),
-  // after the MFMAs of the current slab.
-  __device__ inline void load(const float* __restrict__ base, int64_t ld, int x0, int X, int k0, int k_end) {
-    const int tid = threadIdx.x;
-    if (VEC) {
-#pragma unroll
-      for (int i = 0; i < kElems / 4; ++i) {
-        const int q = tid + kThreads * i;
-        int x, k;
-        if (KMAJ) {
-          x = q / (BK / 4);
-          k = (q % (BK / 4)) * 4;
-        } else {
-          k = q / (BX / 4);
-          x = (q % (BX / 4)) * 4;
-        }
-        const int gx = x0 + x, gk = k0 + k;
-        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-        int n = 0;
-        if (KMAJ) {
-          if (gx < X && gk < k_end) {
-            v = *reinterpret_cast<const f32x4*>(base + gx * ld + gk);
-            n = min(4, k_end - gk);
-          }
-        } else {
-          if (gk < k_end && gx < X) {
-            v = *reinterpret_cast<const f32x4*>(base + gk * ld + gx);
-            n = min(4, X - gx);
-          }
-        }
-        valid[i] = n;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) r[4 * i + j] = v[j];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kElems; ++i) {
-        const int q = tid + kThreads * i;
-        const int x = KMAJ ? q / BK : q % BX;
-        const int k = KMAJ ? q % BK : q / BX;
-        const int gx = x0 + x, gk = k0 + k;
-        float v = 0.0f;
-        if (gx < X && gk < k_end) v = KMAJ ? base[gx * ld + gk] : base[gk * ld + gx];
-        r[i] = v;
-      }
-    }
-  }
-
-  template <int LDS_W>
-  __device__ inline void store(float (*lds)[LDS_W]) {
-    const int tid = threadIdx.x;
-    if (VEC) {
-#pragma unroll
-      for (int i = 0; i < kElems / 4; ++i) {
-        const int q = tid + kThreads * i;
-        float e[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] = j < valid[i] ? r[4 * i + j] : 0.0f;
-        if (KMAJ) {
-          const int x = q / (BK / 4), k = (q % (BK / 4)) * 4;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) lds[k + j][x] = e[j];
-        } else {
-          const int k = q / (BX / 4), x = (q % (BX / 4)) * 4;
-          f32x4 v = {e[0], e[1], e[2], e[3]};
-          *reinterpret_cast<f32x4*>(&lds[k][x]) = v;
-        }
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kElems; ++i) {
-        const int q = tid + kThreads * i;
-        const int x = KMAJ ? q / BK : q % BX;
-        const int k = KMAJ ? q % BK : q / BX;
-        lds[k][x] = r[i];
-      }
-    }
-  }
+struct TileCoord {
+  int pi, split, tm, tn;
 };
 
-template <int BM, int BN, int BK, bool A_KMAJ, bool B_KMAJ, bool A_VEC, bool B_VEC, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(const Group g) {
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int PAD = 4;
-  static_assert(TM >= 1 && TN >= 1, "tile too small");
-  __shared__ __align__(16) float As[2][BK][BM + PAD];
-  __shared__ __align__(16) float Bs[2][BK][BN + PAD];
-
+__device__ inline TileCoord locate(const Group& g) {
   const int b = g.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
   int pi = 0;
 #pragma unroll
@@ -168,19 +81,113 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const Group g) {
   const Problem& P = g.p[pi];
   const int local = b - P.block_begin;
   const int tiles_mn = P.tiles_m * P.tiles_n;
-  const int split = local / tiles_mn;
-  const int t = local - split * tiles_mn;
-  const int tm = t / P.tiles_n;
-  const int tn = t - tm * P.tiles_n;
-  const int row0 = tm * BM;
-  const int col0 = tn * BN;
-  const int k_begin = split * P.k_chunk;
-  const int k_end = min(P.K, k_begin + P.k_chunk);
-  const int M = P.M, N = P.N;
+  TileCoord t;
+  t.pi = pi;
+  t.split = local / tiles_mn;
+  const int r = local - t.split * tiles_mn;
+  t.tm = r / P.tiles_n;
+  t.tn = r - t.tm * P.tiles_n;
+  return t;
+}
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
+// Direct global->LDS copy: every lane of the wave moves `bytes` (16 or 4) from its own global address to
+// lds_wave + lane * bytes.  lds_wave must be wave-uniform.
+template <int BYTES>
+__device__ __forceinline__ void dma(const float* src, float* lds_wave) {
+  static_assert(BYTES == 16 || BYTES == 4, "16- or 4-byte direct loads");
+  if constexpr (BYTES == 16) {
+    __builtin_amdgcn_global_load_lds(src, lds_wave, 16, 0, 0);
+  } else {
+    __builtin_amdgcn_global_load_lds(src, lds_wave, 4, 0, 0);
+  }
+}
+
+// Waits for this wave's outstanding global loads (including the LDS-direct ones, which the compiler does not
+// track as LDS writes: hence the memory clobber).
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// ------------------------------------------------------------------------------------------------------------------
+// NT: operands stored [x][k] (k contiguous); LDS tile [BX][BK] with swizzled 16-byte chunks.
+// ------------------------------------------------------------------------------------------------------------------
+
+// Physical chunk of logical chunk c in LDS row `row` is c ^ swz(row).  gfx950's LDS serves a ds_read_b128 16 lanes
+// (16 x 16 bytes = all 64 banks) at a time; those lanes read one logical chunk of 16 consecutive rows, which the
+// swizzle spreads over 16 distinct 16-byte bank groups (rows sharing a 256-byte window get different chunks).
+template <int BK>
+__device__ __forceinline__ int nt_swz(int row) {
+  constexpr int CPR = BK / 4;
+  static_assert(CPR == 4 || CPR == 8, "BK must be 16 or 32");
+  return CPR == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+// One full k-slab [x0, x0 + BX) x [k0, k0 + BK) of an NT operand into LDS by direct loads (rows >= X clamped).
+template <int BX, int BK, bool W16>
+__device__ __forceinline__ void nt_dma(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
+                                       float* lds_op, int wave, int lane) {
+  constexpr int CPR = BK / 4;
+  if constexpr (W16) {
+    constexpr int RPI = 64 / CPR;  // rows per instruction (64 chunks of 16 bytes)
+    constexpr int NQ = BX / RPI;
+#pragma unroll
+    for (int q0 = 0; q0 < NQ; q0 += 4) {
+      const int q = q0 + wave;
+      if (NQ % 4 == 0 || q < NQ) {
+        const int row = q * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ nt_swz<BK>(row);
+        const int gx = min(x0 + row, X - 1);
+        dma<16>(base + static_cast<int64_t>(gx) * ld + k0 + 4 * c, lds_op + q * 256);
+      }
+    }
+  } else {
+    constexpr int RPI = 64 / BK;  // rows per instruction (64 floats)
+    constexpr int NQ = BX / RPI;
+#pragma unroll
+    for (int q0 = 0; q0 < NQ; q0 += 4) {
+      const int q = q0 + wave;
+      if (NQ % 4 == 0 || q < NQ) {
+        const int row = q * RPI + lane / BK;
+        const int f = lane % BK;
+        const int c = (f >> 2) ^ nt_swz<BK>(row);
+        const int gx = min(x0 + row, X - 1);
+        dma<4>(base + static_cast<int64_t>(gx) * ld + k0 + 4 * c + (f & 3), lds_op + q * 64);
+      }
+    }
+  }
+}
+
+// The partial last k-slab of an NT operand: masked element loads (k >= K -> 0), swizzled float4 LDS stores.
+template <int BX, int BK>
+__device__ __forceinline__ void nt_masked(const float* __restrict__ base, int64_t ld, int x0, int X, int k0, int K,
+                                          float* lds_op) {
+  constexpr int CPR = BK / 4;
+  for (int q = threadIdx.x; q < BX * CPR; q += kThreads) {
+    const int row = q / CPR, c = q % CPR;
+    const float* src = base + static_cast<int64_t>(min(x0 + row, X - 1)) * ld;
+    f32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = k0 + 4 * c + e;
+      v[e] = k < K ? src[k] : 0.0f;
+    }
+    *reinterpret_cast<f32x4*>(lds_op + row * BK + 4 * (c ^ nt_swz<BK>(row))) = v;
+  }
+}
+
+template <int BM, int BN, int BK, bool A16, bool B16, int EPI>
+__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const Group g) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int STAGE = (BM + BN) * BK;
+  static_assert(TM >= 1 && TN >= 1, "tile too small");
+  __shared__ __align__(16) float lds[2 * STAGE];
+
+  const TileCoord tc = locate(g);
+  const Problem& P = g.p[tc.pi];
+  const int row0 = tc.tm * BM, col0 = tc.tn * BN;
+  const int M = P.M, N = P.N, K = P.K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1;
 
   f32x16 acc[TM][TN];
@@ -191,49 +198,48 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const Group g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  Slab<BM, BK, A_KMAJ, A_VEC> sa;
-  Slab<BN, BK, B_KMAJ, B_VEC> sb;
-  const bool do_colsum = (EPI == EPI_PARTIAL) && (P.colsum != nullptr) && (tn == 0);
-  double colsum_acc = 0.0;
-
-  const int nk = k_begin < k_end ? static_cast<int>(ceil_div(k_end - k_begin, BK)) : 0;
-  if (nk > 0) {
-    sa.load(P.A, P.lda, row0, M, k_begin, k_end);
-    sb.load(P.B, P.ldb, col0, N, k_begin, k_end);
-    sa.store(As[0]);
-    sb.store(Bs[0]);
-  }
-  __syncthreads();
+  const int nfull = K / BK;
+  const int nk = (K + BK - 1) / BK;
+  auto issue = [&](int kt, int stage) {
+    float* st = lds + stage * STAGE;
+    const int k0 = kt * BK;
+    if (kt < nfull) {
+      nt_dma<BM, BK, A16>(P.A, P.lda, row0, M, k0, st, wave, lane);
+      nt_dma<BN, BK, B16>(P.B, P.ldb, col0, N, k0, st + BM * BK, wave, lane);
+    } else {
+      nt_masked<BM, BK>(P.A, P.lda, row0, M, k0, K, st);
+      nt_masked<BN, BK>(P.B, P.ldb, col0, N, k0, K, st + BM * BK);
+    }
+  };
+  if (nk > 0) issue(0, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      const int k0 = k_begin + (kt + 1) * BK;
-      sa.load(P.A, P.lda, row0, M, k0, k_end);
-      sb.load(P.B, P.ldb, col0, N, k0, k_end);
+    wait_loads();
+    __syncthreads();  // slab kt is in LDS for every wave; every wave is done with slab kt-1's stage
+    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    const float* As = lds + (kt & 1) * STAGE;
+    const float* Bs = As + BM * BK;
+#pragma unroll
+    for (int gi = 0; gi < BK / 8; ++gi) {
+      const int c = 2 * gi + (lane >> 5);
+      f32x4 fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = wm * WM + 32 * i + (lane & 31);
+        fa[i] = *reinterpret_cast<const f32x4*>(As + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int r = wn * WN + 32 * j + (lane & 31);
+        fb[j] = *reinterpret_cast<const f32x4*>(Bs + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
     }
-    if (do_colsum && tid < BM) {
-#pragma unroll
-      for (int kk = 0; kk < BK; ++kk) colsum_acc += static_cast<double>(As[cur][kk][tid]);
-    }
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      const int k = kk + (lane >> 5);
-      float a[TM], bv[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = As[cur][k][wm * WM + i * 32 + (lane & 31)];
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bv[j] = Bs[cur][k][wn * WN + j * 32 + (lane & 31)];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], bv[j], acc[i][j], 0, 0, 0);
-    }
-    if (more) {
-      sa.store(As[cur ^ 1]);
-      sb.store(Bs[cur ^ 1]);
-    }
-    __syncthreads();
   }
 
   // Epilogue.  MFMA 32x32 output layout: element v of lane l is row 8*(v/4) + 4*(l/32) + v%4, column l%32.
@@ -260,25 +266,178 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const Group g) {
         } else if (EPI == EPI_ELU_GRAD) {
           const float zp = P.aux[rr * P.ldaux + c];
           P.C[rr * P.ldc + c] = zp > 0.0f ? x : x * expf(zp);
-        } else if (EPI == EPI_STORE) {
+        } else {
           P.C[rr * P.ldc + c] = x;
-        } else {  // EPI_PARTIAL
-          P.C[split * P.partial_stride + rr * P.ldc + c] = x;
         }
       }
     }
   }
-  if (do_colsum && tid < BM && row0 + tid < M) P.colsum[static_cast<int64_t>(split) * M + row0 + tid] = colsum_acc;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// TN (weight-grad): operands stored [k][x] (x contiguous); LDS tile [BK][BX], unpadded.
+// ------------------------------------------------------------------------------------------------------------------
+
+// One full k-slab rows [k0, k0 + BK) x [x0, x0 + BX) by direct loads; columns past X read the last in-bounds
+// chunk / element instead (requires ld >= X rounded up to 4 for the 16-byte form).
+template <int BX, int BK, bool W16>
+__device__ __forceinline__ void tn_dma(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
+                                       float* lds_op, int wave, int lane) {
+  if constexpr (W16) {
+    constexpr int NQ = BK * BX / 256;  // instructions of 64 x 16 bytes
+    const int xlast = ((X - 1) >> 2) << 2;
+#pragma unroll
+    for (int q0 = 0; q0 < NQ; q0 += 4) {
+      const int q = q0 + wave;
+      if (NQ % 4 == 0 || q < NQ) {
+        const int flat = 4 * (64 * q + lane);
+        const int row = flat / BX, x = flat % BX;
+        const int gx = min(x0 + x, xlast);
+        dma<16>(base + static_cast<int64_t>(k0 + row) * ld + gx, lds_op + q * 256);
+      }
+    }
+  } else {
+    constexpr int NQ = BK * BX / 64;
+#pragma unroll 4
+    for (int q0 = 0; q0 < NQ; q0 += 4) {
+      const int q = q0 + wave;
+      if (NQ % 4 == 0 || q < NQ) {
+        const int flat = 64 * q + lane;
+        const int row = flat / BX, x = flat % BX;
+        const int gx = min(x0 + x, X - 1);
+        dma<4>(base + static_cast<int64_t>(k0 + row) * ld + gx, lds_op + q * 64);
+      }
+    }
+  }
+}
+
+template <int BX, int BK>
+__device__ __forceinline__ void tn_masked(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
+                                          int k_end, float* lds_op) {
+  for (int q = threadIdx.x; q < BK * BX; q += kThreads) {
+    const int row = q / BX, x = q % BX;
+    const int k = k0 + row;
+    lds_op[q] = k < k_end ? base[static_cast<int64_t>(k) * ld + min(x0 + x, X - 1)] : 0.0f;
+  }
+}
+
+template <int BM, int BN, int BK, bool A16, bool B16>
+__global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const Group g) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int STAGE = BK * (BM + BN);
+  static_assert((TM == 1 || TM == 2) && (TN == 1 || TN == 2), "TN kernel: 1 or 2 MFMA tiles per wave side");
+  __shared__ __align__(16) float lds[2 * STAGE];
+
+  const TileCoord tc = locate(g);
+  const Problem& P = g.p[tc.pi];
+  const int row0 = tc.tm * BM, col0 = tc.tn * BN;
+  const int M = P.M, N = P.N;
+  const int k_begin = tc.split * P.k_chunk;
+  const int k_end = min(P.K, k_begin + P.k_chunk);
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int h = lane >> 5, sg = lane & 31;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const bool do_colsum = P.colsum != nullptr && tc.tn == 0;
+  double colsum_acc = 0.0;
+  const int span = max(k_end - k_begin, 0);
+  const int nfull = span / BK;
+  const int nk = (span + BK - 1) / BK;
+  auto issue = [&](int kt, int stage) {
+    float* st = lds + stage * STAGE;
+    const int k0 = k_begin + kt * BK;
+    if (kt < nfull) {
+      tn_dma<BM, BK, A16>(P.A, P.lda, row0, M, k0, st, wave, lane);
+      tn_dma<BN, BK, B16>(P.B, P.ldb, col0, N, k0, st + BK * BM, wave, lane);
+    } else {
+      tn_masked<BM, BK>(P.A, P.lda, row0, M, k0, k_end, st);
+      tn_masked<BN, BK>(P.B, P.ldb, col0, N, k0, k_end, st + BK * BM);
+    }
+  };
+  if (nk > 0) issue(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_loads();
+    __syncthreads();
+    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    const float* As = lds + (kt & 1) * STAGE;
+    const float* Bs = As + BK * BM;
+    if (do_colsum && tid < BM) {
+#pragma unroll
+      for (int kk = 0; kk < BK; ++kk) colsum_acc += static_cast<double>(As[kk * BM + tid]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 2) {
+      const float* ar = As + (kk + h) * BM + wm * WM;
+      const float* br = Bs + (kk + h) * BN + wn * WN;
+      float fa[TM], fb[TN];
+      if constexpr (TM == 2) {
+        const f32x2 a = *reinterpret_cast<const f32x2*>(ar + 2 * sg);
+        fa[0] = a[0];
+        fa[1] = a[1];
+      } else {
+        fa[0] = ar[sg];
+      }
+      if constexpr (TN == 2) {
+        const f32x2 b = *reinterpret_cast<const f32x2*>(br + 2 * sg);
+        fb[0] = b[0];
+        fb[1] = b[1];
+      } else {
+        fb[0] = br[sg];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Partial store.  Accumulator row rho = 8*(v/4) + 4*h + v%4 of tile i is m = 2*rho + i (TM == 2) or rho, and
+  // column sg of tile j is n = 2*sg + j (TN == 2) or sg.
+  float* Cs = P.C + static_cast<int64_t>(tc.split) * P.partial_stride;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int rho = 8 * (v >> 2) + 4 * h + (v & 3);
+      const int m = row0 + wm * WM + (TM == 2 ? 2 * rho + i : rho);
+      if (m >= M) continue;
+      float* crow = Cs + static_cast<int64_t>(m) * P.ldc;
+      if constexpr (TN == 2) {
+        const int n = col0 + wn * WN + 2 * sg;
+        if (n + 1 < N) {
+          f32x2 o = {acc[i][0][v], acc[i][1][v]};
+          *reinterpret_cast<f32x2*>(crow + n) = o;
+        } else if (n < N) {
+          crow[n] = acc[i][0][v];
+        }
+      } else {
+        const int n = col0 + wn * WN + sg;
+        if (n < N) crow[n] = acc[i][0][v];
+      }
+    }
+  }
+  if (do_colsum && tid < BM && row0 + tid < M) P.colsum[static_cast<int64_t>(tc.split) * M + row0 + tid] = colsum_acc;
 }
 
 // Fixed-order reduction of split-K weight-grad partials: dw = sum_s partial[s], db = sum_s colsum[s].
 struct ReduceItem {
-  const float* partial;  // [splits, out*in]
+  const float* partial;  // [splits, out, ld]
   const double* colsum;  // [splits, out]
   float* dw;
   float* db;
   int64_t begin;         // first flat element of this item in the launch
-  int32_t out, in, splits, pad;
+  int64_t stride;        // floats between splits
+  int32_t out, in, ld, splits;
 };
 struct ReduceGroup {
   ReduceItem it[PPO_MAX_LINEAR_PROBLEMS];
@@ -297,8 +456,10 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
     const int64_t local = e - R.begin;
     const int64_t nw = static_cast<int64_t>(R.out) * R.in;
     if (local < nw) {
+      const int64_t o = local / R.in, i = local - o * R.in;
+      const float* src = R.partial + o * R.ld + i;
       float s = 0.0f;
-      for (int k = 0; k < R.splits; ++k) s += R.partial[k * nw + local];
+      for (int k = 0; k < R.splits; ++k) s += src[k * R.stride];
       R.dw[local] = s;
     } else {
       const int64_t o = local - nw;
@@ -309,47 +470,106 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
   }
 }
 
-template <int BM, int BN, int BK, bool AK, bool BKM, int EPI>
-int launch(Group& g, int count, hipStream_t s, const char* name) {
-  int blocks = 0;
-  bool avec = std::getenv("PPO_HIP_GEMM_SCALAR") == nullptr, bvec = avec;
+// w^T for the input-grad: wt[i, o] = w[o, i], ld of wt = out rounded up to 4.  32 x 32 tiles through LDS.
+struct TransposeItem {
+  const float* w;
+  float* wt;
+  int32_t out, in, ldt, tiles_in, block_begin, pad;
+};
+struct TransposeGroup {
+  TransposeItem it[PPO_MAX_LINEAR_PROBLEMS];
+  int32_t count;
+};
+
+__global__ __launch_bounds__(256) void transpose_kernel(const TransposeGroup g) {
+  __shared__ float tile[32][33];
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < PPO_MAX_LINEAR_PROBLEMS; ++i)
+    if (i < g.count && static_cast<int>(blockIdx.x) >= g.it[i].block_begin) pi = i;
+  const TransposeItem& T = g.it[pi];
+  const int local = blockIdx.x - T.block_begin;
+  const int to = local / T.tiles_in, ti = local % T.tiles_in;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+  for (int r = ty; r < 32; r += 8) {
+    const int o = to * 32 + r, i = ti * 32 + tx;
+    tile[r][tx] = (o < T.out && i < T.in) ? T.w[static_cast<int64_t>(o) * T.in + i] : 0.0f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = ty; r < 32; r += 8) {
+    const int i = ti * 32 + r, o = to * 32 + tx;
+    if (i < T.in && o < T.ldt) T.wt[static_cast<int64_t>(i) * T.ldt + o] = tile[tx][r];
+  }
+}
+
+// 16-byte direct loads need a 16-byte aligned base and a leading dimension that is a multiple of 4.
+bool w16_ok(const float* base, int64_t ld) { return (reinterpret_cast<uintptr_t>(base) % 16 == 0) && ld % 4 == 0; }
+
+int assign_blocks(Group& g, int count, int bm, int bn, const char* name, int& blocks) {
+  blocks = 0;
   for (int i = 0; i < count; ++i) {
     Problem& p = g.p[i];
-    p.tiles_m = static_cast<int>(ceil_div(p.M, BM));
-    p.tiles_n = static_cast<int>(ceil_div(p.N, BN));
+    p.tiles_m = static_cast<int>(ceil_div(p.M, bm));
+    p.tiles_n = static_cast<int>(ceil_div(p.N, bn));
     p.block_begin = blocks;
     const int64_t nb = static_cast<int64_t>(p.tiles_m) * p.tiles_n * p.splits;
     if (blocks + nb > INT32_MAX) return fail(PPO_EUNSUPPORTED, "%s: grid too large", name);
     blocks += static_cast<int>(nb);
-    avec = avec && p.a_vec;
-    bvec = bvec && p.b_vec;
   }
   g.count = count;
   g.xcd_remap = std::getenv("PPO_HIP_NO_XCD_REMAP") == nullptr;
   for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) g.p[i].block_begin = INT32_MAX;
+  return PPO_OK;
+}
+
+template <int BM, int BN, int BK, int EPI>
+int launch_nt(Group& g, int count, hipStream_t s, const char* name) {
+  int blocks;
+  if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
-  // float4 global loads only when every problem of the launch allows them
-  if (avec && bvec) {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (avec) {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, true, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (bvec) {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, false, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  bool a16 = true, b16 = true;
+  for (int i = 0; i < count; ++i) {
+    a16 = a16 && w16_ok(g.p[i].A, g.p[i].lda);
+    b16 = b16 && w16_ok(g.p[i].B, g.p[i].ldb);
+  }
+  if (a16 && b16) {
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else if (a16) {
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, true, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else if (b16) {
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, false, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, BK, AK, BKM, false, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, false, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   }
   return check_launch(name);
 }
 
-// float4 loads along the contiguous dimension need a 16-byte aligned base, a leading dimension that is a multiple
-// of 4, and -- because a partial float4 at the end of a row is read whole and masked -- a leading dimension of at
-// least the contiguous extent rounded up to 4 (the caller's buffer holds rows x ld floats).
-bool vec_ok(const float* base, int64_t ld, int64_t contiguous_extent) {
-  return (reinterpret_cast<uintptr_t>(base) % 16 == 0) && ld % 4 == 0 && ld >= (contiguous_extent + 3) / 4 * 4;
+template <int BM, int BN, int BK>
+int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
+  int blocks;
+  if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
+  if (blocks == 0) return PPO_OK;
+  bool a16 = true, b16 = true;
+  for (int i = 0; i < count; ++i) {
+    a16 = a16 && w16_ok(g.p[i].A, g.p[i].lda);
+    b16 = b16 && w16_ok(g.p[i].B, g.p[i].ldb);
+  }
+  if (a16 && b16) {
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, true, true>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else if (a16) {
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, true, false>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else if (b16) {
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, false, true>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else {
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, false, false>), dim3(blocks), dim3(kThreads), 0, s, g);
+  }
+  return check_launch(name);
 }
 
-// Tile of a launch: "PPO_HIP_GEMM_TILE" (e.g. "128x64k32") overrides the size-based choice (tuning aid).
-enum Tile { T128x128k32, T128x128k16, T128x64k32, T64x64k32, T256x128k16 };
+// NT tile of a launch: "PPO_HIP_GEMM_TILE" (e.g. "128x64k32") overrides the size-based choice (tuning aid).
+enum Tile { T128x128k32, T128x128k16, T128x64k32, T64x64k32, T64x128k32 };
 
 Tile pick_tile(Tile dflt) {
   const char* e = std::getenv("PPO_HIP_GEMM_TILE");
@@ -358,48 +578,29 @@ Tile pick_tile(Tile dflt) {
   if (!std::strcmp(e, "128x128k16")) return T128x128k16;
   if (!std::strcmp(e, "128x64k32")) return T128x64k32;
   if (!std::strcmp(e, "64x64k32")) return T64x64k32;
-  if (!std::strcmp(e, "256x128k16")) return T256x128k16;
+  if (!std::strcmp(e, "64x128k32")) return T64x128k32;
   return dflt;
 }
 
-template <bool AK, bool BKM, int EPI>
-int launch_tile(Tile t, Group& g, int count, hipStream_t s, const char* name) {
+template <int EPI>
+int launch_nt_tile(Tile t, Group& g, int count, hipStream_t s, const char* name) {
   switch (t) {
     case T128x128k16:
-      return launch<128, 128, 16, AK, BKM, EPI>(g, count, s, name);
+      return launch_nt<128, 128, 16, EPI>(g, count, s, name);
     case T128x64k32:
-      return launch<128, 64, 32, AK, BKM, EPI>(g, count, s, name);
+      return launch_nt<128, 64, 32, EPI>(g, count, s, name);
     case T64x64k32:
-      return launch<64, 64, 32, AK, BKM, EPI>(g, count, s, name);
-    case T256x128k16:
-      return launch<256, 128, 16, AK, BKM, EPI>(g, count, s, name);
+      return launch_nt<64, 64, 32, EPI>(g, count, s, name);
+    case T64x128k32:
+      return launch_nt<64, 128, 32, EPI>(g, count, s, name);
     default:
-      return launch<128, 128, 32, AK, BKM, EPI>(g, count, s, name);
+      return launch_nt<128, 128, 32, EPI>(g, count, s, name);
   }
 }
 
-// Split-K policy for the weight-grad: enough blocks to cover the chip (~4 per CU), slabs of at least 256 rows.
-// Tile: "PPO_HIP_DW_TILE" overrides the default 128x128k32 (tuning aid).
-constexpr int kDwBK = 32;  // split-K chunks are multiples of the largest BK
-
-Tile dw_tile() {
-  const char* e = std::getenv("PPO_HIP_DW_TILE");
-  if (e == nullptr) return T128x128k16;
-  if (!std::strcmp(e, "128x128k32")) return T128x128k32;
-  if (!std::strcmp(e, "128x64k32")) return T128x64k32;
-  if (!std::strcmp(e, "64x64k32")) return T64x64k32;
-  if (!std::strcmp(e, "256x128k16")) return T256x128k16;
-  return T128x128k16;
-}
-
-void tile_dims(Tile t, int& bm, int& bn) {
-  switch (t) {
-    case T128x64k32: bm = 128; bn = 64; break;
-    case T64x64k32: bm = 64; bn = 64; break;
-    case T256x128k16: bm = 256; bn = 128; break;
-    default: bm = 128; bn = 128; break;
-  }
-}
+// Weight-grad: 128 x 128 tiles; split-K over the rows so that the launch covers the chip (~4 blocks per CU), in
+// chunks that are multiples of the 32-row slab.  "PPO_HIP_DW_BK" = 16 selects 16-row slabs (tuning aid).
+constexpr int kDwBM = 128, kDwBN = 128, kDwChunk = 32;
 
 int dw_splits(int64_t tiles, int64_t rows) {
   const int64_t target = 1024;
@@ -408,6 +609,8 @@ int dw_splits(int64_t tiles, int64_t rows) {
   s = std::max<int64_t>(1, std::min<int64_t>(s, 256));
   return static_cast<int>(s);
 }
+
+int64_t round4(int64_t n) { return (n + 3) / 4 * 4; }
 
 struct DwPlan {
   int splits[PPO_MAX_LINEAR_PROBLEMS];
@@ -419,20 +622,18 @@ struct DwPlan {
 
 DwPlan plan_dw(const ppo_linear_bwd_dw_problem* probs, int count, int64_t rows) {
   DwPlan plan{};
-  int bm, bn;
-  tile_dims(dw_tile(), bm, bn);
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i)
-    tiles += ceil_div(probs[i].out_features, bm) * ceil_div(probs[i].in_features, bn);
+    tiles += ceil_div(probs[i].out_features, kDwBM) * ceil_div(probs[i].in_features, kDwBN);
   const int s = dw_splits(tiles, rows);
   size_t off = 0;
   for (int i = 0; i < count; ++i) {
-    const int64_t chunk = ceil_div(ceil_div(rows, s), kDwBK) * kDwBK;
+    const int64_t chunk = ceil_div(ceil_div(rows, s), kDwChunk) * kDwChunk;
     const int splits = static_cast<int>(ceil_div(rows, chunk));
     plan.splits[i] = splits;
     plan.k_chunk[i] = static_cast<int>(chunk);
     plan.partial_off[i] = off;
-    off += static_cast<size_t>(splits) * probs[i].out_features * probs[i].in_features;
+    off += static_cast<size_t>(splits) * probs[i].out_features * round4(probs[i].in_features);
     off = (off + 63) & ~static_cast<size_t>(63);
     plan.colsum_off[i] = off;
     off += 2 * static_cast<size_t>(splits) * probs[i].out_features;
@@ -440,6 +641,17 @@ DwPlan plan_dw(const ppo_linear_bwd_dw_problem* probs, int count, int64_t rows) 
   }
   plan.total_floats = off;
   return plan;
+}
+
+// Input-grad workspace: one w^T per problem, [in, round4(out)], 256-byte aligned.
+size_t dx_plan(const ppo_linear_bwd_dx_problem* probs, int count, size_t* offs) {
+  size_t off = 0;
+  for (int i = 0; i < count; ++i) {
+    if (offs) offs[i] = off;
+    off += static_cast<size_t>(probs[i].in_features) * round4(probs[i].out_features);
+    off = (off + 63) & ~static_cast<size_t>(63);
+  }
+  return off;
 }
 
 bool rows_ok(int64_t rows) { return rows > 0 && rows <= INT32_MAX / 2; }
@@ -472,26 +684,29 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
     p.vec = q.b;
     p.M = static_cast<int>(rows); p.N = q.out_features; p.K = q.in_features;
     p.splits = 1; p.k_chunk = q.in_features;
-    p.a_vec = vec_ok(q.x, q.ldx, q.in_features);
-    p.b_vec = vec_ok(q.w, q.in_features, q.in_features);
     max_n = std::max(max_n, q.out_features);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // measured on MI355X for 24576-row mini-batches: wide outputs like 128x128 tiles, 128..256-wide outputs 128x64,
-  // narrow output layers 64x64
-  const Tile t = pick_tile(max_n > 256 ? T128x128k16 : (max_n > 64 ? T128x64k32 : T64x64k32));
-  if (activation == PPO_ACT_ELU) return launch_tile<true, true, EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_elu");
-  return launch_tile<true, true, EPI_BIAS>(t, g, count, s, "linear_fwd");
+  // measured on MI355X for 24576-row mini-batches: outputs wider than 128 like 128x128 tiles with 16-deep slabs,
+  // narrower ones 128x64
+  const Tile t = pick_tile(max_n > 128 ? T128x128k16 : T128x64k32);
+  if (activation == PPO_ACT_ELU) return launch_nt_tile<EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_elu");
+  return launch_nt_tile<EPI_BIAS>(t, g, count, s, "linear_fwd");
+}
+
+extern "C" size_t ppo_linear_bwd_dx_workspace_bytes(const ppo_linear_bwd_dx_problem* problems, int32_t count) {
+  if (problems == nullptr || count < 1 || count > PPO_MAX_LINEAR_PROBLEMS) return 0;
+  for (int i = 0; i < count; ++i)
+    if (problems[i].in_features <= 0 || problems[i].out_features <= 0) return 0;
+  return dx_plan(problems, count, nullptr) * sizeof(float);
 }
 
 extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
-                                 ppo_stream_t stream) {
+                                 void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS,
               "ppo_linear_bwd_dx: count=%d outside [1, %d]", count, PPO_MAX_LINEAR_PROBLEMS);
   PPO_REQUIRE(rows_ok(rows), "ppo_linear_bwd_dx: rows=%lld", (long long)rows);
-  Group g{};
   bool any_act = false, any_plain = false;
-  int max_n = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_linear_bwd_dx_problem& q = problems[i];
     PPO_REQUIRE(q.dz && q.w && q.dz_prev, "ppo_linear_bwd_dx: problem %d has a null pointer", i);
@@ -500,23 +715,45 @@ extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int3
                     (q.z_prev == nullptr || q.ldz_prev >= q.in_features),
                 "ppo_linear_bwd_dx: problem %d leading dims", i);
     (q.z_prev ? any_act : any_plain) = true;
+  }
+  PPO_REQUIRE(!(any_act && any_plain), "ppo_linear_bwd_dx: mix of activation and plain problems in one call");
+  size_t offs[PPO_MAX_LINEAR_PROBLEMS];
+  const size_t need = dx_plan(problems, count, offs) * sizeof(float);
+  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_linear_bwd_dx: workspace too small (%zu < %zu)",
+              workspace_bytes, need);
+  PPO_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "ppo_linear_bwd_dx: workspace must be 16-byte aligned");
+  float* ws = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  TransposeGroup tg{};
+  Group g{};
+  int tblocks = 0, max_n = 0;
+  for (int i = 0; i < count; ++i) {
+    const ppo_linear_bwd_dx_problem& q = problems[i];
+    float* wt = ws + offs[i];
+    TransposeItem& T = tg.it[i];
+    T.w = q.w; T.wt = wt; T.out = q.out_features; T.in = q.in_features;
+    T.ldt = static_cast<int>(round4(q.out_features));
+    T.tiles_in = static_cast<int>(ceil_div(q.in_features, 32));
+    T.block_begin = tblocks;
+    tblocks += static_cast<int>(ceil_div(T.ldt, 32)) * T.tiles_in;
     Problem& p = g.p[i];
     p.A = q.dz; p.lda = q.lddz;
-    p.B = q.w; p.ldb = q.in_features;
+    p.B = wt; p.ldb = T.ldt;
     p.C = q.dz_prev; p.ldc = q.lddz_prev;
     p.aux = q.z_prev; p.ldaux = q.ldz_prev;
     p.M = static_cast<int>(rows); p.N = q.in_features; p.K = q.out_features;
     p.splits = 1; p.k_chunk = q.out_features;
-    p.a_vec = vec_ok(q.dz, q.lddz, q.out_features);
-    p.b_vec = vec_ok(q.w, q.in_features, q.in_features);
     max_n = std::max(max_n, q.in_features);
   }
-  PPO_REQUIRE(!(any_act && any_plain), "ppo_linear_bwd_dx: mix of activation and plain problems in one call");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  // measured on MI355X: 64x64 tiles for every input-grad shape of the [512, 256, 128] MLPs
-  const Tile t = pick_tile(T64x64k32);
-  if (any_act) return launch_tile<true, false, EPI_ELU_GRAD>(t, g, count, s, "linear_bwd_dx_elu");
-  return launch_tile<true, false, EPI_STORE>(t, g, count, s, "linear_bwd_dx");
+  for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) tg.it[i].block_begin = INT32_MAX;
+  tg.count = count;
+  hipLaunchKernelGGL(transpose_kernel, dim3(tblocks), dim3(256), 0, s, tg);
+  if (int rc = check_launch("transpose_kernel")) return rc;
+  // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
+  const Tile t = pick_tile(max_n > 128 ? T64x64k32 : T128x64k32);
+  if (any_act) return launch_nt_tile<EPI_ELU_GRAD>(t, g, count, s, "linear_bwd_dx_elu");
+  return launch_nt_tile<EPI_STORE>(t, g, count, s, "linear_bwd_dx");
 }
 
 extern "C" size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_problem* problems, int32_t count,
@@ -550,18 +787,18 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   for (int i = 0; i < count; ++i) {
     const ppo_linear_bwd_dw_problem& q = problems[i];
     Problem& p = g.p[i];
+    const int64_t ldp = round4(q.in_features);
     p.A = q.dz; p.lda = q.lddz;
     p.B = q.x; p.ldb = q.ldx;
-    p.C = ws + plan.partial_off[i]; p.ldc = q.in_features;
-    p.partial_stride = static_cast<int64_t>(q.out_features) * q.in_features;
+    p.C = ws + plan.partial_off[i]; p.ldc = ldp;
+    p.partial_stride = static_cast<int64_t>(q.out_features) * ldp;
     p.colsum = reinterpret_cast<double*>(ws + plan.colsum_off[i]);
     p.M = q.out_features; p.N = q.in_features; p.K = static_cast<int>(rows);
     p.splits = plan.splits[i]; p.k_chunk = plan.k_chunk[i];
-    p.a_vec = vec_ok(q.dz, q.lddz, q.out_features);
-    p.b_vec = vec_ok(q.x, q.ldx, q.in_features);
     ReduceItem& r = rg.it[i];
     r.partial = p.C; r.colsum = p.colsum; r.dw = q.dw; r.db = q.db;
-    r.out = q.out_features; r.in = q.in_features; r.splits = plan.splits[i];
+    r.out = q.out_features; r.in = q.in_features; r.ld = static_cast<int>(ldp); r.splits = plan.splits[i];
+    r.stride = p.partial_stride;
     r.begin = total;
     total += static_cast<int64_t>(q.out_features) * q.in_features + q.out_features;
   }
@@ -569,7 +806,9 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   rg.count = count;
   rg.total = total;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = launch_tile<false, false, EPI_PARTIAL>(dw_tile(), g, count, s, "linear_bwd_dw");
+  const char* bk = std::getenv("PPO_HIP_DW_BK");
+  int rc = (bk && !std::strcmp(bk, "16")) ? launch_tn<kDwBM, kDwBN, 16>(g, count, s, "linear_bwd_dw")
+                                          : launch_tn<kDwBM, kDwBN, 32>(g, count, s, "linear_bwd_dw");
   if (rc != PPO_OK) return rc;
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 4096);
   hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);

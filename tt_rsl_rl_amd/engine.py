@@ -58,19 +58,20 @@ class ModelBuffers:
 class PhaseTimer:
     """Optional instrumentation: HIP events (torch.cuda.Event on the launch stream) around named launches."""
 
-    def __init__(self) -> None:
+    def __init__(self, only: set[str] | None = None) -> None:
         self.events: dict[str, list[tuple[torch.cuda.Event, torch.cuda.Event]]] = {}
         self._open: dict[str, torch.cuda.Event] = {}
         self.enabled = True
+        self.only = only  # None: every phase; else only these names get events
 
     def start(self, name: str) -> None:
-        if self.enabled:
+        if self.enabled and (self.only is None or name in self.only):
             e = torch.cuda.Event(enable_timing=True)
             e.record()
             self._open[name] = e
 
     def stop(self, name: str) -> None:
-        if self.enabled:
+        if name in self._open:
             e = torch.cuda.Event(enable_timing=True)
             e.record()
             self.events.setdefault(name, []).append((self._open.pop(name), e))
@@ -114,6 +115,7 @@ class UpdateEngine:
         self.loss_ws = torch.empty(ops.loss_workspace_bytes(self.R_max, self.A), dtype=torch.uint8, device=self.device)
         self.dw_ws = ops.Workspace(self.device)
         self.adam_ws = ops.Workspace(self.device)
+        self.dx_ws = ops.Workspace(self.device)
         self.adv_ws = ops.Workspace(self.device)
         self.trace = torch.zeros(5 * alg.num_learning_epochs * self.M, dtype=torch.float64, device=self.device)
 
@@ -194,7 +196,7 @@ class UpdateEngine:
         for i in range(nl - 1, 0, -1):
             tm.start(f"dx{i}")
             ops.linear_bwd_dx([(ba.dz[i][:R], la[i].weight, ba.z[i - 1][:R], ba.dz[i - 1][:R]),
-                               (bc.dz[i][:R], lc[i].weight, bc.z[i - 1][:R], bc.dz[i - 1][:R])], R)
+                               (bc.dz[i][:R], lc[i].weight, bc.z[i - 1][:R], bc.dz[i - 1][:R])], R, self.dx_ws)
             tm.stop(f"dx{i}")
         dw = []
         for model, buf, lins, x0 in ((actor, ba, la, xa), (critic, bc, lc, xc)):

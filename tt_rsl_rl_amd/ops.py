@@ -167,7 +167,7 @@ def linear_fwd(problems: list[tuple], rows: int, elu: bool) -> None:
            L.PPO_ACT_ELU if elu else L.PPO_ACT_NONE, _stream())
 
 
-def linear_bwd_dx(problems: list[tuple], rows: int) -> None:
+def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:
     """problems: (dz [rows, out], w [out, in], z_prev [rows, in] or None, dz_prev [rows, in])."""
     items = []
     for dz, w, z_prev, dz_prev in problems:
@@ -181,7 +181,12 @@ def linear_bwd_dx(problems: list[tuple], rows: int) -> None:
             raise ValueError("linear_bwd_dx: z_prev too small")
         items.append(L.LinearBwdDxProblem(dz.data_ptr(), lddz, w.data_ptr(), _ptr(z_prev), ldzp, dz_prev.data_ptr(),
                                           ldo, in_f, out_f))
-    L.call("ppo_linear_bwd_dx", L.array(L.LinearBwdDxProblem, items), len(items), rows, _stream())
+    arr = L.array(L.LinearBwdDxProblem, items)
+    nbytes = L.load().ppo_linear_bwd_dx_workspace_bytes(arr, len(items))
+    if nbytes == 0:
+        raise ValueError("linear_bwd_dx: invalid problem set")
+    buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
+    L.call("ppo_linear_bwd_dx", arr, len(items), rows, buf.data_ptr(), buf.numel(), _stream())
 
 
 def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:
