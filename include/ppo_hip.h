@@ -30,6 +30,8 @@ enum {
 };
 
 enum { PPO_ACT_NONE = 0, PPO_ACT_ELU = 1 };
+/* what ppo_linear_bwd_dx's z_prev holds: the ELU input (pre-activation) or its output h = elu(z) */
+enum { PPO_ELU_FROM_INPUT = 0, PPO_ELU_FROM_OUTPUT = 1 };
 enum { PPO_STD_SCALAR = 0, PPO_STD_LOG = 1 };
 
 /* Description of the last failure on the calling thread ("" if none). */
@@ -92,7 +94,8 @@ int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_rows, const p
 #define PPO_MAX_LINEAR_PROBLEMS 8
 
 /* forward: z = x w^T + b; with PPO_ACT_ELU also h = elu(z) (alpha 1).  Replaces nn.Linear.forward / nn.ELU.forward.
- * z (pre-activation) is kept for the backward; h may be NULL with PPO_ACT_NONE. */
+ * With PPO_ACT_ELU either output may be NULL (not both): a backward that takes ELU' from h
+ * (PPO_ELU_FROM_OUTPUT) needs only h.  With PPO_ACT_NONE z is required and h is ignored. */
 typedef struct ppo_linear_fwd_problem {
   const float* x; int64_t ldx; /* [rows, in] */
   const float* w;              /* [out, in] */
@@ -107,7 +110,9 @@ int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t count, int64_
                    ppo_stream_t stream);
 
 /* backward to the layer input: dz_prev = (dz w) * act'(z_prev), act' of ELU = 1 if z > 0 else exp(z)
- * (torch's elu_backward on the input).  z_prev == NULL means no activation (plain dx = dz w).
+ * (torch's elu_backward on the input).  z_prev == NULL means no activation (plain dx = dz w).  With
+ * elu_source = PPO_ELU_FROM_OUTPUT, z_prev holds h = elu(z) instead and act' = 1 if h > 0 else h + 1 (the same
+ * derivative, exp(z) = expm1(z) + 1, evaluated from the forward's output so z need not be stored).
  * The workspace (ppo_linear_bwd_dx_workspace_bytes, 16-byte aligned) receives w^T of every problem.
  * Replaces autograd's mm backward + EluBackward (rsl_rl/algorithms/ppo.py:298). */
 typedef struct ppo_linear_bwd_dx_problem {
@@ -120,8 +125,8 @@ typedef struct ppo_linear_bwd_dx_problem {
 } ppo_linear_bwd_dx_problem;
 
 size_t ppo_linear_bwd_dx_workspace_bytes(const ppo_linear_bwd_dx_problem* problems, int32_t count);
-int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, void* workspace,
-                      size_t workspace_bytes, ppo_stream_t stream);
+int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t elu_source,
+                      void* workspace, size_t workspace_bytes, ppo_stream_t stream);
 
 /* backward to the parameters: dw = dz^T x, db = sum_rows dz, reduced over rows in fixed-order split-K partials
  * (deterministic: no float atomics).  Replaces autograd's AddmmBackward for weight and bias. */

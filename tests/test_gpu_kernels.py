@@ -123,19 +123,38 @@ def test_linear_fwd_grouped(cuda, rows):
         assert rel_err(h, _elu64(z64)) < 2e-6
 
 
-@pytest.mark.parametrize("rows,fin,fout,act", [(24576, 512, 256, True), (1000, 128, 29, True), (333, 256, 1, False)])
-def test_linear_bwd_dx(cuda, rows, fin, fout, act):
+@pytest.mark.parametrize("rows,fin,fout,act,from_output", [(24576, 512, 256, True, False), (1000, 128, 29, True, False),
+                                                         (333, 256, 1, False, False), (24576, 512, 256, True, True),
+                                                         (77, 99, 5, True, True)])
+def test_linear_bwd_dx(cuda, rows, fin, fout, act, from_output):
+    """ELU' from the input z (torch's elu_backward) or from the output h = elu(z): the same derivative."""
     ops = _ops()
     torch.manual_seed(fin + fout)
     dz = torch.randn(rows, fout)
     w = torch.randn(fout, fin) / math.sqrt(fout)
-    zp = torch.randn(rows, fin) if act else None
+    zp = torch.randn(rows, fin) * 2 if act else None
+    src = None
+    if act:
+        src = torch.where(zp > 0, zp, torch.expm1(zp)) if from_output else zp
     out = torch.empty(rows, fin, device=cuda)
-    ops.linear_bwd_dx([(dz.to(cuda), w.to(cuda), None if zp is None else zp.to(cuda), out)], rows)
+    ops.linear_bwd_dx([(dz.to(cuda), w.to(cuda), None if src is None else src.to(cuda), out)], rows,
+                      elu_from_output=from_output)
     ref = dz.double() @ w.double()
     if act:
         ref = ref * torch.where(zp.double() > 0, torch.ones_like(ref), torch.exp(zp.double()))
     assert rel_err(out, ref) < 2e-6
+
+
+def test_linear_fwd_h_only(cuda):
+    """With ELU the pre-activation output may be omitted: h alone is written, z's buffer is untouched."""
+    ops = _ops()
+    torch.manual_seed(5)
+    rows, fin, fout = 1000, 96, 512
+    x, w, b = torch.randn(rows, fin), torch.randn(fout, fin) / math.sqrt(fin), torch.randn(fout)
+    h = torch.empty(rows, fout, device=cuda)
+    ops.linear_fwd([(x.to(cuda), w.to(cuda), b.to(cuda), None, h)], rows, elu=True)
+    z64 = x.double() @ w.double().t() + b.double()
+    assert rel_err(h, _elu64(z64)) < 2e-6
 
 
 @pytest.mark.parametrize("rows", [24576, 1000, 5])

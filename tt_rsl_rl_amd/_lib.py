@@ -20,6 +20,8 @@ PPO_EHIP = -2
 PPO_EUNSUPPORTED = -3
 PPO_ACT_NONE = 0
 PPO_ACT_ELU = 1
+PPO_ELU_FROM_INPUT = 0
+PPO_ELU_FROM_OUTPUT = 1
 PPO_STD_SCALAR = 0
 PPO_STD_LOG = 1
 MAX_GATHER_SEGMENTS = 16
@@ -91,7 +93,8 @@ _SIGNATURES = [
     ("ppo_gather_rows", C.c_int, [C.c_void_p, i64, i64, C.POINTER(GatherSegment), i32, f32p, i64, C.c_void_p]),
     ("ppo_linear_fwd", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, C.c_void_p]),
     ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),
-    ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, C.c_void_p, C.c_size_t,
+                                    C.c_void_p]),
     ("ppo_linear_bwd_dw_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDwProblem), i32, i64]),
     ("ppo_linear_bwd_dw", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("ppo_obs_normalize", C.c_int, [f32p, i64, f32p, i64, i64, i32, f32p, f32p, C.c_float, C.c_void_p]),
@@ -111,7 +114,7 @@ _SIGNATURES = [
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib: C.CDLL | None = None
 

@@ -48,6 +48,8 @@ struct Problem {
   int32_t M, N, K;
   int32_t tiles_m, tiles_n, splits, k_chunk;
   int32_t block_begin;
+  int32_t c_vec;            // NT epilogue: C (and C2 / aux when used) allow 16-byte accesses
+  int32_t elu_from_output;  // input-grad: aux holds h = elu(z) (ELU' = 1 if h > 0 else h + 1), else z
 };
 
 struct Group {
@@ -102,9 +104,38 @@ __device__ __forceinline__ void dma(const float* src, float* lds_wave) {
   }
 }
 
-// Waits for this wave's outstanding global loads (including the LDS-direct ones, which the compiler does not
-// track as LDS writes: hence the memory clobber).
-__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Waits until at most N of this wave's vector-memory operations are outstanding.  The LDS-direct loads count here
+// (and are not tracked by the compiler as LDS writes: hence the memory clobber).  Loads complete in issue order.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");
+}
+
+// Workgroup barrier of the LDS ring: this wave's LDS writes are complete and the compiler moves no memory access
+// across it.  Unlike __syncthreads(), whose workgroup release fence also drains every outstanding global load, it
+// leaves the prefetched slabs in flight; their arrival is awaited explicitly with wait_slab().
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Ring of S LDS stages with prefetch distance S - 1: before computing slab kt a wave waits for its own loads of
+// slab kt while the `later` (<= S - 2) slabs issued after it may stay in flight; L = loads per wave per slab.
+// A cap of 63 outstanding only makes the wait stricter (loads retire in order).
+template <int L, int S>
+__device__ __forceinline__ void wait_slab(int later) {
+  if constexpr (S >= 4) {
+    if (later >= 2) {
+      wait_vmcnt<2 * L>();
+      return;
+    }
+  }
+  if constexpr (S >= 3) {
+    if (later >= 1) {
+      wait_vmcnt<L>();
+      return;
+    }
+  }
+  wait_vmcnt<0>();
+}
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -122,40 +153,47 @@ __device__ __forceinline__ int nt_swz(int row) {
   return CPR == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 
-// One full k-slab [x0, x0 + BX) x [k0, k0 + BK) of an NT operand into LDS by direct loads (rows >= X clamped).
+// Direct loads of one NT operand: one full k-slab [x0, x0 + BX) x [k0, k0 + BK) per call, rows >= X clamped to X - 1.
+// Each lane's byte offsets from the slab's first column are fixed for the whole k loop, so a slab costs one
+// uniform (scalar) base pointer and one global_load_lds per instruction.  Wave w issues instructions w, w+4, ...
 template <int BX, int BK, bool W16>
-__device__ __forceinline__ void nt_dma(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
-                                       float* lds_op, int wave, int lane) {
-  constexpr int CPR = BK / 4;
-  if constexpr (W16) {
-    constexpr int RPI = 64 / CPR;  // rows per instruction (64 chunks of 16 bytes)
-    constexpr int NQ = BX / RPI;
+struct NtLoader {
+  static constexpr int CPR = BK / 4;
+  static constexpr int NQ = W16 ? BX * BK / 256 : BX * BK / 64;
+  static constexpr int PER = NQ / 4;
+  static_assert(NQ % 4 == 0, "every wave must issue the same number of loads per slab");
+  uint32_t off[PER];
+
+  __device__ __forceinline__ void init(int64_t ld, int x0, int X, int wave, int lane) {
 #pragma unroll
-    for (int q0 = 0; q0 < NQ; q0 += 4) {
-      const int q = q0 + wave;
-      if (NQ % 4 == 0 || q < NQ) {
-        const int row = q * RPI + lane / CPR;
-        const int c = (lane % CPR) ^ nt_swz<BK>(row);
-        const int gx = min(x0 + row, X - 1);
-        dma<16>(base + static_cast<int64_t>(gx) * ld + k0 + 4 * c, lds_op + q * 256);
-      }
-    }
-  } else {
-    constexpr int RPI = 64 / BK;  // rows per instruction (64 floats)
-    constexpr int NQ = BX / RPI;
-#pragma unroll
-    for (int q0 = 0; q0 < NQ; q0 += 4) {
-      const int q = q0 + wave;
-      if (NQ % 4 == 0 || q < NQ) {
-        const int row = q * RPI + lane / BK;
+    for (int j = 0; j < PER; ++j) {
+      const int q = 4 * j + wave;
+      int row, col;
+      if constexpr (W16) {
+        row = q * (64 / CPR) + lane / CPR;
+        col = 4 * ((lane % CPR) ^ nt_swz<BK>(row));
+      } else {
+        row = q * (64 / BK) + lane / BK;
         const int f = lane % BK;
-        const int c = (f >> 2) ^ nt_swz<BK>(row);
-        const int gx = min(x0 + row, X - 1);
-        dma<4>(base + static_cast<int64_t>(gx) * ld + k0 + 4 * c + (f & 3), lds_op + q * 64);
+        col = 4 * ((f >> 2) ^ nt_swz<BK>(row)) + (f & 3);
+      }
+      const int64_t gx = min(x0 + row, X - 1);
+      off[j] = static_cast<uint32_t>((gx * ld + col) * 4);
+    }
+  }
+  // base: the operand's element (0, k0), wave-uniform.
+  __device__ __forceinline__ void issue(const float* base, float* lds_op, int wave) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float* src = reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off[j]);
+      if constexpr (W16) {
+        dma<16>(src, lds_op + (4 * j + wave) * 256);
+      } else {
+        dma<4>(src, lds_op + (4 * j + wave) * 64);
       }
     }
   }
-}
+};
 
 // The partial last k-slab of an NT operand: masked element loads (k >= K -> 0), swizzled float4 LDS stores.
 template <int BX, int BK>
@@ -175,16 +213,24 @@ __device__ __forceinline__ void nt_masked(const float* __restrict__ base, int64_
   }
 }
 
-template <int BM, int BN, int BK, bool A16, bool B16, int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const Group g) {
+// OCC: waves per SIMD the register allocation must allow (blocks of 4 waves per CU), traded against spills.
+template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16, int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_kernel(
+    const Group g) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = (BM + BN) * BK;
   static_assert(TM >= 1 && TN >= 1, "tile too small");
-  __shared__ __align__(16) float lds[2 * STAGE];
+  static_assert(S >= 2 && S <= 4, "2..4 LDS stages");
+  constexpr int L = NtLoader<BM, BK, A16>::PER + NtLoader<BN, BK, B16>::PER;
+  __shared__ __align__(16) float lds[S * STAGE];
 
   const TileCoord tc = locate(g);
   const Problem& P = g.p[tc.pi];
+  // problem fields as values: the loop's compiler barriers would otherwise re-read them from the argument block
+  const float* const A = P.A;
+  const float* const B = P.B;
+  const int64_t lda = P.lda, ldb = P.ldb;
   const int row0 = tc.tm * BM, col0 = tc.tn * BN;
   const int M = P.M, N = P.N, K = P.K;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -198,25 +244,31 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const Group g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  NtLoader<BM, BK, A16> la;
+  NtLoader<BN, BK, B16> lb;
+  la.init(lda, row0, M, wave, lane);
+  lb.init(ldb, col0, N, wave, lane);
   const int nfull = K / BK;
   const int nk = (K + BK - 1) / BK;
   auto issue = [&](int kt, int stage) {
     float* st = lds + stage * STAGE;
     const int k0 = kt * BK;
     if (kt < nfull) {
-      nt_dma<BM, BK, A16>(P.A, P.lda, row0, M, k0, st, wave, lane);
-      nt_dma<BN, BK, B16>(P.B, P.ldb, col0, N, k0, st + BM * BK, wave, lane);
+      la.issue(A + k0, st, wave);
+      lb.issue(B + k0, st + BM * BK, wave);
     } else {
-      nt_masked<BM, BK>(P.A, P.lda, row0, M, k0, K, st);
-      nt_masked<BN, BK>(P.B, P.ldb, col0, N, k0, K, st + BM * BK);
+      nt_masked<BM, BK>(A, lda, row0, M, k0, K, st);
+      nt_masked<BN, BK>(B, ldb, col0, N, k0, K, st + BM * BK);
     }
   };
-  if (nk > 0) issue(0, 0);
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s, s);
   for (int kt = 0; kt < nk; ++kt) {
-    wait_loads();
-    __syncthreads();  // slab kt is in LDS for every wave; every wave is done with slab kt-1's stage
-    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
-    const float* As = lds + (kt & 1) * STAGE;
+    wait_slab<L, S>(min(S - 2, nk - 1 - kt));
+    lds_barrier();  // slab kt is in LDS for every wave; every wave is done with slab kt-1's stage
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    const float* As = lds + (kt % S) * STAGE;
     const float* Bs = As + BM * BK;
 #pragma unroll
     for (int gi = 0; gi < BK / 8; ++gi) {
@@ -238,36 +290,85 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const Group g) {
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+            // weights (B) as the MFMA's A operand: the accumulator holds the 32 x 32 tile of C transposed
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[j][s], fa[i][s], acc[i][j], 0, 0, 0);
     }
   }
 
-  // Epilogue.  MFMA 32x32 output layout: element v of lane l is row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+  // Epilogue, one 32 x 32 accumulator tile at a time through a private 32 x 36-float LDS patch per wave (the ring is
+  // free once every wave is past its last slab).  Element v of lane l of acc[i][j] is row l%32 and column
+  // 8*(v/4) + 4*(l/32) + v%4 of the tile, so a lane writes 4 float4 runs into the patch; it then reads back 16-byte
+  // chunks in row order (8 lanes per 128-byte row) and finishes them there: +bias / ELU, or * ELU'(z_prev), with
+  // every global access a fully used 128-byte row segment (16-byte vectors when P.c_vec, elements at the N edge).
+  static_assert(4 * 32 * 36 <= S * STAGE, "epilogue patches must fit in the LDS ring");
+  constexpr int PS = 36;  // patch row stride: 144 bytes spreads the 16 rows of a ds_write_b128 over all banks
+  lds_barrier();
+  float* patch = lds + wave * 32 * PS;
+  const int h = lane >> 5;
+  const int pr = lane >> 3, pc = 4 * (lane & 7);  // read-back: row pr (+8 per step), columns pc .. pc + 3
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int c = col0 + wn * WN + j * 32 + (lane & 31);
-      if (c >= N) continue;
-      float bias = 0.0f;
-      if (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) bias = P.vec[c];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = row0 + wm * WM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (r >= M) continue;
-        const float x = acc[i][j][v];
-        const int64_t rr = r;
-        if (EPI == EPI_BIAS) {
-          P.C[rr * P.ldc + c] = x + bias;
-        } else if (EPI == EPI_BIAS_ELU) {
-          const float z = x + bias;
-          P.C[rr * P.ldc + c] = z;
-          P.C2[rr * P.ldc2 + c] = z > 0.0f ? z : expm1f(z);
+      for (int q = 0; q < 4; ++q) {
+        f32x4 x = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        *reinterpret_cast<f32x4*>(patch + (lane & 31) * PS + 8 * q + 4 * h) = x;
+      }
+      const int n = col0 + wn * WN + j * 32 + pc;
+      const bool n_in = n < N;
+      const bool full = P.c_vec && n + 3 < N;
+      f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
+      if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && n_in) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bias[e] = n + e < N ? P.vec[n + e] : 0.0f;
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int r = pr + 8 * rr;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(patch + r * PS + pc);
+        const int m = row0 + wm * WM + i * 32 + r;
+        if (m >= M || !n_in) continue;
+        const int64_t mm = m;
+        f32x4 o, o2;
+        if (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = x[e] + bias[e];
+            o2[e] = o[e] > 0.0f ? o[e] : expm1f(o[e]);
+          }
         } else if (EPI == EPI_ELU_GRAD) {
-          const float zp = P.aux[rr * P.ldaux + c];
-          P.C[rr * P.ldc + c] = zp > 0.0f ? x : x * expf(zp);
+          f32x4 zp;
+          if (full) {
+            zp = *reinterpret_cast<const f32x4*>(P.aux + mm * P.ldaux + n);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) zp[e] = n + e < N ? P.aux[mm * P.ldaux + n + e] : 0.0f;
+          }
+          if (P.elu_from_output) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * (zp[e] + 1.0f);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * expf(zp[e]);
+          }
         } else {
-          P.C[rr * P.ldc + c] = x;
+          o = x;
+        }
+        // with ELU either output may be absent (h alone feeds the next layer and the input-grad)
+        const bool st_c = EPI != EPI_BIAS_ELU || P.C != nullptr;
+        const bool st_c2 = EPI == EPI_BIAS_ELU && P.C2 != nullptr;
+        if (full) {
+          if (st_c) *reinterpret_cast<f32x4*>(P.C + mm * P.ldc + n) = o;
+          if (st_c2) *reinterpret_cast<f32x4*>(P.C2 + mm * P.ldc2 + n) = o2;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (n + e < N) {
+              if (st_c) P.C[mm * P.ldc + n + e] = o[e];
+              if (st_c2) P.C2[mm * P.ldc2 + n + e] = o2[e];
+            }
+          }
         }
       }
     }
@@ -278,38 +379,40 @@ __global__ __launch_bounds__(kThreads) void gemm_nt_kernel(const Group g) {
 // TN (weight-grad): operands stored [k][x] (x contiguous); LDS tile [BK][BX], unpadded.
 // ------------------------------------------------------------------------------------------------------------------
 
-// One full k-slab rows [k0, k0 + BK) x [x0, x0 + BX) by direct loads; columns past X read the last in-bounds
-// chunk / element instead (requires ld >= X rounded up to 4 for the 16-byte form).
+// Direct loads of one TN operand: one full k-slab, rows [k0, k0 + BK) x columns [x0, x0 + BX), per call; columns
+// past X read the last in-bounds chunk / element instead (the 16-byte form needs ld >= X rounded up to 4, which a
+// leading dimension that is a multiple of 4 guarantees).  Per-lane byte offsets from the slab's first row are fixed.
 template <int BX, int BK, bool W16>
-__device__ __forceinline__ void tn_dma(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
-                                       float* lds_op, int wave, int lane) {
-  if constexpr (W16) {
-    constexpr int NQ = BK * BX / 256;  // instructions of 64 x 16 bytes
-    const int xlast = ((X - 1) >> 2) << 2;
+struct TnLoader {
+  static constexpr int NQ = W16 ? BK * BX / 256 : BK * BX / 64;
+  static constexpr int PER = NQ / 4;
+  static_assert(NQ % 4 == 0, "every wave must issue the same number of loads per slab");
+  uint32_t off[PER];
+
+  __device__ __forceinline__ void init(int64_t ld, int x0, int X, int wave, int lane) {
+    const int xlast = W16 ? ((X - 1) >> 2) << 2 : X - 1;
 #pragma unroll
-    for (int q0 = 0; q0 < NQ; q0 += 4) {
-      const int q = q0 + wave;
-      if (NQ % 4 == 0 || q < NQ) {
-        const int flat = 4 * (64 * q + lane);
-        const int row = flat / BX, x = flat % BX;
-        const int gx = min(x0 + x, xlast);
-        dma<16>(base + static_cast<int64_t>(k0 + row) * ld + gx, lds_op + q * 256);
-      }
+    for (int j = 0; j < PER; ++j) {
+      const int q = 4 * j + wave;
+      const int flat = W16 ? 4 * (64 * q + lane) : 64 * q + lane;
+      const int row = flat / BX, x = flat % BX;
+      const int64_t gx = min(x0 + x, xlast);
+      off[j] = static_cast<uint32_t>((row * ld + gx) * 4);
     }
-  } else {
-    constexpr int NQ = BK * BX / 64;
-#pragma unroll 4
-    for (int q0 = 0; q0 < NQ; q0 += 4) {
-      const int q = q0 + wave;
-      if (NQ % 4 == 0 || q < NQ) {
-        const int flat = 64 * q + lane;
-        const int row = flat / BX, x = flat % BX;
-        const int gx = min(x0 + x, X - 1);
-        dma<4>(base + static_cast<int64_t>(k0 + row) * ld + gx, lds_op + q * 64);
+  }
+  // base: the operand's row k0, wave-uniform.
+  __device__ __forceinline__ void issue(const float* base, float* lds_op, int wave) const {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float* src = reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off[j]);
+      if constexpr (W16) {
+        dma<16>(src, lds_op + (4 * j + wave) * 256);
+      } else {
+        dma<4>(src, lds_op + (4 * j + wave) * 64);
       }
     }
   }
-}
+};
 
 template <int BX, int BK>
 __device__ __forceinline__ void tn_masked(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
@@ -321,16 +424,23 @@ __device__ __forceinline__ void tn_masked(const float* __restrict__ base, int64_
   }
 }
 
-template <int BM, int BN, int BK, bool A16, bool B16>
-__global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const Group g) {
+template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_kernel(
+    const Group g) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = BK * (BM + BN);
   static_assert((TM == 1 || TM == 2) && (TN == 1 || TN == 2), "TN kernel: 1 or 2 MFMA tiles per wave side");
-  __shared__ __align__(16) float lds[2 * STAGE];
+  static_assert(S >= 2 && S <= 4, "2..4 LDS stages");
+  constexpr int L = TnLoader<BM, BK, A16>::PER + TnLoader<BN, BK, B16>::PER;
+  __shared__ __align__(16) float lds[S * STAGE];
 
   const TileCoord tc = locate(g);
   const Problem& P = g.p[tc.pi];
+  // problem fields as values: the loop's compiler barriers would otherwise re-read them from the argument block
+  const float* const A = P.A;
+  const float* const B = P.B;
+  const int64_t lda = P.lda, ldb = P.ldb;
   const int row0 = tc.tm * BM, col0 = tc.tn * BN;
   const int M = P.M, N = P.N;
   const int k_begin = tc.split * P.k_chunk;
@@ -352,23 +462,29 @@ __global__ __launch_bounds__(kThreads) void gemm_tn_kernel(const Group g) {
   const int span = max(k_end - k_begin, 0);
   const int nfull = span / BK;
   const int nk = (span + BK - 1) / BK;
+  TnLoader<BM, BK, A16> la;
+  TnLoader<BN, BK, B16> lb;
+  la.init(lda, row0, M, wave, lane);
+  lb.init(ldb, col0, N, wave, lane);
   auto issue = [&](int kt, int stage) {
     float* st = lds + stage * STAGE;
     const int k0 = k_begin + kt * BK;
     if (kt < nfull) {
-      tn_dma<BM, BK, A16>(P.A, P.lda, row0, M, k0, st, wave, lane);
-      tn_dma<BN, BK, B16>(P.B, P.ldb, col0, N, k0, st + BK * BM, wave, lane);
+      la.issue(A + k0 * lda, st, wave);
+      lb.issue(B + k0 * ldb, st + BK * BM, wave);
     } else {
-      tn_masked<BM, BK>(P.A, P.lda, row0, M, k0, k_end, st);
-      tn_masked<BN, BK>(P.B, P.ldb, col0, N, k0, k_end, st + BK * BM);
+      tn_masked<BM, BK>(A, lda, row0, M, k0, k_end, st);
+      tn_masked<BN, BK>(B, ldb, col0, N, k0, k_end, st + BK * BM);
     }
   };
-  if (nk > 0) issue(0, 0);
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s, s);
   for (int kt = 0; kt < nk; ++kt) {
-    wait_loads();
-    __syncthreads();
-    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
-    const float* As = lds + (kt & 1) * STAGE;
+    wait_slab<L, S>(min(S - 2, nk - 1 - kt));
+    lds_barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    const float* As = lds + (kt % S) * STAGE;
     const float* Bs = As + BK * BM;
     if (do_colsum && tid < BM) {
 #pragma unroll
@@ -524,7 +640,7 @@ int assign_blocks(Group& g, int count, int bm, int bn, const char* name, int& bl
   return PPO_OK;
 }
 
-template <int BM, int BN, int BK, int EPI>
+template <int BM, int BN, int BK, int S, int OCC, int EPI>
 int launch_nt(Group& g, int count, hipStream_t s, const char* name) {
   int blocks;
   if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
@@ -535,18 +651,18 @@ int launch_nt(Group& g, int count, hipStream_t s, const char* name) {
     b16 = b16 && w16_ok(g.p[i].B, g.p[i].ldb);
   }
   if (a16 && b16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else if (a16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, true, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else if (b16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, false, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, false, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, false, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, false, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   }
   return check_launch(name);
 }
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, int S, int OCC>
 int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
   int blocks;
   if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
@@ -557,53 +673,72 @@ int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
     b16 = b16 && w16_ok(g.p[i].B, g.p[i].ldb);
   }
   if (a16 && b16) {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, true, true>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, true, true>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else if (a16) {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, true, false>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, true, false>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else if (b16) {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, false, true>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, false, true>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, false, false>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, false, false>), dim3(blocks), dim3(kThreads), 0, s, g);
   }
   return check_launch(name);
 }
 
-// NT tile of a launch: "PPO_HIP_GEMM_TILE" (e.g. "128x64k32") overrides the size-based choice (tuning aid).
-enum Tile { T128x128k32, T128x128k16, T128x64k32, T64x64k32, T64x128k32 };
+// NT tile of a launch (BM x BN, k-slab depth, LDS stages, waves per SIMD): "PPO_HIP_GEMM_TILE" (e.g.
+// "128x128k16s2o3") overrides the size-based choice (tuning aid).
+enum Tile {
+  T128x128k16s2o3, T128x128k16s3o3, T128x128k16s2o2, T128x128k32s2o2, T128x64k16s4o4, T128x64k32s2o4,
+  T64x64k32s2o4, T64x64k32s2o5, T192x128k16s2o2
+};
 
 Tile pick_tile(Tile dflt) {
   const char* e = std::getenv("PPO_HIP_GEMM_TILE");
   if (e == nullptr) return dflt;
-  if (!std::strcmp(e, "128x128k32")) return T128x128k32;
-  if (!std::strcmp(e, "128x128k16")) return T128x128k16;
-  if (!std::strcmp(e, "128x64k32")) return T128x64k32;
-  if (!std::strcmp(e, "64x64k32")) return T64x64k32;
-  if (!std::strcmp(e, "64x128k32")) return T64x128k32;
+  static const struct {
+    const char* name;
+    Tile t;
+  } kTiles[] = {{"128x128k16s2o3", T128x128k16s2o3}, {"128x128k16s3o3", T128x128k16s3o3},
+                {"128x128k16s2o2", T128x128k16s2o2}, {"128x128k32s2o2", T128x128k32s2o2},
+                {"128x64k16s4o4", T128x64k16s4o4},   {"128x64k32s2o4", T128x64k32s2o4},
+                {"64x64k32s2o4", T64x64k32s2o4},     {"64x64k32s2o5", T64x64k32s2o5},
+                {"192x128k16s2o2", T192x128k16s2o2}};
+  for (const auto& k : kTiles)
+    if (!std::strcmp(e, k.name)) return k.t;
   return dflt;
 }
 
 template <int EPI>
 int launch_nt_tile(Tile t, Group& g, int count, hipStream_t s, const char* name) {
   switch (t) {
-    case T128x128k16:
-      return launch_nt<128, 128, 16, EPI>(g, count, s, name);
-    case T128x64k32:
-      return launch_nt<128, 64, 32, EPI>(g, count, s, name);
-    case T64x64k32:
-      return launch_nt<64, 64, 32, EPI>(g, count, s, name);
-    case T64x128k32:
-      return launch_nt<64, 128, 32, EPI>(g, count, s, name);
+    case T128x128k16s3o3:
+      return launch_nt<128, 128, 16, 3, 3, EPI>(g, count, s, name);
+    case T128x128k16s2o2:
+      return launch_nt<128, 128, 16, 2, 2, EPI>(g, count, s, name);
+    case T128x128k32s2o2:
+      return launch_nt<128, 128, 32, 2, 2, EPI>(g, count, s, name);
+    case T128x64k16s4o4:
+      return launch_nt<128, 64, 16, 4, 4, EPI>(g, count, s, name);
+    case T128x64k32s2o4:
+      return launch_nt<128, 64, 32, 2, 4, EPI>(g, count, s, name);
+    case T64x64k32s2o4:
+      return launch_nt<64, 64, 32, 2, 4, EPI>(g, count, s, name);
+    case T64x64k32s2o5:
+      return launch_nt<64, 64, 32, 2, 5, EPI>(g, count, s, name);
+    case T192x128k16s2o2:
+      return launch_nt<192, 128, 16, 2, 2, EPI>(g, count, s, name);
     default:
-      return launch_nt<128, 128, 32, EPI>(g, count, s, name);
+      return launch_nt<128, 128, 16, 2, 3, EPI>(g, count, s, name);
   }
 }
 
-// Weight-grad: 128 x 128 tiles; split-K over the rows so that the launch covers the chip (~4 blocks per CU), in
-// chunks that are multiples of the 32-row slab.  "PPO_HIP_DW_BK" = 16 selects 16-row slabs (tuning aid).
+// Weight-grad: 128 x 128 tiles; split-K over the rows so that the launch covers the chip, in chunks that are
+// multiples of the 32-row slab.  "PPO_HIP_DW_CFG" (bk32s2o2 / bk16s2o3 / bk16s3o3) and "PPO_HIP_DW_BLOCKS" (target block
+// count) override the defaults (tuning aids).
 constexpr int kDwBM = 128, kDwBN = 128, kDwChunk = 32;
 
 int dw_splits(int64_t tiles, int64_t rows) {
-  const int64_t target = 1024;
+  const char* e = std::getenv("PPO_HIP_DW_BLOCKS");
+  const int64_t target = e ? std::max(1, std::atoi(e)) : 1024;
   int64_t s = ceil_div(target, std::max<int64_t>(tiles, 1));
   s = std::min<int64_t>(s, std::max<int64_t>(1, rows / 256));
   s = std::max<int64_t>(1, std::min<int64_t>(s, 256));
@@ -656,6 +791,9 @@ size_t dx_plan(const ppo_linear_bwd_dx_problem* probs, int count, size_t* offs) 
 
 bool rows_ok(int64_t rows) { return rows > 0 && rows <= INT32_MAX / 2; }
 
+// The kernels address an NT operand with 32-bit byte offsets from its first element.
+bool span_ok(int64_t rows, int64_t ld) { return rows * ld < (int64_t(1) << 30); }
+
 }  // namespace
 }  // namespace ppo
 
@@ -671,11 +809,14 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
   int max_n = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_linear_fwd_problem& q = problems[i];
-    PPO_REQUIRE(q.x && q.w && q.b && q.z, "ppo_linear_fwd: problem %d has a null pointer", i);
+    const bool elu = activation == PPO_ACT_ELU;
+    PPO_REQUIRE(q.x && q.w && q.b && (q.z || (elu && q.h)), "ppo_linear_fwd: problem %d has a null pointer", i);
     PPO_REQUIRE(q.in_features > 0 && q.out_features > 0, "ppo_linear_fwd: problem %d features", i);
-    PPO_REQUIRE(q.ldx >= q.in_features && q.ldz >= q.out_features, "ppo_linear_fwd: problem %d leading dims", i);
-    PPO_REQUIRE(activation == PPO_ACT_NONE || (q.h != nullptr && q.ldh >= q.out_features),
-                "ppo_linear_fwd: problem %d needs h for ELU", i);
+    PPO_REQUIRE(q.ldx >= q.in_features && (q.z == nullptr || q.ldz >= q.out_features) &&
+                    (!elu || q.h == nullptr || q.ldh >= q.out_features),
+                "ppo_linear_fwd: problem %d leading dims", i);
+    PPO_REQUIRE(span_ok(rows, q.ldx) && span_ok(q.out_features, q.in_features),
+                "ppo_linear_fwd: problem %d: an operand spans 4 GiB or more", i);
     Problem& p = g.p[i];
     p.A = q.x; p.lda = q.ldx;
     p.B = q.w; p.ldb = q.in_features;
@@ -684,12 +825,14 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
     p.vec = q.b;
     p.M = static_cast<int>(rows); p.N = q.out_features; p.K = q.in_features;
     p.splits = 1; p.k_chunk = q.in_features;
+    p.c_vec = (q.z == nullptr || w16_ok(q.z, q.ldz)) && (!elu || q.h == nullptr || w16_ok(q.h, q.ldh));
+    if (!elu) p.C2 = nullptr;
     max_n = std::max(max_n, q.out_features);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   // measured on MI355X for 24576-row mini-batches: outputs wider than 128 like 128x128 tiles with 16-deep slabs,
   // narrower ones 128x64
-  const Tile t = pick_tile(max_n > 128 ? T128x128k16 : T128x64k32);
+  const Tile t = pick_tile(max_n > 128 ? T128x128k16s2o3 : T128x64k32s2o4);
   if (activation == PPO_ACT_ELU) return launch_nt_tile<EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_elu");
   return launch_nt_tile<EPI_BIAS>(t, g, count, s, "linear_fwd");
 }
@@ -702,9 +845,11 @@ extern "C" size_t ppo_linear_bwd_dx_workspace_bytes(const ppo_linear_bwd_dx_prob
 }
 
 extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
-                                 void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
+                                 int32_t elu_source, void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS,
               "ppo_linear_bwd_dx: count=%d outside [1, %d]", count, PPO_MAX_LINEAR_PROBLEMS);
+  PPO_REQUIRE(elu_source == PPO_ELU_FROM_INPUT || elu_source == PPO_ELU_FROM_OUTPUT,
+              "ppo_linear_bwd_dx: elu_source=%d", elu_source);
   PPO_REQUIRE(rows_ok(rows), "ppo_linear_bwd_dx: rows=%lld", (long long)rows);
   bool any_act = false, any_plain = false;
   for (int i = 0; i < count; ++i) {
@@ -714,6 +859,8 @@ extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int3
     PPO_REQUIRE(q.lddz >= q.out_features && q.lddz_prev >= q.in_features &&
                     (q.z_prev == nullptr || q.ldz_prev >= q.in_features),
                 "ppo_linear_bwd_dx: problem %d leading dims", i);
+    PPO_REQUIRE(span_ok(rows, q.lddz) && span_ok(q.in_features, (q.out_features + 3) / 4 * 4),
+                "ppo_linear_bwd_dx: problem %d: an operand spans 4 GiB or more", i);
     (q.z_prev ? any_act : any_plain) = true;
   }
   PPO_REQUIRE(!(any_act && any_plain), "ppo_linear_bwd_dx: mix of activation and plain problems in one call");
@@ -744,6 +891,8 @@ extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int3
     p.aux = q.z_prev; p.ldaux = q.ldz_prev;
     p.M = static_cast<int>(rows); p.N = q.in_features; p.K = q.out_features;
     p.splits = 1; p.k_chunk = q.out_features;
+    p.c_vec = w16_ok(q.dz_prev, q.lddz_prev) && (q.z_prev == nullptr || w16_ok(q.z_prev, q.ldz_prev));
+    p.elu_from_output = elu_source == PPO_ELU_FROM_OUTPUT;
     max_n = std::max(max_n, q.in_features);
   }
   for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) tg.it[i].block_begin = INT32_MAX;
@@ -751,7 +900,7 @@ extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int3
   hipLaunchKernelGGL(transpose_kernel, dim3(tblocks), dim3(256), 0, s, tg);
   if (int rc = check_launch("transpose_kernel")) return rc;
   // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
-  const Tile t = pick_tile(max_n > 128 ? T64x64k32 : T128x64k32);
+  const Tile t = pick_tile(max_n > 128 ? T64x64k32s2o4 : T128x64k32s2o4);
   if (any_act) return launch_nt_tile<EPI_ELU_GRAD>(t, g, count, s, "linear_bwd_dx_elu");
   return launch_nt_tile<EPI_STORE>(t, g, count, s, "linear_bwd_dx");
 }
@@ -806,9 +955,17 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   rg.count = count;
   rg.total = total;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const char* bk = std::getenv("PPO_HIP_DW_BK");
-  int rc = (bk && !std::strcmp(bk, "16")) ? launch_tn<kDwBM, kDwBN, 16>(g, count, s, "linear_bwd_dw")
-                                          : launch_tn<kDwBM, kDwBN, 32>(g, count, s, "linear_bwd_dw");
+  const char* cfg = std::getenv("PPO_HIP_DW_CFG");
+  int rc;
+  if (cfg && !std::strcmp(cfg, "bk32s2o2")) {
+    rc = launch_tn<kDwBM, kDwBN, 32, 2, 2>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk16s2o3")) {
+    rc = launch_tn<kDwBM, kDwBN, 16, 2, 3>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk16s3o3")) {
+    rc = launch_tn<kDwBM, kDwBN, 16, 3, 3>(g, count, s, "linear_bwd_dw");
+  } else {
+    rc = launch_tn<kDwBM, kDwBN, 32, 2, 2>(g, count, s, "linear_bwd_dw");
+  }
   if (rc != PPO_OK) return rc;
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 4096);
   hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);

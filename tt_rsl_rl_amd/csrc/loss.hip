@@ -164,21 +164,53 @@ __global__ __launch_bounds__(kLossThreads) void ppo_loss_kernel(const LossParams
   }
 }
 
-constexpr int kFinThreads = 256;
+constexpr int kFinThreads = 1024;
+constexpr int kFinUnroll = 8;
 
+// One block: 16 wavefronts own the columns (wave w: columns w, w + 16, ...).  Each lane keeps kFinUnroll
+// independent fp64 partial sums over the block partials (b = lane + 64 u + 512 i), so a column costs one or two
+// load round trips; the partial sums are combined in a fixed order, then across the wave by a fixed butterfly, so
+// the result is the same on every run.  The per-action std values are computed once, in parallel.
 __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
     const LossParams p, const double* __restrict__ partials, int nblocks, float* __restrict__ d_std_param,
     ppo_device_state* __restrict__ state, int adaptive, float kl_hi, float kl_lo, double* __restrict__ trace) {
   const int A = p.a.num_actions;
   const int cols = kFixedCols + A;
   __shared__ double s_col[kFixedCols + PPO_MAX_ACTIONS];
-  // column sums: wavefront w owns columns w, w + 4, ...; its lanes stride the block partials in a fixed order
+  __shared__ float s_sd[PPO_MAX_ACTIONS], s_lg[PPO_MAX_ACTIONS];
+  __shared__ double s_entropy;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   for (int c = wave; c < cols; c += kFinThreads / 64) {
-    double acc = 0.0;
-    for (int b = lane; b < nblocks; b += 64) acc += partials[static_cast<int64_t>(c) * nblocks + b];
-    acc = wave_sum(acc);
-    if (lane == 0) s_col[c] = acc;
+    const double* col = partials + static_cast<int64_t>(c) * nblocks;
+    double acc[kFinUnroll];
+#pragma unroll
+    for (int u = 0; u < kFinUnroll; ++u) acc[u] = 0.0;
+    for (int b0 = lane; b0 < nblocks; b0 += 64 * kFinUnroll) {
+#pragma unroll
+      for (int u = 0; u < kFinUnroll; ++u) {
+        const int b = b0 + 64 * u;
+        if (b < nblocks) acc[u] += col[b];
+      }
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (int u = 0; u < kFinUnroll; ++u) sum += acc[u];
+    sum = wave_sum(sum);
+    if (lane == 0) s_col[c] = sum;
+  }
+  if (threadIdx.x < A) {
+    float sd, lg;
+    std_of(p, threadIdx.x, sd, lg);
+    s_sd[threadIdx.x] = sd;
+    s_lg[threadIdx.x] = lg;
+  }
+  __syncthreads();
+  if (wave == 0) {  // every row's entropy is the same sum over actions: fp64, fixed-order butterfly
+    const float ec = static_cast<float>(kEntropyConst);
+    double e = 0.0;
+    for (int j = lane; j < A; j += 64) e += static_cast<double>(ec + s_lg[j]);
+    e = wave_sum(e);
+    if (lane == 0) s_entropy = e;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -186,14 +218,7 @@ __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
     const float surrogate = static_cast<float>(s_col[0] / R);
     const float value = static_cast<float>(s_col[1] / R);
     const float kl_mean = static_cast<float>(s_col[2] / R);
-    double ent_acc = 0.0;  // every row's entropy is the same sum over actions; accumulate it in fp64
-    const float ec = static_cast<float>(kEntropyConst);
-    for (int j = 0; j < A; ++j) {
-      float sd, lg;
-      std_of(p, j, sd, lg);
-      ent_acc += static_cast<double>(ec + lg);
-    }
-    const float entropy = static_cast<float>(ent_acc);
+    const float entropy = static_cast<float>(s_entropy);
     double lr = state->learning_rate;
     if (adaptive) {
       if (kl_mean > kl_hi) {
@@ -226,10 +251,8 @@ __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
   for (int j = threadIdx.x; j < A; j += kFinThreads) {
     const float q = p.a.std_param[j];
     const bool inside = (q >= p.std_lo) && (q <= p.std_hi);
-    float sd, lg;
-    std_of(p, j, sd, lg);
     const double dlog = s_col[kFixedCols + j] - static_cast<double>(c_e);
-    double g = (p.a.std_type == PPO_STD_LOG) ? dlog : dlog / static_cast<double>(sd);
+    const double g = (p.a.std_type == PPO_STD_LOG) ? dlog : dlog / static_cast<double>(s_sd[j]);
     d_std_param[j] = inside ? static_cast<float>(g) : 0.0f;
   }
 }

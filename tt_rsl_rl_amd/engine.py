@@ -45,14 +45,19 @@ class TableLayout:
 
 
 class ModelBuffers:
-    """Activation and gradient buffers of one MLP for mini-batches of up to `rows` rows."""
+    """Activation and gradient buffers of one MLP for mini-batches of up to `rows` rows.  Rows are padded to a
+    multiple of 4 floats (views keep the logical width) so every buffer can be read with 16-byte loads."""
 
     def __init__(self, model, rows: int, device) -> None:
         lin = model.linears
         self.widths = [l.out_features for l in lin]
-        self.z = [torch.empty(rows, w, device=device) for w in self.widths]
-        self.h = [torch.empty(rows, w, device=device) for w in self.widths[:-1]]
-        self.dz = [torch.empty(rows, w, device=device) for w in self.widths]
+
+        def buf(w: int) -> torch.Tensor:
+            return torch.empty(rows, -(-w // 4) * 4, device=device)[:, :w]
+
+        self.out = buf(self.widths[-1])                 # output layer (no activation): mean / value
+        self.h = [buf(w) for w in self.widths[:-1]]     # hidden layers keep only elu(z); ELU' is taken from it
+        self.dz = [buf(w) for w in self.widths]
 
 
 class PhaseTimer:
@@ -167,8 +172,8 @@ class UpdateEngine:
         ins_a, ins_c = [xa], [xc]
         for i in range(nl):
             last = i == nl - 1
-            probs = [(ins_a[-1], la[i].weight, la[i].bias, ba.z[i][:R], None if last else ba.h[i][:R]),
-                     (ins_c[-1], lc[i].weight, lc[i].bias, bc.z[i][:R], None if last else bc.h[i][:R])]
+            probs = [(ins_a[-1], la[i].weight, la[i].bias, ba.out[:R] if last else None, None if last else ba.h[i][:R]),
+                     (ins_c[-1], lc[i].weight, lc[i].bias, bc.out[:R] if last else None, None if last else bc.h[i][:R])]
             tm.start(f"fwd{i}")
             ops.linear_fwd(probs, R, elu=not last)
             tm.stop(f"fwd{i}")
@@ -182,7 +187,7 @@ class UpdateEngine:
         batch = {"ld": lay.width, "actions": tab[:, lay.actions], "old_mean": tab[:, lay.old_mean],
                  "old_std": tab[:, lay.old_std], "old_logp": tab[:, lay.old_logp], "advantages": tab[:, adv_col],
                  "old_values": tab[:, lay.old_values], "returns": tab[:, lay.returns]}
-        args = ops.make_loss_args(R, ba.z[-1][:R], bc.z[-1][:R, 0], batch, dist.param, dist.kernel_std_type, lo, hi,
+        args = ops.make_loss_args(R, ba.out[:R], bc.out[:R, 0], batch, dist.param, dist.kernel_std_type, lo, hi,
                                   alg.clip_param, alg.value_loss_coef, alg.entropy_coef, alg.use_clipped_value_loss,
                                   ba.dz[-1][:R], bc.dz[-1][:R, 0])
         tm.start("loss")
@@ -195,8 +200,9 @@ class UpdateEngine:
         # backward: input gradients down the chain (grouped), then every weight gradient in one launch
         for i in range(nl - 1, 0, -1):
             tm.start(f"dx{i}")
-            ops.linear_bwd_dx([(ba.dz[i][:R], la[i].weight, ba.z[i - 1][:R], ba.dz[i - 1][:R]),
-                               (bc.dz[i][:R], lc[i].weight, bc.z[i - 1][:R], bc.dz[i - 1][:R])], R, self.dx_ws)
+            ops.linear_bwd_dx([(ba.dz[i][:R], la[i].weight, ba.h[i - 1][:R], ba.dz[i - 1][:R]),
+                               (bc.dz[i][:R], lc[i].weight, bc.h[i - 1][:R], bc.dz[i - 1][:R])], R, self.dx_ws,
+                              elu_from_output=True)
             tm.stop(f"dx{i}")
         dw = []
         for model, buf, lins, x0 in ((actor, ba, la, xa), (critic, bc, lc, xc)):

@@ -271,12 +271,12 @@ class MLPModel(nn.Module):
     def mlp_forward(self, latent: torch.Tensor) -> torch.Tensor:
         rows = latent.shape[0]
         lin = self.linears
-        widths = [l.out_features for l in lin[:-1] for _ in (0, 1)] + [lin[-1].out_features]
+        widths = [l.out_features for l in lin[:-1]]
         bufs = self._fwd.get(rows, widths, latent.device)
         x = latent
         for i, l in enumerate(lin[:-1]):
-            z, h = bufs[2 * i], bufs[2 * i + 1]
-            ops.linear_fwd([(x, l.weight, l.bias, z, h)], rows, elu=True)
+            h = bufs[i]  # hidden layers: only elu(z) is needed
+            ops.linear_fwd([(x, l.weight, l.bias, None, h)], rows, elu=True)
             x = h
         out = torch.empty(rows, lin[-1].out_features, device=latent.device)
         ops.linear_fwd([(x, lin[-1].weight, lin[-1].bias, out, None)], rows, elu=False)

@@ -146,29 +146,36 @@ def _check_weight(w: torch.Tensor, b: torch.Tensor | None) -> tuple[int, int]:
 
 
 def linear_fwd(problems: list[tuple], rows: int, elu: bool) -> None:
-    """problems: (x [rows, in], w [out, in], b [out], z [rows, out], h [rows, out] or None)."""
+    """problems: (x [rows, in], w [out, in], b [out], z [rows, out] or None, h [rows, out] or None).
+    Without ELU z is required; with ELU at least one of z / h."""
     items = []
     for x, w, b, z, h in problems:
         _dev(x, w, b, z, h)
         out_f, in_f = _check_weight(w, b)
-        ldx, ldz = _row_major(x, "x"), _row_major(z, "z")
-        if x.shape[0] < rows or z.shape[0] < rows or x.shape[1] < in_f or z.shape[1] < out_f:
-            raise ValueError("linear_fwd: activation buffers too small")
-        ldh = 0
-        if h is not None:
+        ldx = _row_major(x, "x")
+        if x.shape[0] < rows or x.shape[1] < in_f:
+            raise ValueError("linear_fwd: x too small")
+        if z is None and not (elu and h is not None):
+            raise ValueError("linear_fwd: z is required (without ELU, or without h)")
+        ldz = ldh = 0
+        if z is not None:
+            ldz = _row_major(z, "z")
+            if z.shape[0] < rows or z.shape[1] < out_f:
+                raise ValueError("linear_fwd: z too small")
+        if h is not None and elu:
             ldh = _row_major(h, "h")
             if h.shape[0] < rows or h.shape[1] < out_f:
                 raise ValueError("linear_fwd: h too small")
-        elif elu:
-            raise ValueError("linear_fwd: ELU needs an h buffer")
-        items.append(L.LinearFwdProblem(x.data_ptr(), ldx, w.data_ptr(), b.data_ptr(), z.data_ptr(), ldz, _ptr(h),
-                                        ldh, in_f, out_f))
+        items.append(L.LinearFwdProblem(x.data_ptr(), ldx, w.data_ptr(), b.data_ptr(), _ptr(z), ldz,
+                                        _ptr(h) if elu else None, ldh, in_f, out_f))
     L.call("ppo_linear_fwd", L.array(L.LinearFwdProblem, items), len(items), rows,
            L.PPO_ACT_ELU if elu else L.PPO_ACT_NONE, _stream())
 
 
-def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:
-    """problems: (dz [rows, out], w [out, in], z_prev [rows, in] or None, dz_prev [rows, in])."""
+def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None, elu_from_output: bool = False
+                  ) -> None:
+    """problems: (dz [rows, out], w [out, in], act [rows, in] or None, dz_prev [rows, in]); act is the ELU input z
+    of the layer below, or its output h = elu(z) with elu_from_output."""
     items = []
     for dz, w, z_prev, dz_prev in problems:
         _dev(dz, w, z_prev, dz_prev)
@@ -186,7 +193,8 @@ def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None)
     if nbytes == 0:
         raise ValueError("linear_bwd_dx: invalid problem set")
     buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
-    L.call("ppo_linear_bwd_dx", arr, len(items), rows, buf.data_ptr(), buf.numel(), _stream())
+    src = L.PPO_ELU_FROM_OUTPUT if elu_from_output else L.PPO_ELU_FROM_INPUT
+    L.call("ppo_linear_bwd_dx", arr, len(items), rows, src, buf.data_ptr(), buf.numel(), _stream())
 
 
 def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:

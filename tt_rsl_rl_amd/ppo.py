@@ -91,12 +91,18 @@ def resolve_obs_groups(obs: Mapping, obs_groups: dict, default_sets: list[str]) 
 # ----------------------------------------------------------------------------------------------------------------------
 
 class FlatParams:
-    """Parameters, gradients and Adam moments of an ordered parameter list as views of four flat fp32 buffers."""
+    """Parameters, gradients and Adam moments of an ordered parameter list as views of four flat fp32 buffers.
+
+    Every parameter starts on a 64-byte boundary (ALIGN floats) so the GEMM kernels can fetch weight rows with
+    16-byte loads; the zero padding between parameters has zero gradient and stays zero under Adam."""
+
+    ALIGN = 16
 
     def __init__(self, groups: list[list[nn.Parameter]], device) -> None:
         params = [p for g in groups for p in g]
-        n = sum(p.numel() for p in params)
-        self.param = torch.empty(n, device=device)
+        a = self.ALIGN
+        n = sum(-(-p.numel() // a) * a for p in params)
+        self.param = torch.zeros(n, device=device)
         self.grad = torch.zeros(n, device=device)
         self.exp_avg = torch.zeros(n, device=device)
         self.exp_avg_sq = torch.zeros(n, device=device)
@@ -111,7 +117,7 @@ class FlatParams:
                     p.data = self.param[off:off + k].view(p.shape)
                     p.grad = self.grad[off:off + k].view(p.shape)
                     self.offsets[id(p)] = (off, k)
-                    off += k
+                    off += -(-k // a) * a
                 bounds.append(off)
         self.group_begin = torch.tensor(bounds, dtype=torch.int64)
         self.params = params
