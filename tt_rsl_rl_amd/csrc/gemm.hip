@@ -149,8 +149,8 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 template <int BK>
 __device__ __forceinline__ int nt_swz(int row) {
   constexpr int CPR = BK / 4;
-  static_assert(CPR == 4 || CPR == 8, "BK must be 16 or 32");
-  return CPR == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+  static_assert(CPR == 4 || CPR == 8 || CPR == 16, "BK must be 16, 32 or 64");
+  return CPR == 16 ? (row & 15) : CPR == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 
 // Direct loads of one NT operand: one full k-slab [x0, x0 + BX) x [k0, k0 + BK) per call, rows >= X clamped to X - 1.
@@ -270,20 +270,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
     const float* As = lds + (kt % S) * STAGE;
     const float* Bs = As + BM * BK;
-#pragma unroll
-    for (int gi = 0; gi < BK / 8; ++gi) {
+    // k-groups of 4 MFMA steps; the fragments of group g + 1 are read before the MFMAs of group g issue
+    constexpr int G = BK / 8;
+    f32x4 fa[2][TM], fb[2][TN];
+    auto load_group = [&](int buf, int gi) {
       const int c = 2 * gi + (lane >> 5);
-      f32x4 fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int r = wm * WM + 32 * i + (lane & 31);
-        fa[i] = *reinterpret_cast<const f32x4*>(As + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+        fa[buf][i] = *reinterpret_cast<const f32x4*>(As + r * BK + 4 * (c ^ nt_swz<BK>(r)));
       }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int r = wn * WN + 32 * j + (lane & 31);
-        fb[j] = *reinterpret_cast<const f32x4*>(Bs + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+        fb[buf][j] = *reinterpret_cast<const f32x4*>(Bs + r * BK + 4 * (c ^ nt_swz<BK>(r)));
       }
+    };
+    load_group(0, 0);
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      if (gi + 1 < G) load_group((gi + 1) & 1, gi + 1);
+      // scheduling fences: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -291,7 +299,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             // weights (B) as the MFMA's A operand: the accumulator holds the 32 x 32 tile of C transposed
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[j][s], fa[i][s], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[gi & 1][j][s], fa[gi & 1][i][s], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -430,7 +439,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = BK * (BM + BN);
-  static_assert((TM == 1 || TM == 2) && (TN == 1 || TN == 2), "TN kernel: 1 or 2 MFMA tiles per wave side");
+  static_assert(TM == 2 && TN == 2, "TN kernel: 2 x 2 interleaved MFMA tiles per wave");
+  static_assert(kThreads % BM == 0 && BK % 8 == 0, "TN column sums split the slab over kThreads / BM threads");
   static_assert(S >= 2 && S <= 4, "2..4 LDS stages");
   constexpr int L = TnLoader<BM, BK, A16>::PER + TnLoader<BN, BK, B16>::PER;
   __shared__ __align__(16) float lds[S * STAGE];
@@ -458,7 +468,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
   const bool do_colsum = P.colsum != nullptr && tc.tn == 0;
-  double colsum_acc = 0.0;
+  double colsum_acc[4] = {0.0, 0.0, 0.0, 0.0};
   const int span = max(k_end - k_begin, 0);
   const int nfull = span / BK;
   const int nk = (span + BK - 1) / BK;
@@ -486,34 +496,37 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
     const float* As = lds + (kt % S) * STAGE;
     const float* Bs = As + BK * BM;
-    if (do_colsum && tid < BM) {
+    if (do_colsum) {  // column c = tid % BM, rows of this thread's half of the slab, 4 independent chains
+      const int c = tid % BM, k0 = (tid / BM) * (BK / 2);
 #pragma unroll
-      for (int kk = 0; kk < BK; ++kk) colsum_acc += static_cast<double>(As[kk * BM + tid]);
+      for (int kk = 0; kk < BK / 2; ++kk) colsum_acc[kk & 3] += static_cast<double>(As[(k0 + kk) * BM + c]);
     }
+    // groups of 4 k-steps (8 rows of k): the fragments of group g + 1 are read before the MFMAs of group g issue
+    constexpr int G = BK / 8;
+    f32x2 fa[2][4], fb[2][4];
+    auto load_group = [&](int buf, int gi) {
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 2) {
-      const float* ar = As + (kk + h) * BM + wm * WM;
-      const float* br = Bs + (kk + h) * BN + wn * WN;
-      float fa[TM], fb[TN];
-      if constexpr (TM == 2) {
-        const f32x2 a = *reinterpret_cast<const f32x2*>(ar + 2 * sg);
-        fa[0] = a[0];
-        fa[1] = a[1];
-      } else {
-        fa[0] = ar[sg];
+      for (int st = 0; st < 4; ++st) {
+        const int kk = 8 * gi + 2 * st + h;
+        fa[buf][st] = *reinterpret_cast<const f32x2*>(As + kk * BM + wm * WM + 2 * sg);
+        fb[buf][st] = *reinterpret_cast<const f32x2*>(Bs + kk * BN + wn * WN + 2 * sg);
       }
-      if constexpr (TN == 2) {
-        const f32x2 b = *reinterpret_cast<const f32x2*>(br + 2 * sg);
-        fb[0] = b[0];
-        fb[1] = b[1];
-      } else {
-        fb[0] = br[sg];
-      }
+    };
+    load_group(0, 0);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+    for (int gi = 0; gi < G; ++gi) {
+      if (gi + 1 < G) load_group((gi + 1) & 1, gi + 1);
+      // scheduling fences: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i], fb[j], acc[i][j], 0, 0, 0);
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[gi & 1][st][i], fb[gi & 1][st][j], acc[i][j], 0,
+                                                             0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
@@ -542,7 +555,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       }
     }
   }
-  if (do_colsum && tid < BM && row0 + tid < M) P.colsum[static_cast<int64_t>(tc.split) * M + row0 + tid] = colsum_acc;
+  if (do_colsum) {  // the two halves of each column, combined in a fixed order through the (now free) LDS ring
+    double* part = reinterpret_cast<double*>(lds);
+    const double mine = (colsum_acc[0] + colsum_acc[1]) + (colsum_acc[2] + colsum_acc[3]);
+    lds_barrier();
+    if (tid >= BM) part[tid - BM] = mine;
+    lds_barrier();
+    if (tid < BM && row0 + tid < M) P.colsum[static_cast<int64_t>(tc.split) * M + row0 + tid] = mine + part[tid];
+  }
 }
 
 // Fixed-order reduction of split-K weight-grad partials: dw = sum_s partial[s], db = sum_s colsum[s].
@@ -688,7 +708,8 @@ int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
 // "128x128k16s2o3") overrides the size-based choice (tuning aid).
 enum Tile {
   T128x128k16s2o3, T128x128k16s3o3, T128x128k16s2o2, T128x128k32s2o2, T128x64k16s4o4, T128x64k32s2o4,
-  T64x64k32s2o4, T64x64k32s2o5, T192x128k16s2o2
+  T64x64k32s2o4, T64x64k32s2o5, T192x128k16s2o2, T128x128k64s2o1, T128x128k32s2o1, T256x128k32s2o1,
+  T128x64k64s2o2
 };
 
 Tile pick_tile(Tile dflt) {
@@ -701,7 +722,9 @@ Tile pick_tile(Tile dflt) {
                 {"128x128k16s2o2", T128x128k16s2o2}, {"128x128k32s2o2", T128x128k32s2o2},
                 {"128x64k16s4o4", T128x64k16s4o4},   {"128x64k32s2o4", T128x64k32s2o4},
                 {"64x64k32s2o4", T64x64k32s2o4},     {"64x64k32s2o5", T64x64k32s2o5},
-                {"192x128k16s2o2", T192x128k16s2o2}};
+                {"192x128k16s2o2", T192x128k16s2o2}, {"128x128k64s2o1", T128x128k64s2o1},
+                {"128x128k32s2o1", T128x128k32s2o1}, {"256x128k32s2o1", T256x128k32s2o1},
+                {"128x64k64s2o2", T128x64k64s2o2}};
   for (const auto& k : kTiles)
     if (!std::strcmp(e, k.name)) return k.t;
   return dflt;
@@ -726,15 +749,23 @@ int launch_nt_tile(Tile t, Group& g, int count, hipStream_t s, const char* name)
       return launch_nt<64, 64, 32, 2, 5, EPI>(g, count, s, name);
     case T192x128k16s2o2:
       return launch_nt<192, 128, 16, 2, 2, EPI>(g, count, s, name);
+    case T128x128k64s2o1:
+      return launch_nt<128, 128, 64, 2, 1, EPI>(g, count, s, name);
+    case T128x128k32s2o1:
+      return launch_nt<128, 128, 32, 2, 1, EPI>(g, count, s, name);
+    case T256x128k32s2o1:
+      return launch_nt<256, 128, 32, 2, 1, EPI>(g, count, s, name);
+    case T128x64k64s2o2:
+      return launch_nt<128, 64, 64, 2, 2, EPI>(g, count, s, name);
     default:
       return launch_nt<128, 128, 16, 2, 3, EPI>(g, count, s, name);
   }
 }
 
 // Weight-grad: 128 x 128 tiles; split-K over the rows so that the launch covers the chip, in chunks that are
-// multiples of the 32-row slab.  "PPO_HIP_DW_CFG" (bk32s2o2 / bk16s2o3 / bk16s3o3) and "PPO_HIP_DW_BLOCKS" (target block
+// multiples of the deepest (64-row) slab.  "PPO_HIP_DW_CFG" (bk32s2o2 / bk16s2o3 / bk16s3o3) and "PPO_HIP_DW_BLOCKS" (target block
 // count) override the defaults (tuning aids).
-constexpr int kDwBM = 128, kDwBN = 128, kDwChunk = 32;
+constexpr int kDwBM = 128, kDwBN = 128, kDwChunk = 64;
 
 int dw_splits(int64_t tiles, int64_t rows) {
   const char* e = std::getenv("PPO_HIP_DW_BLOCKS");
@@ -963,6 +994,10 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     rc = launch_tn<kDwBM, kDwBN, 16, 2, 3>(g, count, s, "linear_bwd_dw");
   } else if (cfg && !std::strcmp(cfg, "bk16s3o3")) {
     rc = launch_tn<kDwBM, kDwBN, 16, 3, 3>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk64s2o1")) {
+    rc = launch_tn<kDwBM, kDwBN, 64, 2, 1>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk32s2o1")) {
+    rc = launch_tn<kDwBM, kDwBN, 32, 2, 1>(g, count, s, "linear_bwd_dw");
   } else {
     rc = launch_tn<kDwBM, kDwBN, 32, 2, 2>(g, count, s, "linear_bwd_dw");
   }
