@@ -269,6 +269,72 @@ int ppo_adam_step(float* params, float* grads, float* exp_avg, float* exp_avg_sq
                   double bc2_sqrt, ppo_device_state* state, void* workspace, size_t workspace_bytes,
                   ppo_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------------------------------
+ * A15  LSTM of the recurrent models (torch nn.LSTM, one layer, gates i, f, g, o): rsl_rl/modules/rnn.py:22-86,
+ * rsl_rl/models/rnn_model.py:76-84, the recurrent mini-batches of rsl_rl/storage/rollout_storage.py:262-331 and the
+ * trajectory padding of rsl_rl/utils/utils.py:395-463.
+ *
+ * Upstream splits every env's steps into trajectories at the dones, pads them, runs the LSTM over each from the
+ * state the rollout saved at its first step, and unpads.  A trajectory after a done starts from the zero state the
+ * rollout saved after resetting, so the same outputs come from one sequence per env over the mini-batch's T steps,
+ * from the state saved at step 0, with the state multiplied by keep_t = 1 - done_t after step t.  That is the form
+ * evaluated here: rows are t * E + e (step-major), the envs of a mini-batch being E consecutive envs.
+ *
+ * Gate-interleaved layout ("_g"): row (or column) 4u + q holds gate q (i, f, g, o) of hidden unit u, so that one
+ * 16-byte group holds the four gates of a unit.  H must be a multiple of 4; every pointer 16-byte aligned and
+ * every leading dimension a multiple of 4.
+ * ------------------------------------------------------------------------------------------------------------------ */
+#define PPO_MAX_LSTM_PROBLEMS 2
+
+/* torch-layout weights -> gate-interleaved copies: w_ih_g [4H, D], w_hh_g [4H, H], w_hh_gt = w_hh_g^T [H, 4H],
+ * b_g = b_ih + b_hh [4H] (the gates' bias, nn.LSTM adds both). */
+typedef struct ppo_lstm_pack_problem {
+  const float* w_ih; const float* w_hh; const float* b_ih; const float* b_hh; /* [4H, D], [4H, H], [4H], [4H] */
+  float* w_ih_g; float* w_hh_g; float* w_hh_gt; float* b_g;
+  int32_t input_size;
+  int32_t hidden;
+} ppo_lstm_pack_problem;
+
+int ppo_lstm_pack(const ppo_lstm_pack_problem* problems, int32_t count, ppo_stream_t stream);
+
+/* One model's sequence over T steps x E envs.  The forward consumes gx = x w_ih_g^T + b_g for every row (from
+ * ppo_linear_fwd) and writes, per step, the gate activations, the cell and hidden states, and hs (the state entering
+ * each step: hs[0] = h0, hs[t+1] = h_t * keep_t), which the weight-gradient of w_hh reads as [T*E, H] (its first
+ * T*E rows).  The backward runs t = T-1 .. 0: dL/dh_t = dh[t] + keep_t * (dgates[t+1] w_hh_g) and the carried cell
+ * gradient give dgates[t] (pre-activation gate gradients, the operand of both weight-gradients and of the bias
+ * gradient); dc is scratch (no initialisation needed). */
+typedef struct ppo_lstm_seq_problem {
+  const float* w_hh_g;                       /* [4H, H] */
+  const float* w_hh_gt;                      /* [H, 4H] (backward) */
+  const float* gx; int64_t ldgx;             /* [T*E, 4H] */
+  const float* h0; const float* c0; int64_t ld0; /* [E, H] state entering step 0 */
+  const float* keep; int64_t keep_stride;    /* 1 - done per row t*E + e, elements keep_stride floats apart */
+  float* h; int64_t ldh;                     /* [T*E, H] h_t (before the reset) */
+  float* hs;                                 /* [(T+1)*E, H], ld H */
+  float* c;                                  /* [T*E, H] c_t (before the reset), ld H */
+  float* gates;                              /* [T*E, 4H] activations, ld 4H */
+  const float* dh; int64_t lddh;             /* backward: [T*E, H] dL/dh_t from the layers above */
+  float* dgates;                             /* backward: [T*E, 4H], ld 4H */
+  float* dc;                                 /* backward: [E, H] scratch, ld H */
+  int32_t hidden;
+  int32_t reserved;
+} ppo_lstm_seq_problem;
+
+int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
+                     ppo_stream_t stream);
+int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
+                     ppo_stream_t stream);
+
+/* gate-interleaved gradients -> torch-layout gradients (the bias gradient goes to both b_ih and b_hh). */
+typedef struct ppo_lstm_grad_problem {
+  const float* dw_ih_g; const float* dw_hh_g; const float* db_g;
+  float* dw_ih; float* dw_hh; float* db_ih; float* db_hh;
+  int32_t input_size;
+  int32_t hidden;
+} ppo_lstm_grad_problem;
+
+int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

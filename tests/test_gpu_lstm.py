@@ -1,0 +1,78 @@
+"""The LSTM kernels through the C ABI (ppo_lstm_pack / _seq_fwd / _seq_bwd / _unpack_grads, plus the input projection
+and weight gradients through the linear entry points) against an fp64 reference of torch.nn.LSTM's cell equations
+over the masked per-env sequence (state multiplied by 1 - done after each step) with autograd gradients.  The
+equivalence of that sequence with upstream's padded trajectories is pinned on the CPU
+(tests/test_oracle_recurrent.py)."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from tests.parity import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _reference(x, h0, c0, dones, w_ih, w_hh, b_ih, b_hh, dh):
+    """fp64: outputs [T, E, H] and d(sum(out * dh))/d(w_ih, w_hh, b_ih, b_hh)."""
+    params = [p.detach().double().requires_grad_(True) for p in (w_ih, w_hh, b_ih, b_hh)]
+    w_ih, w_hh, b_ih, b_hh = params
+    H = h0.shape[1]
+    h, c = h0.double(), c0.double()
+    outs = []
+    for t in range(x.shape[0]):
+        g = x[t].double() @ w_ih.t() + b_ih + h @ w_hh.t() + b_hh
+        i, f, gg, o = (g[:, k * H:(k + 1) * H] for k in range(4))
+        c = torch.sigmoid(f) * c + torch.sigmoid(i) * torch.tanh(gg)
+        h = torch.sigmoid(o) * torch.tanh(c)
+        outs.append(h)
+        keep = (1.0 - dones[t].double())[:, None]
+        h, c = h * keep, c * keep
+    out = torch.stack(outs)
+    (out * dh.double()).sum().backward()
+    return out.detach(), [p.grad for p in params]
+
+
+@pytest.mark.parametrize("T,E,D,H", [(7, 64, 48, 256), (5, 200, 13, 8), (24, 1024, 48, 256)])
+def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H):
+    from tt_rsl_rl_amd import ops
+
+    torch.manual_seed(T * 1000 + H)
+    lstm = torch.nn.LSTM(D, H)
+    w_ih, w_hh, b_ih, b_hh = (p.detach() for p in (lstm.weight_ih_l0, lstm.weight_hh_l0, lstm.bias_ih_l0,
+                                                    lstm.bias_hh_l0))
+    x = torch.randn(T, E, D)
+    h0, c0 = torch.randn(E, H) * 0.5, torch.randn(E, H) * 0.5
+    dones = (torch.rand(T, E) < 0.2).float()
+    dh = torch.randn(T, E, H) / math.sqrt(H)
+    ref_out, ref_grads = _reference(x, h0, c0, dones, w_ih, w_hh, b_ih, b_hh, dh)
+
+    dev = cuda
+    g = lambda t: t.contiguous().to(dev)
+    pk = ops.LstmPacked(D, H, dev)
+    wd = [g(w) for w in (w_ih, w_hh, b_ih, b_hh)]
+    ops.lstm_pack([(*wd, pk)])
+    R = T * E
+    xf = g(x.reshape(R, D))
+    gx = torch.empty(R, 4 * H, device=dev)
+    ops.linear_fwd([(xf, pk.w_ih_g, pk.b_g, gx, None)], R, elu=False)
+    keep = g(1.0 - dones.reshape(R))
+    q = dict(packed=pk, hidden=H, gx=gx, h0=g(h0), c0=g(c0), keep=keep, h=torch.empty(R, H, device=dev),
+             hs=torch.empty(R + E, H, device=dev), c=torch.empty(R, H, device=dev),
+             gates=torch.empty(R, 4 * H, device=dev), dh=g(dh.reshape(R, H)),
+             dgates=torch.empty(R, 4 * H, device=dev), dc=torch.empty(E, H, device=dev))
+    ops.lstm_seq_fwd([q], T, E)
+    assert rel_err(q["h"].view(T, E, H), ref_out) < 1e-5
+    ops.lstm_seq_bwd([q], T, E)
+    dw_ih_g, dw_hh_g = torch.empty(4 * H, D, device=dev), torch.empty(4 * H, H, device=dev)
+    db_g, db_g2 = torch.empty(4 * H, device=dev), torch.empty(4 * H, device=dev)
+    ops.linear_bwd_dw([(q["dgates"], q["hs"][:R], dw_hh_g, db_g), (q["dgates"], xf, dw_ih_g, db_g2)], R)
+    grads = [torch.empty_like(t) for t in wd]
+    ops.lstm_unpack_grads([(dw_ih_g, dw_hh_g, db_g, *grads)])
+    torch.cuda.synchronize()
+    for name, got, want in zip(("w_ih", "w_hh", "b_ih", "b_hh"), grads, ref_grads):
+        assert rel_err(got, want) < 1e-5, name
+    assert torch.equal(db_g, db_g2)  # the same column sums of dgates, in the same fixed order

@@ -53,6 +53,13 @@ STRUCTS = {
     "ppo_device_state": ("DeviceState", ["learning_rate", "sum_value_loss", "sum_surrogate_loss", "sum_entropy",
                                          "last_kl_mean", "last_value_loss", "last_surrogate_loss", "last_entropy",
                                          "total_norm", "clip_coef", "num_minibatches"]),
+    "ppo_lstm_pack_problem": ("LstmPackProblem", ["w_ih", "w_hh", "b_ih", "b_hh", "w_ih_g", "w_hh_g", "w_hh_gt",
+                                                  "b_g", "input_size", "hidden"]),
+    "ppo_lstm_seq_problem": ("LstmSeqProblem", ["w_hh_g", "w_hh_gt", "gx", "ldgx", "h0", "c0", "ld0", "keep",
+                                                "keep_stride", "h", "ldh", "hs", "c", "gates", "dh", "lddh",
+                                                "dgates", "dc", "hidden"]),
+    "ppo_lstm_grad_problem": ("LstmGradProblem", ["dw_ih_g", "dw_hh_g", "db_g", "dw_ih", "dw_hh", "db_ih", "db_hh",
+                                                  "input_size", "hidden"]),
 }
 
 
@@ -99,5 +106,17 @@ def test_argument_validation_reports_errors_without_a_gpu():
     assert lib.ppo_loss_workspace_bytes(24576, 29) > 0
     assert lib.ppo_loss_workspace_bytes(24576, 65) == 0
     assert lib.ppo_adam_workspace_bytes(433211) >= 8 * (433211 // 4096)
+    # LSTM entry points: argument checks run before any launch
+    seq = _lib.LstmSeqProblem(hidden=6)
+    with pytest.raises(ValueError, match="hidden=6"):
+        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(seq), 1, 24, 64, None)
+    seq = _lib.LstmSeqProblem(hidden=256)
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.call("ppo_lstm_seq_bwd", ctypes.byref(seq), 1, 24, 64, None)
+    with pytest.raises(ValueError, match="count"):
+        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(seq), 3, 24, 64, None)
+    pack = _lib.LstmPackProblem(8, 8, 8, 8, 8, 8, 8, 8, 48, 250)
+    with pytest.raises(ValueError, match="sizes"):
+        _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)
     probs = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512)])
     assert lib.ppo_linear_bwd_dw_workspace_bytes(probs, 1, 24576) >= 4 * 512 * 96

@@ -82,6 +82,24 @@ class DeviceState(C.Structure):
 
 
 DEVICE_STATE_BYTES = C.sizeof(DeviceState)
+MAX_LSTM_PROBLEMS = 2
+vp = C.c_void_p
+
+
+class LstmPackProblem(C.Structure):
+    _fields_ = [("w_ih", vp), ("w_hh", vp), ("b_ih", vp), ("b_hh", vp), ("w_ih_g", vp), ("w_hh_g", vp),
+                ("w_hh_gt", vp), ("b_g", vp), ("input_size", i32), ("hidden", i32)]
+
+
+class LstmSeqProblem(C.Structure):
+    _fields_ = [("w_hh_g", vp), ("w_hh_gt", vp), ("gx", vp), ("ldgx", i64), ("h0", vp), ("c0", vp), ("ld0", i64),
+                ("keep", vp), ("keep_stride", i64), ("h", vp), ("ldh", i64), ("hs", vp), ("c", vp), ("gates", vp),
+                ("dh", vp), ("lddh", i64), ("dgates", vp), ("dc", vp), ("hidden", i32), ("reserved", i32)]
+
+
+class LstmGradProblem(C.Structure):
+    _fields_ = [("dw_ih_g", vp), ("dw_hh_g", vp), ("db_g", vp), ("dw_ih", vp), ("dw_hh", vp), ("db_ih", vp),
+                ("db_hh", vp), ("input_size", i32), ("hidden", i32)]
 
 # (name, restype, argtypes)
 _SIGNATURES = [
@@ -92,6 +110,10 @@ _SIGNATURES = [
     ("ppo_adv_normalize", C.c_int, [f32p, i64, f32p, i64, i64, C.c_float, C.c_void_p, C.c_size_t, C.c_void_p]),
     ("ppo_gather_rows", C.c_int, [C.c_void_p, i64, i64, C.POINTER(GatherSegment), i32, f32p, i64, C.c_void_p]),
     ("ppo_linear_fwd", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, C.c_void_p]),
+    ("ppo_lstm_pack", C.c_int, [C.POINTER(LstmPackProblem), i32, C.c_void_p]),
+    ("ppo_lstm_seq_fwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p]),
+    ("ppo_lstm_seq_bwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p]),
+    ("ppo_lstm_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
     ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),
     ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, C.c_void_p, C.c_size_t,
                                     C.c_void_p]),

@@ -24,546 +24,10 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "common.hpp"
+#include "gemm_core.hpp"
 
 namespace ppo {
 namespace {
-
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-enum Epilogue : int { EPI_BIAS = 0, EPI_BIAS_ELU = 1, EPI_ELU_GRAD = 2, EPI_STORE = 3, EPI_PARTIAL = 4 };
-
-struct Problem {
-  const float* A;
-  const float* B;
-  float* C;
-  float* C2;
-  const float* vec;  // bias [N]
-  const float* aux;  // ELU'-source z_prev [M, N]
-  double* colsum;    // [splits, M] sums of A over each split's k range (fp64: bias grads cancel heavily)
-  int64_t lda, ldb, ldc, ldc2, ldaux;
-  int64_t partial_stride;  // floats between split partials of C
-  int32_t M, N, K;
-  int32_t tiles_m, tiles_n, splits, k_chunk;
-  int32_t block_begin;
-  int32_t c_vec;            // NT epilogue: C (and C2 / aux when used) allow 16-byte accesses
-  int32_t elu_from_output;  // input-grad: aux holds h = elu(z) (ELU' = 1 if h > 0 else h + 1), else z
-};
-
-struct Group {
-  Problem p[PPO_MAX_LINEAR_PROBLEMS];
-  int32_t count;
-  int32_t xcd_remap;  // 1: permute block ids so each XCD gets a contiguous range of tiles
-};
-
-constexpr int kThreads = 256;
-constexpr int kXcds = 8;
-
-// Blocks are dispatched round-robin over the XCDs; renumber them so that each XCD receives a contiguous range of
-// logical tiles (a bijection of [0, n)).
-__device__ inline int xcd_remap(int b, int n) {
-  const int q = n / kXcds, r = n % kXcds;
-  const int xcd = b % kXcds, slot = b / kXcds;
-  return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-}
-
-struct TileCoord {
-  int pi, split, tm, tn;
-};
-
-__device__ inline TileCoord locate(const Group& g) {
-  const int b = g.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
-  int pi = 0;
-#pragma unroll
-  for (int i = 1; i < PPO_MAX_LINEAR_PROBLEMS; ++i) {
-    if (i < g.count && b >= g.p[i].block_begin) pi = i;
-  }
-  const Problem& P = g.p[pi];
-  const int local = b - P.block_begin;
-  const int tiles_mn = P.tiles_m * P.tiles_n;
-  TileCoord t;
-  t.pi = pi;
-  t.split = local / tiles_mn;
-  const int r = local - t.split * tiles_mn;
-  t.tm = r / P.tiles_n;
-  t.tn = r - t.tm * P.tiles_n;
-  return t;
-}
-
-// Direct global->LDS copy: every lane of the wave moves `bytes` (16 or 4) from its own global address to
-// lds_wave + lane * bytes.  lds_wave must be wave-uniform.
-template <int BYTES>
-__device__ __forceinline__ void dma(const float* src, float* lds_wave) {
-  static_assert(BYTES == 16 || BYTES == 4, "16- or 4-byte direct loads");
-  if constexpr (BYTES == 16) {
-    __builtin_amdgcn_global_load_lds(src, lds_wave, 16, 0, 0);
-  } else {
-    __builtin_amdgcn_global_load_lds(src, lds_wave, 4, 0, 0);
-  }
-}
-
-// Waits until at most N of this wave's vector-memory operations are outstanding.  The LDS-direct loads count here
-// (and are not tracked by the compiler as LDS writes: hence the memory clobber).  Loads complete in issue order.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0, "vmcnt");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");
-}
-
-// Workgroup barrier of the LDS ring: this wave's LDS writes are complete and the compiler moves no memory access
-// across it.  Unlike __syncthreads(), whose workgroup release fence also drains every outstanding global load, it
-// leaves the prefetched slabs in flight; their arrival is awaited explicitly with wait_slab().
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// Ring of S LDS stages with prefetch distance S - 1: before computing slab kt a wave waits for its own loads of
-// slab kt while the `later` (<= S - 2) slabs issued after it may stay in flight; L = loads per wave per slab.
-// A cap of 63 outstanding only makes the wait stricter (loads retire in order).
-template <int L, int S>
-__device__ __forceinline__ void wait_slab(int later) {
-  if constexpr (S >= 4) {
-    if (later >= 2) {
-      wait_vmcnt<2 * L>();
-      return;
-    }
-  }
-  if constexpr (S >= 3) {
-    if (later >= 1) {
-      wait_vmcnt<L>();
-      return;
-    }
-  }
-  wait_vmcnt<0>();
-}
-
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
-
-// ------------------------------------------------------------------------------------------------------------------
-// NT: operands stored [x][k] (k contiguous); LDS tile [BX][BK] with swizzled 16-byte chunks.
-// ------------------------------------------------------------------------------------------------------------------
-
-// Physical chunk of logical chunk c in LDS row `row` is c ^ swz(row).  gfx950's LDS serves a ds_read_b128 16 lanes
-// (16 x 16 bytes = all 64 banks) at a time; those lanes read one logical chunk of 16 consecutive rows, which the
-// swizzle spreads over 16 distinct 16-byte bank groups (rows sharing a 256-byte window get different chunks).
-template <int BK>
-__device__ __forceinline__ int nt_swz(int row) {
-  constexpr int CPR = BK / 4;
-  static_assert(CPR == 4 || CPR == 8 || CPR == 16, "BK must be 16, 32 or 64");
-  return CPR == 16 ? (row & 15) : CPR == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
-}
-
-// Direct loads of one NT operand: one full k-slab [x0, x0 + BX) x [k0, k0 + BK) per call, rows >= X clamped to X - 1.
-// Each lane's byte offsets from the slab's first column are fixed for the whole k loop, so a slab costs one
-// uniform (scalar) base pointer and one global_load_lds per instruction.  Wave w issues instructions w, w+4, ...
-template <int BX, int BK, bool W16>
-struct NtLoader {
-  static constexpr int CPR = BK / 4;
-  static constexpr int NQ = W16 ? BX * BK / 256 : BX * BK / 64;
-  static constexpr int PER = NQ / 4;
-  static_assert(NQ % 4 == 0, "every wave must issue the same number of loads per slab");
-  uint32_t off[PER];
-
-  __device__ __forceinline__ void init(int64_t ld, int x0, int X, int wave, int lane) {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int q = 4 * j + wave;
-      int row, col;
-      if constexpr (W16) {
-        row = q * (64 / CPR) + lane / CPR;
-        col = 4 * ((lane % CPR) ^ nt_swz<BK>(row));
-      } else {
-        row = q * (64 / BK) + lane / BK;
-        const int f = lane % BK;
-        col = 4 * ((f >> 2) ^ nt_swz<BK>(row)) + (f & 3);
-      }
-      const int64_t gx = min(x0 + row, X - 1);
-      off[j] = static_cast<uint32_t>((gx * ld + col) * 4);
-    }
-  }
-  // base: the operand's element (0, k0), wave-uniform.
-  __device__ __forceinline__ void issue(const float* base, float* lds_op, int wave) const {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const float* src = reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off[j]);
-      if constexpr (W16) {
-        dma<16>(src, lds_op + (4 * j + wave) * 256);
-      } else {
-        dma<4>(src, lds_op + (4 * j + wave) * 64);
-      }
-    }
-  }
-};
-
-// The partial last k-slab of an NT operand: masked element loads (k >= K -> 0), swizzled float4 LDS stores.
-template <int BX, int BK>
-__device__ __forceinline__ void nt_masked(const float* __restrict__ base, int64_t ld, int x0, int X, int k0, int K,
-                                          float* lds_op) {
-  constexpr int CPR = BK / 4;
-  for (int q = threadIdx.x; q < BX * CPR; q += kThreads) {
-    const int row = q / CPR, c = q % CPR;
-    const float* src = base + static_cast<int64_t>(min(x0 + row, X - 1)) * ld;
-    f32x4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int k = k0 + 4 * c + e;
-      v[e] = k < K ? src[k] : 0.0f;
-    }
-    *reinterpret_cast<f32x4*>(lds_op + row * BK + 4 * (c ^ nt_swz<BK>(row))) = v;
-  }
-}
-
-// OCC: waves per SIMD the register allocation must allow (blocks of 4 waves per CU), traded against spills.
-template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16, int EPI>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_kernel(
-    const Group g) {
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int STAGE = (BM + BN) * BK;
-  static_assert(TM >= 1 && TN >= 1, "tile too small");
-  static_assert(S >= 2 && S <= 4, "2..4 LDS stages");
-  constexpr int L = NtLoader<BM, BK, A16>::PER + NtLoader<BN, BK, B16>::PER;
-  __shared__ __align__(16) float lds[S * STAGE];
-
-  const TileCoord tc = locate(g);
-  const Problem& P = g.p[tc.pi];
-  // problem fields as values: the loop's compiler barriers would otherwise re-read them from the argument block
-  const float* const A = P.A;
-  const float* const B = P.B;
-  const int64_t lda = P.lda, ldb = P.ldb;
-  const int row0 = tc.tm * BM, col0 = tc.tn * BN;
-  const int M = P.M, N = P.N, K = P.K;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int wm = wave >> 1, wn = wave & 1;
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-  NtLoader<BM, BK, A16> la;
-  NtLoader<BN, BK, B16> lb;
-  la.init(lda, row0, M, wave, lane);
-  lb.init(ldb, col0, N, wave, lane);
-  const int nfull = K / BK;
-  const int nk = (K + BK - 1) / BK;
-  auto issue = [&](int kt, int stage) {
-    float* st = lds + stage * STAGE;
-    const int k0 = kt * BK;
-    if (kt < nfull) {
-      la.issue(A + k0, st, wave);
-      lb.issue(B + k0, st + BM * BK, wave);
-    } else {
-      nt_masked<BM, BK>(A, lda, row0, M, k0, K, st);
-      nt_masked<BN, BK>(B, ldb, col0, N, k0, K, st + BM * BK);
-    }
-  };
-#pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < nk) issue(s, s);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_slab<L, S>(min(S - 2, nk - 1 - kt));
-    lds_barrier();  // slab kt is in LDS for every wave; every wave is done with slab kt-1's stage
-    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
-    const float* As = lds + (kt % S) * STAGE;
-    const float* Bs = As + BM * BK;
-    // k-groups of 4 MFMA steps; the fragments of group g + 1 are read before the MFMAs of group g issue
-    constexpr int G = BK / 8;
-    f32x4 fa[2][TM], fb[2][TN];
-    auto load_group = [&](int buf, int gi) {
-      const int c = 2 * gi + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WM + 32 * i + (lane & 31);
-        fa[buf][i] = *reinterpret_cast<const f32x4*>(As + r * BK + 4 * (c ^ nt_swz<BK>(r)));
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * WN + 32 * j + (lane & 31);
-        fb[buf][j] = *reinterpret_cast<const f32x4*>(Bs + r * BK + 4 * (c ^ nt_swz<BK>(r)));
-      }
-    };
-    load_group(0, 0);
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-      if (gi + 1 < G) load_group((gi + 1) & 1, gi + 1);
-      // scheduling fences: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            // weights (B) as the MFMA's A operand: the accumulator holds the 32 x 32 tile of C transposed
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[gi & 1][j][s], fa[gi & 1][i][s], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-
-  // Epilogue, one 32 x 32 accumulator tile at a time through a private 32 x 36-float LDS patch per wave (the ring is
-  // free once every wave is past its last slab).  Element v of lane l of acc[i][j] is row l%32 and column
-  // 8*(v/4) + 4*(l/32) + v%4 of the tile, so a lane writes 4 float4 runs into the patch; it then reads back 16-byte
-  // chunks in row order (8 lanes per 128-byte row) and finishes them there: +bias / ELU, or * ELU'(z_prev), with
-  // every global access a fully used 128-byte row segment (16-byte vectors when P.c_vec, elements at the N edge).
-  static_assert(4 * 32 * 36 <= S * STAGE, "epilogue patches must fit in the LDS ring");
-  constexpr int PS = 36;  // patch row stride: 144 bytes spreads the 16 rows of a ds_write_b128 over all banks
-  lds_barrier();
-  float* patch = lds + wave * 32 * PS;
-  const int h = lane >> 5;
-  const int pr = lane >> 3, pc = 4 * (lane & 7);  // read-back: row pr (+8 per step), columns pc .. pc + 3
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        f32x4 x = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-        *reinterpret_cast<f32x4*>(patch + (lane & 31) * PS + 8 * q + 4 * h) = x;
-      }
-      const int n = col0 + wn * WN + j * 32 + pc;
-      const bool n_in = n < N;
-      const bool full = P.c_vec && n + 3 < N;
-      f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
-      if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && n_in) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bias[e] = n + e < N ? P.vec[n + e] : 0.0f;
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int r = pr + 8 * rr;
-        const f32x4 x = *reinterpret_cast<const f32x4*>(patch + r * PS + pc);
-        const int m = row0 + wm * WM + i * 32 + r;
-        if (m >= M || !n_in) continue;
-        const int64_t mm = m;
-        f32x4 o, o2;
-        if (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[e] = x[e] + bias[e];
-            o2[e] = o[e] > 0.0f ? o[e] : expm1f(o[e]);
-          }
-        } else if (EPI == EPI_ELU_GRAD) {
-          f32x4 zp;
-          if (full) {
-            zp = *reinterpret_cast<const f32x4*>(P.aux + mm * P.ldaux + n);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) zp[e] = n + e < N ? P.aux[mm * P.ldaux + n + e] : 0.0f;
-          }
-          if (P.elu_from_output) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * (zp[e] + 1.0f);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * expf(zp[e]);
-          }
-        } else {
-          o = x;
-        }
-        // with ELU either output may be absent (h alone feeds the next layer and the input-grad)
-        const bool st_c = EPI != EPI_BIAS_ELU || P.C != nullptr;
-        const bool st_c2 = EPI == EPI_BIAS_ELU && P.C2 != nullptr;
-        if (full) {
-          if (st_c) *reinterpret_cast<f32x4*>(P.C + mm * P.ldc + n) = o;
-          if (st_c2) *reinterpret_cast<f32x4*>(P.C2 + mm * P.ldc2 + n) = o2;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (n + e < N) {
-              if (st_c) P.C[mm * P.ldc + n + e] = o[e];
-              if (st_c2) P.C2[mm * P.ldc2 + n + e] = o2[e];
-            }
-          }
-        }
-      }
-    }
-  }
-}
-
-// ------------------------------------------------------------------------------------------------------------------
-// TN (weight-grad): operands stored [k][x] (x contiguous); LDS tile [BK][BX], unpadded.
-// ------------------------------------------------------------------------------------------------------------------
-
-// Direct loads of one TN operand: one full k-slab, rows [k0, k0 + BK) x columns [x0, x0 + BX), per call; columns
-// past X read the last in-bounds chunk / element instead (the 16-byte form needs ld >= X rounded up to 4, which a
-// leading dimension that is a multiple of 4 guarantees).  Per-lane byte offsets from the slab's first row are fixed.
-template <int BX, int BK, bool W16>
-struct TnLoader {
-  static constexpr int NQ = W16 ? BK * BX / 256 : BK * BX / 64;
-  static constexpr int PER = NQ / 4;
-  static_assert(NQ % 4 == 0, "every wave must issue the same number of loads per slab");
-  uint32_t off[PER];
-
-  __device__ __forceinline__ void init(int64_t ld, int x0, int X, int wave, int lane) {
-    const int xlast = W16 ? ((X - 1) >> 2) << 2 : X - 1;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int q = 4 * j + wave;
-      const int flat = W16 ? 4 * (64 * q + lane) : 64 * q + lane;
-      const int row = flat / BX, x = flat % BX;
-      const int64_t gx = min(x0 + x, xlast);
-      off[j] = static_cast<uint32_t>((row * ld + gx) * 4);
-    }
-  }
-  // base: the operand's row k0, wave-uniform.
-  __device__ __forceinline__ void issue(const float* base, float* lds_op, int wave) const {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const float* src = reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off[j]);
-      if constexpr (W16) {
-        dma<16>(src, lds_op + (4 * j + wave) * 256);
-      } else {
-        dma<4>(src, lds_op + (4 * j + wave) * 64);
-      }
-    }
-  }
-};
-
-template <int BX, int BK>
-__device__ __forceinline__ void tn_masked(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
-                                          int k_end, float* lds_op) {
-  for (int q = threadIdx.x; q < BK * BX; q += kThreads) {
-    const int row = q / BX, x = q % BX;
-    const int k = k0 + row;
-    lds_op[q] = k < k_end ? base[static_cast<int64_t>(k) * ld + min(x0 + x, X - 1)] : 0.0f;
-  }
-}
-
-template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_kernel(
-    const Group g) {
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int STAGE = BK * (BM + BN);
-  static_assert(TM == 2 && TN == 2, "TN kernel: 2 x 2 interleaved MFMA tiles per wave");
-  static_assert(kThreads % BM == 0 && BK % 8 == 0, "TN column sums split the slab over kThreads / BM threads");
-  static_assert(S >= 2 && S <= 4, "2..4 LDS stages");
-  constexpr int L = TnLoader<BM, BK, A16>::PER + TnLoader<BN, BK, B16>::PER;
-  __shared__ __align__(16) float lds[S * STAGE];
-
-  const TileCoord tc = locate(g);
-  const Problem& P = g.p[tc.pi];
-  // problem fields as values: the loop's compiler barriers would otherwise re-read them from the argument block
-  const float* const A = P.A;
-  const float* const B = P.B;
-  const int64_t lda = P.lda, ldb = P.ldb;
-  const int row0 = tc.tm * BM, col0 = tc.tn * BN;
-  const int M = P.M, N = P.N;
-  const int k_begin = tc.split * P.k_chunk;
-  const int k_end = min(P.K, k_begin + P.k_chunk);
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int wm = wave >> 1, wn = wave & 1;
-  const int h = lane >> 5, sg = lane & 31;
-
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-
-  const bool do_colsum = P.colsum != nullptr && tc.tn == 0;
-  double colsum_acc[4] = {0.0, 0.0, 0.0, 0.0};
-  const int span = max(k_end - k_begin, 0);
-  const int nfull = span / BK;
-  const int nk = (span + BK - 1) / BK;
-  TnLoader<BM, BK, A16> la;
-  TnLoader<BN, BK, B16> lb;
-  la.init(lda, row0, M, wave, lane);
-  lb.init(ldb, col0, N, wave, lane);
-  auto issue = [&](int kt, int stage) {
-    float* st = lds + stage * STAGE;
-    const int k0 = k_begin + kt * BK;
-    if (kt < nfull) {
-      la.issue(A + k0 * lda, st, wave);
-      lb.issue(B + k0 * ldb, st + BK * BM, wave);
-    } else {
-      tn_masked<BM, BK>(A, lda, row0, M, k0, k_end, st);
-      tn_masked<BN, BK>(B, ldb, col0, N, k0, k_end, st + BK * BM);
-    }
-  };
-#pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < nk) issue(s, s);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_slab<L, S>(min(S - 2, nk - 1 - kt));
-    lds_barrier();
-    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
-    const float* As = lds + (kt % S) * STAGE;
-    const float* Bs = As + BK * BM;
-    if (do_colsum) {  // column c = tid % BM, rows of this thread's half of the slab, 4 independent chains
-      const int c = tid % BM, k0 = (tid / BM) * (BK / 2);
-#pragma unroll
-      for (int kk = 0; kk < BK / 2; ++kk) colsum_acc[kk & 3] += static_cast<double>(As[(k0 + kk) * BM + c]);
-    }
-    // groups of 4 k-steps (8 rows of k): the fragments of group g + 1 are read before the MFMAs of group g issue
-    constexpr int G = BK / 8;
-    f32x2 fa[2][4], fb[2][4];
-    auto load_group = [&](int buf, int gi) {
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int kk = 8 * gi + 2 * st + h;
-        fa[buf][st] = *reinterpret_cast<const f32x2*>(As + kk * BM + wm * WM + 2 * sg);
-        fb[buf][st] = *reinterpret_cast<const f32x2*>(Bs + kk * BN + wn * WN + 2 * sg);
-      }
-    };
-    load_group(0, 0);
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-      if (gi + 1 < G) load_group((gi + 1) & 1, gi + 1);
-      // scheduling fences: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[gi & 1][st][i], fb[gi & 1][st][j], acc[i][j], 0,
-                                                             0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-
-  // Partial store.  Accumulator row rho = 8*(v/4) + 4*h + v%4 of tile i is m = 2*rho + i (TM == 2) or rho, and
-  // column sg of tile j is n = 2*sg + j (TN == 2) or sg.
-  float* Cs = P.C + static_cast<int64_t>(tc.split) * P.partial_stride;
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int rho = 8 * (v >> 2) + 4 * h + (v & 3);
-      const int m = row0 + wm * WM + (TM == 2 ? 2 * rho + i : rho);
-      if (m >= M) continue;
-      float* crow = Cs + static_cast<int64_t>(m) * P.ldc;
-      if constexpr (TN == 2) {
-        const int n = col0 + wn * WN + 2 * sg;
-        if (n + 1 < N) {
-          f32x2 o = {acc[i][0][v], acc[i][1][v]};
-          *reinterpret_cast<f32x2*>(crow + n) = o;
-        } else if (n < N) {
-          crow[n] = acc[i][0][v];
-        }
-      } else {
-        const int n = col0 + wn * WN + sg;
-        if (n < N) crow[n] = acc[i][0][v];
-      }
-    }
-  }
-  if (do_colsum) {  // the two halves of each column, combined in a fixed order through the (now free) LDS ring
-    double* part = reinterpret_cast<double*>(lds);
-    const double mine = (colsum_acc[0] + colsum_acc[1]) + (colsum_acc[2] + colsum_acc[3]);
-    lds_barrier();
-    if (tid >= BM) part[tid - BM] = mine;
-    lds_barrier();
-    if (tid < BM && row0 + tid < M) P.colsum[static_cast<int64_t>(tc.split) * M + row0 + tid] = mine + part[tid];
-  }
-}
 
 // Fixed-order reduction of split-K weight-grad partials: dw = sum_s partial[s], db = sum_s colsum[s].
 struct ReduceItem {
@@ -637,128 +101,6 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TransposeGroup g) 
   for (int r = ty; r < 32; r += 8) {
     const int i = ti * 32 + r, o = to * 32 + tx;
     if (i < T.in && o < T.ldt) T.wt[static_cast<int64_t>(i) * T.ldt + o] = tile[tx][r];
-  }
-}
-
-// 16-byte direct loads need a 16-byte aligned base and a leading dimension that is a multiple of 4.
-bool w16_ok(const float* base, int64_t ld) { return (reinterpret_cast<uintptr_t>(base) % 16 == 0) && ld % 4 == 0; }
-
-int assign_blocks(Group& g, int count, int bm, int bn, const char* name, int& blocks) {
-  blocks = 0;
-  for (int i = 0; i < count; ++i) {
-    Problem& p = g.p[i];
-    p.tiles_m = static_cast<int>(ceil_div(p.M, bm));
-    p.tiles_n = static_cast<int>(ceil_div(p.N, bn));
-    p.block_begin = blocks;
-    const int64_t nb = static_cast<int64_t>(p.tiles_m) * p.tiles_n * p.splits;
-    if (blocks + nb > INT32_MAX) return fail(PPO_EUNSUPPORTED, "%s: grid too large", name);
-    blocks += static_cast<int>(nb);
-  }
-  g.count = count;
-  g.xcd_remap = std::getenv("PPO_HIP_NO_XCD_REMAP") == nullptr;
-  for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) g.p[i].block_begin = INT32_MAX;
-  return PPO_OK;
-}
-
-template <int BM, int BN, int BK, int S, int OCC, int EPI>
-int launch_nt(Group& g, int count, hipStream_t s, const char* name) {
-  int blocks;
-  if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
-  if (blocks == 0) return PPO_OK;
-  bool a16 = true, b16 = true;
-  for (int i = 0; i < count; ++i) {
-    a16 = a16 && w16_ok(g.p[i].A, g.p[i].lda);
-    b16 = b16 && w16_ok(g.p[i].B, g.p[i].ldb);
-  }
-  if (a16 && b16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (a16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (b16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, false, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, false, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  }
-  return check_launch(name);
-}
-
-template <int BM, int BN, int BK, int S, int OCC>
-int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
-  int blocks;
-  if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
-  if (blocks == 0) return PPO_OK;
-  bool a16 = true, b16 = true;
-  for (int i = 0; i < count; ++i) {
-    a16 = a16 && w16_ok(g.p[i].A, g.p[i].lda);
-    b16 = b16 && w16_ok(g.p[i].B, g.p[i].ldb);
-  }
-  if (a16 && b16) {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, true, true>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (a16) {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, true, false>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (b16) {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, false, true>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else {
-    hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, false, false>), dim3(blocks), dim3(kThreads), 0, s, g);
-  }
-  return check_launch(name);
-}
-
-// NT tile of a launch (BM x BN, k-slab depth, LDS stages, waves per SIMD): "PPO_HIP_GEMM_TILE" (e.g.
-// "128x128k16s2o3") overrides the size-based choice (tuning aid).
-enum Tile {
-  T128x128k16s2o3, T128x128k16s3o3, T128x128k16s2o2, T128x128k32s2o2, T128x64k16s4o4, T128x64k32s2o4,
-  T64x64k32s2o4, T64x64k32s2o5, T192x128k16s2o2, T128x128k64s2o1, T128x128k32s2o1, T256x128k32s2o1,
-  T128x64k64s2o2
-};
-
-Tile pick_tile(Tile dflt) {
-  const char* e = std::getenv("PPO_HIP_GEMM_TILE");
-  if (e == nullptr) return dflt;
-  static const struct {
-    const char* name;
-    Tile t;
-  } kTiles[] = {{"128x128k16s2o3", T128x128k16s2o3}, {"128x128k16s3o3", T128x128k16s3o3},
-                {"128x128k16s2o2", T128x128k16s2o2}, {"128x128k32s2o2", T128x128k32s2o2},
-                {"128x64k16s4o4", T128x64k16s4o4},   {"128x64k32s2o4", T128x64k32s2o4},
-                {"64x64k32s2o4", T64x64k32s2o4},     {"64x64k32s2o5", T64x64k32s2o5},
-                {"192x128k16s2o2", T192x128k16s2o2}, {"128x128k64s2o1", T128x128k64s2o1},
-                {"128x128k32s2o1", T128x128k32s2o1}, {"256x128k32s2o1", T256x128k32s2o1},
-                {"128x64k64s2o2", T128x64k64s2o2}};
-  for (const auto& k : kTiles)
-    if (!std::strcmp(e, k.name)) return k.t;
-  return dflt;
-}
-
-template <int EPI>
-int launch_nt_tile(Tile t, Group& g, int count, hipStream_t s, const char* name) {
-  switch (t) {
-    case T128x128k16s3o3:
-      return launch_nt<128, 128, 16, 3, 3, EPI>(g, count, s, name);
-    case T128x128k16s2o2:
-      return launch_nt<128, 128, 16, 2, 2, EPI>(g, count, s, name);
-    case T128x128k32s2o2:
-      return launch_nt<128, 128, 32, 2, 2, EPI>(g, count, s, name);
-    case T128x64k16s4o4:
-      return launch_nt<128, 64, 16, 4, 4, EPI>(g, count, s, name);
-    case T128x64k32s2o4:
-      return launch_nt<128, 64, 32, 2, 4, EPI>(g, count, s, name);
-    case T64x64k32s2o4:
-      return launch_nt<64, 64, 32, 2, 4, EPI>(g, count, s, name);
-    case T64x64k32s2o5:
-      return launch_nt<64, 64, 32, 2, 5, EPI>(g, count, s, name);
-    case T192x128k16s2o2:
-      return launch_nt<192, 128, 16, 2, 2, EPI>(g, count, s, name);
-    case T128x128k64s2o1:
-      return launch_nt<128, 128, 64, 2, 1, EPI>(g, count, s, name);
-    case T128x128k32s2o1:
-      return launch_nt<128, 128, 32, 2, 1, EPI>(g, count, s, name);
-    case T256x128k32s2o1:
-      return launch_nt<256, 128, 32, 2, 1, EPI>(g, count, s, name);
-    case T128x64k64s2o2:
-      return launch_nt<128, 64, 64, 2, 2, EPI>(g, count, s, name);
-    default:
-      return launch_nt<128, 128, 16, 2, 3, EPI>(g, count, s, name);
   }
 }
 

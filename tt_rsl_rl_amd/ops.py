@@ -328,3 +328,73 @@ def C_ref(struct):
     import ctypes
 
     return ctypes.byref(struct)
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# A15 LSTM
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+class LstmPacked:
+    """Gate-interleaved copies of one nn.LSTM layer's weights (row 4u + q = gate q of unit u)."""
+
+    def __init__(self, input_size: int, hidden: int, device) -> None:
+        H, D = hidden, input_size
+        self.input_size, self.hidden = D, H
+        self.w_ih_g = torch.empty(4 * H, D, device=device)
+        self.w_hh_g = torch.empty(4 * H, H, device=device)
+        self.w_hh_gt = torch.empty(H, 4 * H, device=device)
+        self.b_g = torch.empty(4 * H, device=device)
+
+
+def lstm_pack(items: list[tuple]) -> None:
+    """items: (w_ih [4H, D], w_hh [4H, H], b_ih [4H], b_hh [4H], LstmPacked)."""
+    probs = []
+    for w_ih, w_hh, b_ih, b_hh, pk in items:
+        _dev(w_ih, w_hh, b_ih, b_hh)
+        for t in (w_ih, w_hh, b_ih, b_hh):
+            if not t.is_contiguous():
+                raise ValueError("lstm_pack: weights must be contiguous")
+        probs.append(L.LstmPackProblem(w_ih.data_ptr(), w_hh.data_ptr(), b_ih.data_ptr(), b_hh.data_ptr(),
+                                       pk.w_ih_g.data_ptr(), pk.w_hh_g.data_ptr(), pk.w_hh_gt.data_ptr(),
+                                       pk.b_g.data_ptr(), pk.input_size, pk.hidden))
+    L.call("ppo_lstm_pack", L.array(L.LstmPackProblem, probs), len(probs), _stream())
+
+
+def _seq_problem(q: dict) -> "L.LstmSeqProblem":
+    H = q["hidden"]
+    gx, h0, c0, h = q["gx"], q["h0"], q["c0"], q["h"]
+    keep = q["keep"]
+    _dev(gx, h0, c0, h, keep, q["hs"], q["c"], q["gates"], q.get("dh"), q.get("dgates"), q.get("dc"))
+    if h0.stride(0) != c0.stride(0):
+        raise ValueError("lstm: h0 and c0 must share a leading dimension")
+    dh = q.get("dh")
+    return L.LstmSeqProblem(q["packed"].w_hh_g.data_ptr(), q["packed"].w_hh_gt.data_ptr(), gx.data_ptr(),
+                            _row_major(gx, "gx"), h0.data_ptr(), c0.data_ptr(), _row_major(h0, "h0"), keep.data_ptr(),
+                            keep.stride(0), h.data_ptr(), _row_major(h, "h"), q["hs"].data_ptr(), q["c"].data_ptr(),
+                            q["gates"].data_ptr(), _ptr(dh), _row_major(dh, "dh") if dh is not None else 0,
+                            _ptr(q.get("dgates")), _ptr(q.get("dc")), H, 0)
+
+
+def lstm_seq_fwd(problems: list[dict], steps: int, envs: int) -> None:
+    """problems: dicts with packed (LstmPacked), hidden, gx [T*E, 4H], h0 / c0 [E, H], keep [T*E] (stride = row
+    step), h [T*E, H], hs [(T+1)*E, H], c [T*E, H], gates [T*E, 4H]."""
+    arr = L.array(L.LstmSeqProblem, [_seq_problem(q) for q in problems])
+    L.call("ppo_lstm_seq_fwd", arr, len(problems), steps, envs, _stream())
+
+
+def lstm_seq_bwd(problems: list[dict], steps: int, envs: int) -> None:
+    """As lstm_seq_fwd's problems plus dh [T*E, H], dgates [T*E, 4H], dc [E, H] (scratch)."""
+    arr = L.array(L.LstmSeqProblem, [_seq_problem(q) for q in problems])
+    L.call("ppo_lstm_seq_bwd", arr, len(problems), steps, envs, _stream())
+
+
+def lstm_unpack_grads(items: list[tuple]) -> None:
+    """items: (dw_ih_g [4H, D], dw_hh_g [4H, H], db_g [4H], dw_ih, dw_hh, db_ih, db_hh (torch layout views))."""
+    probs = []
+    for dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh in items:
+        _dev(dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh)
+        H = dw_hh.shape[1]
+        probs.append(L.LstmGradProblem(dw_ih_g.data_ptr(), dw_hh_g.data_ptr(), db_g.data_ptr(), dw_ih.data_ptr(),
+                                       dw_hh.data_ptr(), db_ih.data_ptr(), db_hh.data_ptr(), dw_ih.shape[1], H))
+    L.call("ppo_lstm_unpack_grads", L.array(L.LstmGradProblem, probs), len(probs), _stream())

@@ -89,9 +89,24 @@ class RolloutStorage:
                 for p in transition.distribution_params)
         for i, p in enumerate(transition.distribution_params):
             self.distribution_params[i][s].copy_(p)
-        if transition.hidden_states not in ((None, None), None):
-            raise NotImplementedError("recurrent hidden states are not supported by the MLP storage")
+        self._save_hidden_states(transition.hidden_states)
         self.step += 1
+
+    def _save_hidden_states(self, hidden_states) -> None:
+        """rollout_storage.py:333-359: the recurrent models' state before each step's forward, as saved_hidden_state_a /
+        _c = [h, c] each [T, num_layers, N, H] (zero where a model had no state yet)."""
+        if hidden_states is None or hidden_states == (None, None):
+            return
+        T = self.num_transitions_per_env
+        for side, hs in (("a", hidden_states[0]), ("c", hidden_states[1])):
+            if hs is None:
+                continue
+            hs = hs if isinstance(hs, tuple) else (hs,)
+            name = f"saved_hidden_state_{side}"
+            if getattr(self, name) is None:
+                setattr(self, name, [torch.zeros(T, *h.shape, device=self.device) for h in hs])
+            for buf, h in zip(getattr(self, name), hs):
+                buf[self.step].copy_(h)
 
     def clear(self) -> None:
         self.step = 0
@@ -123,4 +138,6 @@ class RolloutStorage:
                                            old_distribution_params=tuple(p[idx] for p in params))
 
     def recurrent_mini_batch_generator(self, num_mini_batches: int, num_epochs: int = 8):
-        raise NotImplementedError("recurrent mini-batches are not implemented on the MLP storage")
+        """Not provided: the update evaluates upstream's padded trajectories in the equivalent masked per-env form on
+        the GPU (one sequence per env from saved_hidden_state_*[0], state zeroed after every done)."""
+        raise NotImplementedError("the recurrent update does not materialise padded trajectories")
