@@ -99,13 +99,19 @@ def make_oracle(workload: dict, seed: int = 0, **alg_overrides) -> PPO:
     return construct_algorithm(zero_obs(workload), workload["num_envs"], workload["num_actions"], cfg)
 
 
-def generate(workload: dict, seed: int = 0, **alg_overrides) -> tuple[PPO, Rollout]:
-    """Build the oracle algorithm with ``seed`` and fill its storage with one synthetic rollout."""
+def generate(workload: dict, seed: int = 0, carry_state: bool = False, **alg_overrides) -> tuple[PPO, Rollout]:
+    """Build the oracle algorithm with ``seed`` and fill its storage with one synthetic rollout.  With
+    ``carry_state`` recurrent models start the rollout from a random hidden state (as a rollout after the first
+    does), instead of nn.LSTM's zero default."""
     alg = make_oracle(workload, seed, **alg_overrides)
     alg.train_mode()
     roll = Rollout(init_state={"actor": copy.deepcopy(alg.actor.state_dict()),
                                "critic": copy.deepcopy(alg.critic.state_dict())})
     n = workload["num_envs"]
+    if carry_state and "rnn" in workload:
+        H = workload["rnn"]["rnn_hidden_dim"]
+        for model in (alg.actor, alg.critic):
+            model.reset(hidden_state=tuple(0.5 * torch.randn(1, n, H) for _ in range(2)))
     with torch.inference_mode():
         obs = sample_obs(workload)
         for _ in range(workload["steps"]):

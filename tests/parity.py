@@ -32,10 +32,10 @@ def make_hip(workload: dict, seed: int = 0, device: str = "cuda", **alg_override
     return alg
 
 
-def make_pair(workload: dict, seed: int = 0, **alg_overrides):
+def make_pair(workload: dict, seed: int = 0, carry_state: bool = False, **alg_overrides):
     """Oracle with a generated rollout + the HIP plugin with identical weights and the same stored rollout.
     Both have their returns / advantages computed from the same bootstrap values."""
-    ora, roll = R.generate(workload, seed, **alg_overrides)
+    ora, roll = R.generate(workload, seed, carry_state=carry_state, **alg_overrides)
     hip = make_hip(workload, seed, **alg_overrides)
     with torch.no_grad():
         hip.actor.load_state_dict(roll.init_state["actor"])

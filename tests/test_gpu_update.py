@@ -47,6 +47,13 @@ CLIP_MARGIN = 1e-4
 # a ratio this close to 1 +- clip can take either surrogate branch under fp32 rounding of a ~30-magnitude log-prob
 AMBIGUOUS = 1e-5
 
+def _lstm(num_envs: int, steps: int, hidden: int, hidden_dims: list[int], **kw) -> dict:
+    w = R.scaled(R.WORKLOADS["lstm256"], num_envs=num_envs, steps=steps, hidden_dims=hidden_dims)
+    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=hidden)
+    w.update(kw)
+    return w
+
+
 CASES = {
     "humanoid_1k": (R.scaled(R.WORKLOADS["humanoid"], num_envs=1024), {}),
     "flat48_1k": (R.scaled(R.WORKLOADS["flat48"], num_envs=1024), {}),
@@ -55,7 +62,22 @@ CASES = {
                                  {"normalize_advantage_per_mini_batch": True, "num_mini_batches": 3}),
     "flat48_unclipped_fixed": (R.scaled(R.WORKLOADS["flat48"], num_envs=200, steps=5, hidden_dims=[128, 64, 32]),
                                {"use_clipped_value_loss": False, "schedule": "fixed", "num_learning_epochs": 2}),
+    # recurrent (LSTM before the MLP head): env-slice mini-batches, sequences started from the saved states
+    "lstm256_512": (_lstm(512, 24, 256, [256, 128]), {}),
+    "lstm64_norm_carry": (_lstm(128, 16, 64, [64, 32], obs_normalization=True), {"carry_state": True}),
+    "lstm32_ragged_permb_fixed": (_lstm(200, 10, 32, [32, 32, 16]),
+                                  {"num_mini_batches": 3, "normalize_advantage_per_mini_batch": True,
+                                   "schedule": "fixed", "use_clipped_value_loss": False, "carry_state": True}),
 }
+
+
+def _table_order(ora, hip) -> torch.Tensor:
+    """Storage row of every packed-table row: the oracle's permutation (feed-forward) or, for the recurrent update,
+    each env slice's rows t-major (what upstream's recurrent generator yields as [T, E] blocks)."""
+    engine = hip._get_engine()
+    if engine.recurrent:
+        return engine.order.cpu()
+    return torch.cat([t["indices"] for t in ora.trace[:ora.num_mini_batches]])
 
 
 def _update_both(name):
@@ -82,7 +104,7 @@ def test_update_matches_oracle(name):
     w, over, ora, hip, ref, out = _update_both(name)
     # permutation / mini-batch rows: the packed table holds storage rows in oracle permutation order
     B = w["num_envs"] * w["steps"]
-    perm = torch.cat([t["indices"] for t in ora.trace[:ora.num_mini_batches]])
+    perm = _table_order(ora, hip)
     lay = hip._engine.layout
     A = w["num_actions"]
     acts = hip._engine.table[:, lay.actions:lay.actions + A].cpu()
@@ -152,7 +174,7 @@ def test_update_steps_teacher_forced(name):
 
     # the GPU side: the update's packed table (same permutation), then one step at a time from the oracle's state
     engine = hip._get_engine()
-    engine.gather(torch.cat([t["indices"] for t in ora.trace[:M]]).to(hip.device))
+    engine.gather(None if engine.recurrent else _table_order(ora, hip).to(hip.device))
     params = list(chain(hip.actor.parameters(), hip.critic.parameters()))
     names = [n for n, _ in chain(ora.actor.named_parameters(), ora.critic.named_parameters())]
     worst, n_amb = 0.0, 0
@@ -163,8 +185,7 @@ def test_update_steps_teacher_forced(name):
                 hip.flat.exp_avg_view(p).copy_(m1.to(hip.device))
                 hip.flat.exp_avg_sq_view(p).copy_(m2.to(hip.device))
         ops.reset_device_state(hip.device_state, a["lr"])
-        i = k % M
-        engine.minibatch(i * B // M, (i + 1) * B // M, a["step"] + 1)
+        engine.minibatch(*engine.minibatch_rows(k % M), a["step"] + 1)
         torch.cuda.synchronize()
         kl, lr, surr, value, ent = engine.trace[:5].tolist()
         t = ora.trace[k]

@@ -12,7 +12,7 @@ import torch
 from oracle import rollout as R
 from tt_rsl_rl_amd import workloads as W
 from tt_rsl_rl_amd.engine import TableLayout
-from tt_rsl_rl_amd.models import MLPModel
+from tt_rsl_rl_amd.models import MLPModel, RNNModel
 from tt_rsl_rl_amd.ppo import PPO, resolve_callable
 
 
@@ -21,17 +21,19 @@ def test_workload_table_matches_the_oracle_copy():
     assert W.ALGORITHM == R.DEFAULT_ALGORITHM
 
 
-@pytest.mark.parametrize("name", ["flat48", "humanoid", "rough235"])
+@pytest.mark.parametrize("name", ["flat48", "humanoid", "rough235", "lstm256"])
 def test_initial_weights_and_state_dict_layout_equal_upstream(name):
-    """Same seed -> same default nn.Linear init as upstream (actor then critic), same keys, same parameter order."""
+    """Same seed -> same default nn.Linear (and nn.LSTM) init as upstream (actor then critic), same keys, same
+    parameter order."""
     w = R.scaled(R.WORKLOADS[name], num_envs=8)
     ora = R.make_oracle(w, seed=3)
     torch.manual_seed(3)
     cfg = W.train_cfg(w)
     obs = R.zero_obs(w)
     kw = lambda c: {k: v for k, v in c.items() if k != "class_name"}
-    actor = MLPModel(obs, cfg["obs_groups"], "actor", w["num_actions"], **kw(cfg["actor"]))
-    critic = MLPModel(obs, cfg["obs_groups"], "critic", 1, **kw(cfg["critic"]))
+    cls = RNNModel if "rnn" in w else MLPModel
+    actor = cls(obs, cfg["obs_groups"], "actor", w["num_actions"], **kw(cfg["actor"]))
+    critic = cls(obs, cfg["obs_groups"], "critic", 1, **kw(cfg["critic"]))
     for mine, ref in ((actor, ora.actor), (critic, ora.critic)):
         sd, rd = mine.state_dict(), ref.state_dict()
         assert list(sd) == list(rd)
@@ -45,8 +47,8 @@ def test_class_resolution_maps_upstream_names():
     assert resolve_callable("rsl_rl.models:MLPModel") is MLPModel
     assert resolve_callable("rsl_rl.algorithms:PPO") is PPO
     assert resolve_callable("tt_rsl_rl_amd.ppo:PPO") is PPO
-    with pytest.raises(NotImplementedError):
-        resolve_callable("RNNModel")
+    assert resolve_callable("RNNModel") is RNNModel
+    assert resolve_callable("rsl_rl.models:RNNModel") is RNNModel
     with pytest.raises(ValueError):
         resolve_callable("NoSuchClass")
 
@@ -74,6 +76,24 @@ def test_unsupported_options_are_rejected_before_touching_the_gpu(kwargs, exc):
         PPO(actor, critic, None, **kwargs)
 
 
+def test_recurrent_options_outside_the_kernels_are_rejected():
+    w = R.scaled(R.WORKLOADS["lstm256"], num_envs=8)
+    obs, groups = R.zero_obs(w), w["obs_groups"]
+    with pytest.raises(NotImplementedError, match="LSTM"):
+        RNNModel(obs, groups, "actor", 12, rnn_type="gru")
+    with pytest.raises(NotImplementedError, match="one layer"):
+        RNNModel(obs, groups, "actor", 12, rnn_num_layers=2)
+    with pytest.raises(NotImplementedError, match="multiple of 4"):
+        RNNModel(obs, groups, "actor", 12, rnn_hidden_dim=30)
+    # a recurrent actor with a feed-forward critic
+    cfg = W.train_cfg(w)
+    kw = lambda c: {k: v for k, v in c.items() if k != "class_name"}
+    actor = RNNModel(obs, groups, "actor", 12, **kw(cfg["actor"]))
+    critic = MLPModel(obs, groups, "critic", 1, hidden_dims=[8])
+    with pytest.raises(NotImplementedError, match="recurrent"):
+        PPO(actor, critic, None, device="cuda")
+
+
 def test_non_elu_activation_is_rejected():
     w = R.scaled(R.WORKLOADS["flat48"], num_envs=8)
     cfg = W.train_cfg(w)
@@ -92,6 +112,8 @@ def test_table_layout_is_aligned_and_disjoint(da, dc, a):
     for (s0, e0), (s1, e1) in zip(ends, ends[1:]):
         assert e0 <= s1, "columns overlap"
     assert lay.width % 4 == 0 and lay.width >= ends[-1][1]
+    rec = TableLayout(da, dc, a, keep=True)
+    assert rec.keep >= ends[-1][1] and rec.width % 4 == 0 and rec.width > rec.keep
 
 
 def test_gemm_flop_counts():
@@ -99,6 +121,10 @@ def test_gemm_flop_counts():
     assert W.gemm_flops_per_update(W.WORKLOADS["flat48"]) == pytest.approx(1.06791174144e12)
     assert W.gemm_flops_per_update(W.WORKLOADS["humanoid"]) == pytest.approx(1.1739856896e12)
     assert W.gemm_flops_per_update(W.WORKLOADS["rough235"]) == pytest.approx(1.44439246848e12)
+    # LSTM 256 on 48 columns, head [256, 128]: 4 728 576 FLOPs per sample-visit over both models, less the
+    # recurrent input-grad of each sequence's last step (2 models x 4096 envs x 2*1024*256)
+    lstm = W.WORKLOADS["lstm256"]
+    assert W.gemm_flops_per_update(lstm) == pytest.approx(5 * (98304 * 4728576 - 2 * 4096 * 524288))
 
 
 def test_bench_refuses_more_than_one_gpu():

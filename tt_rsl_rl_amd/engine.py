@@ -28,7 +28,7 @@ def _align4(n: int) -> int:
 
 
 class TableLayout:
-    def __init__(self, actor_dim: int, critic_dim: int, num_actions: int) -> None:
+    def __init__(self, actor_dim: int, critic_dim: int, num_actions: int, keep: bool = False) -> None:
         c = 0
         self.xa = c
         c = _align4(c + actor_dim)
@@ -41,7 +41,8 @@ class TableLayout:
         self.old_std = c
         c = _align4(c + num_actions)
         self.old_logp, self.adv, self.old_values, self.returns, self.adv_mb = c, c + 1, c + 2, c + 3, c + 4
-        self.width = _align4(c + 5)
+        self.keep = c + 5 if keep else None  # recurrent: 1 - done of the row's step
+        self.width = _align4(c + (6 if keep else 5))
 
 
 class ModelBuffers:
@@ -101,6 +102,11 @@ class _NoTimer:
 class UpdateEngine:
     """Owns the device workspaces of the update and runs it.  Rebuilt when the rollout shape changes."""
 
+    recurrent = False
+
+    def max_rows(self) -> int:
+        return -(-self.B // self.M)
+
     def __init__(self, alg) -> None:
         self.alg = alg
         self.timer = _NoTimer()
@@ -110,10 +116,10 @@ class UpdateEngine:
         self.M = alg.num_mini_batches
         if not 1 <= self.M <= self.B:
             raise ValueError("num_mini_batches must be between 1 and the rollout batch size.")
-        self.R_max = -(-self.B // self.M)
+        self.R_max = self.max_rows()
         actor, critic = alg.actor, alg.critic
         self.A = actor.distribution.output_dim
-        self.layout = TableLayout(actor.obs_dim, critic.obs_dim, self.A)
+        self.layout = TableLayout(actor.obs_dim, critic.obs_dim, self.A, keep=self.recurrent)
         self.table = torch.empty(self.B, self.layout.width, device=self.device)
         self.buf_a = ModelBuffers(actor, self.R_max, self.device)
         self.buf_c = ModelBuffers(critic, self.R_max, self.device)
@@ -126,6 +132,12 @@ class UpdateEngine:
 
     # -- one update ------------------------------------------------------------------------------------------------
     def gather(self, perm: torch.Tensor) -> None:
+        segs = self.segments()
+        for i in range(0, len(segs), L.MAX_GATHER_SEGMENTS):
+            ops.gather_rows(perm, segs[i:i + L.MAX_GATHER_SEGMENTS], self.table)
+
+    def segments(self) -> list[ops.Segment]:
+        """The packed table's column blocks and their storage sources ([T * N, width] views)."""
         alg, st, lay = self.alg, self.alg.storage, self.layout
         segs: list[ops.Segment] = []
         for model, base in ((alg.actor, lay.xa), (alg.critic, lay.xc)):
@@ -145,29 +157,41 @@ class UpdateEngine:
                  ops.Segment(st.flat(std), lay.old_std), ops.Segment(st.flat(st.actions_log_prob), lay.old_logp),
                  ops.Segment(st.flat(st.advantages), lay.adv), ops.Segment(st.flat(st.values), lay.old_values),
                  ops.Segment(st.flat(st.returns), lay.returns)]
-        for i in range(0, len(segs), L.MAX_GATHER_SEGMENTS):
-            ops.gather_rows(perm, segs[i:i + L.MAX_GATHER_SEGMENTS], self.table)
+        return segs
 
     def minibatch(self, r0: int, r1: int, step: int) -> None:
         alg, lay = self.alg, self.layout
         R = r1 - r0
         tab = self.table[r0:r1]
-        actor, critic = alg.actor, alg.critic
-        la, lc = actor.linears, critic.linears
-        ba, bc = self.buf_a, self.buf_c
-        nl = len(la)
-        if len(lc) != nl:
-            raise NotImplementedError("actor and critic must have the same number of layers")
-        xa = tab[:, lay.xa:lay.xa + actor.obs_dim]
-        xc = tab[:, lay.xc:lay.xc + critic.obs_dim]
+        xa = tab[:, lay.xa:lay.xa + alg.actor.obs_dim]
+        xc = tab[:, lay.xc:lay.xc + alg.critic.obs_dim]
+        adv_col = self.advantage_column(tab, R)
+        self.head_forward(xa, xc, R)
+        self.loss(tab, R, adv_col)
+        self.head_backward(R, down_to=1)
+        self.weight_grads(self.head_dw(xa, xc, R), R)
+        self.adam(step)
 
-        adv_col = lay.adv
-        if alg.normalize_advantage_per_mini_batch and R > 1:
+    # -- pieces shared with the recurrent engine ----------------------------------------------------------------------
+    def advantage_column(self, tab: torch.Tensor, R: int) -> int:
+        lay = self.layout
+        if self.alg.normalize_advantage_per_mini_batch and R > 1:
             ops.adv_normalize(tab[:, lay.adv], tab[:, lay.adv_mb], R, in_stride=lay.width, out_stride=lay.width,
                               ws=self.adv_ws)
-            adv_col = lay.adv_mb
+            return lay.adv_mb
+        return lay.adv
 
-        # forward, actor and critic grouped layer by layer
+    def _layers(self):
+        la, lc = self.alg.actor.linears, self.alg.critic.linears
+        if len(lc) != len(la):
+            raise NotImplementedError("actor and critic must have the same number of layers")
+        return la, lc
+
+    def head_forward(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> None:
+        """The MLPs, actor and critic grouped layer by layer (hidden layers keep only elu(z))."""
+        la, lc = self._layers()
+        ba, bc = self.buf_a, self.buf_c
+        nl = len(la)
         tm = self.timer
         ins_a, ins_c = [xa], [xc]
         for i in range(nl):
@@ -181,8 +205,11 @@ class UpdateEngine:
                 ins_a.append(ba.h[i][:R])
                 ins_c.append(bc.h[i][:R])
 
-        # losses + per-row gradients, then the device-side reduction / LR rule / std-parameter gradient
-        dist = actor.distribution
+    def loss(self, tab: torch.Tensor, R: int, adv_col: int) -> None:
+        """Losses + per-row output gradients, then the device-side reduction / LR rule / std-parameter gradient."""
+        alg, lay = self.alg, self.layout
+        ba, bc = self.buf_a, self.buf_c
+        dist = alg.actor.distribution
         lo, hi = dist.param_range
         batch = {"ld": lay.width, "actions": tab[:, lay.actions], "old_mean": tab[:, lay.old_mean],
                  "old_std": tab[:, lay.old_std], "old_logp": tab[:, lay.old_logp], "advantages": tab[:, adv_col],
@@ -190,6 +217,7 @@ class UpdateEngine:
         args = ops.make_loss_args(R, ba.out[:R], bc.out[:R, 0], batch, dist.param, dist.kernel_std_type, lo, hi,
                                   alg.clip_param, alg.value_loss_coef, alg.entropy_coef, alg.use_clipped_value_loss,
                                   ba.dz[-1][:R], bc.dz[-1][:R, 0])
+        tm = self.timer
         tm.start("loss")
         ops.ppo_loss(args, self.loss_ws)
         adaptive = alg.desired_kl is not None and alg.schedule == "adaptive"
@@ -197,31 +225,51 @@ class UpdateEngine:
                               alg.desired_kl if alg.desired_kl is not None else 0.0, self.trace)
         tm.stop("loss")
 
-        # backward: input gradients down the chain (grouped), then every weight gradient in one launch
-        for i in range(nl - 1, 0, -1):
+    def head_backward(self, R: int, down_to: int) -> None:
+        """Input gradients down the chain (actor and critic grouped) to the input of layer ``down_to``."""
+        la, lc = self._layers()
+        ba, bc = self.buf_a, self.buf_c
+        tm = self.timer
+        for i in range(len(la) - 1, down_to - 1, -1):
             tm.start(f"dx{i}")
             ops.linear_bwd_dx([(ba.dz[i][:R], la[i].weight, ba.h[i - 1][:R], ba.dz[i - 1][:R]),
                                (bc.dz[i][:R], lc[i].weight, bc.h[i - 1][:R], bc.dz[i - 1][:R])], R, self.dx_ws,
                               elu_from_output=True)
             tm.stop(f"dx{i}")
-        dw = []
-        for model, buf, lins, x0 in ((actor, ba, la, xa), (critic, bc, lc, xc)):
-            for i in range(nl):
-                x = x0 if i == 0 else buf.h[i - 1][:R]
-                dw.append((buf.dz[i][:R], x, alg.flat.grad_view(lins[i].weight), alg.flat.grad_view(lins[i].bias)))
-        tm.start("dw")
-        ops.linear_bwd_dw(dw, R, self.dw_ws)
-        tm.stop("dw")
 
-        # per-model clip + Adam over the flat buffers
+    def head_dw(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> list[tuple]:
+        la, lc = self._layers()
+        grad = self.alg.flat.grad_view
+        dw = []
+        for buf, lins, x0 in ((self.buf_a, la, xa), (self.buf_c, lc, xc)):
+            for i in range(len(lins)):
+                x = x0 if i == 0 else buf.h[i - 1][:R]
+                dw.append((buf.dz[i][:R], x, grad(lins[i].weight), grad(lins[i].bias)))
+        return dw
+
+    def weight_grads(self, dw: list[tuple], R: int, phase: str = "dw") -> None:
+        """Weight gradients, as few grouped launches as the problem limit allows."""
+        tm = self.timer
+        tm.start(phase)
+        for i in range(0, len(dw), L.MAX_LINEAR_PROBLEMS):
+            ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, self.dw_ws)
+        tm.stop(phase)
+
+    def adam(self, step: int) -> None:
+        """Per-model clip + Adam over the flat buffers."""
+        alg = self.alg
         b1, b2 = alg.betas
         bc1 = 1 - b1 ** step
         bc2_sqrt = (1 - b2 ** step) ** 0.5
         f = alg.flat
+        tm = self.timer
         tm.start("adam")
         ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin, alg.max_grad_norm, b1, b2, alg.adam_eps,
                       bc1, bc2_sqrt, alg.device_state, self.adam_ws)
         tm.stop("adam")
+
+    def minibatch_rows(self, i: int) -> tuple[int, int]:
+        return i * self.B // self.M, (i + 1) * self.B // self.M
 
     def run(self, perm: torch.Tensor, first_step: int) -> int:
         """All epochs x mini-batches.  Returns the number of optimiser steps taken."""
@@ -232,8 +280,141 @@ class UpdateEngine:
         step = first_step
         for _ in range(self.alg.num_learning_epochs):
             for i in range(self.M):
-                r0 = i * self.B // self.M
-                r1 = (i + 1) * self.B // self.M
+                r0, r1 = self.minibatch_rows(i)
                 step += 1
                 self.minibatch(r0, r1, step)
         return step - first_step
+
+
+class LstmBuffers:
+    """Sequence buffers of one LSTM for mini-batches of up to ``rows`` = T x envs rows (t-major)."""
+
+    def __init__(self, rnn, rows: int, envs: int, device) -> None:
+        H, D = rnn.hidden_size, rnn.input_size
+        e = lambda *shape: torch.empty(*shape, device=device)
+        self.packed = ops.LstmPacked(D, H, device)
+        self.gx, self.gates, self.dgates = e(rows, 4 * H), e(rows, 4 * H), e(rows, 4 * H)
+        self.h, self.c, self.dh = e(rows, H), e(rows, H), e(rows, H)
+        self.hs = e(rows + envs, H)  # the state entering each step, then h of the last step
+        self.dc = e(envs, H)
+        self.zero = torch.zeros(envs, H, device=device)
+        self.dw_ih_g, self.dw_hh_g = e(4 * H, D), e(4 * H, H)
+        self.db_g, self.db_g2 = e(4 * H), e(4 * H)
+
+
+class RecurrentUpdateEngine(UpdateEngine):
+    """The recurrent update (upstream ppo.py:204-236 with rollout_storage.py:262-331 and rnn.py:35-52).
+
+    Upstream splits each env's rollout at dones, pads the trajectories, runs nn.LSTM from the hidden state saved at
+    each trajectory start and unpads.  Here every env of a mini-batch is ONE sequence of T steps started from the
+    state saved at step 0, with the state multiplied by (1 - done) after each step: the state saved at a trajectory
+    start after a done is exactly that zero (``reset(dones)`` zeroes it before the next step), so both give the same
+    outputs on the same T x E valid steps.  Mini-batch i is the env slice [i N / M, (i + 1) N / M), all steps, the
+    same slices every epoch (no permutation; the host generator is not drawn).  The packed table holds those rows
+    t-major per slice, so a mini-batch is one contiguous row block and step t of it is E consecutive rows."""
+
+    def __init__(self, alg) -> None:
+        actor, critic = alg.actor, alg.critic
+        if not (actor.is_recurrent and critic.is_recurrent):
+            raise NotImplementedError("recurrent PPO on the HIP path needs a recurrent actor AND critic")
+        st = alg.storage
+        self.T, self.N = st.num_transitions_per_env, st.num_envs
+        M = alg.num_mini_batches
+        if not 1 <= M <= self.N:
+            raise ValueError("num_mini_batches must be between 1 and the number of environments.")
+        self.E_max = -(-self.N // M)
+        super().__init__(alg)
+        self.seq_a = LstmBuffers(actor.rnn, self.R_max, self.E_max, self.device)
+        self.seq_c = LstmBuffers(critic.rnn, self.R_max, self.E_max, self.device)
+        # row order of the table: per env slice, t-major
+        order = []
+        idx = torch.arange(self.T * self.N).view(self.T, self.N)
+        for i in range(M):
+            e0, e1 = self.env_slice(i)
+            order.append(idx[:, e0:e1].reshape(-1))
+        self.order = torch.cat(order).to(self.device)
+
+    recurrent = True
+
+    def max_rows(self) -> int:
+        return self.T * self.E_max
+
+    def env_slice(self, i: int) -> tuple[int, int]:
+        return i * self.N // self.M, (i + 1) * self.N // self.M
+
+    def minibatch_rows(self, i: int) -> tuple[int, int]:
+        e0, e1 = self.env_slice(i)
+        return self.T * e0, self.T * e1
+
+    def gather(self, perm: torch.Tensor | None = None) -> None:
+        super().gather(self.order if perm is None else perm)
+
+    def segments(self) -> list[ops.Segment]:
+        self._keep = 1.0 - self.alg.storage.dones.reshape(-1, 1).float()
+        return super().segments() + [ops.Segment(self._keep, self.layout.keep)]
+
+    def _initial_state(self, model, side: str, e0: int, e1: int, buf: LstmBuffers):
+        saved = getattr(self.alg.storage, f"saved_hidden_state_{side}")
+        if saved is None:  # no state was recorded (a first rollout of one step): nn.LSTM's zero default
+            return buf.zero[:e1 - e0], buf.zero[:e1 - e0]
+        return saved[0][0, 0, e0:e1], saved[1][0, 0, e0:e1]
+
+    def _seq(self, model, side: str, buf: LstmBuffers, x: torch.Tensor, e0: int, e1: int, tab: torch.Tensor) -> dict:
+        R = self.T * (e1 - e0)
+        h0, c0 = self._initial_state(model, side, e0, e1, buf)
+        return dict(packed=buf.packed, hidden=model.rnn.hidden_size, gx=buf.gx[:R], h0=h0, c0=c0,
+                    keep=tab[:, self.layout.keep], h=buf.h[:R], hs=buf.hs[:R + e1 - e0], c=buf.c[:R],
+                    gates=buf.gates[:R], dh=buf.dh[:R], dgates=buf.dgates[:R], dc=buf.dc[:e1 - e0])
+
+    def _grouped(self, fn, qa: dict, qc: dict, E: int) -> None:
+        if qa["hidden"] == qc["hidden"]:
+            fn([qa, qc], self.T, E)
+        else:
+            fn([qa], self.T, E)
+            fn([qc], self.T, E)
+
+    def minibatch(self, r0: int, r1: int, step: int) -> None:
+        alg, lay, tm = self.alg, self.layout, self.timer
+        actor, critic = alg.actor, alg.critic
+        R = r1 - r0
+        E = R // self.T
+        e0 = r0 // self.T
+        tab = self.table[r0:r1]
+        xa = tab[:, lay.xa:lay.xa + actor.obs_dim]
+        xc = tab[:, lay.xc:lay.xc + critic.obs_dim]
+        sa, sc = self.seq_a, self.seq_c
+        adv_col = self.advantage_column(tab, R)
+
+        # LSTM forward: packed weights, input projection for all T x E rows at once, then the T recurrent steps
+        tm.start("lstm_fwd")
+        ops.lstm_pack([(*actor.rnn.weights, sa.packed), (*critic.rnn.weights, sc.packed)])
+        ops.linear_fwd([(xa, sa.packed.w_ih_g, sa.packed.b_g, sa.gx[:R], None),
+                        (xc, sc.packed.w_ih_g, sc.packed.b_g, sc.gx[:R], None)], R, elu=False)
+        qa = self._seq(actor, "a", sa, xa, e0, e0 + E, tab)
+        qc = self._seq(critic, "c", sc, xc, e0, e0 + E, tab)
+        self._grouped(ops.lstm_seq_fwd, qa, qc, E)
+        tm.stop("lstm_fwd")
+
+        self.head_forward(sa.h[:R], sc.h[:R], R)
+        self.loss(tab, R, adv_col)
+        self.head_backward(R, down_to=1)
+        # the head's first layer has no activation below it: plain input gradient into the LSTM output
+        la, lc = self._layers()
+        tm.start("dx0")
+        ops.linear_bwd_dx([(self.buf_a.dz[0][:R], la[0].weight, None, sa.dh[:R]),
+                           (self.buf_c.dz[0][:R], lc[0].weight, None, sc.dh[:R])], R, self.dx_ws)
+        tm.stop("dx0")
+        tm.start("lstm_bwd")
+        self._grouped(ops.lstm_seq_bwd, qa, qc, E)
+        tm.stop("lstm_bwd")
+
+        self.weight_grads(self.head_dw(sa.h[:R], sc.h[:R], R), R)
+        dw = []
+        for s, x in ((sa, xa), (sc, xc)):
+            dw.append((s.dgates[:R], s.hs[:R], s.dw_hh_g, s.db_g))
+            dw.append((s.dgates[:R], x, s.dw_ih_g, s.db_g2))
+        self.weight_grads(dw, R, "lstm_dw")
+        grad = alg.flat.grad_view
+        ops.lstm_unpack_grads([(s.dw_ih_g, s.dw_hh_g, s.db_g, *(grad(p) for p in m.rnn.weights))
+                               for s, m in ((sa, actor), (sc, critic))])
+        self.adam(step)

@@ -350,6 +350,148 @@ class MLPModel(nn.Module):
         return _ExportMLP(self)
 
 
+class RNN(nn.Module):
+    """rsl_rl/modules/rnn.py:22-86 for a one-layer LSTM, in rollout mode on the GPU.
+
+    The parameters carry nn.LSTM's names (``rnn.weight_ih_l0``, ``rnn.weight_hh_l0``, ``rnn.bias_ih_l0``,
+    ``rnn.bias_hh_l0`` under this module) and its initial values: an ``nn.LSTM`` is built on the CPU (drawing from
+    the global generator exactly as upstream's constructor does) and its tensors are adopted, so no torch RNN
+    kernel ever runs.  ``hidden_state`` is upstream's tuple ``(h, c)`` of [1, N, H] tensors, or None before the
+    first step; every step writes fresh tensors, so a state captured with ``get_hidden_state`` stays valid (upstream
+    relies on that in ``compute_returns``)."""
+
+    def __init__(self, input_size: int, hidden_dim: int = 256, num_layers: int = 1, type: str = "lstm") -> None:
+        super().__init__()
+        if type.lower() != "lstm":
+            raise NotImplementedError(f"rnn_type '{type}': the HIP recurrent path implements the LSTM")
+        if num_layers != 1:
+            raise NotImplementedError("the HIP LSTM kernels implement one layer (rnn_num_layers=1)")
+        if hidden_dim % 4 != 0:
+            raise NotImplementedError(f"rnn_hidden_dim={hidden_dim}: the HIP LSTM kernels need a multiple of 4")
+        ref = nn.LSTM(input_size=input_size, hidden_size=hidden_dim, num_layers=1)
+        self.rnn = nn.Module()
+        for name in ("weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0"):
+            self.rnn.register_parameter(name, nn.Parameter(getattr(ref, name).detach().clone()))
+        self.input_size = input_size
+        self.hidden_size = hidden_dim
+        self.hidden_state: tuple[torch.Tensor, torch.Tensor] | None = None
+        self._packed: ops.LstmPacked | None = None
+        self._fwd = _ForwardBuffers()
+        self._hs = _ForwardBuffers()
+        self._const = _ForwardBuffers()
+
+    @property
+    def weights(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        r = self.rnn
+        return r.weight_ih_l0, r.weight_hh_l0, r.bias_ih_l0, r.bias_hh_l0
+
+    def packed(self, device) -> ops.LstmPacked:
+        """The gate-interleaved weight copies the kernels read (buffers only; ``ops.lstm_pack`` fills them)."""
+        pk = self._packed
+        if pk is None or pk.w_ih_g.device != torch.device(device):
+            self._packed = pk = ops.LstmPacked(self.input_size, self.hidden_size, device)
+        return pk
+
+    def forward(self, x: torch.Tensor, masks=None, hidden_state=None) -> torch.Tensor:
+        """rnn.py:35-52, rollout mode: one step for every env of ``x`` [N, input_size]; returns h' [N, H]."""
+        if masks is not None:
+            raise NotImplementedError("padded trajectory batches: the recurrent update evaluates them on the GPU "
+                                      "inside PPO.update()")
+        _require_gpu(x, "RNN.forward")
+        N, H, dev = x.shape[0], self.hidden_size, x.device
+        pk = self.packed(dev)
+        ops.lstm_pack([(*self.weights, pk)])
+        gx, gates = self._fwd.get(N, [4 * H, 4 * H], dev)
+        zero, ones = self._const.get(N, [H, 1], dev)
+        if self.hidden_state is None:
+            zero.zero_()
+            h0 = c0 = zero
+        else:
+            h0, c0 = (s.reshape(N, H) for s in self.hidden_state)
+            if h0.stride(0) != H or c0.stride(0) != H:
+                h0, c0 = h0.contiguous(), c0.contiguous()
+        ones.fill_(1.0)
+        ops.linear_fwd([(x, pk.w_ih_g, pk.b_g, gx, None)], N, elu=False)
+        h_new = torch.empty(1, N, H, device=dev)
+        c_new = torch.empty(1, N, H, device=dev)
+        # hs: the per-step input states the backward reads ([T + 1 blocks of N rows]); unused in rollout mode
+        hs = self._hs.get(2 * N, [H], dev)[0]
+        ops.lstm_seq_fwd([dict(packed=pk, hidden=H, gx=gx, h0=h0, c0=c0, keep=ones.view(-1), h=h_new[0], hs=hs,
+                               c=c_new[0], gates=gates)], 1, N)
+        self.hidden_state = (h_new, c_new)
+        return h_new[0]
+
+    def reset(self, dones: torch.Tensor | None = None, hidden_state=None) -> None:
+        """rnn.py:54-71."""
+        if dones is None:
+            self.hidden_state = hidden_state
+        elif self.hidden_state is not None:
+            if hidden_state is not None:
+                raise NotImplementedError("Resetting the hidden state of done environments with a custom hidden state "
+                                          "is not implemented")
+            for s in self.hidden_state:
+                s[..., dones == 1, :] = 0.0
+
+    def detach_hidden_state(self, dones: torch.Tensor | None = None) -> None:
+        """rnn.py:73-86: the HIP path keeps no autograd graph, so there is nothing to detach."""
+
+
+class RNNModel(MLPModel):
+    """rsl_rl/models/rnn_model.py:18-107: LSTM on the (normalised) observations, then the MLP head.
+
+    Registration order as upstream (normaliser, distribution, mlp, then ``rnn``), so the parameter order is
+    [distribution, mlp.*, rnn.rnn.weight_ih_l0, weight_hh_l0, bias_ih_l0, bias_hh_l0] and a seed gives upstream's
+    initial weights.  Rollout forwards step the LSTM on the GPU; the update evaluates whole mini-batches of
+    trajectories inside ``PPO.update()``."""
+
+    is_recurrent: bool = True
+
+    def __init__(self, obs: Mapping, obs_groups: dict, obs_set: str, output_dim: int, hidden_dims=(256, 256, 256),
+                 activation: str = "elu", obs_normalization: bool = False, distribution_cfg: dict | None = None,
+                 rnn_type: str = "lstm", rnn_hidden_dim: int = 256, rnn_num_layers: int = 1) -> None:
+        if rnn_type.lower() != "lstm":
+            raise NotImplementedError(f"rnn_type '{rnn_type}': the HIP recurrent path implements the LSTM")
+        self.latent_dim = rnn_hidden_dim
+        super().__init__(obs, obs_groups, obs_set, output_dim, hidden_dims, activation, obs_normalization,
+                         distribution_cfg)
+        self.rnn = RNN(self.obs_dim, rnn_hidden_dim, rnn_num_layers, rnn_type)
+
+    def _get_latent_dim(self) -> int:
+        return self.latent_dim
+
+    def get_latent(self, obs: Mapping, masks=None, hidden_state=None) -> torch.Tensor:
+        """rnn_model.py:76-84 in rollout mode."""
+        if masks is not None:
+            raise NotImplementedError("padded trajectory batches: the recurrent update evaluates them on the GPU "
+                                      "inside PPO.update()")
+        return self.rnn(super().get_latent(obs))
+
+    def forward(self, obs: Mapping, masks=None, hidden_state=None, stochastic_output: bool = False) -> torch.Tensor:
+        out = self.mlp_forward(self.get_latent(obs, masks, hidden_state))
+        if self.distribution is not None:
+            if stochastic_output:
+                self.distribution.update(out)
+                return self.distribution.sample()
+            return self.distribution.deterministic_output(out)
+        return out
+
+    def reset(self, dones=None, hidden_state=None) -> None:
+        self.rnn.reset(dones, hidden_state)
+
+    def get_hidden_state(self):
+        return self.rnn.hidden_state
+
+    def detach_hidden_state(self, dones=None) -> None:
+        self.rnn.detach_hidden_state(dones)
+
+    def as_jit(self) -> nn.Module:
+        """Export copy with plain torch modules (rsl_rl/models/rnn_model.py:129-175) -- export, not the hot path."""
+        return _ExportLSTM(self)
+
+    def as_onnx(self) -> nn.Module:
+        return _ExportLSTM(self)
+
+
 class _TorchNormalizer(nn.Module):
     def __init__(self, norm: EmpiricalNormalization) -> None:
         super().__init__()
@@ -378,6 +520,51 @@ class _ExportMLP(nn.Module):
     @torch.jit.export
     def reset(self) -> None:
         pass
+
+    def get_dummy_inputs(self) -> tuple[torch.Tensor]:
+        return (torch.zeros(1, self.input_size),)
+
+    @property
+    def input_names(self) -> list[str]:
+        return ["obs"]
+
+    @property
+    def output_names(self) -> list[str]:
+        return ["actions"]
+
+
+def _cpu_lstm(model: RNNModel) -> nn.LSTM:
+    lstm = nn.LSTM(model.rnn.input_size, model.rnn.hidden_size)
+    with torch.no_grad():
+        for name, p in zip(("weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0"), model.rnn.weights):
+            getattr(lstm, name).copy_(p.detach().cpu())
+    return lstm
+
+
+class _ExportLSTM(nn.Module):
+    """Deterministic stateful export copy (rsl_rl/models/rnn_model.py:147-175) with plain torch modules."""
+
+    is_recurrent = True
+
+    def __init__(self, model: RNNModel) -> None:
+        super().__init__()
+        self.obs_normalizer = _TorchNormalizer(model.obs_normalizer) if model.obs_normalization else nn.Identity()
+        self.rnn = _cpu_lstm(model)
+        self.mlp = copy.deepcopy(model.mlp).cpu()
+        self.input_size = model.obs_dim
+        self.register_buffer("hidden_state", torch.zeros(1, 1, model.rnn.hidden_size))
+        self.register_buffer("cell_state", torch.zeros(1, 1, model.rnn.hidden_size))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x, (h, c) = self.rnn(self.obs_normalizer(x).unsqueeze(0), (self.hidden_state, self.cell_state))
+        self.hidden_state[:] = h
+        self.cell_state[:] = c
+        return self.mlp(x.squeeze(0))
+
+    @torch.jit.export
+    def reset(self) -> None:
+        self.hidden_state[:] = 0.0
+        self.cell_state[:] = 0.0
 
     def get_dummy_inputs(self) -> tuple[torch.Tensor]:
         return (torch.zeros(1, self.input_size),)

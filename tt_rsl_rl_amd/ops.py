@@ -355,19 +355,39 @@ def lstm_pack(items: list[tuple]) -> None:
         for t in (w_ih, w_hh, b_ih, b_hh):
             if not t.is_contiguous():
                 raise ValueError("lstm_pack: weights must be contiguous")
+        H, D = pk.hidden, pk.input_size
+        if (tuple(w_ih.shape) != (4 * H, D) or tuple(w_hh.shape) != (4 * H, H) or b_ih.numel() != 4 * H
+                or b_hh.numel() != 4 * H):
+            raise ValueError("lstm_pack: weight shapes do not match the packed buffers")
         probs.append(L.LstmPackProblem(w_ih.data_ptr(), w_hh.data_ptr(), b_ih.data_ptr(), b_hh.data_ptr(),
                                        pk.w_ih_g.data_ptr(), pk.w_hh_g.data_ptr(), pk.w_hh_gt.data_ptr(),
                                        pk.b_g.data_ptr(), pk.input_size, pk.hidden))
     L.call("ppo_lstm_pack", L.array(L.LstmPackProblem, probs), len(probs), _stream())
 
 
-def _seq_problem(q: dict) -> "L.LstmSeqProblem":
+def _seq_problem(q: dict, steps: int, envs: int, bwd: bool) -> "L.LstmSeqProblem":
     H = q["hidden"]
     gx, h0, c0, h = q["gx"], q["h0"], q["c0"], q["h"]
     keep = q["keep"]
     _dev(gx, h0, c0, h, keep, q["hs"], q["c"], q["gates"], q.get("dh"), q.get("dgates"), q.get("dc"))
+    if q["packed"].hidden != H:
+        raise ValueError("lstm: packed weights of another hidden size")
     if h0.stride(0) != c0.stride(0):
         raise ValueError("lstm: h0 and c0 must share a leading dimension")
+    # every buffer must hold the rows and columns the kernels touch (the kernels see raw pointers only)
+    R = steps * envs
+    need = {"gx": (R, 4 * H), "h0": (envs, H), "c0": (envs, H), "h": (R, H), "hs": (R + envs, H), "c": (R, H),
+            "gates": (R, 4 * H)}
+    if bwd:
+        need.update({"dh": (R, H), "dgates": (R, 4 * H), "dc": (envs, H)})
+    for name, (rows, cols) in need.items():
+        t = q.get(name)
+        if t is None:
+            raise ValueError(f"lstm: {name} is required")
+        if t.dim() != 2 or t.shape[0] < rows or t.shape[1] < cols or t.stride(1) != 1:
+            raise ValueError(f"lstm: {name} {tuple(t.shape)} must be a row-major view of at least [{rows}, {cols}]")
+    if keep.dim() != 1 or keep.shape[0] < R:
+        raise ValueError(f"lstm: keep must be a vector of at least {R} entries")
     dh = q.get("dh")
     return L.LstmSeqProblem(q["packed"].w_hh_g.data_ptr(), q["packed"].w_hh_gt.data_ptr(), gx.data_ptr(),
                             _row_major(gx, "gx"), h0.data_ptr(), c0.data_ptr(), _row_major(h0, "h0"), keep.data_ptr(),
@@ -379,13 +399,13 @@ def _seq_problem(q: dict) -> "L.LstmSeqProblem":
 def lstm_seq_fwd(problems: list[dict], steps: int, envs: int) -> None:
     """problems: dicts with packed (LstmPacked), hidden, gx [T*E, 4H], h0 / c0 [E, H], keep [T*E] (stride = row
     step), h [T*E, H], hs [(T+1)*E, H], c [T*E, H], gates [T*E, 4H]."""
-    arr = L.array(L.LstmSeqProblem, [_seq_problem(q) for q in problems])
+    arr = L.array(L.LstmSeqProblem, [_seq_problem(q, steps, envs, False) for q in problems])
     L.call("ppo_lstm_seq_fwd", arr, len(problems), steps, envs, _stream())
 
 
 def lstm_seq_bwd(problems: list[dict], steps: int, envs: int) -> None:
     """As lstm_seq_fwd's problems plus dh [T*E, H], dgates [T*E, 4H], dc [E, H] (scratch)."""
-    arr = L.array(L.LstmSeqProblem, [_seq_problem(q) for q in problems])
+    arr = L.array(L.LstmSeqProblem, [_seq_problem(q, steps, envs, True) for q in problems])
     L.call("ppo_lstm_seq_bwd", arr, len(problems), steps, envs, _stream())
 
 
@@ -394,7 +414,11 @@ def lstm_unpack_grads(items: list[tuple]) -> None:
     probs = []
     for dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh in items:
         _dev(dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh)
-        H = dw_hh.shape[1]
+        H, D = dw_hh.shape[1], dw_ih.shape[1]
+        for t, n in ((dw_ih_g, 4 * H * D), (dw_ih, 4 * H * D), (dw_hh_g, 4 * H * H), (dw_hh, 4 * H * H), (db_g, 4 * H),
+                     (db_ih, 4 * H), (db_hh, 4 * H)):
+            if t.numel() != n or not t.is_contiguous():
+                raise ValueError("lstm_unpack_grads: gradient buffers do not match [4H, D] / [4H, H] / [4H]")
         probs.append(L.LstmGradProblem(dw_ih_g.data_ptr(), dw_hh_g.data_ptr(), db_g.data_ptr(), dw_ih.data_ptr(),
                                        dw_hh.data_ptr(), db_ih.data_ptr(), db_hh.data_ptr(), dw_ih.shape[1], H))
     L.call("ppo_lstm_unpack_grads", L.array(L.LstmGradProblem, probs), len(probs), _stream())

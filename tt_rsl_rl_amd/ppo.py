@@ -26,8 +26,8 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .engine import UpdateEngine
-from .models import MLPModel
+from .engine import RecurrentUpdateEngine, UpdateEngine
+from .models import MLPModel, RNNModel
 from .storage import RolloutStorage
 
 
@@ -41,7 +41,7 @@ def resolve_callable(name):
     if not isinstance(name, str):
         raise TypeError(f"Expected callable or string, got {type(name)}")
     short = name.split(":")[-1].split(".")[-1]
-    local = {"PPO": PPO, "MLPModel": MLPModel, "RolloutStorage": RolloutStorage}
+    local = {"PPO": PPO, "MLPModel": MLPModel, "RNNModel": RNNModel, "RolloutStorage": RolloutStorage}
     if ":" in name:
         mod, attr = name.rsplit(":", 1)
         if mod.split(".")[0] == "rsl_rl" and short in local:
@@ -52,8 +52,6 @@ def resolve_callable(name):
         return obj
     if short in local:
         return local[short]
-    if short == "RNNModel":
-        raise NotImplementedError("RNNModel (recurrent PPO) is not implemented on the HIP path yet")
     raise ValueError(f"Could not resolve '{name}'. Use a qualified name like 'module.path:ClassName'.")
 
 
@@ -165,8 +163,8 @@ class PPO:
             raise NotImplementedError(f"optimizer '{optimizer}': the fused update implements Adam")
         if use_mixed_precision:
             raise NotImplementedError("the HIP update computes in fp32; use_mixed_precision is not supported")
-        if actor.is_recurrent or critic.is_recurrent:
-            raise NotImplementedError("recurrent models are not on the HIP MLP path")
+        if actor.is_recurrent != critic.is_recurrent:
+            raise NotImplementedError("the HIP recurrent update needs both actor and critic recurrent (or neither)")
         if actor.distribution is None:
             raise ValueError("the actor needs a GaussianDistribution (distribution_cfg)")
         if not actor.distribution.param.requires_grad:
@@ -242,8 +240,10 @@ class PPO:
 
     def compute_returns(self, obs: Mapping) -> None:
         """ppo.py:166-191: bootstrap value, GAE scan and global advantage normalisation on the GPU."""
-        st = self.storage
+        critic_hidden_state = self.critic.get_hidden_state()
         last_values = self.critic(obs).detach().contiguous()
+        # the bootstrap forward must not advance the critic's rollout state (ppo.py:170-173)
+        self.critic.reset(hidden_state=critic_hidden_state)
         self.compute_returns_from(last_values)
 
     def compute_returns_from(self, last_values: torch.Tensor) -> None:
@@ -254,23 +254,32 @@ class PPO:
             ops.adv_normalize(st.advantages, st.advantages, n, ws=self._adv_ws)
 
     # -- learning side -----------------------------------------------------------------------------------------------
+    @property
+    def is_recurrent(self) -> bool:
+        return bool(self.actor.is_recurrent)
+
     def _get_engine(self) -> UpdateEngine:
         e = self._engine
         if e is None or e.B != self.storage.batch_size or e.M != self.num_mini_batches:
-            self._engine = e = UpdateEngine(self)
+            self._engine = e = (RecurrentUpdateEngine if self.is_recurrent else UpdateEngine)(self)
         return e
 
     def update(self) -> dict[str, float]:
         """ppo.py:193-358."""
         st = self.storage
         B = st.batch_size
-        if not 1 <= self.num_mini_batches <= B:
+        if self.is_recurrent:
+            if not 1 <= self.num_mini_batches <= st.num_envs:
+                raise ValueError("num_mini_batches must be between 1 and the number of environments.")
+        elif not 1 <= self.num_mini_batches <= B:
             raise ValueError("num_mini_batches must be between 1 and the rollout batch size.")
         if st.distribution_params is None:
             raise RuntimeError("update() called before any transition was stored")
         engine = self._get_engine()
         ops.reset_device_state(self.device_state, self.learning_rate)
-        perm = torch.randperm(B).to(self.device, non_blocking=False)
+        # feed-forward: one permutation of the batch for all epochs (ppo.py:207, rollout_storage.py:210-260);
+        # recurrent: fixed env slices, no permutation drawn (rollout_storage.py:262-331)
+        perm = None if self.is_recurrent else torch.randperm(B).to(self.device, non_blocking=False)
         steps = engine.run(perm, self._opt_steps)
         self._opt_steps += steps
 

@@ -59,6 +59,8 @@ def linear_shapes(workload: dict) -> list[list[tuple[int, int]]]:
     out = []
     for model, od in (("actor", workload["num_actions"]), ("critic", 1)):
         d_in = sum(dims[g][1] for g in groups[model])
+        if "rnn" in workload:  # the head reads the LSTM output
+            d_in = workload["rnn"]["rnn_hidden_dim"]
         hs = list(workload["hidden_dims"])
         chain = [d_in] + hs + [od]
         out.append(list(zip(chain[:-1], chain[1:])))
@@ -69,7 +71,27 @@ def gemm_flops_per_update(workload: dict, epochs: int = 5) -> float:
     """Algorithmic GEMM FLOPs of one update: per sample-visit 2*in*out for each of forward, input-grad and
     weight-grad of every layer, except no input-grad for the first layer; B * epochs sample-visits."""
     B = workload["num_envs"] * workload["steps"]
+    if "rnn" in workload:
+        return lstm_gemm_flops_per_update(workload, epochs)
     per = 0
     for layers in linear_shapes(workload):
         per += sum(3 * 2 * i * o for i, o in layers) - 2 * layers[0][0] * layers[0][1]
     return float(per) * B * epochs
+
+
+def lstm_gemm_flops_per_update(workload: dict, epochs: int = 5) -> float:
+    """Recurrent models (one LSTM layer of hidden H on D observation columns, then the MLP head), per model and
+    sample-visit: LSTM forward 2*4H*(D+H) (input projection + recurrent product), weight-grad 2*4H*(D+H), the
+    recurrent input-grad 2*4H*H on all but the last step of each sequence (no gradient flows into the saved initial
+    state or the observations); the head: forward, input-grad and weight-grad of every layer (its first layer's
+    input-grad feeds the LSTM)."""
+    N, T = workload["num_envs"], workload["steps"]
+    B = N * T
+    H = workload["rnn"]["rnn_hidden_dim"]
+    dims, groups = workload["obs"], workload["obs_groups"]
+    total = 0
+    for layers, model in zip(linear_shapes(workload), ("actor", "critic")):
+        D = sum(dims[g][1] for g in groups[model])
+        total += B * (sum(3 * 2 * i * o for i, o in layers) + 2 * 2 * 4 * H * (D + H))
+        total += (B - N) * 2 * 4 * H * H
+    return float(total) * epochs
