@@ -85,6 +85,15 @@ def phase_flops(workload, R: int) -> dict[str, float]:
     for i in range(1, nl):
         out[f"dx{i}"] = sum(2.0 * R * s[i][0] * s[i][1] for s in shapes)
     out["dw"] = sum(2.0 * R * i_ * o_ for s in shapes for i_, o_ in s)
+    if "rnn" in workload:
+        # recurrent: R = T x E rows; one LSTM (hidden H on D observation columns) before each head
+        H = workload["rnn"]["rnn_hidden_dim"]
+        E = R // workload["steps"]
+        dims = [sum(workload["obs"][g][1] for g in workload["obs_groups"][m]) for m in ("actor", "critic")]
+        out["dx0"] = sum(2.0 * R * s[0][0] * s[0][1] for s in shapes)
+        out["lstm_fwd"] = sum(2.0 * R * 4 * H * (D + H) for D in dims)   # input projection + T recurrent steps
+        out["lstm_bwd"] = sum(2.0 * (R - E) * 4 * H * H for _ in dims)    # recurrent input-grad, T - 1 steps
+        out["lstm_dw"] = sum(2.0 * R * 4 * H * (D + H) for D in dims)
     return out
 
 
@@ -108,7 +117,8 @@ def cpu_baseline(workload, reps: int) -> dict:
 
     threads = torch.get_num_threads()
     ora, roll = R.generate(workload, seed=0)
-    ora.compute_returns(roll.last_obs)
+    with torch.inference_mode():  # as upstream's runner collects (the recurrent states are inference tensors)
+        ora.compute_returns(roll.last_obs)
     times = []
     for i in range(reps + 1):
         ora.storage.step = ora.storage.num_transitions_per_env
@@ -133,7 +143,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="humanoid")
     ap.add_argument("--cpu-baseline", choices=("on", "off"), default="on")
-    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--cpu-reps", type=int, default=None,
+                    help="timed oracle updates for cpu_baseline (default 3; 1 for recurrent workloads)")
     ap.add_argument("--no-phase-events", action="store_true", help="do not record per-launch HIP events")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
@@ -164,13 +175,10 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
     workload = W.WORKLOADS[args.workload]
-    if "rnn" in workload:
-        print("bench.py: recurrent workloads are not implemented", file=sys.stderr)
-        return 2
     alg = build_gpu_alg(workload)
     B = workload["num_envs"] * workload["steps"]
     M = alg.num_mini_batches
-    R = B // M
+    R = B // M if "rnn" not in workload else workload["steps"] * (workload["num_envs"] // M)
 
     def one_update():
         alg.storage.step = alg.storage.num_transitions_per_env
@@ -224,12 +232,16 @@ def main() -> int:
                     "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": load_traffic(dom), "kernel": dom,
                     "flops_per_launch": flops[dom], "mean_launch_ms": round(t, 5), "launches_timed": n}
     gemm_total = W.gemm_flops_per_update(workload, alg.num_learning_epochs)
+    lstm = ""
+    if "rnn" in workload:
+        lstm = (f"LSTM {workload['rnn']['rnn_hidden_dim']} on the observations (sequences of {workload['steps']} "
+                f"steps per env, env-slice mini-batches), then ")
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-        "config": {"workload": f"{args.workload}: {len(W.linear_shapes(workload)[0])}-layer actor/critic MLPs "
+        "config": {"workload": f"{args.workload}: {lstm}{len(W.linear_shapes(workload)[0])}-layer actor/critic MLPs "
                                f"{W.linear_shapes(workload)}, {workload['num_envs']} envs x {workload['steps']} steps, "
                                f"{alg.num_learning_epochs} epochs x {M} mini-batches of {R} rows, "
                                f"obs normalisation {workload['obs_normalization']}",
@@ -244,7 +256,8 @@ def main() -> int:
         "cpu_baseline": None,
     }
     if args.cpu_baseline == "on":
-        line["cpu_baseline"] = cpu_baseline(workload, args.cpu_reps)
+        reps = args.cpu_reps if args.cpu_reps is not None else (1 if "rnn" in workload else 3)
+        line["cpu_baseline"] = cpu_baseline(workload, reps)
     print(json.dumps(line))
     return 0
 

@@ -244,6 +244,84 @@ __device__ __forceinline__ void nt_masked(const float* __restrict__ base, int64_
 }
 
 // OCC: waves per SIMD the register allocation must allow (blocks of 4 waves per CU), traded against spills.
+// Per-row operands of the LSTM step epilogues.  They do not depend on the product, so the kernel loads them before
+// its k loop and their latency hides behind it (loaded inside the epilogue, the stores between its row rounds keep
+// the compiler from batching the loads of the next round).  Lane l finishes rows pr + 8 rr (rr = 0..3) at columns
+// pc .. pc + 3 of every 32 x 32 tile (pr = l / 8, pc = 4 (l % 8)); r0 / c0 are the wave's first row / column.
+template <int EPI, int TM, int TN>
+struct LstmPre {
+  __device__ __forceinline__ void load(const Problem&, int, int, int) {}
+};
+
+template <int TM, int TN>
+struct LstmPre<EPI_LSTM_FWD, TM, TN> {
+  f32x4 gx[TM][TN][4];
+  float cp[TM][TN][4];
+  float kp[TM][4];
+  __device__ __forceinline__ void load(const Problem& P, int r0, int c0, int lane) {
+    const LstmArgs& L = P.lstm;
+    const int pr = lane >> 3, pc = 4 * (lane & 7);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int64_t m = r0 + i * 32 + pr + 8 * rr;
+        const bool in = m < P.M;
+        kp[i][rr] = in && L.keep_prev != nullptr ? L.keep_prev[m * L.keep_stride] : 1.0f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = c0 + j * 32 + pc;
+          if (in && n < P.N) {
+            gx[i][j][rr] = *reinterpret_cast<const f32x4*>(L.gx + m * L.ldgx + n);
+            cp[i][j][rr] = L.c_prev[m * L.ldcp + (n >> 2)];
+          } else {
+            gx[i][j][rr] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            cp[i][j][rr] = 0.0f;
+          }
+        }
+      }
+  }
+};
+
+template <int TM, int TN>
+struct LstmPre<EPI_LSTM_BWD, TM, TN> {
+  float keep[TM][4], kp[TM][4];
+  f32x4 dh[TM][TN][4], ct[TM][TN][4], cp[TM][TN][4], dc[TM][TN][4];
+  f32x4 gt[TM][TN][4][4];
+  __device__ __forceinline__ void load(const Problem& P, int r0, int c0, int lane) {
+    const LstmArgs& L = P.lstm;
+    const int64_t H = L.hidden;
+    const int pr = lane >> 3, pc = 4 * (lane & 7);
+    const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int64_t m = r0 + i * 32 + pr + 8 * rr;
+        const bool in = m < P.M;
+        keep[i][rr] = in ? L.keep[m * L.keep_stride] : 0.0f;
+        kp[i][rr] = in && L.keep_prev != nullptr ? L.keep_prev[m * L.keep_stride] : 1.0f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int n = c0 + j * 32 + pc;
+          if (in && n < P.N) {
+            dh[i][j][rr] = *reinterpret_cast<const f32x4*>(L.dh + m * L.lddh + n);
+            ct[i][j][rr] = *reinterpret_cast<const f32x4*>(L.c + m * H + n);
+            cp[i][j][rr] = *reinterpret_cast<const f32x4*>(L.c_prev + m * L.ldcp + n);
+            dc[i][j][rr] = L.first ? z : *reinterpret_cast<const f32x4*>(L.dc + m * H + n);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              gt[i][j][rr][e] = *reinterpret_cast<const f32x4*>(L.gates + m * 4 * H + 4 * (n + e));
+          } else {
+            dh[i][j][rr] = ct[i][j][rr] = cp[i][j][rr] = dc[i][j][rr] = z;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) gt[i][j][rr][e] = z;
+          }
+        }
+      }
+  }
+};
+
 template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16, int EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_kernel(
     const Group g) {
@@ -278,6 +356,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   NtLoader<BN, BK, B16> lb;
   la.init(lda, row0, M, wave, lane);
   lb.init(ldb, col0, N, wave, lane);
+  LstmPre<EPI, TM, TN> pre;
+  pre.load(P, row0 + wm * WM, col0 + wn * WN, lane);
   const int nfull = K / BK;
   const int nk = (K + BK - 1) / BK;
   auto issue = [&](int kt, int stage) {
@@ -373,11 +453,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
           // columns n .. n+3: gates i, f, g, o of hidden unit u of env m (4H and every base are multiples of 4)
           const LstmArgs& L = P.lstm;
           const int64_t H = L.hidden, u = n >> 2;
-          const f32x4 gx = *reinterpret_cast<const f32x4*>(L.gx + mm * L.ldgx + n);
+          const f32x4 gx = pre.gx[i][j][rr];
           const float ig = sigmoidf(x[0] + gx[0]), fg = sigmoidf(x[1] + gx[1]);
           const float gg = tanhf(x[2] + gx[2]), og = sigmoidf(x[3] + gx[3]);
-          float cp = L.c_prev[mm * L.ldcp + u];
-          if (L.keep_prev != nullptr) cp *= L.keep_prev[mm * L.keep_stride];
+          const float cp = pre.cp[i][j][rr] * pre.kp[i][rr];
           const float ct = fg * cp + ig * gg;
           const float ht = og * tanhf(ct);
           const f32x4 act = {ig, fg, gg, og};
@@ -390,17 +469,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
           // columns n .. n+3: hidden units n .. n+3 of env m; x = (dgates of the next step) . W_hh
           const LstmArgs& L = P.lstm;
           const int64_t H = L.hidden;
-          const float keep = L.keep[mm * L.keep_stride];
-          const float keep_prev = L.keep_prev != nullptr ? L.keep_prev[mm * L.keep_stride] : 1.0f;
-          const f32x4 dhu = *reinterpret_cast<const f32x4*>(L.dh + mm * L.lddh + n);
-          const f32x4 ct = *reinterpret_cast<const f32x4*>(L.c + mm * H + n);
-          const f32x4 cp = *reinterpret_cast<const f32x4*>(L.c_prev + mm * L.ldcp + n);
-          f32x4 dcin = {0.0f, 0.0f, 0.0f, 0.0f};
-          if (!L.first) dcin = *reinterpret_cast<const f32x4*>(L.dc + mm * H + n);
+          const float keep = pre.keep[i][rr];
+          const float keep_prev = pre.kp[i][rr];
+          const f32x4 dhu = pre.dh[i][j][rr];
+          const f32x4 ct = pre.ct[i][j][rr];
+          const f32x4 cp = pre.cp[i][j][rr];
+          const f32x4 dcin = pre.dc[i][j][rr];
           f32x4 dcout;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const f32x4 gt = *reinterpret_cast<const f32x4*>(L.gates + mm * 4 * H + 4 * (n + e));
+            const f32x4 gt = pre.gt[i][j][rr][e];
             const float ig = gt[0], fg = gt[1], gg = gt[2], og = gt[3];
             const float dh = dhu[e] + keep * x[e];
             const float tc = tanhf(ct[e]);

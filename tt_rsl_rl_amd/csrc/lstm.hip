@@ -160,18 +160,15 @@ int check_seq(const ppo_lstm_seq_problem* probs, int32_t count, int64_t steps, i
   return PPO_OK;
 }
 
-// Tile of the per-step GEMMs (the step has only E x 4H or E x H outputs): 64 x 64 unless "PPO_HIP_LSTM_TILE"
-// names 128x64k32s2o4 or 128x128k16s2o3 (tuning aid).
+// Per-step GEMMs on 64 x 64 tiles (a step has only E x 4H forward or E x H backward outputs).  The backward step's
+// E x H output gives at most one block per CU, so its instantiation trades occupancy for the registers that hold the
+// prefetched epilogue operands (waves_per_eu 2).
 template <int EPI>
 int launch_step(Group& g, int count, hipStream_t s, const char* name) {
-  switch (pick_tile(T64x64k32s2o4, "PPO_HIP_LSTM_TILE")) {
-    case T128x64k32s2o4:
-      return launch_nt_aligned<128, 64, 32, 2, 4, EPI>(g, count, s, name);
-    case T128x128k16s2o3:
-      return launch_nt_aligned<128, 128, 16, 2, 3, EPI>(g, count, s, name);
-    default:
-      return launch_nt_aligned<64, 64, 32, 2, 4, EPI>(g, count, s, name);
-  }
+  if constexpr (EPI == EPI_LSTM_BWD)
+    return launch_nt_aligned<64, 64, 32, 2, 2, EPI>(g, count, s, name);
+  else
+    return launch_nt_aligned<64, 64, 32, 2, 4, EPI>(g, count, s, name);
 }
 
 }  // namespace
