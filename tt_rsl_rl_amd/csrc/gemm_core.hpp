@@ -244,51 +244,54 @@ __device__ __forceinline__ void nt_masked(const float* __restrict__ base, int64_
 }
 
 // OCC: waves per SIMD the register allocation must allow (blocks of 4 waves per CU), traded against spills.
-// Per-row operands of the LSTM step epilogues.  They do not depend on the product, so the kernel loads them before
-// its k loop and their latency hides behind it (loaded inside the epilogue, the stores between its row rounds keep
-// the compiler from batching the loads of the next round).  Lane l finishes rows pr + 8 rr (rr = 0..3) at columns
-// pc .. pc + 3 of every 32 x 32 tile (pr = l / 8, pc = 4 (l % 8)); r0 / c0 are the wave's first row / column.
-template <int EPI, int TM, int TN>
+// Per-row operands of the LSTM step epilogues.  They do not depend on the product, so the kernels load them before
+// their k loop and their latency hides behind it (loaded inside the epilogue, the stores between its row rounds keep
+// the compiler from batching the loads of the next round).  Lane l finishes rows pr + 8 rr at columns pc .. pc + 3
+// of each 32 x 32 tile (pr = l / 8, pc = 4 (l % 8)); with the k range split KS ways over the block's waves, split ks
+// finishes the rounds rr = ks + KS k, k < 4 / KS.  r0 / c0 are the wave's first row / column.
+template <int EPI, int TM, int TN, int KS>
 struct LstmPre {
-  __device__ __forceinline__ void load(const Problem&, int, int, int) {}
+  __device__ __forceinline__ void load(const Problem&, int, int, int, int) {}
 };
 
-template <int TM, int TN>
-struct LstmPre<EPI_LSTM_FWD, TM, TN> {
-  f32x4 gx[TM][TN][4];
-  float cp[TM][TN][4];
-  float kp[TM][4];
-  __device__ __forceinline__ void load(const Problem& P, int r0, int c0, int lane) {
+template <int TM, int TN, int KS>
+struct LstmPre<EPI_LSTM_FWD, TM, TN, KS> {
+  static constexpr int RR = 4 / KS;
+  f32x4 gx[TM][TN][RR];
+  float cp[TM][TN][RR];
+  float kp[TM][RR];
+  __device__ __forceinline__ void load(const Problem& P, int r0, int c0, int lane, int ks) {
     const LstmArgs& L = P.lstm;
     const int pr = lane >> 3, pc = 4 * (lane & 7);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int64_t m = r0 + i * 32 + pr + 8 * rr;
+      for (int k = 0; k < RR; ++k) {
+        const int64_t m = r0 + i * 32 + pr + 8 * (ks + KS * k);
         const bool in = m < P.M;
-        kp[i][rr] = in && L.keep_prev != nullptr ? L.keep_prev[m * L.keep_stride] : 1.0f;
+        kp[i][k] = in && L.keep_prev != nullptr ? L.keep_prev[m * L.keep_stride] : 1.0f;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int n = c0 + j * 32 + pc;
           if (in && n < P.N) {
-            gx[i][j][rr] = *reinterpret_cast<const f32x4*>(L.gx + m * L.ldgx + n);
-            cp[i][j][rr] = L.c_prev[m * L.ldcp + (n >> 2)];
+            gx[i][j][k] = *reinterpret_cast<const f32x4*>(L.gx + m * L.ldgx + n);
+            cp[i][j][k] = L.c_prev[m * L.ldcp + (n >> 2)];
           } else {
-            gx[i][j][rr] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            cp[i][j][rr] = 0.0f;
+            gx[i][j][k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            cp[i][j][k] = 0.0f;
           }
         }
       }
   }
 };
 
-template <int TM, int TN>
-struct LstmPre<EPI_LSTM_BWD, TM, TN> {
-  float keep[TM][4], kp[TM][4];
-  f32x4 dh[TM][TN][4], ct[TM][TN][4], cp[TM][TN][4], dc[TM][TN][4];
-  f32x4 gt[TM][TN][4][4];
-  __device__ __forceinline__ void load(const Problem& P, int r0, int c0, int lane) {
+template <int TM, int TN, int KS>
+struct LstmPre<EPI_LSTM_BWD, TM, TN, KS> {
+  static constexpr int RR = 4 / KS;
+  float keep[TM][RR], kp[TM][RR];
+  f32x4 dh[TM][TN][RR], ct[TM][TN][RR], cp[TM][TN][RR], dc[TM][TN][RR];
+  f32x4 gt[TM][TN][RR][4];
+  __device__ __forceinline__ void load(const Problem& P, int r0, int c0, int lane, int ks) {
     const LstmArgs& L = P.lstm;
     const int64_t H = L.hidden;
     const int pr = lane >> 3, pc = 4 * (lane & 7);
@@ -296,31 +299,67 @@ struct LstmPre<EPI_LSTM_BWD, TM, TN> {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int64_t m = r0 + i * 32 + pr + 8 * rr;
+      for (int k = 0; k < RR; ++k) {
+        const int64_t m = r0 + i * 32 + pr + 8 * (ks + KS * k);
         const bool in = m < P.M;
-        keep[i][rr] = in ? L.keep[m * L.keep_stride] : 0.0f;
-        kp[i][rr] = in && L.keep_prev != nullptr ? L.keep_prev[m * L.keep_stride] : 1.0f;
+        keep[i][k] = in ? L.keep[m * L.keep_stride] : 0.0f;
+        kp[i][k] = in && L.keep_prev != nullptr ? L.keep_prev[m * L.keep_stride] : 1.0f;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int n = c0 + j * 32 + pc;
           if (in && n < P.N) {
-            dh[i][j][rr] = *reinterpret_cast<const f32x4*>(L.dh + m * L.lddh + n);
-            ct[i][j][rr] = *reinterpret_cast<const f32x4*>(L.c + m * H + n);
-            cp[i][j][rr] = *reinterpret_cast<const f32x4*>(L.c_prev + m * L.ldcp + n);
-            dc[i][j][rr] = L.first ? z : *reinterpret_cast<const f32x4*>(L.dc + m * H + n);
+            dh[i][j][k] = *reinterpret_cast<const f32x4*>(L.dh + m * L.lddh + n);
+            ct[i][j][k] = *reinterpret_cast<const f32x4*>(L.c + m * H + n);
+            cp[i][j][k] = *reinterpret_cast<const f32x4*>(L.c_prev + m * L.ldcp + n);
+            dc[i][j][k] = L.first ? z : *reinterpret_cast<const f32x4*>(L.dc + m * H + n);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              gt[i][j][rr][e] = *reinterpret_cast<const f32x4*>(L.gates + m * 4 * H + 4 * (n + e));
+              gt[i][j][k][e] = *reinterpret_cast<const f32x4*>(L.gates + m * 4 * H + 4 * (n + e));
           } else {
-            dh[i][j][rr] = ct[i][j][rr] = cp[i][j][rr] = dc[i][j][rr] = z;
+            dh[i][j][k] = ct[i][j][k] = cp[i][j][k] = dc[i][j][k] = z;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) gt[i][j][rr][e] = z;
+            for (int e = 0; e < 4; ++e) gt[i][j][k][e] = z;
           }
         }
       }
   }
 };
+
+// LSTM forward cell for env m, gate columns n .. n+3 = gates i, f, g, o of hidden unit n / 4 (4H and every base are
+// multiples of 4); x = this step's recurrent product, cp = c_{t-1} of the unit already multiplied by keep_prev.
+__device__ __forceinline__ void lstm_fwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, const f32x4& gx,
+                                                float cp) {
+  const int64_t H = L.hidden, u = n >> 2;
+  const float ig = sigmoidf(x[0] + gx[0]), fg = sigmoidf(x[1] + gx[1]);
+  const float gg = tanhf(x[2] + gx[2]), og = sigmoidf(x[3] + gx[3]);
+  const float ct = fg * cp + ig * gg;
+  const float ht = og * tanhf(ct);
+  const f32x4 act = {ig, fg, gg, og};
+  *reinterpret_cast<f32x4*>(L.gates + m * 4 * H + n) = act;
+  L.c[m * H + u] = ct;
+  L.h[m * L.ldh + u] = ht;
+  L.hs[m * H + u] = ht * L.keep[m * L.keep_stride];
+}
+
+// LSTM backward cell for env m, hidden units n .. n+3; x = (dgates of the next step) . W_hh for those units.
+__device__ __forceinline__ void lstm_bwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, float keep,
+                                                float keep_prev, const f32x4& dhu, const f32x4& ct, const f32x4& cp,
+                                                const f32x4& dcin, const f32x4 (&gt)[4]) {
+  const int64_t H = L.hidden;
+  f32x4 dcout;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float ig = gt[e][0], fg = gt[e][1], gg = gt[e][2], og = gt[e][3];
+    const float dh = dhu[e] + keep * x[e];
+    const float tc = tanhf(ct[e]);
+    const float dct = dcin[e] + dh * og * (1.0f - tc * tc);
+    const f32x4 dpre = {dct * gg * ig * (1.0f - ig), dct * (cp[e] * keep_prev) * fg * (1.0f - fg),
+                        dct * ig * (1.0f - gg * gg), dh * tc * og * (1.0f - og)};
+    *reinterpret_cast<f32x4*>(L.dgates + m * 4 * H + 4 * (n + e)) = dpre;
+    dcout[e] = dct * fg * keep_prev;
+  }
+  if (!L.last) *reinterpret_cast<f32x4*>(L.dc + m * H + n) = dcout;
+}
 
 template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16, int EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_kernel(
@@ -356,8 +395,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   NtLoader<BN, BK, B16> lb;
   la.init(lda, row0, M, wave, lane);
   lb.init(ldb, col0, N, wave, lane);
-  LstmPre<EPI, TM, TN> pre;
-  pre.load(P, row0 + wm * WM, col0 + wn * WN, lane);
+  LstmPre<EPI, TM, TN, 1> pre;
+  pre.load(P, row0 + wm * WM, col0 + wn * WN, lane, 0);
   const int nfull = K / BK;
   const int nk = (K + BK - 1) / BK;
   auto issue = [&](int kt, int stage) {
@@ -450,45 +489,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         if (m >= M || !n_in) continue;
         const int64_t mm = m;
         if constexpr (EPI == EPI_LSTM_FWD) {
-          // columns n .. n+3: gates i, f, g, o of hidden unit u of env m (4H and every base are multiples of 4)
-          const LstmArgs& L = P.lstm;
-          const int64_t H = L.hidden, u = n >> 2;
-          const f32x4 gx = pre.gx[i][j][rr];
-          const float ig = sigmoidf(x[0] + gx[0]), fg = sigmoidf(x[1] + gx[1]);
-          const float gg = tanhf(x[2] + gx[2]), og = sigmoidf(x[3] + gx[3]);
-          const float cp = pre.cp[i][j][rr] * pre.kp[i][rr];
-          const float ct = fg * cp + ig * gg;
-          const float ht = og * tanhf(ct);
-          const f32x4 act = {ig, fg, gg, og};
-          *reinterpret_cast<f32x4*>(L.gates + mm * 4 * H + n) = act;
-          L.c[mm * H + u] = ct;
-          L.h[mm * L.ldh + u] = ht;
-          L.hs[mm * H + u] = ht * L.keep[mm * L.keep_stride];
+          lstm_fwd_finish(P.lstm, mm, n, x, pre.gx[i][j][rr], pre.cp[i][j][rr] * pre.kp[i][rr]);
           continue;
         } else if constexpr (EPI == EPI_LSTM_BWD) {
-          // columns n .. n+3: hidden units n .. n+3 of env m; x = (dgates of the next step) . W_hh
-          const LstmArgs& L = P.lstm;
-          const int64_t H = L.hidden;
-          const float keep = pre.keep[i][rr];
-          const float keep_prev = pre.kp[i][rr];
-          const f32x4 dhu = pre.dh[i][j][rr];
-          const f32x4 ct = pre.ct[i][j][rr];
-          const f32x4 cp = pre.cp[i][j][rr];
-          const f32x4 dcin = pre.dc[i][j][rr];
-          f32x4 dcout;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const f32x4 gt = pre.gt[i][j][rr][e];
-            const float ig = gt[0], fg = gt[1], gg = gt[2], og = gt[3];
-            const float dh = dhu[e] + keep * x[e];
-            const float tc = tanhf(ct[e]);
-            const float dct = dcin[e] + dh * og * (1.0f - tc * tc);
-            const f32x4 dpre = {dct * gg * ig * (1.0f - ig), dct * (cp[e] * keep_prev) * fg * (1.0f - fg),
-                                dct * ig * (1.0f - gg * gg), dh * tc * og * (1.0f - og)};
-            *reinterpret_cast<f32x4*>(L.dgates + mm * 4 * H + 4 * (n + e)) = dpre;
-            dcout[e] = dct * fg * keep_prev;
-          }
-          if (!L.last) *reinterpret_cast<f32x4*>(L.dc + mm * H + n) = dcout;
+          lstm_bwd_finish(P.lstm, mm, n, x, pre.keep[i][rr], pre.kp[i][rr], pre.dh[i][j][rr], pre.ct[i][j][rr],
+                          pre.cp[i][j][rr], pre.dc[i][j][rr], pre.gt[i][j][rr]);
           continue;
         }
         f32x4 o, o2;
@@ -532,6 +537,126 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
           }
         }
       }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// NT with the k range split over the block's waves, for the LSTM step products (EPI_LSTM_FWD / _BWD only; operands
+// 16-byte aligned).  A step's product is small (E x 4H forward, E x H backward) and long in k (H, 4H): one 32 x 32
+// tile per wave with the whole k range is a long dependent MFMA chain, and 64 x 64 blocks leave CUs idle.  Here the 4
+// waves form a (BM / 32) x (BN / 32) grid of 32 x 32 tiles times KS = 4 / (grid size) k splits: split ks takes
+// k-groups [ks G / KS, (ks + 1) G / KS) of every slab.  The KS partial tiles meet in the epilogue's LDS patches,
+// summed in a fixed order, and each split finishes 4 / KS of the row rounds.
+// ------------------------------------------------------------------------------------------------------------------
+
+template <int BM, int BN, int BK, int S, int OCC, int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_ks_kernel(
+    const Group g) {
+  static_assert(EPI == EPI_LSTM_FWD || EPI == EPI_LSTM_BWD, "k-split kernel: LSTM step epilogues");
+  constexpr int WGM = BM / 32, WGN = BN / 32, NWT = WGM * WGN, KS = 4 / NWT;
+  static_assert(BM % 32 == 0 && BN % 32 == 0 && NWT * KS == 4, "4 waves = wave tiles x k splits");
+  constexpr int G = BK / 8, GPW = G / KS;
+  static_assert(G % KS == 0 && GPW >= 1, "every split takes whole k-groups of each slab");
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int PS = 36;  // epilogue patch row stride (as in gemm_nt_kernel)
+  constexpr int LDS = S * STAGE > 4 * 32 * PS ? S * STAGE : 4 * 32 * PS;
+  constexpr int L = NtLoader<BM, BK, true>::PER + NtLoader<BN, BK, true>::PER;
+  __shared__ __align__(16) float lds[LDS];
+
+  const TileCoord tc = locate(g);
+  const Problem& P = g.p[tc.pi];
+  const float* const A = P.A;
+  const float* const B = P.B;
+  const int64_t lda = P.lda, ldb = P.ldb;
+  const int row0 = tc.tm * BM, col0 = tc.tn * BN;
+  const int M = P.M, N = P.N, K = P.K;
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int ks = wave / NWT, wt = wave % NWT, wm = wt / WGN, wn = wt % WGN;
+
+  f32x16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+
+  NtLoader<BM, BK, true> la;
+  NtLoader<BN, BK, true> lb;
+  la.init(lda, row0, M, wave, lane);
+  lb.init(ldb, col0, N, wave, lane);
+  LstmPre<EPI, 1, 1, KS> pre;
+  pre.load(P, row0 + 32 * wm, col0 + 32 * wn, lane, ks);
+  const int nfull = K / BK;
+  const int nk = (K + BK - 1) / BK;
+  auto issue = [&](int kt, int stage) {
+    float* st = lds + stage * STAGE;
+    const int k0 = kt * BK;
+    if (kt < nfull) {
+      la.issue(A + k0, st, wave);
+      lb.issue(B + k0, st + BM * BK, wave);
+    } else {
+      nt_masked<BM, BK>(A, lda, row0, M, k0, K, st);
+      nt_masked<BN, BK>(B, ldb, col0, N, k0, K, st + BM * BK);
+    }
+  };
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nk) issue(st, st);
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_slab<L, S>(min(S - 2, nk - 1 - kt));
+    lds_barrier();
+    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
+    const float* As = lds + (kt % S) * STAGE;
+    const float* Bs = As + BM * BK;
+    f32x4 fa[2], fb[2];
+    auto load_group = [&](int buf, int gi) {
+      const int c = 2 * gi + (lane >> 5);
+      const int ra = 32 * wm + (lane & 31), rb = 32 * wn + (lane & 31);
+      fa[buf] = *reinterpret_cast<const f32x4*>(As + ra * BK + 4 * (c ^ nt_swz<BK>(ra)));
+      fb[buf] = *reinterpret_cast<const f32x4*>(Bs + rb * BK + 4 * (c ^ nt_swz<BK>(rb)));
+    };
+    load_group(0, ks * GPW);
+#pragma unroll
+    for (int q = 0; q < GPW; ++q) {
+      if (q + 1 < GPW) load_group((q + 1) & 1, ks * GPW + q + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[q & 1][s4], fa[q & 1][s4], acc, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Epilogue: every wave stores its partial tile (transposed accumulator, as in gemm_nt_kernel) into its own patch;
+  // then split ks sums the KS patches of its tile, split 0 first, for its row rounds and finishes them.
+  lds_barrier();
+  {
+    float* patch = lds + wave * 32 * PS;
+    const int h = lane >> 5;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      f32x4 x = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+      *reinterpret_cast<f32x4*>(patch + (lane & 31) * PS + 8 * q + 4 * h) = x;
+    }
+  }
+  lds_barrier();
+  const int pr = lane >> 3, pc = 4 * (lane & 7);
+  const int n = col0 + 32 * wn + pc;
+#pragma unroll
+  for (int k = 0; k < 4 / KS; ++k) {
+    const int r = pr + 8 * (ks + KS * k);
+    f32x4 x = *reinterpret_cast<const f32x4*>(lds + wt * 32 * PS + r * PS + pc);
+#pragma unroll
+    for (int sp = 1; sp < KS; ++sp) {
+      const f32x4 y = *reinterpret_cast<const f32x4*>(lds + (sp * NWT + wt) * 32 * PS + r * PS + pc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] += y[e];
+    }
+    const int m = row0 + 32 * wm + r;
+    if (m >= M || n >= N) continue;
+    if constexpr (EPI == EPI_LSTM_FWD) {
+      lstm_fwd_finish(P.lstm, m, n, x, pre.gx[0][0][k], pre.cp[0][0][k] * pre.kp[0][k]);
+    } else {
+      lstm_bwd_finish(P.lstm, m, n, x, pre.keep[0][k], pre.kp[0][k], pre.dh[0][0][k], pre.ct[0][0][k],
+                      pre.cp[0][0][k], pre.dc[0][0][k], pre.gt[0][0][k]);
     }
   }
 }
@@ -766,6 +891,16 @@ int launch_nt_aligned(Group& g, int count, hipStream_t s, const char* name) {
   if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
   hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  return check_launch(name);
+}
+
+// The k-split LSTM step kernel (operands known to allow 16-byte loads).
+template <int BM, int BN, int BK, int S, int OCC, int EPI>
+int launch_nt_ks(Group& g, int count, hipStream_t s, const char* name) {
+  int blocks;
+  if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
+  if (blocks == 0) return PPO_OK;
+  hipLaunchKernelGGL((gemm_nt_ks_kernel<BM, BN, BK, S, OCC, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   return check_launch(name);
 }
 

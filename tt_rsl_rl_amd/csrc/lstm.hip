@@ -8,6 +8,8 @@
 // columns = hidden units) and its epilogue applies the cell derivatives, carrying dL/dc to the previous step.
 // Actor and critic share every launch.  The two weight gradients are plain split-K GEMMs over all T*E rows
 // (ppo_linear_bwd_dw: dgates^T hs and dgates^T x).
+#include <cstring>
+
 #include "gemm_core.hpp"
 
 namespace ppo {
@@ -160,15 +162,25 @@ int check_seq(const ppo_lstm_seq_problem* probs, int32_t count, int64_t steps, i
   return PPO_OK;
 }
 
-// Per-step GEMMs on 64 x 64 tiles (a step has only E x 4H forward or E x H backward outputs).  The backward step's
-// E x H output gives at most one block per CU, so its instantiation trades occupancy for the registers that hold the
-// prefetched epilogue operands (waves_per_eu 2).
+// Per-step GEMM configuration: "64x64" is the plain NT kernel (whole k range per wave); the others are the k-split
+// kernel with the named block tile ("32x64": 2 splits, "32x32k64": 4 splits over 64-deep slabs, ...).  Measured at
+// E = 1024, H = 256 (two problems): the forward step (k = H) takes ~21 us with every tile, the backward step
+// (k = 4H) 31 us on 64 x 64 and 19 us on 32x32k64, whose 4 splits cut each wave's dependent MFMA chain to a quarter
+// and give 4x the blocks.  "PPO_HIP_LSTM_FWD_CFG" / "PPO_HIP_LSTM_BWD_CFG" override the defaults (tuning aid).  The
+// backward instantiations with 2 splits allow fewer waves per SIMD: their prefetched epilogue operands take
+// registers.
 template <int EPI>
 int launch_step(Group& g, int count, hipStream_t s, const char* name) {
-  if constexpr (EPI == EPI_LSTM_BWD)
-    return launch_nt_aligned<64, 64, 32, 2, 2, EPI>(g, count, s, name);
-  else
-    return launch_nt_aligned<64, 64, 32, 2, 4, EPI>(g, count, s, name);
+  constexpr bool fwd = EPI == EPI_LSTM_FWD;
+  constexpr int O2 = fwd ? 4 : 2;
+  const char* e = std::getenv(fwd ? "PPO_HIP_LSTM_FWD_CFG" : "PPO_HIP_LSTM_BWD_CFG");
+  const char* cfg = e != nullptr ? e : fwd ? "64x64" : "32x32k64";
+  if (!std::strcmp(cfg, "32x64")) return launch_nt_ks<32, 64, 32, 2, O2, EPI>(g, count, s, name);
+  if (!std::strcmp(cfg, "64x32")) return launch_nt_ks<64, 32, 32, 2, O2, EPI>(g, count, s, name);
+  if (!std::strcmp(cfg, "32x64k64")) return launch_nt_ks<32, 64, 64, 2, O2, EPI>(g, count, s, name);
+  if (!std::strcmp(cfg, "32x32k64")) return launch_nt_ks<32, 32, 64, 2, 4, EPI>(g, count, s, name);
+  if (!std::strcmp(cfg, "32x32k32")) return launch_nt_ks<32, 32, 32, 3, 4, EPI>(g, count, s, name);
+  return launch_nt_aligned<64, 64, 32, 2, O2, EPI>(g, count, s, name);
 }
 
 }  // namespace

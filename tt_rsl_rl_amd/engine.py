@@ -247,12 +247,12 @@ class UpdateEngine:
                 dw.append((buf.dz[i][:R], x, grad(lins[i].weight), grad(lins[i].bias)))
         return dw
 
-    def weight_grads(self, dw: list[tuple], R: int, phase: str = "dw") -> None:
+    def weight_grads(self, dw: list[tuple], R: int, phase: str = "dw", ws: ops.Workspace | None = None) -> None:
         """Weight gradients, as few grouped launches as the problem limit allows."""
         tm = self.timer
         tm.start(phase)
         for i in range(0, len(dw), L.MAX_LINEAR_PROBLEMS):
-            ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, self.dw_ws)
+            ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, ws if ws is not None else self.dw_ws)
         tm.stop(phase)
 
     def adam(self, step: int) -> None:
@@ -324,6 +324,9 @@ class RecurrentUpdateEngine(UpdateEngine):
             raise ValueError("num_mini_batches must be between 1 and the number of environments.")
         self.E_max = -(-self.N // M)
         super().__init__(alg)
+        # the heads' weight-grads run on a second stream (default priority) beside the LSTM backward steps
+        self.side = torch.cuda.Stream(device=self.device)
+        self.side_dw_ws = ops.Workspace(self.device)
         self.seq_a = LstmBuffers(actor.rnn, self.R_max, self.E_max, self.device)
         self.seq_c = LstmBuffers(critic.rnn, self.R_max, self.E_max, self.device)
         # row order of the table: per env slice, t-major
@@ -404,11 +407,16 @@ class RecurrentUpdateEngine(UpdateEngine):
         ops.linear_bwd_dx([(self.buf_a.dz[0][:R], la[0].weight, None, sa.dh[:R]),
                            (self.buf_c.dz[0][:R], lc[0].weight, None, sc.dh[:R])], R, self.dx_ws)
         tm.stop("dx0")
+        # the heads' weight gradients need only their dz and inputs: a side stream computes them while the
+        # latency-bound LSTM backward steps run; Adam waits for both
+        main = torch.cuda.current_stream()
+        self.side.wait_stream(main)
+        with torch.cuda.stream(self.side):
+            self.weight_grads(self.head_dw(sa.h[:R], sc.h[:R], R), R, ws=self.side_dw_ws)
         tm.start("lstm_bwd")
         self._grouped(ops.lstm_seq_bwd, qa, qc, E)
         tm.stop("lstm_bwd")
 
-        self.weight_grads(self.head_dw(sa.h[:R], sc.h[:R], R), R)
         dw = []
         for s, x in ((sa, xa), (sc, xc)):
             dw.append((s.dgates[:R], s.hs[:R], s.dw_hh_g, s.db_g))
@@ -417,4 +425,5 @@ class RecurrentUpdateEngine(UpdateEngine):
         grad = alg.flat.grad_view
         ops.lstm_unpack_grads([(s.dw_ih_g, s.dw_hh_g, s.db_g, *(grad(p) for p in m.rnn.weights))
                                for s, m in ((sa, actor), (sc, critic))])
+        main.wait_stream(self.side)
         self.adam(step)
