@@ -80,7 +80,13 @@ struct Problem {
   LstmArgs lstm;            // EPI_LSTM_*
 };
 
-__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+// Logistic function and tanh of the LSTM cell on the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32, each about
+// 1 ulp): sigma(x) = 1 / (1 + 2^(-x log2 e)), tanh(x) = 2 sigma(2x) - 1 (absolute error a few 1e-8).  Both saturate
+// at the ends: 2^(+inf) = inf and 1 / inf = 0.
+__device__ __forceinline__ float sigmoid_hw(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
+}
+__device__ __forceinline__ float tanh_hw(float x) { return 2.0f * sigmoid_hw(2.0f * x) - 1.0f; }
 
 struct Group {
   Problem p[PPO_MAX_LINEAR_PROBLEMS];
@@ -330,10 +336,10 @@ struct LstmPre<EPI_LSTM_BWD, TM, TN, KS> {
 __device__ __forceinline__ void lstm_fwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, const f32x4& gx,
                                                 float cp) {
   const int64_t H = L.hidden, u = n >> 2;
-  const float ig = sigmoidf(x[0] + gx[0]), fg = sigmoidf(x[1] + gx[1]);
-  const float gg = tanhf(x[2] + gx[2]), og = sigmoidf(x[3] + gx[3]);
+  const float ig = sigmoid_hw(x[0] + gx[0]), fg = sigmoid_hw(x[1] + gx[1]);
+  const float gg = tanh_hw(x[2] + gx[2]), og = sigmoid_hw(x[3] + gx[3]);
   const float ct = fg * cp + ig * gg;
-  const float ht = og * tanhf(ct);
+  const float ht = og * tanh_hw(ct);
   const f32x4 act = {ig, fg, gg, og};
   *reinterpret_cast<f32x4*>(L.gates + m * 4 * H + n) = act;
   L.c[m * H + u] = ct;
@@ -351,7 +357,7 @@ __device__ __forceinline__ void lstm_bwd_finish(const LstmArgs& L, int64_t m, in
   for (int e = 0; e < 4; ++e) {
     const float ig = gt[e][0], fg = gt[e][1], gg = gt[e][2], og = gt[e][3];
     const float dh = dhu[e] + keep * x[e];
-    const float tc = tanhf(ct[e]);
+    const float tc = tanh_hw(ct[e]);
     const float dct = dcin[e] + dh * og * (1.0f - tc * tc);
     const f32x4 dpre = {dct * gg * ig * (1.0f - ig), dct * (cp[e] * keep_prev) * fg * (1.0f - fg),
                         dct * ig * (1.0f - gg * gg), dh * tc * og * (1.0f - og)};
