@@ -97,6 +97,72 @@ def phase_flops(workload, R: int) -> dict[str, float]:
     return out
 
 
+def graph_ms(fn, reps: int = 50) -> float:
+    """Mean GPU time of fn's launches: `reps` calls captured in one HIP graph (kernels only) and replayed, so the
+    host's launch overhead is not in the measurement."""
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / reps
+
+
+def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
+    """Achieved bandwidth of the HBM-bound kernels against the 8 TB/s peak: algorithmic bytes per launch / mean launch
+    time.  GAE, the permutation gather and clip + Adam are timed standalone on the resident data by HIP-graph replay
+    (this runs after the timed updates; Adam steps the parameters further); the loss (+ finalize) time is the
+    instrumented pass's HIP events."""
+    import torch
+
+    from tt_rsl_rl_amd import ops
+
+    st = alg.storage
+    T, N = st.num_transitions_per_env, st.num_envs
+    B = T * N
+    A = workload["num_actions"]
+    width = sum(seg.src.shape[1] for seg in engine.segments())
+    nbytes = {
+        "gather": B * (2 * 4 * width + 8),                        # every copied float read + written, int64 index
+        "loss": R * 4 * (4 * A + 6) + R * 4 * (A + 1),            # per-row inputs + per-row output gradients
+        "adam": alg.flat.param.numel() * 36,                      # norm pass 4 B + p, g, m, v read and written
+        "gae": B * (4 + 4 + 1 + 4 + 4) + 4 * N,                   # r, V, done in; returns, advantages out
+    }
+    last = torch.randn(N, 1, device=alg.device)
+    rets, advs = torch.empty_like(st.returns), torch.empty_like(st.advantages)
+    perm = torch.randperm(B).to(alg.device)
+    f = alg.flat
+    b1, b2 = alg.betas
+    ms = {
+        "gae": graph_ms(lambda: ops.gae(st.rewards, st.values, st.dones, last, rets, advs, alg.gamma, alg.lam)),
+        "gather": graph_ms(lambda: engine.gather(perm)),
+        "adam": graph_ms(lambda: ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin,
+                                               alg.max_grad_norm, b1, b2, alg.adam_eps, 0.5, 0.5, alg.device_state,
+                                               engine.adam_ws)),
+    }
+    if "loss" in phases:
+        ms["loss"] = phases["loss"][1]
+    out = {}
+    for k, b in nbytes.items():
+        if k in ms:
+            gbs = b / (ms[k] * 1e-3) / 1e9
+            out[k] = {"bytes": b, "mean_us": round(ms[k] * 1e3, 2), "GB/s": round(gbs, 1),
+                      "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    return out
+
+
 def load_traffic(kernel_phase: str):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter summary, if present."""
     p = ROOT / "profiles" / "traffic_humanoid.json"
@@ -231,6 +297,7 @@ def main() -> int:
         roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": load_traffic(dom), "kernel": dom,
                     "flops_per_launch": flops[dom], "mean_launch_ms": round(t, 5), "launches_timed": n}
+    hbm = hbm_kernels(alg, engine, phases, workload, R)
     gemm_total = W.gemm_flops_per_update(workload, alg.num_learning_epochs)
     lstm = ""
     if "rnn" in workload:
@@ -252,6 +319,7 @@ def main() -> int:
         "update_gemm_mfma_frac": round(gemm_total / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
         "phases": phase_report,
         "roofline": roofline,
+        "hbm_kernels": hbm,
         "losses": losses,
         "cpu_baseline": None,
     }

@@ -312,11 +312,13 @@ def test_kl_is_exactly_zero_for_identical_distributions(cuda):
 # ----------------------------------------------------------------------------------------------------------------------
 
 
-def test_adam_clip_matches_torch(cuda):
+@pytest.mark.parametrize("aligned", [False, True])
+def test_adam_clip_matches_torch(cuda, aligned):
+    """Group sizes 181,021 / 51,329 (scalar path) or 181,024 / 51,332 (multiples of 4: the float4 path)."""
     ops = _ops()
     torch.manual_seed(11)
-    shapes_a = [(29,), (512, 96), (512,), (256, 512), (256,)]
-    shapes_c = [(512, 99), (512,), (1, 128), (1,)]
+    shapes_a = [(32,) if aligned else (29,), (512, 96), (512,), (256, 512), (256,)]
+    shapes_c = [(512, 99), (512,), (1, 128), (4,) if aligned else (1,)]
     pa = [torch.nn.Parameter(torch.randn(s) * 0.1) for s in shapes_a]
     pc = [torch.nn.Parameter(torch.randn(s) * 0.1) for s in shapes_c]
     opt = torch.optim.Adam(pa + pc, lr=1e-3)

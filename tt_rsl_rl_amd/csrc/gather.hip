@@ -2,8 +2,12 @@
 // (rsl_rl/modules/normalization.py:46-48), fused: one pass over the rollout per update writes the packed,
 // permuted, normalised row table that every mini-batch of every epoch then reads contiguously.
 //
-// One wavefront per destination row: each segment of the source row is read as a contiguous run of floats
-// across the lanes (coalesced), so the kernel streams HBM at ~2 x 4 B per copied float plus the 8 B index.
+// The copied floats of a row, segment after segment, are numbered 0 .. total-1 ("flat columns"); lane l of a
+// wavefront owns flat columns l, l + 64, ... (kSlots of them per pass), so consecutive lanes read consecutive floats of
+// a segment and write consecutive destination floats.  The flat column -> (segment, column) map depends only on the
+// segment widths: each wave derives it once per pass (from a copy of the segment table in LDS) and then moves
+// kRowsPerIter rows per iteration, issuing all their loads before any store so a wave waits for memory once per
+// iteration rather than once per segment.
 #include "common.hpp"
 
 #pragma clang fp contract(off)
@@ -13,31 +17,82 @@ namespace {
 
 struct GatherArgs {
   ppo_gather_segment seg[PPO_MAX_GATHER_SEGMENTS];
+  int32_t prefix[PPO_MAX_GATHER_SEGMENTS + 1];  // first flat column of each segment; prefix[num_segments] = total
   int32_t num_segments;
 };
 
+// Source pointers are global memory; read back from the LDS copy of the segment table they would otherwise be
+// generic (flat) pointers, whose loads also count as LDS operations and defeat the wait counters.
+typedef const float __attribute__((address_space(1))) global_float;
+
 constexpr int kGatherThreads = 256;
-constexpr int kRowsPerBlock = kGatherThreads / kWave;
+constexpr int kWavesPerBlock = kGatherThreads / kWave;
+constexpr int kSlots = 8;        // flat columns per lane per pass: 512 floats of a row
+constexpr int kRowsPerIter = 2;  // rows in flight per wave
 
 __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const int64_t* __restrict__ perm, int64_t rows,
-                                                                     int64_t src_rows, GatherArgs args, float* __restrict__ dst,
-                                                                     int64_t dst_stride) {
+                                                                     int64_t src_rows, GatherArgs args,
+                                                                     float* __restrict__ dst, int64_t dst_stride) {
+  __shared__ ppo_gather_segment seg[PPO_MAX_GATHER_SEGMENTS];
+  if (threadIdx.x < args.num_segments) seg[threadIdx.x] = args.seg[threadIdx.x];
+  __syncthreads();
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
-  const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kRowsPerBlock;
-  for (int64_t j = wave_id; j < rows; j += wave_count) {
-    const int64_t src_row = perm[j];
-    if (src_row < 0 || src_row >= src_rows) continue;  // never read outside the source (the host checks perm)
-    float* out = dst + j * dst_stride;
-    for (int s = 0; s < args.num_segments; ++s) {
-      const ppo_gather_segment& g = args.seg[s];
-      const float* in = g.src + src_row * g.src_stride;
-      float* o = out + g.dst_col;
-      if (g.norm_mean != nullptr) {
-        for (int c = lane; c < g.width; c += kWave) o[c] = (in[c] - g.norm_mean[c]) / (g.norm_std[c] + g.norm_eps);
-      } else {
-        for (int c = lane; c < g.width; c += kWave) o[c] = in[c];
+  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const int total = args.prefix[args.num_segments];
+  for (int f0 = 0; f0 < total; f0 += kWave * kSlots) {
+    // this lane's flat columns of the pass -> source base, stride, destination column, normaliser
+    global_float* src[kSlots];
+    int64_t stride[kSlots];
+    int dcol[kSlots];
+    bool valid[kSlots];
+    float mu[kSlots], den[kSlots];
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) {
+      const int fc = f0 + lane + kWave * k;
+      int s = 0;
+      for (int i = 1; i < args.num_segments; ++i) s = fc >= args.prefix[i] ? i : s;
+      const int col = fc - args.prefix[s];
+      const ppo_gather_segment& g = seg[s];
+      const bool in = fc < total;
+      // a lane without a column this slot reads element (0, 0) of the first segment and discards it
+      src[k] = (global_float*)(in ? g.src + col : seg[0].src);  // generic -> global: an address-space cast
+      valid[k] = in;
+      stride[k] = in ? g.src_stride : 0;
+      dcol[k] = g.dst_col + col;
+      const bool norm = in && g.norm_mean != nullptr;
+      mu[k] = norm ? g.norm_mean[col] : 0.0f;
+      den[k] = norm ? g.norm_std[col] + g.norm_eps : 1.0f;
+    }
+    for (int64_t j0 = wave_id * kRowsPerIter; j0 < rows; j0 += wave_count * kRowsPerIter) {
+      int64_t sr[kRowsPerIter];
+#pragma unroll
+      for (int r = 0; r < kRowsPerIter; ++r) {
+        const int64_t j = j0 + r;
+        const int64_t p = j < rows ? perm[j] : -1;
+        sr[r] = p >= 0 && p < src_rows ? p : -1;  // never read outside the source (the host checks perm)
       }
+      // every load unconditional and in straight-line code (rows outside [0, rows) read source row 0), so the
+      // wave issues all of them before it waits
+      float v[kRowsPerIter][kSlots];
+#pragma unroll
+      for (int r = 0; r < kRowsPerIter; ++r) {
+        const int64_t row = sr[r] >= 0 ? sr[r] : 0;
+#pragma unroll
+        for (int k = 0; k < kSlots; ++k) v[r][k] = src[k][row * stride[k]];
+      }
+      // then all arithmetic (plain copies take mu = 0, den = 1: (x - 0) / 1 == x exactly), then all stores: a store
+      // counts in the same counter as the loads, so interleaving them would make every wait drain the stores too
+#pragma unroll
+      for (int r = 0; r < kRowsPerIter; ++r)
+#pragma unroll
+        for (int k = 0; k < kSlots; ++k) v[r][k] = (v[r][k] - mu[k]) / den[k];
+      __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic above the (predicated) stores
+#pragma unroll
+      for (int r = 0; r < kRowsPerIter; ++r)
+#pragma unroll
+        for (int k = 0; k < kSlots; ++k)
+          if (sr[r] >= 0 && valid[k]) dst[(j0 + r) * dst_stride + dcol[k]] = v[r][k];
     }
   }
 }
@@ -70,6 +125,7 @@ extern "C" int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_ro
               "ppo_gather_rows: num_segments=%d outside [1, %d]", num_segments, PPO_MAX_GATHER_SEGMENTS);
   GatherArgs args{};
   args.num_segments = num_segments;
+  int64_t total = 0;
   for (int s = 0; s < num_segments; ++s) {
     const ppo_gather_segment& g = segments[s];
     PPO_REQUIRE(g.src != nullptr && g.width > 0 && g.src_stride >= g.width && g.dst_col >= 0,
@@ -81,8 +137,13 @@ extern "C" int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_ro
     PPO_REQUIRE(g.norm_mean == nullptr || g.norm_std != nullptr, "ppo_gather_rows: segment %d has mean but no std",
                 s);
     args.seg[s] = g;
+    args.prefix[s] = static_cast<int32_t>(total);
+    total += g.width;
+    PPO_REQUIRE(total <= INT32_MAX / 2, "ppo_gather_rows: rows of %lld floats are too wide", (long long)total);
   }
-  const int64_t blocks = std::min<int64_t>(ceil_div(rows, kRowsPerBlock), 65536);
+  args.prefix[num_segments] = static_cast<int32_t>(total);
+  const int64_t blocks =
+      std::min<int64_t>(ceil_div(rows, static_cast<int64_t>(kWavesPerBlock) * kRowsPerIter), 65536);
   hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGatherThreads), 0,
                      static_cast<hipStream_t>(stream), perm, rows, src_rows, args, dst, dst_stride);
   return check_launch("gather_rows_kernel");

@@ -15,6 +15,7 @@ namespace {
 
 constexpr int kAdamThreads = 256;
 constexpr int kChunk = 1024;  // ~420 blocks for the humanoid models: every CU busy
+static_assert(kChunk == 4 * kAdamThreads, "vector path: one float4 per thread per chunk");
 
 struct GroupTable {
   int64_t begin[PPO_MAX_PARAM_GROUPS + 1];
@@ -40,6 +41,9 @@ __device__ inline double block_sum256(double x, double* red) {
   return s;  // same value in every thread
 }
 
+// VEC: every group boundary is a multiple of 4 floats (the host checks), so each chunk is whole 16-byte vectors:
+// one float4 per thread per 1024-element chunk.
+template <bool VEC>
 __global__ __launch_bounds__(kAdamThreads) void grad_sqnorm_kernel(const float* __restrict__ grads, GroupTable t,
                                                                    double* __restrict__ partials) {
   __shared__ double red[kAdamThreads / 64];
@@ -48,9 +52,18 @@ __global__ __launch_bounds__(kAdamThreads) void grad_sqnorm_kernel(const float* 
   const int64_t lo = t.begin[g] + static_cast<int64_t>(chunk - t.first_chunk[g]) * kChunk;
   const int64_t hi = min(lo + kChunk, t.begin[g + 1]);
   double acc = 0.0;
-  for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
-    const double v = grads[i];
-    acc += v * v;
+  if constexpr (VEC) {
+    const int64_t i = lo + 4 * static_cast<int64_t>(threadIdx.x);
+    if (i < hi) {
+      const float4 q = *reinterpret_cast<const float4*>(grads + i);
+      const double a = q.x, b = q.y, c = q.z, d = q.w;
+      acc = ((a * a + b * b) + c * c) + d * d;
+    }
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
+      const double v = grads[i];
+      acc += v * v;
+    }
   }
   const double s = block_sum256(acc, red);
   if (threadIdx.x == 0) partials[chunk] = s;
@@ -61,6 +74,18 @@ struct AdamScalars {
   double bc1;
 };
 
+// One parameter's update in torch's fp32 operation order.
+__device__ __forceinline__ void adam_elem(float& p, float& g, float& m, float& v, float coef, float neg_step,
+                                          const AdamScalars& s) {
+  g = g * coef;
+  m = m + s.w1 * (g - m);
+  v = v * s.b2;
+  v = v + (s.c2 * g) * g;
+  const float denom = sqrtf(v) / s.bc2_sqrt + s.eps;
+  p = p + (neg_step * m) / denom;
+}
+
+template <bool VEC>
 __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ params, float* __restrict__ grads,
                                                             float* __restrict__ exp_avg,
                                                             float* __restrict__ exp_avg_sq, GroupTable t,
@@ -82,18 +107,31 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
   }
   const int64_t lo = t.begin[g] + static_cast<int64_t>(chunk - t.first_chunk[g]) * kChunk;
   const int64_t hi = min(lo + kChunk, t.begin[g + 1]);
-  for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
-    const float gr = grads[i] * coef;
-    grads[i] = gr;
-    float m = exp_avg[i];
-    m = m + s.w1 * (gr - m);
-    float v = exp_avg_sq[i];
-    v = v * s.b2;
-    v = v + (s.c2 * gr) * gr;
-    const float denom = sqrtf(v) / s.bc2_sqrt + s.eps;
-    params[i] = params[i] + (neg_step * m) / denom;
-    exp_avg[i] = m;
-    exp_avg_sq[i] = v;
+  if constexpr (VEC) {
+    const int64_t i = lo + 4 * static_cast<int64_t>(threadIdx.x);
+    if (i < hi) {
+      float4 p = *reinterpret_cast<const float4*>(params + i);
+      float4 gr = *reinterpret_cast<const float4*>(grads + i);
+      float4 m = *reinterpret_cast<const float4*>(exp_avg + i);
+      float4 v = *reinterpret_cast<const float4*>(exp_avg_sq + i);
+      adam_elem(p.x, gr.x, m.x, v.x, coef, neg_step, s);
+      adam_elem(p.y, gr.y, m.y, v.y, coef, neg_step, s);
+      adam_elem(p.z, gr.z, m.z, v.z, coef, neg_step, s);
+      adam_elem(p.w, gr.w, m.w, v.w, coef, neg_step, s);
+      *reinterpret_cast<float4*>(params + i) = p;
+      *reinterpret_cast<float4*>(grads + i) = gr;
+      *reinterpret_cast<float4*>(exp_avg + i) = m;
+      *reinterpret_cast<float4*>(exp_avg_sq + i) = v;
+    }
+  } else {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
+      float p = params[i], gr = grads[i], m = exp_avg[i], v = exp_avg_sq[i];
+      adam_elem(p, gr, m, v, coef, neg_step, s);
+      params[i] = p;
+      grads[i] = gr;
+      exp_avg[i] = m;
+      exp_avg_sq[i] = v;
+    }
   }
 }
 
@@ -153,10 +191,23 @@ extern "C" int ppo_adam_step(float* params, float* grads, float* exp_avg, float*
   s.bc2_sqrt = static_cast<float>(bc2_sqrt);
   double* partials = static_cast<double*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(grad_sqnorm_kernel, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, partials);
+  bool vec = true;
+  const void* bufs[] = {params, grads, exp_avg, exp_avg_sq};
+  for (const void* b : bufs) vec = vec && reinterpret_cast<uintptr_t>(b) % 16 == 0;
+  for (int g = 0; g <= num_groups; ++g) vec = vec && group_begin[g] % 4 == 0;
+  if (vec) {
+    hipLaunchKernelGGL(grad_sqnorm_kernel<true>, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, partials);
+  } else {
+    hipLaunchKernelGGL(grad_sqnorm_kernel<false>, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, partials);
+  }
   rc = check_launch("grad_sqnorm_kernel");
   if (rc != PPO_OK) return rc;
-  hipLaunchKernelGGL(adam_kernel, dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg, exp_avg_sq, t, s,
-                     partials, state);
+  if (vec) {
+    hipLaunchKernelGGL(adam_kernel<true>, dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg, exp_avg_sq,
+                       t, s, partials, state);
+  } else {
+    hipLaunchKernelGGL(adam_kernel<false>, dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
+                       exp_avg_sq, t, s, partials, state);
+  }
   return check_launch("adam_kernel");
 }
