@@ -29,13 +29,15 @@
 namespace ppo {
 namespace {
 
-// Fixed-order reduction of split-K weight-grad partials: dw = sum_s partial[s], db = sum_s colsum[s].
+// Fixed-order reduction of split-K weight-grad partials: dw = sum_s partial[s], db = sum_s colsum[s].  A work item
+// is 4 consecutive columns of one output row (the partials' rows are padded to ld = round4(in), so the loads are
+// float4), summed split after split (every element in the same order as a scalar loop), then the bias entries.
 struct ReduceItem {
   const float* partial;  // [splits, out, ld]
   const double* colsum;  // [splits, out]
   float* dw;
   float* db;
-  int64_t begin;         // first flat element of this item in the launch
+  int64_t begin;         // first work item of this problem in the launch
   int64_t stride;        // floats between splits
   int32_t out, in, ld, splits;
 };
@@ -53,19 +55,26 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
     for (int i = 1; i < PPO_MAX_LINEAR_PROBLEMS; ++i)
       if (i < g.count && e >= g.it[i].begin) pi = i;
     const ReduceItem& R = g.it[pi];
-    const int64_t local = e - R.begin;
-    const int64_t nw = static_cast<int64_t>(R.out) * R.in;
-    if (local < nw) {
-      const int64_t o = local / R.in, i = local - o * R.in;
-      const float* src = R.partial + o * R.ld + i;
-      float s = 0.0f;
-      for (int k = 0; k < R.splits; ++k) s += src[k * R.stride];
-      R.dw[local] = s;
+    const int local = static_cast<int>(e - R.begin);  // < out * (ld / 4 + 1): 32-bit (checked on the host)
+    const int q4 = R.ld >> 2;
+    if (local < R.out * q4) {
+      const int o = local / q4, i = 4 * (local - o * q4);
+      const float* src = R.partial + static_cast<int64_t>(o) * R.ld + i;
+      f32x4 acc = *reinterpret_cast<const f32x4*>(src);
+      for (int k = 1; k < R.splits; ++k) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + k * R.stride);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += v[c];
+      }
+      float* out = R.dw + static_cast<int64_t>(o) * R.in + i;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (i + c < R.in) out[c] = acc[c];
     } else {
-      const int64_t o = local - nw;
-      double s = 0.0;
-      for (int k = 0; k < R.splits; ++k) s += R.colsum[k * static_cast<int64_t>(R.out) + o];
-      R.db[o] = static_cast<float>(s);
+      const int o = local - R.out * q4;
+      double acc = 0.0;
+      for (int k = 0; k < R.splits; ++k) acc += R.colsum[k * static_cast<int64_t>(R.out) + o];
+      R.db[o] = static_cast<float>(acc);
     }
   }
 }
@@ -104,15 +113,19 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TransposeGroup g) 
   }
 }
 
-// Weight-grad: 128 x 128 tiles; split-K over the rows so that the launch covers the chip, in chunks that are
-// multiples of the deepest (64-row) slab.  "PPO_HIP_DW_CFG" (bk32s2o2 / bk16s2o3 / bk16s3o3) and "PPO_HIP_DW_BLOCKS" (target block
-// count) override the defaults (tuning aids).
+// Weight-grad: 128 x 128 tiles; split-K over the rows, in chunks that are multiples of the deepest (64-row) slab.
+// The split count fills ONE wave of resident blocks and no more: the default tile runs two blocks per CU, so 512
+// blocks on gfx950's 256 CUs.  A launch of 1,050 blocks (the humanoid weight-grads' 30 tiles x 35 splits) leaves its
+// last 26 blocks alone on the chip for a third of the kernel time; 30 x 17 = 510 blocks measured 280 us against 324.
+// "PPO_HIP_DW_CFG" (bk32s2o2 / bk16s2o3 / bk16s3o3) and "PPO_HIP_DW_BLOCKS" (resident-block capacity) override the
+// defaults (tuning aids).  Host arithmetic only: the workspace query must give the same plan without a device.
 constexpr int kDwBM = 128, kDwBN = 128, kDwChunk = 64;
+constexpr int kDwConcurrentBlocks = 2 * 256;
 
 int dw_splits(int64_t tiles, int64_t rows) {
   const char* e = std::getenv("PPO_HIP_DW_BLOCKS");
-  const int64_t target = e ? std::max(1, std::atoi(e)) : 1024;
-  int64_t s = ceil_div(target, std::max<int64_t>(tiles, 1));
+  const int64_t capacity = e ? std::max(1, std::atoi(e)) : kDwConcurrentBlocks;
+  int64_t s = capacity / std::max<int64_t>(tiles, 1);
   s = std::min<int64_t>(s, std::max<int64_t>(1, rows / 256));
   s = std::max<int64_t>(1, std::min<int64_t>(s, 256));
   return static_cast<int>(s);
@@ -296,6 +309,8 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     PPO_REQUIRE(q.dz && q.x && q.dw && q.db, "ppo_linear_bwd_dw: problem %d has a null pointer", i);
     PPO_REQUIRE(q.in_features > 0 && q.out_features > 0, "ppo_linear_bwd_dw: problem %d features", i);
     PPO_REQUIRE(q.lddz >= q.out_features && q.ldx >= q.in_features, "ppo_linear_bwd_dw: problem %d leading dims", i);
+    PPO_REQUIRE(static_cast<int64_t>(q.out_features) * (round4(q.in_features) + 4) < (int64_t(1) << 31),
+                "ppo_linear_bwd_dw: problem %d: weight of %d x %d is too large", i, q.out_features, q.in_features);
   }
   const DwPlan plan = plan_dw(problems, count, rows);
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total_floats * sizeof(float),
@@ -322,7 +337,7 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     r.out = q.out_features; r.in = q.in_features; r.ld = static_cast<int>(ldp); r.splits = plan.splits[i];
     r.stride = p.partial_stride;
     r.begin = total;
-    total += static_cast<int64_t>(q.out_features) * q.in_features + q.out_features;
+    total += static_cast<int64_t>(q.out_features) * (ldp / 4 + 1);
   }
   for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) rg.it[i].begin = INT64_MAX;
   rg.count = count;
