@@ -234,18 +234,18 @@ def test_state_dict_and_checkpoint_round_trip(tmp_path):
     assert fresh.learning_rate == ora.learning_rate
 
 
-def test_full_size_humanoid_update_properties():
-    """At the benchmark size (4096 envs x 24 steps, [512, 256, 128], 29 actions): the update runs, the losses are
-    finite, the LR only takes values the rule can produce, parameters moved by at most 20 Adam steps' worth, and
-    two identical updates give bit-identical parameters (deterministic reductions)."""
+@pytest.mark.parametrize("name", ["humanoid", "flat48_65k", "lstm256"])
+def test_full_size_update_properties(name):
+    """At full size (humanoid and lstm256: 4096 envs x 24 steps; flat48_65k: 65,536 envs x 24 steps, mini-batches of
+    393,216 rows), where the CPU oracle is too slow to run: the update runs, the losses are finite, parameters moved
+    by at most 20 Adam steps' worth (the lr is clamped to [1e-5, 1e-2]), and two identical updates give bit-identical
+    parameters (deterministic reductions).  lstm256 starts its sequences from random saved states."""
     from tests.parity import make_hip
 
-    w = R.WORKLOADS["humanoid"]
+    w = R.WORKLOADS[name]
     results = []
     for _ in range(2):
-        ora, roll = None, None
         hip = make_hip(w, seed=0)
-        torch.manual_seed(7)
         g = torch.Generator().manual_seed(7)
         st = hip.storage
         for k, v in st.observations.items():
@@ -254,18 +254,25 @@ def test_full_size_humanoid_update_properties():
         st.rewards.copy_(torch.randn(st.rewards.shape, generator=g) * 0.2)
         st.values.copy_(torch.randn(st.values.shape, generator=g))
         st.dones.copy_((torch.rand(st.dones.shape, generator=g) < 0.01).to(torch.uint8))
-        A = w["num_actions"]
         mean = torch.randn(st.actions.shape, generator=g)
         st.distribution_params = (mean.to(hip.device), torch.ones_like(st.actions))
         st.actions_log_prob.copy_(torch.distributions.Normal(mean, 1.0).log_prob(st.actions.cpu()).sum(-1, keepdim=True))
+        if "rnn" in w:
+            H, T, N = w["rnn"]["rnn_hidden_dim"], w["steps"], w["num_envs"]
+            for side in ("a", "c"):
+                setattr(st, f"saved_hidden_state_{side}",
+                        [(0.5 * torch.randn(T, 1, N, H, generator=g)).to(hip.device) for _ in range(2)])
         st.step = st.num_transitions_per_env
         hip.compute_returns_from(torch.randn(w["num_envs"], 1, generator=g).to(hip.device))
-        p0 = torch.cat([p.detach().reshape(-1).clone() for p in hip.actor.parameters()])
+        params = list(hip.actor.parameters()) + list(hip.critic.parameters())
+        p0 = torch.cat([p.detach().reshape(-1).clone() for p in params])
         torch.manual_seed(1)
         out = hip.update()
-        p1 = torch.cat([p.detach().reshape(-1) for p in hip.actor.parameters()])
-        assert all(torch.isfinite(torch.tensor(v)) for v in out.values())
-        assert (p1 - p0).abs().max().item() <= 20 * 1e-2 * 1.01  # lr is clamped to [1e-5, 1e-2]
+        p1 = torch.cat([p.detach().reshape(-1) for p in params])
+        assert all(torch.isfinite(torch.tensor(v)) for v in out.values()), out
+        assert torch.isfinite(p1).all()
+        assert (p1 - p0).abs().max().item() <= 20 * 1e-2 * 1.01
+        assert (p1 != p0).any()
         results.append(p1.cpu())
         del hip
     assert torch.equal(results[0], results[1]), "the update must be deterministic"
