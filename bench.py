@@ -16,6 +16,7 @@ Prints ONE JSON line.  Alongside the GPU figure it reports:
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import statistics
@@ -274,10 +275,13 @@ def main() -> int:
     gemm_phases = [k for k in phases if k in flops]
     dom = max(gemm_phases, key=lambda k: total_ms[k])
 
-    # Timed region: events only around the dominant kernel's launches (on the stream the kernels use).
+    # Timed region: events only around the dominant kernel's launches (on the stream the kernels use).  The Python heap
+    # is collected and frozen first, so a collection of the objects built so far does not land inside it.
     timer = PhaseTimer(only={dom})
     timer.enabled = not args.no_phase_events
     engine.timer = timer
+    gc.collect()
+    gc.freeze()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     per = []
@@ -315,6 +319,8 @@ def main() -> int:
                    "num_envs": workload["num_envs"], "steps_per_env": workload["steps"], "mini_batch_rows": R,
                    "parallelism": "single GPU"},
         "ms_per_update_median": round(statistics.median(per) * 1e3, 3),
+        "ms_per_update_min_p90_max": [round(min(per) * 1e3, 3), round(sorted(per)[int(0.9 * (len(per) - 1))] * 1e3, 3),
+                                      round(max(per) * 1e3, 3)],
         "update_gemm_tflops": round(gemm_total / (ms * 1e-3) / 1e12, 2),
         "update_gemm_mfma_frac": round(gemm_total / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
         "phases": phase_report,
