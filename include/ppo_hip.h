@@ -86,6 +86,13 @@ typedef struct ppo_gather_segment {
 int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_rows, const ppo_gather_segment* segments,
                     int32_t num_segments, float* dst, int64_t dst_stride, ppo_stream_t stream);
 
+/* The permutation itself, host code: torch.randperm(n) as drawn from torch's CPU generator
+ * (rsl_rl/storage/rollout_storage.py:232), i.e. a Fisher-Yates shuffle of 0..n-1 with z_i = draw_i mod (n - i)
+ * over the generator's 32-bit MT19937 stream.  generator_state: the record torch.get_rng_state() returns
+ * (state_bytes = 5056), advanced in place by the n - 1 draws (write it back with torch.set_rng_state()).
+ * out: int64 [n] host memory.  PPO_EINVAL when the record's layout is not recognised (nothing is written). */
+int ppo_host_randperm(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t* out);
+
 /* ------------------------------------------------------------------------------------------------------------------
  * A6  Linear layers of rsl_rl/modules/mlp.py:27-95 (nn.Linear + nn.ELU), forward and hand-written backward, as fp32
  * MFMA GEMMs.  One call runs up to PPO_MAX_LINEAR_PROBLEMS independent problems (e.g. actor and critic) over the

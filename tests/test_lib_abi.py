@@ -11,6 +11,7 @@ import subprocess
 from pathlib import Path
 
 import pytest
+import torch
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "ppo_hip.h"
@@ -120,3 +121,36 @@ def test_argument_validation_reports_errors_without_a_gpu():
         _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)
     probs = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512)])
     assert lib.ppo_linear_bwd_dw_workspace_bytes(probs, 1, 24576) >= 4 * 512 * 96
+
+
+@pytest.mark.parametrize("seed, n, pre", [(0, 1, 0), (1, 2, 0), (3, 5, 0), (5, 624, 0), (5, 625, 3), (11, 1249, 700),
+                                          (7, 98304, 0), (2, 1572864, 5)])
+def test_host_randperm_is_torch_randperm(seed, n, pre):
+    """The update's permutation (rsl_rl/storage/rollout_storage.py:232) computed natively equals torch.randperm(n) on
+    the CPU generator, and leaves the generator exactly where torch.randperm leaves it (state record and the draws
+    that follow), from a freshly seeded generator and from one part-way through its stream with a cached normal."""
+    from tt_rsl_rl_amd import ops
+
+    torch.manual_seed(seed)
+    if pre:
+        torch.rand(pre)
+        torch.randn(3)
+    start = torch.get_rng_state()
+    ref = torch.randperm(n)
+    ref_state, ref_next = torch.get_rng_state(), torch.rand(4)
+    torch.set_rng_state(start)
+    got = ops.host_randperm(n)
+    assert torch.equal(got, ref)
+    assert torch.equal(torch.get_rng_state(), ref_state)
+    assert torch.equal(torch.rand(4), ref_next)
+
+
+def test_host_randperm_rejects_unknown_generator_records():
+    from tt_rsl_rl_amd import _lib
+
+    lib = _lib.load()
+    rec = (ctypes.c_uint8 * 5056)()  # all zero: `seeded` is 0
+    out = (ctypes.c_int64 * 4)()
+    assert lib.ppo_host_randperm(rec, 5056, 4, out) == _lib.PPO_EINVAL
+    assert "not recognised" in _lib.last_error()
+    assert lib.ppo_host_randperm(rec, 5000, 4, out) == _lib.PPO_EINVAL

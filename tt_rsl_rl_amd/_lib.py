@@ -129,6 +129,7 @@ _SIGNATURES = [
                                     C.c_void_p, C.c_void_p]),
     ("ppo_gauss_sample", C.c_int, [f32p, i64, f32p, i32, C.c_double, C.c_double, f32p, i64, f32p, i64, f32p, f32p,
                                    i64, i64, i32, C.c_void_p]),
+    ("ppo_host_randperm", C.c_int, [C.c_void_p, C.c_size_t, i64, C.c_void_p]),
     ("ppo_adam_workspace_bytes", C.c_size_t, [i64]),
     ("ppo_adam_step", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double, C.c_double,
                                 C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_size_t,
@@ -136,7 +137,7 @@ _SIGNATURES = [
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib: C.CDLL | None = None
 

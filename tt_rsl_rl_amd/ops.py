@@ -98,6 +98,26 @@ class Segment:
     norm_eps: float = 0.0
 
 
+def host_randperm(n: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``torch.randperm(n)`` drawn from torch's CPU generator -- the same permutation, and the generator left in the
+    same state -- computed by libppo_hip.so's native Fisher-Yates (rsl_rl/storage/rollout_storage.py:232).  ``out``:
+    an int64 CPU tensor of n elements (e.g. pinned, for an asynchronous copy to the device).  A generator record of
+    an unexpected layout is left to torch.randperm itself."""
+    import ctypes
+
+    if out is None:
+        out = torch.empty(n, dtype=torch.int64)
+    if out.dtype != torch.int64 or out.device.type != "cpu" or out.numel() != n or not out.is_contiguous():
+        raise ValueError("host_randperm: out must be a contiguous int64 CPU tensor of n elements")
+    rec = bytearray(torch.get_rng_state().numpy().tobytes())
+    buf = (ctypes.c_uint8 * len(rec)).from_buffer(rec)
+    if L.load().ppo_host_randperm(buf, len(rec), n, out.data_ptr()) != L.PPO_OK:
+        out.copy_(torch.randperm(n))
+        return out
+    torch.set_rng_state(torch.frombuffer(rec, dtype=torch.uint8).clone())
+    return out
+
+
 def gather_rows(perm: torch.Tensor, segments: list[Segment], dst: torch.Tensor) -> None:
     """dst[j, seg.dst_col : +width] = f(seg.src[perm[j]])  (f = identity or the obs normaliser)."""
     _dev(dst)

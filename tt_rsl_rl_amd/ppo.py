@@ -213,6 +213,7 @@ class PPO:
         self.device_state = ops.new_device_state(learning_rate, self.device)
         self._engine: UpdateEngine | None = None
         self._adv_ws = ops.Workspace(self.device)
+        self._perm_host: torch.Tensor | None = None
         self.last_trace: list[dict] = []
 
     # -- rollout side ------------------------------------------------------------------------------------------------
@@ -279,7 +280,12 @@ class PPO:
         ops.reset_device_state(self.device_state, self.learning_rate)
         # feed-forward: one permutation of the batch for all epochs (ppo.py:207, rollout_storage.py:210-260);
         # recurrent: fixed env slices, no permutation drawn (rollout_storage.py:262-331)
-        perm = None if self.is_recurrent else torch.randperm(B).to(self.device, non_blocking=False)
+        perm = None
+        if not self.is_recurrent:
+            if self._perm_host is None or self._perm_host.numel() != B:
+                self._perm_host = torch.empty(B, dtype=torch.int64, pin_memory=True)
+            # torch.randperm(B) on the CPU generator, computed natively (same permutation, same generator state)
+            perm = ops.host_randperm(B, self._perm_host).to(self.device, non_blocking=True)
         steps = engine.run(perm, self._opt_steps)
         self._opt_steps += steps
 
