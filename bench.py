@@ -61,16 +61,25 @@ def build_gpu_alg(workload, seed: int = 0):
     alg = PPO.construct_algorithm(obs0, env, cfg, str(dev))
     alg.train_mode()
     gen = torch.Generator(device=dev).manual_seed(seed)
+    rollout_ms = []
     with torch.inference_mode():
-        obs = _sample_obs(workload, n, dev, gen)
-        for _ in range(workload["steps"]):
-            alg.act(obs)
-            rewards = workload["reward_std"] * torch.randn(n, device=dev, generator=gen)
-            dones = (torch.rand(n, device=dev, generator=gen) < workload["p_done"]).float()
+        for _ in range(2):  # the second rollout is timed (act + process_env_step per env step) and kept
+            alg.storage.clear()
             obs = _sample_obs(workload, n, dev, gen)
-            alg.process_env_step(obs, rewards, dones, {})
+            env_s = [_sample_obs(workload, n, dev, gen) for _ in range(workload["steps"])]
+            rewards = workload["reward_std"] * torch.randn(workload["steps"], n, device=dev, generator=gen)
+            dones = (torch.rand(workload["steps"], n, device=dev, generator=gen) < workload["p_done"]).float()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for t in range(workload["steps"]):
+                alg.act(obs)
+                obs = env_s[t]
+                alg.process_env_step(obs, rewards[t], dones[t], {})
+            torch.cuda.synchronize()
+            rollout_ms.append((time.perf_counter() - t0) / workload["steps"] * 1e3)
         alg.compute_returns(obs)
     torch.cuda.synchronize()
+    alg.bench_rollout_ms = rollout_ms[-1]
     return alg
 
 
@@ -326,6 +335,9 @@ def main() -> int:
         "phases": phase_report,
         "roofline": roofline,
         "hbm_kernels": hbm,
+        "rollout": {"ms_per_env_step": round(alg.bench_rollout_ms, 4),
+                    "transitions_per_s": round(workload["num_envs"] / (alg.bench_rollout_ms * 1e-3), 1),
+                    "note": "act() + process_env_step() for all envs, observations already on the GPU"},
         "losses": losses,
         "cpu_baseline": None,
     }
