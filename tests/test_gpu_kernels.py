@@ -136,12 +136,12 @@ def test_linear_bwd_dx(cuda, rows, fin, fout, act, from_output):
     src = None
     if act:
         src = torch.where(zp > 0, zp, torch.expm1(zp)) if from_output else zp
-    out = torch.empty(rows, fin, device=cuda)
-    ops.linear_bwd_dx([(dz.to(cuda), w.to(cuda), None if src is None else src.to(cuda), out)], rows,
-                      elu_from_output=from_output)
     ref = dz.double() @ w.double()
     if act:
         ref = ref * torch.where(zp.double() > 0, torch.ones_like(ref), torch.exp(zp.double()))
+    probs = lambda out: [(dz.to(cuda), w.to(cuda), None if src is None else src.to(cuda), out)]
+    out = torch.empty(rows, fin, device=cuda)
+    ops.linear_bwd_dx(probs(out), rows, elu_from_output=from_output)
     assert rel_err(out, ref) < 2e-6
 
 

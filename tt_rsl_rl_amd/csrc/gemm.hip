@@ -230,49 +230,71 @@ extern "C" size_t ppo_linear_bwd_dx_workspace_bytes(const ppo_linear_bwd_dx_prob
   return dx_plan(problems, count, nullptr) * sizeof(float);
 }
 
-extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
-                                 int32_t elu_source, void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
-  PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS,
-              "ppo_linear_bwd_dx: count=%d outside [1, %d]", count, PPO_MAX_LINEAR_PROBLEMS);
-  PPO_REQUIRE(elu_source == PPO_ELU_FROM_INPUT || elu_source == PPO_ELU_FROM_OUTPUT,
-              "ppo_linear_bwd_dx: elu_source=%d", elu_source);
-  PPO_REQUIRE(rows_ok(rows), "ppo_linear_bwd_dx: rows=%lld", (long long)rows);
-  bool any_act = false, any_plain = false;
-  for (int i = 0; i < count; ++i) {
-    const ppo_linear_bwd_dx_problem& q = problems[i];
-    PPO_REQUIRE(q.dz && q.w && q.dz_prev, "ppo_linear_bwd_dx: problem %d has a null pointer", i);
-    PPO_REQUIRE(q.in_features > 0 && q.out_features > 0, "ppo_linear_bwd_dx: problem %d features", i);
-    PPO_REQUIRE(q.lddz >= q.out_features && q.lddz_prev >= q.in_features &&
-                    (q.z_prev == nullptr || q.ldz_prev >= q.in_features),
-                "ppo_linear_bwd_dx: problem %d leading dims", i);
-    PPO_REQUIRE(span_ok(rows, q.lddz) && span_ok(q.in_features, (q.out_features + 3) / 4 * 4),
-                "ppo_linear_bwd_dx: problem %d: an operand spans 4 GiB or more", i);
-    (q.z_prev ? any_act : any_plain) = true;
-  }
-  PPO_REQUIRE(!(any_act && any_plain), "ppo_linear_bwd_dx: mix of activation and plain problems in one call");
-  size_t offs[PPO_MAX_LINEAR_PROBLEMS];
-  const size_t need = dx_plan(problems, count, offs) * sizeof(float);
-  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_linear_bwd_dx: workspace too small (%zu < %zu)",
-              workspace_bytes, need);
-  PPO_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "ppo_linear_bwd_dx: workspace must be 16-byte aligned");
-  float* ws = static_cast<float*>(workspace);
-  hipStream_t s = static_cast<hipStream_t>(stream);
+namespace ppo {
+namespace {
 
+int check_dx_workspace(const ppo_linear_bwd_dx_problem* problems, int count, void* workspace, size_t workspace_bytes,
+                       size_t* offs, const char* who) {
+  const size_t need = dx_plan(problems, count, offs) * sizeof(float);
+  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", who,
+              workspace_bytes, need);
+  PPO_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "%s: workspace must be 16-byte aligned", who);
+  return PPO_OK;
+}
+
+// w^T of every problem into its slot of the input-grad workspace ([in, round4(out)], dx_plan's offsets).
+int launch_transposes(const ppo_linear_bwd_dx_problem* problems, int count, float* ws, const size_t* offs,
+                      hipStream_t s) {
   TransposeGroup tg{};
-  Group g{};
-  int tblocks = 0, max_n = 0;
+  int tblocks = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_linear_bwd_dx_problem& q = problems[i];
-    float* wt = ws + offs[i];
     TransposeItem& T = tg.it[i];
-    T.w = q.w; T.wt = wt; T.out = q.out_features; T.in = q.in_features;
+    T.w = q.w; T.wt = ws + offs[i]; T.out = q.out_features; T.in = q.in_features;
     T.ldt = static_cast<int>(round4(q.out_features));
     T.tiles_in = static_cast<int>(ceil_div(q.in_features, 32));
     T.block_begin = tblocks;
     tblocks += static_cast<int>(ceil_div(T.ldt, 32)) * T.tiles_in;
+  }
+  for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) tg.it[i].block_begin = INT32_MAX;
+  tg.count = count;
+  hipLaunchKernelGGL(transpose_kernel, dim3(tblocks), dim3(256), 0, s, tg);
+  return check_launch("transpose_kernel");
+}
+
+// w^T of every problem into the workspace, then the input-grad GEMMs on those copies.
+int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t elu_source,
+            void* workspace, size_t workspace_bytes, ppo_stream_t stream, const char* who) {
+  PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS, "%s: count=%d outside [1, %d]",
+              who, count, PPO_MAX_LINEAR_PROBLEMS);
+  PPO_REQUIRE(elu_source == PPO_ELU_FROM_INPUT || elu_source == PPO_ELU_FROM_OUTPUT, "%s: elu_source=%d", who,
+              elu_source);
+  PPO_REQUIRE(rows_ok(rows), "%s: rows=%lld", who, (long long)rows);
+  bool any_act = false, any_plain = false;
+  for (int i = 0; i < count; ++i) {
+    const ppo_linear_bwd_dx_problem& q = problems[i];
+    PPO_REQUIRE(q.dz && q.w && q.dz_prev, "%s: problem %d has a null pointer", who, i);
+    PPO_REQUIRE(q.in_features > 0 && q.out_features > 0, "%s: problem %d features", who, i);
+    PPO_REQUIRE(q.lddz >= q.out_features && q.lddz_prev >= q.in_features &&
+                    (q.z_prev == nullptr || q.ldz_prev >= q.in_features),
+                "%s: problem %d leading dims", who, i);
+    PPO_REQUIRE(span_ok(rows, q.lddz) && span_ok(q.in_features, (q.out_features + 3) / 4 * 4),
+                "%s: problem %d: an operand spans 4 GiB or more", who, i);
+    (q.z_prev ? any_act : any_plain) = true;
+  }
+  PPO_REQUIRE(!(any_act && any_plain), "%s: mix of activation and plain problems in one call", who);
+  size_t offs[PPO_MAX_LINEAR_PROBLEMS];
+  if (int rc = check_dx_workspace(problems, count, workspace, workspace_bytes, offs, who)) return rc;
+  float* ws = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = launch_transposes(problems, count, ws, offs, s)) return rc;
+  Group g{};
+  int max_n = 0;
+  for (int i = 0; i < count; ++i) {
+    const ppo_linear_bwd_dx_problem& q = problems[i];
     Problem& p = g.p[i];
     p.A = q.dz; p.lda = q.lddz;
-    p.B = wt; p.ldb = T.ldt;
+    p.B = ws + offs[i]; p.ldb = round4(q.out_features);
     p.C = q.dz_prev; p.ldc = q.lddz_prev;
     p.aux = q.z_prev; p.ldaux = q.ldz_prev;
     p.M = static_cast<int>(rows); p.N = q.in_features; p.K = q.out_features;
@@ -281,14 +303,18 @@ extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int3
     p.elu_from_output = elu_source == PPO_ELU_FROM_OUTPUT;
     max_n = std::max(max_n, q.in_features);
   }
-  for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) tg.it[i].block_begin = INT32_MAX;
-  tg.count = count;
-  hipLaunchKernelGGL(transpose_kernel, dim3(tblocks), dim3(256), 0, s, tg);
-  if (int rc = check_launch("transpose_kernel")) return rc;
   // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
   const Tile t = pick_tile(max_n > 128 ? T64x64k32s2o4 : T128x64k32s2o4);
   if (any_act) return launch_nt_tile<EPI_ELU_GRAD>(t, g, count, s, "linear_bwd_dx_elu");
   return launch_nt_tile<EPI_STORE>(t, g, count, s, "linear_bwd_dx");
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
+                                 int32_t elu_source, void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
+  return dx_gemm(problems, count, rows, elu_source, workspace, workspace_bytes, stream, "ppo_linear_bwd_dx");
 }
 
 extern "C" size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_problem* problems, int32_t count,

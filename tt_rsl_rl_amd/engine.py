@@ -126,7 +126,7 @@ class UpdateEngine:
         self.loss_ws = torch.empty(ops.loss_workspace_bytes(self.R_max, self.A), dtype=torch.uint8, device=self.device)
         self.dw_ws = ops.Workspace(self.device)
         self.adam_ws = ops.Workspace(self.device)
-        self.dx_ws = ops.Workspace(self.device)
+        self.dx_ws = ops.Workspace(self.device)  # the input-grad's w^T copies
         self.adv_ws = ops.Workspace(self.device)
         self.trace = torch.zeros(5 * alg.num_learning_epochs * self.M, dtype=torch.float64, device=self.device)
 
@@ -168,7 +168,7 @@ class UpdateEngine:
         adv_col = self.advantage_column(tab, R)
         self.head_forward(xa, xc, R)
         self.loss(tab, R, adv_col)
-        self.head_backward(R, down_to=1)
+        self.head_backward(R)
         self.weight_grads(self.head_dw(xa, xc, R), R)
         self.adam(step)
 
@@ -225,16 +225,21 @@ class UpdateEngine:
                               alg.desired_kl if alg.desired_kl is not None else 0.0, self.trace)
         tm.stop("loss")
 
-    def head_backward(self, R: int, down_to: int) -> None:
-        """Input gradients down the chain (actor and critic grouped) to the input of layer ``down_to``."""
+    def dx_layers(self, R: int) -> list[tuple[int, list[tuple], bool]]:
+        """The head's input-gradients, top layer first: (layer, grouped actor / critic problems, ELU' taken from the
+        layer below's output).  Layer 0 has none (no gradient into the observations)."""
         la, lc = self._layers()
         ba, bc = self.buf_a, self.buf_c
+        return [(i, [(ba.dz[i][:R], la[i].weight, ba.h[i - 1][:R], ba.dz[i - 1][:R]),
+                     (bc.dz[i][:R], lc[i].weight, bc.h[i - 1][:R], bc.dz[i - 1][:R])], True)
+                for i in range(len(la) - 1, 0, -1)]
+
+    def head_backward(self, R: int) -> None:
+        """Input gradients down the chain (actor and critic grouped)."""
         tm = self.timer
-        for i in range(len(la) - 1, down_to - 1, -1):
+        for i, probs, from_output in self.dx_layers(R):
             tm.start(f"dx{i}")
-            ops.linear_bwd_dx([(ba.dz[i][:R], la[i].weight, ba.h[i - 1][:R], ba.dz[i - 1][:R]),
-                               (bc.dz[i][:R], lc[i].weight, bc.h[i - 1][:R], bc.dz[i - 1][:R])], R, self.dx_ws,
-                              elu_from_output=True)
+            ops.linear_bwd_dx(probs, R, self.dx_ws, elu_from_output=from_output)
             tm.stop(f"dx{i}")
 
     def head_dw(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> list[tuple]:
@@ -369,6 +374,13 @@ class RecurrentUpdateEngine(UpdateEngine):
                     keep=tab[:, self.layout.keep], h=buf.h[:R], hs=buf.hs[:R + e1 - e0], c=buf.c[:R],
                     gates=buf.gates[:R], dh=buf.dh[:R], dgates=buf.dgates[:R], dc=buf.dc[:e1 - e0])
 
+    def dx_layers(self, R: int) -> list[tuple[int, list[tuple], bool]]:
+        """As the feed-forward head's, plus layer 0: it has no activation below it, so a plain input-gradient into
+        the LSTM outputs' gradient dh."""
+        la, lc = self._layers()
+        return super().dx_layers(R) + [(0, [(self.buf_a.dz[0][:R], la[0].weight, None, self.seq_a.dh[:R]),
+                                            (self.buf_c.dz[0][:R], lc[0].weight, None, self.seq_c.dh[:R])], False)]
+
     def _grouped(self, fn, qa: dict, qc: dict, E: int) -> None:
         if qa["hidden"] == qc["hidden"]:
             fn([qa, qc], self.T, E)
@@ -400,13 +412,7 @@ class RecurrentUpdateEngine(UpdateEngine):
 
         self.head_forward(sa.h[:R], sc.h[:R], R)
         self.loss(tab, R, adv_col)
-        self.head_backward(R, down_to=1)
-        # the head's first layer has no activation below it: plain input gradient into the LSTM output
-        la, lc = self._layers()
-        tm.start("dx0")
-        ops.linear_bwd_dx([(self.buf_a.dz[0][:R], la[0].weight, None, sa.dh[:R]),
-                           (self.buf_c.dz[0][:R], lc[0].weight, None, sc.dh[:R])], R, self.dx_ws)
-        tm.stop("dx0")
+        self.head_backward(R)
         # the heads' weight gradients need only their dz and inputs: a side stream computes them while the
         # latency-bound LSTM backward steps run; Adam waits for both
         main = torch.cuda.current_stream()

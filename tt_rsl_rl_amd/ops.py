@@ -192,10 +192,7 @@ def linear_fwd(problems: list[tuple], rows: int, elu: bool) -> None:
            L.PPO_ACT_ELU if elu else L.PPO_ACT_NONE, _stream())
 
 
-def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None, elu_from_output: bool = False
-                  ) -> None:
-    """problems: (dz [rows, out], w [out, in], act [rows, in] or None, dz_prev [rows, in]); act is the ELU input z
-    of the layer below, or its output h = elu(z) with elu_from_output."""
+def _dx_problems(problems: list[tuple], rows: int):
     items = []
     for dz, w, z_prev, dz_prev in problems:
         _dev(dz, w, z_prev, dz_prev)
@@ -212,9 +209,17 @@ def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None,
     nbytes = L.load().ppo_linear_bwd_dx_workspace_bytes(arr, len(items))
     if nbytes == 0:
         raise ValueError("linear_bwd_dx: invalid problem set")
+    return arr, len(items), nbytes
+
+
+def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None, elu_from_output: bool = False
+                  ) -> None:
+    """problems: (dz [rows, out], w [out, in], act [rows, in] or None, dz_prev [rows, in]); act is the ELU input z
+    of the layer below, or its output h = elu(z) with elu_from_output."""
+    arr, count, nbytes = _dx_problems(problems, rows)
     buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
     src = L.PPO_ELU_FROM_OUTPUT if elu_from_output else L.PPO_ELU_FROM_INPUT
-    L.call("ppo_linear_bwd_dx", arr, len(items), rows, src, buf.data_ptr(), buf.numel(), _stream())
+    L.call("ppo_linear_bwd_dx", arr, count, rows, src, buf.data_ptr(), buf.numel(), _stream())
 
 
 def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:
