@@ -95,6 +95,8 @@ def phase_flops(workload, R: int) -> dict[str, float]:
     for i in range(1, nl):
         out[f"dx{i}"] = sum(2.0 * R * s[i][0] * s[i][1] for s in shapes)
     out["dw"] = sum(2.0 * R * i_ * o_ for s in shapes for i_, o_ in s)
+    # the fused head: the output layers' forward and input-grad (with the loss) in one launch
+    out["head"] = out[f"fwd{nl - 1}"] + out[f"dx{nl - 1}"]
     if "rnn" in workload:
         # recurrent: R = T x E rows; one LSTM (hidden H on D observation columns) before each head
         H = workload["rnn"]["rnn_hidden_dim"]
@@ -143,10 +145,14 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
     T, N = st.num_transitions_per_env, st.num_envs
     B = T * N
     A = workload["num_actions"]
+    ka, kc = alg.actor.linears[-1].in_features, alg.critic.linears[-1].in_features
     width = sum(seg.src.shape[1] for seg in engine.segments())
     nbytes = {
         "gather": B * (2 * 4 * width + 8),                        # every copied float read + written, int64 index
         "loss": R * 4 * (4 * A + 6) + R * 4 * (A + 1),            # per-row inputs + per-row output gradients
+        # fused head: last hidden activations in, their gradients out, batch columns in, mean / value and their
+        # gradients out
+        "head": R * 4 * (2 * (ka + kc) + 3 * A + 4 + 2 * (A + 1)),
         "adam": alg.flat.param.numel() * 36,                      # norm pass 4 B + p, g, m, v read and written
         "gae": B * (4 + 4 + 1 + 4 + 4) + 4 * N,                   # r, V, done in; returns, advantages out
     }
@@ -162,8 +168,9 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
                                                alg.max_grad_norm, b1, b2, alg.adam_eps, 0.5, 0.5, alg.device_state,
                                                engine.adam_ws)),
     }
-    if "loss" in phases:
-        ms["loss"] = phases["loss"][1]
+    for k in ("loss", "head"):
+        if k in phases:
+            ms[k] = phases[k][1]
     out = {}
     for k, b in nbytes.items():
         if k in ms:
@@ -281,7 +288,7 @@ def main() -> int:
         if k in flops:
             entry["tflops"] = round(flops[k] / (t * 1e-3) / 1e12, 2)
         phase_report[k] = entry
-    gemm_phases = [k for k in phases if k in flops]
+    gemm_phases = [k for k in phases if k in flops and k != "head"]  # the fused head is HBM-bound
     dom = max(gemm_phases, key=lambda k: total_ms[k])
 
     # Timed region: events only around the dominant kernel's launches (on the stream the kernels use).  The Python heap

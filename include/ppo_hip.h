@@ -247,6 +247,48 @@ int ppo_loss_finalize(const ppo_loss_args* args, const void* workspace, size_t w
                       ppo_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------------
+ * The output layers fused with the loss: one call does what the actor's and critic's output-layer forward
+ * (rsl_rl/modules/mlp.py's last nn.Linear: mean = h_a W_a^T + b_a, value = h_c w_c^T + b_c), ppo_gauss_ppo_loss,
+ * ppo_loss_finalize and the output layers' input-grad with ELU' of the layer below (the first step of
+ * loss.backward() past the loss, ppo.py:297) do, for the update's MLP heads.  It reads args' batch columns and
+ * writes d_mean / d_value (for the output layers' weight-grad) exactly like ppo_gauss_ppo_loss, and the loss state,
+ * learning rate, trace and d_std_param exactly like ppo_loss_finalize; args->mean / args->value are not read (the
+ * head computes them and stores them to head->mean / head->value when those are not NULL).  The hidden layers'
+ * gradients dz_actor / dz_critic are dloss/dz of the last hidden layers, ELU' taken from their outputs
+ * (h > 0 ? 1 : h + 1).  Supported when ppo_gauss_ppo_head_supported() (num_actions <= 32, k_actor and k_critic
+ * multiples of 16, both <= 128); every row pointer of h_*, dz_*, mean, d_mean, actions, old_mean and old_std
+ * 16-byte aligned (aligned bases, leading dimensions multiples of 4), w_actor contiguous and 16-byte aligned.  The
+ * A-wide runs of actions / old_mean / old_std are read as whole 16-byte chunks (up to 3 floats past column A-1 of a
+ * row, inside the chunk that holds its last column).
+ * ------------------------------------------------------------------------------------------------------------------ */
+typedef struct ppo_policy_head {
+  const float* h_actor;   /* [rows, k_actor] at row stride ld_h_actor: the actor's last hidden ELU output */
+  int64_t ld_h_actor;
+  const float* w_actor;   /* [num_actions, k_actor] row-major (nn.Linear weight) */
+  const float* b_actor;   /* [num_actions] */
+  const float* h_critic;  /* [rows, k_critic] at row stride ld_h_critic */
+  int64_t ld_h_critic;
+  const float* w_critic;  /* [1, k_critic] */
+  const float* b_critic;  /* [1] */
+  float* dz_actor;        /* out [rows, k_actor] at ld_dz_actor */
+  int64_t ld_dz_actor;
+  float* dz_critic;       /* out [rows, k_critic] at ld_dz_critic */
+  int64_t ld_dz_critic;
+  float* mean;            /* out, optional: [rows, num_actions] at ld_mean */
+  int64_t ld_mean;
+  float* value;           /* out, optional: [rows] at stride ld_value */
+  int64_t ld_value;
+  int32_t k_actor;
+  int32_t k_critic;
+} ppo_policy_head;
+
+int ppo_gauss_ppo_head_supported(int32_t num_actions, int32_t k_actor, int32_t k_critic);
+size_t ppo_head_workspace_bytes(int64_t rows, int32_t num_actions);
+int ppo_gauss_ppo_head(const ppo_loss_args* args, const ppo_policy_head* head, void* workspace,
+                       size_t workspace_bytes, float* d_std_param, ppo_device_state* state, int32_t adaptive,
+                       double desired_kl, double* trace, ppo_stream_t stream);
+
+/* ------------------------------------------------------------------------------------------------------------------
  * Rollout-side Gaussian head for act() (rsl_rl/algorithms/ppo.py:124-135; rsl_rl/modules/distribution.py:183-232):
  * std = clamp(std_param) or exp(clamp(log_std_param)); with noise != NULL, actions = noise * std + mean
  * (torch.normal(mean, std) on a standard-normal draw); with noise == NULL the given actions are scored.

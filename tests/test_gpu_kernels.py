@@ -269,6 +269,128 @@ def test_ppo_loss_matches_autograd(cuda, rows, A, std_type, clipped):
     assert tr[1] == lr_ref
 
 
+def _head_case(rows, A, ka, kc, std_type, seed):
+    """Last hidden activations (ELU outputs), output layers, and a batch whose actions / old distribution sit around
+    the head's own means (so the ratios straddle the clip range instead of all clipping)."""
+    g = torch.Generator().manual_seed(seed)
+    h_a = torch.nn.functional.elu(torch.randn(rows, ka, generator=g))
+    h_c = torch.nn.functional.elu(torch.randn(rows, kc, generator=g))
+    w_a = torch.randn(A, ka, generator=g) / math.sqrt(ka)
+    b_a = 0.1 * torch.randn(A, generator=g)
+    w_c = torch.randn(1, kc, generator=g) / math.sqrt(kc)
+    b_c = 0.1 * torch.randn(1, generator=g)
+    mean = (h_a.double() @ w_a.double().T + b_a.double()).float()
+    value = (h_c.double() @ w_c.double().T + b_c.double()).float().squeeze(1)
+    c = _loss_case(rows, A, std_type, True, seed)
+    shift_m = mean - c["mean"]
+    for k in ("actions", "old_mean"):
+        c[k] = c[k] + shift_m
+    shift_v = value - c["value"]
+    for k in ("old_value", "ret"):
+        c[k] = c[k] + shift_v
+    c.update(mean=mean, value=value)
+    return c, dict(h_a=h_a, h_c=h_c, w_a=w_a, b_a=b_a, w_c=w_c, b_c=b_c)
+
+
+def _head_reference(c, net, std_type, clipped):
+    """fp64 autograd through both output layers and the oracle's loss block: the gradients with respect to the last
+    hidden activations, times ELU' taken from those activations (h > 0 ? 1 : h + 1)."""
+    d = {k: v.double() for k, v in net.items()}
+    h_a = d["h_a"].clone().requires_grad_(True)
+    h_c = d["h_c"].clone().requires_grad_(True)
+    dist = O.GaussianDistribution(c["mean"].shape[1], std_type=std_type).double()
+    with torch.no_grad():
+        (dist.std_param if std_type == "scalar" else dist.log_std_param).copy_(c["param"].double())
+    mean = h_a @ d["w_a"].T + d["b_a"]
+    mean.retain_grad()
+    value = (h_c @ d["w_c"].T + d["b_c"]).squeeze(1)
+    value.retain_grad()
+    cc = {k: v.double() for k, v in c.items()}
+    dist.update(mean)
+    logp = dist.log_prob(cc["actions"])
+    s, v, loss = O.ppo_loss_terms(logp, cc["old_logp"].unsqueeze(-1), cc["adv"].unsqueeze(-1), value,
+                                  cc["old_value"], cc["ret"], dist.entropy, 0.2, clipped, 1.0, 0.01)
+    loss.backward()
+    elu_a = torch.where(d["h_a"] > 0, 1.0, d["h_a"] + 1.0)
+    elu_c = torch.where(d["h_c"] > 0, 1.0, d["h_c"] + 1.0)
+    p = dist.std_param if std_type == "scalar" else dist.log_std_param
+    return dict(mean=mean.detach(), value=value.detach(), d_mean=mean.grad, d_value=value.grad,
+                dz_a=h_a.grad * elu_a, dz_c=h_c.grad * elu_c, d_param=p.grad, surrogate=s.item(), value_loss=v.item())
+
+
+@pytest.mark.parametrize("rows,A,ka,kc,std_type,clipped", [
+    (24576, 29, 128, 128, "log", True), (1000, 12, 64, 128, "scalar", True), (33, 32, 32, 16, "log", False),
+    (1, 1, 96, 48, "log", True), (4097, 7, 128, 64, "scalar", False), (50, 17, 16, 16, "log", True),
+    (393216, 12, 128, 128, "log", True)])
+def test_fused_head_matches_autograd_and_the_separate_launches(cuda, rows, A, ka, kc, std_type, clipped):
+    """ppo_gauss_ppo_head (output layers + loss + finalize + output-layer input-grad in one launch) against fp64
+    autograd of the same mathematics, and against the separate launches (linear_fwd, ppo_loss + finalize,
+    linear_bwd_dx) on the same inputs."""
+    ops = _ops()
+    from tt_rsl_rl_amd import _lib as L
+
+    assert ops.head_supported(A, ka, kc)
+    c, net = _head_case(rows, A, ka, kc, std_type, seed=rows + A + ka)
+    ref = _head_reference(c, net, std_type, clipped)
+    pad = lambda n: -(-n // 4) * 4
+    W = 3 * pad(A) + 4 + 4
+    tab = torch.zeros(rows, W)
+    o_m, o_s, o_r = pad(A), 2 * pad(A), 3 * pad(A)
+    tab[:, 0:A], tab[:, o_m:o_m + A], tab[:, o_s:o_s + A] = c["actions"], c["old_mean"], c["old_std"]
+    tab[:, o_r], tab[:, o_r + 1], tab[:, o_r + 2], tab[:, o_r + 3] = c["old_logp"], c["adv"], c["old_value"], c["ret"]
+    tab = tab.to(cuda)
+    batch = {"ld": W, "actions": tab[:, 0], "old_mean": tab[:, o_m], "old_std": tab[:, o_s],
+             "old_logp": tab[:, o_r], "advantages": tab[:, o_r + 1], "old_values": tab[:, o_r + 2],
+             "returns": tab[:, o_r + 3]}
+    dv = {k: v.to(cuda).contiguous() for k, v in net.items()}
+    param = c["param"].to(cuda)
+    if std_type == "log":
+        lo, hi, st = math.log(1e-6), math.log(1e6), L.PPO_STD_LOG
+    else:
+        lo, hi, st = 1e-6, 1e6, L.PPO_STD_SCALAR
+    buf = lambda w: torch.full((rows, pad(w)), float("nan"), device=cuda)[:, :w]
+
+    def run(fused):
+        mean, value = buf(A), buf(1)
+        d_mean, d_value = buf(A), buf(1)
+        dz_a, dz_c = buf(ka), buf(kc)
+        d_param = torch.empty(A, device=cuda)
+        state = ops.new_device_state(1e-3, cuda)
+        trace = torch.zeros(5, dtype=torch.float64, device=cuda)
+        args = ops.make_loss_args(rows, mean, value[:, 0], batch, param, st, lo, hi, 0.2, 1.0, 0.01, clipped, d_mean,
+                                  d_value[:, 0])
+        if fused:
+            ws = torch.empty(ops.head_workspace_bytes(rows, A), dtype=torch.uint8, device=cuda)
+            ops.ppo_head(args, dv["h_a"], dv["w_a"], dv["b_a"], dv["h_c"], dv["w_c"], dv["b_c"], dz_a, dz_c, ws,
+                         d_param, state, True, 0.01, trace, mean=mean, value=value[:, 0])
+        else:
+            ops.linear_fwd([(dv["h_a"], dv["w_a"], dv["b_a"], mean, None), (dv["h_c"], dv["w_c"], dv["b_c"], value,
+                                                                             None)], rows, elu=False)
+            ws = torch.empty(ops.loss_workspace_bytes(rows, A), dtype=torch.uint8, device=cuda)
+            ops.ppo_loss(args, ws)
+            ops.ppo_loss_finalize(args, ws, d_param, state, True, 0.01, trace)
+            ops.linear_bwd_dx([(d_mean, dv["w_a"], dv["h_a"], dz_a), (d_value, dv["w_c"], dv["h_c"], dz_c)], rows,
+                              ops.Workspace(cuda), elu_from_output=True)
+        torch.cuda.synchronize()
+        return dict(mean=mean, value=value[:, 0], d_mean=d_mean, d_value=d_value[:, 0], dz_a=dz_a, dz_c=dz_c,
+                    d_param=d_param, trace=trace.cpu().tolist())
+
+    got, sep = run(True), run(False)
+    for key in ("mean", "value"):
+        assert rel_err(got[key], ref[key]) < 2e-6, key
+    # gradients: fp32 noise of the fp64 truth (the loss-gradient bar), and the separate launches' within the same
+    for key in ("d_mean", "d_value", "dz_a", "dz_c", "d_param"):
+        assert torch.isfinite(got[key]).all(), key
+        assert rel_err(got[key], ref[key], 1e-12) < 1e-5, key
+        assert rel_err(got[key], sep[key], 1e-12) < 2e-5, key
+    tr, ts = got["trace"], sep["trace"]
+    assert abs(tr[2] - ref["surrogate"]) <= 2e-6 * max(1.0, abs(ref["surrogate"]))
+    assert abs(tr[3] - ref["value_loss"]) <= 2e-6 * max(1.0, abs(ref["value_loss"]))
+    assert tr[4] == ts[4]  # entropy depends on the std parameter alone
+    assert abs(tr[0] - ts[0]) <= 1e-5 * max(1e-3, abs(ts[0]))
+    assert tr[1] == O.adaptive_lr(torch.tensor(tr[0], dtype=torch.float32), 1e-3, 0.01)
+
+
 def test_kl_is_exactly_zero_for_identical_distributions(cuda):
     ops = _ops()
     from tt_rsl_rl_amd import _lib as L

@@ -62,6 +62,9 @@ CASES = {
                                  {"normalize_advantage_per_mini_batch": True, "num_mini_batches": 3}),
     "flat48_unclipped_fixed": (R.scaled(R.WORKLOADS["flat48"], num_envs=200, steps=5, hidden_dims=[128, 64, 32]),
                                {"use_clipped_value_loss": False, "schedule": "fixed", "num_learning_epochs": 2}),
+    # 40 actions on a 48-wide last hidden layer: outside the fused head's shapes, the separate output-layer path
+    "flat48_a40_unfused": (dict(R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[64, 48]),
+                                num_actions=40), {}),
     # recurrent (LSTM before the MLP head): env-slice mini-batches, sequences started from the saved states
     "lstm256_512": (_lstm(512, 24, 256, [256, 128]), {}),
     "lstm64_norm_carry": (_lstm(128, 16, 64, [64, 32], obs_normalization=True), {"carry_state": True}),
@@ -69,6 +72,11 @@ CASES = {
                                   {"num_mini_batches": 3, "normalize_advantage_per_mini_batch": True,
                                    "schedule": "fixed", "use_clipped_value_loss": False, "carry_state": True}),
 }
+
+
+# cases whose output layers fall outside the fused head (more than 32 actions, or a last hidden width that is not a
+# multiple of 16)
+UNFUSED = {"flat48_a40_unfused"}
 
 
 def _table_order(ora, hip) -> torch.Tensor:
@@ -110,6 +118,8 @@ def test_update_matches_oracle(name):
     acts = hip._engine.table[:, lay.actions:lay.actions + A].cpu()
     assert torch.equal(acts, ora.storage.actions.flatten(0, 1)[perm]), "mini-batch rows must be bit-exact"
     assert perm.numel() == B
+    # the fused output-layer + loss launch runs wherever it takes the shapes
+    assert hip._engine.fused_head == (name not in UNFUSED), name
     # learning-rate decisions
     assert [t["lr"] for t in hip.last_trace] == [t["lr"] for t in ora.trace]
     assert hip.learning_rate == ora.learning_rate

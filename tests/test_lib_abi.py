@@ -51,6 +51,9 @@ STRUCTS = {
                                    "ld_batch", "std_param", "std_lo", "std_hi", "clip_param", "value_loss_coef",
                                    "entropy_coef", "use_clipped_value_loss", "d_mean", "ld_dmean", "d_value",
                                    "ld_dvalue"]),
+    "ppo_policy_head": ("PolicyHead", ["h_actor", "ld_h_actor", "w_actor", "b_actor", "h_critic", "ld_h_critic",
+                                       "w_critic", "b_critic", "dz_actor", "ld_dz_actor", "dz_critic", "ld_dz_critic",
+                                       "mean", "ld_mean", "value", "ld_value", "k_actor", "k_critic"]),
     "ppo_device_state": ("DeviceState", ["learning_rate", "sum_value_loss", "sum_surrogate_loss", "sum_entropy",
                                          "last_kl_mean", "last_value_loss", "last_surrogate_loss", "last_entropy",
                                          "total_norm", "clip_coef", "num_minibatches"]),
@@ -121,6 +124,21 @@ def test_argument_validation_reports_errors_without_a_gpu():
         _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)
     probs = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512)])
     assert lib.ppo_linear_bwd_dw_workspace_bytes(probs, 1, 24576) >= 4 * 512 * 96
+    # the fused output-layer head: its shape rule, and the rejection of shapes outside it before any pointer is used
+    assert lib.ppo_gauss_ppo_head_supported(29, 128, 128) == 1
+    assert lib.ppo_gauss_ppo_head_supported(1, 16, 16) == 1
+    for shape in ((33, 128, 128), (12, 100, 128), (12, 256, 128), (12, 128, 8), (0, 128, 128)):
+        assert lib.ppo_gauss_ppo_head_supported(*shape) == 0, shape
+    assert lib.ppo_head_workspace_bytes(24576, 29) == 8 * 384 * 32  # one 16-row tile per wave, 4 waves per block
+    args = _lib.LossArgs(rows=10, num_actions=33)
+    head = _lib.PolicyHead(k_actor=128, k_critic=128)
+    with pytest.raises(ValueError, match="not supported"):
+        _lib.call("ppo_gauss_ppo_head", ctypes.byref(args), ctypes.byref(head), None, 0, None, None, 0, 0.0, None,
+                  None)
+    args = _lib.LossArgs(rows=10, num_actions=12)
+    with pytest.raises(ValueError, match="null pointer"):
+        _lib.call("ppo_gauss_ppo_head", ctypes.byref(args), ctypes.byref(head), None, 0, None, None, 0, 0.0, None,
+                  None)
 
 
 @pytest.mark.parametrize("seed, n, pre", [(0, 1, 0), (1, 2, 0), (3, 5, 0), (5, 624, 0), (5, 625, 3), (11, 1249, 700),

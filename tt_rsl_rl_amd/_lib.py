@@ -73,6 +73,14 @@ class LossArgs(C.Structure):
     ]
 
 
+class PolicyHead(C.Structure):
+    _fields_ = [("h_actor", C.c_void_p), ("ld_h_actor", i64), ("w_actor", C.c_void_p), ("b_actor", C.c_void_p),
+                ("h_critic", C.c_void_p), ("ld_h_critic", i64), ("w_critic", C.c_void_p), ("b_critic", C.c_void_p),
+                ("dz_actor", C.c_void_p), ("ld_dz_actor", i64), ("dz_critic", C.c_void_p), ("ld_dz_critic", i64),
+                ("mean", C.c_void_p), ("ld_mean", i64), ("value", C.c_void_p), ("ld_value", i64),
+                ("k_actor", i32), ("k_critic", i32)]
+
+
 class DeviceState(C.Structure):
     _fields_ = [("learning_rate", C.c_double), ("sum_value_loss", C.c_double),
                 ("sum_surrogate_loss", C.c_double), ("sum_entropy", C.c_double),
@@ -127,6 +135,10 @@ _SIGNATURES = [
     ("ppo_gauss_ppo_loss", C.c_int, [C.POINTER(LossArgs), C.c_void_p, C.c_size_t, C.c_void_p]),
     ("ppo_loss_finalize", C.c_int, [C.POINTER(LossArgs), C.c_void_p, C.c_size_t, f32p, C.c_void_p, i32, C.c_double,
                                     C.c_void_p, C.c_void_p]),
+    ("ppo_gauss_ppo_head_supported", C.c_int, [i32, i32, i32]),
+    ("ppo_head_workspace_bytes", C.c_size_t, [i64, i32]),
+    ("ppo_gauss_ppo_head", C.c_int, [C.POINTER(LossArgs), C.POINTER(PolicyHead), C.c_void_p, C.c_size_t, f32p,
+                                     C.c_void_p, i32, C.c_double, C.c_void_p, C.c_void_p]),
     ("ppo_gauss_sample", C.c_int, [f32p, i64, f32p, i32, C.c_double, C.c_double, f32p, i64, f32p, i64, f32p, f32p,
                                    i64, i64, i32, C.c_void_p]),
     ("ppo_host_randperm", C.c_int, [C.c_void_p, C.c_size_t, i64, C.c_void_p]),
@@ -137,7 +149,7 @@ _SIGNATURES = [
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib: C.CDLL | None = None
 

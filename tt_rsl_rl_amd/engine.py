@@ -17,6 +17,8 @@ HBM layout of one update:
 
 from __future__ import annotations
 
+import os
+
 import torch
 
 from . import _lib as L
@@ -124,6 +126,14 @@ class UpdateEngine:
         self.buf_a = ModelBuffers(actor, self.R_max, self.device)
         self.buf_c = ModelBuffers(critic, self.R_max, self.device)
         self.loss_ws = torch.empty(ops.loss_workspace_bytes(self.R_max, self.A), dtype=torch.uint8, device=self.device)
+        # the output layers, loss and their input-grad as one launch (ppo_gauss_ppo_head) where it takes the shapes
+        la, lc = actor.linears, critic.linears
+        self.fused_head = (len(la) >= 2 and len(la) == len(lc) and
+                           ops.head_supported(self.A, la[-1].in_features, lc[-1].in_features) and
+                           os.environ.get("PPO_HIP_FUSED_HEAD", "1") != "0")
+        if self.fused_head:
+            self.head_ws = torch.empty(ops.head_workspace_bytes(self.R_max, self.A), dtype=torch.uint8,
+                                       device=self.device)
         self.dw_ws = ops.Workspace(self.device)
         self.adam_ws = ops.Workspace(self.device)
         self.dx_ws = ops.Workspace(self.device)  # the input-grad's w^T copies
@@ -194,7 +204,7 @@ class UpdateEngine:
         nl = len(la)
         tm = self.timer
         ins_a, ins_c = [xa], [xc]
-        for i in range(nl):
+        for i in range(nl - 1 if self.fused_head else nl):
             last = i == nl - 1
             probs = [(ins_a[-1], la[i].weight, la[i].bias, ba.out[:R] if last else None, None if last else ba.h[i][:R]),
                      (ins_c[-1], lc[i].weight, lc[i].bias, bc.out[:R] if last else None, None if last else bc.h[i][:R])]
@@ -206,7 +216,8 @@ class UpdateEngine:
                 ins_c.append(bc.h[i][:R])
 
     def loss(self, tab: torch.Tensor, R: int, adv_col: int) -> None:
-        """Losses + per-row output gradients, then the device-side reduction / LR rule / std-parameter gradient."""
+        """Losses + per-row output gradients, then the device-side reduction / LR rule / std-parameter gradient.
+        With the fused head the output layers' forward and input-grad run in the same launch."""
         alg, lay = self.alg, self.layout
         ba, bc = self.buf_a, self.buf_c
         dist = alg.actor.distribution
@@ -218,9 +229,18 @@ class UpdateEngine:
                                   alg.clip_param, alg.value_loss_coef, alg.entropy_coef, alg.use_clipped_value_loss,
                                   ba.dz[-1][:R], bc.dz[-1][:R, 0])
         tm = self.timer
+        adaptive = alg.desired_kl is not None and alg.schedule == "adaptive"
+        if self.fused_head:
+            la, lc = self._layers()
+            tm.start("head")
+            ops.ppo_head(args, ba.h[-1][:R], la[-1].weight, la[-1].bias, bc.h[-1][:R], lc[-1].weight, lc[-1].bias,
+                         ba.dz[-2][:R], bc.dz[-2][:R], self.head_ws, alg.flat.grad_view(dist.param),
+                         alg.device_state, adaptive, alg.desired_kl, self.trace, mean=ba.out[:R],
+                         value=bc.out[:R, 0])
+            tm.stop("head")
+            return
         tm.start("loss")
         ops.ppo_loss(args, self.loss_ws)
-        adaptive = alg.desired_kl is not None and alg.schedule == "adaptive"
         ops.ppo_loss_finalize(args, self.loss_ws, alg.flat.grad_view(dist.param), alg.device_state, adaptive,
                               alg.desired_kl if alg.desired_kl is not None else 0.0, self.trace)
         tm.stop("loss")
@@ -230,9 +250,10 @@ class UpdateEngine:
         layer below's output).  Layer 0 has none (no gradient into the observations)."""
         la, lc = self._layers()
         ba, bc = self.buf_a, self.buf_c
+        top = len(la) - 2 if self.fused_head else len(la) - 1  # the fused head produced the output layer's
         return [(i, [(ba.dz[i][:R], la[i].weight, ba.h[i - 1][:R], ba.dz[i - 1][:R]),
                      (bc.dz[i][:R], lc[i].weight, bc.h[i - 1][:R], bc.dz[i - 1][:R])], True)
-                for i in range(len(la) - 1, 0, -1)]
+                for i in range(top, 0, -1)]
 
     def head_backward(self, R: int) -> None:
         """Input gradients down the chain (actor and critic grouped)."""

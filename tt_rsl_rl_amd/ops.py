@@ -330,6 +330,49 @@ def loss_workspace_bytes(rows: int, num_actions: int) -> int:
     return int(L.load().ppo_loss_workspace_bytes(rows, num_actions))
 
 
+def head_supported(num_actions: int, k_actor: int, k_critic: int) -> bool:
+    """Whether ppo_gauss_ppo_head takes these output layers (host arithmetic only)."""
+    return bool(L.load().ppo_gauss_ppo_head_supported(num_actions, k_actor, k_critic))
+
+
+def head_workspace_bytes(rows: int, num_actions: int) -> int:
+    return int(L.load().ppo_head_workspace_bytes(rows, num_actions))
+
+
+def ppo_head(args: L.LossArgs, h_actor: torch.Tensor, w_actor: torch.Tensor, b_actor: torch.Tensor,
+             h_critic: torch.Tensor, w_critic: torch.Tensor, b_critic: torch.Tensor, dz_actor: torch.Tensor,
+             dz_critic: torch.Tensor, ws: torch.Tensor, d_std_param: torch.Tensor, state: torch.Tensor,
+             adaptive: bool, desired_kl: float | None, trace: torch.Tensor | None,
+             mean: torch.Tensor | None = None, value: torch.Tensor | None = None) -> None:
+    """Output layers + loss + finalize + the output layers' input-grad in one call (ppo_gauss_ppo_head).  args
+    carries the batch columns and d_mean / d_value; its mean / value fields are not read."""
+    _dev(h_actor, w_actor, b_actor, h_critic, w_critic, b_critic, dz_actor, dz_critic, mean, value)
+    R = int(args.rows)
+    for name, t in (("h_actor", h_actor), ("h_critic", h_critic), ("dz_actor", dz_actor), ("dz_critic", dz_critic)):
+        if t.dim() != 2 or t.shape[0] < R:
+            raise ValueError(f"ppo_head: {name} must be [rows, width], got {tuple(t.shape)}")
+    ka, kc = h_actor.shape[1], h_critic.shape[1]
+    if tuple(w_actor.shape) != (args.num_actions, ka) or not w_actor.is_contiguous() or \
+            b_actor.numel() != args.num_actions:
+        raise ValueError(f"ppo_head: actor output layer {tuple(w_actor.shape)} does not map {ka} -> "
+                         f"{args.num_actions}")
+    if tuple(w_critic.shape) != (1, kc) or not w_critic.is_contiguous() or b_critic.numel() != 1:
+        raise ValueError(f"ppo_head: critic output layer {tuple(w_critic.shape)} does not map {kc} -> 1")
+    if tuple(dz_actor.shape[1:]) != (ka,) or tuple(dz_critic.shape[1:]) != (kc,):
+        raise ValueError("ppo_head: dz_actor / dz_critic must match the hidden widths")
+    head = L.PolicyHead(
+        h_actor=h_actor.data_ptr(), ld_h_actor=_row_major(h_actor, "h_actor"), w_actor=w_actor.data_ptr(),
+        b_actor=b_actor.data_ptr(), h_critic=h_critic.data_ptr(), ld_h_critic=_row_major(h_critic, "h_critic"),
+        w_critic=w_critic.data_ptr(), b_critic=b_critic.data_ptr(),
+        dz_actor=dz_actor.data_ptr(), ld_dz_actor=_row_major(dz_actor, "dz_actor"),
+        dz_critic=dz_critic.data_ptr(), ld_dz_critic=_row_major(dz_critic, "dz_critic"),
+        mean=_ptr(mean), ld_mean=_row_major(mean, "mean") if mean is not None else 0,
+        value=_ptr(value), ld_value=value.stride(0) if value is not None else 0, k_actor=ka, k_critic=kc)
+    L.call("ppo_gauss_ppo_head", C_ref(args), C_ref(head), ws.data_ptr(), ws.numel(), d_std_param.data_ptr(),
+           state.data_ptr(), 1 if adaptive else 0, float(desired_kl if desired_kl is not None else 0.0), _ptr(trace),
+           _stream())
+
+
 def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max_grad_norm: float, beta1: float,
               beta2: float, eps: float, bc1: float, bc2_sqrt: float, state: torch.Tensor, ws: Workspace) -> None:
     _dev(params, grads, exp_avg, exp_avg_sq)
