@@ -80,6 +80,7 @@ def build_gpu_alg(workload, seed: int = 0):
         alg.compute_returns(obs)
     torch.cuda.synchronize()
     alg.bench_rollout_ms = rollout_ms[-1]
+    alg.bench_last_obs = obs
     return alg
 
 
@@ -317,6 +318,18 @@ def main() -> int:
         roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                     "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": load_traffic(dom), "kernel": dom,
                     "flops_per_launch": flops[dom], "mean_launch_ms": round(t, 5), "launches_timed": n}
+    # compute_returns() (bootstrap critic forward, GAE, advantage normalisation) on the stored rollout, timed after
+    # the updates (it rewrites the same returns / advantages each call), as the runner calls it: in inference mode
+    cr = []
+    with torch.inference_mode():
+        for i in range(12):
+            torch.cuda.synchronize()
+            s0 = time.perf_counter()
+            alg.compute_returns(alg.bench_last_obs)
+            torch.cuda.synchronize()
+            if i >= 2:
+                cr.append(time.perf_counter() - s0)
+    cr_ms = statistics.median(cr) * 1e3
     hbm = hbm_kernels(alg, engine, phases, workload, R)
     gemm_total = W.gemm_flops_per_update(workload, alg.num_learning_epochs)
     lstm = ""
@@ -337,6 +350,9 @@ def main() -> int:
         "ms_per_update_median": round(statistics.median(per) * 1e3, 3),
         "ms_per_update_min_p90_max": [round(min(per) * 1e3, 3), round(sorted(per)[int(0.9 * (len(per) - 1))] * 1e3, 3),
                                       round(max(per) * 1e3, 3)],
+        "sample_visits_per_s": round(value * alg.num_learning_epochs, 1),
+        "compute_returns_ms_median": round(cr_ms, 3),
+        "compute_returns_plus_update_ms": round(cr_ms + statistics.median(per) * 1e3, 3),
         "update_gemm_tflops": round(gemm_total / (ms * 1e-3) / 1e12, 2),
         "update_gemm_mfma_frac": round(gemm_total / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
         "phases": phase_report,

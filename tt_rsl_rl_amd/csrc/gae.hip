@@ -99,11 +99,20 @@ __global__ __launch_bounds__(kNormThreads) void adv_partials_kernel(const float*
 
 // Fixed-order reduction of the partials.  mode 0 -> stats[0] = mean (rounded through fp32 like torch's mean());
 // mode 1 -> stats[1] = unbiased std rounded to fp32.
+// One wavefront: lane l sums partials l, l + 64, ... in order (all of its loads issued before the first add), then
+// a fixed butterfly combines the lanes.
 __global__ __launch_bounds__(64) void adv_stats_kernel(const double* __restrict__ partials, int nparts, int64_t n,
                                                        int mode, double* __restrict__ stats) {
-  if (threadIdx.x != 0) return;
+  constexpr int kPer = (kNormMaxBlocks + 63) / 64;
+  double v[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) v[j] = partials[min(static_cast<int>(threadIdx.x) + 64 * j, nparts - 1)];
   double s = 0.0;
-  for (int i = 0; i < nparts; ++i) s += partials[i];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (static_cast<int>(threadIdx.x) + 64 * j < nparts) s += v[j];
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (threadIdx.x != 0) return;
   if (mode == 0) {
     stats[0] = static_cast<double>(static_cast<float>(s / static_cast<double>(n)));
   } else {

@@ -47,6 +47,8 @@ struct ReduceGroup {
   int64_t total;
 };
 
+constexpr int kReduceBatch = 8;
+
 __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < g.total;
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -61,10 +63,19 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
       const int o = local / q4, i = 4 * (local - o * q4);
       const float* src = R.partial + static_cast<int64_t>(o) * R.ld + i;
       f32x4 acc = *reinterpret_cast<const f32x4*>(src);
-      for (int k = 1; k < R.splits; ++k) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(src + k * R.stride);
+      // splits 1, 2, ... added in order; kReduceBatch loads in flight at a time (clamped addresses past the last
+      // split, discarded), not one dependent round trip per split
+      for (int k0 = 1; k0 < R.splits; k0 += kReduceBatch) {
+        f32x4 v[kReduceBatch];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c] += v[c];
+        for (int j = 0; j < kReduceBatch; ++j)
+          v[j] = *reinterpret_cast<const f32x4*>(src + static_cast<int64_t>(min(k0 + j, R.splits - 1)) * R.stride);
+#pragma unroll
+        for (int j = 0; j < kReduceBatch; ++j)
+          if (k0 + j < R.splits) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] += v[j][c];
+          }
       }
       float* out = R.dw + static_cast<int64_t>(o) * R.in + i;
 #pragma unroll
@@ -73,7 +84,15 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
     } else {
       const int o = local - R.out * q4;
       double acc = 0.0;
-      for (int k = 0; k < R.splits; ++k) acc += R.colsum[k * static_cast<int64_t>(R.out) + o];
+      for (int k0 = 0; k0 < R.splits; k0 += kReduceBatch) {
+        double v[kReduceBatch];
+#pragma unroll
+        for (int j = 0; j < kReduceBatch; ++j)
+          v[j] = R.colsum[min(k0 + j, R.splits - 1) * static_cast<int64_t>(R.out) + o];
+#pragma unroll
+        for (int j = 0; j < kReduceBatch; ++j)
+          if (k0 + j < R.splits) acc += v[j];
+      }
       R.db[o] = static_cast<float>(acc);
     }
   }
