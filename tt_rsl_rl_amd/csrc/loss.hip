@@ -309,9 +309,8 @@ __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
 // dloss/dmean second (a = 16t + 4q + r is the lane's own element), so its accumulator holds row m, hidden units
 // 16kt + 4q + r, which is the lane's own activation chunk kt: ELU' needs no reload.
 // ------------------------------------------------------------------------------------------------------------------
-constexpr int kHeadWaves = 4;
-constexpr int kHeadThreads = 64 * kHeadWaves;
 constexpr int kHeadRows = 16;     // rows per wavefront tile
+constexpr int kHeadWavesDefault = 4;
 constexpr int kHeadMaxK = 128;    // hidden width of either model's last hidden layer
 constexpr int kHeadMaxA = 32;     // two 16-wide MFMA tiles of actions
 constexpr int kHeadG = kHeadMaxK / 16;
@@ -381,7 +380,8 @@ __device__ __forceinline__ T quarter_sum(T x) {
   return x;
 }
 
-__global__ __launch_bounds__(kHeadThreads) void ppo_head_kernel(const HeadParams P, double* __restrict__ partials) {
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void ppo_head_kernel(const HeadParams P, double* __restrict__ partials) {
   const LossParams& p = P.lp;
   const ppo_loss_args& a = p.a;
   const ppo_policy_head& H = P.h;
@@ -391,33 +391,40 @@ __global__ __launch_bounds__(kHeadThreads) void ppo_head_kernel(const HeadParams
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int m = lane & 15, q = lane >> 4;
   const int NT = A > 16 ? 2 : 1;  // 16-wide action tiles
+  constexpr int kThreads = 64 * WAVES;
 
   __shared__ __align__(16) float s_w[kHeadMaxA * kHeadWs];    // W_a [a][k], rows a >= A zero
   __shared__ __align__(16) float s_wt[kHeadMaxK * kHeadWts];  // W_a^T [k][a], columns a >= A zero
   __shared__ __align__(16) float s_wc[kHeadMaxK];
   __shared__ float s_b[kHeadMaxA], s_std[kHeadMaxA], s_var[kHeadMaxA], s_log[kHeadMaxA];
-  __shared__ double s_red[kHeadWaves][kFixedCols + PPO_MAX_ACTIONS];
+  __shared__ double s_red[WAVES][kFixedCols + PPO_MAX_ACTIONS];
 
   // the first tile's loads go out before the weights are staged, so both latencies overlap
   const int64_t tiles = ceil_div(R, kHeadRows);
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kHeadWaves;
-  int64_t tile = static_cast<int64_t>(blockIdx.x) * kHeadWaves + wave;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * WAVES;
+  int64_t tile = static_cast<int64_t>(blockIdx.x) * WAVES + wave;
   HeadTileIn in;
   if (tile < tiles) head_load_tile(P, tile, lane, in);
 
   {  // W_a as float4 rows: every load issued before the first LDS write
-    constexpr int kPer = kHeadMaxA * kHeadMaxK / 4 / kHeadThreads;
+    constexpr int kPer = kHeadMaxA * kHeadMaxK / 4 / kThreads;
     const int cpr = KA / 4;  // float4 chunks per weight row
     f32x4 wv[kPer];
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int i = threadIdx.x + u * kHeadThreads;
+      const int i = threadIdx.x + u * kThreads;
       const int r = i / cpr, k = 4 * (i - r * cpr);
       const bool ok = i < kHeadMaxA * cpr && r < A;
       wv[u] = ld4(H.w_actor + (ok ? static_cast<int64_t>(r) * KA + k : 0));
       if (!ok) wv[u] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    const float wc = threadIdx.x < KC ? H.w_critic[threadIdx.x] : 0.0f;
+    constexpr int kWcPer = (kHeadMaxK + kThreads - 1) / kThreads;
+    float wc[kWcPer];
+#pragma unroll
+    for (int u = 0; u < kWcPer; ++u) {
+      const int k = threadIdx.x + u * kThreads;
+      wc[u] = k < KC ? H.w_critic[k] : 0.0f;
+    }
     float sp = 0.0f, b = 0.0f;
     if (threadIdx.x < A) {
       sp = a.std_param[threadIdx.x];
@@ -425,7 +432,7 @@ __global__ __launch_bounds__(kHeadThreads) void ppo_head_kernel(const HeadParams
     }
 #pragma unroll
     for (int u = 0; u < kPer; ++u) {
-      const int i = threadIdx.x + u * kHeadThreads;
+      const int i = threadIdx.x + u * kThreads;
       if (i < kHeadMaxA * cpr) {
         const int r = i / cpr, k = 4 * (i - r * cpr);
         st4(s_w + r * kHeadWs + k, wv[u]);
@@ -433,7 +440,9 @@ __global__ __launch_bounds__(kHeadThreads) void ppo_head_kernel(const HeadParams
         for (int e = 0; e < 4; ++e) s_wt[(k + e) * kHeadWts + r] = wv[u][e];
       }
     }
-    if (threadIdx.x < KC) s_wc[threadIdx.x] = wc;
+#pragma unroll
+    for (int u = 0; u < kWcPer; ++u)
+      if (threadIdx.x + u * kThreads < KC) s_wc[threadIdx.x + u * kThreads] = wc[u];
     if (threadIdx.x < kHeadMaxA) {
       float sd = 1.0f, lg = 0.0f;
       if (threadIdx.x < A) std_from_param(sp, a.std_type, p.std_lo, p.std_hi, sd, lg);
@@ -648,9 +657,9 @@ __global__ __launch_bounds__(kHeadThreads) void ppo_head_kernel(const HeadParams
   }
   __syncthreads();
   const int cols = kFixedCols + A;
-  for (int c = threadIdx.x; c < cols; c += kHeadThreads) {
+  for (int c = threadIdx.x; c < cols; c += kThreads) {
     double sum = 0.0;
-    for (int w = 0; w < kHeadWaves; ++w) sum += s_red[w][c];
+    for (int w = 0; w < WAVES; ++w) sum += s_red[w][c];
     partials[static_cast<int64_t>(c) * gridDim.x + blockIdx.x] = sum;
   }
 }
@@ -660,10 +669,18 @@ bool head_supported(int num_actions, int k_actor, int k_critic) {
          k_actor % 16 == 0 && k_critic >= 16 && k_critic <= kHeadMaxK && k_critic % 16 == 0;
 }
 
-// Blocks of the fused head kernel: one 16-row tile per wave while that fits in 1024 blocks (4 per CU), else 1024
-// blocks that stride over the tiles (the partials the finalize reduces stay bounded).
+// Wavefronts per block of the fused head kernel; "PPO_HIP_HEAD_WAVES" (1, 2 or 4) overrides it (tuning aid).
+int head_waves() {
+  const char* e = std::getenv("PPO_HIP_HEAD_WAVES");
+  const int w = e ? std::atoi(e) : kHeadWavesDefault;
+  return (w == 1 || w == 2 || w == 4) ? w : kHeadWavesDefault;
+}
+
+// Blocks of the fused head kernel: one 16-row tile per wave while that fits in 1024 blocks, else 1024 blocks that
+// stride over the tiles (the partials the finalize reduces stay bounded).  Host arithmetic only: the workspace query
+// must agree with the launch.
 int64_t head_blocks(int64_t rows) {
-  return std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(ceil_div(rows, kHeadRows), kHeadWaves)));
+  return std::max<int64_t>(1, std::min<int64_t>(1024, ceil_div(ceil_div(rows, kHeadRows), head_waves())));
 }
 
 int lanes_per_row(int num_actions) { return num_actions <= 32 ? 32 : 64; }
@@ -813,8 +830,15 @@ extern "C" int ppo_gauss_ppo_head(const ppo_loss_args* args, const ppo_policy_he
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", who,
               workspace_bytes, need);
   const int64_t blocks = head_blocks(a.rows);
-  hipLaunchKernelGGL(ppo_head_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kHeadThreads), 0,
-                     static_cast<hipStream_t>(stream), P, static_cast<double*>(workspace));
+  auto launch = [&](auto kernel, int waves) {
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * waves), 0,
+                       static_cast<hipStream_t>(stream), P, static_cast<double*>(workspace));
+  };
+  switch (head_waves()) {
+    case 1: launch(ppo_head_kernel<1>, 1); break;
+    case 2: launch(ppo_head_kernel<2>, 2); break;
+    default: launch(ppo_head_kernel<4>, 4); break;
+  }
   rc = check_launch("ppo_head_kernel");
   if (rc != PPO_OK) return rc;
   return launch_finalize(P.lp, workspace, blocks, d_std_param, state, adaptive, desired_kl, trace, stream);
