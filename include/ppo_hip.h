@@ -92,6 +92,12 @@ int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_rows, const p
  * (state_bytes = 5056), advanced in place by the n - 1 draws (write it back with torch.set_rng_state()).
  * out: int64 [n] host memory.  PPO_EINVAL when the record's layout is not recognised (nothing is written). */
 int ppo_host_randperm(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t* out);
+/* The same shuffle in consecutive pieces: iterations [i0, i1) (0 <= i0 <= i1 <= n - 1) of it, drawing i1 - i0
+ * values from the generator record and advancing it; out holds the result of iterations [0, i0) (it is set to the
+ * identity when i0 = 0).  Positions [0, i1) of out are final afterwards.  Running [0, s) then [s, n - 1) gives
+ * exactly ppo_host_randperm's permutation and generator state. */
+int ppo_host_randperm_range(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t i0, int64_t i1,
+                            int64_t* out);
 
 /* ------------------------------------------------------------------------------------------------------------------
  * A6  Linear layers of rsl_rl/modules/mlp.py:27-95 (nn.Linear + nn.ELU), forward and hand-written backward, as fp32

@@ -154,6 +154,34 @@ def test_update_matches_oracle(name):
             assert rel_err(n_h._var, n_o._var) < 1e-6
 
 
+def test_recorded_launches_match_rebuilt_launches():
+    """From the third update on, the engine issues each mini-batch from its recorded launch sequence (only Adam's bias
+    corrections recomputed); those updates must equal, bit for bit, updates whose every launch is rebuilt in Python:
+    parameters, Adam moments, losses and learning rate, over several consecutive updates (obs normalisation on, so the
+    frozen normaliser statistics and the normaliser update are exercised too)."""
+    w = R.scaled(R.WORKLOADS["humanoid"], num_envs=256, steps=8, hidden_dims=[64, 32])
+    _, a, _ = make_pair(w, seed=0)
+    _, b, _ = make_pair(w, seed=0)
+    for alg, replay in ((a, True), (b, False)):
+        alg._get_engine().replay = replay
+    for rep in range(4):
+        outs = []
+        for alg in (a, b):
+            alg.storage.step = alg.storage.num_transitions_per_env
+            torch.manual_seed(1 + rep)
+            outs.append(alg.update())
+        torch.cuda.synchronize()
+        assert outs[0] == outs[1], rep
+        assert a.learning_rate == b.learning_rate
+        for pa, pb in zip(chain(a.actor.parameters(), a.critic.parameters()),
+                          chain(b.actor.parameters(), b.critic.parameters())):
+            assert torch.equal(pa, pb), rep
+        assert torch.equal(a.flat.exp_avg, b.flat.exp_avg) and torch.equal(a.flat.exp_avg_sq, b.flat.exp_avg_sq)
+        for ma, mb in ((a.actor, b.actor), (a.critic, b.critic)):
+            assert torch.equal(ma.obs_normalizer._mean, mb.obs_normalizer._mean)
+    assert a._engine.replays > 0 and b._engine.replays == 0
+
+
 def _adam_state(opt, p):
     st = opt.state.get(p, {})
     if "exp_avg" not in st:

@@ -163,6 +163,44 @@ def test_host_randperm_is_torch_randperm(seed, n, pre):
     assert torch.equal(torch.rand(4), ref_next)
 
 
+@pytest.mark.parametrize("n, split", [(98304, 24576), (1000, 0), (1000, 999), (1000, 5000), (2, 1), (1, 0),
+                                      (1572864, 393216)])
+def test_split_randperm_is_torch_randperm(n, split):
+    """The permutation drawn in two pieces (the first mini-batch's positions, then the rest on a worker thread)
+    equals torch.randperm(n) and leaves the generator where torch.randperm leaves it; positions [0, split) are
+    already final after the first piece."""
+    from tt_rsl_rl_amd import ops
+
+    torch.manual_seed(n + split)
+    torch.rand(3)
+    start = torch.get_rng_state()
+    ref = torch.randperm(n)
+    ref_state, ref_next = torch.get_rng_state(), torch.rand(4)
+    torch.set_rng_state(start)
+    out = torch.empty(n, dtype=torch.int64)
+    sh = ops.SplitRandperm(n, out, split)
+    k = sh.split
+    assert torch.equal(out[:k], ref[:k]), "the first piece's positions must be final"
+    got = sh.join()
+    assert torch.equal(got, ref)
+    assert torch.equal(torch.get_rng_state(), ref_state)
+    assert torch.equal(torch.rand(4), ref_next)
+    sh.join()  # idempotent
+
+
+def test_host_randperm_range_validation():
+    from tt_rsl_rl_amd import _lib
+
+    lib = _lib.load()
+    rec = bytearray(torch.get_rng_state().numpy().tobytes())
+    buf = (ctypes.c_uint8 * len(rec)).from_buffer(rec)
+    out = (ctypes.c_int64 * 10)()
+    assert lib.ppo_host_randperm_range(buf, len(rec), 10, 3, 2, out) == _lib.PPO_EINVAL
+    assert lib.ppo_host_randperm_range(buf, len(rec), 10, 0, 10, out) == _lib.PPO_EINVAL
+    assert "outside" in _lib.last_error()
+    assert lib.ppo_host_randperm_range(buf, len(rec), 10, 0, 9, out) == _lib.PPO_OK
+
+
 def test_host_randperm_rejects_unknown_generator_records():
     from tt_rsl_rl_amd import _lib
 

@@ -142,6 +142,7 @@ _SIGNATURES = [
     ("ppo_gauss_sample", C.c_int, [f32p, i64, f32p, i32, C.c_double, C.c_double, f32p, i64, f32p, i64, f32p, f32p,
                                    i64, i64, i32, C.c_void_p]),
     ("ppo_host_randperm", C.c_int, [C.c_void_p, C.c_size_t, i64, C.c_void_p]),
+    ("ppo_host_randperm_range", C.c_int, [C.c_void_p, C.c_size_t, i64, i64, i64, C.c_void_p]),
     ("ppo_adam_workspace_bytes", C.c_size_t, [i64]),
     ("ppo_adam_step", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double, C.c_double,
                                 C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_size_t,
@@ -189,8 +190,15 @@ def check(status: int, what: str) -> None:
     raise RuntimeError(msg)
 
 
+# When set (a list), every call() is appended to it as (name, args) before it runs: a launch sequence recorded this
+# way can be issued again later with the same arguments (the ctypes objects in args stay referenced by the list).
+recorder: list | None = None
+
+
 def call(name: str, *args) -> None:
     """Call an int-returning entry point and raise on a non-zero status."""
+    if recorder is not None:
+        recorder.append((name, args))
     check(getattr(load(), name)(*args), name)
 
 

@@ -8,6 +8,10 @@
 // are produced in three passes: all n - 1 draws (MT19937 twisted a block of 624 words at a time), all moduli (a
 // vectorisable double quotient with an exact integer correction), then the swaps, which alone are sequential.
 //
+// The shuffle also runs as consecutive ranges of iterations [i0, i1) (ppo_host_randperm_range): iteration i only
+// swaps positions >= i, so positions [0, i1) are final after the first range and their rows can be used while the
+// rest of the shuffle runs; the generator record carries the stream position from one range to the next.
+//
 // The generator state is exchanged as the record torch.get_rng_state() returns (5056 bytes): the initial seed, the
 // MT19937 read position (`left`, `next`) and its 624 state words (each stored in 64 bits), then cached normal
 // samples that the shuffle does not touch.  The caller passes the record in and writes it back with
@@ -106,31 +110,42 @@ void store_state(const Mt19937& mt, uint8_t* rec) {
 
 using namespace ppo;
 
-extern "C" int ppo_host_randperm(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t* out) {
-  PPO_REQUIRE(generator_state != nullptr && out != nullptr, "ppo_host_randperm: null pointer");
-  PPO_REQUIRE(state_bytes == kStateBytes, "ppo_host_randperm: generator record of %zu bytes (expected %zu)",
-              state_bytes, kStateBytes);
-  PPO_REQUIRE(n >= 1 && n < (int64_t(1) << 31), "ppo_host_randperm: n=%lld", (long long)n);
+namespace ppo {
+namespace {
+
+// Iterations [i0, i1) of the shuffle on `out`, which holds the result of iterations [0, i0) (the identity for
+// i0 = 0): z_i = draw mod (n - i), swap(out[i], out[i + z_i]).  Iteration i only touches positions >= i, so after
+// the call out[0, i1) is final.
+int shuffle_range(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t i0, int64_t i1, int64_t* out,
+                  const char* who) {
+  PPO_REQUIRE(generator_state != nullptr && out != nullptr, "%s: null pointer", who);
+  PPO_REQUIRE(state_bytes == kStateBytes, "%s: generator record of %zu bytes (expected %zu)", who, state_bytes,
+              kStateBytes);
+  PPO_REQUIRE(n >= 1 && n < (int64_t(1) << 31), "%s: n=%lld", who, (long long)n);
+  PPO_REQUIRE(i0 >= 0 && i0 <= i1 && i1 <= n - 1, "%s: iterations [%lld, %lld) outside [0, %lld)", who,
+              (long long)i0, (long long)i1, (long long)(n - 1));
   Mt19937 mt;
   if (int rc = load_state(generator_state, mt)) return rc;
-  for (int64_t i = 0; i < n; ++i) out[i] = i;
-  if (n > 1) {
-    const int64_t m = n - 1;
+  if (i0 == 0)
+    for (int64_t i = 0; i < n; ++i) out[i] = i;
+  const int64_t m = i1 - i0;
+  if (m > 0) {
     std::vector<uint32_t> z(static_cast<size_t>(m));
     mt.draws(z.data(), m);
     // z_i = draw_i mod (n - i) through a double quotient (exact operands < 2^32; the rounded quotient is at most
     // one too large, which the correction undoes), so the loop vectorises instead of issuing integer divides
-    for (int64_t i = 0; i < m; ++i) {
-      const double d = static_cast<double>(n - i), x = static_cast<double>(z[i]);
+    for (int64_t k = 0; k < m; ++k) {
+      const double d = static_cast<double>(n - i0 - k), x = static_cast<double>(z[k]);
       double r = x - static_cast<double>(static_cast<int64_t>(x / d)) * d;
       r = r < 0.0 ? r + d : r;
-      z[i] = static_cast<uint32_t>(r);
+      z[k] = static_cast<uint32_t>(r);
     }
     // the swaps are sequential; their targets are known, so the line of a later swap is fetched ahead
     constexpr int64_t kAhead = 16;
-    for (int64_t i = 0; i < m; ++i) {
-      if (i + kAhead < m) __builtin_prefetch(out + i + kAhead + z[i + kAhead], 1);
-      const int64_t j = i + z[i];
+    for (int64_t k = 0; k < m; ++k) {
+      const int64_t i = i0 + k;
+      if (k + kAhead < m) __builtin_prefetch(out + i + kAhead + z[k + kAhead], 1);
+      const int64_t j = i + z[k];
       const int64_t t = out[i];
       out[i] = out[j];
       out[j] = t;
@@ -138,4 +153,16 @@ extern "C" int ppo_host_randperm(uint8_t* generator_state, size_t state_bytes, i
   }
   store_state(mt, generator_state);
   return PPO_OK;
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_host_randperm(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t* out) {
+  return shuffle_range(generator_state, state_bytes, n, 0, n - 1, out, "ppo_host_randperm");
+}
+
+extern "C" int ppo_host_randperm_range(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t i0,
+                                       int64_t i1, int64_t* out) {
+  return shuffle_range(generator_state, state_bytes, n, i0, i1, out, "ppo_host_randperm_range");
 }

@@ -101,8 +101,31 @@ class _NoTimer:
         pass
 
 
+class _RecordingTimer:
+    """Forwards to the engine's timer and appends the phase marks to the launch sequence being recorded."""
+
+    def __init__(self, inner, entries: list) -> None:
+        self.inner, self.entries = inner, entries
+
+    def start(self, name: str) -> None:
+        self.entries.append(("start", name))
+        self.inner.start(name)
+
+    def stop(self, name: str) -> None:
+        self.entries.append(("stop", name))
+        self.inner.stop(name)
+
+
 class UpdateEngine:
-    """Owns the device workspaces of the update and runs it.  Rebuilt when the rollout shape changes."""
+    """Owns the device workspaces of the update and runs it.  Rebuilt when the rollout shape changes.
+
+    Every buffer a launch names is allocated here once, so a mini-batch issues the same launches with the same
+    arguments in every update except for Adam's bias corrections.  The second update (the first one may still grow
+    the workspaces) records each mini-batch's launch sequence (C entry point + ctypes arguments, and the phase-timer
+    marks between them); later updates issue
+    the recorded calls directly, with the bias corrections of their own step, instead of rebuilding every argument
+    in Python: the host then stays ahead of the GPU from the first mini-batch on.  The records are dropped when a
+    hyperparameter or the stream changes."""
 
     recurrent = False
 
@@ -139,12 +162,84 @@ class UpdateEngine:
         self.dx_ws = ops.Workspace(self.device)  # the input-grad's w^T copies
         self.adv_ws = ops.Workspace(self.device)
         self.trace = torch.zeros(5 * alg.num_learning_epochs * self.M, dtype=torch.float64, device=self.device)
+        self.trace_host = torch.empty(self.trace.numel(), dtype=torch.float64, pin_memory=True)
+        # the observation normalisers' statistics as the update's forward passes must see them (pre-update), in
+        # buffers of their own so the recorded gathers keep pointing at them
+        self._norm_frozen: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+        for model in (actor, critic):
+            if model.obs_normalization:
+                norm = model.obs_normalizer
+                self._norm_frozen[id(norm)] = (torch.empty_like(norm._mean.view(-1)),
+                                               torch.empty_like(norm._std.view(-1)))
+        self._frozen = False
+        self._plans: dict = {}
+        self._plan_key = None
+        self._warm = False  # records are kept from the second run on: by then no workspace grows any more
+        self.replays = 0
+        self.replay = os.environ.get("PPO_HIP_LAUNCH_CACHE", "1") != "0" and not self.recurrent
 
     # -- one update ------------------------------------------------------------------------------------------------
-    def gather(self, perm: torch.Tensor) -> None:
+    def freeze_normalizers(self) -> None:
+        """Copy the normalisers' current statistics (device to device, on the stream) for this update's gather, so
+        the normaliser update (upstream runs it after the epochs, ppo.py:327-330) can be launched first and run
+        while the host draws the permutation."""
+        for model in (self.alg.actor, self.alg.critic):
+            if model.obs_normalization:
+                norm = model.obs_normalizer
+                mean, std = self._norm_frozen[id(norm)]
+                mean.copy_(norm._mean.view(-1))
+                std.copy_(norm._std.view(-1))
+        self._frozen = True
+
+    def _norm_stats(self, norm) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._frozen:
+            return self._norm_frozen[id(norm)]
+        return norm._mean.view(-1), norm._std.view(-1)
+
+    # -- recorded launch sequences ------------------------------------------------------------------------------------
+    def _plan_signature(self):
+        a = self.alg
+        return (torch.cuda.current_stream(self.device).cuda_stream, a.clip_param, a.value_loss_coef, a.entropy_coef,
+                a.use_clipped_value_loss, a.desired_kl, a.schedule, a.max_grad_norm, tuple(a.betas), a.adam_eps,
+                a.normalize_advantage_per_mini_batch, a.num_learning_epochs)
+
+    def _issue(self, key, fn, step: int | None = None) -> None:
+        """Run fn (which issues launches through the C ABI) the first time for this key, recording its calls;
+        afterwards issue the recorded calls directly."""
+        plan = self._plans.get(key) if self.replay else None
+        if plan is None:
+            entries: list = []
+            timer = self.timer
+            L.recorder = entries
+            self.timer = _RecordingTimer(timer, entries)
+            try:
+                fn()
+            finally:
+                L.recorder = None
+                self.timer = timer
+            if self.replay and self._warm:
+                self._plans[key] = entries
+            return
+        self.replays += 1
+        lib = L.load()
+        for e in plan:
+            if e[0] == "start":
+                self.timer.start(e[1])
+            elif e[0] == "stop":
+                self.timer.stop(e[1])
+            else:
+                name, args = e
+                if name == "ppo_adam_step":
+                    bc1, bc2_sqrt = self._bias_corrections(step)
+                    args = args[:10] + (float(bc1), float(bc2_sqrt)) + args[12:]
+                L.check(getattr(lib, name)(*args), name)
+
+    def gather(self, perm: torch.Tensor, row0: int = 0) -> None:
+        """Table rows [row0, row0 + len(perm)) = storage rows perm."""
         segs = self.segments()
+        dst = self.table[row0:row0 + perm.numel()]
         for i in range(0, len(segs), L.MAX_GATHER_SEGMENTS):
-            ops.gather_rows(perm, segs[i:i + L.MAX_GATHER_SEGMENTS], self.table)
+            ops.gather_rows(perm, segs[i:i + L.MAX_GATHER_SEGMENTS], dst)
 
     def segments(self) -> list[ops.Segment]:
         """The packed table's column blocks and their storage sources ([T * N, width] views)."""
@@ -157,8 +252,8 @@ class UpdateEngine:
                 src = st.flat(st.observations[g])
                 w = src.shape[1]
                 if norm is not None:
-                    segs.append(ops.Segment(src, base + col, norm._mean.view(-1)[col:col + w],
-                                            norm._std.view(-1)[col:col + w], norm.eps))
+                    mean, std = self._norm_stats(norm)
+                    segs.append(ops.Segment(src, base + col, mean[col:col + w], std[col:col + w], norm.eps))
                 else:
                     segs.append(ops.Segment(src, base + col))
                 col += w
@@ -281,12 +376,16 @@ class UpdateEngine:
             ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, ws if ws is not None else self.dw_ws)
         tm.stop(phase)
 
+    def _bias_corrections(self, step: int) -> tuple[float, float]:
+        """torch.optim.Adam's 1 - b1^t and sqrt(1 - b2^t), in Python floats as torch computes them."""
+        b1, b2 = self.alg.betas
+        return 1 - b1 ** step, (1 - b2 ** step) ** 0.5
+
     def adam(self, step: int) -> None:
         """Per-model clip + Adam over the flat buffers."""
         alg = self.alg
         b1, b2 = alg.betas
-        bc1 = 1 - b1 ** step
-        bc2_sqrt = (1 - b2 ** step) ** 0.5
+        bc1, bc2_sqrt = self._bias_corrections(step)
         f = alg.flat
         tm = self.timer
         tm.start("adam")
@@ -297,18 +396,44 @@ class UpdateEngine:
     def minibatch_rows(self, i: int) -> tuple[int, int]:
         return i * self.B // self.M, (i + 1) * self.B // self.M
 
-    def run(self, perm: torch.Tensor, first_step: int) -> int:
-        """All epochs x mini-batches.  Returns the number of optimiser steps taken."""
-        self.timer.start("gather")
-        self.gather(perm)
-        self.timer.stop("gather")
+    def run(self, perm: torch.Tensor, first_step: int, ready: int | None = None, rest=None) -> int:
+        """All epochs x mini-batches.  Returns the number of optimiser steps taken.  With ``rest``, only
+        ``perm[:ready]`` is final at the call: those rows are gathered first, and ``rest()`` (which completes
+        ``perm``) is called once the first mini-batch is enqueued, before any row past ``ready`` is needed."""
+        sig = self._plan_signature()
+        if sig != self._plan_key:
+            self._plans.clear()
+            self._plan_key = sig
+        first = perm if rest is None else perm[:ready]
+
+        def gather_first():
+            self.timer.start("gather")
+            self.gather(first)
+            self.timer.stop("gather")
+
+        self._issue(("gather", 0, None if perm is None else first.numel(), None if perm is None else perm.data_ptr()),
+                    gather_first)
         self.trace.zero_()
         step = first_step
-        for _ in range(self.alg.num_learning_epochs):
-            for i in range(self.M):
-                r0, r1 = self.minibatch_rows(i)
-                step += 1
-                self.minibatch(r0, r1, step)
+        try:
+            for _ in range(self.alg.num_learning_epochs):
+                for i in range(self.M):
+                    r0, r1 = self.minibatch_rows(i)
+                    if rest is not None and r1 > ready:
+                        rest()
+                        rest = None
+
+                        def gather_rest():
+                            self.timer.start("gather")
+                            self.gather(perm[ready:], ready)
+                            self.timer.stop("gather")
+
+                        self._issue(("gather", ready, perm.numel() - ready, perm.data_ptr()), gather_rest)
+                    step += 1
+                    self._issue(("minibatch", r0, r1), lambda: self.minibatch(r0, r1, step), step)
+        finally:
+            self._frozen = False
+        self._warm = True
         return step - first_step
 
 

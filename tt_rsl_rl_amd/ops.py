@@ -118,6 +118,57 @@ def host_randperm(n: int, out: torch.Tensor | None = None) -> torch.Tensor:
     return out
 
 
+class SplitRandperm:
+    """``torch.randperm(n)`` on the CPU generator in two pieces (rsl_rl/storage/rollout_storage.py:232): iterations
+    [0, split) of the shuffle now, which makes positions [0, split) final, and iterations [split, n - 1) on a worker
+    thread (the native call runs without the GIL) while the caller launches work on the first rows.  ``join()``
+    waits for the rest and writes the generator state back; between ``__init__`` and ``join()`` nothing may draw
+    from the CPU generator.  The result is bit-identical to ``host_randperm``: the same permutation, the same final
+    generator state.  A generator record of an unexpected layout falls back to ``torch.randperm`` in one piece."""
+
+    _pool = None
+
+    def __init__(self, n: int, out: torch.Tensor, split: int) -> None:
+        import ctypes
+
+        if out.dtype != torch.int64 or out.device.type != "cpu" or out.numel() != n or not out.is_contiguous():
+            raise ValueError("SplitRandperm: out must be a contiguous int64 CPU tensor of n elements")
+        self.n, self.out = n, out
+        self.split = max(0, min(int(split), n - 1))
+        self._rec = bytearray(torch.get_rng_state().numpy().tobytes())
+        self._buf = (ctypes.c_uint8 * len(self._rec)).from_buffer(self._rec)
+        self._future = None
+        lib = L.load()
+        if lib.ppo_host_randperm_range(self._buf, len(self._rec), n, 0, self.split, out.data_ptr()) != L.PPO_OK:
+            out.copy_(torch.randperm(n))
+            self._rec = None
+            self.split = n
+            return
+        if self.split < n - 1:
+            if SplitRandperm._pool is None:
+                from concurrent.futures import ThreadPoolExecutor
+
+                SplitRandperm._pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="ppo-randperm")
+            self._future = SplitRandperm._pool.submit(self._rest)
+
+    def _rest(self) -> str | None:
+        lib = L.load()
+        rc = lib.ppo_host_randperm_range(self._buf, len(self._rec), self.n, self.split, self.n - 1,
+                                         self.out.data_ptr())
+        return None if rc == L.PPO_OK else L.last_error()  # the error text is thread-local: read it here
+
+    def join(self) -> torch.Tensor:
+        if self._future is not None:
+            err = self._future.result()
+            self._future = None
+            if err is not None:
+                raise RuntimeError(f"ppo_host_randperm_range: {err}")
+        if self._rec is not None:
+            torch.set_rng_state(torch.frombuffer(self._rec, dtype=torch.uint8).clone())
+            self._rec = None
+        return self.out
+
+
 def gather_rows(perm: torch.Tensor, segments: list[Segment], dst: torch.Tensor) -> None:
     """dst[j, seg.dst_col : +width] = f(seg.src[perm[j]])  (f = identity or the obs normaliser)."""
     _dev(dst)
@@ -290,6 +341,15 @@ def reset_device_state(st: torch.Tensor, learning_rate: float) -> None:
 def read_device_state(st: torch.Tensor) -> L.DeviceState:
     raw = st.cpu().numpy().tobytes()
     return L.DeviceState.from_buffer_copy(raw)
+
+
+def pinned_state_buffer() -> torch.Tensor:
+    """Host staging buffer for an asynchronous read-back of a device state."""
+    return torch.empty(L.DEVICE_STATE_BYTES, dtype=torch.uint8, pin_memory=True)
+
+
+def device_state_from_host(host: torch.Tensor) -> L.DeviceState:
+    return L.DeviceState.from_buffer_copy(host.numpy().tobytes())
 
 
 def make_loss_args(rows: int, mean: torch.Tensor, value: torch.Tensor, batch: dict, std_param: torch.Tensor,

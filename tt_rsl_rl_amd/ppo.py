@@ -214,6 +214,7 @@ class PPO:
         self._engine: UpdateEngine | None = None
         self._adv_ws = ops.Workspace(self.device)
         self._perm_host: torch.Tensor | None = None
+        self._state_host = ops.pinned_state_buffer()
         self.last_trace: list[dict] = []
 
     # -- rollout side ------------------------------------------------------------------------------------------------
@@ -278,39 +279,66 @@ class PPO:
             raise RuntimeError("update() called before any transition was stored")
         engine = self._get_engine()
         ops.reset_device_state(self.device_state, self.learning_rate)
-        # feed-forward: one permutation of the batch for all epochs (ppo.py:207, rollout_storage.py:210-260);
-        # recurrent: fixed env slices, no permutation drawn (rollout_storage.py:262-331)
-        perm = None
-        if not self.is_recurrent:
-            if self._perm_host is None or self._perm_host.numel() != B:
-                self._perm_host = torch.empty(B, dtype=torch.int64, pin_memory=True)
-            # torch.randperm(B) on the CPU generator, computed natively (same permutation, same generator state)
-            perm = ops.host_randperm(B, self._perm_host).to(self.device, non_blocking=True)
-        steps = engine.run(perm, self._opt_steps)
-        self._opt_steps += steps
-
+        # The normaliser update (upstream: after the epochs, ppo.py:327-330) reads only the stored raw observations;
+        # launched first, on the frozen pre-update statistics the gather uses, it runs while the host draws the
+        # permutation.  The epochs see the same statistics as upstream's.
+        engine.freeze_normalizers()
         obs = st.observations
         self.actor.update_normalization(obs)
         self.critic.update_normalization(obs)
+        # feed-forward: one permutation of the batch for all epochs (ppo.py:207, rollout_storage.py:210-260);
+        # recurrent: fixed env slices, no permutation drawn (rollout_storage.py:262-331)
+        perm, ready, rest, shuffle = None, None, None, None
+        if not self.is_recurrent:
+            if self._perm_host is None or self._perm_host.numel() != B:
+                self._perm_host = torch.empty(B, dtype=torch.int64, pin_memory=True)
+                self._perm_dev = torch.empty(B, dtype=torch.int64, device=self.device)
+            # torch.randperm(B) on the CPU generator, computed natively (same permutation, same generator state):
+            # the first mini-batch's positions now, the rest on a worker thread while its kernels are enqueued
+            ready = engine.minibatch_rows(0)[1]
+            shuffle = ops.SplitRandperm(B, self._perm_host, ready)
+            ready = shuffle.split if shuffle.split < B - 1 else B
+            perm = self._perm_dev
+            perm[:ready].copy_(self._perm_host[:ready], non_blocking=True)
+            if ready < B:
+                def rest():
+                    shuffle.join()
+                    perm[ready:].copy_(self._perm_host[ready:], non_blocking=True)
+            else:
+                shuffle.join()
+        try:
+            steps = engine.run(perm, self._opt_steps, ready, rest)
+        finally:
+            if shuffle is not None:
+                shuffle.join()  # idempotent; on an error path it still restores the generator before raising
+        self._opt_steps += steps
 
-        state = ops.read_device_state(self.device_state)  # the one host sync of the update
+        # the one host sync of the update: device state and per-mini-batch trace, two async copies, one wait
+        self._state_host.copy_(self.device_state, non_blocking=True)
+        engine.trace_host.copy_(engine.trace, non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        state = ops.device_state_from_host(self._state_host)
         self.learning_rate = state.learning_rate
         for group in self.optimizer.param_groups:
             group["lr"] = self.learning_rate
         self._sync_optimizer_state()
         n = self.num_learning_epochs * self.num_mini_batches
-        trace = engine.trace.view(-1, 5).cpu().tolist()
+        trace = engine.trace_host.view(-1, 5).tolist()
         self.last_trace = [dict(kl_mean=t[0], lr=t[1], surrogate=t[2], value=t[3], entropy=t[4]) for t in trace]
         st.clear()
         return {"value": state.sum_value_loss / n, "surrogate": state.sum_surrogate_loss / n,
                 "entropy": state.sum_entropy / n}
 
     def _sync_optimizer_state(self) -> None:
-        """Expose the flat Adam moments through torch.optim.Adam's state (views, no copies)."""
-        step = torch.tensor(float(self._opt_steps))
+        """Expose the flat Adam moments through torch.optim.Adam's state (views, no copies); the per-parameter step
+        tensors are updated in place once they exist."""
+        steps = float(self._opt_steps)
         for p in self.flat.params:
             s = self.optimizer.state[p]
-            s["step"] = step.clone()
+            if s.get("exp_avg") is not None and s["exp_avg"].data_ptr() == self.flat.exp_avg_view(p).data_ptr():
+                s["step"].fill_(steps)
+                continue
+            s["step"] = torch.tensor(steps)
             s["exp_avg"] = self.flat.exp_avg_view(p)
             s["exp_avg_sq"] = self.flat.exp_avg_sq_view(p)
 
