@@ -331,11 +331,16 @@ def new_device_state(learning_rate: float, device) -> torch.Tensor:
     return st
 
 
-def reset_device_state(st: torch.Tensor, learning_rate: float) -> None:
+def reset_device_state(st: torch.Tensor, learning_rate: float, staging: torch.Tensor | None = None) -> None:
+    """Zero the device state and set its learning rate.  With ``staging`` (a pinned host buffer of the state's size,
+    not in use by an earlier copy still in flight) the copy is asynchronous."""
     host = L.DeviceState()
     host.learning_rate = float(learning_rate)
-    raw = torch.frombuffer(bytearray(bytes(host)), dtype=torch.uint8)
-    st.copy_(raw)
+    if staging is None:
+        st.copy_(torch.frombuffer(bytearray(bytes(host)), dtype=torch.uint8))
+        return
+    staging.numpy()[:] = memoryview(bytes(host))
+    st.copy_(staging, non_blocking=True)
 
 
 def read_device_state(st: torch.Tensor) -> L.DeviceState:

@@ -215,7 +215,9 @@ class PPO:
         self._adv_ws = ops.Workspace(self.device)
         self._perm_host: torch.Tensor | None = None
         self._state_host = ops.pinned_state_buffer()
-        self.last_trace: list[dict] = []
+        self._reset_host = ops.pinned_state_buffer()
+        self._trace_rows: list | None = None
+        self._step_tensor: torch.Tensor | None = None
 
     # -- rollout side ------------------------------------------------------------------------------------------------
     def act(self, obs: Mapping) -> torch.Tensor:
@@ -278,7 +280,8 @@ class PPO:
         if st.distribution_params is None:
             raise RuntimeError("update() called before any transition was stored")
         engine = self._get_engine()
-        ops.reset_device_state(self.device_state, self.learning_rate)
+        # the staging buffer's previous copy (one update ago) completed at that update's read-back
+        ops.reset_device_state(self.device_state, self.learning_rate, self._reset_host)
         # The normaliser update (upstream: after the epochs, ppo.py:327-330) reads only the stored raw observations;
         # launched first, on the frozen pre-update statistics the gather uses, it runs while the host draws the
         # permutation.  The epochs see the same statistics as upstream's.
@@ -323,22 +326,31 @@ class PPO:
             group["lr"] = self.learning_rate
         self._sync_optimizer_state()
         n = self.num_learning_epochs * self.num_mini_batches
-        trace = engine.trace_host.view(-1, 5).tolist()
-        self.last_trace = [dict(kl_mean=t[0], lr=t[1], surrogate=t[2], value=t[3], entropy=t[4]) for t in trace]
+        self._trace_rows = engine.trace_host.view(-1, 5).clone()
         st.clear()
         return {"value": state.sum_value_loss / n, "surrogate": state.sum_surrogate_loss / n,
                 "entropy": state.sum_entropy / n}
 
+    @property
+    def last_trace(self) -> list[dict]:
+        """Per mini-batch of the last update: KL mean, learning rate after the adaptive rule, and the three losses."""
+        if self._trace_rows is None:
+            return []
+        return [dict(kl_mean=t[0], lr=t[1], surrogate=t[2], value=t[3], entropy=t[4])
+                for t in self._trace_rows.tolist()]
+
     def _sync_optimizer_state(self) -> None:
-        """Expose the flat Adam moments through torch.optim.Adam's state (views, no copies); the per-parameter step
-        tensors are updated in place once they exist."""
+        """Expose the flat Adam moments through torch.optim.Adam's state (views, no copies).  Every parameter takes
+        the same number of steps, so they share one step tensor, updated in place."""
         steps = float(self._opt_steps)
+        if self._step_tensor is not None and all(
+                self.optimizer.state[p].get("step") is self._step_tensor for p in self.flat.params):
+            self._step_tensor.fill_(steps)
+            return
+        self._step_tensor = torch.tensor(steps)
         for p in self.flat.params:
             s = self.optimizer.state[p]
-            if s.get("exp_avg") is not None and s["exp_avg"].data_ptr() == self.flat.exp_avg_view(p).data_ptr():
-                s["step"].fill_(steps)
-                continue
-            s["step"] = torch.tensor(steps)
+            s["step"] = self._step_tensor
             s["exp_avg"] = self.flat.exp_avg_view(p)
             s["exp_avg_sq"] = self.flat.exp_avg_sq_view(p)
 
