@@ -55,6 +55,8 @@ def _lstm(num_envs: int, steps: int, hidden: int, hidden_dims: list[int], **kw) 
 
 
 CASES = {
+    # the headline workload at its full size: 4096 envs x 24 steps, 5 epochs x 4 mini-batches of 24,576 rows
+    "humanoid_full": (R.WORKLOADS["humanoid"], {}),
     "humanoid_1k": (R.scaled(R.WORKLOADS["humanoid"], num_envs=1024), {}),
     "flat48_1k": (R.scaled(R.WORKLOADS["flat48"], num_envs=1024), {}),
     "rough235_512": (R.scaled(R.WORKLOADS["rough235"], num_envs=512), {}),
@@ -275,7 +277,7 @@ def test_state_dict_and_checkpoint_round_trip(tmp_path):
 @pytest.mark.parametrize("name", ["humanoid", "flat48_65k", "lstm256"])
 def test_full_size_update_properties(name):
     """At full size (humanoid and lstm256: 4096 envs x 24 steps; flat48_65k: 65,536 envs x 24 steps, mini-batches of
-    393,216 rows), where the CPU oracle is too slow to run: the update runs, the losses are finite, parameters moved
+    393,216 rows; humanoid is also compared with the oracle in test_update_matches_oracle): the update runs, the losses are finite, parameters moved
     by at most 20 Adam steps' worth (the lr is clamped to [1e-5, 1e-2]), and two identical updates give bit-identical
     parameters (deterministic reductions).  lstm256 starts its sequences from random saved states."""
     from tests.parity import make_hip
