@@ -798,13 +798,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
     const float* As = lds + (kt % S) * STAGE;
     const float* Bs = As + BK * BM;
-    if (do_colsum) {  // column c = tid % BM, rows of this thread's half of the slab, 4 independent chains
-      const int c = tid % BM, k0 = (tid / BM) * (BK / 2);
-#pragma unroll
-      for (int kk = 0; kk < BK / 2; ++kk) colsum_acc[kk & 3] += static_cast<double>(As[(k0 + kk) * BM + c]);
-    }
+    // Column sums for the bias gradient: column c = tid % BM over this thread's half of the slab (BK / 2 = 4 G
+    // rows), in 4 independent chains (row kk into chain kk & 3).  One row per MFMA k-step, read one step ahead, so
+    // the reads and fp64 adds issue between the MFMAs instead of as a phase of their own; every block computes them
+    // (only the tn == 0 blocks store them), so all blocks of a launch take the same time.
+    const float* cs_col = As + (tid / BM) * (BK / 2) * BM + tid % BM;
+    float cs_cur = cs_col[0];
     // groups of 4 k-steps (8 rows of k): the fragments of group g + 1 are read before the MFMAs of group g issue
     constexpr int G = BK / 8;
+    static_assert(BK / 2 == 4 * G, "one column-sum row per MFMA k-step");
     f32x2 fa[2][4], fb[2][4];
     auto load_group = [&](int buf, int gi) {
 #pragma unroll
@@ -821,13 +823,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       // scheduling fences: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
+      for (int st = 0; st < 4; ++st) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[gi & 1][st][i], fb[gi & 1][st][j], acc[i][j], 0,
                                                              0, 0);
+        const int kk = 4 * gi + st;
+        const float cs_next = kk + 1 < BK / 2 ? cs_col[(kk + 1) * BM] : 0.0f;
+        colsum_acc[st] += static_cast<double>(cs_cur);
+        cs_cur = cs_next;
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
