@@ -435,35 +435,49 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       nt_masked<BN, BK>(B, ldb, col0, N, k0, K, st + BM * BK);
     }
   };
+  // k-groups of 4 MFMA steps; the fragments of group g + 1 are read before the MFMAs of group g issue, and the
+  // fragments of group 0 of slab kt + 1 before the MFMAs of the last group of slab kt: the slab-boundary wait and
+  // barrier sit between the last fragment reads of slab kt and its last MFMAs, so no MFMA waits on an LDS read.
+  constexpr int G = BK / 8;
+  f32x4 fa[2][TM], fb[2][TN];
+  auto load_group = [&](int kt, int buf, int gi) {
+    const float* As = lds + (kt % S) * STAGE;
+    const float* Bs = As + BM * BK;
+    const int c = 2 * gi + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * WM + 32 * i + (lane & 31);
+      fa[buf][i] = *reinterpret_cast<const f32x4*>(As + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn * WN + 32 * j + (lane & 31);
+      fb[buf][j] = *reinterpret_cast<const f32x4*>(Bs + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+    }
+  };
 #pragma unroll
   for (int s = 0; s < S - 1; ++s)
     if (s < nk) issue(s, s);
+  if (nk > 0) {
+    wait_slab<L, S>(min(S - 2, nk - 1));
+    lds_barrier();  // slab 0 is in LDS for every wave
+    if (S - 1 < nk) issue(S - 1, S - 1);
+    load_group(0, 0, 0);
+  }
+  int buf = 0;
   for (int kt = 0; kt < nk; ++kt) {
-    wait_slab<L, S>(min(S - 2, nk - 1 - kt));
-    lds_barrier();  // slab kt is in LDS for every wave; every wave is done with slab kt-1's stage
-    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
-    const float* As = lds + (kt % S) * STAGE;
-    const float* Bs = As + BM * BK;
-    // k-groups of 4 MFMA steps; the fragments of group g + 1 are read before the MFMAs of group g issue
-    constexpr int G = BK / 8;
-    f32x4 fa[2][TM], fb[2][TN];
-    auto load_group = [&](int buf, int gi) {
-      const int c = 2 * gi + (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int r = wm * WM + 32 * i + (lane & 31);
-        fa[buf][i] = *reinterpret_cast<const f32x4*>(As + r * BK + 4 * (c ^ nt_swz<BK>(r)));
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int r = wn * WN + 32 * j + (lane & 31);
-        fb[buf][j] = *reinterpret_cast<const f32x4*>(Bs + r * BK + 4 * (c ^ nt_swz<BK>(r)));
-      }
-    };
-    load_group(0, 0);
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-      if (gi + 1 < G) load_group((gi + 1) & 1, gi + 1);
+      if (gi + 1 < G) {
+        load_group(kt, buf ^ 1, gi + 1);
+      } else if (kt + 1 < nk) {
+        // every wave has its fragments of slab kt (the barrier's lgkmcnt(0)), and slab kt + 1 has landed: slab
+        // kt's stage is free for slab kt + S
+        wait_slab<L, S>(min(S - 2, nk - 2 - kt));
+        lds_barrier();
+        if (kt + S < nk) issue(kt + S, kt % S);
+        load_group(kt + 1, buf ^ 1, 0);
+      }
       // scheduling fences: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -473,8 +487,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
           for (int j = 0; j < TN; ++j)
             // weights (B) as the MFMA's A operand: the accumulator holds the 32 x 32 tile of C transposed
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[gi & 1][j][s], fa[gi & 1][i][s], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[buf][j][s], fa[buf][i][s], acc[i][j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
+      buf ^= 1;
     }
   }
 
