@@ -375,10 +375,20 @@ typedef struct ppo_lstm_seq_problem {
   int32_t reserved;
 } ppo_lstm_seq_problem;
 
+/* Synchronisation buffer of the whole-sequence launches: int32 words for `count` problems of `envs` rows (-1 for an
+ * invalid count or envs).  Word 0 is a sticky status: the library sets it non-zero when the blocks of a
+ * whole-sequence launch stopped waiting for each other (after about 2 s; the outputs of that call are then invalid).
+ * The caller zeroes the buffer once and reads word 0 whenever it checks for errors; the library clears the other
+ * words itself at the start of every call.  Calls that share a buffer must not overlap. */
+int64_t ppo_lstm_seq_sync_words(int32_t count, int64_t envs);
+
+/* sync = NULL: one launch per step.  sync != NULL (sync_words >= ppo_lstm_seq_sync_words(count, envs)): the forward
+ * runs all steps in one launch when H is a multiple of 32 up to 256 and the device holds one row group's blocks at
+ * once (else one launch per step); the results are identical either way.  The backward ignores sync for now. */
 int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
-                     ppo_stream_t stream);
+                     int32_t* sync, int64_t sync_words, ppo_stream_t stream);
 int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
-                     ppo_stream_t stream);
+                     int32_t* sync, int64_t sync_words, ppo_stream_t stream);
 
 /* gate-interleaved gradients -> torch-layout gradients (the bias gradient goes to both b_ih and b_hh). */
 typedef struct ppo_lstm_grad_problem {

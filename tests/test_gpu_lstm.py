@@ -76,3 +76,51 @@ def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H):
     for name, got, want in zip(("w_ih", "w_hh", "b_ih", "b_hh"), grads, ref_grads):
         assert rel_err(got, want) < 1e-5, name
     assert torch.equal(db_g, db_g2)  # the same column sums of dgates, in the same fixed order
+
+
+def _random_sequences(dev, T, E, H, count, seed):
+    from tt_rsl_rl_amd import ops
+
+    gen = torch.Generator().manual_seed(seed)
+    qs = []
+    for _ in range(count):
+        pk = ops.LstmPacked(8, H, dev)
+        w = [torch.randn(4 * H, 8, generator=gen) * 0.3, torch.randn(4 * H, H, generator=gen) / math.sqrt(H),
+             torch.randn(4 * H, generator=gen) * 0.1, torch.randn(4 * H, generator=gen) * 0.1]
+        ops.lstm_pack([(*(t.to(dev) for t in w), pk)])
+        R = T * E
+        dones = (torch.rand(R, generator=gen) < 0.05).float()
+        qs.append(dict(packed=pk, hidden=H, gx=torch.randn(R, 4 * H, generator=gen).to(dev),
+                       h0=(torch.randn(E, H, generator=gen) * 0.5).to(dev),
+                       c0=(torch.randn(E, H, generator=gen) * 0.5).to(dev), keep=(1.0 - dones).to(dev)))
+    return qs
+
+
+def _outputs(q, T, E, H, dev):
+    R = T * E
+    return dict(q, h=torch.full((R, H), float("nan"), device=dev), hs=torch.full((R + E, H), float("nan"), device=dev),
+                c=torch.full((R, H), float("nan"), device=dev), gates=torch.full((R, 4 * H), float("nan"), device=dev))
+
+
+@pytest.mark.parametrize("T,E,H,count", [(24, 1024, 256, 2), (9, 200, 64, 1), (5, 70, 96, 2), (4, 8192, 256, 2),
+                                         (3, 64, 512, 1), (1, 100, 256, 2)])
+def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count):
+    """The whole-sequence forward (row groups of 64 envs synchronised through the sync buffer; 8192 envs need more
+    row groups than the device holds at once, so blocks take several in turn; H = 512 and T = 1 take the per-step
+    launches) gives bit-identical outputs to one launch per step, and leaves the status word clear."""
+    from tt_rsl_rl_amd import ops
+
+    dev = cuda
+    qs = _random_sequences(dev, T, E, H, count, seed=T * 7919 + E + H)
+    per_step = [_outputs(q, T, E, H, dev) for q in qs]
+    ops.lstm_seq_fwd(per_step, T, E)
+    sync = torch.zeros(ops.lstm_seq_sync_words(count, E), dtype=torch.int32, device=dev)
+    for rep in range(2):  # a second call reuses the buffer (the library clears its counters)
+        one = [_outputs(q, T, E, H, dev) for q in qs]
+        ops.lstm_seq_fwd(one, T, E, sync)
+        torch.cuda.synchronize()
+        assert int(sync[0]) == 0
+        for a, b in zip(per_step, one):
+            for k in ("h", "c", "gates"):
+                assert torch.equal(a[k], b[k]), (k, rep)
+            assert torch.equal(a["hs"], b["hs"]), ("hs", rep)

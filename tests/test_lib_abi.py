@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "ppo_hip.h"
 
 def _declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|size_t|const char\*)\s+(ppo_\w+)\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|size_t|const char\*)\s+(ppo_\w+)\(", text, flags=re.M)))
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -113,12 +113,20 @@ def test_argument_validation_reports_errors_without_a_gpu():
     # LSTM entry points: argument checks run before any launch
     seq = _lib.LstmSeqProblem(hidden=6)
     with pytest.raises(ValueError, match="hidden=6"):
-        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(seq), 1, 24, 64, None)
+        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(seq), 1, 24, 64, None, 0, None)
     seq = _lib.LstmSeqProblem(hidden=256)
     with pytest.raises(ValueError, match="null pointer"):
-        _lib.call("ppo_lstm_seq_bwd", ctypes.byref(seq), 1, 24, 64, None)
+        _lib.call("ppo_lstm_seq_bwd", ctypes.byref(seq), 1, 24, 64, None, 0, None)
     with pytest.raises(ValueError, match="count"):
-        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(seq), 3, 24, 64, None)
+        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(seq), 3, 24, 64, None, 0, None)
+    # the one-launch sequences' synchronisation buffer: 32 header words + one 32-word line per 64-row group and problem
+    assert lib.ppo_lstm_seq_sync_words(2, 1024) == 32 + 2 * 16 * 32
+    assert lib.ppo_lstm_seq_sync_words(1, 65) == 32 + 2 * 32
+    assert lib.ppo_lstm_seq_sync_words(3, 64) == -1 and lib.ppo_lstm_seq_sync_words(1, 0) == -1
+    full = _lib.LstmSeqProblem(w_hh_g=16, w_hh_gt=16, gx=16, ldgx=1024, h0=16, c0=16, ld0=256, keep=16,
+                               keep_stride=1, h=16, ldh=256, hs=16, c=16, gates=16, hidden=256)
+    with pytest.raises(ValueError, match="sync buffer"):
+        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(full), 1, 24, 1024, 16, 32 + 16 * 32 - 1, None)
     pack = _lib.LstmPackProblem(8, 8, 8, 8, 8, 8, 8, 8, 48, 250)
     with pytest.raises(ValueError, match="sizes"):
         _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)

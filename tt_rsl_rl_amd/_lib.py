@@ -119,8 +119,9 @@ _SIGNATURES = [
     ("ppo_gather_rows", C.c_int, [C.c_void_p, i64, i64, C.POINTER(GatherSegment), i32, f32p, i64, C.c_void_p]),
     ("ppo_linear_fwd", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, C.c_void_p]),
     ("ppo_lstm_pack", C.c_int, [C.POINTER(LstmPackProblem), i32, C.c_void_p]),
-    ("ppo_lstm_seq_fwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p]),
-    ("ppo_lstm_seq_bwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p]),
+    ("ppo_lstm_seq_sync_words", i64, [i32, i64]),
+    ("ppo_lstm_seq_fwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
+    ("ppo_lstm_seq_bwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
     ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),
     ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, C.c_void_p, C.c_size_t,
@@ -150,7 +151,7 @@ _SIGNATURES = [
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib: C.CDLL | None = None
 

@@ -352,18 +352,29 @@ struct LstmPre<EPI_LSTM_BWD, TM, TN, KS> {
 
 // LSTM forward cell for env m, gate columns n .. n+3 = gates i, f, g, o of hidden unit n / 4 (4H and every base are
 // multiples of 4); x = this step's recurrent product, cp = c_{t-1} of the unit already multiplied by keep_prev.
+// The cell arithmetic itself, shared with the whole-sequence kernel so that both give identical results.
+struct LstmCellFwd {
+  f32x4 act;  // i, f, g, o
+  float c, h;
+};
+__device__ __forceinline__ LstmCellFwd lstm_cell_fwd(const f32x4& x, const f32x4& gx, float cp) {
+  LstmCellFwd o;
+  const float ig = sigmoid_hw(x[0] + gx[0]), fg = sigmoid_hw(x[1] + gx[1]);
+  const float gg = tanh_hw(x[2] + gx[2]), og = sigmoid_hw(x[3] + gx[3]);
+  o.c = fg * cp + ig * gg;
+  o.h = og * tanh_hw(o.c);
+  o.act = f32x4{ig, fg, gg, og};
+  return o;
+}
+
 __device__ __forceinline__ void lstm_fwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, const f32x4& gx,
                                                 float cp) {
   const int64_t H = L.hidden, u = n >> 2;
-  const float ig = sigmoid_hw(x[0] + gx[0]), fg = sigmoid_hw(x[1] + gx[1]);
-  const float gg = tanh_hw(x[2] + gx[2]), og = sigmoid_hw(x[3] + gx[3]);
-  const float ct = fg * cp + ig * gg;
-  const float ht = og * tanh_hw(ct);
-  const f32x4 act = {ig, fg, gg, og};
-  *reinterpret_cast<f32x4*>(L.gates + m * 4 * H + n) = act;
-  L.c[m * H + u] = ct;
-  L.h[m * L.ldh + u] = ht;
-  L.hs[m * H + u] = ht * L.keep[m * L.keep_stride];
+  const LstmCellFwd o = lstm_cell_fwd(x, gx, cp);
+  *reinterpret_cast<f32x4*>(L.gates + m * 4 * H + n) = o.act;
+  L.c[m * H + u] = o.c;
+  L.h[m * L.ldh + u] = o.h;
+  L.hs[m * H + u] = o.h * L.keep[m * L.keep_stride];
 }
 
 // LSTM backward cell for env m, hidden units n .. n+3; x = (dgates of the next step) . W_hh for those units.

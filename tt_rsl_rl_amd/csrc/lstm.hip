@@ -8,6 +8,7 @@
 // columns = hidden units) and its epilogue applies the cell derivatives, carrying dL/dc to the previous step.
 // Actor and critic share every launch.  The two weight gradients are plain split-K GEMMs over all T*E rows
 // (ppo_linear_bwd_dw: dgates^T hs and dgates^T x).
+#include <atomic>
 #include <cstring>
 
 #include "gemm_core.hpp"
@@ -131,6 +132,216 @@ __global__ __launch_bounds__(256) void lstm_copy_state_kernel(const CopyGroup g)
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// ---- Whole-sequence forward: one launch for all T steps ----
+//
+// Block (problem p, row-group slot g, column block cb) holds gate columns [64 cb, 64 cb + 64) of w_hh_g (64 x H
+// floats) in LDS for the whole sequence and computes rows [64 rg, 64 rg + 64) of every step, for rg = g, g + slots,
+// ...  Step t of a row group reads hs[t] of its rows, which all ncb column blocks of that row group write at step
+// t - 1.  hs[t + 1] is written and hs[t] read with device-scope (sc1) accesses, which the XCDs' separate L2 caches
+// keep coherent without a whole-cache write-back or invalidate; after its stores have completed (vmcnt 0) a block
+// adds 1 to the row group's counter (its own 128-byte line), and before step t a block polls the counter until it
+// reaches ncb t.  The host sizes the grid to the blocks the device holds at once (occupancy query), so the peers of
+// a row group are resident together.  A wait still gives up after kSeqSpinTicks of the 100 MHz real-time clock: it
+// sets the sticky status word and the abort word, every block then leaves at its next wait, and the caller sees
+// status != 0 (no hang).
+//
+// The MFMA sequence per accumulator (32-deep k slabs, k-groups of 8, element s of the f32x4 fragments) and the cell
+// arithmetic are those of the per-step kernel on 64 x 64 tiles, so both paths give identical results.
+constexpr int kMaxDevices = 64;
+constexpr int kSeqRows = 64, kSeqCols = 64, kSeqBK = 32;
+constexpr int kSeqMaxSlabs = 8;  // H <= 256: the w_hh_g slice is 64 KB of LDS, two blocks per CU
+constexpr int kSyncHeader = 32;  // int32 words ahead of the counters: [0] status (sticky), [1] abort
+constexpr int kSyncStride = 32;  // one counter per 128-byte line: blocks of other row groups poll their own lines
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data (gfx9 family)
+constexpr int kDeviceScope = 16;          // buffer-load cache policy: sc1, coherent at device scope
+constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
+
+struct SeqFwdItem {
+  const float* w;  // w_hh_g [4H, H]
+  const float* gx;
+  const float* c0;
+  const float* keep;
+  float* gates;
+  float* c;
+  float* h;
+  float* hs;
+  int64_t ldgx, ld0, keep_stride, ldh;
+};
+struct SeqFwdArgs {
+  SeqFwdItem it[PPO_MAX_LSTM_PROBLEMS];
+  int32_t* sync;
+  int32_t H, E, T, nrg, ncb, slots;
+};
+
+// Zeroes the abort word and the counters of one sequence call (the status word stays).
+__global__ __launch_bounds__(256) void seq_sync_reset_kernel(int32_t* sync, int32_t words) {
+  for (int i = 1 + threadIdx.x; i < words; i += blockDim.x) sync[i] = 0;
+}
+
+// Waits until *ctr >= target; every thread of the block returns the same verdict (false: the sequence was aborted).
+// `flag` is an LDS word that no wave touches between the previous workgroup barrier and this one.  The data the
+// counter announces is read afterwards with device-scope loads only, so the poll needs no cache invalidate.
+__device__ __forceinline__ bool seq_wait(int32_t* sync, int32_t* ctr, int target, volatile float* flag) {
+  if (threadIdx.x == 0) {
+    float ok = 1.0f;
+    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      const uint64_t t0 = wall_clock64();
+      while (true) {
+        __builtin_amdgcn_s_sleep(1);
+        if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+        if (__hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+          ok = 0.0f;
+          break;
+        }
+        if (wall_clock64() - t0 > kSeqSpinTicks) {
+          __hip_atomic_store(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0.0f;
+          break;
+        }
+      }
+    }
+    *flag = ok;
+  }
+  __syncthreads();
+  return *flag != 0.0f;
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// x[q] belongs to unit 2q + hl of the lane's pair (lanes l and l + 32); returns units 4 hl .. 4 hl + 3 of the pair.
+__device__ __forceinline__ f32x4 trade_halves(const float (&x)[4], int hl) {
+  const float r0 = __shfl_xor(hl ? x[0] : x[2], 32), r1 = __shfl_xor(hl ? x[1] : x[3], 32);
+  return hl ? f32x4{r0, x[2], r1, x[3]} : f32x4{x[0], r0, x[1], r1};
+}
+
+// Counts the block in for the row group once every wave's device-scope stores of the step have completed.
+__device__ __forceinline__ void seq_signal(int32_t* ctr) {
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NS>
+__global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
+  constexpr int BK = kSeqBK, WSLAB = kSeqCols * BK, ASLAB = kSeqRows * BK;
+  __shared__ __align__(16) float wl[NS * WSLAB];
+  __shared__ __align__(16) float al[2 * ASLAB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1, hl = lane >> 5;
+  const int per_p = a.slots * a.ncb;
+  const int p = blockIdx.x / per_p, r = blockIdx.x % per_p, g = r / a.ncb, cb = r % a.ncb;
+  const SeqFwdItem& S = a.it[p];
+  const int64_t H = a.H, E = a.E;
+  const int n0 = cb * kSeqCols;
+  // slice of w_hh_g: slab s, row r, 16-byte chunk cc at wl[s WSLAB + r BK + 4 (cc ^ swz(r))], the per-step layout
+  for (int i = tid; i < kSeqCols * 8 * NS; i += 256) {
+    const int row = i / (8 * NS), c4 = i % (8 * NS), sl = c4 >> 3, cc = c4 & 7;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(S.w + (n0 + row) * H + 4 * c4);
+    *reinterpret_cast<f32x4*>(wl + sl * WSLAB + row * BK + 4 * (cc ^ nt_swz<BK>(row))) = v;
+  }
+  // the lane's cell outputs: env row wm*32 + lane%32 of the tile, gate columns ncol + 8q (q = 0..3) = 4 units
+  const int ncol = n0 + wn * 32 + 4 * hl;
+  int32_t* const ctr0 = a.sync + kSyncHeader + p * a.nrg * kSyncStride;
+  volatile float* const flag = al + ASLAB;  // free between a step's last barrier and the next wait's barrier
+  for (int rg = g; rg < a.nrg; rg += a.slots) {
+    __syncthreads();  // the previous row group's last slab reads are done; the slice is staged (first pass)
+    const int64_t m0 = static_cast<int64_t>(rg) * kSeqRows;
+    const int64_t m = m0 + wm * 32 + (lane & 31);
+    const bool in = m < E;
+    const int64_t mc = in ? m : E - 1;
+    float cp[4];  // c_{t-1} * keep_{t-1} of the lane's units; step 0: c0
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cp[q] = S.c0[mc * S.ld0 + ((ncol + 8 * q) >> 2)];
+    // this thread's two 16-byte chunks of every 64 x 32 slab of hs[t]: rows clamped to E - 1
+    int64_t aoff[2];
+    int lofs[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = tid + 256 * j, row = i >> 3, cc = i & 7;
+      aoff[j] = std::min<int64_t>(m0 + row, E - 1) * H + 4 * cc;
+      lofs[j] = row * BK + 4 * (cc ^ nt_swz<BK>(row));
+    }
+    for (int t = 0; t < a.T; ++t) {
+      const int64_t rowt = static_cast<int64_t>(t) * E + mc;
+      f32x4 gx[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) gx[q] = *reinterpret_cast<const f32x4*>(S.gx + rowt * S.ldgx + ncol + 8 * q);
+      const float keep = S.keep[rowt * S.keep_stride];
+      if (t > 0 && !seq_wait(a.sync, ctr0 + rg * kSyncStride, a.ncb * t, flag)) return;
+      const __amdgpu_buffer_rsrc_t At = __builtin_amdgcn_make_buffer_rsrc(
+          S.hs + static_cast<int64_t>(t) * E * H, 0, static_cast<int>(E * H * 4), kBufferWord3);
+      f32x4 ra[NS][2];
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          ra[sl][j] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(At, static_cast<int>(4 * (aoff[j] + sl * BK)), 0,
+                                                           kDeviceScope));
+      f32x16 acc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) *reinterpret_cast<f32x4*>(al + lofs[j]) = ra[0][j];
+      lds_barrier();
+#pragma unroll
+      for (int sl = 0; sl < NS; ++sl) {
+        const float* As = al + (sl & 1) * ASLAB;
+        const float* Ws = wl + sl * WSLAB;
+        const int rA = wm * 32 + (lane & 31), rB = wn * 32 + (lane & 31);
+#pragma unroll
+        for (int gi = 0; gi < BK / 8; ++gi) {
+          const int c = 2 * gi + hl;
+          const f32x4 fa = *reinterpret_cast<const f32x4*>(As + rA * BK + 4 * (c ^ nt_swz<BK>(rA)));
+          const f32x4 fb = *reinterpret_cast<const f32x4*>(Ws + rB * BK + 4 * (c ^ nt_swz<BK>(rB)));
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[k], fa[k], acc, 0, 0, 0);
+        }
+        if (sl + 1 < NS) {
+          // the other buffer's slab sl - 1 was read by every wave before the previous barrier
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            *reinterpret_cast<f32x4*>(al + ((sl + 1) & 1) * ASLAB + lofs[j]) = ra[sl + 1][j];
+          lds_barrier();
+        }
+      }
+      // the cell for the lane's units 2q + hl (of the wave's 8); lanes l and l + 32 (same row) then trade halves so
+      // that each holds 4 consecutive units (hl = 0: units 0..3, hl = 1: units 4..7) and stores 16 bytes per array
+      f32x4 act[4];
+      float cv[4], hv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 x = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+        const LstmCellFwd o = lstm_cell_fwd(x, gx[q], cp[q]);
+        act[q] = o.act;
+        cv[q] = o.c;
+        hv[q] = o.h;
+        cp[q] = o.c * keep;
+      }
+      const f32x4 c4 = trade_halves(cv, hl), h4 = trade_halves(hv, hl);
+      const f32x4 hs4 = {h4[0] * keep, h4[1] * keep, h4[2] * keep, h4[3] * keep};
+      const int64_t ub = ((n0 + wn * 32) >> 2) + 4 * hl;
+      // hs[t + 1] first (device scope, the other blocks read it), then the count, then the outputs nobody waits for
+      if (in) {
+        const __amdgpu_buffer_rsrc_t Hs = __builtin_amdgcn_make_buffer_rsrc(
+            S.hs + static_cast<int64_t>(t + 1) * E * H, 0, static_cast<int>(E * H * 4), kBufferWord3);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hs4), Hs, static_cast<int>(4 * (mc * H + ub)),
+                                               0, kDeviceScope);
+      }
+      if (t + 1 < a.T) seq_signal(ctr0 + rg * kSyncStride);
+      if (in) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<f32x4*>(S.gates + rowt * 4 * H + ncol + 8 * q) = act[q];
+        *reinterpret_cast<f32x4*>(S.c + rowt * H + ub) = c4;
+        *reinterpret_cast<f32x4*>(S.h + rowt * S.ldh + ub) = h4;
+      }
+    }
+  }
+}
+
+
+
 int64_t grid_for(int64_t total) { return std::max<int64_t>(1, std::min<int64_t>(ceil_div(total, 256), 8192)); }
 
 int check_seq(const ppo_lstm_seq_problem* probs, int32_t count, int64_t steps, int64_t envs, bool bwd,
@@ -183,6 +394,83 @@ int launch_step(Group& g, int count, hipStream_t s, const char* name) {
   return launch_nt_aligned<64, 64, 32, 2, O2, EPI>(g, count, s, name);
 }
 
+int64_t seq_row_groups(int64_t envs) { return ceil_div(envs, static_cast<int64_t>(kSeqRows)); }
+
+// Blocks of kernel k the current device holds at once (0 when unknown), cached per device.
+template <typename K>
+int resident_blocks(K kernel, std::atomic<int>* cache) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    v = std::max(per_cu, 0) * std::max(cus, 0) + 1;  // stored + 1: 0 marks "not queried yet"
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v - 1;
+}
+
+// Launches the whole-sequence forward when the shape allows it and the device holds at least one row-group slot
+// (count * ncb blocks) at once.  Returns PPO_OK, an error, or PPO_EUNSUPPORTED to ask for the per-step launches.
+template <int NS>
+int launch_seq_fwd(SeqFwdArgs& a, int count, hipStream_t s) {
+  static std::atomic<int> cache[kMaxDevices];
+  const int resident = resident_blocks(lstm_seq_fwd_kernel<NS>, cache);
+  const int per_slot = count * a.ncb;
+  const int slots = std::min(a.nrg, resident / per_slot);
+  if (slots < 1) return PPO_EUNSUPPORTED;
+  a.slots = slots;
+  hipLaunchKernelGGL(seq_sync_reset_kernel, dim3(1), dim3(256), 0, s, a.sync,
+                     static_cast<int32_t>(kSyncHeader + count * a.nrg * kSyncStride));
+  if (int rc = check_launch("seq_sync_reset_kernel")) return rc;
+  hipLaunchKernelGGL((lstm_seq_fwd_kernel<NS>), dim3(count * slots * a.ncb), dim3(256), 0, s, a);
+  return check_launch("lstm_seq_fwd_kernel");
+}
+
+int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t envs, int32_t* sync,
+            hipStream_t s) {
+  const int64_t H = probs[0].hidden;
+  if (H % kSeqBK != 0 || H / kSeqBK > kSeqMaxSlabs) return PPO_EUNSUPPORTED;
+  SeqFwdArgs a{};
+  for (int i = 0; i < count; ++i) {
+    const ppo_lstm_seq_problem& q = probs[i];
+    SeqFwdItem& it = a.it[i];
+    it.w = q.w_hh_g; it.gx = q.gx; it.c0 = q.c0; it.keep = q.keep;
+    it.gates = q.gates; it.c = q.c; it.h = q.h; it.hs = q.hs;
+    it.ldgx = q.ldgx; it.ld0 = q.ld0; it.keep_stride = q.keep_stride; it.ldh = q.ldh;
+  }
+  a.sync = sync;
+  a.H = static_cast<int32_t>(H);
+  a.E = static_cast<int32_t>(envs);
+  a.T = static_cast<int32_t>(steps);
+  a.nrg = static_cast<int32_t>(seq_row_groups(envs));
+  a.ncb = static_cast<int32_t>(4 * H / kSeqCols);
+  switch (H / kSeqBK) {
+    case 1: return launch_seq_fwd<1>(a, count, s);
+    case 2: return launch_seq_fwd<2>(a, count, s);
+    case 3: return launch_seq_fwd<3>(a, count, s);
+    case 4: return launch_seq_fwd<4>(a, count, s);
+    case 5: return launch_seq_fwd<5>(a, count, s);
+    case 6: return launch_seq_fwd<6>(a, count, s);
+    case 7: return launch_seq_fwd<7>(a, count, s);
+    default: return launch_seq_fwd<8>(a, count, s);
+  }
+}
+
+int check_sync(int32_t* sync, int64_t sync_words, int count, int64_t envs, const char* who) {
+  if (sync == nullptr) return PPO_OK;
+  const int64_t need = kSyncHeader + count * seq_row_groups(envs) * kSyncStride;
+  PPO_REQUIRE(sync_words >= need, "%s: sync buffer of %lld int32 words, %lld needed", who, (long long)sync_words,
+              (long long)need);
+  PPO_REQUIRE(reinterpret_cast<uintptr_t>(sync) % 4 == 0, "%s: sync must be 4-byte aligned", who);
+  return PPO_OK;
+}
+
 }  // namespace
 }  // namespace ppo
 
@@ -231,9 +519,15 @@ extern "C" int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int3
   return check_launch("lstm_unpack_kernel");
 }
 
+extern "C" int64_t ppo_lstm_seq_sync_words(int32_t count, int64_t envs) {
+  if (count < 1 || count > PPO_MAX_LSTM_PROBLEMS || envs < 1) return -1;
+  return kSyncHeader + count * seq_row_groups(envs) * kSyncStride;
+}
+
 extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
-                                ppo_stream_t stream) {
+                                int32_t* sync, int64_t sync_words, ppo_stream_t stream) {
   if (int rc = check_seq(problems, count, steps, envs, false, "ppo_lstm_seq_fwd")) return rc;
+  if (int rc = check_sync(sync, sync_words, count, envs, "ppo_lstm_seq_fwd")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t E = envs;
   CopyGroup cg{};
@@ -251,6 +545,10 @@ extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t co
   cg.total = total;
   hipLaunchKernelGGL(lstm_copy_state_kernel, dim3(grid_for(total)), dim3(256), 0, s, cg);
   if (int rc = check_launch("lstm_copy_state_kernel")) return rc;
+  if (sync != nullptr && steps > 1) {
+    const int rc = seq_fwd(problems, count, steps, envs, sync, s);
+    if (rc != PPO_EUNSUPPORTED) return rc;
+  }
   for (int64_t t = 0; t < steps; ++t) {
     Group g{};
     for (int i = 0; i < count; ++i) {
@@ -281,8 +579,9 @@ extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t co
 }
 
 extern "C" int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
-                                ppo_stream_t stream) {
+                                int32_t* sync, int64_t sync_words, ppo_stream_t stream) {
   if (int rc = check_seq(problems, count, steps, envs, true, "ppo_lstm_seq_bwd")) return rc;
+  if (int rc = check_sync(sync, sync_words, count, envs, "ppo_lstm_seq_bwd")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t E = envs;
   for (int64_t t = steps - 1; t >= 0; --t) {

@@ -34,4 +34,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* ppo_last_error(void) { return ppo::g_error; }
 
-extern "C" int ppo_abi_version(void) { return 4; }
+extern "C" int ppo_abi_version(void) { return 5; }

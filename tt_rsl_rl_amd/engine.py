@@ -396,6 +396,12 @@ class UpdateEngine:
     def minibatch_rows(self, i: int) -> tuple[int, int]:
         return i * self.B // self.M, (i + 1) * self.B // self.M
 
+    def read_status(self) -> None:
+        """Queue the read-back of device-side error words (none on the feed-forward path)."""
+
+    def check_status(self) -> None:
+        """Raise if a read-back error word is set (after the stream was synchronised)."""
+
     def run(self, perm: torch.Tensor, first_step: int, ready: int | None = None, rest=None) -> int:
         """All epochs x mini-batches.  Returns the number of optimiser steps taken.  With ``rest``, only
         ``perm[:ready]`` is final at the call: those rows are gathered first, and ``rest()`` (which completes
@@ -480,6 +486,13 @@ class RecurrentUpdateEngine(UpdateEngine):
         self.side_dw_ws = ops.Workspace(self.device)
         self.seq_a = LstmBuffers(actor.rnn, self.R_max, self.E_max, self.device)
         self.seq_c = LstmBuffers(critic.rnn, self.R_max, self.E_max, self.device)
+        # synchronisation words of the one-launch sequences (word 0: sticky status, read back with every update);
+        # PPO_HIP_LSTM_SEQ=0 selects one launch per step (same results)
+        self.lstm_sync = None
+        if os.environ.get("PPO_HIP_LSTM_SEQ", "1") != "0":
+            self.lstm_sync = torch.zeros(ops.lstm_seq_sync_words(2, self.E_max), dtype=torch.int32,
+                                         device=self.device)
+            self._status_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         # row order of the table: per env slice, t-major
         order = []
         idx = torch.arange(self.T * self.N).view(self.T, self.N)
@@ -527,12 +540,21 @@ class RecurrentUpdateEngine(UpdateEngine):
         return super().dx_layers(R) + [(0, [(self.buf_a.dz[0][:R], la[0].weight, None, self.seq_a.dh[:R]),
                                             (self.buf_c.dz[0][:R], lc[0].weight, None, self.seq_c.dh[:R])], False)]
 
+    def read_status(self) -> None:
+        if self.lstm_sync is not None:
+            self._status_host.copy_(self.lstm_sync[:1], non_blocking=True)
+
+    def check_status(self) -> None:
+        if self.lstm_sync is not None and int(self._status_host[0]) != 0:
+            raise RuntimeError("LSTM sequence launch: blocks stopped waiting for each other (another whole-sequence "
+                               "launch overlapped on this GPU?); the update's results are invalid")
+
     def _grouped(self, fn, qa: dict, qc: dict, E: int) -> None:
         if qa["hidden"] == qc["hidden"]:
-            fn([qa, qc], self.T, E)
+            fn([qa, qc], self.T, E, self.lstm_sync)
         else:
-            fn([qa], self.T, E)
-            fn([qc], self.T, E)
+            fn([qa], self.T, E, self.lstm_sync)
+            fn([qc], self.T, E, self.lstm_sync)
 
     def minibatch(self, r0: int, r1: int, step: int) -> None:
         alg, lay, tm = self.alg, self.layout, self.timer

@@ -529,17 +529,35 @@ def _seq_problem(q: dict, steps: int, envs: int, bwd: bool) -> "L.LstmSeqProblem
                             _ptr(q.get("dgates")), _ptr(q.get("dc")), H, 0)
 
 
-def lstm_seq_fwd(problems: list[dict], steps: int, envs: int) -> None:
+def lstm_seq_sync_words(count: int, envs: int) -> int:
+    """int32 words of the whole-sequence launches' synchronisation buffer (word 0: sticky status)."""
+    n = L.load().ppo_lstm_seq_sync_words(count, envs)
+    if n < 0:
+        raise ValueError(f"lstm_seq_sync_words: count={count} envs={envs}")
+    return n
+
+
+def _sync_args(sync: torch.Tensor | None, count: int, envs: int) -> tuple[int, int]:
+    if sync is None:
+        return 0, 0
+    if sync.dtype != torch.int32 or not sync.is_contiguous() or sync.device.type != "cuda":
+        raise ValueError("lstm sync buffer must be a contiguous int32 device tensor")
+    return sync.data_ptr(), sync.numel()
+
+
+def lstm_seq_fwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor | None = None) -> None:
     """problems: dicts with packed (LstmPacked), hidden, gx [T*E, 4H], h0 / c0 [E, H], keep [T*E] (stride = row
-    step), h [T*E, H], hs [(T+1)*E, H], c [T*E, H], gates [T*E, 4H]."""
+    step), h [T*E, H], hs [(T+1)*E, H], c [T*E, H], gates [T*E, 4H].  sync: int32 device buffer of
+    lstm_seq_sync_words(len(problems), envs) words (zeroed once by the caller) for the one-launch sequence, or None
+    for one launch per step."""
     arr = L.array(L.LstmSeqProblem, [_seq_problem(q, steps, envs, False) for q in problems])
-    L.call("ppo_lstm_seq_fwd", arr, len(problems), steps, envs, _stream())
+    L.call("ppo_lstm_seq_fwd", arr, len(problems), steps, envs, *_sync_args(sync, len(problems), envs), _stream())
 
 
-def lstm_seq_bwd(problems: list[dict], steps: int, envs: int) -> None:
+def lstm_seq_bwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor | None = None) -> None:
     """As lstm_seq_fwd's problems plus dh [T*E, H], dgates [T*E, 4H], dc [E, H] (scratch)."""
     arr = L.array(L.LstmSeqProblem, [_seq_problem(q, steps, envs, True) for q in problems])
-    L.call("ppo_lstm_seq_bwd", arr, len(problems), steps, envs, _stream())
+    L.call("ppo_lstm_seq_bwd", arr, len(problems), steps, envs, *_sync_args(sync, len(problems), envs), _stream())
 
 
 def lstm_unpack_grads(items: list[tuple]) -> None:

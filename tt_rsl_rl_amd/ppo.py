@@ -319,7 +319,9 @@ class PPO:
         # the one host sync of the update: device state and per-mini-batch trace, two async copies, one wait
         self._state_host.copy_(self.device_state, non_blocking=True)
         engine.trace_host.copy_(engine.trace, non_blocking=True)
+        engine.read_status()
         torch.cuda.current_stream(self.device).synchronize()
+        engine.check_status()
         state = ops.device_state_from_host(self._state_host)
         self.learning_rate = state.learning_rate
         for group in self.optimizer.param_groups:
