@@ -282,6 +282,8 @@ def main() -> int:
         one_update()
     torch.cuda.synchronize()
     phases = full.summary()
+    if "lstm_dw" in phases and "dw" not in phases:
+        flops["lstm_dw"] += flops["dw"]  # the heads' weight-grads share the LSTM weight-grads' launch
     total_ms = {k: n * t for k, (n, t) in phases.items()}
     phase_report = {}
     for k, (n, t) in phases.items():

@@ -36,8 +36,11 @@ def _reference(x, h0, c0, dones, w_ih, w_hh, b_ih, b_hh, dh):
     return out.detach(), [p.grad for p in params]
 
 
-@pytest.mark.parametrize("T,E,D,H", [(7, 64, 48, 256), (5, 200, 13, 8), (24, 1024, 48, 256)])
-def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H):
+@pytest.mark.parametrize("one_launch", [False, True], ids=["per_step", "one_launch"])
+@pytest.mark.parametrize("T,E,D,H", [(7, 64, 48, 256), (5, 200, 13, 8), (24, 1024, 48, 256), (6, 100, 20, 96),
+                                     (4, 1000, 16, 128)])
+def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H, one_launch):
+    """Both the per-step launches and the whole-sequence launches (H = 8 takes the per-step path either way)."""
     from tt_rsl_rl_amd import ops
 
     torch.manual_seed(T * 1000 + H)
@@ -64,9 +67,10 @@ def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H):
              hs=torch.empty(R + E, H, device=dev), c=torch.empty(R, H, device=dev),
              gates=torch.empty(R, 4 * H, device=dev), dh=g(dh.reshape(R, H)),
              dgates=torch.empty(R, 4 * H, device=dev), dc=torch.empty(E, H, device=dev))
-    ops.lstm_seq_fwd([q], T, E)
+    sync = torch.zeros(ops.lstm_seq_sync_words(1, E), dtype=torch.int32, device=dev) if one_launch else None
+    ops.lstm_seq_fwd([q], T, E, sync)
     assert rel_err(q["h"].view(T, E, H), ref_out) < 1e-5
-    ops.lstm_seq_bwd([q], T, E)
+    ops.lstm_seq_bwd([q], T, E, sync)
     dw_ih_g, dw_hh_g = torch.empty(4 * H, D, device=dev), torch.empty(4 * H, H, device=dev)
     db_g, db_g2 = torch.empty(4 * H, device=dev), torch.empty(4 * H, device=dev)
     ops.linear_bwd_dw([(q["dgates"], q["hs"][:R], dw_hh_g, db_g), (q["dgates"], xf, dw_ih_g, db_g2)], R)
@@ -76,6 +80,8 @@ def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H):
     for name, got, want in zip(("w_ih", "w_hh", "b_ih", "b_hh"), grads, ref_grads):
         assert rel_err(got, want) < 1e-5, name
     assert torch.equal(db_g, db_g2)  # the same column sums of dgates, in the same fixed order
+    if sync is not None:
+        assert int(sync[0]) == 0
 
 
 def _random_sequences(dev, T, E, H, count, seed):
@@ -124,3 +130,37 @@ def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count):
             for k in ("h", "c", "gates"):
                 assert torch.equal(a[k], b[k]), (k, rep)
             assert torch.equal(a["hs"], b["hs"]), ("hs", rep)
+
+
+@pytest.mark.parametrize("T,E,H,count", [(24, 1024, 256, 2), (9, 200, 64, 1), (5, 70, 96, 2), (4, 8192, 256, 2),
+                                         (3, 64, 512, 1)])
+def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count):
+    """The whole-sequence backward against one launch per step on the same forward: dgates of every step agree to
+    fp32 rounding (the recurrent product sums its 4H terms in another order), the status word stays clear, and a
+    second call on the same buffer gives the same bits."""
+    from tt_rsl_rl_amd import ops
+
+    dev = cuda
+    qs = _random_sequences(dev, T, E, H, count, seed=T * 31 + E + H)
+    gen = torch.Generator().manual_seed(E + H)
+    qs = [_outputs(q, T, E, H, dev) for q in qs]
+    ops.lstm_seq_fwd(qs, T, E)
+    for q in qs:
+        q["dh"] = (torch.randn(T * E, H, generator=gen) / math.sqrt(H)).to(dev)
+        q["dc"] = torch.empty(E, H, device=dev)
+    per_step = [dict(q, dgates=torch.full((T * E, 4 * H), float("nan"), device=dev)) for q in qs]
+    ops.lstm_seq_bwd(per_step, T, E)
+    sync = torch.zeros(ops.lstm_seq_sync_words(count, E), dtype=torch.int32, device=dev)
+    first = None
+    for rep in range(2):
+        one = [dict(q, dgates=torch.full((T * E, 4 * H), float("nan"), device=dev)) for q in qs]
+        ops.lstm_seq_bwd(one, T, E, sync)
+        torch.cuda.synchronize()
+        assert int(sync[0]) == 0
+        for a, b in zip(per_step, one):
+            assert torch.isfinite(b["dgates"]).all()
+            assert rel_err(b["dgates"], a["dgates"]) < 1e-5, rep
+        if first is None:
+            first = [b["dgates"].clone() for b in one]
+        else:
+            assert all(torch.equal(x, b["dgates"]) for x, b in zip(first, one))

@@ -378,22 +378,31 @@ __device__ __forceinline__ void lstm_fwd_finish(const LstmArgs& L, int64_t m, in
 }
 
 // LSTM backward cell for env m, hidden units n .. n+3; x = (dgates of the next step) . W_hh for those units.
-__device__ __forceinline__ void lstm_bwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, float keep,
-                                                float keep_prev, const f32x4& dhu, const f32x4& ct, const f32x4& cp,
-                                                const f32x4& dcin, const f32x4 (&gt)[4]) {
-  const int64_t H = L.hidden;
-  f32x4 dcout;
+// The cell derivatives for 4 units (the arithmetic shared with the whole-sequence kernel): dpre[e] = the four gate
+// pre-activation gradients of unit e, dcout = dL/dc carried to the previous step.
+__device__ __forceinline__ void lstm_cell_bwd(const f32x4& x, float keep, float keep_prev, const f32x4& dhu,
+                                              const f32x4& ct, const f32x4& cp, const f32x4& dcin,
+                                              const f32x4 (&gt)[4], f32x4 (&dpre)[4], f32x4& dcout) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const float ig = gt[e][0], fg = gt[e][1], gg = gt[e][2], og = gt[e][3];
     const float dh = dhu[e] + keep * x[e];
     const float tc = tanh_hw(ct[e]);
     const float dct = dcin[e] + dh * og * (1.0f - tc * tc);
-    const f32x4 dpre = {dct * gg * ig * (1.0f - ig), dct * (cp[e] * keep_prev) * fg * (1.0f - fg),
-                        dct * ig * (1.0f - gg * gg), dh * tc * og * (1.0f - og)};
-    *reinterpret_cast<f32x4*>(L.dgates + m * 4 * H + 4 * (n + e)) = dpre;
+    dpre[e] = f32x4{dct * gg * ig * (1.0f - ig), dct * (cp[e] * keep_prev) * fg * (1.0f - fg),
+                    dct * ig * (1.0f - gg * gg), dh * tc * og * (1.0f - og)};
     dcout[e] = dct * fg * keep_prev;
   }
+}
+
+__device__ __forceinline__ void lstm_bwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, float keep,
+                                                float keep_prev, const f32x4& dhu, const f32x4& ct, const f32x4& cp,
+                                                const f32x4& dcin, const f32x4 (&gt)[4]) {
+  const int64_t H = L.hidden;
+  f32x4 dpre[4], dcout;
+  lstm_cell_bwd(x, keep, keep_prev, dhu, ct, cp, dcin, gt, dpre, dcout);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) *reinterpret_cast<f32x4*>(L.dgates + m * 4 * H + 4 * (n + e)) = dpre[e];
   if (!L.last) *reinterpret_cast<f32x4*>(L.dc + m * H + n) = dcout;
 }
 

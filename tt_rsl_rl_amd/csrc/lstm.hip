@@ -10,6 +10,7 @@
 // (ppo_linear_bwd_dw: dgates^T hs and dgates^T x).
 #include <atomic>
 #include <cstring>
+#include <type_traits>
 
 #include "gemm_core.hpp"
 
@@ -215,6 +216,45 @@ __device__ __forceinline__ f32x4 trade_halves(const float (&x)[4], int hl) {
   return hl ? f32x4{r0, x[2], r1, x[3]} : f32x4{x[0], r0, x[1], r1};
 }
 
+// This wave's XCD (accelerator complex die): the hardware register XCC_ID.
+__device__ __forceinline__ int xcd_id() {
+  int v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+  return v;
+}
+
+// Row-group line: word 0 the counter, word 1 + j the XCD (+ 1) of the row group's block j, published before the
+// block's first count.  True when all nblk writers run on XCD `mine`.  Every block of the row group reads the same
+// words, so all of them reach the same verdict.  When true, the row group's exchange goes through that XCD's L2:
+// ordinary stores (complete once the L2 has them) and ordinary loads (none of those lines was read earlier in the
+// launch, so no copy older than the stores sits in an L1).  The blocks are numbered so that a row group's blocks land
+// on one XCD under round-robin dispatch; where they do not, the exchange stays device-scope (sc1) stores and loads,
+// which the separate L2s keep coherent.
+__device__ __forceinline__ bool writers_on_xcd(const int32_t* line, int nblk, int mine) {
+  const int lane = threadIdx.x & 63;
+  const int v = lane < nblk ? __hip_atomic_load(line + 1 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                            : mine + 1;
+  return __all(v == mine + 1);
+}
+
+// Block numbering of the sequence kernels: the grid is P = problems x slots row-group slots of nblk blocks each.
+// Blocks are dispatched round-robin over the 8 XCDs (block b to XCD b % 8, checked at run time by writers_on_xcd), so
+// a slot's blocks share an XCD when they are 8 apart: b = x + 8 (j + nblk k) for slot pg = x + 8 k.  Within the XCD,
+// block j of slot k is then followed by block j + 1 of the same slot, so that a CU's second resident block (one XCD
+// pass later) belongs to another row group and the two do not run their MFMA phases in lockstep.  When P is not a
+// multiple of 8: pg = b % P, j = b / P.
+__device__ __forceinline__ void seq_block(int nblk, int& pg, int& j) {
+  const int b = blockIdx.x, P = gridDim.x / nblk;
+  if (P % kXcds == 0) {
+    const int i = b / kXcds;
+    j = i % nblk;
+    pg = b % kXcds + kXcds * (i / nblk);
+  } else {
+    pg = b % P;
+    j = b / P;
+  }
+}
+
 // Counts the block in for the row group once every wave's device-scope stores of the step have completed.
 __device__ __forceinline__ void seq_signal(int32_t* ctr) {
   wait_vmcnt<0>();
@@ -229,8 +269,10 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
   __shared__ __align__(16) float al[2 * ASLAB];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1, hl = lane >> 5;
-  const int per_p = a.slots * a.ncb;
-  const int p = blockIdx.x / per_p, r = blockIdx.x % per_p, g = r / a.ncb, cb = r % a.ncb;
+  int pg, cb;
+  seq_block(a.ncb, pg, cb);
+  const int p = pg / a.slots, g = pg % a.slots;
+  const int xcd = xcd_id();
   const SeqFwdItem& S = a.it[p];
   const int64_t H = a.H, E = a.E;
   const int n0 = cb * kSeqCols;
@@ -246,6 +288,9 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
   volatile float* const flag = al + ASLAB;  // free between a step's last barrier and the next wait's barrier
   for (int rg = g; rg < a.nrg; rg += a.slots) {
     __syncthreads();  // the previous row group's last slab reads are done; the slice is staged (first pass)
+    int32_t* const line = ctr0 + rg * kSyncStride;
+    if (tid == 0) __hip_atomic_store(line + 1 + cb, xcd + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool peers = false;  // every writer of the row group on this XCD (known after the first wait)
     const int64_t m0 = static_cast<int64_t>(rg) * kSeqRows;
     const int64_t m = m0 + wm * 32 + (lane & 31);
     const bool in = m < E;
@@ -268,17 +313,27 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) gx[q] = *reinterpret_cast<const f32x4*>(S.gx + rowt * S.ldgx + ncol + 8 * q);
       const float keep = S.keep[rowt * S.keep_stride];
-      if (t > 0 && !seq_wait(a.sync, ctr0 + rg * kSyncStride, a.ncb * t, flag)) return;
+      if (t > 0) {
+        if (!seq_wait(a.sync, line, a.ncb * t, flag)) return;
+        if (t == 1) peers = writers_on_xcd(line, a.ncb, xcd);
+      }
       const __amdgpu_buffer_rsrc_t At = __builtin_amdgcn_make_buffer_rsrc(
           S.hs + static_cast<int64_t>(t) * E * H, 0, static_cast<int>(E * H * 4), kBufferWord3);
       f32x4 ra[NS][2];
+      auto load_hs = [&](auto policy) {
 #pragma unroll
-      for (int sl = 0; sl < NS; ++sl)
+        for (int sl = 0; sl < NS; ++sl)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          ra[sl][j] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(At, static_cast<int>(4 * (aoff[j] + sl * BK)), 0,
-                                                           kDeviceScope));
+          for (int j = 0; j < 2; ++j)
+            ra[sl][j] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(At, static_cast<int>(4 * (aoff[j] + sl * BK)), 0,
+                                                             decltype(policy)::value));
+      };
+      if (t == 0 || peers) {  // hs[0] was written before the launch
+        load_hs(std::integral_constant<int, 0>{});
+      } else {
+        load_hs(std::integral_constant<int, kDeviceScope>{});
+      }
       f32x16 acc;
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
@@ -322,14 +377,20 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
       const f32x4 c4 = trade_halves(cv, hl), h4 = trade_halves(hv, hl);
       const f32x4 hs4 = {h4[0] * keep, h4[1] * keep, h4[2] * keep, h4[3] * keep};
       const int64_t ub = ((n0 + wn * 32) >> 2) + 4 * hl;
-      // hs[t + 1] first (device scope, the other blocks read it), then the count, then the outputs nobody waits for
+      // hs[t + 1] first (the other blocks read it: through this XCD's L2 when they all run here, else device
+      // scope), then the count, then the outputs nobody waits for
       if (in) {
         const __amdgpu_buffer_rsrc_t Hs = __builtin_amdgcn_make_buffer_rsrc(
             S.hs + static_cast<int64_t>(t + 1) * E * H, 0, static_cast<int>(E * H * 4), kBufferWord3);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hs4), Hs, static_cast<int>(4 * (mc * H + ub)),
-                                               0, kDeviceScope);
+        const u32x4 v = __builtin_bit_cast(u32x4, hs4);
+        const int off = static_cast<int>(4 * (mc * H + ub));
+        if (peers) {
+          __builtin_amdgcn_raw_buffer_store_b128(v, Hs, off, 0, 0);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(v, Hs, off, 0, kDeviceScope);
+        }
       }
-      if (t + 1 < a.T) seq_signal(ctr0 + rg * kSyncStride);
+      if (t + 1 < a.T) seq_signal(line);
       if (in) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) *reinterpret_cast<f32x4*>(S.gates + rowt * 4 * H + ncol + 8 * q) = act[q];
@@ -341,6 +402,167 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
 }
 
 
+
+// ---- Whole-sequence backward: one launch for all T steps ----
+//
+// Block (problem p, row-group slot g, unit block ub) holds rows [32 ub, 32 ub + 32) of w_hh_gt (32 units x 4H, LDS,
+// 16-byte chunks XOR-swizzled by row) for the whole sequence and runs t = T-1 .. 0 for rows [64 rg, 64 rg + 64).
+// Step t's product dgates[t+1] w_hh_g (k = 4H) reads all 4H columns of dgates[t+1] of its rows, which the nub unit
+// blocks of the row group write at step t + 1: the same device-scope exchange and per-row-group counters as the
+// forward.  Wave w takes rows 16 w .. 16 w + 15 of the row group and both 16-unit halves of the block's units on
+// v_mfma_f32_16x16x4f32 with the weights as the first operand, so a lane's accumulator holds 4 consecutive units of
+// one env row: the shape the cell derivatives take.  dgates[t+1] goes from memory straight into registers,
+// kSeqBwdAhead 64-deep k slabs ahead of the MFMAs (no LDS, no barrier inside a step); the carried dL/dc stays in
+// registers from step to step.
+constexpr int kSeqBwdUnits = 32, kSeqBwdKS = 64, kSeqBwdAhead = 4;
+constexpr int kSeqBwdMaxSlabs = 16;  // 4H <= 1024: the w_hh_gt slice is 128 KB of LDS, one block per CU
+
+struct SeqBwdItem {
+  const float* wt;  // w_hh_gt [H, 4H]
+  const float* c0;
+  const float* keep;
+  const float* gates;
+  const float* c;
+  const float* dh;
+  float* dgates;
+  int64_t ld0, keep_stride, lddh;
+};
+struct SeqBwdArgs {
+  SeqBwdItem it[PPO_MAX_LSTM_PROBLEMS];
+  int32_t* sync;
+  int32_t H, E, T, nrg, nub, slots;
+};
+
+template <int NS>
+__global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
+  constexpr int K = kSeqBwdKS * NS, KC = K / 4, U = kSeqBwdUnits, AH = kSeqBwdAhead < NS ? kSeqBwdAhead : NS;
+  __shared__ __align__(16) float wl[U * K];
+  __shared__ float flag_word;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int lr = lane & 15, lq = lane >> 4;
+  int pg, ub;
+  seq_block(a.nub, pg, ub);
+  const int p = pg / a.slots, g = pg % a.slots;
+  const int xcd = xcd_id();
+  const SeqBwdItem& S = a.it[p];
+  const int64_t H = a.H, E = a.E;
+  const int u0 = ub * U;
+  for (int i = tid; i < U * KC; i += 256) {
+    const int row = i / KC, c = i % KC;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(S.wt + (u0 + row) * K + 4 * c);
+    *reinterpret_cast<f32x4*>(wl + row * K + 4 * (c ^ (row & 15))) = v;
+  }
+  __syncthreads();
+  int32_t* const ctr0 = a.sync + kSyncHeader + p * a.nrg * kSyncStride;
+  for (int rg = g; rg < a.nrg; rg += a.slots) {
+    int32_t* const line = ctr0 + rg * kSyncStride;
+    if (tid == 0) __hip_atomic_store(line + 1 + ub, xcd + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool l2 = false;
+    const int64_t m = static_cast<int64_t>(rg) * kSeqRows + 16 * wave + lr;
+    const bool in = m < E;
+    const int64_t mc = in ? m : E - 1;
+    f32x4 dc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};  // dL/dc_t carried from step t + 1
+    for (int t = a.T - 1; t >= 0; --t) {
+      const int64_t rowt = static_cast<int64_t>(t) * E + mc;
+      // the cell's operands (written before the launch): this row, units n .. n + 3 of each half
+      const float keep = S.keep[rowt * S.keep_stride];
+      const float kp = t > 0 ? S.keep[(rowt - E) * S.keep_stride] : 1.0f;
+      f32x4 dhu[2], ct[2], cp[2], gt[2][4];
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti) {
+        const int n = u0 + 16 * ti + 4 * lq;
+        dhu[ti] = *reinterpret_cast<const f32x4*>(S.dh + rowt * S.lddh + n);
+        ct[ti] = *reinterpret_cast<const f32x4*>(S.c + rowt * H + n);
+        cp[ti] = t > 0 ? *reinterpret_cast<const f32x4*>(S.c + (rowt - E) * H + n)
+                       : *reinterpret_cast<const f32x4*>(S.c0 + mc * S.ld0 + n);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gt[ti][e] = *reinterpret_cast<const f32x4*>(S.gates + rowt * 4 * H + 4 * (n + e));
+      }
+      // 4 partial sums per half (k-groups j = 0..3 of every slab): 8 independent MFMA chains per wave, so a
+      // single wave per SIMD keeps the matrix pipe busy
+      f32x4 acc[2][4];
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[ti][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (t + 1 < a.T) {
+        // dgates[t + 1] complete for the row group: every unit block has finished T - 1 - t steps
+        if (!seq_wait(a.sync, line, a.nub * (a.T - 1 - t), &flag_word)) return;
+        if (t + 2 == a.T) l2 = writers_on_xcd(line, a.nub, xcd);
+        const __amdgpu_buffer_rsrc_t Dg = __builtin_amdgcn_make_buffer_rsrc(
+            S.dgates + static_cast<int64_t>(t + 1) * E * K, 0, static_cast<int>(E * K * 4), kBufferWord3);
+        const int abase = static_cast<int>(4 * (mc * K + 4 * lq));
+        // slab sl, k-group j (16 deep): the lane's 4 consecutive k of its row; one copy of the loop per load policy
+        auto product = [&](auto policy) {
+          f32x4 ra[NS][4];
+          auto issue = [&](int sl) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              ra[sl][j] = __builtin_bit_cast(
+                  f32x4, __builtin_amdgcn_raw_buffer_load_b128(Dg, abase + 4 * (kSeqBwdKS * sl + 16 * j), 0,
+                                                               decltype(policy)::value));
+          };
+#pragma unroll
+          for (int sl = 0; sl < AH; ++sl) issue(sl);
+#pragma unroll
+          for (int sl = 0; sl < NS; ++sl) {
+            if (sl + AH < NS) issue(sl + AH);
+            f32x4 fw[4][2];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int c = (kSeqBwdKS * sl + 16 * j) / 4 + lq;
+#pragma unroll
+              for (int ti = 0; ti < 2; ++ti) {
+                const int row = 16 * ti + lr;
+                fw[j][ti] = *reinterpret_cast<const f32x4*>(wl + row * K + 4 * (c ^ (row & 15)));
+              }
+            }
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int ti = 0; ti < 2; ++ti)
+                  acc[ti][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fw[j][ti][s4], ra[sl][j][s4], acc[ti][j], 0, 0, 0);
+          }
+        };
+        if (l2) {
+          product(std::integral_constant<int, 0>{});
+        } else {
+          product(std::integral_constant<int, kDeviceScope>{});
+        }
+      }
+      f32x4 dpre[2][4];
+#pragma unroll
+      for (int ti = 0; ti < 2; ++ti) {
+        const f32x4 x = (acc[ti][0] + acc[ti][1]) + (acc[ti][2] + acc[ti][3]);
+        f32x4 dcout;
+        lstm_cell_bwd(x, keep, kp, dhu[ti], ct[ti], cp[ti], dc[ti], gt[ti], dpre[ti], dcout);
+        dc[ti] = dcout;
+      }
+      // dgates[t]: the next step's operand (through this XCD's L2 when every writer of the row group runs here, else
+      // device scope), then the count
+      if (in) {
+        const __amdgpu_buffer_rsrc_t Dt = __builtin_amdgcn_make_buffer_rsrc(
+            S.dgates + static_cast<int64_t>(t) * E * K, 0, static_cast<int>(E * K * 4), kBufferWord3);
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const u32x4 v = __builtin_bit_cast(u32x4, dpre[ti][e]);
+            const int off = static_cast<int>(4 * (mc * K + 4 * (u0 + 16 * ti + 4 * lq + e)));
+            if (l2) {
+              __builtin_amdgcn_raw_buffer_store_b128(v, Dt, off, 0, 0);
+            } else {
+              __builtin_amdgcn_raw_buffer_store_b128(v, Dt, off, 0, kDeviceScope);
+            }
+          }
+      }
+      if (t > 0) seq_signal(line);
+    }
+    __syncthreads();  // flag_word is reused by the next row group's first wait
+  }
+}
 
 int64_t grid_for(int64_t total) { return std::max<int64_t>(1, std::min<int64_t>(ceil_div(total, 256), 8192)); }
 
@@ -459,6 +681,50 @@ int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
     case 6: return launch_seq_fwd<6>(a, count, s);
     case 7: return launch_seq_fwd<7>(a, count, s);
     default: return launch_seq_fwd<8>(a, count, s);
+  }
+}
+
+template <int NS>
+int launch_seq_bwd(SeqBwdArgs& a, int count, hipStream_t s) {
+  static std::atomic<int> cache[kMaxDevices];
+  const int resident = resident_blocks(lstm_seq_bwd_kernel<NS>, cache);
+  const int per_slot = count * a.nub;
+  const int slots = std::min(a.nrg, resident / per_slot);
+  if (slots < 1) return PPO_EUNSUPPORTED;
+  a.slots = slots;
+  hipLaunchKernelGGL(seq_sync_reset_kernel, dim3(1), dim3(256), 0, s, a.sync,
+                     static_cast<int32_t>(kSyncHeader + count * a.nrg * kSyncStride));
+  if (int rc = check_launch("seq_sync_reset_kernel")) return rc;
+  hipLaunchKernelGGL((lstm_seq_bwd_kernel<NS>), dim3(count * slots * a.nub), dim3(256), 0, s, a);
+  return check_launch("lstm_seq_bwd_kernel");
+}
+
+int seq_bwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t envs, int32_t* sync,
+            hipStream_t s) {
+  const int64_t H = probs[0].hidden;
+  if (H % kSeqBwdUnits != 0 || 4 * H / kSeqBwdKS > kSeqBwdMaxSlabs) return PPO_EUNSUPPORTED;
+  SeqBwdArgs a{};
+  for (int i = 0; i < count; ++i) {
+    const ppo_lstm_seq_problem& q = probs[i];
+    SeqBwdItem& it = a.it[i];
+    it.wt = q.w_hh_gt; it.c0 = q.c0; it.keep = q.keep; it.gates = q.gates; it.c = q.c; it.dh = q.dh;
+    it.dgates = q.dgates; it.ld0 = q.ld0; it.keep_stride = q.keep_stride; it.lddh = q.lddh;
+  }
+  a.sync = sync;
+  a.H = static_cast<int32_t>(H);
+  a.E = static_cast<int32_t>(envs);
+  a.T = static_cast<int32_t>(steps);
+  a.nrg = static_cast<int32_t>(seq_row_groups(envs));
+  a.nub = static_cast<int32_t>(H / kSeqBwdUnits);
+  switch (4 * H / kSeqBwdKS) {
+    case 2: return launch_seq_bwd<2>(a, count, s);
+    case 4: return launch_seq_bwd<4>(a, count, s);
+    case 6: return launch_seq_bwd<6>(a, count, s);
+    case 8: return launch_seq_bwd<8>(a, count, s);
+    case 10: return launch_seq_bwd<10>(a, count, s);
+    case 12: return launch_seq_bwd<12>(a, count, s);
+    case 14: return launch_seq_bwd<14>(a, count, s);
+    default: return launch_seq_bwd<16>(a, count, s);
   }
 }
 
@@ -584,6 +850,10 @@ extern "C" int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t co
   if (int rc = check_sync(sync, sync_words, count, envs, "ppo_lstm_seq_bwd")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t E = envs;
+  if (sync != nullptr && steps > 1) {
+    const int rc = seq_bwd(problems, count, steps, envs, sync, s);
+    if (rc != PPO_EUNSUPPORTED) return rc;
+  }
   for (int64_t t = steps - 1; t >= 0; --t) {
     Group g{};
     for (int i = 0; i < count; ++i) {

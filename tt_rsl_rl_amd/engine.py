@@ -581,12 +581,16 @@ class RecurrentUpdateEngine(UpdateEngine):
         self.head_forward(sa.h[:R], sc.h[:R], R)
         self.loss(tab, R, adv_col)
         self.head_backward(R)
-        # the heads' weight gradients need only their dz and inputs: a side stream computes them while the
-        # latency-bound LSTM backward steps run; Adam waits for both
+        # the heads' weight gradients need only their dz and inputs.  Beside one launch per LSTM step they run on a
+        # side stream (Adam waits for both); the whole-sequence backward keeps every CU's LDS for its whole run, so
+        # there they join the LSTM weight gradients' grouped launch after it
         main = torch.cuda.current_stream()
-        self.side.wait_stream(main)
-        with torch.cuda.stream(self.side):
-            self.weight_grads(self.head_dw(sa.h[:R], sc.h[:R], R), R, ws=self.side_dw_ws)
+        head_dw = self.head_dw(sa.h[:R], sc.h[:R], R)
+        if self.lstm_sync is None:
+            self.side.wait_stream(main)
+            with torch.cuda.stream(self.side):
+                self.weight_grads(head_dw, R, ws=self.side_dw_ws)
+            head_dw = []
         tm.start("lstm_bwd")
         self._grouped(ops.lstm_seq_bwd, qa, qc, E)
         tm.stop("lstm_bwd")
@@ -595,9 +599,10 @@ class RecurrentUpdateEngine(UpdateEngine):
         for s, x in ((sa, xa), (sc, xc)):
             dw.append((s.dgates[:R], s.hs[:R], s.dw_hh_g, s.db_g))
             dw.append((s.dgates[:R], x, s.dw_ih_g, s.db_g2))
-        self.weight_grads(dw, R, "lstm_dw")
+        self.weight_grads(dw + head_dw, R, "lstm_dw")
         grad = alg.flat.grad_view
         ops.lstm_unpack_grads([(s.dw_ih_g, s.dw_hh_g, s.db_g, *(grad(p) for p in m.rnn.weights))
                                for s, m in ((sa, actor), (sc, critic))])
-        main.wait_stream(self.side)
+        if self.lstm_sync is None:
+            main.wait_stream(self.side)
         self.adam(step)
