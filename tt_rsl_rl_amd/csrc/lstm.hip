@@ -495,6 +495,7 @@ __global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
         // slab sl, k-group j (16 deep): the lane's 4 consecutive k of its row; one copy of the loop per load policy
         auto product = [&](auto policy) {
           f32x4 ra[NS][4];
+          f32x4 fw[2][4][2];  // the weight fragments of two slabs: the next slab's are read under this one's MFMAs
           auto issue = [&](int sl) {
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -502,28 +503,36 @@ __global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
                   f32x4, __builtin_amdgcn_raw_buffer_load_b128(Dg, abase + 4 * (kSeqBwdKS * sl + 16 * j), 0,
                                                                decltype(policy)::value));
           };
-#pragma unroll
-          for (int sl = 0; sl < AH; ++sl) issue(sl);
-#pragma unroll
-          for (int sl = 0; sl < NS; ++sl) {
-            if (sl + AH < NS) issue(sl + AH);
-            f32x4 fw[4][2];
+          auto wfrag = [&](int sl) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int c = (kSeqBwdKS * sl + 16 * j) / 4 + lq;
 #pragma unroll
               for (int ti = 0; ti < 2; ++ti) {
                 const int row = 16 * ti + lr;
-                fw[j][ti] = *reinterpret_cast<const f32x4*>(wl + row * K + 4 * (c ^ (row & 15)));
+                fw[sl & 1][j][ti] = *reinterpret_cast<const f32x4*>(wl + row * K + 4 * (c ^ (row & 15)));
               }
             }
+          };
+#pragma unroll
+          for (int sl = 0; sl < AH; ++sl) issue(sl);
+          wfrag(0);
+#pragma unroll
+          for (int sl = 0; sl < NS; ++sl) {
+            // scheduling fences: the compiler would otherwise move each load next to its use (fewer registers,
+            // but one slab's load latency exposed per slab)
+            __builtin_amdgcn_sched_barrier(0);
+            if (sl + AH < NS) issue(sl + AH);
+            if (sl + 1 < NS) wfrag(sl + 1);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
               for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti)
-                  acc[ti][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fw[j][ti][s4], ra[sl][j][s4], acc[ti][j], 0, 0, 0);
+                  acc[ti][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(fw[sl & 1][j][ti][s4], ra[sl][j][s4], acc[ti][j],
+                                                                    0, 0, 0);
           }
         };
         if (l2) {
