@@ -164,3 +164,47 @@ def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count):
             first = [b["dgates"].clone() for b in one]
         else:
             assert all(torch.equal(x, b["dgates"]) for x, b in zip(first, one))
+
+
+def test_sequence_wait_gives_up_and_the_update_raises(cuda, monkeypatch):
+    """A wait limit of 0 ticks, forced from the host, makes the blocks of a one-launch sequence give up waiting for
+    each other: every launch still runs to its end, the sticky status word is set (and stays set through a normal
+    call, which clears only the counters), and a recurrent update that hit it raises instead of returning results."""
+    from oracle import rollout as R
+    from tests.parity import make_hip
+    from tt_rsl_rl_amd import ops
+
+    dev = cuda
+    T, E, H = 24, 1024, 256
+    qs = [_outputs(q, T, E, H, dev) for q in _random_sequences(dev, T, E, H, 2, seed=5)]
+    sync = torch.zeros(ops.lstm_seq_sync_words(2, E), dtype=torch.int32, device=dev)
+    monkeypatch.setenv("PPO_HIP_SEQ_SPIN_TICKS", "0")
+    ops.lstm_seq_fwd(qs, T, E, sync)
+    torch.cuda.synchronize()
+    assert int(sync[0]) == 1
+    monkeypatch.delenv("PPO_HIP_SEQ_SPIN_TICKS")
+    ops.lstm_seq_fwd(qs, T, E, sync)
+    torch.cuda.synchronize()
+    assert int(sync[0]) == 1
+    sync.zero_()
+    ops.lstm_seq_fwd(qs, T, E, sync)
+    torch.cuda.synchronize()
+    assert int(sync[0]) == 0
+
+    w = R.scaled(R.WORKLOADS["lstm256"], num_envs=512, steps=24, hidden_dims=[256, 128])
+    hip = make_hip(w, seed=0)
+    g = torch.Generator().manual_seed(3)
+    st = hip.storage
+    for v in st.observations.values():
+        v.copy_(torch.randn(v.shape, generator=g))
+    st.actions.copy_(torch.randn(st.actions.shape, generator=g))
+    st.rewards.copy_(torch.randn(st.rewards.shape, generator=g) * 0.2)
+    st.values.copy_(torch.randn(st.values.shape, generator=g))
+    mean = torch.randn(st.actions.shape, generator=g)
+    st.distribution_params = (mean.to(hip.device), torch.ones_like(st.actions))
+    st.actions_log_prob.copy_(torch.distributions.Normal(mean, 1.0).log_prob(st.actions.cpu()).sum(-1, keepdim=True))
+    st.step = st.num_transitions_per_env
+    hip.compute_returns_from(torch.randn(w["num_envs"], 1, generator=g).to(hip.device))
+    monkeypatch.setenv("PPO_HIP_SEQ_SPIN_TICKS", "0")
+    with pytest.raises(RuntimeError, match="stopped waiting"):
+        hip.update()

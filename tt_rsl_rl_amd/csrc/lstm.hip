@@ -9,6 +9,7 @@
 // Actor and critic share every launch.  The two weight gradients are plain split-K GEMMs over all T*E rows
 // (ppo_linear_bwd_dw: dgates^T hs and dgates^T x).
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <type_traits>
 
@@ -155,7 +156,7 @@ constexpr int kSyncHeader = 32;  // int32 words ahead of the counters: [0] statu
 constexpr int kSyncStride = 32;  // one counter per 128-byte line: blocks of other row groups poll their own lines
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data (gfx9 family)
 constexpr int kDeviceScope = 16;          // buffer-load cache policy: sc1, coherent at device scope
-constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock
+constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock (PPO_HIP_SEQ_SPIN_TICKS overrides it)
 
 struct SeqFwdItem {
   const float* w;  // w_hh_g [4H, H]
@@ -171,6 +172,7 @@ struct SeqFwdItem {
 struct SeqFwdArgs {
   SeqFwdItem it[PPO_MAX_LSTM_PROBLEMS];
   int32_t* sync;
+  uint64_t spin_ticks;
   int32_t H, E, T, nrg, ncb, slots;
 };
 
@@ -182,7 +184,8 @@ __global__ __launch_bounds__(256) void seq_sync_reset_kernel(int32_t* sync, int3
 // Waits until *ctr >= target; every thread of the block returns the same verdict (false: the sequence was aborted).
 // `flag` is an LDS word that no wave touches between the previous workgroup barrier and this one.  The data the
 // counter announces is read afterwards with device-scope loads only, so the poll needs no cache invalidate.
-__device__ __forceinline__ bool seq_wait(int32_t* sync, int32_t* ctr, int target, volatile float* flag) {
+__device__ __forceinline__ bool seq_wait(int32_t* sync, int32_t* ctr, int target, volatile float* flag,
+                                         uint64_t spin_ticks) {
   if (threadIdx.x == 0) {
     float ok = 1.0f;
     if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
@@ -194,7 +197,7 @@ __device__ __forceinline__ bool seq_wait(int32_t* sync, int32_t* ctr, int target
           ok = 0.0f;
           break;
         }
-        if (wall_clock64() - t0 > kSeqSpinTicks) {
+        if (wall_clock64() - t0 > spin_ticks) {
           __hip_atomic_store(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           ok = 0.0f;
@@ -314,7 +317,7 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
       for (int q = 0; q < 4; ++q) gx[q] = *reinterpret_cast<const f32x4*>(S.gx + rowt * S.ldgx + ncol + 8 * q);
       const float keep = S.keep[rowt * S.keep_stride];
       if (t > 0) {
-        if (!seq_wait(a.sync, line, a.ncb * t, flag)) return;
+        if (!seq_wait(a.sync, line, a.ncb * t, flag, a.spin_ticks)) return;
         if (t == 1) peers = writers_on_xcd(line, a.ncb, xcd);
       }
       const __amdgpu_buffer_rsrc_t At = __builtin_amdgcn_make_buffer_rsrc(
@@ -430,6 +433,7 @@ struct SeqBwdItem {
 struct SeqBwdArgs {
   SeqBwdItem it[PPO_MAX_LSTM_PROBLEMS];
   int32_t* sync;
+  uint64_t spin_ticks;
   int32_t H, E, T, nrg, nub, slots;
 };
 
@@ -487,7 +491,7 @@ __global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
         for (int j = 0; j < 4; ++j) acc[ti][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
       if (t + 1 < a.T) {
         // dgates[t + 1] complete for the row group: every unit block has finished T - 1 - t steps
-        if (!seq_wait(a.sync, line, a.nub * (a.T - 1 - t), &flag_word)) return;
+        if (!seq_wait(a.sync, line, a.nub * (a.T - 1 - t), &flag_word, a.spin_ticks)) return;
         if (t + 2 == a.T) l2 = writers_on_xcd(line, a.nub, xcd);
         const __amdgpu_buffer_rsrc_t Dg = __builtin_amdgcn_make_buffer_rsrc(
             S.dgates + static_cast<int64_t>(t + 1) * E * K, 0, static_cast<int>(E * K * 4), kBufferWord3);
@@ -627,6 +631,13 @@ int launch_step(Group& g, int count, hipStream_t s, const char* name) {
 
 int64_t seq_row_groups(int64_t envs) { return ceil_div(envs, static_cast<int64_t>(kSeqRows)); }
 
+// How long a block of a sequence kernel waits for the others before it gives up (100 MHz ticks).  The variable
+// exists so that tests can force the give-up path from the host; every kernel still runs to its end.
+uint64_t seq_spin_ticks() {
+  const char* e = std::getenv("PPO_HIP_SEQ_SPIN_TICKS");
+  return e != nullptr ? std::strtoull(e, nullptr, 10) : kSeqSpinTicks;
+}
+
 // Blocks of kernel k the current device holds at once (0 when unknown), cached per device.
 template <typename K>
 int resident_blocks(K kernel, std::atomic<int>* cache) {
@@ -676,6 +687,7 @@ int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
     it.ldgx = q.ldgx; it.ld0 = q.ld0; it.keep_stride = q.keep_stride; it.ldh = q.ldh;
   }
   a.sync = sync;
+  a.spin_ticks = seq_spin_ticks();
   a.H = static_cast<int32_t>(H);
   a.E = static_cast<int32_t>(envs);
   a.T = static_cast<int32_t>(steps);
@@ -720,6 +732,7 @@ int seq_bwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
     it.dgates = q.dgates; it.ld0 = q.ld0; it.keep_stride = q.keep_stride; it.lddh = q.lddh;
   }
   a.sync = sync;
+  a.spin_ticks = seq_spin_ticks();
   a.H = static_cast<int32_t>(H);
   a.E = static_cast<int32_t>(envs);
   a.T = static_cast<int32_t>(steps);
