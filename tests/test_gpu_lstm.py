@@ -38,7 +38,7 @@ def _reference(x, h0, c0, dones, w_ih, w_hh, b_ih, b_hh, dh):
 
 @pytest.mark.parametrize("one_launch", [False, True], ids=["per_step", "one_launch"])
 @pytest.mark.parametrize("T,E,D,H", [(7, 64, 48, 256), (5, 200, 13, 8), (24, 1024, 48, 256), (6, 100, 20, 96),
-                                     (4, 1000, 16, 128)])
+                                     (4, 1000, 16, 128), (9, 130, 7, 32)])
 def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H, one_launch):
     """Both the per-step launches and the whole-sequence launches (H = 8 takes the per-step path either way)."""
     from tt_rsl_rl_amd import ops
@@ -109,7 +109,7 @@ def _outputs(q, T, E, H, dev):
 
 
 @pytest.mark.parametrize("T,E,H,count", [(24, 1024, 256, 2), (9, 200, 64, 1), (5, 70, 96, 2), (4, 8192, 256, 2),
-                                         (3, 64, 512, 1), (1, 100, 256, 2)])
+                                         (3, 64, 512, 1), (1, 100, 256, 2), (6, 65, 32, 2)])
 def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count):
     """The whole-sequence forward (row groups of 64 envs synchronised through the sync buffer; 8192 envs need more
     row groups than the device holds at once, so blocks take several in turn; H = 512 and T = 1 take the per-step
@@ -133,7 +133,7 @@ def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count):
 
 
 @pytest.mark.parametrize("T,E,H,count", [(24, 1024, 256, 2), (9, 200, 64, 1), (5, 70, 96, 2), (4, 8192, 256, 2),
-                                         (3, 64, 512, 1)])
+                                         (3, 64, 512, 1), (6, 65, 32, 2)])
 def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count):
     """The whole-sequence backward against one launch per step on the same forward: dgates of every step agree to
     fp32 rounding (the recurrent product sums its 4H terms in another order), the status word stays clear, and a
