@@ -139,10 +139,11 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 // Block (problem p, row-group slot g, column block cb) holds gate columns [64 cb, 64 cb + 64) of w_hh_g (64 x H
 // floats) in LDS for the whole sequence and computes rows [64 rg, 64 rg + 64) of every step, for rg = g, g + slots,
 // ...  Step t of a row group reads hs[t] of its rows, which all ncb column blocks of that row group write at step
-// t - 1.  hs[t + 1] is written and hs[t] read with device-scope (sc1) accesses, which the XCDs' separate L2 caches
-// keep coherent without a whole-cache write-back or invalidate; after its stores have completed (vmcnt 0) a block
-// adds 1 to the row group's counter (its own 128-byte line), and before step t a block polls the counter until it
-// reaches ncb t.  The host sizes the grid to the blocks the device holds at once (occupancy query), so the peers of
+// t - 1.  hs[t + 1] is written and hs[t] read through the L2 of the XCD when all blocks of the row group run on it
+// (the usual case, see writers_on_xcd), else with device-scope (sc1) accesses, which the XCDs' separate L2 caches
+// keep coherent; neither needs a whole-cache write-back or invalidate.  After its stores have completed (vmcnt 0) a
+// block adds 1 to the row group's counter (word 0 of the row group's 128-byte line), and before step t a block polls
+// the counter until it reaches ncb t.  The host sizes the grid to the blocks the device holds at once (occupancy query), so the peers of
 // a row group are resident together.  A wait still gives up after kSeqSpinTicks of the 100 MHz real-time clock: it
 // sets the sticky status word and the abort word, every block then leaves at its next wait, and the caller sees
 // status != 0 (no hang).
@@ -152,8 +153,8 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 constexpr int kMaxDevices = 64;
 constexpr int kSeqRows = 64, kSeqCols = 64, kSeqBK = 32;
 constexpr int kSeqMaxSlabs = 8;  // H <= 256: the w_hh_g slice is 64 KB of LDS, two blocks per CU
-constexpr int kSyncHeader = 32;  // int32 words ahead of the counters: [0] status (sticky), [1] abort
-constexpr int kSyncStride = 32;  // one counter per 128-byte line: blocks of other row groups poll their own lines
+constexpr int kSyncHeader = 32;  // int32 words ahead of the row-group lines: [0] status (sticky), [1] abort
+constexpr int kSyncStride = 32;  // one 128-byte line per row group: [0] counter, [16 + j] XCD of block j
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data (gfx9 family)
 constexpr int kDeviceScope = 16;          // buffer-load cache policy: sc1, coherent at device scope
 constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock (PPO_HIP_SEQ_SPIN_TICKS overrides it)
@@ -183,7 +184,8 @@ __global__ __launch_bounds__(256) void seq_sync_reset_kernel(int32_t* sync, int3
 
 // Waits until *ctr >= target; every thread of the block returns the same verdict (false: the sequence was aborted).
 // `flag` is an LDS word that no wave touches between the previous workgroup barrier and this one.  The data the
-// counter announces is read afterwards with device-scope loads only, so the poll needs no cache invalidate.
+// counter announces is read afterwards either through the L2 that all its writers share or with device-scope loads,
+// so the poll needs no cache invalidate.
 __device__ __forceinline__ bool seq_wait(int32_t* sync, int32_t* ctr, int target, volatile float* flag,
                                          uint64_t spin_ticks) {
   if (threadIdx.x == 0) {
