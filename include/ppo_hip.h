@@ -382,9 +382,10 @@ typedef struct ppo_lstm_seq_problem {
  * words itself at the start of every call.  Calls that share a buffer must not overlap. */
 int64_t ppo_lstm_seq_sync_words(int32_t count, int64_t envs);
 
-/* sync = NULL: one launch per step.  sync != NULL (sync_words >= ppo_lstm_seq_sync_words(count, envs)): the forward
- * runs all steps in one launch when H is a multiple of 32 up to 256 and the device holds one row group's blocks at
- * once (else one launch per step); the results are identical either way.  The backward ignores sync for now. */
+/* sync = NULL: one launch per step.  sync != NULL (sync_words >= ppo_lstm_seq_sync_words(count, envs)): all steps
+ * run in one launch when H is a multiple of 32 up to 256 and the device holds one row group's blocks at once, else
+ * one launch per step.  The forward gives identical results either way; the backward's recurrent product sums in
+ * another order (agreement to fp32 rounding). */
 int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
                      int32_t* sync, int64_t sync_words, ppo_stream_t stream);
 int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
