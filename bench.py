@@ -220,6 +220,70 @@ def cpu_baseline(workload, reps: int) -> dict:
             "ms_per_update": med * 1e3}
 
 
+class FenceFreeTimer:
+    """The engine's phase-timer interface (start / stop / summary / reset) on HIP events created with
+    hipEventDisableSystemFence, recorded on the stream the kernels use.  Such events only time: recording one skips
+    the system-scope cache write-back and invalidate that a default event performs, which otherwise adds a few
+    microseconds of idle GPU before and after every timed launch.  Read only after a device synchronisation."""
+
+    FLAGS = 0x20000000  # hipEventDisableSystemFence (hip_runtime_api.h)
+
+    def __init__(self, only: set[str]) -> None:
+        import ctypes
+
+        import torch
+        from tt_rsl_rl_amd import _lib
+
+        self.ct, self.torch = ctypes, torch
+        self.hip = _lib.load()  # dlsym through libppo_hip.so reaches the HIP runtime it (and torch) already loaded
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.only, self.enabled = only, True
+        self.events: dict[str, list[tuple[int, int]]] = {}
+        self._open: dict[str, int] = {}
+        self._pool: list[int] = []
+
+    def _record(self) -> int:
+        ev = self._pool.pop() if self._pool else None
+        if ev is None:
+            h = self.ct.c_void_p()
+            if self.hip.hipEventCreateWithFlags(self.ct.byref(h), self.FLAGS) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
+            ev = h.value
+        if self.hip.hipEventRecord(ev, self.torch.cuda.current_stream().cuda_stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
+        return ev
+
+    def start(self, name: str) -> None:
+        if self.enabled and name in self.only:
+            self._open[name] = self._record()
+
+    def stop(self, name: str) -> None:
+        if name in self._open:
+            self.events.setdefault(name, []).append((self._open.pop(name), self._record()))
+
+    def reset(self) -> None:
+        for pairs in self.events.values():
+            for a, b in pairs:
+                self._pool += [a, b]
+        self.events.clear()
+        self._open.clear()
+
+    def summary(self) -> dict[str, tuple[int, float]]:
+        out = {}
+        for k, pairs in self.events.items():
+            tot = 0.0
+            for a, b in pairs:
+                ms = self.ct.c_float()
+                if self.hip.hipEventElapsedTime(self.ct.byref(ms), a, b) != 0:
+                    raise RuntimeError("hipEventElapsedTime failed")
+                tot += ms.value
+            out[k] = (len(pairs), tot / len(pairs))
+        return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,7 +362,7 @@ def main() -> int:
     # is collected and frozen first, so a collection of the objects built so far does not land inside it.  The GPU
     # idles through that collection and comes back at a lower clock: one more untimed update restores its working
     # clock (without it the first timed update took 16.2 ms against 13.9 for the rest).
-    timer = PhaseTimer(only={dom})
+    timer = FenceFreeTimer(only={dom})
     timer.enabled = not args.no_phase_events
     engine.timer = timer
     gc.collect()
