@@ -551,21 +551,85 @@ def gae_returns(rewards, values, dones, last_values, gamma: float, lam: float, n
 
 
 def ppo_loss_terms(logp, old_logp, advantages, values, old_values, returns, entropy, clip_param: float,
-                   use_clipped_value_loss: bool, value_loss_coef: float, entropy_coef: float):
-    """ppo.py:268-285: clipped surrogate, (clipped) value loss and the total loss."""
+                   use_clipped_value_loss: bool, value_loss_coef: float, entropy_coef: float, branch=None):
+    """ppo.py:268-285: clipped surrogate, (clipped) value loss and the total loss.
+
+    ``branch`` (not upstream; None gives upstream's arithmetic unchanged) is a BranchRecord.  It takes the rows whose
+    gradient is zero or not from elsewhere (another implementation's decisions), and records which rows then differ
+    from this evaluation's own decision and how far each lies from a clip boundary.  A row that another evaluation
+    computes a few ulps differently may fall on the other side of a boundary of max / clamp, where the gradient
+    jumps between -adv (or 2 (V - R)) and 0; everywhere else the arithmetic is upstream's."""
     ratio = torch.exp(logp - old_logp.squeeze(-1))
-    surrogate = -advantages.squeeze(-1) * ratio
-    surrogate_clipped = -advantages.squeeze(-1) * torch.clamp(ratio, 1.0 - clip_param, 1.0 + clip_param)
-    surrogate_loss = torch.max(surrogate, surrogate_clipped).mean()
+    adv = advantages.squeeze(-1)
+    surrogate = -adv * ratio
+    lo, hi = 1.0 - clip_param, 1.0 + clip_param
+    surrogate_clipped = -adv * torch.clamp(ratio, lo, hi)
+    surrogate_rows = torch.max(surrogate, surrogate_clipped)
+    if branch is not None:
+        with torch.no_grad():
+            inside = (ratio >= lo) & (ratio <= hi)
+            own = (inside | (surrogate > surrogate_clipped)) & (adv != 0)
+            r64 = ratio.double()
+            dist = torch.minimum((r64 - hi).abs(), (r64 - lo).abs())
+        surrogate_rows = branch.apply("surrogate", surrogate_rows, surrogate, own, dist, ratio)
+    surrogate_loss = surrogate_rows.mean()
     if use_clipped_value_loss:
         value_clipped = old_values + (values - old_values).clamp(-clip_param, clip_param)
         value_losses = (values - returns).pow(2)
         value_losses_clipped = (value_clipped - returns).pow(2)
-        value_loss = torch.max(value_losses, value_losses_clipped).mean()
+        value_rows = torch.max(value_losses, value_losses_clipped)
+        if branch is not None:
+            with torch.no_grad():
+                dv = (values - old_values).double()
+                own = ~((value_losses < value_losses_clipped) & ((dv < -clip_param) | (dv > clip_param)))
+                l1, l2 = value_losses.double(), value_losses_clipped.double()
+                # the gradient is zero or not depending on the clamp edge and on which square is larger
+                dist = torch.minimum((dv - clip_param).abs(), (dv + clip_param).abs())
+                gap = (l1 - l2).abs() / torch.maximum(l1, l2).clamp(min=1e-30)
+            value_rows = branch.apply("value", value_rows, value_losses, own, dist, values,
+                                      {"gap": gap, "err": (values - returns).double().abs()})
+        value_loss = value_rows.mean()
     else:
         value_loss = (returns - values).pow(2).mean()
     loss = surrogate_loss + value_loss_coef * value_loss - entropy_coef * entropy.mean()
     return surrogate_loss, value_loss, loss
+
+
+class BranchRecord:
+    """Per mini-batch record of the clip branches (not upstream; see ppo_loss_terms).
+
+    ``forced``: kind ("surrogate" / "value") -> bool tensor of the rows whose gradient must be non-zero, in the
+    mini-batch's row order (None: keep this evaluation's own decisions).  After the loss is built, ``own[kind]``
+    holds this evaluation's decisions, ``q[kind]`` the quantity they depend on (the ratio, the value V; fp64 copies)
+    and ``flips[kind]`` = (rows, distance to the boundary) of the rows where the forced decision differs from the own
+    one: |ratio - (1 +- clip)| for the surrogate, |(V - V_old) -+ clip| for the value loss, whose rows also carry
+    ``extra["value"]``: "gap" = |l1 - l2| / max(l1, l2) of the two squares and "err" = |V - R|."""
+
+    def __init__(self, forced: dict | None = None) -> None:
+        self.forced = forced or {}
+        self.own: dict = {}
+        self.q: dict = {}
+        self.extra: dict = {}
+        self.flips: dict = {}
+
+    def apply(self, kind: str, rows, active, own, dist, q, extra: dict | None = None):
+        """rows: the per-row loss term; active: the term whose gradient a forced non-zero row takes."""
+        self.own[kind] = own.reshape(-1).clone()
+        self.q[kind] = q.detach().reshape(-1).double().clone()
+        if extra is not None:
+            self.extra[kind] = {k: v.reshape(-1).clone() for k, v in extra.items()}
+        forced = self.forced.get(kind)
+        if forced is None:
+            self.flips[kind] = (torch.zeros(0, dtype=torch.int64), torch.zeros(0, dtype=torch.float64))
+            return rows
+        forced = forced.reshape(own.shape).to(torch.bool)
+        off = own & ~forced   # this evaluation's gradient is non-zero, the other's zero
+        on = ~own & forced    # and the reverse
+        idx = torch.nonzero((off | on).reshape(-1)).reshape(-1)
+        self.flips[kind] = (idx, dist.reshape(-1)[idx].clone())
+        if idx.numel() == 0:
+            return rows
+        return torch.where(off, rows.detach(), torch.where(on, active, rows))
 
 
 def adaptive_lr(kl_mean: torch.Tensor, learning_rate: float, desired_kl: float) -> float:
@@ -623,7 +687,11 @@ class PPO:
         # per-mini-batch state hook (not upstream): called as recorder("pre", self) before a mini-batch's forward
         # pass and recorder("post", self) after its optimiser step; tests use it to snapshot the training state
         self.recorder = None
-        # hook to replace the KL (upstream's tests monkeypatch actor.get_kl_divergence the same way)
+        # per-mini-batch clip-branch decisions to take from another evaluation (not upstream): a list with one dict
+        # kind -> bool rows (or None) per optimiser step; see BranchRecord.  The trace then reports the flipped rows.
+        self.forced_branches: list | None = None
+        # stop after this many optimiser steps (not upstream; tests that check only the first steps of a large update)
+        self.max_steps: int | None = None
 
     # -- rollout side ------------------------------------------------------------------------------------------------
     def act(self, obs: Mapping) -> torch.Tensor:
@@ -666,58 +734,71 @@ class PPO:
         mean_surrogate_loss = 0.0
         mean_entropy = 0.0
         self.trace = []
-        if self.actor.is_recurrent or self.critic.is_recurrent:
-            generator = self.storage.recurrent_mini_batch_generator(self.num_mini_batches, self.num_learning_epochs)
-        else:
-            generator = self.storage.mini_batch_generator(self.num_mini_batches, self.num_learning_epochs)
-        for batch in generator:
+        for batch in self.batches():
+            if self.max_steps is not None and len(self.trace) >= self.max_steps:
+                break
             if self.recorder is not None:
                 self.recorder("pre", self)
-            if self.normalize_advantage_per_mini_batch and batch.advantages.numel() > 1:
-                with torch.no_grad():
-                    batch.advantages = (batch.advantages - batch.advantages.mean()) / (batch.advantages.std() + 1e-8)
-            with torch.amp.autocast(device_type="cpu", enabled=self.use_mixed_precision, dtype=torch.bfloat16):
-                self.actor(batch.observations, masks=batch.masks, hidden_state=batch.hidden_states[0],
-                           stochastic_output=True)
-                logp = self.actor.get_output_log_prob(batch.actions)
-                values = self.critic(batch.observations, masks=batch.masks, hidden_state=batch.hidden_states[1])
-                dist_params = self.actor.output_distribution_params
-                entropy = self.actor.output_entropy
-                kl_value = None
-                if self.desired_kl is not None and self.schedule == "adaptive":
-                    with torch.inference_mode():
-                        kl = self.actor.get_kl_divergence(batch.old_distribution_params, dist_params)
-                        kl_mean = torch.mean(kl)
-                        kl_value = float(kl_mean)
-                        self.learning_rate = adaptive_lr(kl_mean, self.learning_rate, self.desired_kl)
-                        for group in self.optimizer.param_groups:
-                            group["lr"] = self.learning_rate
-                surrogate_loss, value_loss, loss = ppo_loss_terms(
-                    logp, batch.old_actions_log_prob, batch.advantages, values, batch.values, batch.returns, entropy,
-                    self.clip_param, self.use_clipped_value_loss, self.value_loss_coef, self.entropy_coef)
-            self.optimizer.zero_grad()
-            loss.backward()
-            nn.utils.clip_grad_norm_(self.actor.parameters(), self.max_grad_norm)
-            nn.utils.clip_grad_norm_(self.critic.parameters(), self.max_grad_norm)
-            self.optimizer.step()
+            k = len(self.trace)
+            forced = self.forced_branches[k] if self.forced_branches is not None else None
+            t = self.minibatch_step(batch, forced)
             if self.recorder is not None:
                 self.recorder("post", self)
-            with torch.no_grad():  # diagnostic: distance of the nearest ratio to a clip boundary (not upstream)
-                ratio = torch.exp(logp.detach() - batch.old_actions_log_prob.squeeze(-1)).double()
-                margin = torch.minimum((ratio - (1.0 + self.clip_param)).abs(),
-                                       (ratio - (1.0 - self.clip_param)).abs()).min().item()
-            v, s, e = value_loss.item(), surrogate_loss.item(), entropy.mean().item()
-            mean_value_loss += v
-            mean_surrogate_loss += s
-            mean_entropy += e
-            self.trace.append({"kl_mean": kl_value, "lr": self.learning_rate, "value": v, "surrogate": s,
-                               "entropy": e, "indices": batch.indices, "clip_margin": margin})
+            mean_value_loss += t["value"]
+            mean_surrogate_loss += t["surrogate"]
+            mean_entropy += t["entropy"]
+            self.trace.append(t)
         obs = {k: v.flatten(0, 1) for k, v in self.storage.observations.items()}
         self.actor.update_normalization(obs)
         self.critic.update_normalization(obs)
         n = self.num_learning_epochs * self.num_mini_batches
         self.storage.clear()
         return {"value": mean_value_loss / n, "surrogate": mean_surrogate_loss / n, "entropy": mean_entropy / n}
+
+    def batches(self):
+        """The mini-batches update() iterates (ppo.py:204-208): one randperm per call for feed-forward models."""
+        if self.actor.is_recurrent or self.critic.is_recurrent:
+            return self.storage.recurrent_mini_batch_generator(self.num_mini_batches, self.num_learning_epochs)
+        return self.storage.mini_batch_generator(self.num_mini_batches, self.num_learning_epochs)
+
+    def minibatch_step(self, batch, forced: dict | None = None) -> dict:
+        """The body of update()'s loop for one mini-batch (ppo.py:210-319): losses, backward, per-model clipping,
+        Adam.  Returns the trace entry of the step.  ``forced``: see ``forced_branches``."""
+        if self.normalize_advantage_per_mini_batch and batch.advantages.numel() > 1:
+            with torch.no_grad():
+                batch.advantages = (batch.advantages - batch.advantages.mean()) / (batch.advantages.std() + 1e-8)
+        branch = BranchRecord(forced)
+        with torch.amp.autocast(device_type="cpu", enabled=self.use_mixed_precision, dtype=torch.bfloat16):
+            self.actor(batch.observations, masks=batch.masks, hidden_state=batch.hidden_states[0],
+                       stochastic_output=True)
+            logp = self.actor.get_output_log_prob(batch.actions)
+            values = self.critic(batch.observations, masks=batch.masks, hidden_state=batch.hidden_states[1])
+            dist_params = self.actor.output_distribution_params
+            entropy = self.actor.output_entropy
+            kl_value = None
+            if self.desired_kl is not None and self.schedule == "adaptive":
+                with torch.inference_mode():
+                    kl = self.actor.get_kl_divergence(batch.old_distribution_params, dist_params)
+                    kl_mean = torch.mean(kl)
+                    kl_value = float(kl_mean)
+                    self.learning_rate = adaptive_lr(kl_mean, self.learning_rate, self.desired_kl)
+                    for group in self.optimizer.param_groups:
+                        group["lr"] = self.learning_rate
+            surrogate_loss, value_loss, loss = ppo_loss_terms(
+                logp, batch.old_actions_log_prob, batch.advantages, values, batch.values, batch.returns, entropy,
+                self.clip_param, self.use_clipped_value_loss, self.value_loss_coef, self.entropy_coef, branch)
+        self.optimizer.zero_grad()
+        loss.backward()
+        nn.utils.clip_grad_norm_(self.actor.parameters(), self.max_grad_norm)
+        nn.utils.clip_grad_norm_(self.critic.parameters(), self.max_grad_norm)
+        self.optimizer.step()
+        with torch.no_grad():  # diagnostic: distance of the nearest ratio to a clip boundary (not upstream)
+            ratio = torch.exp(logp.detach() - batch.old_actions_log_prob.squeeze(-1)).double()
+            margin = torch.minimum((ratio - (1.0 + self.clip_param)).abs(),
+                                   (ratio - (1.0 - self.clip_param)).abs()).min().item()
+        return {"kl_mean": kl_value, "lr": self.learning_rate, "value": value_loss.item(),
+                "surrogate": surrogate_loss.item(), "entropy": entropy.mean().item(), "indices": batch.indices,
+                "clip_margin": margin, "branches": branch}
 
     def train_mode(self) -> None:
         self.actor.train()

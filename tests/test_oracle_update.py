@@ -183,3 +183,133 @@ def test_full_batch_gradient_matches_fp64_objective(clipped):
         t.grad = None
     _objective64(p, batch, ce=-0.01, clipped=clipped).backward()
     assert not torch.allclose(got[0].double(), p["log_std"].grad, rtol=2e-4, atol=1e-7)
+
+
+def test_full_batch_gradient_clipped_per_model():
+    """clip_grad_norm_ per model (ppo.py:309-310) with clipping active: each model's gradient is the fp64 objective's
+    gradient scaled by min(1, max_norm / (||g_model|| + 1e-6)), the actor's norm including its std parameter.  Negative
+    control: one norm over both models (a plausible mistake) gives other gradients."""
+    torch.manual_seed(5)
+    n, T, d, A = 16, 4, 5, 3
+    obs = {"policy": torch.randn(n, d)}
+    groups = {"actor": ["policy"], "critic": ["policy"]}
+    actor = O.MLPModel(obs, groups, "actor", A, hidden_dims=[8, 6],
+                       distribution_cfg={"class_name": "GaussianDistribution", "init_std": 0.8, "std_type": "log"})
+    critic = O.MLPModel(obs, groups, "critic", 1, hidden_dims=[8, 6])
+    max_norm = 0.05
+    ppo = O.PPO(actor, critic, O.RolloutStorage(n, T, obs, [A]), num_learning_epochs=1, num_mini_batches=1,
+                learning_rate=0.0, max_grad_norm=max_norm, schedule="fixed")
+    ppo.train_mode()
+    with torch.no_grad():
+        for _ in range(T):
+            o = {"policy": torch.randn(n, d)}
+            ppo.act(o)
+            ppo.process_env_step(o, torch.randn(n), (torch.rand(n) < 0.2).float(), {})
+    ppo.compute_returns({"policy": torch.randn(n, d)})
+    st = ppo.storage
+    lin = lambda m: [(l.weight.detach().double().clone().requires_grad_(True),
+                      l.bias.detach().double().clone().requires_grad_(True))
+                     for l in m.mlp if isinstance(l, torch.nn.Linear)]
+    p = {"actor": lin(actor), "critic": lin(critic),
+         "log_std": actor.distribution.log_std_param.detach().double().clone().requires_grad_(True)}
+    f = lambda t: t.flatten(0, 1).double()
+    batch = {"obs": f(st.observations["policy"]) * 1.01, "actions": f(st.actions),
+             "old_logp": f(st.actions_log_prob)[:, 0], "adv": f(st.advantages)[:, 0], "old_v": f(st.values)[:, 0],
+             "ret": f(st.returns)[:, 0]}
+    _objective64(p, batch).backward()  # no normaliser here: undo the fresh normaliser's 1/(1 + eps) of _objective64
+    torch.manual_seed(1)
+    ppo.update()
+    ref_a = [p["log_std"].grad] + [t.grad for wb in p["actor"] for t in wb]
+    ref_c = [t.grad for wb in p["critic"] for t in wb]
+    norm = lambda gs: math.sqrt(sum(float((g * g).sum()) for g in gs))
+    coef = lambda gs: min(1.0, max_norm / (norm(gs) + 1e-6))
+    ca, cc = coef(ref_a), coef(ref_c)
+    assert ca < 0.5 and cc < 0.5  # clipping is active for both models
+    got_a = [actor.distribution.log_std_param.grad] + [t.grad for l in actor.mlp if isinstance(l, torch.nn.Linear)
+                                                        for t in (l.weight, l.bias)]
+    got_c = [t.grad for l in critic.mlp if isinstance(l, torch.nn.Linear) for t in (l.weight, l.bias)]
+    for g, r in zip(got_a, ref_a):
+        assert torch.allclose(g.double(), r * ca, rtol=2e-4, atol=1e-9)
+    for g, r in zip(got_c, ref_c):
+        assert torch.allclose(g.double(), r * cc, rtol=2e-4, atol=1e-9)
+    # negative control: a single norm over both models
+    cg = coef(ref_a + ref_c)
+    assert not all(torch.allclose(g.double(), r * cg, rtol=2e-4, atol=1e-9) for g, r in zip(got_a, ref_a))
+
+
+# ----------------------------------------------------------------------------------------------------------------------
+# clip-branch forcing (test infrastructure of the GPU parity tests: not upstream)
+# ----------------------------------------------------------------------------------------------------------------------
+
+
+def _loss_case(n=4000, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    logp = (torch.randn(n, generator=g) * 0.15).requires_grad_(True)
+    old = torch.zeros(n, 1)
+    adv = torch.randn(n, 1, generator=g)
+    adv[:7] = 0.0
+    values = (torch.randn(n, 1, generator=g) * 0.3).requires_grad_(True)
+    old_v = torch.zeros(n, 1)
+    ret = torch.randn(n, 1, generator=g) * 0.3
+    ent = torch.full((n,), 1.3)
+    return logp, old, adv, values, old_v, ret, ent
+
+
+def _loss_grads(branch):
+    logp, old, adv, values, old_v, ret, ent = _loss_case()
+    s, v, loss = O.ppo_loss_terms(logp, old, adv, values, old_v, ret, ent, 0.2, True, 1.0, 0.01, branch)
+    loss.backward()
+    return logp.grad.clone(), values.grad.reshape(-1).clone(), (logp, old, adv, values, old_v, ret)
+
+
+def test_branch_record_own_decisions_are_autograds():
+    """The recorded decisions are exactly the rows where torch's autograd passes a non-zero gradient (max ties split,
+    clamp closed interval), on rows spread over both sides of both boundaries, and forcing them changes nothing."""
+    plain_lp, plain_v, _ = _loss_grads(None)
+    rec = O.BranchRecord()
+    lp, v, _ = _loss_grads(rec)
+    assert torch.equal(lp, plain_lp) and torch.equal(v, plain_v)
+    assert torch.equal(rec.own["surrogate"], plain_lp != 0)
+    assert torch.equal(rec.own["value"], plain_v != 0)
+    s = rec.own["surrogate"]
+    assert 0 < int(s.sum()) < s.numel() and 0 < int(rec.own["value"].sum()) < s.numel()
+    forced = O.BranchRecord({"surrogate": rec.own["surrogate"].clone(), "value": rec.own["value"].clone()})
+    lp2, v2, _ = _loss_grads(forced)
+    assert torch.equal(lp2, plain_lp) and torch.equal(v2, plain_v)
+    assert all(idx.numel() == 0 for idx, _ in forced.flips.values())
+
+
+def test_branch_record_forces_single_rows_and_reports_their_distance():
+    """Forcing one row's surrogate off and another's on, and one value row on: only those rows' gradients change,
+    to 0 and to the unclipped branch's -adv * ratio / R and 2 (V - R) / R; every other row is bit-identical, and the
+    flips are reported with |ratio - (1 +- clip)| and the value rows' distance."""
+    plain_lp, plain_v, (logp, old, adv, values, old_v, ret) = _loss_grads(None)
+    n = plain_lp.numel()
+    ratio = torch.exp(logp.detach() - old.squeeze(-1))
+    on_rows = torch.nonzero(plain_lp != 0).reshape(-1)
+    off_rows = torch.nonzero((plain_lp == 0) & (adv.squeeze(-1) != 0)).reshape(-1)
+    voff = torch.nonzero(plain_v == 0).reshape(-1)
+    i, j, kv = int(on_rows[0]), int(off_rows[0]), int(voff[0])
+    s_mask = plain_lp != 0
+    s_mask[i] = False
+    s_mask[j] = True
+    v_mask = plain_v != 0
+    v_mask[kv] = True
+    rec = O.BranchRecord({"surrogate": s_mask, "value": v_mask})
+    lp, v, _ = _loss_grads(rec)
+    keep = torch.ones(n, dtype=torch.bool)
+    keep[[i, j]] = False
+    assert torch.equal(lp[keep], plain_lp[keep])
+    assert lp[i] == 0
+    expect_j = -adv[j, 0] * ratio[j] / n
+    assert torch.allclose(lp[j], expect_j, rtol=1e-6)
+    keep_v = torch.ones(n, dtype=torch.bool)
+    keep_v[kv] = False
+    assert torch.equal(v[keep_v], plain_v[keep_v])
+    assert torch.allclose(v[kv], 2 * (values[kv, 0] - ret[kv, 0]).detach() / n, rtol=1e-6)
+    idx, dist = rec.flips["surrogate"]
+    assert sorted(idx.tolist()) == sorted([i, j])
+    r64 = ratio.double()
+    for row, d in zip(idx.tolist(), dist.tolist()):
+        assert d == pytest.approx(min(abs(float(r64[row]) - 1.2), abs(float(r64[row]) - 0.8)), rel=1e-12)
+    assert rec.flips["value"][0].tolist() == [kv]

@@ -177,6 +177,9 @@ class UpdateEngine:
         self._warm = False  # records are kept from the second run on: by then no workspace grows any more
         self.replays = 0
         self.replay = os.environ.get("PPO_HIP_LAUNCH_CACHE", "1") != "0" and not self.recurrent
+        # inspection hook (None in normal use): called as step_hook(engine, r0, r1) after each mini-batch's launches
+        # are enqueued, before the next mini-batch's; the buffers then hold that mini-batch's activations / gradients
+        self.step_hook = None
 
     # -- one update ------------------------------------------------------------------------------------------------
     def freeze_normalizers(self) -> None:
@@ -437,6 +440,8 @@ class UpdateEngine:
                         self._issue(("gather", ready, perm.numel() - ready, perm.data_ptr()), gather_rest)
                     step += 1
                     self._issue(("minibatch", r0, r1), lambda: self.minibatch(r0, r1, step), step)
+                    if self.step_hook is not None:
+                        self.step_hook(self, r0, r1)
         finally:
             self._frozen = False
         self._warm = True
