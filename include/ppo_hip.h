@@ -324,6 +324,20 @@ int ppo_adam_step(float* params, float* grads, float* exp_avg, float* exp_avg_sq
                   double bc2_sqrt, ppo_device_state* state, void* workspace, size_t workspace_bytes,
                   ppo_stream_t stream);
 
+/* ppo_adam_step without a workspace argument: it allocates nothing and takes no caller memory besides its inputs and
+ * outputs.  No counterpart in the reference (upstream's torch.optim.Adam allocates as it likes); it is for callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight training / serving loops, harnesses that
+ * forbid hipMalloc.  Same kernels and results as ppo_adam_step, with the per-chunk norm partials in a static device
+ * array of PPO_ADAM_STATIC_SCRATCH_DOUBLES doubles (64 KiB, one copy per GPU, held until the process ends), which
+ * bounds the flat buffers to PPO_ADAM_STATIC_MAX_PARAMS floats: larger counts return PPO_EINVAL before any HIP call.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (concurrent streams or threads) race
+ * and must be serialised by the caller.  Nothing in the array needs clearing between calls. */
+#define PPO_ADAM_STATIC_SCRATCH_DOUBLES 8192
+#define PPO_ADAM_STATIC_MAX_PARAMS ((int64_t)(PPO_ADAM_STATIC_SCRATCH_DOUBLES - PPO_MAX_PARAM_GROUPS) * 1024)
+int ppo_adam_step_static(float* params, float* grads, float* exp_avg, float* exp_avg_sq, const int64_t* group_begin,
+                         int32_t num_groups, double max_grad_norm, double beta1, double beta2, double eps, double bc1,
+                         double bc2_sqrt, ppo_device_state* state, ppo_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------------------------
  * A15  LSTM of the recurrent models (torch nn.LSTM, one layer, gates i, f, g, o): rsl_rl/modules/rnn.py:22-86,
  * rsl_rl/models/rnn_model.py:76-84, the recurrent mini-batches of rsl_rl/storage/rollout_storage.py:262-331 and the

@@ -110,6 +110,12 @@ def test_argument_validation_reports_errors_without_a_gpu():
     assert lib.ppo_loss_workspace_bytes(24576, 29) > 0
     assert lib.ppo_loss_workspace_bytes(24576, 65) == 0
     assert lib.ppo_adam_workspace_bytes(433211) >= 8 * (433211 // 4096)
+    # the allocation-free Adam step checks its size against the static scratch before any HIP call
+    begin = torch.tensor([0, _lib.ADAM_STATIC_MAX_PARAMS + 1], dtype=torch.int64)
+    assert lib.ppo_adam_step_static(16, 16, 16, 16, begin.data_ptr(), 1, 1.0, 0.9, 0.999, 1e-8, 0.1, 0.1, 16,
+                                    None) == _lib.PPO_EINVAL
+    assert "static scratch" in _lib.last_error()
+    assert _lib.ADAM_STATIC_MAX_PARAMS // 1024 + _lib.MAX_PARAM_GROUPS <= _lib.ADAM_STATIC_SCRATCH_DOUBLES
     # LSTM entry points: argument checks run before any launch
     seq = _lib.LstmSeqProblem(hidden=6)
     with pytest.raises(ValueError, match="hidden=6"):

@@ -28,6 +28,8 @@ MAX_GATHER_SEGMENTS = 16
 MAX_LINEAR_PROBLEMS = 8
 MAX_PARAM_GROUPS = 4
 MAX_ACTIONS = 64
+ADAM_STATIC_SCRATCH_DOUBLES = 8192
+ADAM_STATIC_MAX_PARAMS = (ADAM_STATIC_SCRATCH_DOUBLES - MAX_PARAM_GROUPS) * 1024
 
 f32p = C.c_void_p  # device pointers are passed as plain addresses
 i64 = C.c_int64
@@ -148,6 +150,8 @@ _SIGNATURES = [
     ("ppo_adam_step", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double, C.c_double,
                                 C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_size_t,
                                 C.c_void_p]),
+    ("ppo_adam_step_static", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double,
+                                       C.c_double, C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p]),
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]

@@ -6,9 +6,17 @@
 //      derives the clip coefficient and streams p, g, m, v once: 16 B read + 12 B written per parameter
 //      (+4 B rewriting the clipped gradient, which upstream leaves in .grad).
 // The element update follows torch's fp32 operation order with contraction disabled.
+#include <mutex>
+
 #include "common.hpp"
 
 #pragma clang fp contract(off)
+
+// Scratch of ppo_adam_step_static: the per-chunk partial sums of squares in a file-scope device array instead of a
+// caller workspace, so that call allocates nothing.  Every GPU the library runs on holds its own copy until the
+// process ends.  In host code the array's name is not a device address: the address of the current device's copy
+// comes from hipGetSymbolAddress (static_scratch below) and only that address is handed to kernels.
+static __device__ __align__(256) double scratch[PPO_ADAM_STATIC_SCRATCH_DOUBLES];
 
 namespace ppo {
 namespace {
@@ -157,29 +165,44 @@ int build_table(const int64_t* group_begin, int num_groups, GroupTable& t, int& 
   return PPO_OK;
 }
 
-}  // namespace
-}  // namespace ppo
-
-using namespace ppo;
-
-extern "C" size_t ppo_adam_workspace_bytes(int64_t num_params) {
+size_t workspace_bytes_for(int64_t num_params) {
   if (num_params <= 0) return 0;
   return sizeof(double) * static_cast<size_t>(ceil_div(num_params, kChunk) + PPO_MAX_PARAM_GROUPS);
 }
 
-extern "C" int ppo_adam_step(float* params, float* grads, float* exp_avg, float* exp_avg_sq,
-                             const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1,
-                             double beta2, double eps, double bc1, double bc2_sqrt, ppo_device_state* state,
-                             void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
-  PPO_REQUIRE(params && grads && exp_avg && exp_avg_sq && state, "ppo_adam_step: null pointer");
+// The current device's copy of `scratch`, looked up once per device (with that device current) and kept.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+double* g_scratch[kMaxDevices] = {};
+
+int static_scratch(double** out) {
+  int dev = -1;
+  PPO_HIP_CHECK(hipGetDevice(&dev));
+  PPO_REQUIRE(dev >= 0 && dev < kMaxDevices, "ppo_adam_step_static: device %d outside [0, %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    PPO_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    PPO_REQUIRE(p != nullptr, "ppo_adam_step_static: no device address for the scratch array");
+    g_scratch[dev] = static_cast<double*>(p);
+  }
+  *out = g_scratch[dev];
+  return PPO_OK;
+}
+
+int adam_step(const char* who, float* params, float* grads, float* exp_avg, float* exp_avg_sq,
+              const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1, double beta2,
+              double eps, double bc1, double bc2_sqrt, ppo_device_state* state, void* workspace,
+              size_t workspace_bytes, ppo_stream_t stream) {
+  PPO_REQUIRE(params && grads && exp_avg && exp_avg_sq && state, "%s: null pointer", who);
   GroupTable t;
   int chunks = 0;
   int rc = build_table(group_begin, num_groups, t, chunks);
   if (rc != PPO_OK) return rc;
-  const size_t need = ppo_adam_workspace_bytes(group_begin[num_groups]);
-  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_adam_step: workspace too small (%zu < %zu)",
+  const size_t need = workspace_bytes_for(group_begin[num_groups]);
+  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", who,
               workspace_bytes, need);
-  PPO_REQUIRE(bc1 > 0.0 && bc2_sqrt > 0.0, "ppo_adam_step: bias corrections must be positive");
+  PPO_REQUIRE(bc1 > 0.0 && bc2_sqrt > 0.0, "%s: bias corrections must be positive", who);
   AdamScalars s;
   // torch passes max_norm, 1 - beta1, beta2, 1 - beta2 and eps as Python doubles that the fp32 kernels round once
   s.max_norm = static_cast<float>(max_grad_norm);
@@ -210,4 +233,40 @@ extern "C" int ppo_adam_step(float* params, float* grads, float* exp_avg, float*
                        exp_avg_sq, t, s, partials, state);
   }
   return check_launch("adam_kernel");
+}
+
+}  // namespace
+}  // namespace ppo
+
+using namespace ppo;
+
+extern "C" size_t ppo_adam_workspace_bytes(int64_t num_params) { return workspace_bytes_for(num_params); }
+
+extern "C" int ppo_adam_step(float* params, float* grads, float* exp_avg, float* exp_avg_sq,
+                             const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1,
+                             double beta2, double eps, double bc1, double bc2_sqrt, ppo_device_state* state,
+                             void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
+  return adam_step("ppo_adam_step", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups, max_grad_norm,
+                   beta1, beta2, eps, bc1, bc2_sqrt, state, workspace, workspace_bytes, stream);
+}
+
+// The same kernels on the static scratch: the parameter count is checked against the array's capacity before any
+// HIP call; every partial is written before it is read within the call, so nothing needs clearing between calls.
+extern "C" int ppo_adam_step_static(float* params, float* grads, float* exp_avg, float* exp_avg_sq,
+                                    const int64_t* group_begin, int32_t num_groups, double max_grad_norm,
+                                    double beta1, double beta2, double eps, double bc1, double bc2_sqrt,
+                                    ppo_device_state* state, ppo_stream_t stream) {
+  PPO_REQUIRE(group_begin != nullptr && num_groups >= 1 && num_groups <= PPO_MAX_PARAM_GROUPS,
+              "ppo_adam_step_static: num_groups=%d outside [1, %d]", num_groups, PPO_MAX_PARAM_GROUPS);
+  const int64_t n = group_begin[num_groups];
+  PPO_REQUIRE(n > 0 && n <= PPO_ADAM_STATIC_MAX_PARAMS,
+              "ppo_adam_step_static: %lld parameters; the static scratch holds the partials of at most %lld "
+              "(use ppo_adam_step with a workspace)", (long long)n, (long long)PPO_ADAM_STATIC_MAX_PARAMS);
+  static_assert(PPO_ADAM_STATIC_MAX_PARAMS / kChunk + PPO_MAX_PARAM_GROUPS <= PPO_ADAM_STATIC_SCRATCH_DOUBLES,
+                "the static scratch must hold the partials of the largest accepted parameter count");
+  double* ws = nullptr;
+  if (int rc = static_scratch(&ws)) return rc;
+  return adam_step("ppo_adam_step_static", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups,
+                   max_grad_norm, beta1, beta2, eps, bc1, bc2_sqrt, state, ws,
+                   sizeof(double) * PPO_ADAM_STATIC_SCRATCH_DOUBLES, stream);
 }
