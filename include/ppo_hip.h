@@ -67,18 +67,23 @@ int ppo_adv_normalize(const float* x, int64_t in_stride, float* out, int64_t out
  * the contiguous row range [i*B/M, (i+1)*B/M) of the table.
  *   dst[j*dst_stride + seg.dst_col + c] = f(seg.src[perm[j]*seg.src_stride + c]),  c < seg.width,
  * with f the identity, or the observation normaliser (x - mean[c]) / (std[c] + eps)
- * (rsl_rl/modules/normalization.py:46-48) when seg.norm_mean != NULL.  Data moves bit-exactly.
+ * (rsl_rl/modules/normalization.py:46-48) when seg.norm_mean != NULL.  Data moves bit-exactly.  A segment of kind
+ * PPO_GATHER_KEEP_U8 reads uint8 done flags d instead and writes 1 - d as fp32 (the recurrent update's per-step
+ * state-keep factor, rsl_rl/modules/rnn.py:56-60 resets the state where a done was stored).  Every element is read
+ * as the aligned 32-bit word that holds it, so fp32 sources must be 4-byte aligned and the word around each flag
+ * must lie in the flags' allocation (true of any device allocation, whose size is rounded up to 256 bytes or more).
  * perm: int64 [rows], every entry in [0, src_rows).
  * ------------------------------------------------------------------------------------------------------------------ */
+enum { PPO_GATHER_FLOAT = 0, PPO_GATHER_KEEP_U8 = 1 };
 typedef struct ppo_gather_segment {
-  const float* src;       /* [src_rows, src_stride] */
-  int64_t src_stride;     /* floats */
-  int32_t width;          /* floats copied per row */
+  const void* src;        /* [src_rows, src_stride] fp32 (PPO_GATHER_FLOAT) or uint8 (PPO_GATHER_KEEP_U8) */
+  int64_t src_stride;     /* elements */
+  int32_t width;          /* elements copied per row */
   int32_t dst_col;        /* first destination column */
-  const float* norm_mean; /* [width] or NULL */
+  const float* norm_mean; /* [width] or NULL (PPO_GATHER_FLOAT only) */
   const float* norm_std;  /* [width] (required with norm_mean) */
   float norm_eps;
-  int32_t reserved;
+  int32_t kind;           /* PPO_GATHER_FLOAT or PPO_GATHER_KEEP_U8 */
 } ppo_gather_segment;
 
 #define PPO_MAX_GATHER_SEGMENTS 16
@@ -147,7 +152,7 @@ typedef struct ppo_linear_bwd_dw_problem {
   const float* dz; int64_t lddz; /* [rows, out] */
   const float* x; int64_t ldx;   /* [rows, in] */
   float* dw;                     /* [out, in] */
-  float* db;                     /* [out] */
+  float* db;                     /* [out], or NULL: no bias gradient (the column sums are skipped) */
   int32_t in_features;
   int32_t out_features;
 } ppo_linear_bwd_dw_problem;
@@ -246,11 +251,12 @@ typedef struct ppo_device_state {
  * fp32 losses, applies the adaptive-KL learning-rate rule of ppo.py:240-266 when adaptive != 0
  * (kl > 2 desired -> lr = max(1e-5, lr/1.5); 0 < kl < desired/2 -> lr = min(1e-2, lr*1.5); fp32 comparisons),
  * accumulates the loss sums, and writes the std-parameter gradient d_std_param [A] (entropy term and clamp mask
- * included).  trace, if not NULL, receives {kl_mean, lr, surrogate, value, entropy} (fp64) at
- * trace[5*state->num_minibatches]. */
+ * included).  trace, if not NULL, is a buffer of trace_rows rows of 5 doubles: row state->num_minibatches receives
+ * {kl_mean, lr, surrogate, value, entropy} while that index is below trace_rows (later mini-batches are not
+ * traced). */
 int ppo_loss_finalize(const ppo_loss_args* args, const void* workspace, size_t workspace_bytes, float* d_std_param,
                       ppo_device_state* state, int32_t adaptive, double desired_kl, double* trace,
-                      ppo_stream_t stream);
+                      int32_t trace_rows, ppo_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------------
  * The output layers fused with the loss: one call does what the actor's and critic's output-layer forward
@@ -258,7 +264,7 @@ int ppo_loss_finalize(const ppo_loss_args* args, const void* workspace, size_t w
  * ppo_loss_finalize and the output layers' input-grad with ELU' of the layer below (the first step of
  * loss.backward() past the loss, ppo.py:297) do, for the update's MLP heads.  It reads args' batch columns and
  * writes d_mean / d_value (for the output layers' weight-grad) exactly like ppo_gauss_ppo_loss, and the loss state,
- * learning rate, trace and d_std_param exactly like ppo_loss_finalize; args->mean / args->value are not read (the
+ * learning rate, trace (trace_rows as there) and d_std_param exactly like ppo_loss_finalize; args->mean / args->value are not read (the
  * head computes them and stores them to head->mean / head->value when those are not NULL).  The hidden layers'
  * gradients dz_actor / dz_critic are dloss/dz of the last hidden layers, ELU' taken from their outputs
  * (h > 0 ? 1 : h + 1).  Supported when ppo_gauss_ppo_head_supported() (num_actions <= 32, k_actor and k_critic
@@ -292,7 +298,7 @@ int ppo_gauss_ppo_head_supported(int32_t num_actions, int32_t k_actor, int32_t k
 size_t ppo_head_workspace_bytes(int64_t rows, int32_t num_actions);
 int ppo_gauss_ppo_head(const ppo_loss_args* args, const ppo_policy_head* head, void* workspace,
                        size_t workspace_bytes, float* d_std_param, ppo_device_state* state, int32_t adaptive,
-                       double desired_kl, double* trace, ppo_stream_t stream);
+                       double desired_kl, double* trace, int32_t trace_rows, ppo_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------------
  * Rollout-side Gaussian head for act() (rsl_rl/algorithms/ppo.py:124-135; rsl_rl/modules/distribution.py:183-232):

@@ -79,8 +79,10 @@ def test_gather_rows_bit_exact(cuda):
     perm = torch.randperm(B)
     W = 140
     dst = torch.full((B, W), float("nan"), device=cuda)
+    dones = (torch.rand(B, 1) < 0.3).to(torch.uint8)
     segs = [ops.Segment(obs.to(cuda), 0, mean.view(-1).to(cuda), std.view(-1).to(cuda), 1e-2),
-            ops.Segment(act.to(cuda), 100), ops.Segment(logp.to(cuda), 132)]
+            ops.Segment(act.to(cuda), 100), ops.Segment(logp.to(cuda), 132),
+            ops.Segment(dones.to(cuda), 134, keep=True)]
     ops.gather_rows(perm.to(cuda), segs, dst)
     out = dst.cpu()
     norm = O.EmpiricalNormalization(99)
@@ -89,7 +91,9 @@ def test_gather_rows_bit_exact(cuda):
     assert torch.equal(out[:, :99], norm(obs[perm])), "normalised gather must be bit-exact"
     assert torch.equal(out[:, 100:129], act[perm])
     assert torch.equal(out[:, 132:133], logp[perm])
+    assert torch.equal(out[:, 134:135], 1.0 - dones[perm].float()), "keep = 1 - done from the uint8 flags"
     assert torch.isnan(out[:, 99]).all() and torch.isnan(out[:, 129:132]).all(), "gather wrote outside its columns"
+    assert torch.isnan(out[:, 133]).all() and torch.isnan(out[:, 135:]).all(), "gather wrote outside its columns"
 
 
 # ----------------------------------------------------------------------------------------------------------------------
@@ -101,20 +105,31 @@ def _elu64(z):
     return torch.where(z > 0, z, torch.expm1(z))
 
 
-@pytest.mark.parametrize("rows", [1, 77, 1000, 24576])
-def test_linear_fwd_grouped(cuda, rows):
+@pytest.mark.parametrize("rows,aligned_x", [(1, False), (77, False), (1000, False), (24576, False), (1000, True),
+                                            (24576, True)])
+def test_linear_fwd_grouped(cuda, rows, aligned_x):
+    """Strided inputs (ld = in + 5, offset 2: 4-byte loads), or 16-byte aligned inputs with one weight of 96 and one of
+    99 input columns in the same launch (16-byte weight loads for the first problem only, as the update's first
+    layer with a 99-wide critic input issues them)."""
     ops = _ops()
     torch.manual_seed(rows)
     shapes = [(96, 512), (99, 512)] if rows != 77 else [(99, 29), (48, 1)]
     probs, refs = [], []
     for i, (fin, fout) in enumerate(shapes):
-        x = torch.randn(rows, fin + 5)[:, 2:2 + fin]  # strided view (ld = fin + 5)
+        x = torch.randn(rows, fin)
         w = torch.randn(fout, fin) / math.sqrt(fin)
         b = torch.randn(fout)
-        xd = torch.randn(rows, fin + 5, device=cuda)
-        xd.copy_(torch.cat([torch.zeros(rows, 2), x, torch.zeros(rows, 3)], 1))
+        if aligned_x:
+            ld = (fin + 3) // 4 * 4 + 4
+            xd = torch.zeros(rows, ld, device=cuda)
+            xd[:, :fin].copy_(x)
+            xv = xd[:, :fin]
+        else:
+            xd = torch.zeros(rows, fin + 5, device=cuda)
+            xd[:, 2:2 + fin].copy_(x)
+            xv = xd[:, 2:2 + fin]
         z, h = torch.empty(rows, fout, device=cuda), torch.empty(rows, fout, device=cuda)
-        probs.append((xd[:, 2:2 + fin], w.to(cuda), b.to(cuda), z, h))
+        probs.append((xv, w.to(cuda), b.to(cuda), z, h))
         z64 = x.double() @ w.double().t() + b.double()
         refs.append((z, h, z64))
     ops.linear_fwd(probs, rows, elu=True)
@@ -170,11 +185,16 @@ def test_linear_bwd_dw_grouped(cuda, rows):
         db = torch.full((fout,), float("nan"), device=cuda)
         probs.append((dz.to(cuda), x.to(cuda), dw, db))
         refs.append((dw, db, dz.double().t() @ x.double(), dz.double().sum(0), dz.double().abs().sum(0)))
+    # the last problem without a bias gradient (db = NULL: its column sums are skipped)
+    nb = probs[-1][3]
+    probs[-1] = probs[-1][:3] + (None,)
     ops.linear_bwd_dw(probs, rows)
-    for dw, db, rw, rb, rb_abs in refs:
+    assert torch.isnan(nb).all()
+    for dw, db, rw, rb, rb_abs in refs[:-1]:
         assert rel_err(dw, rw) < 2e-6
         # a bias gradient is a sum that can cancel: bound the error by the sum of |terms| (dot-product bound)
         assert ((db.cpu().double() - rb).abs() / rb_abs).max().item() < 1e-6
+    assert rel_err(refs[-1][0], refs[-1][2]) < 2e-6
 
 
 # ----------------------------------------------------------------------------------------------------------------------

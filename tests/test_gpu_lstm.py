@@ -169,7 +169,8 @@ def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count):
 def test_sequence_wait_gives_up_and_the_update_raises(cuda, monkeypatch):
     """A wait limit of 0 ticks, forced from the host, makes the blocks of a one-launch sequence give up waiting for
     each other: every launch still runs to its end, the sticky status word is set (and stays set through a normal
-    call, which clears only the counters), and a recurrent update that hit it raises instead of returning results."""
+    call, which clears only the counters), and a recurrent update that hit it raises instead of returning results,
+    rolled back to the state before it, after which the next update runs normally."""
     from oracle import rollout as R
     from tests.parity import make_hip
     from tt_rsl_rl_amd import ops
@@ -205,6 +206,19 @@ def test_sequence_wait_gives_up_and_the_update_raises(cuda, monkeypatch):
     st.actions_log_prob.copy_(torch.distributions.Normal(mean, 1.0).log_prob(st.actions.cpu()).sum(-1, keepdim=True))
     st.step = st.num_transitions_per_env
     hip.compute_returns_from(torch.randn(w["num_envs"], 1, generator=g).to(hip.device))
+    before = [t.clone() for t in (hip.flat.param, hip.flat.exp_avg, hip.flat.exp_avg_sq)]
+    lr, steps = hip.learning_rate, hip._opt_steps
     monkeypatch.setenv("PPO_HIP_SEQ_SPIN_TICKS", "0")
     with pytest.raises(RuntimeError, match="stopped waiting"):
         hip.update()
+    # the failed update is rolled back: parameters, moments, learning rate and step count as before, status cleared
+    for a, b in zip(before, (hip.flat.param, hip.flat.exp_avg, hip.flat.exp_avg_sq)):
+        assert torch.equal(a, b)
+    assert hip.learning_rate == lr and hip._opt_steps == steps
+    assert int(hip._engine.lstm_sync[0]) == 0
+    # and the algorithm stays usable: the same update with the normal wait limit completes
+    monkeypatch.delenv("PPO_HIP_SEQ_SPIN_TICKS")
+    out = hip.update()
+    assert all(torch.isfinite(torch.tensor(v)) for v in out.values())
+    assert hip._opt_steps == steps + hip.num_learning_epochs * hip.num_mini_batches
+    assert not torch.equal(before[0], hip.flat.param)

@@ -446,3 +446,26 @@ def test_full_size_update_properties(name):
         results.append(p1.cpu())
         del hip
     assert torch.equal(results[0], results[1]), "the update must be deterministic"
+
+
+def test_more_epochs_between_updates_grow_the_trace():
+    """num_learning_epochs raised between two updates: the per-mini-batch trace grows with it (the finalize kernels
+    write no row past the buffer they are given), and the second update still follows the oracle's: same
+    learning-rate decisions and losses."""
+    w = R.scaled(R.WORKLOADS["humanoid"], num_envs=128, steps=8, hidden_dims=[64, 32])
+    from tests.parity import make_pair
+
+    ora, hip, _ = make_pair(w, seed=0, num_learning_epochs=1)
+    for epochs, seed in ((1, 1), (6, 2)):
+        outs = []
+        for alg in (ora, hip):
+            alg.num_learning_epochs = epochs
+            alg.storage.step = alg.storage.num_transitions_per_env
+            torch.manual_seed(seed)
+            outs.append(alg.update())
+        torch.cuda.synchronize()
+        assert len(hip.last_trace) == len(ora.trace) == epochs * ora.num_mini_batches
+        assert [t["lr"] for t in hip.last_trace] == [t["lr"] for t in ora.trace]
+        for k in ("value", "surrogate", "entropy"):
+            assert abs(outs[1][k] - outs[0][k]) <= 1e-4 * max(abs(outs[0][k]), 0.1), (epochs, k)
+    assert hip._engine.trace.numel() >= 5 * 6 * hip.num_mini_batches

@@ -38,7 +38,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 STRUCTS = {
     "ppo_gather_segment": ("GatherSegment", ["src", "src_stride", "width", "dst_col", "norm_mean", "norm_std",
-                                             "norm_eps"]),
+                                             "norm_eps", "kind"]),
     "ppo_linear_fwd_problem": ("LinearFwdProblem", ["x", "ldx", "w", "b", "z", "ldz", "h", "ldh", "in_features",
                                                     "out_features"]),
     "ppo_linear_bwd_dx_problem": ("LinearBwdDxProblem", ["dz", "lddz", "w", "z_prev", "ldz_prev", "dz_prev",
@@ -148,11 +148,11 @@ def test_argument_validation_reports_errors_without_a_gpu():
     head = _lib.PolicyHead(k_actor=128, k_critic=128)
     with pytest.raises(ValueError, match="not supported"):
         _lib.call("ppo_gauss_ppo_head", ctypes.byref(args), ctypes.byref(head), None, 0, None, None, 0, 0.0, None,
-                  None)
+                  0, None)
     args = _lib.LossArgs(rows=10, num_actions=12)
     with pytest.raises(ValueError, match="null pointer"):
         _lib.call("ppo_gauss_ppo_head", ctypes.byref(args), ctypes.byref(head), None, 0, None, None, 0, 0.0, None,
-                  None)
+                  0, None)
 
 
 @pytest.mark.parametrize("seed, n, pre", [(0, 1, 0), (1, 2, 0), (3, 5, 0), (5, 624, 0), (5, 625, 3), (11, 1249, 700),

@@ -36,9 +36,13 @@ i64 = C.c_int64
 i32 = C.c_int32
 
 
+PPO_GATHER_FLOAT = 0
+PPO_GATHER_KEEP_U8 = 1
+
+
 class GatherSegment(C.Structure):
     _fields_ = [("src", C.c_void_p), ("src_stride", i64), ("width", i32), ("dst_col", i32),
-                ("norm_mean", C.c_void_p), ("norm_std", C.c_void_p), ("norm_eps", C.c_float), ("reserved", i32)]
+                ("norm_mean", C.c_void_p), ("norm_std", C.c_void_p), ("norm_eps", C.c_float), ("kind", i32)]
 
 
 class LinearFwdProblem(C.Structure):
@@ -137,11 +141,11 @@ _SIGNATURES = [
     ("ppo_loss_workspace_bytes", C.c_size_t, [i64, i32]),
     ("ppo_gauss_ppo_loss", C.c_int, [C.POINTER(LossArgs), C.c_void_p, C.c_size_t, C.c_void_p]),
     ("ppo_loss_finalize", C.c_int, [C.POINTER(LossArgs), C.c_void_p, C.c_size_t, f32p, C.c_void_p, i32, C.c_double,
-                                    C.c_void_p, C.c_void_p]),
+                                    C.c_void_p, i32, C.c_void_p]),
     ("ppo_gauss_ppo_head_supported", C.c_int, [i32, i32, i32]),
     ("ppo_head_workspace_bytes", C.c_size_t, [i64, i32]),
     ("ppo_gauss_ppo_head", C.c_int, [C.POINTER(LossArgs), C.POINTER(PolicyHead), C.c_void_p, C.c_size_t, f32p,
-                                     C.c_void_p, i32, C.c_double, C.c_void_p, C.c_void_p]),
+                                     C.c_void_p, i32, C.c_double, C.c_void_p, i32, C.c_void_p]),
     ("ppo_gauss_sample", C.c_int, [f32p, i64, f32p, i32, C.c_double, C.c_double, f32p, i64, f32p, i64, f32p, f32p,
                                    i64, i64, i32, C.c_void_p]),
     ("ppo_host_randperm", C.c_int, [C.c_void_p, C.c_size_t, i64, C.c_void_p]),
@@ -155,7 +159,7 @@ _SIGNATURES = [
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib: C.CDLL | None = None
 

@@ -31,6 +31,10 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
 ]
+# PPO_HIP_TUNING=1 at build time compiles the tile / split / wave variants and their environment overrides used for
+# tuning sweeps; the default library holds only the configurations the tests cover.
+if os.environ.get("PPO_HIP_TUNING") == "1":
+    HIPCC_FLAGS.append("-DPPO_HIP_TUNING")
 
 
 def hipcc() -> str:

@@ -21,6 +21,15 @@ int fail(int code, const char* fmt, ...);
 // Checks the launch that was just enqueued (does not synchronise).
 int check_launch(const char* what);
 
+// Compute units and XCDs (accelerator complex dies, each with its own L2) of the current device, queried once per
+// device; {0, 0} when no device is current.  A partitioned MI355X shows fewer of both than the whole chip's 256 / 8.
+struct DeviceInfo {
+  int cus;
+  int xcds;
+};
+DeviceInfo device_info();
+constexpr int kMaxDevices = 64;
+
 constexpr int kWave = 64;
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

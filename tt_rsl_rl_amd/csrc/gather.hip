@@ -1,6 +1,7 @@
 // A5 permutation gather (rsl_rl/storage/rollout_storage.py:232-259) and the observation-normaliser forward
 // (rsl_rl/modules/normalization.py:46-48), fused: one pass over the rollout per update writes the packed,
-// permuted, normalised row table that every mini-batch of every epoch then reads contiguously.
+// permuted, normalised row table that every mini-batch of every epoch then reads contiguously (for the recurrent
+// update also the keep = 1 - done column, from the stored uint8 dones).
 //
 // The copied floats of a row, segment after segment, are numbered 0 .. total-1 ("flat columns"); lane l of a
 // wavefront owns flat columns l, l + 64, ... (kSlots of them per pass), so consecutive lanes read consecutive floats of
@@ -23,7 +24,7 @@ struct GatherArgs {
 
 // Source pointers are global memory; read back from the LDS copy of the segment table they would otherwise be
 // generic (flat) pointers, whose loads also count as LDS operations and defeat the wait counters.
-typedef const float __attribute__((address_space(1))) global_float;
+typedef const uint32_t __attribute__((address_space(1))) global_u32;
 
 constexpr int kGatherThreads = 256;
 constexpr int kWavesPerBlock = kGatherThreads / kWave;
@@ -41,11 +42,13 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const int64
   const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
   const int total = args.prefix[args.num_segments];
   for (int f0 = 0; f0 < total; f0 += kWave * kSlots) {
-    // this lane's flat columns of the pass -> source base, stride, destination column, normaliser
-    global_float* src[kSlots];
+    // this lane's flat columns of the pass -> source address and row stride (bytes), destination column,
+    // normaliser.  Every source element is read as the aligned 32-bit word that holds it: the float itself, or for a
+    // keep segment the word around the uint8 done flag (inside the flags' allocation), from which the byte is taken.
+    uintptr_t src[kSlots];
     int64_t stride[kSlots];
     int dcol[kSlots];
-    bool valid[kSlots];
+    bool valid[kSlots], keep[kSlots];
     float mu[kSlots], den[kSlots];
 #pragma unroll
     for (int k = 0; k < kSlots; ++k) {
@@ -55,10 +58,13 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const int64
       const int col = fc - args.prefix[s];
       const ppo_gather_segment& g = seg[s];
       const bool in = fc < total;
+      const bool u8 = in && g.kind == PPO_GATHER_KEEP_U8;
+      const int esz = u8 ? 1 : 4;
       // a lane without a column this slot reads element (0, 0) of the first segment and discards it
-      src[k] = (global_float*)(in ? g.src + col : seg[0].src);  // generic -> global: an address-space cast
+      src[k] = reinterpret_cast<uintptr_t>(in ? g.src : seg[0].src) + (in ? col * esz : 0);
       valid[k] = in;
-      stride[k] = in ? g.src_stride : 0;
+      keep[k] = u8;
+      stride[k] = in ? g.src_stride * esz : 0;
       dcol[k] = g.dst_col + col;
       const bool norm = in && g.norm_mean != nullptr;
       mu[k] = norm ? g.norm_mean[col] : 0.0f;
@@ -75,18 +81,29 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const int64
       // every load unconditional and in straight-line code (rows outside [0, rows) read source row 0), so the
       // wave issues all of them before it waits
       float v[kRowsPerIter][kSlots];
+      uint32_t word[kRowsPerIter][kSlots];
+      int shift[kRowsPerIter][kSlots];
 #pragma unroll
       for (int r = 0; r < kRowsPerIter; ++r) {
         const int64_t row = sr[r] >= 0 ? sr[r] : 0;
 #pragma unroll
-        for (int k = 0; k < kSlots; ++k) v[r][k] = src[k][row * stride[k]];
+        for (int k = 0; k < kSlots; ++k) {
+          const uintptr_t a = src[k] + row * stride[k];
+          word[r][k] = *reinterpret_cast<global_u32*>(a & ~static_cast<uintptr_t>(3));
+          shift[r][k] = static_cast<int>(a & 3) * 8;
+        }
       }
-      // then all arithmetic (plain copies take mu = 0, den = 1: (x - 0) / 1 == x exactly), then all stores: a store
-      // counts in the same counter as the loads, so interleaving them would make every wait drain the stores too
+      // then all arithmetic (plain copies take mu = 0, den = 1: (x - 0) / 1 == x exactly; keep = 1 - done), then all
+      // stores: a store counts in the same counter as the loads, so interleaving them would make every wait drain the
+      // stores too
 #pragma unroll
       for (int r = 0; r < kRowsPerIter; ++r)
 #pragma unroll
-        for (int k = 0; k < kSlots; ++k) v[r][k] = (v[r][k] - mu[k]) / den[k];
+        for (int k = 0; k < kSlots; ++k) {
+          const float x = keep[k] ? 1.0f - static_cast<float>((word[r][k] >> shift[r][k]) & 0xffu)
+                                  : __uint_as_float(word[r][k]);
+          v[r][k] = (x - mu[k]) / den[k];
+        }
       __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic above the (predicated) stores
 #pragma unroll
       for (int r = 0; r < kRowsPerIter; ++r)
@@ -136,6 +153,10 @@ extern "C" int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_ro
                 (long long)(g.dst_col + g.width), (long long)dst_stride);
     PPO_REQUIRE(g.norm_mean == nullptr || g.norm_std != nullptr, "ppo_gather_rows: segment %d has mean but no std",
                 s);
+    PPO_REQUIRE(g.kind == PPO_GATHER_FLOAT || (g.kind == PPO_GATHER_KEEP_U8 && g.norm_mean == nullptr),
+                "ppo_gather_rows: segment %d: kind %d (a keep segment takes no normaliser)", s, g.kind);
+    PPO_REQUIRE(g.kind != PPO_GATHER_FLOAT || reinterpret_cast<uintptr_t>(g.src) % 4 == 0,
+                "ppo_gather_rows: segment %d: fp32 source not 4-byte aligned", s);
     args.seg[s] = g;
     args.prefix[s] = static_cast<int32_t>(total);
     total += g.width;

@@ -133,17 +133,29 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TransposeGroup g) 
 }
 
 // Weight-grad: 128 x 128 tiles; split-K over the rows, in chunks that are multiples of the deepest (64-row) slab.
-// The split count fills ONE wave of resident blocks and no more: the default tile runs two blocks per CU, so 512
-// blocks on gfx950's 256 CUs.  A launch of 1,050 blocks (the humanoid weight-grads' 30 tiles x 35 splits) leaves its
-// last 26 blocks alone on the chip for a third of the kernel time; 30 x 17 = 510 blocks measured 280 us against 324.
-// "PPO_HIP_DW_CFG" (bk32s2o2 / bk16s2o3 / bk16s3o3) and "PPO_HIP_DW_BLOCKS" (resident-block capacity) override the
-// defaults (tuning aids).  Host arithmetic only: the workspace query must give the same plan without a device.
+// The split count fills ONE wave of resident blocks and no more: the tile runs two blocks per CU, so 512 blocks on
+// the 256 CUs of a whole MI355X (fewer on a partitioned one).  A launch of 1,050 blocks (the humanoid weight-grads'
+// 30 tiles x 35 splits) leaves its last 26 blocks alone on the chip for a third of the kernel time; 30 x 17 = 510
+// blocks measured 280 us against 324.  The workspace query is host arithmetic (no device needed): it plans for the
+// largest capacity, kDwMaxConcurrent, and a launch on a smaller device uses fewer splits, i.e. less workspace.
 constexpr int kDwBM = 128, kDwBN = 128, kDwChunk = 64;
-constexpr int kDwConcurrentBlocks = 2 * 256;
+constexpr int kDwBlocksPerCu = 2;
+constexpr int kDwMaxConcurrent = kDwBlocksPerCu * 256;
 
-int dw_splits(int64_t tiles, int64_t rows) {
-  const char* e = std::getenv("PPO_HIP_DW_BLOCKS");
-  const int64_t capacity = e ? std::max(1, std::atoi(e)) : kDwConcurrentBlocks;
+int dw_query_capacity() {
+#ifdef PPO_HIP_TUNING
+  if (const char* e = std::getenv("PPO_HIP_DW_BLOCKS")) return std::max(1, std::atoi(e));  // tuning aid
+#endif
+  return kDwMaxConcurrent;
+}
+
+int dw_launch_capacity() {
+  const int cus = device_info().cus;
+  const int cap = dw_query_capacity();
+  return cus > 0 ? std::min(cap, kDwBlocksPerCu * cus) : cap;
+}
+
+int dw_splits(int64_t tiles, int64_t rows, int capacity) {
   int64_t s = capacity / std::max<int64_t>(tiles, 1);
   s = std::min<int64_t>(s, std::max<int64_t>(1, rows / 256));
   s = std::max<int64_t>(1, std::min<int64_t>(s, 256));
@@ -160,12 +172,12 @@ struct DwPlan {
   size_t total_floats;
 };
 
-DwPlan plan_dw(const ppo_linear_bwd_dw_problem* probs, int count, int64_t rows) {
+DwPlan plan_dw(const ppo_linear_bwd_dw_problem* probs, int count, int64_t rows, int capacity) {
   DwPlan plan{};
   int64_t tiles = 0;
   for (int i = 0; i < count; ++i)
     tiles += ceil_div(probs[i].out_features, kDwBM) * ceil_div(probs[i].in_features, kDwBN);
-  const int s = dw_splits(tiles, rows);
+  const int s = dw_splits(tiles, rows, capacity);
   size_t off = 0;
   for (int i = 0; i < count; ++i) {
     const int64_t chunk = ceil_div(ceil_div(rows, s), kDwChunk) * kDwChunk;
@@ -341,7 +353,7 @@ extern "C" size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_prob
   if (problems == nullptr || count < 1 || count > PPO_MAX_LINEAR_PROBLEMS || !rows_ok(rows)) return 0;
   for (int i = 0; i < count; ++i)
     if (problems[i].in_features <= 0 || problems[i].out_features <= 0) return 0;
-  return plan_dw(problems, count, rows).total_floats * sizeof(float);
+  return plan_dw(problems, count, rows, dw_query_capacity()).total_floats * sizeof(float);
 }
 
 extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows,
@@ -351,13 +363,13 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   PPO_REQUIRE(rows_ok(rows), "ppo_linear_bwd_dw: rows=%lld", (long long)rows);
   for (int i = 0; i < count; ++i) {
     const ppo_linear_bwd_dw_problem& q = problems[i];
-    PPO_REQUIRE(q.dz && q.x && q.dw && q.db, "ppo_linear_bwd_dw: problem %d has a null pointer", i);
+    PPO_REQUIRE(q.dz && q.x && q.dw, "ppo_linear_bwd_dw: problem %d has a null pointer", i);
     PPO_REQUIRE(q.in_features > 0 && q.out_features > 0, "ppo_linear_bwd_dw: problem %d features", i);
     PPO_REQUIRE(q.lddz >= q.out_features && q.ldx >= q.in_features, "ppo_linear_bwd_dw: problem %d leading dims", i);
     PPO_REQUIRE(static_cast<int64_t>(q.out_features) * (round4(q.in_features) + 4) < (int64_t(1) << 31),
                 "ppo_linear_bwd_dw: problem %d: weight of %d x %d is too large", i, q.out_features, q.in_features);
   }
-  const DwPlan plan = plan_dw(problems, count, rows);
+  const DwPlan plan = plan_dw(problems, count, rows, dw_launch_capacity());
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total_floats * sizeof(float),
               "ppo_linear_bwd_dw: workspace too small (%zu < %zu)", workspace_bytes,
               plan.total_floats * sizeof(float));
@@ -374,7 +386,7 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     p.B = q.x; p.ldb = q.ldx;
     p.C = ws + plan.partial_off[i]; p.ldc = ldp;
     p.partial_stride = static_cast<int64_t>(q.out_features) * ldp;
-    p.colsum = reinterpret_cast<double*>(ws + plan.colsum_off[i]);
+    p.colsum = q.db != nullptr ? reinterpret_cast<double*>(ws + plan.colsum_off[i]) : nullptr;
     p.M = q.out_features; p.N = q.in_features; p.K = static_cast<int>(rows);
     p.splits = plan.splits[i]; p.k_chunk = plan.k_chunk[i];
     ReduceItem& r = rg.it[i];
@@ -382,17 +394,16 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     r.out = q.out_features; r.in = q.in_features; r.ld = static_cast<int>(ldp); r.splits = plan.splits[i];
     r.stride = p.partial_stride;
     r.begin = total;
-    total += static_cast<int64_t>(q.out_features) * (ldp / 4 + 1);
+    total += static_cast<int64_t>(q.out_features) * (ldp / 4 + (q.db != nullptr ? 1 : 0));
   }
   for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) rg.it[i].begin = INT64_MAX;
   rg.count = count;
   rg.total = total;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const char* cfg = std::getenv("PPO_HIP_DW_CFG");
   int rc;
-  if (cfg && !std::strcmp(cfg, "bk32s2o2")) {
-    rc = launch_tn<kDwBM, kDwBN, 32, 2, 2>(g, count, s, "linear_bwd_dw");
-  } else if (cfg && !std::strcmp(cfg, "bk16s2o3")) {
+#ifdef PPO_HIP_TUNING
+  const char* cfg = std::getenv("PPO_HIP_DW_CFG");  // tuning aid: other slab depths / stages / occupancies
+  if (cfg && !std::strcmp(cfg, "bk16s2o3")) {
     rc = launch_tn<kDwBM, kDwBN, 16, 2, 3>(g, count, s, "linear_bwd_dw");
   } else if (cfg && !std::strcmp(cfg, "bk16s3o3")) {
     rc = launch_tn<kDwBM, kDwBN, 16, 3, 3>(g, count, s, "linear_bwd_dw");
@@ -401,8 +412,11 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   } else if (cfg && !std::strcmp(cfg, "bk32s2o1")) {
     rc = launch_tn<kDwBM, kDwBN, 32, 2, 1>(g, count, s, "linear_bwd_dw");
   } else {
-    rc = launch_tn<kDwBM, kDwBN, 32, 2, 2>(g, count, s, "linear_bwd_dw");
+    rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
   }
+#else
+  rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+#endif
   if (rc != PPO_OK) return rc;
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 4096);
   hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);

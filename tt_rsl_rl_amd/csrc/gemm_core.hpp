@@ -77,6 +77,7 @@ struct Problem {
   int32_t block_begin;
   int32_t c_vec;            // NT epilogue: C (and C2 / aux when used) allow 16-byte accesses
   int32_t elu_from_output;  // input-grad: aux holds h = elu(z) (ELU' = 1 if h > 0 else h + 1), else z
+  int32_t b16;              // NT: B allows 16-byte direct loads (set by launch_nt)
   LstmArgs lstm;            // EPI_LSTM_*
 };
 
@@ -110,17 +111,16 @@ __device__ __forceinline__ float elu_fwd(float x) {
 struct Group {
   Problem p[PPO_MAX_LINEAR_PROBLEMS];
   int32_t count;
-  int32_t xcd_remap;  // 1: permute block ids so each XCD gets a contiguous range of tiles
+  int32_t xcds;  // > 1: the device's XCDs; block ids are permuted so each XCD gets a contiguous range of tiles
 };
 
 constexpr int kThreads = 256;
-constexpr int kXcds = 8;
 
-// Blocks are dispatched round-robin over the XCDs; renumber them so that each XCD receives a contiguous range of
+// Blocks are dispatched round-robin over the X XCDs; renumber them so that each XCD receives a contiguous range of
 // logical tiles (a bijection of [0, n)).
-__device__ inline int xcd_remap(int b, int n) {
-  const int q = n / kXcds, r = n % kXcds;
-  const int xcd = b % kXcds, slot = b / kXcds;
+__device__ inline int xcd_remap(int b, int n, int X) {
+  const int q = n / X, r = n % X;
+  const int xcd = b % X, slot = b / X;
   return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
 }
 
@@ -129,7 +129,7 @@ struct TileCoord {
 };
 
 __device__ inline TileCoord locate(const Group& g) {
-  const int b = g.xcd_remap ? xcd_remap(blockIdx.x, gridDim.x) : static_cast<int>(blockIdx.x);
+  const int b = g.xcds > 1 ? xcd_remap(blockIdx.x, gridDim.x, g.xcds) : static_cast<int>(blockIdx.x);
   int pi = 0;
 #pragma unroll
   for (int i = 1; i < PPO_MAX_LINEAR_PROBLEMS; ++i) {
@@ -406,18 +406,16 @@ __device__ __forceinline__ void lstm_bwd_finish(const LstmArgs& L, int64_t m, in
   if (!L.last) *reinterpret_cast<f32x4*>(L.dc + m * H + n) = dcout;
 }
 
+// The NT tile's body; `lds` is the kernel's ring of S stages.
 template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16, int EPI>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_kernel(
-    const Group g) {
+__device__ __forceinline__ void gemm_nt_tile(const Group& g, const TileCoord& tc, float* lds) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = (BM + BN) * BK;
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(S >= 2 && S <= 4, "2..4 LDS stages");
   constexpr int L = NtLoader<BM, BK, A16>::PER + NtLoader<BN, BK, B16>::PER;
-  __shared__ __align__(16) float lds[S * STAGE];
 
-  const TileCoord tc = locate(g);
   const Problem& P = g.p[tc.pi];
   // problem fields as values: the loop's compiler barriers would otherwise re-read them from the argument block
   const float* const A = P.A;
@@ -598,6 +596,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         }
       }
     }
+  }
+}
+
+// B16M: the second operand's loads are 16 bytes wide in every problem (1), 4 bytes in every problem (0), or chosen
+// per problem from Problem::b16 (2: a grouped launch whose weights differ in alignment, e.g. a 99-wide critic input
+// beside a 96-wide actor input; the branch is uniform per block).
+template <int BM, int BN, int BK, int S, int OCC, bool A16, int B16M, int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_kernel(
+    const Group g) {
+  __shared__ __align__(16) float lds[S * (BM + BN) * BK];
+  const TileCoord tc = locate(g);
+  if constexpr (B16M == 2) {
+    if (g.p[tc.pi].b16) {
+      gemm_nt_tile<BM, BN, BK, S, OCC, A16, true, EPI>(g, tc, lds);
+    } else {
+      gemm_nt_tile<BM, BN, BK, S, OCC, A16, false, EPI>(g, tc, lds);
+    }
+  } else {
+    gemm_nt_tile<BM, BN, BK, S, OCC, A16, B16M == 1, EPI>(g, tc, lds);
   }
 }
 
@@ -924,7 +941,10 @@ int assign_blocks(Group& g, int count, int bm, int bn, const char* name, int& bl
     blocks += static_cast<int>(nb);
   }
   g.count = count;
-  g.xcd_remap = std::getenv("PPO_HIP_NO_XCD_REMAP") == nullptr;
+  g.xcds = device_info().xcds;
+#ifdef PPO_HIP_TUNING
+  if (std::getenv("PPO_HIP_NO_XCD_REMAP") != nullptr) g.xcds = 1;
+#endif
   for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) g.p[i].block_begin = INT32_MAX;
   return PPO_OK;
 }
@@ -934,19 +954,24 @@ int launch_nt(Group& g, int count, hipStream_t s, const char* name) {
   int blocks;
   if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
-  bool a16 = true, b16 = true;
+  bool a16 = true, all_b16 = true, any_b16 = false;
   for (int i = 0; i < count; ++i) {
     a16 = a16 && w16_ok(g.p[i].A, g.p[i].lda);
-    b16 = b16 && w16_ok(g.p[i].B, g.p[i].ldb);
+    g.p[i].b16 = w16_ok(g.p[i].B, g.p[i].ldb);
+    all_b16 = all_b16 && g.p[i].b16;
+    any_b16 = any_b16 || g.p[i].b16;
   }
-  if (a16 && b16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (a16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  } else if (b16) {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, false, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  const dim3 grid(blocks), block(kThreads);
+  if (a16) {
+    if (all_b16) {
+      hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, 1, EPI>), grid, block, 0, s, g);
+    } else if (any_b16) {
+      hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, 2, EPI>), grid, block, 0, s, g);
+    } else {
+      hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, 0, EPI>), grid, block, 0, s, g);
+    }
   } else {
-    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, false, false, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+    hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, false, 0, EPI>), grid, block, 0, s, g);
   }
   return check_launch(name);
 }
@@ -957,7 +982,8 @@ int launch_nt_aligned(Group& g, int count, hipStream_t s, const char* name) {
   int blocks;
   if (int rc = assign_blocks(g, count, BM, BN, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
-  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, true, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  for (int i = 0; i < count; ++i) g.p[i].b16 = 1;
+  hipLaunchKernelGGL((gemm_nt_kernel<BM, BN, BK, S, OCC, true, 1, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
   return check_launch(name);
 }
 
@@ -993,16 +1019,20 @@ int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
   return check_launch(name);
 }
 
-// NT tile of a launch (BM x BN, k-slab depth, LDS stages, waves per SIMD): "PPO_HIP_GEMM_TILE" (e.g.
-// "128x128k16s2o3") overrides the size-based choice (tuning aid).
+// NT tile of a launch (BM x BN, k-slab depth, LDS stages, waves per SIMD).  The library ships the three the layers'
+// shapes use (chosen by timing every tile on MI355X at 24,576-row mini-batches); a build with PPO_HIP_TUNING defined
+// adds the others and the "PPO_HIP_GEMM_TILE" override (e.g. "128x128k16s2o3") for such sweeps.
 enum Tile {
-  T128x128k16s2o3, T128x128k16s3o3, T128x128k16s2o2, T128x128k32s2o2, T128x64k16s4o4, T128x64k32s2o4,
-  T64x64k32s2o4, T64x64k32s2o5, T192x128k16s2o2, T128x128k64s2o1, T128x128k32s2o1, T256x128k32s2o1,
-  T128x64k64s2o2
+  T128x128k16s2o3, T128x64k32s2o4, T64x64k32s2o4,
+#ifdef PPO_HIP_TUNING
+  T128x128k16s3o3, T128x128k16s2o2, T128x128k32s2o2, T128x64k16s4o4, T64x64k32s2o5, T192x128k16s2o2,
+  T128x128k64s2o1, T128x128k32s2o1, T256x128k32s2o1, T128x64k64s2o2
+#endif
 };
 
-Tile pick_tile(Tile dflt, const char* var = "PPO_HIP_GEMM_TILE") {
-  const char* e = std::getenv(var);
+Tile pick_tile(Tile dflt) {
+#ifdef PPO_HIP_TUNING
+  const char* e = std::getenv("PPO_HIP_GEMM_TILE");
   if (e == nullptr) return dflt;
   static const struct {
     const char* name;
@@ -1016,12 +1046,18 @@ Tile pick_tile(Tile dflt, const char* var = "PPO_HIP_GEMM_TILE") {
                 {"128x64k64s2o2", T128x64k64s2o2}};
   for (const auto& k : kTiles)
     if (!std::strcmp(e, k.name)) return k.t;
+#endif
   return dflt;
 }
 
 template <int EPI>
 int launch_nt_tile(Tile t, Group& g, int count, hipStream_t s, const char* name) {
   switch (t) {
+    case T128x64k32s2o4:
+      return launch_nt<128, 64, 32, 2, 4, EPI>(g, count, s, name);
+    case T64x64k32s2o4:
+      return launch_nt<64, 64, 32, 2, 4, EPI>(g, count, s, name);
+#ifdef PPO_HIP_TUNING
     case T128x128k16s3o3:
       return launch_nt<128, 128, 16, 3, 3, EPI>(g, count, s, name);
     case T128x128k16s2o2:
@@ -1030,10 +1066,6 @@ int launch_nt_tile(Tile t, Group& g, int count, hipStream_t s, const char* name)
       return launch_nt<128, 128, 32, 2, 2, EPI>(g, count, s, name);
     case T128x64k16s4o4:
       return launch_nt<128, 64, 16, 4, 4, EPI>(g, count, s, name);
-    case T128x64k32s2o4:
-      return launch_nt<128, 64, 32, 2, 4, EPI>(g, count, s, name);
-    case T64x64k32s2o4:
-      return launch_nt<64, 64, 32, 2, 4, EPI>(g, count, s, name);
     case T64x64k32s2o5:
       return launch_nt<64, 64, 32, 2, 5, EPI>(g, count, s, name);
     case T192x128k16s2o2:
@@ -1046,6 +1078,7 @@ int launch_nt_tile(Tile t, Group& g, int count, hipStream_t s, const char* name)
       return launch_nt<256, 128, 32, 2, 1, EPI>(g, count, s, name);
     case T128x64k64s2o2:
       return launch_nt<128, 64, 64, 2, 2, EPI>(g, count, s, name);
+#endif
     default:
       return launch_nt<128, 128, 16, 2, 3, EPI>(g, count, s, name);
   }

@@ -198,7 +198,8 @@ constexpr int kFinUnroll = 8;  // partials per lane and pass
 template <int CI>
 __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
     const LossParams p, const double* __restrict__ partials, int nblocks, float* __restrict__ d_std_param,
-    ppo_device_state* __restrict__ state, int adaptive, float kl_hi, float kl_lo, double* __restrict__ trace) {
+    ppo_device_state* __restrict__ state, int adaptive, float kl_hi, float kl_lo, double* __restrict__ trace,
+    int trace_rows) {
   const int A = p.a.num_actions;
   const int cols = kFixedCols + A;
   __shared__ double s_col[kFixedCols + PPO_MAX_ACTIONS];
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(kFinThreads) void ppo_loss_finalize_kernel(
     state->last_surrogate_loss = surrogate;
     state->last_value_loss = value;
     state->last_entropy = entropy;
-    if (trace != nullptr) {
+    if (trace != nullptr && nmb < trace_rows) {  // rows past the caller's buffer are not written
       double* t = trace + 5 * static_cast<int64_t>(nmb);
       t[0] = kl_mean;
       t[1] = lr;
@@ -669,11 +670,16 @@ bool head_supported(int num_actions, int k_actor, int k_critic) {
          k_actor % 16 == 0 && k_critic >= 16 && k_critic <= kHeadMaxK && k_critic % 16 == 0;
 }
 
-// Wavefronts per block of the fused head kernel; "PPO_HIP_HEAD_WAVES" (1, 2 or 4) overrides it (tuning aid).
+// Wavefronts per block of the fused head kernel; in a build with PPO_HIP_TUNING, "PPO_HIP_HEAD_WAVES" (1, 2 or 4)
+// overrides it (tuning aid).
 int head_waves() {
+#ifdef PPO_HIP_TUNING
   const char* e = std::getenv("PPO_HIP_HEAD_WAVES");
   const int w = e ? std::atoi(e) : kHeadWavesDefault;
   return (w == 1 || w == 2 || w == 4) ? w : kHeadWavesDefault;
+#else
+  return kHeadWavesDefault;
+#endif
 }
 
 // Blocks of the fused head kernel: one 16-row tile per wave while that fits in 1024 blocks, else 1024 blocks that
@@ -686,12 +692,16 @@ int64_t head_blocks(int64_t rows) {
 int lanes_per_row(int num_actions) { return num_actions <= 32 ? 32 : 64; }
 
 // Blocks of the loss kernel (= block partials the finalize reduces), at most 512 (measured: 26.5 us for loss +
-// finalize at 512, 28.0 at 1024, 32.2 at 256 on 24,576 rows); "PPO_HIP_LOSS_BLOCKS" overrides the cap
-// (tuning aid).  Host arithmetic only: the workspace query must agree with the launch.
+// finalize at 512, 28.0 at 1024, 32.2 at 256 on 24,576 rows); in a build with PPO_HIP_TUNING, "PPO_HIP_LOSS_BLOCKS"
+// overrides the cap (tuning aid).  Host arithmetic only: the workspace query must agree with the launch.
 int64_t loss_blocks(int64_t rows, int num_actions) {
   const int groups = kLossThreads / lanes_per_row(num_actions);
+#ifdef PPO_HIP_TUNING
   const char* e = std::getenv("PPO_HIP_LOSS_BLOCKS");
   const int64_t cap = e ? std::max(1, std::min(1024, std::atoi(e))) : 512;
+#else
+  const int64_t cap = 512;
+#endif
   return std::max<int64_t>(1, std::min<int64_t>(cap, ceil_div(rows, groups)));
 }
 
@@ -724,7 +734,8 @@ int make_params(const ppo_loss_args* args, LossParams& p, const char* who, bool 
 }
 
 int launch_finalize(const LossParams& p, const void* workspace, int64_t blocks, float* d_std_param,
-                    ppo_device_state* state, int32_t adaptive, double desired_kl, double* trace, ppo_stream_t stream) {
+                    ppo_device_state* state, int32_t adaptive, double desired_kl, double* trace, int32_t trace_rows,
+                    ppo_stream_t stream) {
   // upstream compares the fp32 kl_mean with the Python floats desired_kl*2 and desired_kl/2, which torch rounds
   // to fp32 before comparing.
   const float kl_hi = static_cast<float>(desired_kl * 2.0);
@@ -733,7 +744,7 @@ int launch_finalize(const LossParams& p, const void* workspace, int64_t blocks, 
   auto launch = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(1), dim3(kFinThreads), 0, static_cast<hipStream_t>(stream), p,
                        static_cast<const double*>(workspace), static_cast<int>(blocks), d_std_param, state,
-                       adaptive ? 1 : 0, kl_hi, kl_lo, trace);
+                       adaptive ? 1 : 0, kl_hi, kl_lo, trace, trace != nullptr ? trace_rows : 0);
   };
   static_assert(kFixedCols + PPO_MAX_ACTIONS <= 5 * kFinWaves, "five column rounds cover every column");
   switch (ci) {
@@ -777,15 +788,16 @@ extern "C" int ppo_gauss_ppo_loss(const ppo_loss_args* args, void* workspace, si
 
 extern "C" int ppo_loss_finalize(const ppo_loss_args* args, const void* workspace, size_t workspace_bytes,
                                  float* d_std_param, ppo_device_state* state, int32_t adaptive, double desired_kl,
-                                 double* trace, ppo_stream_t stream) {
+                                 double* trace, int32_t trace_rows, ppo_stream_t stream) {
   LossParams p{};
   int rc = make_params(args, p, "ppo_loss_finalize");
+  PPO_REQUIRE(trace == nullptr || trace_rows > 0, "ppo_loss_finalize: trace_rows=%d", trace_rows);
   if (rc != PPO_OK) return rc;
   const size_t need = ppo_loss_workspace_bytes(args->rows, args->num_actions);
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "ppo_loss_finalize: workspace too small");
   PPO_REQUIRE(d_std_param != nullptr && state != nullptr, "ppo_loss_finalize: null pointer");
   return launch_finalize(p, workspace, loss_blocks(args->rows, args->num_actions), d_std_param, state, adaptive,
-                         desired_kl, trace, stream);
+                         desired_kl, trace, trace_rows, stream);
 }
 
 extern "C" int ppo_gauss_ppo_head_supported(int32_t num_actions, int32_t k_actor, int32_t k_critic) {
@@ -799,9 +811,11 @@ extern "C" size_t ppo_head_workspace_bytes(int64_t rows, int32_t num_actions) {
 
 extern "C" int ppo_gauss_ppo_head(const ppo_loss_args* args, const ppo_policy_head* head, void* workspace,
                                   size_t workspace_bytes, float* d_std_param, ppo_device_state* state,
-                                  int32_t adaptive, double desired_kl, double* trace, ppo_stream_t stream) {
+                                  int32_t adaptive, double desired_kl, double* trace, int32_t trace_rows,
+                                  ppo_stream_t stream) {
   static const char* who = "ppo_gauss_ppo_head";
   PPO_REQUIRE(args != nullptr && head != nullptr, "%s: null args / head", who);
+  PPO_REQUIRE(trace == nullptr || trace_rows > 0, "%s: trace_rows=%d", who, trace_rows);
   const ppo_policy_head& h = *head;
   const ppo_loss_args& a = *args;
   PPO_REQUIRE(head_supported(a.num_actions, h.k_actor, h.k_critic),
@@ -835,11 +849,14 @@ extern "C" int ppo_gauss_ppo_head(const ppo_loss_args* args, const ppo_policy_he
                        static_cast<hipStream_t>(stream), P, static_cast<double*>(workspace));
   };
   switch (head_waves()) {
+#ifdef PPO_HIP_TUNING
     case 1: launch(ppo_head_kernel<1>, 1); break;
     case 2: launch(ppo_head_kernel<2>, 2); break;
-    default: launch(ppo_head_kernel<4>, 4); break;
+#endif
+    default: launch(ppo_head_kernel<kHeadWavesDefault>, kHeadWavesDefault); break;
   }
   rc = check_launch("ppo_head_kernel");
   if (rc != PPO_OK) return rc;
-  return launch_finalize(P.lp, workspace, blocks, d_std_param, state, adaptive, desired_kl, trace, stream);
+  return launch_finalize(P.lp, workspace, blocks, d_std_param, state, adaptive, desired_kl, trace, trace_rows,
+                         stream);
 }

@@ -150,7 +150,6 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 //
 // The MFMA sequence per accumulator (32-deep k slabs, k-groups of 8, element s of the f32x4 fragments) and the cell
 // arithmetic are those of the per-step kernel on 64 x 64 tiles, so both paths give identical results.
-constexpr int kMaxDevices = 64;
 constexpr int kSeqRows = 64, kSeqCols = 64, kSeqBK = 32;
 constexpr int kSeqMaxSlabs = 8;  // H <= 256: the w_hh_g slice is 64 KB of LDS, two blocks per CU
 constexpr int kSyncHeader = 32;  // int32 words ahead of the row-group lines: [0] status (sticky), [1] abort
@@ -175,6 +174,7 @@ struct SeqFwdArgs {
   int32_t* sync;
   uint64_t spin_ticks;
   int32_t H, E, T, nrg, ncb, slots;
+  int32_t xcds;  // XCDs of the device (block b runs on XCD b % xcds)
 };
 
 // Zeroes the abort word and the counters of one sequence call (the status word stays).
@@ -243,17 +243,17 @@ __device__ __forceinline__ bool writers_on_xcd(const int32_t* line, int nblk, in
 }
 
 // Block numbering of the sequence kernels: the grid is P = problems x slots row-group slots of nblk blocks each.
-// Blocks are dispatched round-robin over the 8 XCDs (block b to XCD b % 8, checked at run time by writers_on_xcd), so
-// a slot's blocks share an XCD when they are 8 apart: b = x + 8 (j + nblk k) for slot pg = x + 8 k.  Within the XCD,
-// block j of slot k is then followed by block j + 1 of the same slot, so that a CU's second resident block (one XCD
-// pass later) belongs to another row group and the two do not run their MFMA phases in lockstep.  When P is not a
-// multiple of 8: pg = b % P, j = b / P.
-__device__ __forceinline__ void seq_block(int nblk, int& pg, int& j) {
+// Blocks are dispatched round-robin over the X XCDs of the device (block b to XCD b % X, checked at run time by
+// writers_on_xcd), so a slot's blocks share an XCD when they are X apart: b = x + X (j + nblk k) for slot
+// pg = x + X k.  Within the XCD, block j of slot k is then followed by block j + 1 of the same slot, so that a CU's
+// second resident block (one XCD pass later) belongs to another row group and the two do not run their MFMA phases
+// in lockstep.  When P is not a multiple of X: pg = b % P, j = b / P.
+__device__ __forceinline__ void seq_block(int nblk, int xcds, int& pg, int& j) {
   const int b = blockIdx.x, P = gridDim.x / nblk;
-  if (P % kXcds == 0) {
-    const int i = b / kXcds;
+  if (xcds > 1 && P % xcds == 0) {
+    const int i = b / xcds;
     j = i % nblk;
-    pg = b % kXcds + kXcds * (i / nblk);
+    pg = b % xcds + xcds * (i / nblk);
   } else {
     pg = b % P;
     j = b / P;
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1, hl = lane >> 5;
   int pg, cb;
-  seq_block(a.ncb, pg, cb);
+  seq_block(a.ncb, a.xcds, pg, cb);
   const int p = pg / a.slots, g = pg % a.slots;
   const int xcd = xcd_id();
   const SeqFwdItem& S = a.it[p];
@@ -437,6 +437,7 @@ struct SeqBwdArgs {
   int32_t* sync;
   uint64_t spin_ticks;
   int32_t H, E, T, nrg, nub, slots;
+  int32_t xcds;
 };
 
 template <int NS>
@@ -447,7 +448,7 @@ __global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int lr = lane & 15, lq = lane >> 4;
   int pg, ub;
-  seq_block(a.nub, pg, ub);
+  seq_block(a.nub, a.xcds, pg, ub);
   const int p = pg / a.slots, g = pg % a.slots;
   const int xcd = xcd_id();
   const SeqBwdItem& S = a.it[p];
@@ -614,13 +615,14 @@ int check_seq(const ppo_lstm_seq_problem* probs, int32_t count, int64_t steps, i
 // kernel with the named block tile ("32x64": 2 splits, "32x32k64": 4 splits over 64-deep slabs, ...).  Measured at
 // E = 1024, H = 256 (two problems): the forward step (k = H) takes ~21 us with every tile, the backward step
 // (k = 4H) 31 us on 64 x 64 and 19 us on 32x32k64, whose 4 splits cut each wave's dependent MFMA chain to a quarter
-// and give 4x the blocks.  "PPO_HIP_LSTM_FWD_CFG" / "PPO_HIP_LSTM_BWD_CFG" override the defaults (tuning aid).  The
-// backward instantiations with 2 splits allow fewer waves per SIMD: their prefetched epilogue operands take
-// registers.
+// and give 4x the blocks.  In a build with PPO_HIP_TUNING, "PPO_HIP_LSTM_FWD_CFG" / "PPO_HIP_LSTM_BWD_CFG" override
+// the defaults (tuning aid).  The backward instantiations with 2 splits allow fewer waves per SIMD: their prefetched
+// epilogue operands take registers.
 template <int EPI>
 int launch_step(Group& g, int count, hipStream_t s, const char* name) {
   constexpr bool fwd = EPI == EPI_LSTM_FWD;
   constexpr int O2 = fwd ? 4 : 2;
+#ifdef PPO_HIP_TUNING
   const char* e = std::getenv(fwd ? "PPO_HIP_LSTM_FWD_CFG" : "PPO_HIP_LSTM_BWD_CFG");
   const char* cfg = e != nullptr ? e : fwd ? "64x64" : "32x32k64";
   if (!std::strcmp(cfg, "32x64")) return launch_nt_ks<32, 64, 32, 2, O2, EPI>(g, count, s, name);
@@ -629,6 +631,13 @@ int launch_step(Group& g, int count, hipStream_t s, const char* name) {
   if (!std::strcmp(cfg, "32x32k64")) return launch_nt_ks<32, 32, 64, 2, 4, EPI>(g, count, s, name);
   if (!std::strcmp(cfg, "32x32k32")) return launch_nt_ks<32, 32, 32, 3, 4, EPI>(g, count, s, name);
   return launch_nt_aligned<64, 64, 32, 2, O2, EPI>(g, count, s, name);
+#else
+  if constexpr (fwd) {
+    return launch_nt_aligned<64, 64, 32, 2, O2, EPI>(g, count, s, name);
+  } else {
+    return launch_nt_ks<32, 32, 64, 2, 4, EPI>(g, count, s, name);
+  }
+#endif
 }
 
 int64_t seq_row_groups(int64_t envs) { return ceil_div(envs, static_cast<int64_t>(kSeqRows)); }
@@ -690,6 +699,7 @@ int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
   }
   a.sync = sync;
   a.spin_ticks = seq_spin_ticks();
+  a.xcds = std::max(device_info().xcds, 1);
   a.H = static_cast<int32_t>(H);
   a.E = static_cast<int32_t>(envs);
   a.T = static_cast<int32_t>(steps);
@@ -735,6 +745,7 @@ int seq_bwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
   }
   a.sync = sync;
   a.spin_ticks = seq_spin_ticks();
+  a.xcds = std::max(device_info().xcds, 1);
   a.H = static_cast<int32_t>(H);
   a.E = static_cast<int32_t>(envs);
   a.T = static_cast<int32_t>(steps);

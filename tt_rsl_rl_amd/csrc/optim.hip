@@ -171,7 +171,6 @@ size_t workspace_bytes_for(int64_t num_params) {
 }
 
 // The current device's copy of `scratch`, looked up once per device (with that device current) and kept.
-constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 double* g_scratch[kMaxDevices] = {};
 

@@ -161,8 +161,6 @@ class UpdateEngine:
         self.adam_ws = ops.Workspace(self.device)
         self.dx_ws = ops.Workspace(self.device)  # the input-grad's w^T copies
         self.adv_ws = ops.Workspace(self.device)
-        self.trace = torch.zeros(5 * alg.num_learning_epochs * self.M, dtype=torch.float64, device=self.device)
-        self.trace_host = torch.empty(self.trace.numel(), dtype=torch.float64, pin_memory=True)
         # the observation normalisers' statistics as the update's forward passes must see them (pre-update), in
         # buffers of their own so the recorded gathers keep pointing at them
         self._norm_frozen: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
@@ -173,6 +171,8 @@ class UpdateEngine:
                                                torch.empty_like(norm._std.view(-1)))
         self._frozen = False
         self._plans: dict = {}
+        self.trace = torch.zeros(0, dtype=torch.float64, device=self.device)
+        self._ensure_trace()
         self._plan_key = None
         self._warm = False  # records are kept from the second run on: by then no workspace grows any more
         self.replays = 0
@@ -182,6 +182,15 @@ class UpdateEngine:
         self.step_hook = None
 
     # -- one update ------------------------------------------------------------------------------------------------
+    def _ensure_trace(self) -> None:
+        """Per-mini-batch trace rows (5 doubles each) for every optimiser step of an update; grown (and the recorded
+        launches, which hold the old buffer, dropped) when num_learning_epochs rises between updates."""
+        need = 5 * self.alg.num_learning_epochs * self.M
+        if self.trace.numel() < need:
+            self.trace = torch.zeros(need, dtype=torch.float64, device=self.device)
+            self.trace_host = torch.empty(need, dtype=torch.float64, pin_memory=True)
+            self._plans.clear()
+
     def freeze_normalizers(self) -> None:
         """Copy the normalisers' current statistics (device to device, on the stream) for this update's gather, so
         the normaliser update (upstream runs it after the epochs, ppo.py:327-330) can be launched first and run
@@ -399,16 +408,24 @@ class UpdateEngine:
     def minibatch_rows(self, i: int) -> tuple[int, int]:
         return i * self.B // self.M, (i + 1) * self.B // self.M
 
+    # the feed-forward update has no device-side failure; the recurrent one overrides these
+    can_fail = False
+
     def read_status(self) -> None:
         """Queue the read-back of device-side error words (none on the feed-forward path)."""
 
-    def check_status(self) -> None:
-        """Raise if a read-back error word is set (after the stream was synchronised)."""
+    def failure(self) -> str | None:
+        """The error a read-back status word reports (after the stream was synchronised), else None."""
+        return None
+
+    def clear_status(self) -> None:
+        """Reset the device-side error words after a failure was reported."""
 
     def run(self, perm: torch.Tensor, first_step: int, ready: int | None = None, rest=None) -> int:
         """All epochs x mini-batches.  Returns the number of optimiser steps taken.  With ``rest``, only
         ``perm[:ready]`` is final at the call: those rows are gathered first, and ``rest()`` (which completes
         ``perm``) is called once the first mini-batch is enqueued, before any row past ``ready`` is needed."""
+        self._ensure_trace()
         sig = self._plan_signature()
         if sig != self._plan_key:
             self._plans.clear()
@@ -461,7 +478,7 @@ class LstmBuffers:
         self.dc = e(envs, H)
         self.zero = torch.zeros(envs, H, device=device)
         self.dw_ih_g, self.dw_hh_g = e(4 * H, D), e(4 * H, H)
-        self.db_g, self.db_g2 = e(4 * H), e(4 * H)
+        self.db_g = e(4 * H)  # the gates' bias gradient (column sums of dgates), once for b_ih and b_hh
 
 
 class RecurrentUpdateEngine(UpdateEngine):
@@ -522,8 +539,9 @@ class RecurrentUpdateEngine(UpdateEngine):
         super().gather(self.order if perm is None else perm)
 
     def segments(self) -> list[ops.Segment]:
-        self._keep = 1.0 - self.alg.storage.dones.reshape(-1, 1).float()
-        return super().segments() + [ops.Segment(self._keep, self.layout.keep)]
+        # keep = 1 - done of each row's step, converted from the stored uint8 dones by the gather itself
+        return super().segments() + [ops.Segment(self.alg.storage.dones.reshape(-1, 1), self.layout.keep,
+                                                 keep=True)]
 
     def _initial_state(self, model, side: str, e0: int, e1: int, buf: LstmBuffers):
         saved = getattr(self.alg.storage, f"saved_hidden_state_{side}")
@@ -545,14 +563,23 @@ class RecurrentUpdateEngine(UpdateEngine):
         return super().dx_layers(R) + [(0, [(self.buf_a.dz[0][:R], la[0].weight, None, self.seq_a.dh[:R]),
                                             (self.buf_c.dz[0][:R], lc[0].weight, None, self.seq_c.dh[:R])], False)]
 
+    @property
+    def can_fail(self) -> bool:
+        return self.lstm_sync is not None
+
     def read_status(self) -> None:
         if self.lstm_sync is not None:
             self._status_host.copy_(self.lstm_sync[:1], non_blocking=True)
 
-    def check_status(self) -> None:
+    def failure(self) -> str | None:
         if self.lstm_sync is not None and int(self._status_host[0]) != 0:
-            raise RuntimeError("LSTM sequence launch: blocks stopped waiting for each other (another whole-sequence "
-                               "launch overlapped on this GPU?); the update's results are invalid")
+            return ("LSTM sequence launch: blocks stopped waiting for each other (another whole-sequence launch "
+                    "overlapped on this GPU?)")
+        return None
+
+    def clear_status(self) -> None:
+        if self.lstm_sync is not None:
+            self.lstm_sync.zero_()
 
     def _grouped(self, fn, qa: dict, qc: dict, E: int) -> None:
         if qa["hidden"] == qc["hidden"]:
@@ -603,7 +630,7 @@ class RecurrentUpdateEngine(UpdateEngine):
         dw = []
         for s, x in ((sa, xa), (sc, xc)):
             dw.append((s.dgates[:R], s.hs[:R], s.dw_hh_g, s.db_g))
-            dw.append((s.dgates[:R], x, s.dw_ih_g, s.db_g2))
+            dw.append((s.dgates[:R], x, s.dw_ih_g, None))  # same operand dgates: its column sums once
         self.weight_grads(dw + head_dw, R, "lstm_dw")
         grad = alg.flat.grad_view
         ops.lstm_unpack_grads([(s.dw_ih_g, s.dw_hh_g, s.db_g, *(grad(p) for p in m.rnn.weights))

@@ -91,11 +91,12 @@ def adv_normalize(x: torch.Tensor, out: torch.Tensor, n: int, in_stride: int = 1
 
 @dataclass
 class Segment:
-    src: torch.Tensor          # [src_rows, >= width] row-major view
+    src: torch.Tensor          # [src_rows, >= width] row-major view (float32; uint8 done flags for keep)
     dst_col: int
     norm_mean: torch.Tensor | None = None
     norm_std: torch.Tensor | None = None
     norm_eps: float = 0.0
+    keep: bool = False         # src holds uint8 done flags d, written as 1 - d
 
 
 def host_randperm(n: int, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -181,14 +182,20 @@ def gather_rows(perm: torch.Tensor, segments: list[Segment], dst: torch.Tensor) 
     segs = []
     src_rows = None
     for s in segments:
-        _dev(s.src, s.norm_mean, s.norm_std)
+        if s.keep:
+            if s.src.dtype != torch.uint8 or s.src.device.type != "cuda" or s.norm_mean is not None:
+                raise ValueError("a keep segment reads uint8 done flags on the GPU (no normaliser)")
+        else:
+            _dev(s.src)
+        _dev(s.norm_mean, s.norm_std)
         ld = _row_major(s.src, "segment src")
         src_rows = s.src.shape[0] if src_rows is None else min(src_rows, s.src.shape[0])
         if s.norm_mean is not None and (s.norm_mean.numel() < s.src.shape[1] or s.norm_std is None
                                         or s.norm_std.numel() < s.src.shape[1]):
             raise ValueError("normaliser statistics narrower than the segment")
         segs.append(L.GatherSegment(s.src.data_ptr(), ld, s.src.shape[1], s.dst_col, _ptr(s.norm_mean),
-                                    _ptr(s.norm_std), float(s.norm_eps), 0))
+                                    _ptr(s.norm_std), float(s.norm_eps),
+                                    L.PPO_GATHER_KEEP_U8 if s.keep else L.PPO_GATHER_FLOAT))
     L.call("ppo_gather_rows", perm.data_ptr(), perm.numel(), int(src_rows), L.array(L.GatherSegment, segs), len(segs),
            dst.data_ptr(), ld_dst, _stream())
 
@@ -274,7 +281,7 @@ def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None,
 
 
 def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:
-    """problems: (dz [rows, out], x [rows, in], dw [out, in], db [out])."""
+    """problems: (dz [rows, out], x [rows, in], dw [out, in], db [out] or None for no bias gradient)."""
     items = []
     for dz, x, dw, db in problems:
         _dev(dz, x, dw, db)
@@ -282,7 +289,7 @@ def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None)
         lddz, ldx = _row_major(dz, "dz"), _row_major(x, "x")
         if dz.shape[0] < rows or x.shape[0] < rows or dz.shape[1] < out_f or x.shape[1] < in_f:
             raise ValueError("linear_bwd_dw: buffers too small")
-        items.append(L.LinearBwdDwProblem(dz.data_ptr(), lddz, x.data_ptr(), ldx, dw.data_ptr(), db.data_ptr(), in_f,
+        items.append(L.LinearBwdDwProblem(dz.data_ptr(), lddz, x.data_ptr(), ldx, dw.data_ptr(), _ptr(db), in_f,
                                           out_f))
     arr = L.array(L.LinearBwdDwProblem, items)
     nbytes = L.load().ppo_linear_bwd_dw_workspace_bytes(arr, len(items), rows)
@@ -388,7 +395,17 @@ def ppo_loss(args: L.LossArgs, ws: torch.Tensor) -> None:
 def ppo_loss_finalize(args: L.LossArgs, ws: torch.Tensor, d_std_param: torch.Tensor, state: torch.Tensor,
                       adaptive: bool, desired_kl: float, trace: torch.Tensor | None) -> None:
     L.call("ppo_loss_finalize", C_ref(args), ws.data_ptr(), ws.numel(), d_std_param.data_ptr(), state.data_ptr(),
-           1 if adaptive else 0, float(desired_kl if desired_kl is not None else 0.0), _ptr(trace), _stream())
+           1 if adaptive else 0, float(desired_kl if desired_kl is not None else 0.0), _ptr(trace), _trace_rows(trace),
+           _stream())
+
+
+def _trace_rows(trace: torch.Tensor | None) -> int:
+    """Rows of 5 doubles a trace buffer holds (the finalize kernels write none past them)."""
+    if trace is None:
+        return 0
+    if trace.dtype != torch.float64 or not trace.is_contiguous():
+        raise ValueError("trace: a contiguous float64 buffer")
+    return trace.numel() // 5
 
 
 def loss_workspace_bytes(rows: int, num_actions: int) -> int:
@@ -435,7 +452,7 @@ def ppo_head(args: L.LossArgs, h_actor: torch.Tensor, w_actor: torch.Tensor, b_a
         value=_ptr(value), ld_value=value.stride(0) if value is not None else 0, k_actor=ka, k_critic=kc)
     L.call("ppo_gauss_ppo_head", C_ref(args), C_ref(head), ws.data_ptr(), ws.numel(), d_std_param.data_ptr(),
            state.data_ptr(), 1 if adaptive else 0, float(desired_kl if desired_kl is not None else 0.0), _ptr(trace),
-           _stream())
+           _trace_rows(trace), _stream())
 
 
 def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max_grad_norm: float, beta1: float,

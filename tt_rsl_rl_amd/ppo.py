@@ -280,6 +280,9 @@ class PPO:
         if st.distribution_params is None:
             raise RuntimeError("update() called before any transition was stored")
         engine = self._get_engine()
+        # an update whose kernels can report a failure (the recurrent one-launch sequences) starts from a copy of
+        # the state it changes, so a failed update leaves the algorithm as it was
+        saved = self._save_state() if engine.can_fail else None
         # the staging buffer's previous copy (one update ago) completed at that update's read-back
         ops.reset_device_state(self.device_state, self.learning_rate, self._reset_host)
         # The normaliser update (upstream: after the epochs, ppo.py:327-330) reads only the stored raw observations;
@@ -314,24 +317,46 @@ class PPO:
         finally:
             if shuffle is not None:
                 shuffle.join()  # idempotent; on an error path it still restores the generator before raising
-        self._opt_steps += steps
 
         # the one host sync of the update: device state and per-mini-batch trace, two async copies, one wait
         self._state_host.copy_(self.device_state, non_blocking=True)
         engine.trace_host.copy_(engine.trace, non_blocking=True)
         engine.read_status()
         torch.cuda.current_stream(self.device).synchronize()
-        engine.check_status()
+        failure = engine.failure()
+        if failure is not None:
+            self._restore_state(saved)
+            engine.clear_status()
+            raise RuntimeError(f"{failure}; the update was rolled back (parameters, optimiser state and normaliser "
+                               "statistics are those before it, the rollout is kept)")
+        self._opt_steps += steps
         state = ops.device_state_from_host(self._state_host)
         self.learning_rate = state.learning_rate
         for group in self.optimizer.param_groups:
             group["lr"] = self.learning_rate
         self._sync_optimizer_state()
         n = self.num_learning_epochs * self.num_mini_batches
-        self._trace_rows = engine.trace_host.view(-1, 5).clone()
+        self._trace_rows = engine.trace_host.view(-1, 5)[:n].clone()
         st.clear()
         return {"value": state.sum_value_loss / n, "surrogate": state.sum_surrogate_loss / n,
                 "entropy": state.sum_entropy / n}
+
+    def _save_state(self) -> dict:
+        """Device copies of what an update changes: the flat parameters and Adam moments, and the observation
+        normalisers' statistics (a few MB, copied on the update's stream)."""
+        f = self.flat
+        norms = [m.obs_normalizer for m in (self.actor, self.critic) if m.obs_normalization]
+        return {"flat": [t.clone() for t in (f.param, f.exp_avg, f.exp_avg_sq)],
+                "norms": [(n, {k: v.clone() for k, v in n.state_dict().items()}) for n in norms]}
+
+    def _restore_state(self, saved: dict) -> None:
+        f = self.flat
+        with torch.no_grad():
+            for dst, src in zip((f.param, f.exp_avg, f.exp_avg_sq), saved["flat"]):
+                dst.copy_(src)
+            for norm, sd in saved["norms"]:
+                for k, v in sd.items():
+                    getattr(norm, k).copy_(v)
 
     @property
     def last_trace(self) -> list[dict]:
