@@ -103,6 +103,12 @@ int ppo_host_randperm(uint8_t* generator_state, size_t state_bytes, int64_t n, i
  * exactly ppo_host_randperm's permutation and generator state. */
 int ppo_host_randperm_range(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t i0, int64_t i1,
                             int64_t* out);
+/* Advances the same generator record past `draws` 32-bit outputs without producing them, host code.  Upstream's
+ * update draws and discards a Normal sample of the mini-batch's [rows, A] means in every mini-batch (the stochastic
+ * forward, rsl_rl/models/mlp_model.py:103-106 via rsl_rl/algorithms/ppo.py:228-233); on the CPU generator a float
+ * normal_ of n >= 16 contiguous elements takes n uniform draws plus 16 more when n % 16 != 0, so skipping those keeps
+ * the next rollout's noise where upstream's CPU run draws it. */
+int ppo_host_rng_skip(uint8_t* generator_state, size_t state_bytes, int64_t draws);
 
 /* ------------------------------------------------------------------------------------------------------------------
  * A6  Linear layers of rsl_rl/modules/mlp.py:27-95 (nn.Linear + nn.ELU), forward and hand-written backward, as fp32

@@ -150,6 +150,7 @@ _SIGNATURES = [
                                    i64, i64, i32, C.c_void_p]),
     ("ppo_host_randperm", C.c_int, [C.c_void_p, C.c_size_t, i64, C.c_void_p]),
     ("ppo_host_randperm_range", C.c_int, [C.c_void_p, C.c_size_t, i64, i64, i64, C.c_void_p]),
+    ("ppo_host_rng_skip", C.c_int, [C.c_void_p, C.c_size_t, i64]),
     ("ppo_adam_workspace_bytes", C.c_size_t, [i64]),
     ("ppo_adam_step", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double, C.c_double,
                                 C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_size_t,

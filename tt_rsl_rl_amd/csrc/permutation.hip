@@ -17,6 +17,10 @@
 // samples that the shuffle does not touch.  The caller passes the record in and writes it back with
 // torch.set_rng_state().
 //
+// The update also advances the generator past the samples upstream's stochastic forward draws and discards in every
+// mini-batch (rsl_rl/models/mlp_model.py:103-106 via rsl_rl/algorithms/ppo.py:228-233): ppo_host_rng_skip moves the
+// stream on by a number of draws without producing them, so the next rollout draws where upstream's would.
+//
 // MT19937 (Matsumoto & Nishimura, 1998): the standard recurrence and output tempering.
 #include "common.hpp"
 
@@ -39,7 +43,7 @@ struct Mt19937 {
 
   static uint32_t mix(uint32_t u, uint32_t v, uint32_t far) {
     const uint32_t y = (u & 0x80000000u) | (v & 0x7fffffffu);
-    return far ^ (y >> 1) ^ ((y & 1u) ? kMtMatrixA : 0u);
+    return far ^ (y >> 1) ^ ((0u - (y & 1u)) & kMtMatrixA);  // branch-free, so the twist loops vectorise
   }
   // in place, in index order: word i combines words i, i+1 and i+M (mod N), the last ones already new
   void twist() {
@@ -57,6 +61,18 @@ struct Mt19937 {
     y ^= (y << 15) & 0xefc60000u;
     y ^= y >> 18;
     return y;
+  }
+
+  // Advance the stream by `count` draws without producing them: only the twists matter (tempering touches the
+  // outputs, not the state).
+  void skip(int64_t count) {
+    while (count > 0) {
+      if (--left == 0) twist();
+      const int64_t run = std::min<int64_t>(count, left);
+      next += static_cast<int>(run);
+      left -= static_cast<int>(run - 1);
+      count -= run;
+    }
   }
 
   // out[0 .. count): the next `count` draws.
@@ -157,6 +173,19 @@ int shuffle_range(uint8_t* generator_state, size_t state_bytes, int64_t n, int64
 
 }  // namespace
 }  // namespace ppo
+
+// Skip `draws` 32-bit outputs of the generator record's stream (no outputs produced).
+extern "C" int ppo_host_rng_skip(uint8_t* generator_state, size_t state_bytes, int64_t draws) {
+  PPO_REQUIRE(generator_state != nullptr, "ppo_host_rng_skip: null pointer");
+  PPO_REQUIRE(state_bytes == kStateBytes, "ppo_host_rng_skip: generator record of %zu bytes (expected %zu)",
+              state_bytes, kStateBytes);
+  PPO_REQUIRE(draws >= 0, "ppo_host_rng_skip: draws=%lld", (long long)draws);
+  Mt19937 mt;
+  if (int rc = load_state(generator_state, mt)) return rc;
+  mt.skip(draws);
+  store_state(mt, generator_state);
+  return PPO_OK;
+}
 
 extern "C" int ppo_host_randperm(uint8_t* generator_state, size_t state_bytes, int64_t n, int64_t* out) {
   return shuffle_range(generator_state, state_bytes, n, 0, n - 1, out, "ppo_host_randperm");

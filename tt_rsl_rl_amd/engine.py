@@ -408,6 +408,12 @@ class UpdateEngine:
     def minibatch_rows(self, i: int) -> tuple[int, int]:
         return i * self.B // self.M, (i + 1) * self.B // self.M
 
+    def discard_sizes(self) -> list[int]:
+        """Elements of the Normal sample upstream's stochastic forward draws (and discards) in each mini-batch of an
+        update, in its order: epoch after epoch, mini-batch after mini-batch, rows x actions."""
+        sizes = [(r1 - r0) * self.A for r0, r1 in (self.minibatch_rows(i) for i in range(self.M))]
+        return sizes * self.alg.num_learning_epochs
+
     # the feed-forward update has no device-side failure; the recurrent one overrides these
     can_fail = False
 

@@ -111,6 +111,8 @@ class GaussianDistribution(nn.Module):
         self.log_std_range = [float(np.log(self.std_range[0])), float(np.log(self.std_range[1]))]
         self._mean: torch.Tensor | None = None
         self._std: torch.Tensor | None = None
+        self.host_noise = True
+        self._host_noise = _HostNoise()
 
     # parameter in its own space and the clamp bounds that go with it
     @property
@@ -151,7 +153,11 @@ class GaussianDistribution(nn.Module):
         self._std = std
 
     def sample(self) -> torch.Tensor:
-        noise = torch.randn_like(self._mean)
+        """torch.normal(mean, std) (distribution.py:193-195): a standard-normal draw scaled on the GPU.  The draw
+        comes from torch's CPU generator (``host_noise``, the default: the stream upstream's CPU run consumes, so the
+        actions and every later draw of that stream are upstream's) or from the device's generator."""
+        noise = self._host_noise.draw(self._mean.shape, self._mean.device) if self.host_noise \
+            else torch.randn_like(self._mean)
         actions = torch.empty_like(self._mean)
         self.sample_from(self._mean, noise, actions, None, None)
         return actions
@@ -181,6 +187,39 @@ class GaussianDistribution(nn.Module):
 
     def deterministic_output(self, mlp_output: torch.Tensor) -> torch.Tensor:
         return mlp_output
+
+
+class _HostNoise:
+    """Standard-normal draws from torch's CPU generator into pinned buffers, copied to the device asynchronously.
+    torch.randn(shape) takes exactly the draws torch.normal(mean, std) takes for that shape on the CPU, and
+    randn * std + mean (two fp32 roundings, as the kernel evaluates it) is its result.  Two buffer pairs alternate; a
+    pinned buffer is refilled only once its previous copy has completed."""
+
+    def __init__(self) -> None:
+        self.host: list[torch.Tensor] = []
+        self.dev: list[torch.Tensor] = []
+        self.done: list = [None, None]
+        self.i = 0
+
+    def draw(self, shape, device) -> torch.Tensor:
+        shape = tuple(shape)
+        if not self.host or tuple(self.host[0].shape) != shape or self.dev[0].device != torch.device(device):
+            for ev in self.done:
+                if ev is not None:
+                    ev.synchronize()
+            self.host = [torch.empty(shape, pin_memory=True) for _ in range(2)]
+            self.dev = [torch.empty(shape, device=device) for _ in range(2)]
+            self.done = [None, None]
+        k = self.i
+        self.i ^= 1
+        if self.done[k] is not None:
+            self.done[k].synchronize()
+        torch.randn(shape, out=self.host[k])
+        self.dev[k].copy_(self.host[k], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.done[k] = ev
+        return self.dev[k]
 
 
 class _ForwardBuffers:

@@ -119,51 +119,110 @@ def host_randperm(n: int, out: torch.Tensor | None = None) -> torch.Tensor:
     return out
 
 
+def normal_draws(n: int) -> int | None:
+    """32-bit draws torch's CPU generator gives a float ``normal_`` of n contiguous elements (what ``torch.normal`` /
+    ``Normal.sample()`` take on the CPU): n >= 16 fills n uniforms and, when n % 16 != 0, redraws the last 16.  None
+    below 16 elements, which go through another path (pairs of 64-bit draws with a cached sample)."""
+    if n < 16:
+        return None
+    return n + (16 if n % 16 else 0)
+
+
 class SplitRandperm:
-    """``torch.randperm(n)`` on the CPU generator in two pieces (rsl_rl/storage/rollout_storage.py:232): iterations
-    [0, split) of the shuffle now, which makes positions [0, split) final, and iterations [split, n - 1) on a worker
-    thread (the native call runs without the GIL) while the caller launches work on the first rows.  ``join()``
-    waits for the rest and writes the generator state back; between ``__init__`` and ``join()`` nothing may draw
-    from the CPU generator.  The result is bit-identical to ``host_randperm``: the same permutation, the same final
-    generator state.  A generator record of an unexpected layout falls back to ``torch.randperm`` in one piece."""
+    """Upstream's CPU-generator draws during one update, in upstream's order, computed natively.
+
+    ``torch.randperm(n)`` (rsl_rl/storage/rollout_storage.py:232) in two pieces: iterations [0, split) of the shuffle
+    now, which makes positions [0, split) final, and iterations [split, n - 1) on a worker thread (the native call
+    runs without the GIL) while the caller launches work on the first rows.  Then, on the same thread, the samples
+    upstream's stochastic forward draws and discards in every mini-batch (``normals``: element counts, in order;
+    rsl_rl/models/mlp_model.py:103-106): skipped natively (``ppo_host_rng_skip``), or drawn with torch below 16
+    elements.  n = 0: no permutation (the recurrent update).  ``join()`` waits and writes the generator state back;
+    between ``__init__`` and ``join()`` nothing else may draw from the CPU generator.  The permutation and the final
+    generator state are bit-identical to torch's.  A generator record of an unexpected layout falls back to torch
+    itself."""
 
     _pool = None
 
-    def __init__(self, n: int, out: torch.Tensor, split: int) -> None:
+    def __init__(self, n: int, out: torch.Tensor | None, split: int, normals: list[int] | tuple = ()) -> None:
         import ctypes
 
-        if out.dtype != torch.int64 or out.device.type != "cpu" or out.numel() != n or not out.is_contiguous():
+        if n > 0 and (out is None or out.dtype != torch.int64 or out.device.type != "cpu" or out.numel() != n
+                      or not out.is_contiguous()):
             raise ValueError("SplitRandperm: out must be a contiguous int64 CPU tensor of n elements")
-        self.n, self.out = n, out
-        self.split = max(0, min(int(split), n - 1))
+        self.n, self.out, self.normals = n, out, list(normals)
+        self.split = max(0, min(int(split), n - 1)) if n > 0 else 0
         self._rec = bytearray(torch.get_rng_state().numpy().tobytes())
         self._buf = (ctypes.c_uint8 * len(self._rec)).from_buffer(self._rec)
-        self._future = None
+        self._perm_future = self._future = None
         lib = L.load()
-        if lib.ppo_host_randperm_range(self._buf, len(self._rec), n, 0, self.split, out.data_ptr()) != L.PPO_OK:
+        if n > 0 and lib.ppo_host_randperm_range(self._buf, len(self._rec), n, 0, self.split,
+                                                 out.data_ptr()) != L.PPO_OK:
             out.copy_(torch.randperm(n))
+            for k in self.normals:
+                torch.randn(k)
             self._rec = None
             self.split = n
             return
-        if self.split < n - 1:
+        if (n > 0 and self.split < n - 1) or self.normals:
             if SplitRandperm._pool is None:
                 from concurrent.futures import ThreadPoolExecutor
 
-                SplitRandperm._pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="ppo-randperm")
-            self._future = SplitRandperm._pool.submit(self._rest)
+                SplitRandperm._pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="ppo-host-rng")
+            # one worker: the skips run after the permutation's rest, in stream order
+            if n > 0 and self.split < n - 1:
+                self._perm_future = SplitRandperm._pool.submit(self._perm_rest)
+            if self.normals:
+                self._future = SplitRandperm._pool.submit(self._skips)
 
-    def _rest(self) -> str | None:
-        lib = L.load()
-        rc = lib.ppo_host_randperm_range(self._buf, len(self._rec), self.n, self.split, self.n - 1,
-                                         self.out.data_ptr())
+    def _perm_rest(self) -> str | None:
+        rc = L.load().ppo_host_randperm_range(self._buf, len(self._rec), self.n, self.split, self.n - 1,
+                                              self.out.data_ptr())
         return None if rc == L.PPO_OK else L.last_error()  # the error text is thread-local: read it here
 
-    def join(self) -> torch.Tensor:
-        if self._future is not None:
-            err = self._future.result()
-            self._future = None
+    def _skips(self) -> str | None:
+        import ctypes
+
+        lib = L.load()
+        if self._perm_future is not None and self._perm_future.result() is not None:
+            return None  # the permutation failed: reported by join()
+        pending = 0
+        for k in self.normals:
+            d = normal_draws(k)
+            if d is not None:
+                pending += d
+                continue
+            if pending and lib.ppo_host_rng_skip(self._buf, len(self._rec), pending) != L.PPO_OK:
+                return L.last_error()
+            pending = 0
+            # a sample below 16 elements: drawn by torch on the record (nothing else uses the generator meanwhile)
+            torch.set_rng_state(torch.frombuffer(self._rec, dtype=torch.uint8).clone())
+            torch.randn(k)
+            ctypes.memmove(self._buf, torch.get_rng_state().numpy().tobytes(), len(self._rec))
+        if pending and lib.ppo_host_rng_skip(self._buf, len(self._rec), pending) != L.PPO_OK:
+            return L.last_error()
+        return None
+
+    def perm_ready(self) -> torch.Tensor | None:
+        """Wait for the permutation only (the skips may still run); the generator state is written back by join()."""
+        if self._perm_future is not None:
+            err = self._perm_future.result()
+            self._perm_future = None
             if err is not None:
+                self.join()
                 raise RuntimeError(f"ppo_host_randperm_range: {err}")
+        return self.out
+
+    def join(self) -> torch.Tensor | None:
+        errs = []
+        for f in (self._perm_future, self._future):
+            if f is not None:
+                e = f.result()
+                if e is not None:
+                    errs.append(e)
+        self._perm_future = self._future = None
+        if errs:
+            self._rec = None
+            raise RuntimeError(f"host generator draws: {errs[0]}")
         if self._rec is not None:
             torch.set_rng_state(torch.frombuffer(self._rec, dtype=torch.uint8).clone())
             self._rec = None

@@ -10,8 +10,12 @@ Compatibility kept with upstream:
   * actor / critic / optimizer state_dict layouts: the models keep upstream's module names and parameter order,
     and ``self.optimizer`` is a real ``torch.optim.Adam`` whose state tensors are views of the flat buffers the
     kernels update, so ``save()`` / ``load()`` produce and accept upstream checkpoints;
-  * the permutation is ``torch.randperm`` on the host CPU generator, drawn once per update, so the mini-batch
-    indices are bit-identical to upstream's CPU run after the same ``torch.manual_seed``.
+  * the random stream of upstream's CPU run: the rollout's action noise is drawn from torch's CPU generator, each
+    update draws its permutation (``torch.randperm``) from it and then skips the samples upstream's stochastic forward
+    draws and discards in every mini-batch, so after the same ``torch.manual_seed`` the actions' noise and every
+    update's mini-batch indices are bit-identical to upstream's over any number of iterations
+    (``hip_cfg={"rng_stream": "device"}`` draws the rollout noise from the device generator instead and skips no
+    samples: the permutation stays on the CPU generator).
 """
 
 from __future__ import annotations
@@ -173,6 +177,9 @@ class PPO:
         if self.device.type != "cuda":
             raise RuntimeError("tt_rsl_rl_amd.ppo.PPO runs on a GPU device (no CPU path)")
         self.hip_cfg = dict(hip_cfg or {})
+        self.rng_stream = self.hip_cfg.get("rng_stream", "cpu")
+        if self.rng_stream not in ("cpu", "device"):
+            raise ValueError(f"hip_cfg rng_stream '{self.rng_stream}': 'cpu' or 'device'")
         self.is_multi_gpu = False
         self.gpu_global_rank = 0
         self.gpu_world_size = 1
@@ -182,6 +189,7 @@ class PPO:
 
         self.actor = actor.to(self.device)
         self.critic = critic.to(self.device)
+        self.actor.distribution.host_noise = self.rng_stream == "cpu"
         self._raw_actor = self.actor
         self._raw_critic = self.critic
 
@@ -293,25 +301,29 @@ class PPO:
         self.actor.update_normalization(obs)
         self.critic.update_normalization(obs)
         # feed-forward: one permutation of the batch for all epochs (ppo.py:207, rollout_storage.py:210-260);
-        # recurrent: fixed env slices, no permutation drawn (rollout_storage.py:262-331)
+        # recurrent: fixed env slices, no permutation drawn (rollout_storage.py:262-331).  Then the samples upstream's
+        # stochastic forward draws and discards, one [rows, A] Normal sample per mini-batch (mlp_model.py:103-106 via
+        # ppo.py:228-233): skipped on the CPU generator by the same worker, beside the GPU update
+        discards = engine.discard_sizes() if self.rng_stream == "cpu" else []
         perm, ready, rest, shuffle = None, None, None, None
-        if not self.is_recurrent:
+        if self.is_recurrent:
+            if discards:
+                shuffle = ops.SplitRandperm(0, None, 0, discards)
+        else:
             if self._perm_host is None or self._perm_host.numel() != B:
                 self._perm_host = torch.empty(B, dtype=torch.int64, pin_memory=True)
                 self._perm_dev = torch.empty(B, dtype=torch.int64, device=self.device)
             # torch.randperm(B) on the CPU generator, computed natively (same permutation, same generator state):
             # the first mini-batch's positions now, the rest on a worker thread while its kernels are enqueued
             ready = engine.minibatch_rows(0)[1]
-            shuffle = ops.SplitRandperm(B, self._perm_host, ready)
+            shuffle = ops.SplitRandperm(B, self._perm_host, ready, discards)
             ready = shuffle.split if shuffle.split < B - 1 else B
             perm = self._perm_dev
             perm[:ready].copy_(self._perm_host[:ready], non_blocking=True)
             if ready < B:
                 def rest():
-                    shuffle.join()
+                    shuffle.perm_ready()
                     perm[ready:].copy_(self._perm_host[ready:], non_blocking=True)
-            else:
-                shuffle.join()
         try:
             steps = engine.run(perm, self._opt_steps, ready, rest)
         finally:
