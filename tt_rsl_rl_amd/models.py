@@ -188,6 +188,10 @@ class GaussianDistribution(nn.Module):
     def deterministic_output(self, mlp_output: torch.Tensor) -> torch.Tensor:
         return mlp_output
 
+    def as_deterministic_output_module(self) -> nn.Module:
+        """distribution.py:201-203: the mean is the MLP output itself."""
+        return nn.Identity()
+
 
 class _HostNoise:
     """Standard-normal draws from torch's CPU generator into pinned buffers, copied to the device asynchronously.
@@ -382,11 +386,26 @@ class MLPModel(nn.Module):
             self.obs_normalizer.update_columns(cols)
 
     def as_jit(self) -> nn.Module:
-        """Export copy in plain torch modules (rsl_rl/models/mlp_model.py:196-218) -- export, not the hot path."""
-        return _ExportMLP(self)
+        """Export copy in plain torch modules (rsl_rl/models/mlp_model.py:163-165, 196-218) -- export, not the hot
+        path."""
+        return _TorchMLPModel(self)
 
     def as_onnx(self) -> nn.Module:
-        return _ExportMLP(self)
+        """rsl_rl/models/mlp_model.py:167-169, 221-255."""
+        return _OnnxMLPModel(self)
+
+    def to(self, *args, **kwargs):
+        """On a GPU device (the one the parameters live on) a no-op that keeps the parameters as views of the
+        update's flat buffers.  On any other device a plain-torch inference copy (``TorchPolicy``), which is what
+        upstream's ``runner.get_inference_policy(device)`` (rsl_rl/runners/on_policy_runner.py:171-174) then hands
+        out; the model itself stays where the update runs."""
+        device = torch._C._nn._parse_to(*args, **kwargs)[0]
+        if device is not None and torch.device(device).type != "cuda":
+            return TorchPolicy(self, device)
+        return super().to(*args, **kwargs)
+
+    def cpu(self):
+        return self.to("cpu")
 
 
 class RNN(nn.Module):
@@ -524,52 +543,34 @@ class RNNModel(MLPModel):
         self.rnn.detach_hidden_state(dones)
 
     def as_jit(self) -> nn.Module:
-        """Export copy with plain torch modules (rsl_rl/models/rnn_model.py:129-175) -- export, not the hot path."""
-        return _ExportLSTM(self)
+        """Export copy with plain torch modules (rsl_rl/models/rnn_model.py:98-105, 147-175) -- export, not the hot
+        path."""
+        return _TorchLSTMModel(self)
 
     def as_onnx(self) -> nn.Module:
-        return _ExportLSTM(self)
+        """rsl_rl/models/rnn_model.py:107-109, 178-247."""
+        return _OnnxRNNModel(self)
 
 
 class _TorchNormalizer(nn.Module):
+    """Plain-torch copy of an EmpiricalNormalization for export: the same buffers (``_mean``, ``_var``, ``_std`` [1, D],
+    ``count``), forward (x - _mean) / (_std + eps) (rsl_rl/modules/normalization.py:46-48)."""
+
     def __init__(self, norm: EmpiricalNormalization) -> None:
         super().__init__()
         self.eps = norm.eps
-        self.register_buffer("_mean", norm._mean.detach().clone().cpu())
-        self.register_buffer("_std", norm._std.detach().clone().cpu())
+        for name in ("_mean", "_var", "_std", "count"):
+            self.register_buffer(name, getattr(norm, name).detach().clone().cpu())
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return (x - self._mean) / (self._std + self.eps)
 
 
-class _ExportMLP(nn.Module):
-    """Deterministic export copy (mean output) with plain torch modules, for TorchScript / ONNX."""
-
-    is_recurrent = False
-
-    def __init__(self, model: MLPModel) -> None:
-        super().__init__()
-        self.obs_normalizer = _TorchNormalizer(model.obs_normalizer) if model.obs_normalization else nn.Identity()
-        self.mlp = copy.deepcopy(model.mlp).cpu()
-        self.input_size = model.obs_dim
-
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.mlp(self.obs_normalizer(x))
-
-    @torch.jit.export
-    def reset(self) -> None:
-        pass
-
-    def get_dummy_inputs(self) -> tuple[torch.Tensor]:
-        return (torch.zeros(1, self.input_size),)
-
-    @property
-    def input_names(self) -> list[str]:
-        return ["obs"]
-
-    @property
-    def output_names(self) -> list[str]:
-        return ["actions"]
+def _export_parts(model) -> tuple[nn.Module, nn.Module, nn.Module]:
+    """CPU copies of the normaliser, the MLP head and the deterministic output (the distribution's mean)."""
+    norm = _TorchNormalizer(model.obs_normalizer) if model.obs_normalization else nn.Identity()
+    det = model.distribution.as_deterministic_output_module() if model.distribution is not None else nn.Identity()
+    return norm, copy.deepcopy(model.mlp).cpu(), det
 
 
 def _cpu_lstm(model: RNNModel) -> nn.LSTM:
@@ -580,30 +581,37 @@ def _cpu_lstm(model: RNNModel) -> nn.LSTM:
     return lstm
 
 
-class _ExportLSTM(nn.Module):
-    """Deterministic stateful export copy (rsl_rl/models/rnn_model.py:147-175) with plain torch modules."""
+class _TorchMLPModel(nn.Module):
+    """TorchScript export copy, rsl_rl/models/mlp_model.py:196-218: normaliser, MLP, deterministic output."""
 
-    is_recurrent = True
-
-    def __init__(self, model: RNNModel) -> None:
+    def __init__(self, model: MLPModel) -> None:
         super().__init__()
-        self.obs_normalizer = _TorchNormalizer(model.obs_normalizer) if model.obs_normalization else nn.Identity()
-        self.rnn = _cpu_lstm(model)
-        self.mlp = copy.deepcopy(model.mlp).cpu()
-        self.input_size = model.obs_dim
-        self.register_buffer("hidden_state", torch.zeros(1, 1, model.rnn.hidden_size))
-        self.register_buffer("cell_state", torch.zeros(1, 1, model.rnn.hidden_size))
+        self.obs_normalizer, self.mlp, self.deterministic_output = _export_parts(model)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x, (h, c) = self.rnn(self.obs_normalizer(x).unsqueeze(0), (self.hidden_state, self.cell_state))
-        self.hidden_state[:] = h
-        self.cell_state[:] = c
-        return self.mlp(x.squeeze(0))
+        x = self.obs_normalizer(x)
+        out = self.mlp(x)
+        return self.deterministic_output(out)
 
     @torch.jit.export
     def reset(self) -> None:
-        self.hidden_state[:] = 0.0
-        self.cell_state[:] = 0.0
+        pass
+
+
+class _OnnxMLPModel(nn.Module):
+    """ONNX export copy, rsl_rl/models/mlp_model.py:221-255: input "obs", output "actions"."""
+
+    is_recurrent: bool = False
+
+    def __init__(self, model: MLPModel) -> None:
+        super().__init__()
+        self.obs_normalizer, self.mlp, self.deterministic_output = _export_parts(model)
+        self.input_size = model.obs_dim
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = self.obs_normalizer(x)
+        out = self.mlp(x)
+        return self.deterministic_output(out)
 
     def get_dummy_inputs(self) -> tuple[torch.Tensor]:
         return (torch.zeros(1, self.input_size),)
@@ -615,3 +623,107 @@ class _ExportLSTM(nn.Module):
     @property
     def output_names(self) -> list[str]:
         return ["actions"]
+
+
+class _TorchLSTMModel(nn.Module):
+    """TorchScript export copy, rsl_rl/models/rnn_model.py:147-175: one LSTM step per call on a batch-1 state kept in
+    the ``hidden_state`` / ``cell_state`` buffers, ``reset()`` zeroes them."""
+
+    def __init__(self, model: RNNModel) -> None:
+        super().__init__()
+        norm, mlp, det = _export_parts(model)
+        self.obs_normalizer = norm  # upstream's attribute order: normaliser, rnn, mlp, deterministic output
+        self.rnn = _cpu_lstm(model)
+        self.mlp, self.deterministic_output = mlp, det
+        self.register_buffer("hidden_state", torch.zeros(self.rnn.num_layers, 1, self.rnn.hidden_size))
+        self.register_buffer("cell_state", torch.zeros(self.rnn.num_layers, 1, self.rnn.hidden_size))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = self.obs_normalizer(x)
+        x, (h, c) = self.rnn(x.unsqueeze(0), (self.hidden_state, self.cell_state))
+        self.hidden_state[:] = h
+        self.cell_state[:] = c
+        x = x.squeeze(0)
+        out = self.mlp(x)
+        return self.deterministic_output(out)
+
+    @torch.jit.export
+    def reset(self) -> None:
+        self.hidden_state[:] = 0.0
+        self.cell_state[:] = 0.0
+
+
+class _OnnxRNNModel(nn.Module):
+    """ONNX export copy of the LSTM model, rsl_rl/models/rnn_model.py:178-247: the state is an explicit input and
+    output (inputs "obs", "h_in", "c_in"; outputs "actions", "h_out", "c_out")."""
+
+    is_recurrent: bool = True
+
+    def __init__(self, model: RNNModel) -> None:
+        super().__init__()
+        norm, mlp, det = _export_parts(model)
+        self.obs_normalizer = norm
+        self.rnn = _cpu_lstm(model)
+        self.mlp, self.deterministic_output = mlp, det
+        self.rnn_type = "lstm"
+        self.input_size = model.obs_dim
+        self.hidden_size = self.rnn.hidden_size
+        self.num_layers = self.rnn.num_layers
+
+    def forward(self, obs: torch.Tensor, h_in: torch.Tensor, c_in: torch.Tensor):
+        x = self.obs_normalizer(obs)
+        x, (h, c) = self.rnn(x.unsqueeze(0), (h_in, c_in))
+        x = x.squeeze(0)
+        out = self.mlp(x)
+        out = self.deterministic_output(out)
+        return out, h, c
+
+    def get_dummy_inputs(self) -> tuple[torch.Tensor, ...]:
+        obs = torch.zeros(1, self.input_size)
+        h_in = torch.zeros(self.num_layers, 1, self.hidden_size)
+        c_in = torch.zeros(self.num_layers, 1, self.hidden_size)
+        return (obs, h_in, c_in)
+
+    @property
+    def input_names(self) -> list[str]:
+        return ["obs", "h_in", "c_in"]
+
+    @property
+    def output_names(self) -> list[str]:
+        return ["actions", "h_out", "c_out"]
+
+
+class TorchPolicy(nn.Module):
+    """Plain-torch inference copy of a plugin model on a device the HIP kernels do not run on (what
+    ``model.to("cpu")``, and so upstream's ``runner.get_inference_policy("cpu")``, returns: the plugin model itself
+    stays on the GPU, its parameters views of the update's flat buffers).  Upstream's MLPModel / RNNModel forward for
+    observation dicts: concatenated groups -> normaliser -> (LSTM, state carried per env and zeroed by
+    ``reset(dones)``) -> MLP -> the distribution's mean.  A copy: later updates do not reach it."""
+
+    def __init__(self, model, device) -> None:
+        super().__init__()
+        self.obs_groups = list(model.obs_groups)
+        self.is_recurrent = bool(model.is_recurrent)
+        self.obs_normalizer, self.mlp, self.deterministic_output = _export_parts(model)
+        self.rnn = _cpu_lstm(model) if self.is_recurrent else None
+        self.hidden_state = None
+        self.to(device)
+
+    def forward(self, obs: Mapping, masks=None, hidden_state=None, stochastic_output: bool = False) -> torch.Tensor:
+        if stochastic_output or masks is not None:
+            raise NotImplementedError("the inference copy evaluates the deterministic policy on rollout observations")
+        x = self.obs_normalizer(torch.cat([obs[g] for g in self.obs_groups], dim=-1))
+        if self.rnn is not None:
+            x, self.hidden_state = self.rnn(x.unsqueeze(0), self.hidden_state)
+            x = x.squeeze(0)
+        return self.deterministic_output(self.mlp(x))
+
+    def reset(self, dones=None, hidden_state=None) -> None:
+        if dones is None:
+            self.hidden_state = hidden_state
+        elif self.hidden_state is not None:
+            for s in self.hidden_state:
+                s[..., dones == 1, :] = 0.0
+
+    def get_hidden_state(self):
+        return self.hidden_state
