@@ -138,6 +138,70 @@ class RolloutStorage:
                                            old_distribution_params=tuple(p[idx] for p in params))
 
     def recurrent_mini_batch_generator(self, num_mini_batches: int, num_epochs: int = 8):
-        """Not provided: the update evaluates upstream's padded trajectories in the equivalent masked per-env form on
-        the GPU (one sequence per env from saved_hidden_state_*[0], state zeroed after every done)."""
-        raise NotImplementedError("the recurrent update does not materialise padded trajectories")
+        """rollout_storage.py:262-331 (API compatibility; the update itself evaluates the same trajectories in the
+        masked per-env form on the GPU).  Mini-batch i is the env slice [i N / M, (i + 1) N / M), all steps, the same
+        slices every epoch: its observations as trajectories split at the dones and zero-padded to T steps
+        ([T, trajectories, ...], rsl_rl/utils/utils.py:395-449, trajectories in env-major order), the masks of their
+        valid steps, the state each trajectory starts from, and the other fields unpadded [T, envs, ...]."""
+        if not 1 <= num_mini_batches <= self.num_envs:
+            raise ValueError("num_mini_batches must be between 1 and the number of environments.")
+        padded_obs, masks, starts = self._padded_trajectories()
+        starts_env_major = starts.transpose(1, 0)  # [N, T]: which (env, step) begin a trajectory
+        # trajectories of env slice [0, e): every start of those envs (counted env-major)
+        starts_per_env = starts_env_major.sum(dim=1).cumsum(0).tolist()
+
+        def states(saved):
+            if saved is None:
+                return None
+            # [T, layers, N, H] -> the states at the trajectory starts, env-major -> [layers, trajectories, H]
+            picked = [h.permute(2, 0, 1, 3)[starts_env_major] for h in saved]
+            return picked
+
+        sa, sc = states(self.saved_hidden_state_a), states(self.saved_hidden_state_c)
+
+        def select(picked, t0, t1):
+            if picked is None:
+                return None
+            out = [p[t0:t1].transpose(1, 0).contiguous() for p in picked]
+            return out[0] if len(out) == 1 else tuple(out)
+
+        for _ in range(num_epochs):
+            for i in range(num_mini_batches):
+                start = i * self.num_envs // num_mini_batches
+                stop = (i + 1) * self.num_envs // num_mini_batches
+                first = starts_per_env[start - 1] if start > 0 else 0
+                last = starts_per_env[stop - 1]
+                yield RolloutStorage.Batch(
+                    observations={k: v[:, first:last] for k, v in padded_obs.items()},
+                    actions=self.actions[:, start:stop], values=self.values[:, start:stop],
+                    advantages=self.advantages[:, start:stop], returns=self.returns[:, start:stop],
+                    old_actions_log_prob=self.actions_log_prob[:, start:stop],
+                    old_distribution_params=tuple(p[:, start:stop] for p in self.distribution_params),
+                    hidden_states=(select(sa, first, last), select(sc, first, last)),
+                    masks=masks[:, first:last])
+
+    def _padded_trajectories(self):
+        """The observations split into trajectories at the dones (the last step closes every env's last one) and
+        zero-padded to T steps, trajectories in env-major order: [T, trajectories, ...]; the masks of their valid
+        steps [T, trajectories]; and the steps that begin a trajectory [T, N] (step 0 and every step after a done)."""
+        T, N = self.num_transitions_per_env, self.num_envs
+        dones = self.dones[..., 0].bool()
+        starts = torch.zeros_like(dones)
+        starts[0] = True
+        starts[1:] = dones[:-1]
+        # env-major numbering: trajectory id of every (env, step), and the step's position inside its trajectory
+        se = starts.transpose(1, 0)                                  # [N, T]
+        traj = se.reshape(-1).cumsum(0).view(N, T) - 1               # [N, T]
+        steps = torch.arange(T, device=dones.device).expand(N, T)
+        begin = torch.where(se, steps, torch.zeros_like(steps)).cummax(dim=1).values
+        pos = steps - begin                                          # [N, T]
+        count = int(se.sum())
+        masks = torch.zeros(T, count, dtype=torch.bool, device=dones.device)
+        masks[pos.reshape(-1), traj.reshape(-1)] = True
+        padded = {}
+        for k, v in self.observations.items():
+            ve = v.transpose(1, 0).reshape(N * T, *v.shape[2:])
+            out = torch.zeros(T, count, *v.shape[2:], dtype=v.dtype, device=v.device)
+            out[pos.reshape(-1), traj.reshape(-1)] = ve
+            padded[k] = out
+        return padded, masks, starts
