@@ -181,9 +181,10 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
     return out
 
 
-def load_traffic(kernel_phase: str):
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter summary, if present."""
-    p = ROOT / "profiles" / "traffic_humanoid.json"
+def load_traffic(workload_name: str, kernel_phase: str):
+    """HBM bytes per launch of the dominant kernel from the workload's committed rocprofv3 counter summary
+    (profiles/traffic_<workload>.json), else None."""
+    p = ROOT / "profiles" / f"traffic_{workload_name}.json"
     if not p.exists():
         return None
     try:
@@ -203,6 +204,12 @@ def cpu_baseline(workload, reps: int) -> dict:
     ora, roll = R.generate(workload, seed=0)
     with torch.inference_mode():  # as upstream's runner collects (the recurrent states are inference tensors)
         ora.compute_returns(roll.last_obs)
+    B = workload["num_envs"] * workload["steps"]
+    steps_total = ora.num_learning_epochs * ora.num_mini_batches
+    # Bounded sample: above ~100k transitions a whole CPU update takes minutes, so only the first `k` mini-batch
+    # steps (plus the observation-normaliser update) are timed and scaled to the update's steps.
+    k = steps_total if B <= 100_000 else 2
+    ora.max_steps = k if k < steps_total else None
     times = []
     for i in range(reps + 1):
         ora.storage.step = ora.storage.num_transitions_per_env
@@ -211,13 +218,25 @@ def cpu_baseline(workload, reps: int) -> dict:
         ora.update()
         dt = time.perf_counter() - t0
         if i > 0:
-            times.append(dt)
+            times.append(dt * steps_total / k)
     med = statistics.median(times)
-    B = workload["num_envs"] * workload["steps"]
+    scope = ("the whole update" if k == steps_total else
+             f"the first {k} of its {steps_total} mini-batch steps, scaled by {steps_total}/{k}")
     return {"value": B / med, "unit": "samples/s", "cores": threads, "kind": "port",
-            "sample": f"oracle PPO.update (upstream restated in CPU torch) on the same workload, median of {reps} "
-                      f"after 1 warm-up, {threads} torch threads, cpu_count={os.cpu_count()}",
-            "ms_per_update": med * 1e3}
+            "sample": f"oracle PPO.update (upstream restated in CPU torch) on the same workload, {scope}; median of "
+                      f"{reps} after 1 warm-up, {threads} torch threads, cpu_count={os.cpu_count()}",
+            "cpu_model": cpu_model(), "ms_per_update": med * 1e3}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or "unknown"."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 class FenceFreeTimer:
@@ -393,7 +412,7 @@ def main() -> int:
         n, t = timer.summary()[dom]
         ach = flops[dom] / (t * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": load_traffic(dom), "kernel": dom,
+                    "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": load_traffic(args.workload, dom), "kernel": dom,
                     "flops_per_launch": flops[dom], "mean_launch_ms": round(t, 5), "launches_timed": n}
     # compute_returns() (bootstrap critic forward, GAE, advantage normalisation) on the stored rollout, timed after
     # the updates (it rewrites the same returns / advantages each call), as the runner calls it: in inference mode

@@ -138,6 +138,34 @@ def test_linear_fwd_grouped(cuda, rows, aligned_x):
         assert rel_err(h, _elu64(z64)) < 2e-6
 
 
+@pytest.mark.parametrize("rows", [1, 130, 24576 + 77])
+@pytest.mark.parametrize("elu", [True, False])
+def test_linear_fwd_narrow_inputs(cuda, rows, elu):
+    """First-layer shapes: inputs of 33..104 columns with 16-byte aligned rows, widths that are not multiples of the
+    k-slab (the masked tail slab; the input columns past the width hold NaN and must not reach the result), ragged rows
+    and outputs, weights with and without 16-byte rows in one launch.  Checked against fp64."""
+    ops = _ops()
+    torch.manual_seed(rows + 7)
+    shapes = [(33, 200), (48, 512), (99, 130), (104, 96)]
+    probs, refs = [], []
+    for fin, fout in shapes:
+        x = torch.randn(rows, fin)
+        w = torch.randn(fout, fin) / math.sqrt(fin)
+        b = torch.randn(fout)
+        ld = (fin + 3) // 4 * 4 + 8
+        xd = torch.full((rows, ld), float("nan"), device=cuda)  # columns past `fin` must never reach the result
+        xd[:, :fin].copy_(x)
+        z = torch.empty(rows, fout, device=cuda)
+        h = torch.empty(rows, fout, device=cuda) if elu else None
+        probs.append((xd[:, :fin], w.to(cuda), b.to(cuda), z, h))
+        refs.append((z, h, x.double() @ w.double().t() + b.double()))
+    ops.linear_fwd(probs, rows, elu=elu)
+    for z, h, z64 in refs:
+        assert rel_err(z, z64) < 2e-6
+        if elu:
+            assert rel_err(h, _elu64(z64)) < 2e-6
+
+
 @pytest.mark.parametrize("rows,fin,fout,act,from_output", [(24576, 512, 256, True, False), (1000, 128, 29, True, False),
                                                          (333, 256, 1, False, False), (24576, 512, 256, True, True),
                                                          (77, 99, 5, True, True)])
