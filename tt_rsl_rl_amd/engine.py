@@ -29,6 +29,16 @@ def _align4(n: int) -> int:
     return (n + 3) // 4 * 4
 
 
+# The forward GEMM's k-slab is 16 floats: a first layer whose input width is not a multiple of 16 runs on a copy of
+# its weight zero-padded to the next multiple (16-byte loads of both operands, no masked tail slab; measured on
+# MI355X for 24,576 rows x 512 outputs: inputs 96 + 99 86.5 -> 75.5 us, 235 + 235 141 -> 120 us).
+K_SLACK = 16
+
+
+def _pad16(n: int) -> int:
+    return (n + 15) // 16 * 16
+
+
 class TableLayout:
     def __init__(self, actor_dim: int, critic_dim: int, num_actions: int, keep: bool = False) -> None:
         c = 0
@@ -44,7 +54,9 @@ class TableLayout:
         c = _align4(c + num_actions)
         self.old_logp, self.adv, self.old_values, self.returns, self.adv_mb = c, c + 1, c + 2, c + 3, c + 4
         self.keep = c + 5 if keep else None  # recurrent: 1 - done of the row's step
-        self.width = _align4(c + (6 if keep else 5))
+        # + K_SLACK zero columns: the first layers' GEMMs may read up to K_SLACK - 1 columns past an observation
+        # block (against zero weight columns), which must stay inside the row and hold finite values
+        self.width = _align4(c + (6 if keep else 5)) + K_SLACK
 
 
 class ModelBuffers:
@@ -145,7 +157,17 @@ class UpdateEngine:
         actor, critic = alg.actor, alg.critic
         self.A = actor.distribution.output_dim
         self.layout = TableLayout(actor.obs_dim, critic.obs_dim, self.A, keep=self.recurrent)
-        self.table = torch.empty(self.B, self.layout.width, device=self.device)
+        self.table = torch.zeros(self.B, self.layout.width, device=self.device)  # padding columns stay zero
+        # zero-padded copies of first-layer weights whose input width is not a multiple of 16 (refreshed from the
+        # parameters before every mini-batch's forward by a row gather)
+        self.w0_pad: dict[int, torch.Tensor] = {}
+        if not self.recurrent:
+            for model in (actor, critic):
+                w = model.linears[0].weight
+                if w.shape[1] % 16:
+                    self.w0_pad[id(model)] = torch.zeros(w.shape[0], _pad16(w.shape[1]), device=self.device)
+            rows = max((w.shape[0] for w in self.w0_pad.values()), default=0)
+            self.w0_rows = torch.arange(rows, dtype=torch.int64, device=self.device)
         self.buf_a = ModelBuffers(actor, self.R_max, self.device)
         self.buf_c = ModelBuffers(critic, self.R_max, self.device)
         self.loss_ws = torch.empty(ops.loss_workspace_bytes(self.R_max, self.A), dtype=torch.uint8, device=self.device)
@@ -276,6 +298,14 @@ class UpdateEngine:
                  ops.Segment(st.flat(st.returns), lay.returns)]
         return segs
 
+    def refresh_padded_weights(self) -> None:
+        """w0_pad[:, :in] = the first layer's weight (the padding columns were zeroed at allocation)."""
+        for model in (self.alg.actor, self.alg.critic):
+            wp = self.w0_pad.get(id(model))
+            if wp is not None:
+                w = model.linears[0].weight
+                ops.gather_rows(self.w0_rows[:w.shape[0]], [ops.Segment(w, 0)], wp)
+
     def minibatch(self, r0: int, r1: int, step: int) -> None:
         alg, lay = self.alg, self.layout
         R = r1 - r0
@@ -283,7 +313,10 @@ class UpdateEngine:
         xa = tab[:, lay.xa:lay.xa + alg.actor.obs_dim]
         xc = tab[:, lay.xc:lay.xc + alg.critic.obs_dim]
         adv_col = self.advantage_column(tab, R)
-        self.head_forward(xa, xc, R)
+        self.refresh_padded_weights()
+        fa, wa0 = self._first_layer(alg.actor, tab, lay.xa, xa)
+        fc, wc0 = self._first_layer(alg.critic, tab, lay.xc, xc)
+        self.head_forward(fa, fc, R, w0=(wa0, wc0))
         self.loss(tab, R, adv_col)
         self.head_backward(R)
         self.weight_grads(self.head_dw(xa, xc, R), R)
@@ -304,8 +337,9 @@ class UpdateEngine:
             raise NotImplementedError("actor and critic must have the same number of layers")
         return la, lc
 
-    def head_forward(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> None:
-        """The MLPs, actor and critic grouped layer by layer (hidden layers keep only elu(z))."""
+    def head_forward(self, xa: torch.Tensor, xc: torch.Tensor, R: int, w0: tuple | None = None) -> None:
+        """The MLPs, actor and critic grouped layer by layer (hidden layers keep only elu(z)).  w0: the first layer's
+        (actor, critic) weights to use in place of the parameters (zero-padded copies, with inputs as wide)."""
         la, lc = self._layers()
         ba, bc = self.buf_a, self.buf_c
         nl = len(la)
@@ -313,14 +347,23 @@ class UpdateEngine:
         ins_a, ins_c = [xa], [xc]
         for i in range(nl - 1 if self.fused_head else nl):
             last = i == nl - 1
-            probs = [(ins_a[-1], la[i].weight, la[i].bias, ba.out[:R] if last else None, None if last else ba.h[i][:R]),
-                     (ins_c[-1], lc[i].weight, lc[i].bias, bc.out[:R] if last else None, None if last else bc.h[i][:R])]
+            wa, wc = w0 if i == 0 and w0 is not None else (la[i].weight, lc[i].weight)
+            probs = [(ins_a[-1], wa, la[i].bias, ba.out[:R] if last else None, None if last else ba.h[i][:R]),
+                     (ins_c[-1], wc, lc[i].bias, bc.out[:R] if last else None, None if last else bc.h[i][:R])]
             tm.start(f"fwd{i}")
             ops.linear_fwd(probs, R, elu=not last)
             tm.stop(f"fwd{i}")
             if not last:
                 ins_a.append(ba.h[i][:R])
                 ins_c.append(bc.h[i][:R])
+
+    def _first_layer(self, model, tab: torch.Tensor, col: int, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """(input, weight) of the model's first forward GEMM: the padded weight copy and the table block read
+        as wide as it, where the model has one."""
+        wp = self.w0_pad.get(id(model))
+        if wp is None:
+            return x, model.linears[0].weight
+        return tab[:, col:col + wp.shape[1]], wp
 
     def loss(self, tab: torch.Tensor, R: int, adv_col: int) -> None:
         """Losses + per-row output gradients, then the device-side reduction / LR rule / std-parameter gradient.
