@@ -154,7 +154,8 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
         # fused head: last hidden activations in, their gradients out, batch columns in, mean / value and their
         # gradients out
         "head": R * 4 * (2 * (ka + kc) + 3 * A + 4 + 2 * (A + 1)),
-        "adam": alg.flat.param.numel() * 36,                      # norm pass 4 B + p, g, m, v read and written
+        # p, g, m, v read and written (+ a 4 B norm pass without the weight-grad launch's norm partials)
+        "adam": alg.flat.param.numel() * (32 if engine.grad_norm is not None else 36),
         "gae": B * (4 + 4 + 1 + 4 + 4) + 4 * N,                   # r, V, done in; returns, advantages out
     }
     last = torch.randn(N, 1, device=alg.device)
@@ -167,7 +168,8 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
         "gather": graph_ms(lambda: engine.gather(perm)),
         "adam": graph_ms(lambda: ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin,
                                                alg.max_grad_norm, b1, b2, alg.adam_eps, 0.5, 0.5, alg.device_state,
-                                               engine.adam_ws)),
+                                               engine.adam_ws, prenorm=None if engine.grad_norm is None
+                                               else engine.grad_norm.partials)),
     }
     for k in ("loss", "head"):
         if k in phases:
@@ -178,6 +180,18 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
             gbs = b / (ms[k] * 1e-3) / 1e9
             out[k] = {"bytes": b, "mean_us": round(ms[k] * 1e3, 2), "GB/s": round(gbs, 1),
                       "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    # Single-launch floor at these sizes: one plain streaming kernel (torch's elementwise y = x * 1, half the bytes
+    # read, half written) moving the same bytes as the kernel, and an empty launch (one element), both by graph replay
+    empty = torch.ones(1, device=alg.device)
+    out["floor"] = {"empty_launch_us": round(graph_ms(lambda: torch.mul(empty, 1.0, out=empty)) * 1e3, 2)}
+    for k in ("gae", "adam", "gather"):
+        n = max(1, nbytes[k] // 8)
+        x, y = torch.ones(n, device=alg.device), torch.empty(n, device=alg.device)
+        us = graph_ms(lambda: torch.mul(x, 1.0, out=y)) * 1e3
+        gbs = 8 * n / (us * 1e-6) / 1e9
+        out["floor"][k] = {"copy_bytes": 8 * n, "copy_us": round(us, 2), "GB/s": round(gbs, 1),
+                           "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        del x, y
     return out
 
 

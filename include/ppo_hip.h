@@ -161,11 +161,32 @@ typedef struct ppo_linear_bwd_dw_problem {
   float* db;                     /* [out], or NULL: no bias gradient (the column sums are skipped) */
   int32_t in_features;
   int32_t out_features;
+  int32_t grad_norm_group;       /* ppo_linear_bwd_dw_norm: 0 = not counted, g + 1 = dw and db count in group g */
+  int32_t reserved;              /* 0 */
 } ppo_linear_bwd_dw_problem;
 
 size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows);
 int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows, void* workspace,
                       size_t workspace_bytes, ppo_stream_t stream);
+
+/* A contiguous range [begin, end) of a flat gradient buffer that belongs to parameter group `group`. */
+typedef struct ppo_grad_range {
+  int64_t begin, end;
+  int32_t group, reserved;
+} ppo_grad_range;
+
+/* ppo_linear_bwd_dw that also returns the fp64 sums of squares of the gradients it writes, per parameter group
+ * (problems with grad_norm_group g + 1), for ppo_adam_step_prenorm: PPO_DW_NORM_BLOCKS partial rows of
+ * PPO_MAX_PARAM_GROUPS doubles (row-major, every row written) in norm_partials.  The `num_extra` (<= PPO_MAX_EXTRA_GRADS)
+ * ranges of extra_grads -- gradients the launch does not produce but that belong to a group's norm, such as the
+ * distribution's std parameter, written before this call -- are added to the same partial rows.  No counterpart in the
+ * reference (upstream's clip_grad_norm_ reads the gradients once more); the Adam step that follows then needs no pass
+ * over the gradients of its own. */
+#define PPO_DW_NORM_BLOCKS 512
+#define PPO_MAX_EXTRA_GRADS 4
+int ppo_linear_bwd_dw_norm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows, void* workspace,
+                           size_t workspace_bytes, const float* extra_grads, const ppo_grad_range* extra,
+                           int32_t num_extra, double* norm_partials, ppo_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------------
  * A7  Empirical observation normaliser, rsl_rl/modules/normalization.py:46-78.
@@ -335,6 +356,15 @@ int ppo_adam_step(float* params, float* grads, float* exp_avg, float* exp_avg_sq
                   int32_t num_groups, double max_grad_norm, double beta1, double beta2, double eps, double bc1,
                   double bc2_sqrt, ppo_device_state* state, void* workspace, size_t workspace_bytes,
                   ppo_stream_t stream);
+
+/* ppo_adam_step with the group norms from ppo_linear_bwd_dw_norm's partial rows instead of a pass over the gradients
+ * (one launch): total_g^2 = the sum of norm_partials[row][g] over the PPO_DW_NORM_BLOCKS rows in row order.  The
+ * caller guarantees that the partials cover every gradient of every group exactly once (the weight-grad problems plus
+ * the extra ranges); the update itself is ppo_adam_step's. */
+int ppo_adam_step_prenorm(float* params, float* grads, float* exp_avg, float* exp_avg_sq, const int64_t* group_begin,
+                          int32_t num_groups, double max_grad_norm, double beta1, double beta2, double eps,
+                          double bc1, double bc2_sqrt, ppo_device_state* state, const double* norm_partials,
+                          ppo_stream_t stream);
 
 /* ppo_adam_step without a workspace argument: it allocates nothing and takes no caller memory besides its inputs and
  * outputs.  No counterpart in the reference (upstream's torch.optim.Adam allocates as it likes); it is for callers that

@@ -522,6 +522,76 @@ def test_adam_clip_matches_torch(cuda, aligned):
         assert rel_err(grad, ref_g) < 1e-6, "clipped gradients are left in the gradient buffer like upstream"
 
 
+def test_adam_prenorm_matches_torch(cuda):
+    """Clip norms from the weight-grad launch: ppo_linear_bwd_dw_norm writes the gradients of two models' layers
+    (groups 0 and 1) and the per-group sums of squares, plus an extra range (a std parameter written beforehand);
+    the partial rows sum to the gradients' squared norms, and the one-launch Adam on them matches torch's
+    clip_grad_norm_ per model + Adam, with the clip active and inactive."""
+    ops = _ops()
+    from tt_rsl_rl_amd import _lib as L
+
+    torch.manual_seed(12)
+    rows = 1000
+    layers = [[(48, 64), (64, 12)], [(48, 64), (64, 1)]]
+    pad = lambda n: -(-n // 16) * 16  # noqa: E731
+    shapes, offs, groups_of, off = [], [], [], 0
+    std_off = off
+    off += pad(12)
+    bounds = [0]
+    for g, model in enumerate(layers):
+        for i, o in model:
+            for shp in ((o, i), (o,)):
+                shapes.append(shp)
+                offs.append(off)
+                groups_of.append(g)
+                off += pad(torch.Size(shp).numel())
+        bounds.append(off)
+    n = off
+    params = torch.randn(n) * 0.1
+    ref_p = [torch.nn.Parameter(params[std_off:std_off + 12].clone())]
+    ref_p += [torch.nn.Parameter(params[o:o + torch.Size(sh).numel()].view(sh).clone()) for o, sh in zip(offs, shapes)]
+    group0 = [ref_p[0]] + [p for p, g in zip(ref_p[1:], groups_of) if g == 0]
+    group1 = [p for p, g in zip(ref_p[1:], groups_of) if g == 1]
+    opt = torch.optim.Adam(group0 + group1, lr=1e-3)
+    flat = params.to(cuda)
+    grad = torch.zeros(n, device=cuda)
+    m, v = torch.zeros_like(flat), torch.zeros_like(flat)
+    gb = torch.tensor(bounds, dtype=torch.int64)
+    state = ops.new_device_state(1e-3, cuda)
+    partials = ops.grad_norm_partials(cuda)
+    ws = ops.Workspace(cuda)
+    for step in range(1, 7):
+        scale = 10.0 if step % 2 == 0 else 0.001
+        grad[std_off:std_off + 12] = torch.randn(12, device=cuda) * scale
+        probs, k = [], 0
+        for model in layers:
+            for i, o in model:
+                dz, x = torch.randn(rows, o, device=cuda) * scale, torch.randn(rows, i, device=cuda)
+                probs.append((dz, x, grad[offs[k]:offs[k] + o * i].view(o, i), grad[offs[k + 1]:offs[k + 1] + o]))
+                k += 2
+        norm = ops.GradNorm(partials, [0, 0, 1, 1], grad, ((std_off, std_off + 12, 0),))
+        ops.linear_bwd_dw(probs, rows, ws, norm=norm)
+        g64 = grad.double()
+        for g in (0, 1):
+            want = float((g64[bounds[g]:bounds[g + 1]] ** 2).sum())
+            got = float(partials[:, g].sum())
+            assert abs(got - want) <= 1e-12 * want, (step, g, got, want)
+        assert float(partials[:, 2:].abs().sum()) == 0.0
+        for p_, o in zip(ref_p, [std_off] + offs):
+            p_.grad = grad[o:o + p_.numel()].view(p_.shape).cpu().clone()
+        torch.nn.utils.clip_grad_norm_(group0, 1.0)
+        torch.nn.utils.clip_grad_norm_(group1, 1.0)
+        opt.step()
+        ops.reset_device_state(state, 1e-3)
+        ops.adam_step(flat, grad, m, v, gb, 1.0, 0.9, 0.999, 1e-8, 1 - 0.9 ** step, (1 - 0.999 ** step) ** 0.5,
+                      state, None, prenorm=partials)
+        for p_, o in zip(ref_p, [std_off] + offs):
+            got = flat[o:o + p_.numel()].cpu()
+            assert rel_err(got, p_.detach().reshape(-1)) < 1e-6, step
+            assert rel_err(grad[o:o + p_.numel()].cpu(), p_.grad.reshape(-1)) < 1e-6, "clipped gradient kept"
+    assert L.DW_NORM_BLOCKS == partials.shape[0]
+
+
 def test_adam_first_step_moves_by_lr(cuda):
     """tests/algorithms/test_ppo.py:492-505: the first Adam step moves every parameter by lr."""
     ops = _ops()

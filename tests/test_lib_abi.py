@@ -44,7 +44,8 @@ STRUCTS = {
     "ppo_linear_bwd_dx_problem": ("LinearBwdDxProblem", ["dz", "lddz", "w", "z_prev", "ldz_prev", "dz_prev",
                                                          "lddz_prev", "in_features", "out_features"]),
     "ppo_linear_bwd_dw_problem": ("LinearBwdDwProblem", ["dz", "lddz", "x", "ldx", "dw", "db", "in_features",
-                                                         "out_features"]),
+                                                         "out_features", "grad_norm_group", "reserved"]),
+    "ppo_grad_range": ("GradRange", ["begin", "end", "group", "reserved"]),
     "ppo_column_block": ("ColumnBlock", ["src", "stride", "width"]),
     "ppo_loss_args": ("LossArgs", ["rows", "num_actions", "std_type", "mean", "ld_mean", "value", "ld_value",
                                    "actions", "old_mean", "old_std", "old_logp", "advantages", "old_values", "returns",
@@ -67,6 +68,13 @@ STRUCTS = {
 }
 
 
+# the header's size limits and the Python mirror's copies of them
+CONSTANTS = {"PPO_MAX_GATHER_SEGMENTS": "MAX_GATHER_SEGMENTS", "PPO_MAX_LINEAR_PROBLEMS": "MAX_LINEAR_PROBLEMS",
+             "PPO_MAX_PARAM_GROUPS": "MAX_PARAM_GROUPS", "PPO_DW_NORM_BLOCKS": "DW_NORM_BLOCKS",
+             "PPO_MAX_EXTRA_GRADS": "MAX_EXTRA_GRADS", "PPO_ADAM_STATIC_SCRATCH_DOUBLES": "ADAM_STATIC_SCRATCH_DOUBLES",
+             "PPO_ADAM_STATIC_MAX_PARAMS": "ADAM_STATIC_MAX_PARAMS"}
+
+
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
 def test_struct_layouts_match_the_c_compiler(tmp_path):
     from tt_rsl_rl_amd import _lib
@@ -76,6 +84,8 @@ def test_struct_layouts_match_the_c_compiler(tmp_path):
         lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
         for f in fields:
             lines.append(f'  printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    for macro in CONSTANTS:
+        lines.append(f'  printf("{macro} %lld\\n", (long long)({macro}));')
     lines += ["  return 0;", "}"]
     src = tmp_path / "layout.c"
     src.write_text("\n".join(lines))
@@ -90,6 +100,8 @@ def test_struct_layouts_match_the_c_compiler(tmp_path):
         assert got[f"{cname} size"] == ctypes.sizeof(cls), cname
         for f in fields:
             assert got[f"{cname}.{f}"] == getattr(cls, f).offset, f"{cname}.{f}"
+    for macro, pyname in CONSTANTS.items():
+        assert got[macro] == getattr(_lib, pyname), macro
 
 
 def test_argument_validation_reports_errors_without_a_gpu():
@@ -138,6 +150,19 @@ def test_argument_validation_reports_errors_without_a_gpu():
         _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)
     probs = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512)])
     assert lib.ppo_linear_bwd_dw_workspace_bytes(probs, 1, 24576) >= 4 * 512 * 96
+    # the norm-partials variant rejects a group outside [0, PPO_MAX_PARAM_GROUPS] and malformed extra ranges before
+    # any launch, and needs its output buffer
+    bad = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512,
+                                                                       _lib.MAX_PARAM_GROUPS + 1, 0)])
+    with pytest.raises(ValueError, match="grad_norm_group"):
+        _lib.call("ppo_linear_bwd_dw_norm", bad, 1, 24576, 16, 1 << 30, None, None, 0, 16, None)
+    rng = _lib.array(_lib.GradRange, [_lib.GradRange(10, 5, 0, 0)])
+    with pytest.raises(ValueError, match="extra range 0"):
+        _lib.call("ppo_linear_bwd_dw_norm", probs, 1, 24576, 16, 1 << 30, 16, rng, 1, 16, None)
+    with pytest.raises(ValueError, match="norm_partials"):
+        _lib.call("ppo_linear_bwd_dw_norm", probs, 1, 24576, 16, 1 << 30, None, None, 0, None, None)
+    with pytest.raises(ValueError, match="norm_partials"):
+        _lib.call("ppo_adam_step_prenorm", 16, 16, 16, 16, None, 1, 1.0, 0.9, 0.999, 1e-8, 0.1, 0.1, 16, None, None)
     # the fused output-layer head: its shape rule, and the rejection of shapes outside it before any pointer is used
     assert lib.ppo_gauss_ppo_head_supported(29, 128, 128) == 1
     assert lib.ppo_gauss_ppo_head_supported(1, 16, 16) == 1

@@ -28,6 +28,8 @@ MAX_GATHER_SEGMENTS = 16
 MAX_LINEAR_PROBLEMS = 8
 MAX_PARAM_GROUPS = 4
 MAX_ACTIONS = 64
+DW_NORM_BLOCKS = 512
+MAX_EXTRA_GRADS = 4
 ADAM_STATIC_SCRATCH_DOUBLES = 8192
 ADAM_STATIC_MAX_PARAMS = (ADAM_STATIC_SCRATCH_DOUBLES - MAX_PARAM_GROUPS) * 1024
 
@@ -57,7 +59,12 @@ class LinearBwdDxProblem(C.Structure):
 
 class LinearBwdDwProblem(C.Structure):
     _fields_ = [("dz", C.c_void_p), ("lddz", i64), ("x", C.c_void_p), ("ldx", i64), ("dw", C.c_void_p),
-                ("db", C.c_void_p), ("in_features", i32), ("out_features", i32)]
+                ("db", C.c_void_p), ("in_features", i32), ("out_features", i32), ("grad_norm_group", i32),
+                ("reserved", i32)]
+
+
+class GradRange(C.Structure):
+    _fields_ = [("begin", i64), ("end", i64), ("group", i32), ("reserved", i32)]
 
 
 class ColumnBlock(C.Structure):
@@ -134,6 +141,8 @@ _SIGNATURES = [
                                     C.c_void_p]),
     ("ppo_linear_bwd_dw_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDwProblem), i32, i64]),
     ("ppo_linear_bwd_dw", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("ppo_linear_bwd_dw_norm", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, f32p,
+                                         C.POINTER(GradRange), i32, C.c_void_p, C.c_void_p]),
     ("ppo_obs_normalize", C.c_int, [f32p, i64, f32p, i64, i64, i32, f32p, f32p, C.c_float, C.c_void_p]),
     ("ppo_normalizer_update_workspace_bytes", C.c_size_t, [i64, i32]),
     ("ppo_normalizer_update", C.c_int, [C.POINTER(ColumnBlock), i32, i64, f32p, f32p, f32p, C.c_void_p, C.c_void_p,
@@ -157,10 +166,13 @@ _SIGNATURES = [
                                 C.c_void_p]),
     ("ppo_adam_step_static", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double,
                                        C.c_double, C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p]),
+    ("ppo_adam_step_prenorm", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double,
+                                        C.c_double, C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p,
+                                        C.c_void_p]),
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib: C.CDLL | None = None
 

@@ -32,6 +32,10 @@ namespace {
 // Fixed-order reduction of split-K weight-grad partials: dw = sum_s partial[s], db = sum_s colsum[s].  A work item
 // is 4 consecutive columns of one output row (the partials' rows are padded to ld = round4(in), so the loads are
 // float4), summed split after split (every element in the same order as a scalar loop), then the bias entries.
+//
+// With a norm buffer (ppo_linear_bwd_dw_norm) the launch has exactly PPO_DW_NORM_BLOCKS blocks and every block also
+// writes one row of PPO_MAX_PARAM_GROUPS fp64 partial sums of squares of the values it stored (its items in order,
+// then a fixed-order block reduction), block 0 adding the squares of the caller's extra gradient ranges.
 struct ReduceItem {
   const float* partial;  // [splits, out, ld]
   const double* colsum;  // [splits, out]
@@ -40,16 +44,31 @@ struct ReduceItem {
   int64_t begin;         // first work item of this problem in the launch
   int64_t stride;        // floats between splits
   int32_t out, in, ld, splits;
+  int32_t group;         // 0: not in a norm, g + 1: parameter group g
 };
 struct ReduceGroup {
   ReduceItem it[PPO_MAX_LINEAR_PROBLEMS];
   int32_t count;
   int64_t total;
+  double* norm;  // [PPO_DW_NORM_BLOCKS][PPO_MAX_PARAM_GROUPS] or null
+  const float* extra_grads;
+  ppo_grad_range extra[PPO_MAX_EXTRA_GRADS];
+  int32_t num_extra;
 };
 
 constexpr int kReduceBatch = 8;
 
+// Adds x to the accumulator of group `group` (1-based; 0 adds nothing) with static register indexing.
+__device__ __forceinline__ void add_sq(double (&sq)[PPO_MAX_PARAM_GROUPS], int group, double x) {
+#pragma unroll
+  for (int k = 0; k < PPO_MAX_PARAM_GROUPS; ++k)
+    if (group == k + 1) sq[k] += x;
+}
+
 __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
+  double sq[PPO_MAX_PARAM_GROUPS];
+#pragma unroll
+  for (int k = 0; k < PPO_MAX_PARAM_GROUPS; ++k) sq[k] = 0.0;
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < g.total;
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     int pi = 0;
@@ -78,9 +97,14 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
           }
       }
       float* out = R.dw + static_cast<int64_t>(o) * R.in + i;
+      double s2 = 0.0;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        if (i + c < R.in) out[c] = acc[c];
+        if (i + c < R.in) {
+          out[c] = acc[c];
+          s2 += static_cast<double>(acc[c]) * acc[c];
+        }
+      add_sq(sq, R.group, s2);
     } else {
       const int o = local - R.out * q4;
       double acc = 0.0;
@@ -93,8 +117,31 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
         for (int j = 0; j < kReduceBatch; ++j)
           if (k0 + j < R.splits) acc += v[j];
       }
-      R.db[o] = static_cast<float>(acc);
+      const float b = static_cast<float>(acc);
+      R.db[o] = b;
+      add_sq(sq, R.group, static_cast<double>(b) * b);
     }
+  }
+  if (g.norm == nullptr) return;
+  if (blockIdx.x == 0) {
+    for (int r = 0; r < g.num_extra; ++r)
+      for (int64_t e = g.extra[r].begin + threadIdx.x; e < g.extra[r].end; e += blockDim.x) {
+        const double x = g.extra_grads[e];
+        add_sq(sq, g.extra[r].group + 1, x * x);
+      }
+  }
+  __shared__ double red[256 / 64][PPO_MAX_PARAM_GROUPS];
+#pragma unroll
+  for (int k = 0; k < PPO_MAX_PARAM_GROUPS; ++k) {
+    double x = sq[k];
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_down(x, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][k] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x < PPO_MAX_PARAM_GROUPS) {
+    double x = 0.0;
+    for (int w = 0; w < 256 / 64; ++w) x += red[w][threadIdx.x];
+    g.norm[static_cast<int64_t>(blockIdx.x) * PPO_MAX_PARAM_GROUPS + threadIdx.x] = x;
   }
 }
 
@@ -356,8 +403,12 @@ extern "C" size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_prob
   return plan_dw(problems, count, rows, dw_query_capacity()).total_floats * sizeof(float);
 }
 
-extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows,
-                                 void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
+namespace ppo {
+namespace {
+
+int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows, void* workspace,
+            size_t workspace_bytes, const float* extra_grads, const ppo_grad_range* extra, int32_t num_extra,
+            double* norm, ppo_stream_t stream) {
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS,
               "ppo_linear_bwd_dw: count=%d outside [1, %d]", count, PPO_MAX_LINEAR_PROBLEMS);
   PPO_REQUIRE(rows_ok(rows), "ppo_linear_bwd_dw: rows=%lld", (long long)rows);
@@ -368,7 +419,17 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     PPO_REQUIRE(q.lddz >= q.out_features && q.ldx >= q.in_features, "ppo_linear_bwd_dw: problem %d leading dims", i);
     PPO_REQUIRE(static_cast<int64_t>(q.out_features) * (round4(q.in_features) + 4) < (int64_t(1) << 31),
                 "ppo_linear_bwd_dw: problem %d: weight of %d x %d is too large", i, q.out_features, q.in_features);
+    PPO_REQUIRE(q.grad_norm_group >= 0 && q.grad_norm_group <= PPO_MAX_PARAM_GROUPS,
+                "ppo_linear_bwd_dw: problem %d: grad_norm_group %d outside [0, %d]", i, q.grad_norm_group,
+                PPO_MAX_PARAM_GROUPS);
   }
+  PPO_REQUIRE(num_extra >= 0 && num_extra <= PPO_MAX_EXTRA_GRADS && (num_extra == 0 || (extra && extra_grads)),
+              "ppo_linear_bwd_dw_norm: %d extra gradient ranges (at most %d, with their buffer)", num_extra,
+              PPO_MAX_EXTRA_GRADS);
+  for (int r = 0; r < num_extra; ++r)
+    PPO_REQUIRE(extra[r].begin >= 0 && extra[r].end >= extra[r].begin && extra[r].group >= 0 &&
+                    extra[r].group < PPO_MAX_PARAM_GROUPS,
+                "ppo_linear_bwd_dw_norm: extra range %d malformed", r);
   const DwPlan plan = plan_dw(problems, count, rows, dw_launch_capacity());
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total_floats * sizeof(float),
               "ppo_linear_bwd_dw: workspace too small (%zu < %zu)", workspace_bytes,
@@ -393,12 +454,17 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
     r.partial = p.C; r.colsum = p.colsum; r.dw = q.dw; r.db = q.db;
     r.out = q.out_features; r.in = q.in_features; r.ld = static_cast<int>(ldp); r.splits = plan.splits[i];
     r.stride = p.partial_stride;
+    r.group = norm != nullptr ? q.grad_norm_group : 0;
     r.begin = total;
     total += static_cast<int64_t>(q.out_features) * (ldp / 4 + (q.db != nullptr ? 1 : 0));
   }
   for (int i = count; i < PPO_MAX_LINEAR_PROBLEMS; ++i) rg.it[i].begin = INT64_MAX;
   rg.count = count;
   rg.total = total;
+  rg.norm = norm;
+  rg.extra_grads = extra_grads;
+  for (int r = 0; r < num_extra; ++r) rg.extra[r] = extra[r];
+  rg.num_extra = num_extra;
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc;
 #ifdef PPO_HIP_TUNING
@@ -418,7 +484,24 @@ extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int3
   rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
 #endif
   if (rc != PPO_OK) return rc;
-  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 4096);
+  const int64_t blocks = norm != nullptr ? PPO_DW_NORM_BLOCKS : std::min<int64_t>(ceil_div(total, 256), 4096);
   hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);
   return check_launch("dw_reduce_kernel");
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_linear_bwd_dw(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows,
+                                 void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
+  return dw_gemm(problems, count, rows, workspace, workspace_bytes, nullptr, nullptr, 0, nullptr, stream);
+}
+
+extern "C" int ppo_linear_bwd_dw_norm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows,
+                                      void* workspace, size_t workspace_bytes, const float* extra_grads,
+                                      const ppo_grad_range* extra, int32_t num_extra, double* norm_partials,
+                                      ppo_stream_t stream) {
+  PPO_REQUIRE(norm_partials != nullptr, "ppo_linear_bwd_dw_norm: null norm_partials");
+  return dw_gemm(problems, count, rows, workspace, workspace_bytes, extra_grads, extra, num_extra, norm_partials,
+                 stream);
 }

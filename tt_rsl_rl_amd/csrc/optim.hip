@@ -1,10 +1,12 @@
 // A12 + A13: per-group gradient-norm clipping (torch.nn.utils.clip_grad_norm_, rsl_rl/algorithms/ppo.py:309-310)
 // fused with Adam (torch.optim.Adam, single-tensor path, ppo.py:311) over flat parameter / gradient / moment
-// buffers.  Two launches:
+// buffers.  ppo_adam_step, two launches:
 //   1. sum of squares of the gradient, one fp64 partial per 1024-element chunk (chunks never straddle groups);
 //   2. every block re-reduces its group's partials in the same fixed order (so all blocks agree bit for bit),
 //      derives the clip coefficient and streams p, g, m, v once: 16 B read + 12 B written per parameter
 //      (+4 B rewriting the clipped gradient, which upstream leaves in .grad).
+// ppo_adam_step_prenorm is launch 2 alone, on the per-group partial rows that the weight-grad reduce wrote while it
+// stored the gradients (ppo_linear_bwd_dw_norm).
 // The element update follows torch's fp32 operation order with contraction disabled.
 #include <mutex>
 
@@ -93,7 +95,9 @@ __device__ __forceinline__ void adam_elem(float& p, float& g, float& m, float& v
   p = p + (neg_step * m) / denom;
 }
 
-template <bool VEC>
+// PRE: the group's squared norm is the sum of column g of the PPO_DW_NORM_BLOCKS partial rows the weight-grad reduce
+// wrote (ppo_adam_step_prenorm); else the sum of the group's per-chunk partials from grad_sqnorm_kernel.
+template <bool VEC, bool PRE>
 __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ params, float* __restrict__ grads,
                                                             float* __restrict__ exp_avg,
                                                             float* __restrict__ exp_avg_sq, GroupTable t,
@@ -103,7 +107,11 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
   const int chunk = blockIdx.x;
   const int g = group_of_chunk(t, chunk);
   double acc = 0.0;
-  for (int c = t.first_chunk[g] + threadIdx.x; c < t.first_chunk[g + 1]; c += kAdamThreads) acc += partials[c];
+  if constexpr (PRE) {
+    for (int r = threadIdx.x; r < PPO_DW_NORM_BLOCKS; r += kAdamThreads) acc += partials[r * PPO_MAX_PARAM_GROUPS + g];
+  } else {
+    for (int c = t.first_chunk[g] + threadIdx.x; c < t.first_chunk[g + 1]; c += kAdamThreads) acc += partials[c];
+  }
   const double sq = block_sum256(acc, red);
   const float total = static_cast<float>(sqrt(sq));
   const float coef = fminf(s.max_norm / (total + 1e-6f), 1.0f);
@@ -189,18 +197,22 @@ int static_scratch(double** out) {
   return PPO_OK;
 }
 
+// prenorm != nullptr: one launch taking the norms from the weight-grad reduce's partial rows; else the per-chunk
+// norm pass into `workspace`, then the update.
 int adam_step(const char* who, float* params, float* grads, float* exp_avg, float* exp_avg_sq,
               const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1, double beta2,
               double eps, double bc1, double bc2_sqrt, ppo_device_state* state, void* workspace,
-              size_t workspace_bytes, ppo_stream_t stream) {
+              size_t workspace_bytes, const double* prenorm, ppo_stream_t stream) {
   PPO_REQUIRE(params && grads && exp_avg && exp_avg_sq && state, "%s: null pointer", who);
   GroupTable t;
   int chunks = 0;
   int rc = build_table(group_begin, num_groups, t, chunks);
   if (rc != PPO_OK) return rc;
-  const size_t need = workspace_bytes_for(group_begin[num_groups]);
-  PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", who,
-              workspace_bytes, need);
+  if (prenorm == nullptr) {
+    const size_t need = workspace_bytes_for(group_begin[num_groups]);
+    PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", who,
+                workspace_bytes, need);
+  }
   PPO_REQUIRE(bc1 > 0.0 && bc2_sqrt > 0.0, "%s: bias corrections must be positive", who);
   AdamScalars s;
   // torch passes max_norm, 1 - beta1, beta2, 1 - beta2 and eps as Python doubles that the fp32 kernels round once
@@ -211,12 +223,22 @@ int adam_step(const char* who, float* params, float* grads, float* exp_avg, floa
   s.eps = static_cast<float>(eps);
   s.bc1 = bc1;
   s.bc2_sqrt = static_cast<float>(bc2_sqrt);
-  double* partials = static_cast<double*>(workspace);
   hipStream_t st = static_cast<hipStream_t>(stream);
   bool vec = true;
   const void* bufs[] = {params, grads, exp_avg, exp_avg_sq};
   for (const void* b : bufs) vec = vec && reinterpret_cast<uintptr_t>(b) % 16 == 0;
   for (int g = 0; g <= num_groups; ++g) vec = vec && group_begin[g] % 4 == 0;
+  if (prenorm != nullptr) {
+    if (vec) {
+      hipLaunchKernelGGL((adam_kernel<true, true>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
+                         exp_avg_sq, t, s, prenorm, state);
+    } else {
+      hipLaunchKernelGGL((adam_kernel<false, true>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads,
+                         exp_avg, exp_avg_sq, t, s, prenorm, state);
+    }
+    return check_launch("adam_kernel");
+  }
+  double* partials = static_cast<double*>(workspace);
   if (vec) {
     hipLaunchKernelGGL(grad_sqnorm_kernel<true>, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, partials);
   } else {
@@ -225,11 +247,11 @@ int adam_step(const char* who, float* params, float* grads, float* exp_avg, floa
   rc = check_launch("grad_sqnorm_kernel");
   if (rc != PPO_OK) return rc;
   if (vec) {
-    hipLaunchKernelGGL(adam_kernel<true>, dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg, exp_avg_sq,
-                       t, s, partials, state);
-  } else {
-    hipLaunchKernelGGL(adam_kernel<false>, dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
+    hipLaunchKernelGGL((adam_kernel<true, false>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
                        exp_avg_sq, t, s, partials, state);
+  } else {
+    hipLaunchKernelGGL((adam_kernel<false, false>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads,
+                       exp_avg, exp_avg_sq, t, s, partials, state);
   }
   return check_launch("adam_kernel");
 }
@@ -246,7 +268,16 @@ extern "C" int ppo_adam_step(float* params, float* grads, float* exp_avg, float*
                              double beta2, double eps, double bc1, double bc2_sqrt, ppo_device_state* state,
                              void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
   return adam_step("ppo_adam_step", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups, max_grad_norm,
-                   beta1, beta2, eps, bc1, bc2_sqrt, state, workspace, workspace_bytes, stream);
+                   beta1, beta2, eps, bc1, bc2_sqrt, state, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int ppo_adam_step_prenorm(float* params, float* grads, float* exp_avg, float* exp_avg_sq,
+                                     const int64_t* group_begin, int32_t num_groups, double max_grad_norm,
+                                     double beta1, double beta2, double eps, double bc1, double bc2_sqrt,
+                                     ppo_device_state* state, const double* norm_partials, ppo_stream_t stream) {
+  PPO_REQUIRE(norm_partials != nullptr, "ppo_adam_step_prenorm: null norm_partials");
+  return adam_step("ppo_adam_step_prenorm", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups,
+                   max_grad_norm, beta1, beta2, eps, bc1, bc2_sqrt, state, nullptr, 0, norm_partials, stream);
 }
 
 // The same kernels on the static scratch: the parameter count is checked against the array's capacity before any
@@ -267,5 +298,5 @@ extern "C" int ppo_adam_step_static(float* params, float* grads, float* exp_avg,
   if (int rc = static_scratch(&ws)) return rc;
   return adam_step("ppo_adam_step_static", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups,
                    max_grad_norm, beta1, beta2, eps, bc1, bc2_sqrt, state, ws,
-                   sizeof(double) * PPO_ADAM_STATIC_SCRATCH_DOUBLES, stream);
+                   sizeof(double) * PPO_ADAM_STATIC_SCRATCH_DOUBLES, nullptr, stream);
 }

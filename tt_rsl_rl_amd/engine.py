@@ -168,6 +168,7 @@ class UpdateEngine:
                     self.w0_pad[id(model)] = torch.zeros(w.shape[0], _pad16(w.shape[1]), device=self.device)
             rows = max((w.shape[0] for w in self.w0_pad.values()), default=0)
             self.w0_rows = torch.arange(rows, dtype=torch.int64, device=self.device)
+        self.grad_norm = None if self.recurrent else self._grad_norm_plan()
         self.buf_a = ModelBuffers(actor, self.R_max, self.device)
         self.buf_c = ModelBuffers(critic, self.R_max, self.device)
         self.loss_ws = torch.empty(ops.loss_workspace_bytes(self.R_max, self.A), dtype=torch.uint8, device=self.device)
@@ -263,7 +264,7 @@ class UpdateEngine:
                 self.timer.stop(e[1])
             else:
                 name, args = e
-                if name == "ppo_adam_step":
+                if name in ("ppo_adam_step", "ppo_adam_step_prenorm"):
                     bc1, bc2_sqrt = self._bias_corrections(step)
                     args = args[:10] + (float(bc1), float(bc2_sqrt)) + args[12:]
                 L.check(getattr(lib, name)(*args), name)
@@ -319,8 +320,8 @@ class UpdateEngine:
         self.head_forward(fa, fc, R, w0=(wa0, wc0))
         self.loss(tab, R, adv_col)
         self.head_backward(R)
-        self.weight_grads(self.head_dw(xa, xc, R), R)
-        self.adam(step)
+        self.weight_grads(self.head_dw(xa, xc, R), R, norm=self.grad_norm)
+        self.adam(step, prenorm=self.grad_norm.partials if self.grad_norm is not None else None)
 
     # -- pieces shared with the recurrent engine ----------------------------------------------------------------------
     def advantage_column(self, tab: torch.Tensor, R: int) -> int:
@@ -356,6 +357,27 @@ class UpdateEngine:
             if not last:
                 ins_a.append(ba.h[i][:R])
                 ins_c.append(bc.h[i][:R])
+
+    def _grad_norm_plan(self) -> ops.GradNorm | None:
+        """The clip norms from the weight-grad launch (ppo_linear_bwd_dw_norm + ppo_adam_step_prenorm, one Adam launch
+        instead of two), when that launch writes every linear layer's gradients and the few other gradients (the
+        distribution's std parameter) fit as extra ranges; else None (ppo_adam_step computes the norms itself)."""
+        f = self.alg.flat
+        la, lc = self._layers()
+        linear = {id(p) for lin in (*la, *lc) for p in (lin.weight, lin.bias)}
+        if 2 * len(la) > L.MAX_LINEAR_PROBLEMS or any(lin.bias is None for lin in (*la, *lc)):
+            return None
+        bounds = f.group_begin.tolist()
+        group = lambda off: max(i for i in range(len(bounds) - 1) if bounds[i] <= off)  # noqa: E731
+        extra = []
+        for p in f.params:
+            if id(p) not in linear:
+                off, k = f.offsets[id(p)]
+                extra.append((off, off + k, group(off)))
+        if len(extra) > L.MAX_EXTRA_GRADS or len(bounds) - 1 > L.MAX_PARAM_GROUPS:
+            return None
+        groups = [group(f.offsets[id(lin.weight)][0]) for lin in la] + [group(f.offsets[id(lin.weight)][0]) for lin in lc]
+        return ops.GradNorm(ops.grad_norm_partials(self.device), groups, f.grad, tuple(extra))
 
     def _first_layer(self, model, tab: torch.Tensor, col: int, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """(input, weight) of the model's first forward GEMM: the padded weight copy and the table block read
@@ -423,12 +445,19 @@ class UpdateEngine:
                 dw.append((buf.dz[i][:R], x, grad(lins[i].weight), grad(lins[i].bias)))
         return dw
 
-    def weight_grads(self, dw: list[tuple], R: int, phase: str = "dw", ws: ops.Workspace | None = None) -> None:
-        """Weight gradients, as few grouped launches as the problem limit allows."""
+    def weight_grads(self, dw: list[tuple], R: int, phase: str = "dw", ws: ops.Workspace | None = None,
+                     norm: ops.GradNorm | None = None) -> None:
+        """Weight gradients, as few grouped launches as the problem limit allows (with `norm`: one launch that also
+        sums the squares for the clip norms)."""
         tm = self.timer
         tm.start(phase)
-        for i in range(0, len(dw), L.MAX_LINEAR_PROBLEMS):
-            ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, ws if ws is not None else self.dw_ws)
+        if norm is not None:
+            if len(dw) > L.MAX_LINEAR_PROBLEMS:
+                raise RuntimeError("weight_grads: the norm partials need all problems in one launch")
+            ops.linear_bwd_dw(dw, R, ws if ws is not None else self.dw_ws, norm=norm)
+        else:
+            for i in range(0, len(dw), L.MAX_LINEAR_PROBLEMS):
+                ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, ws if ws is not None else self.dw_ws)
         tm.stop(phase)
 
     def _bias_corrections(self, step: int) -> tuple[float, float]:
@@ -436,8 +465,9 @@ class UpdateEngine:
         b1, b2 = self.alg.betas
         return 1 - b1 ** step, (1 - b2 ** step) ** 0.5
 
-    def adam(self, step: int) -> None:
-        """Per-model clip + Adam over the flat buffers."""
+    def adam(self, step: int, prenorm: torch.Tensor | None = None) -> None:
+        """Per-model clip + Adam over the flat buffers (prenorm: the norm partials of this mini-batch's weight-grad
+        launch)."""
         alg = self.alg
         b1, b2 = alg.betas
         bc1, bc2_sqrt = self._bias_corrections(step)
@@ -445,7 +475,7 @@ class UpdateEngine:
         tm = self.timer
         tm.start("adam")
         ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin, alg.max_grad_norm, b1, b2, alg.adam_eps,
-                      bc1, bc2_sqrt, alg.device_state, self.adam_ws)
+                      bc1, bc2_sqrt, alg.device_state, self.adam_ws, prenorm=prenorm)
         tm.stop("adam")
 
     def minibatch_rows(self, i: int) -> tuple[int, int]:

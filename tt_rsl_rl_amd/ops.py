@@ -339,23 +339,57 @@ def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None,
     L.call("ppo_linear_bwd_dx", arr, count, rows, src, buf.data_ptr(), buf.numel(), _stream())
 
 
-def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None) -> None:
-    """problems: (dz [rows, out], x [rows, in], dw [out, in], db [out] or None for no bias gradient)."""
+@dataclass
+class GradNorm:
+    """Per-group sums of squares of the gradients a weight-grad launch writes, for adam_step(prenorm=...):
+    `partials` [DW_NORM_BLOCKS, MAX_PARAM_GROUPS] fp64; `groups[i]` = the parameter group of problem i (None: not
+    counted); `extra` = (begin, end, group) ranges of `extra_grads` (a flat fp32 buffer) that belong to a group's
+    norm but are written by another launch."""
+    partials: torch.Tensor
+    groups: list
+    extra_grads: torch.Tensor | None = None
+    extra: tuple = ()
+
+
+def grad_norm_partials(device) -> torch.Tensor:
+    return torch.zeros(L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS, dtype=torch.float64, device=device)
+
+
+def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None, norm: GradNorm | None = None) -> None:
+    """problems: (dz [rows, out], x [rows, in], dw [out, in], db [out] or None for no bias gradient).  With `norm`
+    the launch also writes the per-group sums of squares of what it stores (ppo_linear_bwd_dw_norm)."""
     items = []
-    for dz, x, dw, db in problems:
+    for i, (dz, x, dw, db) in enumerate(problems):
         _dev(dz, x, dw, db)
         out_f, in_f = _check_weight(dw, db)
         lddz, ldx = _row_major(dz, "dz"), _row_major(x, "x")
         if dz.shape[0] < rows or x.shape[0] < rows or dz.shape[1] < out_f or x.shape[1] < in_f:
             raise ValueError("linear_bwd_dw: buffers too small")
+        group = 0
+        if norm is not None and norm.groups[i] is not None:
+            group = int(norm.groups[i]) + 1
         items.append(L.LinearBwdDwProblem(dz.data_ptr(), lddz, x.data_ptr(), ldx, dw.data_ptr(), _ptr(db), in_f,
-                                          out_f))
+                                          out_f, group, 0))
     arr = L.array(L.LinearBwdDwProblem, items)
     nbytes = L.load().ppo_linear_bwd_dw_workspace_bytes(arr, len(items), rows)
     if nbytes == 0:
         raise ValueError("linear_bwd_dw: invalid problem set")
     buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
-    L.call("ppo_linear_bwd_dw", arr, len(items), rows, buf.data_ptr(), buf.numel(), _stream())
+    if norm is None:
+        L.call("ppo_linear_bwd_dw", arr, len(items), rows, buf.data_ptr(), buf.numel(), _stream())
+        return
+    p = norm.partials
+    _dev(p, dtype=torch.float64)
+    if tuple(p.shape) != (L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS) or not p.is_contiguous():
+        raise ValueError("linear_bwd_dw: norm partials must be a contiguous [DW_NORM_BLOCKS, MAX_PARAM_GROUPS] fp64")
+    extra = [L.GradRange(int(b), int(e), int(g), 0) for b, e, g in norm.extra]
+    if extra:
+        _dev(norm.extra_grads)
+        if any(r.begin < 0 or r.end > norm.extra_grads.numel() for r in extra):
+            raise ValueError("linear_bwd_dw: extra gradient range outside its buffer")
+    L.call("ppo_linear_bwd_dw_norm", arr, len(items), rows, buf.data_ptr(), buf.numel(),
+           _ptr(norm.extra_grads) if extra else None, L.array(L.GradRange, extra) if extra else None, len(extra),
+           p.data_ptr(), _stream())
 
 
 # ----------------------------------------------------------------------------------------------------------------------
@@ -515,7 +549,10 @@ def ppo_head(args: L.LossArgs, h_actor: torch.Tensor, w_actor: torch.Tensor, b_a
 
 
 def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max_grad_norm: float, beta1: float,
-              beta2: float, eps: float, bc1: float, bc2_sqrt: float, state: torch.Tensor, ws: Workspace) -> None:
+              beta2: float, eps: float, bc1: float, bc2_sqrt: float, state: torch.Tensor, ws: Workspace | None,
+              prenorm: torch.Tensor | None = None) -> None:
+    """Clip + Adam over the flat buffers.  prenorm: the GradNorm partials of the weight-grad launch that wrote every
+    gradient of every group (ppo_adam_step_prenorm, one launch); else the norms are computed here (two launches)."""
     _dev(params, grads, exp_avg, exp_avg_sq)
     n = params.numel()
     for t in (grads, exp_avg, exp_avg_sq):
@@ -526,6 +563,15 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max
     groups = group_begin.numel() - 1
     if int(group_begin[-1]) != n:
         raise ValueError("adam_step: the groups must cover the flat buffer")
+    if prenorm is not None:
+        _dev(prenorm, dtype=torch.float64)
+        if tuple(prenorm.shape) != (L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS) or not prenorm.is_contiguous():
+            raise ValueError("adam_step: prenorm must be a contiguous [DW_NORM_BLOCKS, MAX_PARAM_GROUPS] fp64 tensor")
+        L.call("ppo_adam_step_prenorm", params.data_ptr(), grads.data_ptr(), exp_avg.data_ptr(),
+               exp_avg_sq.data_ptr(), group_begin.data_ptr(), groups, float(max_grad_norm), float(beta1),
+               float(beta2), float(eps), float(bc1), float(bc2_sqrt), state.data_ptr(), prenorm.data_ptr(),
+               _stream())
+        return
     nbytes = L.load().ppo_adam_workspace_bytes(n)
     buf = ws.get(nbytes)
     L.call("ppo_adam_step", params.data_ptr(), grads.data_ptr(), exp_avg.data_ptr(), exp_avg_sq.data_ptr(),
