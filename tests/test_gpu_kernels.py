@@ -188,6 +188,52 @@ def test_linear_bwd_dx(cuda, rows, fin, fout, act, from_output):
     assert rel_err(out, ref) < 2e-6
 
 
+@pytest.mark.parametrize("elu", [True, False])
+def test_linear_persistent_walks_several_tiles(cuda, elu):
+    """The persistent forward / input-grad launches (16-byte operands, k a multiple of 16): 100,003 rows give each
+    resident block several tiles, the last row tile ragged; grouped problems with different k (96, 112, 48) and
+    output widths (512, 12) stream their k-slabs across tile boundaries.  Output rows and columns past the problem
+    (a NaN sentinel) must stay untouched: the epilogue's dropped stores land nowhere."""
+    ops = _ops()
+    torch.manual_seed(41 + elu)
+    rows = 100_003
+    shapes = [(96, 512), (112, 512), (48, 12)]
+    table = torch.randn(rows, 272, device=cuda)  # inputs: column blocks of one row-major table
+    probs, refs, col = [], [], 0
+    for fin, fout in shapes:
+        xv = table[:, col:col + fin]
+        col += fin
+        w = torch.randn(fout, fin, device=cuda) / math.sqrt(fin)
+        b = torch.randn(fout, device=cuda)
+        z = torch.full((rows + 3, fout + 4), float("nan"), device=cuda)
+        h = torch.full((rows + 3, fout + 4), float("nan"), device=cuda) if elu else None
+        probs.append((xv, w, b, z[:rows, :fout], None if h is None else h[:rows, :fout]))
+        refs.append((z, h, xv.double() @ w.double().t() + b.double(), fout))
+    ops.linear_fwd(probs, rows, elu=elu)
+    for z, h, z64, fout in refs:
+        for out, want in ((z, z64), (h, None if h is None else _elu64(z64))):
+            if out is None:
+                continue
+            assert rel_err(out[:rows, :fout], want) < 2e-6
+            assert torch.isnan(out[rows:]).all() and torch.isnan(out[:, fout:]).all(), "store outside the output"
+    # input-grads of two layers in one launch, ELU' from the layer's output
+    dx_shapes = [(512, 256), (256, 128)]
+    probs, refs = [], []
+    for fin, fout in dx_shapes:
+        dz = torch.randn(rows, fout, device=cuda)
+        w = torch.randn(fout, fin, device=cuda) / math.sqrt(fout)
+        zp = torch.randn(rows, fin, device=cuda) * 2
+        hp = torch.where(zp > 0, zp, torch.expm1(zp))
+        out = torch.full((rows + 3, fin + 4), float("nan"), device=cuda)
+        probs.append((dz, w, hp, out[:rows, :fin]))
+        ref = (dz.double() @ w.double()) * torch.where(zp.double() > 0, 1.0, torch.exp(zp.double()))
+        refs.append((out, ref, fin))
+    ops.linear_bwd_dx(probs, rows, elu_from_output=True)
+    for out, ref, fin in refs:
+        assert rel_err(out[:rows, :fin], ref) < 2e-6
+        assert torch.isnan(out[rows:]).all() and torch.isnan(out[:, fin:]).all(), "store outside the output"
+
+
 def test_linear_fwd_h_only(cuda):
     """With ELU the pre-activation output may be omitted: h alone is written, z's buffer is untouched."""
     ops = _ops()

@@ -253,6 +253,74 @@ size_t dx_plan(const ppo_linear_bwd_dx_problem* probs, int count, size_t* offs) 
   return off;
 }
 
+// The persistent NT kernel when every problem of the launch meets its requirements (16-byte operands, whole
+// k-slabs, 16-byte aligned outputs of a width divisible by 4 under 2 GiB, 16-byte aligned biases); PPO_EUNSUPPORTED
+// otherwise, and the caller launches gemm_nt_kernel.
+template <int BM, int BN, int BK, int OCC, int EPI>
+int launch_nt_pipe(Group& g, int count, hipStream_t s, const char* name) {
+  auto fits = [](const float* c, int64_t rows, int64_t ld) {
+    return c == nullptr || (w16_ok(c, ld) && rows * ld * 4 < (int64_t(1) << 31));
+  };
+  for (int i = 0; i < count; ++i) {
+    const Problem& p = g.p[i];
+    if (!w16_ok(p.A, p.lda) || !w16_ok(p.B, p.ldb) || p.K % BK != 0 || p.N % 4 != 0) return PPO_EUNSUPPORTED;
+    if (!fits(p.C, p.M, p.ldc) || (EPI == EPI_BIAS_ELU && !fits(p.C2, p.M, p.ldc2))) return PPO_EUNSUPPORTED;
+    if (EPI == EPI_ELU_GRAD && !w16_ok(p.aux, p.ldaux)) return PPO_EUNSUPPORTED;
+    if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && reinterpret_cast<uintptr_t>(p.vec) % 16 != 0)
+      return PPO_EUNSUPPORTED;
+  }
+  int tiles;
+  if (int rc = assign_blocks(g, count, BM, BN, name, tiles)) return rc;
+  if (tiles == 0) return PPO_OK;
+  static std::atomic<int> cache[kMaxDevices];
+  const int resident = resident_blocks(gemm_nt_pipe_kernel<BM, BN, BK, OCC, EPI>, cache);
+  if (resident <= 0) return PPO_EUNSUPPORTED;
+  hipLaunchKernelGGL((gemm_nt_pipe_kernel<BM, BN, BK, OCC, EPI>), dim3(std::min(tiles, resident)), dim3(kThreads), 0,
+                     s, g, tiles);
+  return check_launch(name);
+}
+
+// Tile of the persistent NT launches: 0 = none (gemm_nt_kernel only).  A PPO_HIP_TUNING build reads `var`
+// (0 = off, 1..) for sweeps.
+int pipe_tile(const char* var, int dflt) {
+#ifdef PPO_HIP_TUNING
+  if (const char* e = std::getenv(var)) return std::atoi(e);
+#else
+  (void)var;
+#endif
+  return dflt;
+}
+
+template <int EPI>
+int launch_nt_pipe_tile(int t, Group& g, int count, hipStream_t s, const char* name) {
+  switch (t) {
+    case 1:  // (its ELU'-source registers would not fit 3 blocks per CU: not for the input-grads)
+      if constexpr (EPI == EPI_ELU_GRAD) {
+        return PPO_EUNSUPPORTED;
+      } else {
+        return launch_nt_pipe<128, 128, 16, 3, EPI>(g, count, s, name);
+      }
+    case 2:
+      return launch_nt_pipe<128, 64, 16, 3, EPI>(g, count, s, name);
+    case 3:
+      return launch_nt_pipe<64, 64, 16, 4, EPI>(g, count, s, name);
+#ifdef PPO_HIP_TUNING
+    case 4:
+      return launch_nt_pipe<64, 64, 32, 3, EPI>(g, count, s, name);
+    case 5:
+      if constexpr (EPI == EPI_ELU_GRAD) {
+        return PPO_EUNSUPPORTED;
+      } else {
+        return launch_nt_pipe<128, 128, 32, 2, EPI>(g, count, s, name);
+      }
+    case 6:
+      return launch_nt_pipe<128, 64, 32, 2, EPI>(g, count, s, name);
+#endif
+    default:
+      return PPO_EUNSUPPORTED;
+  }
+}
+
 bool rows_ok(int64_t rows) { return rows > 0 && rows <= INT32_MAX / 2; }
 
 // The kernels address an NT operand with 32-bit byte offsets from its first element.
@@ -296,6 +364,10 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
   hipStream_t s = static_cast<hipStream_t>(stream);
   // measured on MI355X for 24576-row mini-batches: outputs wider than 128 like 128x128 tiles with 16-deep slabs,
   // narrower ones 128x64
+  const int pt = pipe_tile("PPO_HIP_PIPE_FWD", max_n > 128 ? 1 : 2);
+  const int prc = activation == PPO_ACT_ELU ? launch_nt_pipe_tile<EPI_BIAS_ELU>(pt, g, count, s, "linear_fwd_elu")
+                                            : launch_nt_pipe_tile<EPI_BIAS>(pt, g, count, s, "linear_fwd");
+  if (prc != PPO_EUNSUPPORTED) return prc;
   const Tile t = pick_tile(max_n > 128 ? T128x128k16s2o3 : T128x64k32s2o4);
   if (activation == PPO_ACT_ELU) return launch_nt_tile<EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_elu");
   return launch_nt_tile<EPI_BIAS>(t, g, count, s, "linear_fwd");
@@ -382,6 +454,10 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
     max_n = std::max(max_n, q.in_features);
   }
   // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
+  const int pt = pipe_tile("PPO_HIP_PIPE_DX", max_n > 128 ? 3 : 2);
+  const int prc = any_act ? launch_nt_pipe_tile<EPI_ELU_GRAD>(pt, g, count, s, "linear_bwd_dx_elu")
+                          : launch_nt_pipe_tile<EPI_STORE>(pt, g, count, s, "linear_bwd_dx");
+  if (prc != PPO_EUNSUPPORTED) return prc;
   const Tile t = pick_tile(max_n > 128 ? T64x64k32s2o4 : T128x64k32s2o4);
   if (any_act) return launch_nt_tile<EPI_ELU_GRAD>(t, g, count, s, "linear_bwd_dx_elu");
   return launch_nt_tile<EPI_STORE>(t, g, count, s, "linear_bwd_dx");

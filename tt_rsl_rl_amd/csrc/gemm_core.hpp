@@ -23,6 +23,7 @@
 // offsets, after an XCD-aware permutation that places consecutive tiles (which share an A panel) on one XCD / L2.
 #pragma once
 
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 
@@ -616,6 +617,274 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   } else {
     gemm_nt_tile<BM, BN, BK, S, OCC, A16, B16M == 1, EPI>(g, tc, lds);
   }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Persistent NT for the forward and input-grad epilogues (bias / bias+ELU / ELU' / plain store).
+//
+// A launch of one block per output tile runs as one or two waves of blocks that start together, so every block
+// loads, multiplies and stores in the same phase: the epilogue's stores (an output tile is as many bytes as its
+// operands at k = BM, BN) are a burst at HBM write speed that no MFMA work overlaps.  Here a grid of resident blocks
+// walks the tiles (block b takes tiles r * grid + b', b' its XCD-contiguous slot) and the LDS ring streams k-slabs
+// across tile boundaries: the first slabs of tile r + 1 are in flight while tile r's epilogue runs, and tile r's
+// stores drain while tile r + 1 multiplies.  Vector-memory operations retire in issue order on this target, so the
+// wait for the slab issued before an epilogue may leave that epilogue's stores outstanding: vmcnt(NSTORE), NSTORE
+// being exactly the stores the epilogue issues.  To keep that count exact, every epilogue store is a buffer store
+// issued by every lane (lanes outside the output get an offset past the buffer's end, which the hardware drops).
+// Requirements (checked on the host): 16-byte aligned operands with leading dimensions that are multiples of 4,
+// K a multiple of BK, 16-byte aligned outputs with N a multiple of 4, outputs smaller than 2 GiB.
+// ------------------------------------------------------------------------------------------------------------------
+
+// Tile t of a grouped launch (problems' tile ranges in block_begin, one split each).
+__device__ inline TileCoord tile_at(const Group& g, int t) {
+  int pi = 0;
+#pragma unroll
+  for (int i = 1; i < PPO_MAX_LINEAR_PROBLEMS; ++i)
+    if (i < g.count && t >= g.p[i].block_begin) pi = i;
+  const Problem& P = g.p[pi];
+  const int local = t - P.block_begin;
+  TileCoord c;
+  c.pi = pi;
+  c.split = 0;
+  c.tm = local / P.tiles_n;
+  c.tn = local - c.tm * P.tiles_n;
+  return c;
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kDropOffset = 0x80000000u;  // past every output buffer (the host keeps them under 2 GiB)
+
+// Raw buffer over a row-major [rows, ld] fp32 output (null: a zero-length buffer, every store dropped).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_buffer(float* base, int rows, int64_t ld) {
+  const int bytes = base != nullptr ? static_cast<int>(static_cast<int64_t>(rows) * ld * 4) : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ void store_b128(__amdgpu_buffer_rsrc_t r, uint32_t off, const f32x4& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
+}
+
+// The epilogue of one wave's (TM x TN) 32 x 32 accumulator tiles (layout as in gemm_nt_tile): each tile through the
+// wave's own LDS patch, finished in row order, TM * TN * 4 * OUTS buffer stores in every lane.
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void nt_pipe_epilogue(const Problem& P, const f32x16 (&acc)[TM][TN], int row0w, int col0w,
+                                                 float* patch, int lane) {
+  constexpr int PS = 36;
+  const int h = lane >> 5;
+  const int pr = lane >> 3, pc = 4 * (lane & 7);
+  const int M = P.M, N = P.N;
+  const __amdgpu_buffer_rsrc_t rc = out_buffer(EPI == EPI_BIAS_ELU && P.C == nullptr ? nullptr : P.C, M, P.ldc);
+  const __amdgpu_buffer_rsrc_t rc2 = out_buffer(EPI == EPI_BIAS_ELU ? P.C2 : nullptr, M, P.ldc2);
+  // every load of the epilogue before its first store: a wait for a load issued after a store would wait for the
+  // store as well (in-order retirement)
+  f32x4 bias[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    bias[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int n = col0w + j * 32 + pc;
+    if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && n < N) bias[j] = *reinterpret_cast<const f32x4*>(P.vec + n);
+  }
+  f32x4 zsrc[EPI == EPI_ELU_GRAD ? TM : 1][EPI == EPI_ELU_GRAD ? TN : 1][4];
+  if constexpr (EPI == EPI_ELU_GRAD) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int n = col0w + j * 32 + pc, m = row0w + i * 32 + pr + 8 * rr;
+          zsrc[i][j][rr] = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+          if (m < M && n < N) zsrc[i][j][rr] = *reinterpret_cast<const f32x4*>(P.aux + int64_t(m) * P.ldaux + n);
+        }
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        f32x4 x = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        *reinterpret_cast<f32x4*>(patch + (lane & 31) * PS + 8 * q + 4 * h) = x;
+      }
+      const int n = col0w + j * 32 + pc;
+      const bool n_in = n < N;  // N % 4 == 0: columns n .. n + 3 are all in or all out
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int r = pr + 8 * rr;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(patch + r * PS + pc);
+        const int m = row0w + i * 32 + r;
+        const bool ok = m < M && n_in;
+        const int64_t mm = ok ? m : 0;
+        f32x4 o, o2;
+        if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = x[e] + bias[j][e];
+            o2[e] = elu_fwd(o[e]);
+          }
+        } else if constexpr (EPI == EPI_ELU_GRAD) {
+          const f32x4 zp = zsrc[i][j][rr];
+          if (P.elu_from_output) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * (zp[e] + 1.0f);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * expf(zp[e]);
+          }
+        } else {
+          o = x;
+        }
+        store_b128(rc, ok ? static_cast<uint32_t>((mm * P.ldc + n) * 4) : kDropOffset, o);
+        if constexpr (EPI == EPI_BIAS_ELU)
+          store_b128(rc2, ok ? static_cast<uint32_t>((mm * P.ldc2 + n) * 4) : kDropOffset, o2);
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int BK, int OCC, int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_pipe_kernel(
+    const Group g, int tiles) {
+  static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_ELU || EPI == EPI_ELU_GRAD || EPI == EPI_STORE,
+                "persistent NT: forward / input-grad epilogues");
+  constexpr int S = 2;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int G = BK / 8;
+  constexpr int PS = 36;
+  constexpr int NSTORE = TM * TN * 4 * (EPI == EPI_BIAS_ELU ? 2 : 1);
+  static_assert(TM >= 1 && TN >= 1 && NSTORE < 63, "tile");
+  __shared__ __align__(16) float lds[S * STAGE + 4 * 32 * PS];
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+  float* const patch = lds + S * STAGE + wave * 32 * PS;
+  const int nblk = gridDim.x;
+  const int slot = g.xcds > 1 ? xcd_remap(blockIdx.x, nblk, g.xcds) : static_cast<int>(blockIdx.x);
+  if (slot >= tiles) return;
+
+  // issue cursor: the next k-slab to load (tile itile, slab ikt), LDS stage istage
+  int itile = slot, ikt = 0, istage = 0, ink = 0;
+  const float* iA = nullptr;
+  const float* iB = nullptr;
+  NtLoader<BM, BK, true> la;
+  NtLoader<BN, BK, true> lb;
+  auto cursor_tile = [&]() {
+    const TileCoord c = tile_at(g, itile);
+    const Problem& P = g.p[c.pi];
+    iA = P.A;
+    iB = P.B;
+    ink = P.K / BK;
+    la.init(P.lda, c.tm * BM, P.M, wave, lane);
+    lb.init(P.ldb, c.tn * BN, P.N, wave, lane);
+  };
+  cursor_tile();
+  auto issue_next = [&]() {
+    float* st = lds + istage * STAGE;
+    la.issue(iA + ikt * BK, st, wave);
+    lb.issue(iB + ikt * BK, st + BM * BK, wave);
+    istage ^= 1;
+    if (++ikt == ink) {
+      ikt = 0;
+      itile += nblk;
+      if (itile < tiles) cursor_tile();
+    }
+  };
+  auto more = [&]() { return itile < tiles; };
+
+  f32x4 fa[2][TM], fb[2][TN];
+  auto load_group = [&](int stage, int buf, int gi) {
+    const float* As = lds + stage * STAGE;
+    const float* Bs = As + BM * BK;
+    const int c = 2 * gi + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * WM + 32 * i + (lane & 31);
+      fa[buf][i] = *reinterpret_cast<const f32x4*>(As + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn * WN + 32 * j + (lane & 31);
+      fb[buf][j] = *reinterpret_cast<const f32x4*>(Bs + r * BK + 4 * (c ^ nt_swz<BK>(r)));
+    }
+  };
+
+  // prologue: slab 0 in LDS for every wave, slab 1 in flight, slab 0's first fragments in registers
+  issue_next();
+  wait_vmcnt<0>();
+  lds_barrier();
+  if (more()) issue_next();
+  int cstage = 0, buf = 0;
+  load_group(cstage, buf, 0);
+
+  int ctile = slot;
+  bool first = true;
+  for (;;) {
+    const TileCoord cc = tile_at(g, ctile);
+    const Problem& P = g.p[cc.pi];
+    const int nk = P.K / BK;
+    const bool next_tile = ctile + nblk < tiles;
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+    for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+      for (int gi = 0; gi < G; ++gi) {
+        if (gi + 1 < G) {
+          load_group(cstage, buf ^ 1, gi + 1);
+        } else if (kt + 1 < nk || next_tile) {
+          // the next slab (issued one slab ago, before the previous tile's epilogue when this is a tile's first
+          // slab) has landed for every wave, and every wave is done with this slab's stage
+          if (kt == 0 && !first) {
+            wait_vmcnt<NSTORE>();
+          } else {
+            wait_vmcnt<0>();
+          }
+          lds_barrier();
+          if (more()) issue_next();
+          load_group(cstage ^ 1, buf ^ 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[buf][j][s4], fa[buf][i][s4], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        buf ^= 1;
+      }
+      cstage ^= 1;
+    }
+    nt_pipe_epilogue<TM, TN, EPI>(P, acc, cc.tm * BM + wm * WM, cc.tn * BN + wn * WN, patch, lane);
+    if (!next_tile) break;
+    ctile += nblk;
+    first = false;
+  }
+}
+
+// Blocks of kernel k the current device holds at once (0 when unknown), cached per device in `cache`.
+template <typename K>
+int resident_blocks(K kernel, std::atomic<int>* cache) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    v = std::max(per_cu, 0) * std::max(cus, 0) + 1;  // stored + 1: 0 marks "not queried yet"
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v - 1;
 }
 
 // ------------------------------------------------------------------------------------------------------------------

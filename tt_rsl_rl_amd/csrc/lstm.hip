@@ -649,25 +649,6 @@ uint64_t seq_spin_ticks() {
   return e != nullptr ? std::strtoull(e, nullptr, 10) : kSeqSpinTicks;
 }
 
-// Blocks of kernel k the current device holds at once (0 when unknown), cached per device.
-template <typename K>
-int resident_blocks(K kernel, std::atomic<int>* cache) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  int v = cache[dev].load(std::memory_order_relaxed);
-  if (v == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-      (void)hipGetLastError();
-      return 0;
-    }
-    v = std::max(per_cu, 0) * std::max(cus, 0) + 1;  // stored + 1: 0 marks "not queried yet"
-    cache[dev].store(v, std::memory_order_relaxed);
-  }
-  return v - 1;
-}
-
 // Launches the whole-sequence forward when the shape allows it and the device holds at least one row-group slot
 // (count * ncb blocks) at once.  Returns PPO_OK, an error, or PPO_EUNSUPPORTED to ask for the per-step launches.
 template <int NS>
