@@ -74,6 +74,14 @@ int ppo_adv_normalize(const float* x, int64_t in_stride, float* out, int64_t out
  * must lie in the flags' allocation (true of any device allocation, whose size is rounded up to 256 bytes or more).
  * perm: int64 [rows], every entry in [0, src_rows).
  * ------------------------------------------------------------------------------------------------------------------ */
+/* A column block of a row-major fp32 matrix: columns [0, width) of rows r * stride. */
+typedef struct ppo_column_block {
+  const float* src; /* [rows, stride] */
+  int64_t stride;
+  int32_t width;
+  int32_t reserved;
+} ppo_column_block;
+
 enum { PPO_GATHER_FLOAT = 0, PPO_GATHER_KEEP_U8 = 1 };
 typedef struct ppo_gather_segment {
   const void* src;        /* [src_rows, src_stride] fp32 (PPO_GATHER_FLOAT) or uint8 (PPO_GATHER_KEEP_U8) */
@@ -90,6 +98,16 @@ typedef struct ppo_gather_segment {
 
 int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_rows, const ppo_gather_segment* segments,
                     int32_t num_segments, float* dst, int64_t dst_stride, ppo_stream_t stream);
+
+/* dst[r, c .. c + width_i) = cols[i].src[r * cols[i].stride + 0 .. width_i), column blocks side by side in order
+ * (c = sum of the earlier widths; at most PPO_MAX_INTERLEAVE_FLOATS in all), for r < rows: the rollout's
+ * per-transition scalars (log-prob, advantage, value, return) packed into one short record per row ahead of the
+ * gather, which then reads one 16-byte piece per sampled row instead of four 4-byte ones (each pulling a whole cache
+ * line).  No counterpart in the reference (upstream indexes the four [T*N, 1] tensors separately,
+ * rollout_storage.py:244-258).  Data moves bit-exactly. */
+#define PPO_MAX_INTERLEAVE_FLOATS 16
+int ppo_interleave_columns(const ppo_column_block* cols, int32_t num_cols, int64_t rows, float* dst,
+                           int64_t dst_stride, ppo_stream_t stream);
 
 /* The permutation itself, host code: torch.randperm(n) as drawn from torch's CPU generator
  * (rsl_rl/storage/rollout_storage.py:232), i.e. a Fisher-Yates shuffle of 0..n-1 with z_i = draw_i mod (n - i)
@@ -197,13 +215,6 @@ int ppo_linear_bwd_dw_norm(const ppo_linear_bwd_dw_problem* problems, int32_t co
  * ------------------------------------------------------------------------------------------------------------------ */
 int ppo_obs_normalize(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows, int32_t width,
                       const float* mean, const float* std, float eps, ppo_stream_t stream);
-
-typedef struct ppo_column_block {
-  const float* src; /* [rows, stride] */
-  int64_t stride;
-  int32_t width;
-  int32_t reserved;
-} ppo_column_block;
 
 size_t ppo_normalizer_update_workspace_bytes(int64_t rows, int32_t dim);
 int ppo_normalizer_update(const ppo_column_block* blocks, int32_t num_blocks, int64_t rows, float* state_mean,

@@ -96,6 +96,22 @@ def test_gather_rows_bit_exact(cuda):
     assert torch.isnan(out[:, 133]).all() and torch.isnan(out[:, 135:]).all(), "gather wrote outside its columns"
 
 
+@pytest.mark.parametrize("rows", [1, 1000, 98304 + 5])
+def test_interleave_columns_matches_cat(cuda, rows):
+    """Column blocks of different widths and strides side by side, bit-exact (torch.cat of the same views); the
+    destination's columns past them stay untouched."""
+    ops = _ops()
+    torch.manual_seed(rows)
+    a = torch.randn(rows, 3, device=cuda)
+    b = torch.randn(rows, 5, device=cuda)[:, 1:2]
+    c = torch.randn(rows, 1, device=cuda)
+    d = torch.randn(rows, 9, device=cuda)[:, 2:8]
+    dst = torch.full((rows, 16), float("nan"), device=cuda)
+    ops.interleave_columns([a, b, c, d], dst)
+    assert torch.equal(dst[:, :11], torch.cat([a, b, c, d], 1))
+    assert torch.isnan(dst[:, 11:]).all()
+
+
 # ----------------------------------------------------------------------------------------------------------------------
 # A6 linear layers
 # ----------------------------------------------------------------------------------------------------------------------

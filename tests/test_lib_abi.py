@@ -69,7 +69,7 @@ STRUCTS = {
 
 
 # the header's size limits and the Python mirror's copies of them
-CONSTANTS = {"PPO_MAX_GATHER_SEGMENTS": "MAX_GATHER_SEGMENTS", "PPO_MAX_LINEAR_PROBLEMS": "MAX_LINEAR_PROBLEMS",
+CONSTANTS = {"PPO_MAX_GATHER_SEGMENTS": "MAX_GATHER_SEGMENTS", "PPO_MAX_INTERLEAVE_FLOATS": "MAX_INTERLEAVE_FLOATS", "PPO_MAX_LINEAR_PROBLEMS": "MAX_LINEAR_PROBLEMS",
              "PPO_MAX_PARAM_GROUPS": "MAX_PARAM_GROUPS", "PPO_DW_NORM_BLOCKS": "DW_NORM_BLOCKS",
              "PPO_MAX_EXTRA_GRADS": "MAX_EXTRA_GRADS", "PPO_ADAM_STATIC_SCRATCH_DOUBLES": "ADAM_STATIC_SCRATCH_DOUBLES",
              "PPO_ADAM_STATIC_MAX_PARAMS": "ADAM_STATIC_MAX_PARAMS"}
@@ -150,6 +150,15 @@ def test_argument_validation_reports_errors_without_a_gpu():
         _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)
     probs = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512)])
     assert lib.ppo_linear_bwd_dw_workspace_bytes(probs, 1, 24576) >= 4 * 512 * 96
+    # column interleave: at most MAX_INTERLEAVE_FLOATS per row, a destination wide enough, 32-bit element count
+    wide = _lib.array(_lib.ColumnBlock, [_lib.ColumnBlock(16, 9, 9, 0), _lib.ColumnBlock(16, 8, 8, 0)])
+    with pytest.raises(ValueError, match="more than 16"):
+        _lib.call("ppo_interleave_columns", wide, 2, 10, 16, 32, None)
+    one = _lib.array(_lib.ColumnBlock, [_lib.ColumnBlock(16, 1, 1, 0)])
+    with pytest.raises(ValueError, match="dst_stride"):
+        _lib.call("ppo_interleave_columns", one, 1, 10, 16, 0, None)
+    with pytest.raises(ValueError, match="too many"):
+        _lib.call("ppo_interleave_columns", one, 1, 1 << 31, 16, 1, None)
     # the norm-partials variant rejects a group outside [0, PPO_MAX_PARAM_GROUPS] and malformed extra ranges before
     # any launch, and needs its output buffer
     bad = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512,

@@ -25,6 +25,7 @@ PPO_ELU_FROM_OUTPUT = 1
 PPO_STD_SCALAR = 0
 PPO_STD_LOG = 1
 MAX_GATHER_SEGMENTS = 16
+MAX_INTERLEAVE_FLOATS = 16
 MAX_LINEAR_PROBLEMS = 8
 MAX_PARAM_GROUPS = 4
 MAX_ACTIONS = 64
@@ -141,6 +142,7 @@ _SIGNATURES = [
                                     C.c_void_p]),
     ("ppo_linear_bwd_dw_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDwProblem), i32, i64]),
     ("ppo_linear_bwd_dw", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),
+    ("ppo_interleave_columns", C.c_int, [C.POINTER(ColumnBlock), i32, i64, f32p, i64, C.c_void_p]),
     ("ppo_linear_bwd_dw_norm", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, f32p,
                                          C.POINTER(GradRange), i32, C.c_void_p, C.c_void_p]),
     ("ppo_obs_normalize", C.c_int, [f32p, i64, f32p, i64, i64, i32, f32p, f32p, C.c_float, C.c_void_p]),

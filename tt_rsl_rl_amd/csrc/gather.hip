@@ -127,10 +127,59 @@ __global__ __launch_bounds__(256) void obs_normalize_kernel(const float* __restr
   }
 }
 
+// One thread per output element (row r = t / W, column c = t % W of the W-float rows): consecutive threads write
+// consecutive floats of the destination and read consecutive rows of each source block.
+struct InterleaveArgs {
+  ppo_column_block col[PPO_MAX_INTERLEAVE_FLOATS];
+  int32_t first[PPO_MAX_INTERLEAVE_FLOATS];  // first output column of each block
+  int32_t num_cols, width;
+};
+
+__global__ __launch_bounds__(256) void interleave_kernel(const InterleaveArgs a, int64_t rows, float* __restrict__ dst,
+                                                         int64_t dst_stride) {
+  const uint32_t total = static_cast<uint32_t>(rows) * a.width;  // < 2^31 (checked on the host)
+  for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < total; t += gridDim.x * blockDim.x) {
+    const uint32_t r = t / a.width;
+    const int c = static_cast<int>(t - r * a.width);
+    int b = 0;
+#pragma unroll
+    for (int i = 1; i < PPO_MAX_INTERLEAVE_FLOATS; ++i)
+      if (i < a.num_cols && c >= a.first[i]) b = i;
+    dst[static_cast<int64_t>(r) * dst_stride + c] = a.col[b].src[static_cast<int64_t>(r) * a.col[b].stride + (c - a.first[b])];
+  }
+}
+
 }  // namespace
 }  // namespace ppo
 
 using namespace ppo;
+
+extern "C" int ppo_interleave_columns(const ppo_column_block* cols, int32_t num_cols, int64_t rows, float* dst,
+                                      int64_t dst_stride, ppo_stream_t stream) {
+  PPO_REQUIRE(cols && dst, "ppo_interleave_columns: null pointer");
+  PPO_REQUIRE(rows > 0 && num_cols > 0 && num_cols <= PPO_MAX_INTERLEAVE_FLOATS,
+              "ppo_interleave_columns: rows=%lld num_cols=%d", (long long)rows, num_cols);
+  InterleaveArgs a{};
+  int total = 0;
+  for (int i = 0; i < num_cols; ++i) {
+    PPO_REQUIRE(cols[i].src != nullptr && cols[i].width > 0 && cols[i].stride >= cols[i].width,
+                "ppo_interleave_columns: column block %d malformed", i);
+    a.col[i] = cols[i];
+    a.first[i] = total;
+    total += cols[i].width;
+    PPO_REQUIRE(total <= PPO_MAX_INTERLEAVE_FLOATS, "ppo_interleave_columns: more than %d floats per row",
+                PPO_MAX_INTERLEAVE_FLOATS);
+  }
+  PPO_REQUIRE(dst_stride >= total, "ppo_interleave_columns: dst_stride %lld < %d", (long long)dst_stride, total);
+  PPO_REQUIRE(rows * total < (int64_t(1) << 31), "ppo_interleave_columns: %lld rows of %d floats are too many",
+              (long long)rows, total);
+  a.num_cols = num_cols;
+  a.width = total;
+  const int64_t blocks = std::min<int64_t>(ceil_div(rows * total, 256), 16384);
+  hipLaunchKernelGGL(interleave_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a, rows, dst, dst_stride);
+  return check_launch("interleave_kernel");
+}
 
 extern "C" int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_rows,
                                const ppo_gather_segment* segments, int32_t num_segments, float* dst,

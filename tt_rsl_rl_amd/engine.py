@@ -158,6 +158,7 @@ class UpdateEngine:
         self.A = actor.distribution.output_dim
         self.layout = TableLayout(actor.obs_dim, critic.obs_dim, self.A, keep=self.recurrent)
         self.table = torch.zeros(self.B, self.layout.width, device=self.device)  # padding columns stay zero
+        self.scalars = torch.empty(self.B, 4, device=self.device)  # pack_scalars
         # zero-padded copies of first-layer weights whose input width is not a multiple of 16 (refreshed from the
         # parameters before every mini-batch's forward by a row gather)
         self.w0_pad: dict[int, torch.Tensor] = {}
@@ -270,7 +271,10 @@ class UpdateEngine:
                 L.check(getattr(lib, name)(*args), name)
 
     def gather(self, perm: torch.Tensor, row0: int = 0) -> None:
-        """Table rows [row0, row0 + len(perm)) = storage rows perm."""
+        """Table rows [row0, row0 + len(perm)) = storage rows perm (from row 0: the scalar records are packed
+        first)."""
+        if row0 == 0:
+            self.pack_scalars()
         segs = self.segments()
         dst = self.table[row0:row0 + perm.numel()]
         for i in range(0, len(segs), L.MAX_GATHER_SEGMENTS):
@@ -293,11 +297,35 @@ class UpdateEngine:
                     segs.append(ops.Segment(src, base + col))
                 col += w
         mean, std = st.distribution_params
-        segs += [ops.Segment(st.flat(st.actions), lay.actions), ops.Segment(st.flat(mean), lay.old_mean),
-                 ops.Segment(st.flat(std), lay.old_std), ops.Segment(st.flat(st.actions_log_prob), lay.old_logp),
-                 ops.Segment(st.flat(st.advantages), lay.adv), ops.Segment(st.flat(st.values), lay.old_values),
-                 ops.Segment(st.flat(st.returns), lay.returns)]
+        if self._record_matches():
+            # actions | mean | std with their padding, one contiguous record per row, in the table's column order
+            segs.append(ops.Segment(st.act_record.view(self.B, -1), lay.actions))
+        else:
+            segs += [ops.Segment(st.flat(st.actions), lay.actions), ops.Segment(st.flat(mean), lay.old_mean),
+                     ops.Segment(st.flat(std), lay.old_std)]
+        # log-prob, advantage, value, return: one 16-byte record per row (pack_scalars)
+        segs.append(ops.Segment(self.scalars, lay.old_logp))
         return segs
+
+    def _record_matches(self) -> bool:
+        """The storage's actions and (mean, std) are still the views of its interleaved record, laid out as the
+        table's actions / old mean / old std columns."""
+        st, lay = self.alg.storage, self.layout
+        rec = st.act_record
+        if rec is None or rec.shape[-1] != 3 * st.act_record_pad or len(st.distribution_params) != 2:
+            return False
+        ap = st.act_record_pad
+        views = (st.actions, *st.distribution_params)
+        return (all(v.data_ptr() == rec.data_ptr() + 4 * i * ap and v.stride() == rec[..., :1].stride()
+                    for i, v in enumerate(views)) and
+                lay.old_mean == lay.actions + ap and lay.old_std == lay.old_mean + ap)
+
+    def pack_scalars(self) -> None:
+        """scalars[r] = (log-prob, advantage, value, return) of storage row r, one coalesced pass over the four
+        [T, N, 1] buffers (the rows the gather then picks at random are one 16-byte read each)."""
+        st = self.alg.storage
+        ops.interleave_columns([st.flat(st.actions_log_prob), st.flat(st.advantages), st.flat(st.values),
+                                st.flat(st.returns)], self.scalars)
 
     def refresh_padded_weights(self) -> None:
         """w0_pad[:, :in] = the first layer's weight (the padding columns were zeroed at allocation)."""

@@ -259,6 +259,19 @@ def gather_rows(perm: torch.Tensor, segments: list[Segment], dst: torch.Tensor) 
            dst.data_ptr(), ld_dst, _stream())
 
 
+def interleave_columns(cols: list[torch.Tensor], dst: torch.Tensor) -> None:
+    """dst[:, c:c + w_i] = cols[i] for row-major [rows, w_i] fp32 views, side by side in order."""
+    _dev(dst, *cols)
+    rows = dst.shape[0]
+    blocks = []
+    for c in cols:
+        if c.dim() != 2 or c.shape[0] != rows:
+            raise ValueError("interleave_columns: every block must be [rows, width]")
+        blocks.append(L.ColumnBlock(c.data_ptr(), _row_major(c, "column block"), c.shape[1], 0))
+    L.call("ppo_interleave_columns", L.array(L.ColumnBlock, blocks), len(blocks), rows, dst.data_ptr(),
+           _row_major(dst, "dst"), _stream())
+
+
 def obs_normalize(x: torch.Tensor, y: torch.Tensor, mean: torch.Tensor, std: torch.Tensor, eps: float) -> None:
     _dev(x, y, mean, std)
     ldx, ldy = _row_major(x, "x"), _row_major(y, "y")

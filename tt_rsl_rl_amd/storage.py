@@ -65,6 +65,10 @@ class RolloutStorage:
         self.values = torch.zeros(T, N, 1, device=self.device)
         self.actions_log_prob = torch.zeros(T, N, 1, device=self.device)
         self.distribution_params: tuple[torch.Tensor, ...] | None = None
+        # actions and the distribution parameters as column blocks of one record per transition (set up at the first
+        # transition, when the parameters' shapes are known): see _interleave
+        self.act_record: torch.Tensor | None = None
+        self.act_record_pad = 0
         self.returns = torch.zeros(T, N, 1, device=self.device)
         self.advantages = torch.zeros(T, N, 1, device=self.device)
         self.saved_hidden_state_a = None
@@ -76,6 +80,8 @@ class RolloutStorage:
         if self.step >= self.num_transitions_per_env:
             raise OverflowError("Rollout buffer overflow! You should call clear() before adding new transitions.")
         s = self.step
+        if self.distribution_params is None:
+            self._interleave(transition.distribution_params)
         for k in self.observations:
             self.observations[k][s].copy_(transition.observations[k])
         self.actions[s].copy_(transition.actions)
@@ -83,14 +89,28 @@ class RolloutStorage:
         self.dones[s].copy_(transition.dones.view(-1, 1))
         self.values[s].copy_(transition.values)
         self.actions_log_prob[s].copy_(transition.actions_log_prob.view(-1, 1))
-        if self.distribution_params is None:
-            self.distribution_params = tuple(
-                torch.zeros(self.num_transitions_per_env, *p.shape, device=self.device)
-                for p in transition.distribution_params)
         for i, p in enumerate(transition.distribution_params):
             self.distribution_params[i][s].copy_(p)
         self._save_hidden_states(transition.hidden_states)
         self.step += 1
+
+    def _interleave(self, params) -> None:
+        """Storage for the actions and the distribution parameters.  When every parameter has the actions' [N, A]
+        shape (a Gaussian's mean and std), they are column blocks of one record per transition, [T, N, k * Ap] with
+        block i at columns i * Ap .. i * Ap + A (Ap = A rounded up to 4, zero padding between), and ``actions`` /
+        ``distribution_params`` are views of it with upstream's shapes: the update's gather then reads one
+        contiguous record per sampled row instead of k scattered short rows (each of which pulls whole cache lines).
+        Otherwise separate [T, N, ...] buffers as upstream allocates them."""
+        T, N = self.num_transitions_per_env, self.num_envs
+        if len(self.actions_shape) == 1 and all(tuple(p.shape) == (N, self.actions_shape[0]) for p in params):
+            A = self.actions_shape[0]
+            ap = -(-A // 4) * 4
+            rec = torch.zeros(T, N, (1 + len(params)) * ap, device=self.device)
+            self.act_record, self.act_record_pad = rec, ap
+            self.actions = rec[..., :A]
+            self.distribution_params = tuple(rec[..., (i + 1) * ap:(i + 1) * ap + A] for i in range(len(params)))
+        else:
+            self.distribution_params = tuple(torch.zeros(T, *p.shape, device=self.device) for p in params)
 
     def _save_hidden_states(self, hidden_states) -> None:
         """rollout_storage.py:333-359: the recurrent models' state before each step's forward, as saved_hidden_state_a /
