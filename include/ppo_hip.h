@@ -45,6 +45,7 @@ int ppo_abi_version(void);
  * last_values: [N].  For t = T-1..0, in upstream's fp32 operation order (no contraction):
  *   nt = 1 - done[t];  delta = (r[t] + (nt*gamma)*V[t+1]) - V[t];  adv = delta + ((nt*gamma)*lam)*adv;
  *   ret[t] = adv + V[t]   (V[T] = last_values, adv starts at 0);   advantages = ret - V  (ppo.py:188).
+ * T * N < 2^31.
  * ------------------------------------------------------------------------------------------------------------------ */
 int ppo_gae(const float* rewards, const float* values, const uint8_t* dones, const float* last_values,
             float* returns, float* advantages, int64_t num_steps, int64_t num_envs, float gamma, float lam,

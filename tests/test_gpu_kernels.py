@@ -30,7 +30,8 @@ def _ops():
 # ----------------------------------------------------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("T,N,p_done", [(24, 4096, 0.005), (7, 333, 0.3), (1, 1, 0.0), (24, 65536, 0.01)])
+@pytest.mark.parametrize("T,N,p_done", [(24, 4096, 0.005), (7, 333, 0.3), (1, 1, 0.0), (24, 65536, 0.01),
+                                        (16, 1000, 0.02), (40, 500, 0.05)])
 def test_gae_matches_oracle(cuda, T, N, p_done):
     ops = _ops()
     g = torch.Generator().manual_seed(T * 1000 + N)

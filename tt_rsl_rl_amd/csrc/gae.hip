@@ -13,12 +13,14 @@
 namespace ppo {
 namespace {
 
-// One lane per environment.  The loads of a chunk of up to kGaeChunk steps are issued before its scan (they do not
-// depend on the recurrence), so a lane waits for memory once per chunk instead of once per step.  The arithmetic is
-// unchanged: the same fp32 operations in the same order as upstream's loop.
+// One lane per environment.  All loads of a chunk of CHUNK steps are issued before its scan (they do not depend on
+// the recurrence) in straight-line code, so a lane waits for memory once per chunk instead of once per step: steps
+// past the first `cnt` of a chunk re-read a step inside it (discarded), and the done flags stay bytes until the
+// scan (a load whose result is converted at once, or a load under a branch, compiles to a wait of its own).
+// The arithmetic is unchanged: the same fp32 operations in the same order as upstream's loop.
 constexpr int kGaeThreads = 64;
-constexpr int kGaeChunk = 32;
 
+template <int CHUNK>
 __global__ __launch_bounds__(kGaeThreads) void gae_kernel(const float* __restrict__ rewards,
                                                           const float* __restrict__ values,
                                                           const uint8_t* __restrict__ dones,
@@ -26,35 +28,41 @@ __global__ __launch_bounds__(kGaeThreads) void gae_kernel(const float* __restric
                                                           float* __restrict__ returns,
                                                           float* __restrict__ advantages, int64_t T, int64_t N,
                                                           float gamma, float lam) {
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (n >= N) return;
+  // 32-bit element indices (T * N < 2^31, checked on the host)
+  const uint32_t n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= static_cast<uint32_t>(N)) return;
+  const uint32_t NN = static_cast<uint32_t>(N);
   float next_value = last_values[n];
   float adv = 0.0f;
-  for (int64_t t0 = T - 1; t0 >= 0; t0 -= kGaeChunk) {
-    const int cnt = static_cast<int>(t0 + 1 < kGaeChunk ? t0 + 1 : kGaeChunk);
-    float r[kGaeChunk], v[kGaeChunk], d[kGaeChunk];
+  for (int t0 = static_cast<int>(T) - 1; t0 >= 0; t0 -= CHUNK) {
+    const int cnt = t0 + 1 < CHUNK ? t0 + 1 : CHUNK;
+    float r[CHUNK], v[CHUNK];
+    uint32_t d[CHUNK];
 #pragma unroll
-    for (int j = 0; j < kGaeChunk; ++j) {
-      if (j < cnt) {
-        const int64_t i = (t0 - j) * N + n;
-        r[j] = rewards[i];
-        v[j] = values[i];
-        d[j] = static_cast<float>(dones[i]);
-      }
+    for (int j = 0; j < CHUNK; ++j) {
+      const uint32_t i = static_cast<uint32_t>(t0 - (j < cnt ? j : cnt - 1)) * NN + n;
+      r[j] = rewards[i];
+      v[j] = values[i];
+      d[j] = dones[i];
     }
+    auto step = [&](int j) {
+      const uint32_t i = static_cast<uint32_t>(t0 - j) * NN + n;
+      const float not_terminal = 1.0f - static_cast<float>(d[j]);
+      const float ng = not_terminal * gamma;
+      const float delta = (r[j] + ng * next_value) - v[j];
+      adv = delta + (ng * lam) * adv;
+      const float ret = adv + v[j];
+      returns[i] = ret;
+      advantages[i] = ret - v[j];
+      next_value = v[j];
+    };
+    if (cnt == CHUNK) {  // a full chunk (every chunk of a rollout of CHUNK steps): no branch the loads could sink into
 #pragma unroll
-    for (int j = 0; j < kGaeChunk; ++j) {
-      if (j < cnt) {
-        const int64_t i = (t0 - j) * N + n;
-        const float not_terminal = 1.0f - d[j];
-        const float ng = not_terminal * gamma;
-        const float delta = (r[j] + ng * next_value) - v[j];
-        adv = delta + (ng * lam) * adv;
-        const float ret = adv + v[j];
-        returns[i] = ret;
-        advantages[i] = ret - v[j];
-        next_value = v[j];
-      }
+      for (int j = 0; j < CHUNK; ++j) step(j);
+    } else {
+#pragma unroll
+      for (int j = 0; j < CHUNK; ++j)
+        if (j < cnt) step(j);
     }
   }
 }
@@ -154,11 +162,26 @@ extern "C" int ppo_gae(const float* rewards, const float* values, const uint8_t*
   PPO_REQUIRE(rewards && values && dones && last_values && returns && advantages, "ppo_gae: null pointer");
   PPO_REQUIRE(num_steps > 0 && num_envs > 0, "ppo_gae: num_steps=%lld num_envs=%lld must be positive",
               (long long)num_steps, (long long)num_envs);
+  PPO_REQUIRE(num_steps * num_envs < (int64_t(1) << 31), "ppo_gae: %lld x %lld elements (at most 2^31 - 1)",
+              (long long)num_steps, (long long)num_envs);
   const int64_t blocks = ceil_div(num_envs, kGaeThreads);
-  PPO_REQUIRE(blocks <= INT32_MAX, "ppo_gae: too many environments");
-  hipLaunchKernelGGL(gae_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGaeThreads), 0,
-                     static_cast<hipStream_t>(stream), rewards, values, dones, last_values, returns, advantages,
-                     num_steps, num_envs, gamma, lam);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 block(kGaeThreads);
+  // the chunk: all of a rollout of up to 32 steps at once (the smallest of 8, 16, 24, 32 that holds it)
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (num_steps <= 8) {
+    hipLaunchKernelGGL(gae_kernel<8>, grid, block, 0, s, rewards, values, dones, last_values, returns, advantages,
+                       num_steps, num_envs, gamma, lam);
+  } else if (num_steps <= 16) {
+    hipLaunchKernelGGL(gae_kernel<16>, grid, block, 0, s, rewards, values, dones, last_values, returns, advantages,
+                       num_steps, num_envs, gamma, lam);
+  } else if (num_steps <= 24) {
+    hipLaunchKernelGGL(gae_kernel<24>, grid, block, 0, s, rewards, values, dones, last_values, returns, advantages,
+                       num_steps, num_envs, gamma, lam);
+  } else {
+    hipLaunchKernelGGL(gae_kernel<32>, grid, block, 0, s, rewards, values, dones, last_values, returns, advantages,
+                       num_steps, num_envs, gamma, lam);
+  }
   return check_launch("gae_kernel");
 }
 
