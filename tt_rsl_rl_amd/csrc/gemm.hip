@@ -553,6 +553,14 @@ int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t ro
     rc = launch_tn<kDwBM, kDwBN, 64, 2, 1>(g, count, s, "linear_bwd_dw");
   } else if (cfg && !std::strcmp(cfg, "bk32s2o1")) {
     rc = launch_tn<kDwBM, kDwBN, 32, 2, 1>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk16s4o2")) {
+    rc = launch_tn<kDwBM, kDwBN, 16, 4, 2>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk16s3o2")) {
+    rc = launch_tn<kDwBM, kDwBN, 16, 3, 2>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk32s3o1")) {
+    rc = launch_tn<kDwBM, kDwBN, 32, 3, 1>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "bk32s4o1")) {
+    rc = launch_tn<kDwBM, kDwBN, 32, 4, 1>(g, count, s, "linear_bwd_dw");
   } else {
     rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
   }

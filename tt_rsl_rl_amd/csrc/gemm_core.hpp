@@ -2,8 +2,8 @@
 //
 // Two kernel families, both 256 threads = 4 wavefronts in a 2 x 2 arrangement over a BM x BN output tile, each
 // wave owning (BM/2) x (BN/2) of 32 x 32 v_mfma_f32_32x32x2f32 accumulators, both fed by gfx950's direct
-// global->LDS loads (global_load_lds_dwordx4 / _dword: no register staging, no ds_write) into a two-stage LDS ring
-// with one barrier per BK-deep k-slab:
+// global->LDS loads (buffer_load_dwordx4 / _dword ... lds: no register staging, no ds_write) into an LDS ring of
+// stages with one barrier per BK-deep k-slab:
 //
 //   NT  C[m,n] = sum_k A[m,k] B[n,k]        both operands k-contiguous in memory
 //       forward     z[r,o]   = sum_i x[r,i]  w[o,i]    A = x,  B = w           epilogue +b (ELU)
@@ -17,8 +17,8 @@
 // group g, lane half h contributes k = 8g + 4h + s for both operands (any bijection of k works if A and B agree).
 // TN tiles are stored k-major (row per k, BM or BN floats), and rows are interleaved across the two 32-wide MFMA
 // tiles of a wave (tile i takes m = 2*rho + i) so one ds_read_b64 feeds both tiles and the partial stores are
-// float2-wide.  Reads of rows past M or N are clamped into the operand (their results are discarded); the K tail
-// is loaded through a masked path with zeros.  Several independent problems (actor and critic, or all layers of
+// float2-wide.  Reads of rows past M or N are clamped into the operand (their results are discarded); the NT K
+// tail is loaded through a masked path with zeros, the TN one by the buffer's record limit.  Several independent problems (actor and critic, or all layers of
 // the weight-grad) share one launch: the block index maps to (problem, split, tile) through per-problem block
 // offsets, after an XCD-aware permutation that places consecutive tiles (which share an A panel) on one XCD / L2.
 #pragma once
@@ -148,30 +148,59 @@ __device__ inline TileCoord locate(const Group& g) {
   return t;
 }
 
-// Direct global->LDS copy: every lane of the wave moves `bytes` (16 or 4) from its own global address to
-// lds_wave + lane * bytes.  lds_wave must be wave-uniform.
+// Direct global->LDS copy through a raw buffer: every lane moves BYTES from byte offset `off` of buffer r to
+// lds_wave + lane * BYTES (lds_wave wave-uniform), and an offset at or past the buffer's record count reads zeros.
+// Unlike the flat-encoded global_load_lds, the compiler's wait-count pass does not treat it as a possible LDS access
+// that may complete out of order, so the LDS reads issued while it is in flight keep exact (not zero) wait counts.
 template <int BYTES>
-__device__ __forceinline__ void dma(const float* src, float* lds_wave) {
+__device__ __forceinline__ void dma_buf(__amdgpu_buffer_rsrc_t r, uint32_t off, float* lds_wave) {
   static_assert(BYTES == 16 || BYTES == 4, "16- or 4-byte direct loads");
+  auto* dst = (__attribute__((address_space(3))) void*)lds_wave;
   if constexpr (BYTES == 16) {
-    __builtin_amdgcn_global_load_lds(src, lds_wave, 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, off, 0, 0, 0);
   } else {
-    __builtin_amdgcn_global_load_lds(src, lds_wave, 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 4, off, 0, 0, 0);
   }
 }
 
+// Raw buffer of `bytes` bytes at `base` (both wave-uniform), built from scalar registers: the compiler otherwise
+// may compute the descriptor in vector registers and wrap every load that uses it in a per-lane loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t uniform_buffer(const float* base, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  float* const p = reinterpret_cast<float*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8; a field at its maximum
+// does not wait).  The waits and the barrier are the compiler's builtins, not inline assembly: after an opaque asm
+// statement the compiler's wait-count pass must assume unknown LDS / scalar-memory events are in flight, and every
+// later LDS read it waits for becomes "lgkmcnt(0)" (measured: one full LDS round trip before each MFMA group).
+// The builtins carry no memory ordering of their own, so compiler-only fences on both sides keep every memory
+// access of the source on its side of the wait.
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
+
 // Waits until at most N of this wave's vector-memory operations are outstanding.  The LDS-direct loads count here
-// (and are not tracked by the compiler as LDS writes: hence the memory clobber).  Loads complete in issue order.
+// (the compiler does not track them as LDS writes).  Loads complete in issue order.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0, "vmcnt");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N < 63 ? N : 63) : "memory");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(N < 63 ? N : 63));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Workgroup barrier of the LDS ring: this wave's LDS writes are complete and the compiler moves no memory access
+// Workgroup barrier of the LDS ring: this wave's LDS accesses are complete and the compiler moves no memory access
 // across it.  Unlike __syncthreads(), whose workgroup release fence also drains every outstanding global load, it
 // leaves the prefetched slabs in flight; their arrival is awaited explicitly with wait_slab().
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 // Ring of S LDS stages with prefetch distance S - 1: before computing slab kt a wave waits for its own loads of
 // slab kt while the `later` (<= S - 2) slabs issued after it may stay in flight; L = loads per wave per slab.
@@ -211,7 +240,7 @@ __device__ __forceinline__ int nt_swz(int row) {
 
 // Direct loads of one NT operand: one full k-slab [x0, x0 + BX) x [k0, k0 + BK) per call, rows >= X clamped to X - 1.
 // Each lane's byte offsets from the slab's first column are fixed for the whole k loop, so a slab costs one
-// uniform (scalar) base pointer and one global_load_lds per instruction.  Wave w issues instructions w, w+4, ...
+// uniform (scalar) base pointer and one buffer_load ... lds per instruction.  Wave w issues instructions w, w+4, ...
 template <int BX, int BK, bool W16>
 struct NtLoader {
   static constexpr int CPR = BK / 4;
@@ -237,15 +266,16 @@ struct NtLoader {
       off[j] = static_cast<uint32_t>((gx * ld + col) * 4);
     }
   }
-  // base: the operand's element (0, k0), wave-uniform.
+  // base: the operand's element (0, k0), wave-uniform.  The offsets stay under 4 GiB (the host rejects operands that
+  // span more), so the buffer needs no bound of its own.
   __device__ __forceinline__ void issue(const float* base, float* lds_op, int wave) const {
+    const __amdgpu_buffer_rsrc_t r = uniform_buffer(base, -1);
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const float* src = reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off[j]);
       if constexpr (W16) {
-        dma<16>(src, lds_op + (4 * j + wave) * 256);
+        dma_buf<16>(r, off[j], lds_op + (4 * j + wave) * 256);
       } else {
-        dma<4>(src, lds_op + (4 * j + wave) * 64);
+        dma_buf<4>(r, off[j], lds_op + (4 * j + wave) * 64);
       }
     }
   }
@@ -836,16 +866,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       for (int gi = 0; gi < G; ++gi) {
         if (gi + 1 < G) {
           load_group(cstage, buf ^ 1, gi + 1);
-        } else if (kt + 1 < nk || next_tile) {
-          // the next slab (issued one slab ago, before the previous tile's epilogue when this is a tile's first
-          // slab) has landed for every wave, and every wave is done with this slab's stage
-          if (kt == 0 && !first) {
-            wait_vmcnt<NSTORE>();
-          } else {
-            wait_vmcnt<0>();
+        } else {
+          if (kt + 1 < nk || next_tile) {
+            // the next slab (issued one slab ago, before the previous tile's epilogue when this is a tile's first
+            // slab) has landed for every wave, and every wave is done with this slab's stage
+            if (kt == 0 && !first) {
+              wait_vmcnt<NSTORE>();
+            } else {
+              wait_vmcnt<0>();
+            }
+            lds_barrier();
+            if (more()) issue_next();
           }
-          lds_barrier();
-          if (more()) issue_next();
+          // read on every path (after the last slab: stale values, never used), so both paths reach the MFMAs with
+          // the same LDS reads in flight and the compiler's wait counts stay exact
           load_group(cstage ^ 1, buf ^ 1, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1011,9 +1045,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 // TN (weight-grad): operands stored [k][x] (x contiguous); LDS tile [BK][BX], unpadded.
 // ------------------------------------------------------------------------------------------------------------------
 
-// Direct loads of one TN operand: one full k-slab, rows [k0, k0 + BK) x columns [x0, x0 + BX), per call; columns
-// past X read the last in-bounds chunk / element instead (the 16-byte form needs ld >= X rounded up to 4, which a
-// leading dimension that is a multiple of 4 guarantees).  Per-lane byte offsets from the slab's first row are fixed.
+// Direct loads of one TN operand: one k-slab, rows [k0, k0 + BK) x columns [x0, x0 + BX), per call, through a raw
+// buffer that ends after the slab's last existing row (rows past it read zeros); columns past X read the last
+// in-bounds chunk / element instead (the 16-byte form needs ld >= X rounded up to 4, which a leading dimension that
+// is a multiple of 4 guarantees).  Per-lane byte offsets from the slab's first row are fixed.
 template <int BX, int BK, bool W16>
 struct TnLoader {
   static constexpr int NQ = W16 ? BK * BX / 256 : BK * BX / 64;
@@ -1032,29 +1067,22 @@ struct TnLoader {
       off[j] = static_cast<uint32_t>((row * ld + gx) * 4);
     }
   }
-  // base: the operand's row k0, wave-uniform.
-  __device__ __forceinline__ void issue(const float* base, float* lds_op, int wave) const {
+  // base: the operand's row k0, wave-uniform; rows (<= BK): the slab's rows that exist, the others read zeros.
+  // Issues this wave's loads j0 .. j1 - 1 of the slab (all of them by default).
+  __device__ __forceinline__ void issue(const float* base, int64_t ld, int rows, float* lds_op, int wave, int j0 = 0,
+                                        int j1 = PER) const {
+    const __amdgpu_buffer_rsrc_t r = uniform_buffer(base, static_cast<int>(rows * ld * 4));
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      const float* src = reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off[j]);
+      if (j < j0 || j >= j1) continue;
       if constexpr (W16) {
-        dma<16>(src, lds_op + (4 * j + wave) * 256);
+        dma_buf<16>(r, off[j], lds_op + (4 * j + wave) * 256);
       } else {
-        dma<4>(src, lds_op + (4 * j + wave) * 64);
+        dma_buf<4>(r, off[j], lds_op + (4 * j + wave) * 64);
       }
     }
   }
 };
-
-template <int BX, int BK>
-__device__ __forceinline__ void tn_masked(const float* __restrict__ base, int64_t ld, int x0, int X, int k0,
-                                          int k_end, float* lds_op) {
-  for (int q = threadIdx.x; q < BK * BX; q += kThreads) {
-    const int row = q / BX, x = q % BX;
-    const int k = k0 + row;
-    lds_op[q] = k < k_end ? base[static_cast<int64_t>(k) * ld + min(x0 + x, X - 1)] : 0.0f;
-  }
-}
 
 template <int BM, int BN, int BK, int S, int OCC, bool A16, bool B16>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_kernel(
@@ -1063,9 +1091,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = BK * (BM + BN);
   static_assert(TM == 2 && TN == 2, "TN kernel: 2 x 2 interleaved MFMA tiles per wave");
-  static_assert(kThreads % BM == 0 && BK % 8 == 0, "TN column sums split the slab over kThreads / BM threads");
+  static_assert(BK % 8 == 0, "TN slabs hold whole groups of 4 k-steps");
   static_assert(S >= 2 && S <= 4, "2..4 LDS stages");
   constexpr int L = TnLoader<BM, BK, A16>::PER + TnLoader<BN, BK, B16>::PER;
+  constexpr int G = BK / 8;  // groups of 4 MFMA k-steps (8 rows of k) per slab
   __shared__ __align__(16) float lds[S * STAGE];
 
   const TileCoord tc = locate(g);
@@ -1078,7 +1107,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   const int M = P.M, N = P.N;
   const int k_begin = tc.split * P.k_chunk;
   const int k_end = min(P.K, k_begin + P.k_chunk);
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1;
   const int h = lane >> 5, sg = lane & 31;
 
@@ -1090,75 +1119,101 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const bool do_colsum = P.colsum != nullptr && tc.tn == 0;
-  double colsum_acc[4] = {0.0, 0.0, 0.0, 0.0};
+  // Bias-gradient column sums from the A fragments already in registers: lane (h, sg) holds A[k][c] for the columns
+  // c = wm * WM + 2 sg + i (i = 0, 1) at the rows k = h (mod 2) of the block's range, added in row order in fp64;
+  // the two row parities meet in the end.  No LDS reads of their own, so no wait between the MFMAs.  Every wave
+  // adds (the wn = 1 waves hold the same fragments) so the waves of a block take the same time.
+  double colsum_acc[2] = {0.0, 0.0};
   const int span = max(k_end - k_begin, 0);
-  const int nfull = span / BK;
   const int nk = (span + BK - 1) / BK;
   TnLoader<BM, BK, A16> la;
   TnLoader<BN, BK, B16> lb;
   la.init(lda, row0, M, wave, lane);
   lb.init(ldb, col0, N, wave, lane);
-  auto issue = [&](int kt, int stage) {
+  // Rows past k_end (the split's last, partial slab) read zeros; a slab wholly past it (the loop's look-ahead at the
+  // end) becomes a zero fill that fetches nothing.  part = -1: every load of the slab; part = 0 .. 3: this wave's
+  // loads of quarter `part` of each operand.
+  constexpr int PA = TnLoader<BM, BK, A16>::PER, PB = TnLoader<BN, BK, B16>::PER;
+  static_assert(PA % 4 == 0 && PB % 4 == 0, "slab loads split in quarters");
+  auto issue = [&](int kt, int stage, int part) {
     float* st = lds + stage * STAGE;
     const int k0 = k_begin + kt * BK;
-    if (kt < nfull) {
-      la.issue(A + k0 * lda, st, wave);
-      lb.issue(B + k0 * ldb, st + BK * BM, wave);
+    const int rows = max(0, min(BK, k_end - k0));
+    if (part < 0) {
+      la.issue(A + k0 * lda, lda, rows, st, wave);
+      lb.issue(B + k0 * ldb, ldb, rows, st + BK * BM, wave);
     } else {
-      tn_masked<BM, BK>(A, lda, row0, M, k0, k_end, st);
-      tn_masked<BN, BK>(B, ldb, col0, N, k0, k_end, st + BK * BM);
+      la.issue(A + k0 * lda, lda, rows, st, wave, part * PA / 4, (part + 1) * PA / 4);
+      lb.issue(B + k0 * ldb, ldb, rows, st + BK * BM, wave, part * PB / 4, (part + 1) * PB / 4);
     }
   };
-#pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < nk) issue(s, s);
-  for (int kt = 0; kt < nk; ++kt) {
-    wait_slab<L, S>(min(S - 2, nk - 1 - kt));
-    lds_barrier();
-    if (kt + S - 1 < nk) issue(kt + S - 1, (kt + S - 1) % S);
-    const float* As = lds + (kt % S) * STAGE;
+  f32x2 fa[2][4], fb[2][4];
+  auto load_group = [&](int stage, int buf, int gi) {
+    const float* As = lds + stage * STAGE;
     const float* Bs = As + BK * BM;
-    // Column sums for the bias gradient: column c = tid % BM over this thread's half of the slab (BK / 2 = 4 G
-    // rows), in 4 independent chains (row kk into chain kk & 3).  One row per MFMA k-step, read one step ahead, so
-    // the reads and fp64 adds issue between the MFMAs instead of as a phase of their own; every block computes them
-    // (only the tn == 0 blocks store them), so all blocks of a launch take the same time.
-    const float* cs_col = As + (tid / BM) * (BK / 2) * BM + tid % BM;
-    float cs_cur = cs_col[0];
-    // groups of 4 k-steps (8 rows of k): the fragments of group g + 1 are read before the MFMAs of group g issue
-    constexpr int G = BK / 8;
-    static_assert(BK / 2 == 4 * G, "one column-sum row per MFMA k-step");
-    f32x2 fa[2][4], fb[2][4];
-    auto load_group = [&](int buf, int gi) {
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int kk = 8 * gi + 2 * st + h;
-        fa[buf][st] = *reinterpret_cast<const f32x2*>(As + kk * BM + wm * WM + 2 * sg);
-        fb[buf][st] = *reinterpret_cast<const f32x2*>(Bs + kk * BN + wn * WN + 2 * sg);
-      }
-    };
-    load_group(0, 0);
+    for (int st = 0; st < 4; ++st) {
+      const int kk = 8 * gi + 2 * st + h;
+      fa[buf][st] = *reinterpret_cast<const f32x2*>(As + kk * BM + wm * WM + 2 * sg);
+      fb[buf][st] = *reinterpret_cast<const f32x2*>(Bs + kk * BN + wn * WN + 2 * sg);
+    }
+  };
+
+  if (nk > 0) {
+    // prologue: slab 0 in LDS for every wave, slabs 1 .. S - 1 in flight, slab 0's first fragments in registers
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+      if (s < nk) issue(s, s, -1);
+    wait_slab<L, S>(min(S - 2, nk - 1));
+    lds_barrier();
+    if (S - 1 < nk) issue(S - 1, S - 1, -1);
+    load_group(0, 0, 0);
+  }
+  int buf = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cstage = kt % S;
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-      if (gi + 1 < G) load_group((gi + 1) & 1, gi + 1);
-      // scheduling fences: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
-      __builtin_amdgcn_sched_barrier(0);
+      const bool last = gi + 1 == G;
+      if (!last) {
+        load_group(cstage, buf ^ 1, gi + 1);
+        // scheduling fence: the compiler would otherwise sink the reads below the MFMAs and reuse one register set
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+        // The last group's fragments are in registers: once slab kt + 1 has landed for every wave and every wave is
+        // done reading this stage, slab kt + S streams into it (on every slab, the last ones as zero fills, so the
+        // loads share a block with the MFMAs below) and slab kt + 1's first fragments load under this group's
+        // MFMAs (after the last slab: stale values, never used).
+        wait_slab<L, S>(max(0, min(S - 2, nk - 2 - kt)));
+        lds_barrier();
+        load_group((kt + 1) % S, buf ^ 1, 0);
+      }
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i) {
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[gi & 1][st][i], fb[gi & 1][st][j], acc[i][j], 0,
-                                                             0, 0);
-        const int kk = 4 * gi + st;
-        const float cs_next = kk + 1 < BK / 2 ? cs_col[(kk + 1) * BM] : 0.0f;
-        colsum_acc[st] += static_cast<double>(cs_cur);
-        cs_cur = cs_next;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[buf][st][i], fb[buf][st][j], acc[i][j], 0, 0, 0);
+          if (last && i == 0) {
+            // a quarter of the next slab's loads per k-step, between MFMAs: a whole slab's loads issued back to back
+            // fill the texture unit's queue and hold every wave of the CU at its next load with the MFMA pipe idle
+            __builtin_amdgcn_sched_barrier(0);
+            issue(kt + S, cstage, st);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) colsum_acc[i] += static_cast<double>(fa[buf][st][i]);
       }
+      // keeps the group's adds here: the compiler would otherwise sink the whole chain behind the slab's last
+      // branch, 32 dependent fp64 adds in a row between two MFMA groups
+      asm volatile("" : "+v"(colsum_acc[0]), "+v"(colsum_acc[1]));
       __builtin_amdgcn_sched_barrier(0);
+      buf ^= 1;
     }
   }
+  wait_vmcnt<0>();  // the look-ahead's zero fills land before the block ends
 
   // Partial store.  Accumulator row rho = 8*(v/4) + 4*h + v%4 of tile i is m = 2*rho + i (TM == 2) or rho, and
   // column sg of tile j is n = 2*sg + j (TN == 2) or sg.
@@ -1185,13 +1240,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       }
     }
   }
-  if (do_colsum) {  // the two halves of each column, combined in a fixed order through the (now free) LDS ring
-    double* part = reinterpret_cast<double*>(lds);
-    const double mine = (colsum_acc[0] + colsum_acc[1]) + (colsum_acc[2] + colsum_acc[3]);
-    lds_barrier();
-    if (tid >= BM) part[tid - BM] = mine;
-    lds_barrier();
-    if (tid < BM && row0 + tid < M) P.colsum[static_cast<int64_t>(tc.split) * M + row0 + tid] = mine + part[tid];
+  if (P.colsum != nullptr && tc.tn == 0) {  // the two row parities of each column, h = 0 first
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const double other = __shfl_xor(colsum_acc[i], 32, 64);
+      const double sum = h == 0 ? colsum_acc[i] + other : other + colsum_acc[i];
+      const int m = row0 + wm * WM + 2 * sg + i;
+      if (wn == 0 && h == 0 && m < M) P.colsum[static_cast<int64_t>(tc.split) * M + m] = sum;
+    }
   }
 }
 
