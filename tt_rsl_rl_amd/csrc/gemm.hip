@@ -280,6 +280,43 @@ int launch_nt_pipe(Group& g, int count, hipStream_t s, const char* name) {
   return check_launch(name);
 }
 
+// The bf16x6 NT kernel (fp32 accuracy on the bf16 matrix cores) when every problem of the launch meets its
+// requirements (16-byte operands, whole 16-deep k-slabs, 16-byte aligned outputs of a width divisible by 4 under
+// 2 GiB, 16-byte aligned biases / ELU' sources); PPO_EUNSUPPORTED otherwise.  128 x 128 output tiles: measured on
+// MI355X in the 24,576-row humanoid update they beat 128 x 64 tiles on every layer (11.1 against 12.4 ms per update),
+// also where 128 x 64 would fill the last wave of blocks better.  A PPO_HIP_TUNING build reads "PPO_HIP_BX6" (0: off,
+// 64 / 128: that tile).
+template <int EPI>
+int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
+  auto fits = [](const float* c, int64_t rows, int64_t ld) {
+    return c == nullptr || (w16_ok(c, ld) && rows * ld * 4 < (int64_t(1) << 31));
+  };
+  for (int i = 0; i < count; ++i) {
+    const Problem& p = g.p[i];
+    if (!w16_ok(p.A, p.lda) || !w16_ok(p.B, p.ldb) || p.K % 16 != 0 || p.N % 4 != 0) return PPO_EUNSUPPORTED;
+    if (!fits(p.C, p.M, p.ldc) || (EPI == EPI_BIAS_ELU && !fits(p.C2, p.M, p.ldc2))) return PPO_EUNSUPPORTED;
+    if (EPI == EPI_ELU_GRAD && !w16_ok(p.aux, p.ldaux)) return PPO_EUNSUPPORTED;
+    if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && reinterpret_cast<uintptr_t>(p.vec) % 16 != 0)
+      return PPO_EUNSUPPORTED;
+  }
+  int bn = 128;
+#ifdef PPO_HIP_TUNING
+  if (const char* e = std::getenv("PPO_HIP_BX6")) bn = std::atoi(e);
+  if (bn != 64 && bn != 128) return PPO_EUNSUPPORTED;
+#endif
+  int blocks;
+  if (int rc = assign_blocks(g, count, 128, bn, name, blocks)) return rc;
+  if (blocks == 0) return PPO_OK;
+#ifdef PPO_HIP_TUNING
+  if (bn == 64) {
+    hipLaunchKernelGGL((gemm_nt_bx6_kernel<64, 2, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+    return check_launch(name);
+  }
+#endif
+  hipLaunchKernelGGL((gemm_nt_bx6_kernel<128, 2, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  return check_launch(name);
+}
+
 // Tile of the persistent NT launches: 0 = none (gemm_nt_kernel only).  A PPO_HIP_TUNING build reads `var`
 // (0 = off, 1..) for sweeps.
 int pipe_tile(const char* var, int dflt) {
@@ -315,6 +352,14 @@ int launch_nt_pipe_tile(int t, Group& g, int count, hipStream_t s, const char* n
       }
     case 6:
       return launch_nt_pipe<128, 64, 32, 2, EPI>(g, count, s, name);
+    case 7:
+      return launch_nt_pipe<128, 128, 16, 2, EPI>(g, count, s, name);
+    case 8:
+      return launch_nt_pipe<128, 64, 16, 4, EPI>(g, count, s, name);
+    case 9:
+      return launch_nt_pipe<64, 128, 16, 4, EPI>(g, count, s, name);
+    case 10:
+      return launch_nt_pipe<64, 64, 16, 3, EPI>(g, count, s, name);
 #endif
     default:
       return PPO_EUNSUPPORTED;
@@ -364,6 +409,9 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
   hipStream_t s = static_cast<hipStream_t>(stream);
   // measured on MI355X for 24576-row mini-batches: outputs wider than 128 like 128x128 tiles with 16-deep slabs,
   // narrower ones 128x64
+  const int brc = activation == PPO_ACT_ELU ? launch_nt_bx6<EPI_BIAS_ELU>(g, count, s, "linear_fwd_elu")
+                                            : launch_nt_bx6<EPI_BIAS>(g, count, s, "linear_fwd");
+  if (brc != PPO_EUNSUPPORTED) return brc;
   const int pt = pipe_tile("PPO_HIP_PIPE_FWD", max_n > 128 ? 1 : 2);
   const int prc = activation == PPO_ACT_ELU ? launch_nt_pipe_tile<EPI_BIAS_ELU>(pt, g, count, s, "linear_fwd_elu")
                                             : launch_nt_pipe_tile<EPI_BIAS>(pt, g, count, s, "linear_fwd");
@@ -454,6 +502,9 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
     max_n = std::max(max_n, q.in_features);
   }
   // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
+  const int brc = any_act ? launch_nt_bx6<EPI_ELU_GRAD>(g, count, s, "linear_bwd_dx_elu")
+                          : launch_nt_bx6<EPI_STORE>(g, count, s, "linear_bwd_dx");
+  if (brc != PPO_EUNSUPPORTED) return brc;
   const int pt = pipe_tile("PPO_HIP_PIPE_DX", max_n > 128 ? 3 : 2);
   const int prc = any_act ? launch_nt_pipe_tile<EPI_ELU_GRAD>(pt, g, count, s, "linear_bwd_dx_elu")
                           : launch_nt_pipe_tile<EPI_STORE>(pt, g, count, s, "linear_bwd_dx");
@@ -561,11 +612,13 @@ int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t ro
     rc = launch_tn<kDwBM, kDwBN, 32, 3, 1>(g, count, s, "linear_bwd_dw");
   } else if (cfg && !std::strcmp(cfg, "bk32s4o1")) {
     rc = launch_tn<kDwBM, kDwBN, 32, 4, 1>(g, count, s, "linear_bwd_dw");
-  } else {
+  } else if (cfg && !std::strcmp(cfg, "f32")) {
     rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+  } else {
+    rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
   }
 #else
-  rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+  rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
 #endif
   if (rc != PPO_OK) return rc;
   const int64_t blocks = norm != nullptr ? PPO_DW_NORM_BLOCKS : std::min<int64_t>(ceil_div(total, 256), 4096);

@@ -1133,8 +1133,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   // Rows past k_end (the split's last, partial slab) read zeros; a slab wholly past it (the loop's look-ahead at the
   // end) becomes a zero fill that fetches nothing.  part = -1: every load of the slab; part = 0 .. 3: this wave's
   // loads of quarter `part` of each operand.
-  constexpr int PA = TnLoader<BM, BK, A16>::PER, PB = TnLoader<BN, BK, B16>::PER;
-  static_assert(PA % 4 == 0 && PB % 4 == 0, "slab loads split in quarters");
+  constexpr int PA = TnLoader<BM, BK, A16>::PER, PB = TnLoader<BN, BK, B16>::PER;  // quarters [q PER / 4, ...)
   auto issue = [&](int kt, int stage, int part) {
     float* st = lds + stage * STAGE;
     const int k0 = k_begin + kt * BK;
@@ -1251,6 +1250,303 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   }
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// TN weight-grad on the bf16 matrix cores at fp32 accuracy.  Every operand element splits exactly into three bf16
+// parts x = hi + mid + lo (each rounded to nearest from what the previous parts leave: 8 significant bits each, the
+// 24 of fp32, for values in the normal range), and a product a b is taken as the six part products down to 16 bits
+// below the leading one: lo.hi + mid.mid + hi.lo + mid.hi + hi.mid + hi.hi (small terms first); the three left out
+// (mid.lo, lo.mid, lo.lo) are at most 2^-23 of |a b| together, the order of one fp32 rounding.  This is the
+// published bf16x6 scheme (Henry, Tang and Heinecke, "Leveraging the bfloat16 artificial intelligence datatype for
+// higher-precision computations", ARITH 2019).  Part products of bf16 values are exact in the fp32 accumulators.
+// One v_mfma_f32_32x32x16_bf16 is 16 k-steps of a 32 x 32 tile at an eighth of the 32x32x2 fp32 MFMA's cycles per
+// k-step, so the six take 3/4 of the fp32 MFMA's time... per 16 k-steps: 6 x 8 passes against 8 x 16.
+//
+// Each slab (16 rows of k) is staged through registers: thread t loads the 8 rows 8 (t / 128) .. + 7 of column t % 128
+// of both operands (one dword per row: 64 lanes read 256 contiguous bytes), splits them once per block (not once per
+// wave that reads them), and writes the three parts of each operand as 16-byte chunks of a [128][16] bf16 plane per
+// part, the two chunks of a row XOR-swapped on bit 3 of the row (conflict-free 16-byte reads and writes).  A wave's
+// MFMA operand for 32 rows is then one ds_read_b128 per part.  A slab's loads are issued two slabs ahead of its
+// MFMAs, at the top of an iteration, and split into the third bf16 stage at its end; rows at or past the split's end
+// read zeros through the buffer's record limit.  The fp64 bias sums come from the
+// staged A values (k rows of column m, in order), the two row halves of a column meeting in the end.
+// ------------------------------------------------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Three-way split of two floats into packed bf16 pairs (element 0 in the low half).
+__device__ __forceinline__ void split_bf16x3(float x0, float x1, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  float r0 = x0, r1 = x1;
+  uint32_t u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{r0, r1}), bf16x2));
+  hi = u;
+  r0 -= __builtin_bit_cast(float, u << 16);
+  r1 -= __builtin_bit_cast(float, u & 0xffff0000u);
+  u = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{r0, r1}), bf16x2));
+  mid = u;
+  r0 -= __builtin_bit_cast(float, u << 16);
+  r1 -= __builtin_bit_cast(float, u & 0xffff0000u);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{r0, r1}), bf16x2));
+}
+
+template <int OCC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_bx6_kernel(
+    const Group g) {
+  constexpr int BM = 128, BN = 128, BK = 16;
+  constexpr int PLANE = BM * BK * 2;  // bytes of one part of one operand
+  constexpr int STAGE = 6 * PLANE;    // 3 parts x 2 operands
+  constexpr int NS = 3;               // bf16 stages: slab kt read, kt + 1 ready, kt + 2 being written
+  __shared__ __align__(16) unsigned char lds[NS * STAGE];
+
+  const TileCoord tc = locate(g);
+  const Problem& P = g.p[tc.pi];
+  const float* const A = P.A;
+  const float* const B = P.B;
+  const int64_t lda = P.lda, ldb = P.ldb;
+  const int row0 = tc.tm * BM, col0 = tc.tn * BN;
+  const int M = P.M, N = P.N;
+  const int k_begin = tc.split * P.k_chunk;
+  const int k_end = min(P.K, k_begin + P.k_chunk);
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nk = (max(k_end - k_begin, 0) + BK - 1) / BK;
+
+  // staging: column sm of both operands (clamped into the matrix: results past M / N are discarded), rows 8 sh + e
+  const int sm = tid & 127, sh = tid >> 7;
+  const uint32_t voff_a = static_cast<uint32_t>((8 * sh * lda + min(row0 + sm, M - 1)) * 4);
+  const uint32_t voff_b = static_cast<uint32_t>((8 * sh * ldb + min(col0 + sm, N - 1)) * 4);
+  const int swz_w = 16 * (sh ^ ((sm >> 3) & 1));  // byte offset of this thread's chunk within its 32-byte row
+  float stage_v[16];
+  auto load_slab = [&](int kt) {  // 16 dword loads (8 of A, then 8 of B); zeros past k_end
+    const int k0 = k_begin + kt * BK;
+    const int rows = max(0, min(BK, k_end - k0));
+    const __amdgpu_buffer_rsrc_t ra = uniform_buffer(A + static_cast<int64_t>(k0) * lda, static_cast<int>(rows * lda * 4));
+    const __amdgpu_buffer_rsrc_t rb = uniform_buffer(B + static_cast<int64_t>(k0) * ldb, static_cast<int>(rows * ldb * 4));
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      stage_v[e] =
+          __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, voff_a, static_cast<int>(e * lda * 4), 0));
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      stage_v[8 + e] =
+          __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, voff_b, static_cast<int>(e * ldb * 4), 0));
+  };
+  double colsum_acc = 0.0;  // column sm of A over rows 8 sh .. 8 sh + 7 of every slab, in order
+  auto split_store = [&](int stage) {
+    unsigned char* st = lds + stage * STAGE;
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+      uint32_t h[4], md[4], l[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) split_bf16x3(stage_v[8 * o + 2 * q], stage_v[8 * o + 2 * q + 1], h[q], md[q], l[q]);
+      const u32x4 hi = {h[0], h[1], h[2], h[3]}, mid = {md[0], md[1], md[2], md[3]}, lo = {l[0], l[1], l[2], l[3]};
+      unsigned char* row = st + o * 3 * PLANE + sm * 32 + swz_w;
+      *reinterpret_cast<u32x4*>(row) = hi;
+      *reinterpret_cast<u32x4*>(row + PLANE) = mid;
+      *reinterpret_cast<u32x4*>(row + 2 * PLANE) = lo;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) colsum_acc += static_cast<double>(stage_v[e]);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // fragment reads: rows r = w * 64 + 32 t + lane % 32, chunk lane / 32 (8 k-steps each), one 16-byte read per part
+  const int fr = lane & 31, fc = lane >> 5;
+  auto frag = [&](const unsigned char* st, int o, int r, int part) {
+    const unsigned char* pl = st + (o * 3 + part) * PLANE;
+    return *reinterpret_cast<const bf16x8*>(pl + r * 32 + 16 * (fc ^ ((r >> 3) & 1)));
+  };
+
+  if (nk > 0) {  // slabs 0 and 1 in the first two stages
+    load_slab(0);
+    split_store(0);
+    load_slab(1);
+    split_store(1);
+    lds_barrier();
+  }
+  int cs = 0;  // stage of slab kt
+  for (int kt = 0; kt < nk; ++kt) {
+    // slab kt + 2's loads first (zeros past the split's end), split into the third stage after this slab's MFMAs:
+    // the loads have the whole slab to land, and no load is in flight across iterations
+    load_slab(kt + 2);
+    __builtin_amdgcn_sched_barrier(0);  // (the compiler would sink the loads to their use at the iteration's end)
+    const unsigned char* st = lds + cs * STAGE;
+    bf16x8 fa[2][3], fb[2][3];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int pp = 0; pp < 3; ++pp) {
+        fa[i][pp] = frag(st, 0, wm * 64 + 32 * i + fr, pp);
+        fb[i][pp] = frag(st, 1, wn * 64 + 32 * i + fr, pp);
+      }
+    constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+    for (int t = 0; t < 6; ++t)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][pa[t]], fb[j][pb[t]], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // the stage of slab kt + 2 is that of slab kt - 1, which every wave finished reading before the last barrier
+    const int ws = cs == 0 ? 2 : cs - 1;
+    split_store(ws);
+    lds_barrier();
+    cs = cs == 2 ? 0 : cs + 1;
+  }
+
+  // partial store: accumulator element v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of its tile
+  float* Cs = P.C + static_cast<int64_t>(tc.split) * P.partial_stride;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = col0 + wn * 64 + 32 * j + fr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = row0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * fc + (v & 3);
+        if (m < M && n < N) Cs[static_cast<int64_t>(m) * P.ldc + n] = acc[i][j][v];
+      }
+    }
+  if (P.colsum != nullptr && tc.tn == 0) {  // the two row halves of each column, sh = 0 first
+    double* part = reinterpret_cast<double*>(lds);
+    lds_barrier();
+    if (sh == 1) part[sm] = colsum_acc;
+    lds_barrier();
+    if (sh == 0 && row0 + sm < M) P.colsum[static_cast<int64_t>(tc.split) * M + row0 + sm] = colsum_acc + part[sm];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// NT (forward / input-grad) on the bf16 matrix cores at fp32 accuracy, with the part products of the weight-grad's
+// bf16x6 kernel above: one BM x BN output tile per block (BM = 128, BN = 128 or 64; 4 waves in 2 x 2, each
+// 64 x BN / 2), 16-deep k-slabs.  Both operands are k-contiguous: thread t stages row t / 2 of a 128-row operand slab,
+// k-half t % 2 (8 consecutive k: two 16-byte loads), splits it and writes each part as one 16-byte chunk of a [rows][16]
+// bf16 plane (chunks XOR-swapped on bit 3 of the row as in the weight-grad kernel); a 64-row B slab (BN = 64) is
+// staged by the first two waves.  The accumulators have the fp32 NT kernels' layout (B fragment first), so the
+// persistent kernel's epilogues finish the tile, through patches in the (then free) stage memory.
+// ------------------------------------------------------------------------------------------------------------------
+template <int BN, int OCC, int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_bx6_kernel(
+    const Group g) {
+  static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_ELU || EPI == EPI_ELU_GRAD || EPI == EPI_STORE,
+                "bf16x6 NT: forward / input-grad epilogues");
+  static_assert(BN == 128 || BN == 64, "tile");
+  constexpr int BM = 128, BK = 16;
+  constexpr int TM = 2, TN = BN / 64;
+  constexpr int PLANE_A = BM * BK * 2, PLANE_B = BN * BK * 2;  // bytes of one part of one operand
+  constexpr int STAGE = 3 * (PLANE_A + PLANE_B);
+  constexpr int NS = 3;
+  constexpr int PS = 36;
+  static_assert(4 * 32 * PS * 4 <= NS * STAGE, "epilogue patches fit in the stage memory");
+  __shared__ __align__(16) unsigned char lds[NS * STAGE];
+
+  const TileCoord tc = locate(g);
+  const Problem& P = g.p[tc.pi];
+  const float* const A = P.A;
+  const float* const B = P.B;
+  const int64_t lda = P.lda, ldb = P.ldb;
+  const int row0 = tc.tm * BM, col0 = tc.tn * BN;
+  const int M = P.M, N = P.N;
+  const int nk = P.K / BK;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int sr = tid >> 1, sh = tid & 1;  // staged row, k-half
+  const bool stage_b = BN == 128 || sr < BN;
+  // (plain 16-byte global loads: this compiler turns element reads of __builtin_amdgcn_raw_buffer_load_b128's result
+  // into one 4-byte load)
+  const float* const arow = A + static_cast<int64_t>(min(row0 + sr, M - 1)) * lda + 8 * sh;
+  const float* const brow = B + static_cast<int64_t>(min(col0 + (stage_b ? sr : 0), N - 1)) * ldb + 8 * sh;
+  const int swz_w = sr * 32 + 16 * (sh ^ ((sr >> 3) & 1));
+  u32x4 stage_v[4];
+  auto load_slab = [&](int kt) {  // the slab index is clamped into [0, nk): the look-ahead past the end re-reads
+    const int k0 = min(kt, nk - 1) * BK;
+    stage_v[0] = *reinterpret_cast<const u32x4*>(arow + k0);
+    stage_v[1] = *reinterpret_cast<const u32x4*>(arow + k0 + 4);
+    if (stage_b) {
+      stage_v[2] = *reinterpret_cast<const u32x4*>(brow + k0);
+      stage_v[3] = *reinterpret_cast<const u32x4*>(brow + k0 + 4);
+    }
+  };
+  auto split_store = [&](int stage) {
+    unsigned char* st = lds + stage * STAGE;
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+      if (o == 1 && !stage_b) break;
+      uint32_t w[8], h[4], md[4], l[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[e] = stage_v[2 * o][e];
+        w[4 + e] = stage_v[2 * o + 1][e];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        split_bf16x3(__builtin_bit_cast(float, w[2 * q]), __builtin_bit_cast(float, w[2 * q + 1]), h[q], md[q], l[q]);
+      const int plane = o == 0 ? PLANE_A : PLANE_B;
+      unsigned char* row = st + o * 3 * PLANE_A + swz_w;
+      *reinterpret_cast<u32x4*>(row) = u32x4{h[0], h[1], h[2], h[3]};
+      *reinterpret_cast<u32x4*>(row + plane) = u32x4{md[0], md[1], md[2], md[3]};
+      *reinterpret_cast<u32x4*>(row + 2 * plane) = u32x4{l[0], l[1], l[2], l[3]};
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int fr = lane & 31, fc = lane >> 5;
+  auto frag = [&](const unsigned char* pl, int r) {
+    return *reinterpret_cast<const bf16x8*>(pl + r * 32 + 16 * (fc ^ ((r >> 3) & 1)));
+  };
+
+  if (nk > 0) {
+    load_slab(0);
+    split_store(0);
+    load_slab(1);
+    split_store(1);
+    lds_barrier();
+  }
+  int cs = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    load_slab(kt + 2);
+    __builtin_amdgcn_sched_barrier(0);  // (the compiler would sink the loads to their use at the iteration's end)
+    const unsigned char* st = lds + cs * STAGE;
+    bf16x8 fa[TM][3], fb[TN][3];
+#pragma unroll
+    for (int pp = 0; pp < 3; ++pp) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i][pp] = frag(st + pp * PLANE_A, wm * 64 + 32 * i + fr);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j][pp] = frag(st + 3 * PLANE_A + pp * PLANE_B, wn * (BN / 2) + 32 * j + fr);
+    }
+    constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+    for (int t = 0; t < 6; ++t)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j][pb[t]], fa[i][pa[t]], acc[i][j], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // the stage of slab kt + 2 is that of slab kt - 1, which every wave finished reading before the last barrier
+    split_store(cs == 0 ? 2 : cs - 1);
+    lds_barrier();
+    cs = cs == 2 ? 0 : cs + 1;
+  }
+  float* const patch = reinterpret_cast<float*>(lds) + wave * 32 * PS;  // every wave is past the last barrier
+  nt_pipe_epilogue<TM, TN, EPI>(P, acc, row0 + wm * 64, col0 + wn * (BN / 2), patch, lane);
+}
+
 // 16-byte direct loads need a 16-byte aligned base and a leading dimension that is a multiple of 4.
 bool w16_ok(const float* base, int64_t ld) { return (reinterpret_cast<uintptr_t>(base) % 16 == 0) && ld % 4 == 0; }
 
@@ -1341,6 +1637,15 @@ int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
   } else {
     hipLaunchKernelGGL((gemm_tn_kernel<BM, BN, BK, S, OCC, false, false>), dim3(blocks), dim3(kThreads), 0, s, g);
   }
+  return check_launch(name);
+}
+
+template <int OCC>
+int launch_tn_bx6(Group& g, int count, hipStream_t s, const char* name) {
+  int blocks;
+  if (int rc = assign_blocks(g, count, 128, 128, name, blocks)) return rc;
+  if (blocks == 0) return PPO_OK;
+  hipLaunchKernelGGL((gemm_tn_bx6_kernel<OCC>), dim3(blocks), dim3(kThreads), 0, s, g);
   return check_launch(name);
 }
 
