@@ -616,9 +616,11 @@ int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t ro
     rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
   } else {
     rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+    if (rc == PPO_EUNSUPPORTED) rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
   }
 #else
   rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+  if (rc == PPO_EUNSUPPORTED) rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
 #endif
   if (rc != PPO_OK) return rc;
   const int64_t blocks = norm != nullptr ? PPO_DW_NORM_BLOCKS : std::min<int64_t>(ceil_div(total, 256), 4096);

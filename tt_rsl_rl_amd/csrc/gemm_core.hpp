@@ -1261,14 +1261,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 // One v_mfma_f32_32x32x16_bf16 is 16 k-steps of a 32 x 32 tile at an eighth of the 32x32x2 fp32 MFMA's cycles per
 // k-step, so the six take 3/4 of the fp32 MFMA's time... per 16 k-steps: 6 x 8 passes against 8 x 16.
 //
-// Each slab (16 rows of k) is staged through registers: thread t loads the 8 rows 8 (t / 128) .. + 7 of column t % 128
-// of both operands (one dword per row: 64 lanes read 256 contiguous bytes), splits them once per block (not once per
-// wave that reads them), and writes the three parts of each operand as 16-byte chunks of a [128][16] bf16 plane per
-// part, the two chunks of a row XOR-swapped on bit 3 of the row (conflict-free 16-byte reads and writes).  A wave's
-// MFMA operand for 32 rows is then one ds_read_b128 per part.  A slab's loads are issued two slabs ahead of its
-// MFMAs, at the top of an iteration, and split into the third bf16 stage at its end; rows at or past the split's end
-// read zeros through the buffer's record limit.  The fp64 bias sums come from the
-// staged A values (k rows of column m, in order), the two row halves of a column meeting in the end.
+// Each slab (16 rows of k) is staged through registers with 16-byte loads along the columns (the operands are
+// k-major), split once per block (not once per wave that reads it), and written as bf16 parts into k-major planes;
+// gfx950's transposing LDS read (ds_read_b64_tr_b16) then hands each lane 4 consecutive k of one column, two of them
+// a wave's MFMA operand.  A slab's loads are issued two slabs ahead of its MFMAs (two register buffers), and its
+// split into the free one of two stages runs between the MFMA groups of the slab before it, so each wave's VALU
+// work overlaps its own MFMAs.  The fp64 bias sums come from the staged A values.
 // ------------------------------------------------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -1287,14 +1285,15 @@ __device__ __forceinline__ void split_bf16x3(float x0, float x1, uint32_t& hi, u
   lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{r0, r1}), bf16x2));
 }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
 template <int OCC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_bx6_kernel(
     const Group g) {
   constexpr int BM = 128, BN = 128, BK = 16;
-  constexpr int PLANE = BM * BK * 2;  // bytes of one part of one operand
+  constexpr int PLANE = BK * BM * 2;  // bytes of one part of one operand: [16 rows of k][128 columns] bf16
   constexpr int STAGE = 6 * PLANE;    // 3 parts x 2 operands
-  constexpr int NS = 3;               // bf16 stages: slab kt read, kt + 1 ready, kt + 2 being written
-  __shared__ __align__(16) unsigned char lds[NS * STAGE];
+  __shared__ __align__(16) unsigned char lds[2 * STAGE];
 
   const TileCoord tc = locate(g);
   const Problem& P = g.p[tc.pi];
@@ -1307,44 +1306,57 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   const int k_end = min(P.K, k_begin + P.k_chunk);
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1;
-  const int nk = (max(k_end - k_begin, 0) + BK - 1) / BK;
+  // slabs in pairs (the unrolled loop's two halves use the two register buffers); a slab past k_end is all zeros
+  const int nk2 = (max(k_end - k_begin, 0) + 2 * BK - 1) / (2 * BK);
 
-  // staging: column sm of both operands (clamped into the matrix: results past M / N are discarded), rows 8 sh + e
-  const int sm = tid & 127, sh = tid >> 7;
-  const uint32_t voff_a = static_cast<uint32_t>((8 * sh * lda + min(row0 + sm, M - 1)) * 4);
-  const uint32_t voff_b = static_cast<uint32_t>((8 * sh * ldb + min(col0 + sm, N - 1)) * 4);
-  const int swz_w = 16 * (sh ^ ((sm >> 3) & 1));  // byte offset of this thread's chunk within its 32-byte row
-  float stage_v[16];
-  auto load_slab = [&](int kt) {  // 16 dword loads (8 of A, then 8 of B); zeros past k_end
+  // Staging: thread t loads the 4 columns 4 (t % 32) .. + 3 (clamped into the matrix: results past M / N are
+  // discarded; ld % 4 == 0 keeps the chunk inside its row) of rows t / 32 and t / 32 + 8 of both operands' slab
+  // (16-byte loads; a wave reads two 512-byte row pieces per load), rows at or past k_end as zeros.  Its part
+  // chunks go to [row][column] planes (a row is 64 banks wide), the 8-byte chunk index XOR-ed with 8 (row % 4): the
+  // transposing reads below take, per 32 lanes, 4 consecutive rows at 8 consecutive chunks, which this spreads over
+  // all 64 banks.
+  const int sc = tid & 31, sk = tid >> 5;
+  const int mc_a = min(row0 + 4 * sc, ((M - 1) >> 2) << 2), mc_b = min(col0 + 4 * sc, ((N - 1) >> 2) << 2);
+  const float* const a_col = A + mc_a;
+  const float* const b_col = B + mc_b;
+  auto chunk_off = [](int k, int c) { return k * (BM * 2) + ((c ^ (8 * (k & 3))) << 3); };
+  const int w_off0 = chunk_off(sk, sc), w_off1 = chunk_off(sk + 8, sc);
+  f32x4 stage_v[2][4];  // two buffers of: A rows sk, sk + 8; B rows sk, sk + 8
+  // Rows past k_end load row k_end - 1 and are zeroed afterwards: unconditional loads (no branch) keep the
+  // compiler's wait counts for them exact across the loop.
+  auto load_slab = [&](int kt, f32x4 (&v)[4]) {
     const int k0 = k_begin + kt * BK;
-    const int rows = max(0, min(BK, k_end - k0));
-    const __amdgpu_buffer_rsrc_t ra = uniform_buffer(A + static_cast<int64_t>(k0) * lda, static_cast<int>(rows * lda * 4));
-    const __amdgpu_buffer_rsrc_t rb = uniform_buffer(B + static_cast<int64_t>(k0) * ldb, static_cast<int>(rows * ldb * 4));
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      stage_v[e] =
-          __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ra, voff_a, static_cast<int>(e * lda * 4), 0));
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      stage_v[8 + e] =
-          __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rb, voff_b, static_cast<int>(e * ldb * 4), 0));
-  };
-  double colsum_acc = 0.0;  // column sm of A over rows 8 sh .. 8 sh + 7 of every slab, in order
-  auto split_store = [&](int stage) {
-    unsigned char* st = lds + stage * STAGE;
-#pragma unroll
-    for (int o = 0; o < 2; ++o) {
-      uint32_t h[4], md[4], l[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) split_bf16x3(stage_v[8 * o + 2 * q], stage_v[8 * o + 2 * q + 1], h[q], md[q], l[q]);
-      const u32x4 hi = {h[0], h[1], h[2], h[3]}, mid = {md[0], md[1], md[2], md[3]}, lo = {l[0], l[1], l[2], l[3]};
-      unsigned char* row = st + o * 3 * PLANE + sm * 32 + swz_w;
-      *reinterpret_cast<u32x4*>(row) = hi;
-      *reinterpret_cast<u32x4*>(row + PLANE) = mid;
-      *reinterpret_cast<u32x4*>(row + 2 * PLANE) = lo;
+    for (int h = 0; h < 2; ++h) {
+      const int k = k0 + sk + 8 * h;
+      const int kc = min(k, k_end - 1);
+      v[h] = *reinterpret_cast<const f32x4*>(a_col + static_cast<int64_t>(kc) * lda);
+      v[2 + h] = *reinterpret_cast<const f32x4*>(b_col + static_cast<int64_t>(kc) * ldb);
     }
+  };
+  auto zero_tail = [&](int kt, f32x4 (&v)[4]) {  // (applied where the values are used)
+    const int k0 = k_begin + kt * BK;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) colsum_acc += static_cast<double>(stage_v[e]);
+    for (int h = 0; h < 2; ++h) {
+      if (k0 + sk + 8 * h >= k_end) {
+        v[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        v[2 + h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
+  };
+  auto split_row = [&](const f32x4& v, int q, unsigned char* st) {  // q: A row sk, A row sk + 8, B row sk, B sk + 8
+    uint32_t h[2], md[2], l[2];
+    split_bf16x3(v[0], v[1], h[0], md[0], l[0]);
+    split_bf16x3(v[2], v[3], h[1], md[1], l[1]);
+    unsigned char* c = st + (q >> 1) * 3 * PLANE + ((q & 1) ? w_off1 : w_off0);
+    *reinterpret_cast<uint64_t*>(c) = (static_cast<uint64_t>(h[1]) << 32) | h[0];
+    *reinterpret_cast<uint64_t*>(c + PLANE) = (static_cast<uint64_t>(md[1]) << 32) | md[0];
+    *reinterpret_cast<uint64_t*>(c + 2 * PLANE) = (static_cast<uint64_t>(l[1]) << 32) | l[0];
+  };
+  double colsum_acc[4] = {0.0, 0.0, 0.0, 0.0};  // columns 4 sc + e of A over rows sk, sk + 8 of every slab, in order
+  auto add_colsum = [&](const f32x4 (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) colsum_acc[e] += static_cast<double>(v[0][e]) + static_cast<double>(v[1][e]);
   };
 
   f32x16 acc[2][2];
@@ -1355,52 +1367,69 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // fragment reads: rows r = w * 64 + 32 t + lane % 32, chunk lane / 32 (8 k-steps each), one 16-byte read per part
-  const int fr = lane & 31, fc = lane >> 5;
-  auto frag = [&](const unsigned char* st, int o, int r, int part) {
-    const unsigned char* pl = st + (o * 3 + part) * PLANE;
-    return *reinterpret_cast<const bf16x8*>(pl + r * 32 + 16 * (fc ^ ((r >> 3) & 1)));
+  // MFMA operand of 32 columns x 16 rows (lane l: column l % 32, rows 8 (l / 32) .. + 7) by two transposing reads:
+  // within each 16 lanes, lane 4 r + i addresses row k0 + r, chunk i of its group's 16 columns, and lane d receives
+  // rows k0 .. k0 + 3 of column d.
+  const int grp = lane >> 4, gi = lane & 3, gr = (lane >> 2) & 3;
+  const int rd_k = 8 * (grp >> 1) + gr, rd_c = 4 * (grp & 1) + gi;  // row (first read), chunk within 32 columns
+  auto frag = [&](const unsigned char* pl, int col32) {  // col32: first column of the 32 (a multiple of 32)
+    const int c = col32 / 4 + rd_c;
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(pl + chunk_off(rd_k, c)));
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(pl + chunk_off(rd_k + 4, c)));
+    typedef short i16x8 __attribute__((ext_vector_type(8)));
+    const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, v);
   };
 
-  if (nk > 0) {  // slabs 0 and 1 in the first two stages
-    load_slab(0);
-    split_store(0);
-    load_slab(1);
-    split_store(1);
+  if (nk2 > 0) {  // slab 0 in stage 0, slab 1 in registers
+    load_slab(0, stage_v[0]);
+    load_slab(1, stage_v[1]);
+    zero_tail(0, stage_v[0]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) split_row(stage_v[0][q], q, lds);
+    add_colsum(stage_v[0]);
     lds_barrier();
   }
-  int cs = 0;  // stage of slab kt
-  for (int kt = 0; kt < nk; ++kt) {
-    // slab kt + 2's loads first (zeros past the split's end), split into the third stage after this slab's MFMAs:
-    // the loads have the whole slab to land, and no load is in flight across iterations
-    load_slab(kt + 2);
-    __builtin_amdgcn_sched_barrier(0);  // (the compiler would sink the loads to their use at the iteration's end)
-    const unsigned char* st = lds + cs * STAGE;
-    bf16x8 fa[2][3], fb[2][3];
+  for (int kp = 0; kp < nk2; ++kp) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int pp = 0; pp < 3; ++pp) {
-        fa[i][pp] = frag(st, 0, wm * 64 + 32 * i + fr, pp);
-        fb[i][pp] = frag(st, 1, wn * 64 + 32 * i + fr, pp);
-      }
-    constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
-#pragma unroll
-    for (int t = 0; t < 6; ++t)
+    for (int u = 0; u < 2; ++u) {
+      // slab kt = 2 kp + u sits in stage u; slab kt + 1 in buffer u ^ 1 is split into stage u ^ 1 (which every wave
+      // finished reading before the last barrier) between this slab's MFMA groups, while slab kt + 2 loads into
+      // buffer u
+      const int kt = 2 * kp + u;
+      load_slab(kt + 2, stage_v[u]);
+      __builtin_amdgcn_sched_barrier(0);
+      const unsigned char* st = lds + u * STAGE;
+      unsigned char* nst = lds + (u ^ 1) * STAGE;
+      bf16x8 fa[2][3], fb[2][3];
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][pa[t]], fb[j][pb[t]], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // the stage of slab kt + 2 is that of slab kt - 1, which every wave finished reading before the last barrier
-    const int ws = cs == 0 ? 2 : cs - 1;
-    split_store(ws);
-    lds_barrier();
-    cs = cs == 2 ? 0 : cs + 1;
+        for (int pp = 0; pp < 3; ++pp) {
+          fa[i][pp] = frag(st + pp * PLANE, wm * 64 + 32 * i);
+          fb[i][pp] = frag(st + (3 + pp) * PLANE, wn * 64 + 32 * i);
+        }
+      zero_tail(kt + 1, stage_v[u ^ 1]);
+      constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+      for (int t = 0; t < 6; ++t) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][pa[t]], fb[j][pb[t]], acc[i][j], 0, 0, 0);
+        if (t < 4) split_row(stage_v[u ^ 1][t], t, nst);
+        if (t == 4) add_colsum(stage_v[u ^ 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      lds_barrier();
+    }
   }
 
   // partial store: accumulator element v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of its tile
+  const int fr = lane & 31, fc = lane >> 5;
   float* Cs = P.C + static_cast<int64_t>(tc.split) * P.partial_stride;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -1413,12 +1442,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         if (m < M && n < N) Cs[static_cast<int64_t>(m) * P.ldc + n] = acc[i][j][v];
       }
     }
-  if (P.colsum != nullptr && tc.tn == 0) {  // the two row halves of each column, sh = 0 first
-    double* part = reinterpret_cast<double*>(lds);
+  if (P.colsum != nullptr && tc.tn == 0) {  // column 4 sc + e: the 8 row groups sk = 0 .. 7 in order
+    double* part = reinterpret_cast<double*>(lds);  // [8][128]
     lds_barrier();
-    if (sh == 1) part[sm] = colsum_acc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) part[sk * 128 + 4 * sc + e] = colsum_acc[e];
     lds_barrier();
-    if (sh == 0 && row0 + sm < M) P.colsum[static_cast<int64_t>(tc.split) * M + row0 + sm] = colsum_acc + part[sm];
+    if (tid < 128 && row0 + tid < M) {
+      double sum = part[tid];
+      for (int r = 1; r < 8; ++r) sum += part[r * 128 + tid];
+      P.colsum[static_cast<int64_t>(tc.split) * M + row0 + tid] = sum;
+    }
   }
 }
 
@@ -1640,8 +1674,12 @@ int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
   return check_launch(name);
 }
 
+// The bf16x6 weight-grad when every problem's operands allow 16-byte loads (16-byte aligned, leading dimension a
+// multiple of 4); PPO_EUNSUPPORTED otherwise.
 template <int OCC>
 int launch_tn_bx6(Group& g, int count, hipStream_t s, const char* name) {
+  for (int i = 0; i < count; ++i)
+    if (!w16_ok(g.p[i].A, g.p[i].lda) || !w16_ok(g.p[i].B, g.p[i].ldb)) return PPO_EUNSUPPORTED;
   int blocks;
   if (int rc = assign_blocks(g, count, 128, 128, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
