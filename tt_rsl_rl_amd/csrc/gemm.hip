@@ -282,10 +282,11 @@ int launch_nt_pipe(Group& g, int count, hipStream_t s, const char* name) {
 
 // The bf16x6 NT kernel (fp32 accuracy on the bf16 matrix cores) when every problem of the launch meets its
 // requirements (16-byte operands, whole 16-deep k-slabs, 16-byte aligned outputs of a width divisible by 4 under
-// 2 GiB, 16-byte aligned biases / ELU' sources); PPO_EUNSUPPORTED otherwise.  128 x 128 output tiles: measured on
-// MI355X in the 24,576-row humanoid update they beat 128 x 64 tiles on every layer (11.1 against 12.4 ms per update),
-// also where 128 x 64 would fill the last wave of blocks better.  A PPO_HIP_TUNING build reads "PPO_HIP_BX6" (0: off,
-// 64 / 128: that tile).
+// 2 GiB, 16-byte aligned biases / ELU' sources); PPO_EUNSUPPORTED otherwise.  128 x 128 output tiles in two LDS
+// stages, three blocks per CU, four lanes per staged row: measured on MI355X in the 24,576-row humanoid update
+// (ms per update, same box) 10.72 against 11.2 with three stages (two blocks per CU), 10.84 with two lanes per
+// row and 11.4 with 128 x 64 tiles.  A PPO_HIP_TUNING build reads "PPO_HIP_BX6" = "bn[:stages[:four_lanes]]"
+// (0: off).
 template <int EPI>
 int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
   auto fits = [](const float* c, int64_t rows, int64_t ld) {
@@ -299,22 +300,34 @@ int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
     if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && reinterpret_cast<uintptr_t>(p.vec) % 16 != 0)
       return PPO_EUNSUPPORTED;
   }
-  int bn = 128;
+  int bn = 128, ns = 2, q4 = 1;
 #ifdef PPO_HIP_TUNING
-  if (const char* e = std::getenv("PPO_HIP_BX6")) bn = std::atoi(e);
-  if (bn != 64 && bn != 128) return PPO_EUNSUPPORTED;
+  if (const char* e = std::getenv("PPO_HIP_BX6")) {  // "bn[:ns[:q4]]"
+    bn = std::atoi(e);
+    if (const char* c = std::strchr(e, ':')) {
+      ns = std::atoi(c + 1);
+      if (const char* c2 = std::strchr(c + 1, ':')) q4 = std::atoi(c2 + 1);
+    }
+  }
+  if ((bn != 64 && bn != 128) || (ns != 2 && ns != 3)) return PPO_EUNSUPPORTED;
 #endif
   int blocks;
   if (int rc = assign_blocks(g, count, 128, bn, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
-#ifdef PPO_HIP_TUNING
-  if (bn == 64) {
-    hipLaunchKernelGGL((gemm_nt_bx6_kernel<64, 2, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, s, g);
     return check_launch(name);
+  };
+#ifdef PPO_HIP_TUNING
+  if (bn == 64 || ns == 3 || !q4) {
+    if (bn == 64 && ns == 2) return q4 ? go(gemm_nt_bx6_kernel<64, 3, EPI, 2, true>) : go(gemm_nt_bx6_kernel<64, 3, EPI, 2, false>);
+    if (bn == 64) return q4 ? go(gemm_nt_bx6_kernel<64, 2, EPI, 3, true>) : go(gemm_nt_bx6_kernel<64, 2, EPI, 3, false>);
+    if (ns == 3) return q4 ? go(gemm_nt_bx6_kernel<128, 2, EPI, 3, true>) : go(gemm_nt_bx6_kernel<128, 2, EPI, 3, false>);
+    return go(gemm_nt_bx6_kernel<128, 3, EPI, 2, false>);
   }
 #endif
-  hipLaunchKernelGGL((gemm_nt_bx6_kernel<128, 2, EPI>), dim3(blocks), dim3(kThreads), 0, s, g);
-  return check_launch(name);
+  // two LDS stages (48 KiB with 128 x 128 tiles): three blocks per CU
+  return go(gemm_nt_bx6_kernel<128, 3, EPI, 2, true>);
 }
 
 // Tile of the persistent NT launches: 0 = none (gemm_nt_kernel only).  A PPO_HIP_TUNING build reads `var`

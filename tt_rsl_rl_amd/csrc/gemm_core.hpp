@@ -682,6 +682,7 @@ __device__ inline TileCoord tile_at(const Group& g, int t) {
 }
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kDropOffset = 0x80000000u;  // past every output buffer (the host keeps them under 2 GiB)
 
 // Raw buffer over a row-major [rows, ld] fp32 output (null: a zero-length buffer, every store dropped).
@@ -1459,13 +1460,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 // ------------------------------------------------------------------------------------------------------------------
 // NT (forward / input-grad) on the bf16 matrix cores at fp32 accuracy, with the part products of the weight-grad's
 // bf16x6 kernel above: one BM x BN output tile per block (BM = 128, BN = 128 or 64; 4 waves in 2 x 2, each
-// 64 x BN / 2), 16-deep k-slabs.  Both operands are k-contiguous: thread t stages row t / 2 of a 128-row operand slab,
-// k-half t % 2 (8 consecutive k: two 16-byte loads), splits it and writes each part as one 16-byte chunk of a [rows][16]
-// bf16 plane (chunks XOR-swapped on bit 3 of the row as in the weight-grad kernel); a 64-row B slab (BN = 64) is
-// staged by the first two waves.  The accumulators have the fp32 NT kernels' layout (B fragment first), so the
-// persistent kernel's epilogues finish the tile, through patches in the (then free) stage memory.
+// 64 x BN / 2), 16-deep k-slabs in NS LDS stages (two: 48 KiB with 128 x 128 tiles, three blocks per CU).  Both
+// operands are k-contiguous: each staged row is read by four lanes (Q4, one 16-byte load of 4 consecutive k each) or
+// two (two 16-byte loads of 8 k each), split into its bf16 parts and written to [rows][16] bf16 planes (16-byte
+// chunks XOR-swapped on bit 3 of the row as in the weight-grad kernel).  A slab's loads go out NS iterations before
+// its MFMAs into one of two register buffers, and its split lands in LDS one iteration later.  The accumulators have
+// the fp32 NT kernels' layout (B fragment first), so the persistent kernel's epilogues finish the tile, through
+// patches in the (then free) stage memory.
 // ------------------------------------------------------------------------------------------------------------------
-template <int BN, int OCC, int EPI>
+template <int BN, int OCC, int EPI, int NS, bool Q4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_bx6_kernel(
     const Group g) {
   static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_ELU || EPI == EPI_ELU_GRAD || EPI == EPI_STORE,
@@ -1475,7 +1478,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   constexpr int TM = 2, TN = BN / 64;
   constexpr int PLANE_A = BM * BK * 2, PLANE_B = BN * BK * 2;  // bytes of one part of one operand
   constexpr int STAGE = 3 * (PLANE_A + PLANE_B);
-  constexpr int NS = 3;
+  static_assert(NS == 2 || NS == 3, "LDS stages");
   constexpr int PS = 36;
   static_assert(4 * 32 * PS * 4 <= NS * STAGE, "epilogue patches fit in the stage memory");
   __shared__ __align__(16) unsigned char lds[NS * STAGE];
@@ -1491,42 +1494,76 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave >> 1, wn = wave & 1;
 
-  const int sr = tid >> 1, sh = tid & 1;  // staged row, k-half
-  const bool stage_b = BN == 128 || sr < BN;
+  // staging: Q4 -- four lanes per row, each one 16-byte load of 4 consecutive k (a wave's load covers 16 rows x 64
+  // bytes), parts written as 8-byte halves of the chunks; else two lanes per row, each two 16-byte loads of 8
+  // consecutive k (32 rows x 2 x 32 bytes), parts written as whole 16-byte chunks
+  constexpr int LPR = Q4 ? 4 : 2;                 // lanes per staged row
+  constexpr int RPP = kThreads / LPR;             // rows per staging pass
+  constexpr int NA = BM / RPP;                    // A rows per thread
+  constexpr int NB = BN >= RPP ? BN / RPP : 1;    // B rows per thread
+  constexpr int LD = Q4 ? 1 : 2;                  // 16-byte loads per staged row
+  const int sr = tid / LPR, sq = tid % LPR;       // first staged row, k part
+  const bool stage_b = BN >= RPP || sr < BN;
   // (plain 16-byte global loads: this compiler turns element reads of __builtin_amdgcn_raw_buffer_load_b128's result
   // into one 4-byte load)
-  const float* const arow = A + static_cast<int64_t>(min(row0 + sr, M - 1)) * lda + 8 * sh;
-  const float* const brow = B + static_cast<int64_t>(min(col0 + (stage_b ? sr : 0), N - 1)) * ldb + 8 * sh;
-  const int swz_w = sr * 32 + 16 * (sh ^ ((sr >> 3) & 1));
-  u32x4 stage_v[4];
-  auto load_slab = [&](int kt) {  // the slab index is clamped into [0, nk): the look-ahead past the end re-reads
+  const float* arow[NA];
+  const float* brow[NB];
+  int swz[NA > NB ? NA : NB];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+    arow[i] = A + static_cast<int64_t>(min(row0 + sr + i * RPP, M - 1)) * lda + (16 / LPR) * sq;
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+    brow[i] = B + static_cast<int64_t>(min(col0 + (stage_b ? sr + i * RPP : 0), N - 1)) * ldb + (16 / LPR) * sq;
+#pragma unroll
+  for (int i = 0; i < (NA > NB ? NA : NB); ++i) {  // byte offset of the thread's piece of row sr + i RPP in a plane
+    const int r = sr + i * RPP;
+    swz[i] = Q4 ? r * 32 + 16 * ((sq >> 1) ^ ((r >> 3) & 1)) + 8 * (sq & 1) : r * 32 + 16 * (sq ^ ((r >> 3) & 1));
+  }
+  // two register buffers: slab s is loaded NS iterations before its MFMAs and split into LDS one iteration later
+  constexpr int NV = (NA + NB) * LD;
+  u32x4 stage_v[2][NV];
+  auto load_slab = [&](int kt, int rb) {  // the slab index is clamped into [0, nk): the look-ahead past the end re-reads
     const int k0 = min(kt, nk - 1) * BK;
-    stage_v[0] = *reinterpret_cast<const u32x4*>(arow + k0);
-    stage_v[1] = *reinterpret_cast<const u32x4*>(arow + k0 + 4);
+    u32x4* const sv = stage_v[rb];
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+#pragma unroll
+      for (int l = 0; l < LD; ++l) sv[i * LD + l] = *reinterpret_cast<const u32x4*>(arow[i] + k0 + 4 * l);
     if (stage_b) {
-      stage_v[2] = *reinterpret_cast<const u32x4*>(brow + k0);
-      stage_v[3] = *reinterpret_cast<const u32x4*>(brow + k0 + 4);
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int l = 0; l < LD; ++l) sv[(NA + i) * LD + l] = *reinterpret_cast<const u32x4*>(brow[i] + k0 + 4 * l);
     }
   };
-  auto split_store = [&](int stage) {
+  auto split_store = [&](int stage, int rb) {
     unsigned char* st = lds + stage * STAGE;
+    const u32x4* const sv = stage_v[rb];
 #pragma unroll
-    for (int o = 0; o < 2; ++o) {
-      if (o == 1 && !stage_b) break;
-      uint32_t w[8], h[4], md[4], l[4];
+    for (int o = 0; o < NA + NB; ++o) {
+      if (o >= NA && !stage_b) break;
+      const int i = o < NA ? o : o - NA;
+      const int plane = o < NA ? PLANE_A : PLANE_B;
+      unsigned char* row = st + (o < NA ? 0 : 3 * PLANE_A) + swz[i];
+      uint32_t w[4 * LD];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[e] = stage_v[2 * o][e];
-        w[4 + e] = stage_v[2 * o + 1][e];
+      for (int l = 0; l < LD; ++l)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * l + e] = sv[o * LD + l][e];
+      uint32_t h[2 * LD], md[2 * LD], lo[2 * LD];
+#pragma unroll
+      for (int q = 0; q < 2 * LD; ++q)
+        split_bf16x3(__builtin_bit_cast(float, w[2 * q]), __builtin_bit_cast(float, w[2 * q + 1]), h[q], md[q], lo[q]);
+      if constexpr (Q4) {
+        *reinterpret_cast<u32x2*>(row) = u32x2{h[0], h[1]};
+        *reinterpret_cast<u32x2*>(row + plane) = u32x2{md[0], md[1]};
+        *reinterpret_cast<u32x2*>(row + 2 * plane) = u32x2{lo[0], lo[1]};
+      } else {
+        *reinterpret_cast<u32x4*>(row) = u32x4{h[0], h[1], h[2], h[3]};
+        *reinterpret_cast<u32x4*>(row + plane) = u32x4{md[0], md[1], md[2], md[3]};
+        *reinterpret_cast<u32x4*>(row + 2 * plane) = u32x4{lo[0], lo[1], lo[2], lo[3]};
       }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        split_bf16x3(__builtin_bit_cast(float, w[2 * q]), __builtin_bit_cast(float, w[2 * q + 1]), h[q], md[q], l[q]);
-      const int plane = o == 0 ? PLANE_A : PLANE_B;
-      unsigned char* row = st + o * 3 * PLANE_A + swz_w;
-      *reinterpret_cast<u32x4*>(row) = u32x4{h[0], h[1], h[2], h[3]};
-      *reinterpret_cast<u32x4*>(row + plane) = u32x4{md[0], md[1], md[2], md[3]};
-      *reinterpret_cast<u32x4*>(row + 2 * plane) = u32x4{l[0], l[1], l[2], l[3]};
     }
   };
 
@@ -1544,16 +1581,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   };
 
   if (nk > 0) {
-    load_slab(0);
-    split_store(0);
-    load_slab(1);
-    split_store(1);
+    load_slab(0, 0);
+    load_slab(1, 1);
+    split_store(0, 0);
+    if constexpr (NS == 3) {
+      load_slab(2, 0);
+      split_store(1, 1);
+    }
     lds_barrier();
   }
-  int cs = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-    load_slab(kt + 2);
-    __builtin_amdgcn_sched_barrier(0);  // (the compiler would sink the loads to their use at the iteration's end)
+  // slab s is loaded into register buffer s % 2 at iteration s - NS (the first NS in the prologue) and split into
+  // LDS stage s % NS at iteration s - NS + 1, so iteration kt loads slab kt + NS and stores slab kt + NS - 1 (into the
+  // stage of slab kt - 1, which every wave finished reading before the last barrier)
+  auto step = [&](int kt, int cs, int rb_load, int rb_store) {
+    load_slab(kt + NS, rb_load);
+    __builtin_amdgcn_sched_barrier(0);  // (the compiler would sink the loads to their use)
     const unsigned char* st = lds + cs * STAGE;
     bf16x8 fa[TM][3], fb[TN][3];
 #pragma unroll
@@ -1572,11 +1614,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j][pb[t]], fa[i][pa[t]], acc[i][j], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    // the stage of slab kt + 2 is that of slab kt - 1, which every wave finished reading before the last barrier
-    split_store(cs == 0 ? 2 : cs - 1);
+    split_store(cs == 0 ? NS - 1 : cs - 1, rb_store);
     lds_barrier();
-    cs = cs == 2 ? 0 : cs + 1;
+  };
+  constexpr int RB_EVEN = NS % 2;  // the buffer iteration kt loads into, kt even
+  int cs = 0, kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    step(kt, cs, RB_EVEN, 1 - RB_EVEN);
+    cs = cs == NS - 1 ? 0 : cs + 1;
+    step(kt + 1, cs, 1 - RB_EVEN, RB_EVEN);
+    cs = cs == NS - 1 ? 0 : cs + 1;
   }
+  if (kt < nk) step(kt, cs, RB_EVEN, 1 - RB_EVEN);
   float* const patch = reinterpret_cast<float*>(lds) + wave * 32 * PS;  // every wave is past the last barrier
   nt_pipe_epilogue<TM, TN, EPI>(P, acc, row0 + wm * 64, col0 + wn * (BN / 2), patch, lane);
 }
