@@ -180,13 +180,14 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TransposeGroup g) 
 }
 
 // Weight-grad: 128 x 128 tiles; split-K over the rows, in chunks that are multiples of the deepest (64-row) slab.
-// The split count fills ONE wave of resident blocks and no more: the tile runs two blocks per CU, so 512 blocks on
-// the 256 CUs of a whole MI355X (fewer on a partitioned one).  A launch of 1,050 blocks (the humanoid weight-grads'
-// 30 tiles x 35 splits) leaves its last 26 blocks alone on the chip for a third of the kernel time; 30 x 17 = 510
-// blocks measured 280 us against 324.  The workspace query is host arithmetic (no device needed): it plans for the
+// The split count fills ONE wave of resident blocks and no more: the bf16x6 tile runs three blocks per CU (the fp32
+// one two), so 768 blocks on the 256 CUs of a whole MI355X (fewer on a partitioned one).  A launch of 1,050 blocks
+// (the humanoid weight-grads' 30 tiles x 35 splits, fp32 tile) leaves its last 26 blocks alone on the chip for a
+// third of the kernel time; 30 x 17 = 510 blocks measured 280 us against 324.  The workspace query is host arithmetic (no device needed): it plans for the
 // largest capacity, kDwMaxConcurrent, and a launch on a smaller device uses fewer splits, i.e. less workspace.
 constexpr int kDwBM = 128, kDwBN = 128, kDwChunk = 64;
-constexpr int kDwBlocksPerCu = 2;
+constexpr int kDwBlocksPerCu = 3;     // the bf16x6 kernel (168 VGPRs, 48 KiB LDS)
+constexpr int kDwF32BlocksPerCu = 2;  // the fp32 kernel, for operands without 16-byte rows
 constexpr int kDwMaxConcurrent = kDwBlocksPerCu * 256;
 
 int dw_query_capacity() {
@@ -196,10 +197,10 @@ int dw_query_capacity() {
   return kDwMaxConcurrent;
 }
 
-int dw_launch_capacity() {
+int dw_launch_capacity(int blocks_per_cu) {
   const int cus = device_info().cus;
   const int cap = dw_query_capacity();
-  return cus > 0 ? std::min(cap, kDwBlocksPerCu * cus) : cap;
+  return cus > 0 ? std::min(cap, blocks_per_cu * cus) : cap;
 }
 
 int dw_splits(int64_t tiles, int64_t rows, int capacity) {
@@ -570,7 +571,20 @@ int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t ro
     PPO_REQUIRE(extra[r].begin >= 0 && extra[r].end >= extra[r].begin && extra[r].group >= 0 &&
                     extra[r].group < PPO_MAX_PARAM_GROUPS,
                 "ppo_linear_bwd_dw_norm: extra range %d malformed", r);
-  const DwPlan plan = plan_dw(problems, count, rows, dw_launch_capacity());
+  // the bf16x6 kernel takes operands with 16-byte rows (the fp32 kernel the rest, at fewer blocks per CU)
+  bool bx6 = true;
+  for (int i = 0; i < count; ++i)
+    bx6 = bx6 && w16_ok(problems[i].dz, problems[i].lddz) && w16_ok(problems[i].x, problems[i].ldx);
+  int occ = bx6 ? kDwBlocksPerCu : kDwF32BlocksPerCu;
+#ifdef PPO_HIP_TUNING
+  const char* cfg = std::getenv("PPO_HIP_DW_CFG");  // tuning aid: other slab depths / stages / occupancies
+  if (cfg && !std::strcmp(cfg, "bx6o2")) occ = 2;
+  if (cfg && std::strcmp(cfg, "bx6o2") && std::strcmp(cfg, "bx6")) {
+    bx6 = false;
+    occ = cfg[std::strlen(cfg) - 1] - '0';
+  }
+#endif
+  const DwPlan plan = plan_dw(problems, count, rows, dw_launch_capacity(occ));
   PPO_REQUIRE(workspace != nullptr && workspace_bytes >= plan.total_floats * sizeof(float),
               "ppo_linear_bwd_dw: workspace too small (%zu < %zu)", workspace_bytes,
               plan.total_floats * sizeof(float));
@@ -608,33 +622,25 @@ int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t ro
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc;
 #ifdef PPO_HIP_TUNING
-  const char* cfg = std::getenv("PPO_HIP_DW_CFG");  // tuning aid: other slab depths / stages / occupancies
   if (cfg && !std::strcmp(cfg, "bk16s2o3")) {
     rc = launch_tn<kDwBM, kDwBN, 16, 2, 3>(g, count, s, "linear_bwd_dw");
   } else if (cfg && !std::strcmp(cfg, "bk16s3o3")) {
     rc = launch_tn<kDwBM, kDwBN, 16, 3, 3>(g, count, s, "linear_bwd_dw");
-  } else if (cfg && !std::strcmp(cfg, "bk64s2o1")) {
-    rc = launch_tn<kDwBM, kDwBN, 64, 2, 1>(g, count, s, "linear_bwd_dw");
   } else if (cfg && !std::strcmp(cfg, "bk32s2o1")) {
     rc = launch_tn<kDwBM, kDwBN, 32, 2, 1>(g, count, s, "linear_bwd_dw");
   } else if (cfg && !std::strcmp(cfg, "bk16s4o2")) {
     rc = launch_tn<kDwBM, kDwBN, 16, 4, 2>(g, count, s, "linear_bwd_dw");
-  } else if (cfg && !std::strcmp(cfg, "bk16s3o2")) {
-    rc = launch_tn<kDwBM, kDwBN, 16, 3, 2>(g, count, s, "linear_bwd_dw");
-  } else if (cfg && !std::strcmp(cfg, "bk32s3o1")) {
-    rc = launch_tn<kDwBM, kDwBN, 32, 3, 1>(g, count, s, "linear_bwd_dw");
-  } else if (cfg && !std::strcmp(cfg, "bk32s4o1")) {
-    rc = launch_tn<kDwBM, kDwBN, 32, 4, 1>(g, count, s, "linear_bwd_dw");
-  } else if (cfg && !std::strcmp(cfg, "f32")) {
-    rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
-  } else {
-    rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
-    if (rc == PPO_EUNSUPPORTED) rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
-  }
-#else
-  rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
-  if (rc == PPO_EUNSUPPORTED) rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+  } else if (cfg && !std::strcmp(cfg, "f32o2")) {
+    rc = launch_tn<kDwBM, kDwBN, 32, 2, 2>(g, count, s, "linear_bwd_dw");
+  } else if (bx6 && occ == 2) {
+    rc = launch_tn_bx6<2>(g, count, s, "linear_bwd_dw");
+  } else
 #endif
+  if (bx6) {
+    rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+  } else {
+    rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwF32BlocksPerCu>(g, count, s, "linear_bwd_dw");
+  }
   if (rc != PPO_OK) return rc;
   const int64_t blocks = norm != nullptr ? PPO_DW_NORM_BLOCKS : std::min<int64_t>(ceil_div(total, 256), 4096);
   hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);
