@@ -9,7 +9,8 @@ are timed on the resident rollout (each update = one step; inputs already in HBM
 
 Prints ONE JSON line.  Alongside the GPU figure it reports:
   * roofline: the dominant kernel's algorithmic FLOP rate (HIP events on the launch stream, timed region) against
-    the fp32 MFMA peak, and the HBM traffic per launch measured with rocprofv3 counters (profiles/, else null);
+    its MFMA ceiling (bf16x6 kernel: the dense bf16 MFMA peak over six; fp32-MFMA kernel: the fp32 MFMA peak), and
+    the HBM traffic per launch measured with rocprofv3 counters (profiles/, else null);
   * cpu_baseline: the CPU oracle's update() on this host's cores on the same workload (a bounded sample).
 """
 
@@ -30,7 +31,31 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "PPO update samples/s (fwd+bwd+Adam) and ms/update at 4096 envs×24 steps, 1 GPU"
 PEAK_FP32_MFMA_TFLOPS = 157.3
+# The bf16x6 GEMMs compute each fp32 product from six bf16 MFMA products of the operands' three-part splits: their
+# ceiling, in algorithmic fp32 FLOP/s, is the dense bf16 MFMA peak (2.5 PFLOP/s) over six.
+PEAK_BF16_MFMA_TFLOPS = 2500.0
+PEAK_BX6_TFLOPS = PEAK_BF16_MFMA_TFLOPS / 6
 PEAK_HBM_GBS = 8000.0
+
+
+def dw_arith(engine, R: int) -> str:
+    """Arithmetic of the weight-grad launch: the bf16x6 kernel runs when every problem's operands (dz and the layer
+    input) have 16-byte aligned rows, else the fp32-MFMA kernel (the library's own rule, restated on the operands the
+    engine passes)."""
+    tab = engine.table[:R]
+    lay = engine.layout
+    alg = engine.alg
+    xa = tab[:, lay.xa:lay.xa + alg.actor.obs_dim]
+    xc = tab[:, lay.xc:lay.xc + alg.critic.obs_dim]
+    if engine.recurrent:
+        sa, sc = engine.seq_a, engine.seq_c
+        ops = [(s.dgates[:R], h) for s, x in ((sa, xa), (sc, xc)) for h in (s.hs[:R], x)]
+        if engine.lstm_sync is not None:
+            ops += [(dz, x) for dz, x, *_ in engine.head_dw(sa.h[:R], sc.h[:R], R)]
+    else:
+        ops = [(dz, x) for dz, x, *_ in engine.head_dw(xa, xc, R)]
+    aligned = all(t.data_ptr() % 16 == 0 and t.stride(0) % 4 == 0 for pair in ops for t in pair)
+    return "bf16x6" if aligned else "fp32"
 
 
 def _sample_obs(workload, n, device, gen):
@@ -425,8 +450,13 @@ def main() -> int:
     if timer.enabled:
         n, t = timer.summary()[dom]
         ach = flops[dom] / (t * 1e-3) / 1e12
-        roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(ach / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": load_traffic(args.workload, dom), "kernel": dom,
+        arith = dw_arith(engine, R) if dom in ("dw", "lstm_dw") else "fp32"
+        peak = PEAK_BX6_TFLOPS if arith == "bf16x6" else PEAK_FP32_MFMA_TFLOPS
+        roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": round(peak, 2), "unit": "TFLOP/s",
+                    "frac": round(ach / peak, 4), "traffic": load_traffic(args.workload, dom), "kernel": dom,
+                    "arith": arith, "peak_basis": ("bf16 dense MFMA 2.5 PFLOP/s / 6 products per fp32 product"
+                                                   if arith == "bf16x6" else "fp32 dense MFMA"),
+                    "frac_of_fp32_mfma_peak": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
                     "flops_per_launch": flops[dom], "mean_launch_ms": round(t, 5), "launches_timed": n}
     # compute_returns() (bootstrap critic forward, GAE, advantage normalisation) on the stored rollout, timed after
     # the updates (it rewrites the same returns / advantages each call), as the runner calls it: in inference mode
@@ -451,6 +481,8 @@ def main() -> int:
         "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "gemm_arith": ("fp32 operands and results; GEMMs with 16-byte aligned operand rows as bf16x6 (three bf16 "
+                       "parts per operand, six bf16 MFMA products, fp32 accumulation), the rest on fp32 MFMA"),
         "config": {"workload": f"{args.workload}: {lstm}{len(W.linear_shapes(workload)[0])}-layer actor/critic MLPs "
                                f"{W.linear_shapes(workload)}, {workload['num_envs']} envs x {workload['steps']} steps, "
                                f"{alg.num_learning_epochs} epochs x {M} mini-batches of {R} rows, "
@@ -464,7 +496,8 @@ def main() -> int:
         "compute_returns_ms_median": round(cr_ms, 3),
         "compute_returns_plus_update_ms": round(cr_ms + statistics.median(per) * 1e3, 3),
         "update_gemm_tflops": round(gemm_total / (ms * 1e-3) / 1e12, 2),
-        "update_gemm_mfma_frac": round(gemm_total / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "update_gemm_frac_of_fp32_mfma_peak": round(gemm_total / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+        "update_gemm_frac_of_bf16x6_peak": round(gemm_total / (ms * 1e-3) / 1e12 / PEAK_BX6_TFLOPS, 4),
         "phases": phase_report,
         "roofline": roofline,
         "hbm_kernels": hbm,
