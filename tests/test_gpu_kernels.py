@@ -263,18 +263,30 @@ def test_linear_fwd_h_only(cuda):
     assert rel_err(h, _elu64(z64)) < 2e-6
 
 
-@pytest.mark.parametrize("rows", [24576, 1000, 5])
-def test_linear_bwd_dw_grouped(cuda, rows):
+@pytest.mark.parametrize("rows,padded", [(24576, False), (1000, False), (5, False), (24576, True), (1000, True),
+                                         (64, True), (5, True)])
+def test_linear_bwd_dw_grouped(cuda, rows, padded):
+    """Contiguous operands (widths 29, 1, 99: the fp32 kernel) or operands in rows padded to 16 bytes, as the update
+    stores them (the bf16x6 kernel: whole 32-row slab pairs at 24,576 and 64 rows, a clamped and zeroed tail at 1000
+    and 5); bias gradients included."""
     ops = _ops()
     torch.manual_seed(rows + 1)
     shapes = [(99, 512), (512, 256), (256, 128), (128, 29), (96, 512), (512, 256), (256, 128), (128, 1)]
+
+    def dev(t):
+        if not padded:
+            return t.to(cuda)
+        buf = torch.full((t.shape[0], -(-t.shape[1] // 4) * 4), float("nan"), device=cuda)
+        buf[:, :t.shape[1]].copy_(t)
+        return buf[:, :t.shape[1]]
+
     probs, refs = [], []
     for fin, fout in shapes:
         dz = torch.randn(rows, fout) / rows
         x = torch.randn(rows, fin)
         dw = torch.full((fout, fin), float("nan"), device=cuda)
         db = torch.full((fout,), float("nan"), device=cuda)
-        probs.append((dz.to(cuda), x.to(cuda), dw, db))
+        probs.append((dev(dz), dev(x), dw, db))
         refs.append((dw, db, dz.double().t() @ x.double(), dz.double().sum(0), dz.double().abs().sum(0)))
     # the last problem without a bias gradient (db = NULL: its column sums are skipped)
     nb = probs[-1][3]

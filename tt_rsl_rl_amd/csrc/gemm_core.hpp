@@ -1269,6 +1269,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 // split into the free one of two stages runs between the MFMA groups of the slab before it, so each wave's VALU
 // work overlaps its own MFMAs.  The fp64 bias sums come from the staged A values.
 // ------------------------------------------------------------------------------------------------------------------
+template <bool V>
+struct BoolC {
+  static constexpr bool value = V;
+};
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -1288,7 +1293,7 @@ __device__ __forceinline__ void split_bf16x3(float x0, float x1, uint32_t& hi, u
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-template <int OCC>
+template <int OCC, bool FULL>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_bx6_kernel(
     const Group g) {
   constexpr int BM = 128, BN = 128, BK = 16;
@@ -1309,6 +1314,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   const int wm = wave >> 1, wn = wave & 1;
   // slabs in pairs (the unrolled loop's two halves use the two register buffers); a slab past k_end is all zeros
   const int nk2 = (max(k_end - k_begin, 0) + 2 * BK - 1) / (2 * BK);
+  // FULL (every chunk of the launch whole slab pairs: rows and split chunks multiples of 32): no per-row clamp and
+  // no zeroing, each slab's address a wave-uniform offset from the lane's rows.  Only the blocks of the first column
+  // tile that have a bias gradient sum columns; with and without, the loop has its own copy (no branch inside it).
+  const bool want_colsum = P.colsum != nullptr && tc.tn == 0;
 
   // Staging: thread t loads the 4 columns 4 (t % 32) .. + 3 (clamped into the matrix: results past M / N are
   // discarded; ld % 4 == 0 keeps the chunk inside its row) of rows t / 32 and t / 32 + 8 of both operands' slab
@@ -1325,14 +1334,29 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   f32x4 stage_v[2][4];  // two buffers of: A rows sk, sk + 8; B rows sk, sk + 8
   // Rows past k_end load row k_end - 1 and are zeroed afterwards: unconditional loads (no branch) keep the
   // compiler's wait counts for them exact across the loop.
-  auto load_slab = [&](int kt, f32x4 (&v)[4]) {
-    const int k0 = k_begin + kt * BK;
+  // FULL: the slab's rows from a wave-uniform base and 32-bit lane offsets (the launcher checks that 16 rows of
+  // either operand span less than 2^31 bytes); the look-ahead past the end re-reads the last slab
+  const int last_k0 = k_end - k_begin - BK;
+  const uint32_t a_off[2] = {static_cast<uint32_t>((sk * lda + mc_a) * 4), static_cast<uint32_t>(((sk + 8) * lda + mc_a) * 4)};
+  const uint32_t b_off[2] = {static_cast<uint32_t>((sk * ldb + mc_b) * 4), static_cast<uint32_t>(((sk + 8) * ldb + mc_b) * 4)};
+  auto load_slab = [&](int kt, f32x4 (&v)[4]) __attribute__((always_inline)) {
+    if constexpr (FULL) {
+      const int64_t k0 = k_begin + min(kt * BK, last_k0);
+      const unsigned char* const abase = reinterpret_cast<const unsigned char*>(A + k0 * lda);
+      const unsigned char* const bbase = reinterpret_cast<const unsigned char*>(B + k0 * ldb);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int k = k0 + sk + 8 * h;
-      const int kc = min(k, k_end - 1);
-      v[h] = *reinterpret_cast<const f32x4*>(a_col + static_cast<int64_t>(kc) * lda);
-      v[2 + h] = *reinterpret_cast<const f32x4*>(b_col + static_cast<int64_t>(kc) * ldb);
+      for (int h = 0; h < 2; ++h) {
+        v[h] = *reinterpret_cast<const f32x4*>(abase + a_off[h]);
+        v[2 + h] = *reinterpret_cast<const f32x4*>(bbase + b_off[h]);
+      }
+    } else {
+      const int k0 = k_begin + kt * BK;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kc = min(k0 + sk + 8 * h, k_end - 1);
+        v[h] = *reinterpret_cast<const f32x4*>(a_col + static_cast<int64_t>(kc) * lda);
+        v[2 + h] = *reinterpret_cast<const f32x4*>(b_col + static_cast<int64_t>(kc) * ldb);
+      }
     }
   };
   auto zero_tail = [&](int kt, f32x4 (&v)[4]) {  // (applied where the values are used)
@@ -1384,13 +1408,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     return __builtin_bit_cast(bf16x8, v);
   };
 
+  auto run = [&](auto colsum_c) __attribute__((always_inline)) {
+  constexpr bool CS = decltype(colsum_c)::value;
   if (nk2 > 0) {  // slab 0 in stage 0, slab 1 in registers
     load_slab(0, stage_v[0]);
     load_slab(1, stage_v[1]);
-    zero_tail(0, stage_v[0]);
+    if constexpr (!FULL) zero_tail(0, stage_v[0]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) split_row(stage_v[0][q], q, lds);
-    add_colsum(stage_v[0]);
+    if constexpr (CS) add_colsum(stage_v[0]);
     lds_barrier();
   }
   for (int kp = 0; kp < nk2; ++kp) {
@@ -1412,7 +1438,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
           fa[i][pp] = frag(st + pp * PLANE, wm * 64 + 32 * i);
           fb[i][pp] = frag(st + (3 + pp) * PLANE, wn * 64 + 32 * i);
         }
-      zero_tail(kt + 1, stage_v[u ^ 1]);
+      if constexpr (!FULL) zero_tail(kt + 1, stage_v[u ^ 1]);
       constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
       for (int t = 0; t < 6; ++t) {
@@ -1422,11 +1448,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][pa[t]], fb[j][pb[t]], acc[i][j], 0, 0, 0);
         if (t < 4) split_row(stage_v[u ^ 1][t], t, nst);
-        if (t == 4) add_colsum(stage_v[u ^ 1]);
+        // (FULL: the look-ahead past the last slab re-reads it; it must not count twice)
+        if (t == 4 && CS && (!FULL || kt + 1 < 2 * nk2)) add_colsum(stage_v[u ^ 1]);
         __builtin_amdgcn_sched_barrier(0);
       }
       lds_barrier();
     }
+  }
+  };
+  if (!FULL || want_colsum) {  // (the general case keeps one copy: a second one would not fit the registers)
+    run(BoolC<true>{});
+  } else {
+    run(BoolC<false>{});
   }
 
   // partial store: accumulator element v of lane l is row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of its tile
@@ -1443,7 +1476,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         if (m < M && n < N) Cs[static_cast<int64_t>(m) * P.ldc + n] = acc[i][j][v];
       }
     }
-  if (P.colsum != nullptr && tc.tn == 0) {  // column 4 sc + e: the 8 row groups sk = 0 .. 7 in order
+  if (want_colsum) {  // column 4 sc + e: the 8 row groups sk = 0 .. 7 in order
     double* part = reinterpret_cast<double*>(lds);  // [8][128]
     lds_barrier();
 #pragma unroll
@@ -1727,12 +1760,20 @@ int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
 // multiple of 4); PPO_EUNSUPPORTED otherwise.
 template <int OCC>
 int launch_tn_bx6(Group& g, int count, hipStream_t s, const char* name) {
-  for (int i = 0; i < count; ++i)
-    if (!w16_ok(g.p[i].A, g.p[i].lda) || !w16_ok(g.p[i].B, g.p[i].ldb)) return PPO_EUNSUPPORTED;
+  bool full = true;  // every split chunk whole slab pairs, 16 rows of an operand under 2^31 bytes
+  for (int i = 0; i < count; ++i) {
+    const Problem& p = g.p[i];
+    if (!w16_ok(p.A, p.lda) || !w16_ok(p.B, p.ldb)) return PPO_EUNSUPPORTED;
+    full = full && p.K % 32 == 0 && p.k_chunk % 32 == 0 && 16 * std::max(p.lda, p.ldb) * 4 < (int64_t(1) << 31);
+  }
   int blocks;
   if (int rc = assign_blocks(g, count, 128, 128, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
-  hipLaunchKernelGGL((gemm_tn_bx6_kernel<OCC>), dim3(blocks), dim3(kThreads), 0, s, g);
+  if (full) {
+    hipLaunchKernelGGL((gemm_tn_bx6_kernel<OCC, true>), dim3(blocks), dim3(kThreads), 0, s, g);
+  } else {  // (the clamped, zeroed rows need more registers than three blocks per CU leave: two)
+    hipLaunchKernelGGL((gemm_tn_bx6_kernel<(OCC < 2 ? OCC : 2), false>), dim3(blocks), dim3(kThreads), 0, s, g);
+  }
   return check_launch(name);
 }
 
