@@ -251,6 +251,51 @@ def test_linear_persistent_walks_several_tiles(cuda, elu):
         assert torch.isnan(out[rows:]).all() and torch.isnan(out[:, fin:]).all(), "store outside the output"
 
 
+@pytest.mark.parametrize("rows", [1, 5, 130, 24576 + 77])
+def test_linear_matrix_core_path_small_and_ragged(cuda, rows):
+    """Operands with 16-byte rows and k a multiple of 16 (the bf16x6 matrix-core kernels) at row counts below one
+    tile, ragged and above: forward with ELU (outputs of 512 and 12 columns, the second a partial column tile),
+    input-grad with ELU' from the output, weight-grad with bias sums; fp64 references, NaN in every padding column
+    of the operands (it must not reach a result) and around the outputs (nothing stored outside)."""
+    ops = _ops()
+    torch.manual_seed(rows + 13)
+
+    def padded(t):
+        buf = torch.full((t.shape[0], -(-t.shape[1] // 4) * 4 + 4), float("nan"), device=cuda)
+        buf[:, :t.shape[1]].copy_(t)
+        return buf[:, :t.shape[1]]
+
+    shapes = [(112, 512), (64, 12)]
+    probs, refs = [], []
+    for fin, fout in shapes:
+        x = torch.randn(rows, fin)
+        w = torch.randn(fout, fin) / math.sqrt(fin)
+        b = torch.randn(fout)
+        out = torch.full((rows + 2, fout + 4), float("nan"), device=cuda)
+        probs.append((padded(x), w.to(cuda), b.to(cuda), None, out[:rows, :fout]))
+        refs.append((out, fout, _elu64(x.double() @ w.double().t() + b.double())))
+    ops.linear_fwd(probs, rows, elu=True)
+    for out, fout, ref in refs:
+        assert rel_err(out[:rows, :fout], ref) < 2e-6
+        assert torch.isnan(out[rows:]).all() and torch.isnan(out[:, fout:]).all()
+
+    dz = torch.randn(rows, 256)
+    w = torch.randn(256, 128) / 16
+    zp = torch.randn(rows, 128) * 2
+    hp = torch.where(zp > 0, zp, torch.expm1(zp))
+    out = torch.full((rows + 2, 132), float("nan"), device=cuda)
+    ops.linear_bwd_dx([(padded(dz), w.to(cuda), padded(hp), out[:rows, :128])], rows, elu_from_output=True)
+    ref = (dz.double() @ w.double()) * torch.where(zp.double() > 0, 1.0, torch.exp(zp.double()))
+    assert rel_err(out[:rows, :128], ref) < 2e-6
+    assert torch.isnan(out[rows:]).all() and torch.isnan(out[:, 128:]).all()
+
+    dw = torch.full((256, 128), float("nan"), device=cuda)
+    db = torch.full((256,), float("nan"), device=cuda)
+    ops.linear_bwd_dw([(padded(dz), padded(hp), dw, db)], rows)
+    assert rel_err(dw, dz.double().t() @ hp.double()) < 2e-6
+    assert ((db.cpu().double() - dz.double().sum(0)).abs() / dz.double().abs().sum(0)).max().item() < 1e-6
+
+
 def test_linear_fwd_h_only(cuda):
     """With ELU the pre-activation output may be omitted: h alone is written, z's buffer is untouched."""
     ops = _ops()

@@ -288,7 +288,7 @@ int launch_nt_pipe(Group& g, int count, hipStream_t s, const char* name) {
 // (ms per update, same box) 10.72 against 11.2 with three stages (two blocks per CU), 10.84 with two lanes per
 // row and 11.4 with 128 x 64 tiles.  A PPO_HIP_TUNING build reads "PPO_HIP_BX6" = "bn[:stages[:four_lanes]]"
 // (0: off).
-template <int EPI>
+template <int EPI, bool BKM = false>
 int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
   auto fits = [](const float* c, int64_t rows, int64_t ld) {
     return c == nullptr || (w16_ok(c, ld) && rows * ld * 4 < (int64_t(1) << 31));
@@ -311,6 +311,9 @@ int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
     }
   }
   if ((bn != 64 && bn != 128) || (ns != 2 && ns != 3)) return PPO_EUNSUPPORTED;
+  if (BKM && (bn != 128 || !q4 || ns != 2)) return PPO_EUNSUPPORTED;
+  if (const char* e = std::getenv("PPO_HIP_BX6_KMAJOR"); BKM && e != nullptr && std::atoi(e) == 0)
+    return PPO_EUNSUPPORTED;
 #endif
   int blocks;
   if (int rc = assign_blocks(g, count, 128, bn, name, blocks)) return rc;
@@ -319,6 +322,7 @@ int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, s, g);
     return check_launch(name);
   };
+  if constexpr (BKM) return go(gemm_nt_bx6_kernel<128, 3, EPI, 2, true, true>);
 #ifdef PPO_HIP_TUNING
   if (bn == 64 || ns == 3 || !q4) {
     if (bn == 64 && ns == 2) return q4 ? go(gemm_nt_bx6_kernel<64, 3, EPI, 2, true>) : go(gemm_nt_bx6_kernel<64, 3, EPI, 2, false>);
@@ -499,14 +503,13 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
   if (int rc = check_dx_workspace(problems, count, workspace, workspace_bytes, offs, who)) return rc;
   float* ws = static_cast<float*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (int rc = launch_transposes(problems, count, ws, offs, s)) return rc;
   Group g{};
   int max_n = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_linear_bwd_dx_problem& q = problems[i];
     Problem& p = g.p[i];
     p.A = q.dz; p.lda = q.lddz;
-    p.B = ws + offs[i]; p.ldb = round4(q.out_features);
+    p.B = q.w; p.ldb = q.in_features;
     p.C = q.dz_prev; p.ldc = q.lddz_prev;
     p.aux = q.z_prev; p.ldaux = q.ldz_prev;
     p.M = static_cast<int>(rows); p.N = q.in_features; p.K = q.out_features;
@@ -515,10 +518,20 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
     p.elu_from_output = elu_source == PPO_ELU_FROM_OUTPUT;
     max_n = std::max(max_n, q.in_features);
   }
-  // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
+  // the bf16x6 kernel reads the weights as stored (k-major, 16-byte rows): no transpose
+  const int krc = any_act ? launch_nt_bx6<EPI_ELU_GRAD, true>(g, count, s, "linear_bwd_dx_elu")
+                          : launch_nt_bx6<EPI_STORE, true>(g, count, s, "linear_bwd_dx");
+  if (krc != PPO_EUNSUPPORTED) return krc;
+  // else w^T (k-contiguous) into the workspace for the other kernels
+  if (int rc = launch_transposes(problems, count, ws, offs, s)) return rc;
+  for (int i = 0; i < count; ++i) {
+    g.p[i].B = ws + offs[i];
+    g.p[i].ldb = round4(problems[i].out_features);
+  }
   const int brc = any_act ? launch_nt_bx6<EPI_ELU_GRAD>(g, count, s, "linear_bwd_dx_elu")
                           : launch_nt_bx6<EPI_STORE>(g, count, s, "linear_bwd_dx");
   if (brc != PPO_EUNSUPPORTED) return brc;
+  // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
   const int pt = pipe_tile("PPO_HIP_PIPE_DX", max_n > 128 ? 3 : 2);
   const int prc = any_act ? launch_nt_pipe_tile<EPI_ELU_GRAD>(pt, g, count, s, "linear_bwd_dx_elu")
                           : launch_nt_pipe_tile<EPI_STORE>(pt, g, count, s, "linear_bwd_dx");

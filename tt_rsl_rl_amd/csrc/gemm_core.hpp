@@ -1501,12 +1501,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 // the fp32 NT kernels' layout (B fragment first), so the persistent kernel's epilogues finish the tile, through
 // patches in the (then free) stage memory.
 // ------------------------------------------------------------------------------------------------------------------
-template <int BN, int OCC, int EPI, int NS, bool Q4>
+template <int BN, int OCC, int EPI, int NS, bool Q4, bool BKM = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_bx6_kernel(
     const Group g) {
   static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_ELU || EPI == EPI_ELU_GRAD || EPI == EPI_STORE,
                 "bf16x6 NT: forward / input-grad epilogues");
   static_assert(BN == 128 || BN == 64, "tile");
+  static_assert(!BKM || (BN == 128 && Q4), "k-major B: 128-wide tiles, four lanes per A row");
   constexpr int BM = 128, BK = 16;
   constexpr int TM = 2, TN = BN / 64;
   constexpr int PLANE_A = BM * BK * 2, PLANE_B = BN * BK * 2;  // bytes of one part of one operand
@@ -1545,9 +1546,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
   for (int i = 0; i < NA; ++i)
     arow[i] = A + static_cast<int64_t>(min(row0 + sr + i * RPP, M - 1)) * lda + (16 / LPR) * sq;
+  // BKM: B is k-major (B[k][n], the weights of an input-grad as stored); thread t loads columns 4 (t % 32) .. + 3
+  // (clamped into the row; ldb % 4 == 0) of slab rows t / 32 and t / 32 + 8, as the weight-grad kernel stages
+  const int bsc = tid & 31, bsk = tid >> 5;
+  int boff[2];
+  if constexpr (BKM) {
+    const float* const bcol = B + min(col0 + 4 * bsc, ((N - 1) >> 2) << 2);
 #pragma unroll
-  for (int i = 0; i < NB; ++i)
-    brow[i] = B + static_cast<int64_t>(min(col0 + (stage_b ? sr + i * RPP : 0), N - 1)) * ldb + (16 / LPR) * sq;
+    for (int h = 0; h < 2; ++h) {
+      brow[h] = bcol + static_cast<int64_t>(bsk + 8 * h) * ldb;
+      const int kr = bsk + 8 * h;  // [16 k][128 n] plane, 8-byte chunk index XOR-ed with 8 (k % 4)
+      boff[h] = kr * (BN * 2) + (((bsc) ^ (8 * (kr & 3))) << 3);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+      brow[i] = B + static_cast<int64_t>(min(col0 + (stage_b ? sr + i * RPP : 0), N - 1)) * ldb + (16 / LPR) * sq;
+  }
 #pragma unroll
   for (int i = 0; i < (NA > NB ? NA : NB); ++i) {  // byte offset of the thread's piece of row sr + i RPP in a plane
     const int r = sr + i * RPP;
@@ -1563,7 +1578,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     for (int i = 0; i < NA; ++i)
 #pragma unroll
       for (int l = 0; l < LD; ++l) sv[i * LD + l] = *reinterpret_cast<const u32x4*>(arow[i] + k0 + 4 * l);
-    if (stage_b) {
+    if constexpr (BKM) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) sv[NA + h] = *reinterpret_cast<const u32x4*>(brow[h] + static_cast<int64_t>(k0) * ldb);
+    } else if (stage_b) {
 #pragma unroll
       for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -1578,7 +1596,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       if (o >= NA && !stage_b) break;
       const int i = o < NA ? o : o - NA;
       const int plane = o < NA ? PLANE_A : PLANE_B;
-      unsigned char* row = st + (o < NA ? 0 : 3 * PLANE_A) + swz[i];
+      unsigned char* row = st + (o < NA ? swz[i] : 3 * PLANE_A + (BKM ? boff[i] : swz[i]));
       uint32_t w[4 * LD];
 #pragma unroll
       for (int l = 0; l < LD; ++l)
@@ -1612,6 +1630,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   auto frag = [&](const unsigned char* pl, int r) {
     return *reinterpret_cast<const bf16x8*>(pl + r * 32 + 16 * (fc ^ ((r >> 3) & 1)));
   };
+  // BKM: the B operand of 32 columns by transposing reads of the k-major plane, as in the weight-grad kernel
+  const int grp = lane >> 4, gi = lane & 3, gr = (lane >> 2) & 3;
+  const int rd_k = 8 * (grp >> 1) + gr, rd_c = 4 * (grp & 1) + gi;
+  auto frag_t = [&](const unsigned char* pl, int col32) {
+    const int c = col32 / 4 + rd_c;
+    auto off = [](int kk, int cc) { return kk * (BN * 2) + ((cc ^ (8 * (kk & 3))) << 3); };
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(pl + off(rd_k, c)));
+    const i16x4 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(pl + off(rd_k + 4, c)));
+    typedef short i16x8 __attribute__((ext_vector_type(8)));
+    const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, v);
+  };
 
   if (nk > 0) {
     load_slab(0, 0);
@@ -1636,7 +1667,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[i][pp] = frag(st + pp * PLANE_A, wm * 64 + 32 * i + fr);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j][pp] = frag(st + 3 * PLANE_A + pp * PLANE_B, wn * (BN / 2) + 32 * j + fr);
+      for (int j = 0; j < TN; ++j)
+        fb[j][pp] = BKM ? frag_t(st + 3 * PLANE_A + pp * PLANE_B, wn * (BN / 2) + 32 * j)
+                        : frag(st + 3 * PLANE_A + pp * PLANE_B, wn * (BN / 2) + 32 * j + fr);
     }
     constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
