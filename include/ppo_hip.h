@@ -156,7 +156,8 @@ int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t count, int64_
  * (torch's elu_backward on the input).  z_prev == NULL means no activation (plain dx = dz w).  With
  * elu_source = PPO_ELU_FROM_OUTPUT, z_prev holds h = elu(z) instead and act' = 1 if h > 0 else h + 1 (the same
  * derivative, exp(z) = expm1(z) + 1, evaluated from the forward's output so z need not be stored).
- * The workspace (ppo_linear_bwd_dx_workspace_bytes, 16-byte aligned) receives w^T of every problem.
+ * The workspace (ppo_linear_bwd_dx_workspace_bytes, 16-byte aligned) receives w^T of every problem when the
+ * weights cannot be read as stored (rows not 16-byte aligned); it is required either way.
  * Replaces autograd's mm backward + EluBackward (rsl_rl/algorithms/ppo.py:298). */
 typedef struct ppo_linear_bwd_dx_problem {
   const float* dz; int64_t lddz;         /* [rows, out] */
