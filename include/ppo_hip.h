@@ -130,9 +130,12 @@ int ppo_host_randperm_range(uint8_t* generator_state, size_t state_bytes, int64_
 int ppo_host_rng_skip(uint8_t* generator_state, size_t state_bytes, int64_t draws);
 
 /* ------------------------------------------------------------------------------------------------------------------
- * A6  Linear layers of rsl_rl/modules/mlp.py:27-95 (nn.Linear + nn.ELU), forward and hand-written backward, as fp32
- * MFMA GEMMs.  One call runs up to PPO_MAX_LINEAR_PROBLEMS independent problems (e.g. actor and critic) over the
- * same number of rows in a single grouped launch.  Weights use torch's layout: w[out, in], row-major.
+ * A6  Linear layers of rsl_rl/modules/mlp.py:27-95 (nn.Linear + nn.ELU), forward and hand-written backward, as
+ * fp32-accurate MFMA GEMMs: where every operand of a call has 16-byte aligned rows (and, forward / input-grad, k is a
+ * multiple of 16) on the bf16 matrix cores, each fp32 operand split into three bf16 parts and each fp32 product taken
+ * as six bf16 products accumulated in fp32 (error of the fp32 MFMA's order); otherwise on the fp32 MFMA.  One call
+ * runs up to PPO_MAX_LINEAR_PROBLEMS independent problems (e.g. actor and critic) over the same number of rows in a
+ * single grouped launch.  Weights use torch's layout: w[out, in], row-major.
  * ------------------------------------------------------------------------------------------------------------------ */
 #define PPO_MAX_LINEAR_PROBLEMS 8
 
