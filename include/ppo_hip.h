@@ -134,10 +134,11 @@ int ppo_host_rng_skip(uint8_t* generator_state, size_t state_bytes, int64_t draw
  * fp32-accurate MFMA GEMMs: where every operand of a call has 16-byte aligned rows (and, forward / input-grad, k is a
  * multiple of 16) on the bf16 matrix cores, each fp32 operand split into three bf16 parts and each fp32 product taken
  * as six bf16 products accumulated in fp32 (error of the fp32 MFMA's order); otherwise on the fp32 MFMA.  One call
- * runs up to PPO_MAX_LINEAR_PROBLEMS independent problems (e.g. actor and critic) over the same number of rows in a
- * single grouped launch.  Weights use torch's layout: w[out, in], row-major.
+ * runs up to PPO_MAX_LINEAR_PROBLEMS independent problems (e.g. actor and critic; the recurrent update's ten weight
+ * gradients) over the same number of rows in a single grouped launch.  Weights use torch's layout: w[out, in],
+ * row-major.
  * ------------------------------------------------------------------------------------------------------------------ */
-#define PPO_MAX_LINEAR_PROBLEMS 8
+#define PPO_MAX_LINEAR_PROBLEMS 12
 
 /* forward: z = x w^T + b; with PPO_ACT_ELU also h = elu(z) (alpha 1).  Replaces nn.Linear.forward / nn.ELU.forward.
  * With PPO_ACT_ELU either output may be NULL (not both): a backward that takes ELU' from h

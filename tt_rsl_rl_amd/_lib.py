@@ -26,7 +26,7 @@ PPO_STD_SCALAR = 0
 PPO_STD_LOG = 1
 MAX_GATHER_SEGMENTS = 16
 MAX_INTERLEAVE_FLOATS = 16
-MAX_LINEAR_PROBLEMS = 8
+MAX_LINEAR_PROBLEMS = 12
 MAX_PARAM_GROUPS = 4
 MAX_ACTIONS = 64
 DW_NORM_BLOCKS = 512

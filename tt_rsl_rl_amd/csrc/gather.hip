@@ -9,6 +9,8 @@
 // segment widths: each wave derives it once per pass (from a copy of the segment table in LDS) and then moves
 // kRowsPerIter rows per iteration, issuing all their loads before any store so a wave waits for memory once per
 // iteration rather than once per segment.
+#include <cstdlib>
+
 #include "common.hpp"
 
 #pragma clang fp contract(off)
@@ -28,9 +30,13 @@ typedef const uint32_t __attribute__((address_space(1))) global_u32;
 
 constexpr int kGatherThreads = 256;
 constexpr int kWavesPerBlock = kGatherThreads / kWave;
-constexpr int kSlots = 8;        // flat columns per lane per pass: 512 floats of a row
-constexpr int kRowsPerIter = 2;  // rows in flight per wave
 
+constexpr int kGatherRowsPerIter = 4;
+
+// kSlots: flat columns per lane per pass (64 kSlots floats of a row; the launcher takes the fewest that cover a row,
+// up to 8); kRowsPerIter: rows whose loads a wave has in flight at once (4: 96 against 105 us with 2 for the humanoid
+// table's 98,304 rows of 295 copied floats, 131 us with 8)
+template <int kSlots, int kRowsPerIter>
 __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const int64_t* __restrict__ perm, int64_t rows,
                                                                      int64_t src_rows, GatherArgs args,
                                                                      float* __restrict__ dst, int64_t dst_stride) {
@@ -212,11 +218,30 @@ extern "C" int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_ro
     PPO_REQUIRE(total <= INT32_MAX / 2, "ppo_gather_rows: rows of %lld floats are too wide", (long long)total);
   }
   args.prefix[num_segments] = static_cast<int32_t>(total);
-  const int64_t blocks =
-      std::min<int64_t>(ceil_div(rows, static_cast<int64_t>(kWavesPerBlock) * kRowsPerIter), 65536);
-  hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGatherThreads), 0,
-                     static_cast<hipStream_t>(stream), perm, rows, src_rows, args, dst, dst_stride);
-  return check_launch("gather_rows_kernel");
+  // the fewest slots that cover a row (a slot past the row still issues its load), 8 for wider rows (more passes)
+  const int slots = static_cast<int>(std::min<int64_t>(ceil_div(total, static_cast<int64_t>(kWave)), 8));
+  auto go = [&](auto kernel, int r) {
+    const int64_t blocks = std::min<int64_t>(ceil_div(rows, static_cast<int64_t>(kWavesPerBlock) * r), 65536);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGatherThreads), 0,
+                       static_cast<hipStream_t>(stream), perm, rows, src_rows, args, dst, dst_stride);
+    return check_launch("gather_rows_kernel");
+  };
+#ifdef PPO_HIP_TUNING
+  if (const char* e = std::getenv("PPO_HIP_GATHER_ROWS"); e != nullptr && std::atoi(e) == 2) {
+    return slots <= 4 ? go(gather_rows_kernel<4, 2>, 2) : go(gather_rows_kernel<8, 2>, 2);
+  }
+#endif
+  constexpr int R = kGatherRowsPerIter;
+  switch (slots) {
+    case 1: return go(gather_rows_kernel<1, R>, R);
+    case 2: return go(gather_rows_kernel<2, R>, R);
+    case 3: return go(gather_rows_kernel<3, R>, R);
+    case 4: return go(gather_rows_kernel<4, R>, R);
+    case 5: return go(gather_rows_kernel<5, R>, R);
+    case 6: return go(gather_rows_kernel<6, R>, R);
+    case 7: return go(gather_rows_kernel<7, R>, R);
+    default: return go(gather_rows_kernel<8, R>, R);
+  }
 }
 
 extern "C" int ppo_obs_normalize(const float* x, int64_t ldx, float* y, int64_t ldy, int64_t rows, int32_t width,

@@ -546,7 +546,8 @@ class UpdateEngine:
 
         self._issue(("gather", 0, None if perm is None else first.numel(), None if perm is None else perm.data_ptr()),
                     gather_first)
-        self.trace.zero_()
+        # (no clearing of the trace: the finalize of mini-batch i writes all 5 values of row i, and the host reads
+        # back only the rows of this update's mini-batches)
         step = first_step
         try:
             for _ in range(self.alg.num_learning_epochs):
