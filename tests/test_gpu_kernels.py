@@ -345,6 +345,34 @@ def test_linear_bwd_dw_grouped(cuda, rows, padded):
     assert rel_err(refs[-1][0], refs[-1][2]) < 2e-6
 
 
+@pytest.mark.parametrize("rows", [24576, 1000, 64, 5])
+def test_linear_bwd_dw_narrow_tiles(cuda, rows):
+    """Problems at most 64 inputs wide (the 48-wide first layers of the flat and recurrent workloads, 64, 33 and 1)
+    run on 128 x 64 tiles with half the splits of the full-width problems in the same launch; operands in rows padded
+    to 16 bytes with NaN in the padding, fp64 references, bias gradients included."""
+    ops = _ops()
+    torch.manual_seed(rows + 7)
+    shapes = [(48, 512), (512, 256), (64, 1024), (33, 128), (256, 12), (1, 64)]
+
+    def dev(t):
+        buf = torch.full((t.shape[0], -(-t.shape[1] // 4) * 4), float("nan"), device=cuda)
+        buf[:, :t.shape[1]].copy_(t)
+        return buf[:, :t.shape[1]]
+
+    probs, refs = [], []
+    for fin, fout in shapes:
+        dz = torch.randn(rows, fout) / rows
+        x = torch.randn(rows, fin)
+        dw = torch.full((fout, fin), float("nan"), device=cuda)
+        db = torch.full((fout,), float("nan"), device=cuda)
+        probs.append((dev(dz), dev(x), dw, db))
+        refs.append((dw, db, dz.double().t() @ x.double(), dz.double().sum(0), dz.double().abs().sum(0)))
+    ops.linear_bwd_dw(probs, rows)
+    for dw, db, rw, rb, rb_abs in refs:
+        assert rel_err(dw, rw) < 2e-6
+        assert ((db.cpu().double() - rb).abs() / rb_abs).max().item() < 1e-6
+
+
 # ----------------------------------------------------------------------------------------------------------------------
 # A8-A11 losses
 # ----------------------------------------------------------------------------------------------------------------------

@@ -220,14 +220,20 @@ struct DwPlan {
   size_t total_floats;
 };
 
+// A problem at most 64 columns wide (in_features) runs on 128 x 64 tiles in the bf16x6 kernel (half a tile's work per
+// block), so it gets half the splits of the others: every block of the launch then has about the same work.
+bool dw_narrow(const ppo_linear_bwd_dw_problem& q) { return q.in_features <= kDwBN / 2; }
+
 DwPlan plan_dw(const ppo_linear_bwd_dw_problem* probs, int count, int64_t rows, int capacity) {
   DwPlan plan{};
-  int64_t tiles = 0;
+  int64_t halves = 0;  // work in half tiles (128 x 64)
   for (int i = 0; i < count; ++i)
-    tiles += ceil_div(probs[i].out_features, kDwBM) * ceil_div(probs[i].in_features, kDwBN);
-  const int s = dw_splits(tiles, rows, capacity);
+    halves += ceil_div(probs[i].out_features, kDwBM) *
+              (dw_narrow(probs[i]) ? 1 : 2 * ceil_div(probs[i].in_features, kDwBN));
+  const int s_full = dw_splits((halves + 1) / 2, rows, capacity);
   size_t off = 0;
   for (int i = 0; i < count; ++i) {
+    const int s = dw_narrow(probs[i]) ? std::max(1, s_full / 2) : s_full;
     const int64_t chunk = ceil_div(ceil_div(rows, s), kDwChunk) * kDwChunk;
     const int splits = static_cast<int>(ceil_div(rows, chunk));
     plan.splits[i] = splits;

@@ -79,6 +79,7 @@ struct Problem {
   int32_t c_vec;            // NT epilogue: C (and C2 / aux when used) allow 16-byte accesses
   int32_t elu_from_output;  // input-grad: aux holds h = elu(z) (ELU' = 1 if h > 0 else h + 1), else z
   int32_t b16;              // NT: B allows 16-byte direct loads (set by launch_nt)
+  int32_t tn64;             // TN bf16x6: 128 x 64 output tiles (problems at most 64 columns wide)
   LstmArgs lstm;            // EPI_LSTM_*
 };
 
@@ -1273,6 +1274,10 @@ template <bool V>
 struct BoolC {
   static constexpr bool value = V;
 };
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -1293,15 +1298,26 @@ __device__ __forceinline__ void split_bf16x3(float x0, float x1, uint32_t& hi, u
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
-template <int OCC, bool FULL>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_bx6_kernel(
-    const Group g) {
-  constexpr int BM = 128, BN = 128, BK = 16;
-  constexpr int PLANE = BK * BM * 2;  // bytes of one part of one operand: [16 rows of k][128 columns] bf16
-  constexpr int STAGE = 6 * PLANE;    // 3 parts x 2 operands
-  __shared__ __align__(16) unsigned char lds[2 * STAGE];
+// Byte offset of the 8-byte chunk c (4 bf16 columns) of row k in a k-major plane of W bf16 columns: the chunk index
+// XOR-ed so that the 4 consecutive rows one transposing read takes (8 consecutive chunks each, per 32 lanes) fall on
+// all 64 banks: W = 128 (256-byte rows) 8 (k % 4); W = 64 (128-byte rows: rows k and k + 1 already on different
+// halves) 8 ((k / 2) % 2).
+template <int W>
+__device__ __forceinline__ int tn_chunk_off(int k, int c) {
+  static_assert(W == 128 || W == 64, "plane width");
+  return k * (W * 2) + ((c ^ (W == 128 ? 8 * (k & 3) : 8 * ((k >> 1) & 1))) << 3);
+}
 
-  const TileCoord tc = locate(g);
+// One BM x BN tile (BN = 128, or 64 for narrow problems: then each wave owns 64 x 32 and B is staged one row per
+// thread) of one split of the weight-grad.
+template <int BN, bool FULL>
+__device__ __forceinline__ void tn_bx6_tile(const Group& g, const TileCoord tc, unsigned char* lds) {
+  constexpr int BM = 128, BK = 16;
+  constexpr int TN = BN / 64;                  // 32-column accumulator tiles per wave
+  constexpr int PLANE = BK * BM * 2;           // bytes of one part of A: [16 rows of k][128 columns] bf16
+  constexpr int PLANE_B = BK * BN * 2;         // one part of B
+  constexpr int STAGE = 3 * (PLANE + PLANE_B);  // 3 parts x 2 operands
+  constexpr int NBR = BN == 128 ? 2 : 1;       // B rows staged per thread and slab
   const Problem& P = g.p[tc.pi];
   const float* const A = P.A;
   const float* const B = P.B;
@@ -1325,70 +1341,77 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   // chunks go to [row][column] planes (a row is 64 banks wide), the 8-byte chunk index XOR-ed with 8 (row % 4): the
   // transposing reads below take, per 32 lanes, 4 consecutive rows at 8 consecutive chunks, which this spreads over
   // all 64 banks.
+  // (BN = 64: thread t loads the B columns 4 (t % 16) .. + 3 of slab row t / 16)
   const int sc = tid & 31, sk = tid >> 5;
-  const int mc_a = min(row0 + 4 * sc, ((M - 1) >> 2) << 2), mc_b = min(col0 + 4 * sc, ((N - 1) >> 2) << 2);
+  const int bsc = BN == 128 ? sc : tid & 15, bsk = BN == 128 ? sk : tid >> 4;
+  const int mc_a = min(row0 + 4 * sc, ((M - 1) >> 2) << 2), mc_b = min(col0 + 4 * bsc, ((N - 1) >> 2) << 2);
   const float* const a_col = A + mc_a;
   const float* const b_col = B + mc_b;
-  auto chunk_off = [](int k, int c) { return k * (BM * 2) + ((c ^ (8 * (k & 3))) << 3); };
-  const int w_off0 = chunk_off(sk, sc), w_off1 = chunk_off(sk + 8, sc);
-  f32x4 stage_v[2][4];  // two buffers of: A rows sk, sk + 8; B rows sk, sk + 8
+  const int w_off0 = tn_chunk_off<BM>(sk, sc), w_off1 = tn_chunk_off<BM>(sk + 8, sc);
+  const int wb_off0 = tn_chunk_off<BN>(bsk, bsc), wb_off1 = tn_chunk_off<BN>(bsk + 8, bsc);
+  f32x4 stage_v[2][2 + NBR];  // two buffers of: A rows sk, sk + 8; B rows bsk (, bsk + 8)
   // Rows past k_end load row k_end - 1 and are zeroed afterwards: unconditional loads (no branch) keep the
   // compiler's wait counts for them exact across the loop.
   // FULL: the slab's rows from a wave-uniform base and 32-bit lane offsets (the launcher checks that 16 rows of
   // either operand span less than 2^31 bytes); the look-ahead past the end re-reads the last slab
   const int last_k0 = k_end - k_begin - BK;
   const uint32_t a_off[2] = {static_cast<uint32_t>((sk * lda + mc_a) * 4), static_cast<uint32_t>(((sk + 8) * lda + mc_a) * 4)};
-  const uint32_t b_off[2] = {static_cast<uint32_t>((sk * ldb + mc_b) * 4), static_cast<uint32_t>(((sk + 8) * ldb + mc_b) * 4)};
-  auto load_slab = [&](int kt, f32x4 (&v)[4]) __attribute__((always_inline)) {
+  const uint32_t b_off[2] = {static_cast<uint32_t>((bsk * ldb + mc_b) * 4),
+                             static_cast<uint32_t>(((bsk + 8) * ldb + mc_b) * 4)};
+  auto load_slab = [&](int kt, f32x4 (&v)[2 + NBR]) __attribute__((always_inline)) {
     if constexpr (FULL) {
       const int64_t k0 = k_begin + min(kt * BK, last_k0);
       const unsigned char* const abase = reinterpret_cast<const unsigned char*>(A + k0 * lda);
       const unsigned char* const bbase = reinterpret_cast<const unsigned char*>(B + k0 * ldb);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        v[h] = *reinterpret_cast<const f32x4*>(abase + a_off[h]);
-        v[2 + h] = *reinterpret_cast<const f32x4*>(bbase + b_off[h]);
-      }
+      for (int h = 0; h < 2; ++h) v[h] = *reinterpret_cast<const f32x4*>(abase + a_off[h]);
+#pragma unroll
+      for (int h = 0; h < NBR; ++h) v[2 + h] = *reinterpret_cast<const f32x4*>(bbase + b_off[h]);
     } else {
       const int k0 = k_begin + kt * BK;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int kc = min(k0 + sk + 8 * h, k_end - 1);
         v[h] = *reinterpret_cast<const f32x4*>(a_col + static_cast<int64_t>(kc) * lda);
+      }
+#pragma unroll
+      for (int h = 0; h < NBR; ++h) {
+        const int kc = min(k0 + bsk + 8 * h, k_end - 1);
         v[2 + h] = *reinterpret_cast<const f32x4*>(b_col + static_cast<int64_t>(kc) * ldb);
       }
     }
   };
-  auto zero_tail = [&](int kt, f32x4 (&v)[4]) {  // (applied where the values are used)
+  auto zero_tail = [&](int kt, f32x4 (&v)[2 + NBR]) {  // (applied where the values are used)
     const int k0 = k_begin + kt * BK;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      if (k0 + sk + 8 * h >= k_end) {
-        v[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        v[2 + h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      }
-    }
+    for (int h = 0; h < 2; ++h)
+      if (k0 + sk + 8 * h >= k_end) v[h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int h = 0; h < NBR; ++h)
+      if (k0 + bsk + 8 * h >= k_end) v[2 + h] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   };
-  auto split_row = [&](const f32x4& v, int q, unsigned char* st) {  // q: A row sk, A row sk + 8, B row sk, B sk + 8
+  // q: A row sk, A row sk + 8, B row bsk (, B row bsk + 8)
+  auto split_row = [&](const f32x4& v, int q, unsigned char* st) {
     uint32_t h[2], md[2], l[2];
     split_bf16x3(v[0], v[1], h[0], md[0], l[0]);
     split_bf16x3(v[2], v[3], h[1], md[1], l[1]);
-    unsigned char* c = st + (q >> 1) * 3 * PLANE + ((q & 1) ? w_off1 : w_off0);
+    const int pl = q < 2 ? PLANE : PLANE_B;
+    unsigned char* c = st + (q < 2 ? ((q & 1) ? w_off1 : w_off0) : 3 * PLANE + ((q & 1) ? wb_off1 : wb_off0));
     *reinterpret_cast<uint64_t*>(c) = (static_cast<uint64_t>(h[1]) << 32) | h[0];
-    *reinterpret_cast<uint64_t*>(c + PLANE) = (static_cast<uint64_t>(md[1]) << 32) | md[0];
-    *reinterpret_cast<uint64_t*>(c + 2 * PLANE) = (static_cast<uint64_t>(l[1]) << 32) | l[0];
+    *reinterpret_cast<uint64_t*>(c + pl) = (static_cast<uint64_t>(md[1]) << 32) | md[0];
+    *reinterpret_cast<uint64_t*>(c + 2 * pl) = (static_cast<uint64_t>(l[1]) << 32) | l[0];
   };
   double colsum_acc[4] = {0.0, 0.0, 0.0, 0.0};  // columns 4 sc + e of A over rows sk, sk + 8 of every slab, in order
-  auto add_colsum = [&](const f32x4 (&v)[4]) {
+  auto add_colsum = [&](const f32x4 (&v)[2 + NBR]) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) colsum_acc[e] += static_cast<double>(v[0][e]) + static_cast<double>(v[1][e]);
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][TN];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
@@ -1397,12 +1420,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   // rows k0 .. k0 + 3 of column d.
   const int grp = lane >> 4, gi = lane & 3, gr = (lane >> 2) & 3;
   const int rd_k = 8 * (grp >> 1) + gr, rd_c = 4 * (grp & 1) + gi;  // row (first read), chunk within 32 columns
-  auto frag = [&](const unsigned char* pl, int col32) {  // col32: first column of the 32 (a multiple of 32)
+  // (W: the plane's width in columns)
+  auto frag = [&](auto w_c, const unsigned char* pl, int col32) {  // col32: first column of the 32 (a multiple of 32)
+    constexpr int W = decltype(w_c)::value;
     const int c = col32 / 4 + rd_c;
     const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) i16x4*)(pl + chunk_off(rd_k, c)));
+        (__attribute__((address_space(3))) i16x4*)(pl + tn_chunk_off<W>(rd_k, c)));
     const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) i16x4*)(pl + chunk_off(rd_k + 4, c)));
+        (__attribute__((address_space(3))) i16x4*)(pl + tn_chunk_off<W>(rd_k + 4, c)));
     typedef short i16x8 __attribute__((ext_vector_type(8)));
     const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(bf16x8, v);
@@ -1415,7 +1440,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     load_slab(1, stage_v[1]);
     if constexpr (!FULL) zero_tail(0, stage_v[0]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) split_row(stage_v[0][q], q, lds);
+    for (int q = 0; q < 2 + NBR; ++q) split_row(stage_v[0][q], q, lds);
     if constexpr (CS) add_colsum(stage_v[0]);
     lds_barrier();
   }
@@ -1430,14 +1455,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       __builtin_amdgcn_sched_barrier(0);
       const unsigned char* st = lds + u * STAGE;
       unsigned char* nst = lds + (u ^ 1) * STAGE;
-      bf16x8 fa[2][3], fb[2][3];
+      bf16x8 fa[2][3], fb[TN][3];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int pp = 0; pp < 3; ++pp) {
 #pragma unroll
-        for (int pp = 0; pp < 3; ++pp) {
-          fa[i][pp] = frag(st + pp * PLANE, wm * 64 + 32 * i);
-          fb[i][pp] = frag(st + (3 + pp) * PLANE, wn * 64 + 32 * i);
-        }
+        for (int i = 0; i < 2; ++i) fa[i][pp] = frag(IntC<BM>{}, st + pp * PLANE, wm * 64 + 32 * i);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[j][pp] = frag(IntC<BN>{}, st + 3 * PLANE + pp * PLANE_B, wn * (BN / 2) + 32 * j);
+      }
       if constexpr (!FULL) zero_tail(kt + 1, stage_v[u ^ 1]);
       constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
@@ -1445,9 +1470,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < TN; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][pa[t]], fb[j][pb[t]], acc[i][j], 0, 0, 0);
-        if (t < 4) split_row(stage_v[u ^ 1][t], t, nst);
+        if (t < 2 + NBR) split_row(stage_v[u ^ 1][t], t, nst);
         // (FULL: the look-ahead past the last slab re-reads it; it must not count twice)
         if (t == 4 && CS && (!FULL || kt + 1 < 2 * nk2)) add_colsum(stage_v[u ^ 1]);
         __builtin_amdgcn_sched_barrier(0);
@@ -1468,8 +1493,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = col0 + wn * 64 + 32 * j + fr;
+    for (int j = 0; j < TN; ++j) {
+      const int n = col0 + wn * (BN / 2) + 32 * j + fr;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = row0 + wm * 64 + 32 * i + 8 * (v >> 2) + 4 * fc + (v & 3);
@@ -1487,6 +1512,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
       for (int r = 1; r < 8; ++r) sum += part[r * 128 + tid];
       P.colsum[static_cast<int64_t>(tc.split) * M + row0 + tid] = sum;
     }
+  }
+}
+
+template <int OCC, bool FULL>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_bx6_kernel(
+    const Group g) {
+  __shared__ __align__(16) unsigned char lds[2 * 6 * 16 * 128 * 2];  // two stages of the 128 x 128 tile's planes
+  const TileCoord tc = locate(g);
+  if (g.p[tc.pi].tn64) {
+    tn_bx6_tile<64, FULL>(g, tc, lds);
+  } else {
+    tn_bx6_tile<128, FULL>(g, tc, lds);
   }
 }
 
@@ -1801,6 +1838,15 @@ int launch_tn_bx6(Group& g, int count, hipStream_t s, const char* name) {
   }
   int blocks;
   if (int rc = assign_blocks(g, count, 128, 128, name, blocks)) return rc;
+  // problems at most 64 columns wide: 128 x 64 tiles (the split plan gave them half the others' splits)
+  blocks = 0;
+  for (int i = 0; i < count; ++i) {
+    Problem& p = g.p[i];
+    p.tn64 = p.N <= 64 ? 1 : 0;
+    p.tiles_n = static_cast<int>(ceil_div(p.N, p.tn64 ? 64 : 128));
+    p.block_begin = blocks;
+    blocks += p.tiles_m * p.tiles_n * p.splits;  // (at most the 128 x 128 count assign_blocks checked)
+  }
   if (blocks == 0) return PPO_OK;
   if (full) {
     hipLaunchKernelGGL((gemm_tn_bx6_kernel<OCC, true>), dim3(blocks), dim3(kThreads), 0, s, g);
