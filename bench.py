@@ -359,6 +359,9 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=None,
                     help="timed oracle updates for cpu_baseline (default 3; 1 for recurrent workloads)")
     ap.add_argument("--no-phase-events", action="store_true", help="do not record per-launch HIP events")
+    ap.add_argument("--census", type=int, default=None, metavar="N",
+                    help="only collect the rollout and run N updates (no timing; for a kernel census under rocprofv3: "
+                         "the kernels of N updates = this run's minus the run with N = 0)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -397,6 +400,14 @@ def main() -> int:
         alg.storage.step = alg.storage.num_transitions_per_env
         torch.manual_seed(1)
         return alg.update()
+
+    if args.census is not None:
+        torch.cuda.synchronize()
+        for _ in range(args.census):
+            one_update()
+        torch.cuda.synchronize()
+        print(json.dumps({"census_updates": args.census, "workload": args.workload}))
+        return 0
 
     for _ in range(args.warmup):
         one_update()

@@ -97,6 +97,28 @@ def test_gather_rows_bit_exact(cuda):
     assert torch.isnan(out[:, 133]).all() and torch.isnan(out[:, 135:]).all(), "gather wrote outside its columns"
 
 
+@pytest.mark.parametrize("width", [1, 63, 64, 65, 130, 190, 250, 300, 380, 420, 511, 600, 1100])
+def test_gather_rows_every_slot_count(cuda, width):
+    """Rows of every width class the launcher distinguishes (1 to 8 slots of 64 floats per lane, and rows wider than
+    512 floats, which take several passes): a float segment of `width` - 1 columns plus a keep column, gathered
+    bit-exactly from a ragged source (5,003 rows) into a NaN-filled table, nothing written outside the columns."""
+    ops = _ops()
+    torch.manual_seed(width)
+    src_rows, rows = 5003, 4999
+    wf = max(width - 1, 1)
+    xd = torch.randn(src_rows, wf + 3, device=cuda)[:, :wf]  # a strided view (leading dimension wf + 3)
+    x = xd.cpu()
+    dones = (torch.rand(src_rows, 1) < 0.5).to(torch.uint8)
+    perm = torch.randperm(src_rows)[:rows]
+    dst = torch.full((rows, wf + 8), float("nan"), device=cuda)
+    ops.gather_rows(perm.to(cuda), [ops.Segment(xd, 2), ops.Segment(dones.to(cuda), wf + 4, keep=True)], dst)
+    out = dst.cpu()
+    assert torch.equal(out[:, 2:2 + wf], x[perm])
+    assert torch.equal(out[:, wf + 4:wf + 5], 1.0 - dones[perm].float())
+    assert torch.isnan(out[:, :2]).all() and torch.isnan(out[:, 2 + wf:wf + 4]).all()
+    assert torch.isnan(out[:, wf + 5:]).all()
+
+
 @pytest.mark.parametrize("rows", [1, 1000, 98304 + 5])
 def test_interleave_columns_matches_cat(cuda, rows):
     """Column blocks of different widths and strides side by side, bit-exact (torch.cat of the same views); the

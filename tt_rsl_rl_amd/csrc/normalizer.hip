@@ -16,6 +16,7 @@ constexpr int kNormThreads = 256;
 constexpr int kColTile = 64;     // one wavefront covers 64 consecutive columns
 constexpr int kMaxSlabs = 256;   // row slabs (blocks along the rows)
 constexpr int kMaxBlocks = PPO_MAX_GATHER_SEGMENTS;
+constexpr int kUnroll = 16;   // rows per wave whose loads are in flight together
 
 struct Blocks {
   ppo_column_block b[kMaxBlocks];
@@ -25,7 +26,8 @@ struct Blocks {
 };
 
 // pass 0: per-slab column sums; pass 1: per-slab sums of (x - mean)^2 (mean from stats[0..dim)).
-// grid = (column tiles, slabs); lane = column inside the tile, wave w takes rows r0 + w, r0 + w + 4, ...
+// grid = (column tiles, slabs); lane = column inside the tile, wave w takes rows r0 + w, r0 + w + 4, ... (each row's
+// value added in that order)
 __global__ __launch_bounds__(kNormThreads) void moments_kernel(const Blocks bl, int64_t rows, int64_t slab_rows,
                                                                int pass, const double* __restrict__ stats,
                                                                double* __restrict__ partials) {
@@ -42,13 +44,27 @@ __global__ __launch_bounds__(kNormThreads) void moments_kernel(const Blocks bl, 
     const float* src = bl.b[i].src + (c - bl.col_begin[i]);
     const int64_t stride = bl.b[i].stride;
     const double mu = pass ? stats[c] : 0.0;
-    for (int64_t r = r0 + wave; r < r1; r += kNormThreads / 64) {
-      const double v = src[r * stride];
-      if (pass == 0) {
-        acc += v;
-      } else {
-        const double d = v - mu;
-        acc += d * d;
+    // kUnroll rows' loads in flight before they are added, in the same order as one row at a time (rows past the
+    // slab re-read row r0 and are not added)
+    constexpr int kStep = kNormThreads / 64;
+    for (int64_t rb = r0 + wave; rb < r1; rb += kStep * kUnroll) {
+      float x[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int64_t r = rb + u * kStep;
+        x[u] = src[(r < r1 ? r : r0) * stride];
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (rb + u * kStep < r1) {
+          const double v = x[u];
+          if (pass == 0) {
+            acc += v;
+          } else {
+            const double d = v - mu;
+            acc += d * d;
+          }
+        }
       }
     }
   }
