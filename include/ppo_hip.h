@@ -383,6 +383,29 @@ int ppo_adam_step_prenorm(float* params, float* grads, float* exp_avg, float* ex
                           double bc1, double bc2_sqrt, ppo_device_state* state, const double* norm_partials,
                           ppo_stream_t stream);
 
+/* A parameter written a second time, into a buffer with another row stride, by the Adam step that updates it: the
+ * rows x cols floats at params[begin] (row-major, row stride cols) also go to dst[r * ld_dst + c] (ld_dst >= cols;
+ * columns past cols are not touched).  For a first layer whose input width is not a multiple of 16, the forward GEMM
+ * reads a zero-padded copy of the weight with 16-float-aligned rows; written by the optimiser step itself, that copy
+ * needs no launch of its own before each mini-batch. */
+typedef struct ppo_param_mirror {
+  int64_t begin;
+  int32_t rows;
+  int32_t cols;
+  float* dst;
+  int64_t ld_dst;
+} ppo_param_mirror;
+#define PPO_MAX_PARAM_MIRRORS 2
+
+/* ppo_adam_step_prenorm that also writes up to PPO_MAX_PARAM_MIRRORS mirrored parameters (the updated values, bit
+ * for bit).  No counterpart in the reference (upstream's parameters have one layout); the mirrors' ranges must not
+ * overlap. */
+int ppo_adam_step_prenorm_mirror(float* params, float* grads, float* exp_avg, float* exp_avg_sq,
+                                 const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1,
+                                 double beta2, double eps, double bc1, double bc2_sqrt, ppo_device_state* state,
+                                 const double* norm_partials, const ppo_param_mirror* mirrors, int32_t num_mirrors,
+                                 ppo_stream_t stream);
+
 /* ppo_adam_step without a workspace argument: it allocates nothing and takes no caller memory besides its inputs and
  * outputs.  No counterpart in the reference (upstream's torch.optim.Adam allocates as it likes); it is for callers that
  * cannot allocate device memory -- code under HIP graph capture, tight training / serving loops, harnesses that

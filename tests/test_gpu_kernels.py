@@ -762,6 +762,34 @@ def test_adam_prenorm_matches_torch(cuda):
     assert L.DW_NORM_BLOCKS == partials.shape[0]
 
 
+def test_adam_prenorm_mirror_matches_prenorm(cuda):
+    """ppo_adam_step_prenorm_mirror: the flat buffers bit-identical to ppo_adam_step_prenorm's on the same inputs, and
+    each mirrored range (row-major rows x cols at any flat offset, float4 boundaries straddled) written to its
+    destination rows with the updated values bit for bit, the destination's columns past cols untouched."""
+    ops = _ops()
+    torch.manual_seed(21)
+    n = 200_003 + 1
+    bounds = torch.tensor([0, 120_000, n], dtype=torch.int64)
+    flat = [torch.randn(n, device=cuda) * s for s in (0.1, 0.5, 0.01)] + [torch.rand(n, device=cuda) * 1e-3]
+    partials = ops.grad_norm_partials(cuda)
+    partials[:, :2] = torch.rand(partials.shape[0], 2, device=cuda, dtype=torch.float64) * 1e-3
+    mirrors_spec = [(1003, 512, 99, 112), (150_001, 30, 235, 240)]  # (begin, rows, cols, ld)
+    a = [t.clone() for t in flat]
+    b = [t.clone() for t in flat]
+    dsts = [torch.full((r, ld), float("nan"), device=cuda) for _, r, _, ld in mirrors_spec]
+    mirrors = [(bg, r, c, d) for (bg, r, c, _), d in zip(mirrors_spec, dsts)]
+    for step in (1, 2):
+        for bufs, mir in ((a, None), (b, mirrors)):
+            st = ops.new_device_state(1e-3, cuda)
+            ops.adam_step(*bufs, bounds, 1.0, 0.9, 0.999, 1e-8, 1 - 0.9 ** step, (1 - 0.999 ** step) ** 0.5, st, None,
+                          prenorm=partials, mirrors=mir)
+        for x, y in zip(a, b):
+            assert torch.equal(x, y), step
+        for (bg, r, c, _), d in zip(mirrors_spec, dsts):
+            assert torch.equal(d[:, :c], b[0][bg:bg + r * c].view(r, c)), step
+            assert torch.isnan(d[:, c:]).all(), "columns past cols written"
+
+
 def test_adam_first_step_moves_by_lr(cuda):
     """tests/algorithms/test_ppo.py:492-505: the first Adam step moves every parameter by lr."""
     ops = _ops()

@@ -46,6 +46,7 @@ STRUCTS = {
     "ppo_linear_bwd_dw_problem": ("LinearBwdDwProblem", ["dz", "lddz", "x", "ldx", "dw", "db", "in_features",
                                                          "out_features", "grad_norm_group", "reserved"]),
     "ppo_grad_range": ("GradRange", ["begin", "end", "group", "reserved"]),
+    "ppo_param_mirror": ("ParamMirror", ["begin", "rows", "cols", "dst", "ld_dst"]),
     "ppo_column_block": ("ColumnBlock", ["src", "stride", "width"]),
     "ppo_loss_args": ("LossArgs", ["rows", "num_actions", "std_type", "mean", "ld_mean", "value", "ld_value",
                                    "actions", "old_mean", "old_std", "old_logp", "advantages", "old_values", "returns",
@@ -72,7 +73,7 @@ STRUCTS = {
 CONSTANTS = {"PPO_MAX_GATHER_SEGMENTS": "MAX_GATHER_SEGMENTS", "PPO_MAX_INTERLEAVE_FLOATS": "MAX_INTERLEAVE_FLOATS", "PPO_MAX_LINEAR_PROBLEMS": "MAX_LINEAR_PROBLEMS",
              "PPO_MAX_PARAM_GROUPS": "MAX_PARAM_GROUPS", "PPO_DW_NORM_BLOCKS": "DW_NORM_BLOCKS",
              "PPO_MAX_EXTRA_GRADS": "MAX_EXTRA_GRADS", "PPO_ADAM_STATIC_SCRATCH_DOUBLES": "ADAM_STATIC_SCRATCH_DOUBLES",
-             "PPO_ADAM_STATIC_MAX_PARAMS": "ADAM_STATIC_MAX_PARAMS"}
+             "PPO_ADAM_STATIC_MAX_PARAMS": "ADAM_STATIC_MAX_PARAMS", "PPO_MAX_PARAM_MIRRORS": "MAX_PARAM_MIRRORS"}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")

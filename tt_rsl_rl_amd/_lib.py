@@ -28,6 +28,7 @@ MAX_GATHER_SEGMENTS = 16
 MAX_INTERLEAVE_FLOATS = 16
 MAX_LINEAR_PROBLEMS = 12
 MAX_PARAM_GROUPS = 4
+MAX_PARAM_MIRRORS = 2
 MAX_ACTIONS = 64
 DW_NORM_BLOCKS = 512
 MAX_EXTRA_GRADS = 4
@@ -66,6 +67,10 @@ class LinearBwdDwProblem(C.Structure):
 
 class GradRange(C.Structure):
     _fields_ = [("begin", i64), ("end", i64), ("group", i32), ("reserved", i32)]
+
+
+class ParamMirror(C.Structure):
+    _fields_ = [("begin", i64), ("rows", i32), ("cols", i32), ("dst", C.c_void_p), ("ld_dst", i64)]
 
 
 class ColumnBlock(C.Structure):
@@ -171,10 +176,13 @@ _SIGNATURES = [
     ("ppo_adam_step_prenorm", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double,
                                         C.c_double, C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p,
                                         C.c_void_p]),
+    ("ppo_adam_step_prenorm_mirror", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double,
+                                               C.c_double, C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p,
+                                               C.c_void_p, i32, C.c_void_p]),
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib: C.CDLL | None = None
 

@@ -79,6 +79,26 @@ __global__ __launch_bounds__(kAdamThreads) void grad_sqnorm_kernel(const float* 
   if (threadIdx.x == 0) partials[chunk] = s;
 }
 
+// Mirrored parameters (ppo_param_mirror): element begin + r * cols + c of the flat buffer also goes to
+// dst[r * ld + c].
+struct MirrorTable {
+  int64_t begin[PPO_MAX_PARAM_MIRRORS], end[PPO_MAX_PARAM_MIRRORS], ld[PPO_MAX_PARAM_MIRRORS];
+  float* dst[PPO_MAX_PARAM_MIRRORS];
+  int32_t cols[PPO_MAX_PARAM_MIRRORS];
+  int32_t count;
+};
+
+__device__ __forceinline__ void mirror_store(const MirrorTable& mt, int64_t i, float p) {
+#pragma unroll
+  for (int k = 0; k < PPO_MAX_PARAM_MIRRORS; ++k) {
+    if (k < mt.count && i >= mt.begin[k] && i < mt.end[k]) {
+      const int64_t rel = i - mt.begin[k];
+      const int64_t r = rel / mt.cols[k];
+      mt.dst[k][r * mt.ld[k] + (rel - r * mt.cols[k])] = p;
+    }
+  }
+}
+
 struct AdamScalars {
   float max_norm, w1, b2, c2, eps, bc2_sqrt;
   double bc1;
@@ -102,7 +122,7 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
                                                             float* __restrict__ exp_avg,
                                                             float* __restrict__ exp_avg_sq, GroupTable t,
                                                             AdamScalars s, const double* __restrict__ partials,
-                                                            ppo_device_state* __restrict__ state) {
+                                                            ppo_device_state* __restrict__ state, MirrorTable mt) {
   __shared__ double red[kAdamThreads / 64];
   const int chunk = blockIdx.x;
   const int g = group_of_chunk(t, chunk);
@@ -138,6 +158,12 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
       *reinterpret_cast<float4*>(grads + i) = gr;
       *reinterpret_cast<float4*>(exp_avg + i) = m;
       *reinterpret_cast<float4*>(exp_avg_sq + i) = v;
+      if (mt.count > 0) {  // (a float4 may straddle a mirror's first or last element: per element)
+        mirror_store(mt, i, p.x);
+        mirror_store(mt, i + 1, p.y);
+        mirror_store(mt, i + 2, p.z);
+        mirror_store(mt, i + 3, p.w);
+      }
     }
   } else {
     for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
@@ -147,6 +173,7 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
       grads[i] = gr;
       exp_avg[i] = m;
       exp_avg_sq[i] = v;
+      if (mt.count > 0) mirror_store(mt, i, p);
     }
   }
 }
@@ -202,12 +229,32 @@ int static_scratch(double** out) {
 int adam_step(const char* who, float* params, float* grads, float* exp_avg, float* exp_avg_sq,
               const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1, double beta2,
               double eps, double bc1, double bc2_sqrt, ppo_device_state* state, void* workspace,
-              size_t workspace_bytes, const double* prenorm, ppo_stream_t stream) {
+              size_t workspace_bytes, const double* prenorm, ppo_stream_t stream,
+              const ppo_param_mirror* mirrors = nullptr, int num_mirrors = 0) {
   PPO_REQUIRE(params && grads && exp_avg && exp_avg_sq && state, "%s: null pointer", who);
   GroupTable t;
   int chunks = 0;
   int rc = build_table(group_begin, num_groups, t, chunks);
   if (rc != PPO_OK) return rc;
+  MirrorTable mt{};
+  PPO_REQUIRE(num_mirrors >= 0 && num_mirrors <= PPO_MAX_PARAM_MIRRORS && (num_mirrors == 0 || mirrors != nullptr),
+              "%s: %d mirrors (at most %d, with their table)", who, num_mirrors, PPO_MAX_PARAM_MIRRORS);
+  for (int k = 0; k < num_mirrors; ++k) {
+    const ppo_param_mirror& q = mirrors[k];
+    const int64_t end = q.begin + static_cast<int64_t>(q.rows) * q.cols;
+    PPO_REQUIRE(q.dst != nullptr && q.rows > 0 && q.cols > 0 && q.ld_dst >= q.cols && q.begin >= 0 &&
+                    end <= group_begin[num_groups],
+                "%s: mirror %d malformed (begin=%lld rows=%d cols=%d ld=%lld)", who, k, (long long)q.begin, q.rows,
+                q.cols, (long long)q.ld_dst);
+    for (int j = 0; j < k; ++j)
+      PPO_REQUIRE(end <= mt.begin[j] || q.begin >= mt.end[j], "%s: mirrors %d and %d overlap", who, j, k);
+    mt.begin[k] = q.begin;
+    mt.end[k] = end;
+    mt.ld[k] = q.ld_dst;
+    mt.dst[k] = q.dst;
+    mt.cols[k] = q.cols;
+  }
+  mt.count = num_mirrors;
   if (prenorm == nullptr) {
     const size_t need = workspace_bytes_for(group_begin[num_groups]);
     PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", who,
@@ -231,10 +278,10 @@ int adam_step(const char* who, float* params, float* grads, float* exp_avg, floa
   if (prenorm != nullptr) {
     if (vec) {
       hipLaunchKernelGGL((adam_kernel<true, true>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
-                         exp_avg_sq, t, s, prenorm, state);
+                         exp_avg_sq, t, s, prenorm, state, mt);
     } else {
       hipLaunchKernelGGL((adam_kernel<false, true>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads,
-                         exp_avg, exp_avg_sq, t, s, prenorm, state);
+                         exp_avg, exp_avg_sq, t, s, prenorm, state, mt);
     }
     return check_launch("adam_kernel");
   }
@@ -248,10 +295,10 @@ int adam_step(const char* who, float* params, float* grads, float* exp_avg, floa
   if (rc != PPO_OK) return rc;
   if (vec) {
     hipLaunchKernelGGL((adam_kernel<true, false>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
-                       exp_avg_sq, t, s, partials, state);
+                       exp_avg_sq, t, s, partials, state, mt);
   } else {
     hipLaunchKernelGGL((adam_kernel<false, false>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads,
-                       exp_avg, exp_avg_sq, t, s, partials, state);
+                       exp_avg, exp_avg_sq, t, s, partials, state, mt);
   }
   return check_launch("adam_kernel");
 }
@@ -278,6 +325,17 @@ extern "C" int ppo_adam_step_prenorm(float* params, float* grads, float* exp_avg
   PPO_REQUIRE(norm_partials != nullptr, "ppo_adam_step_prenorm: null norm_partials");
   return adam_step("ppo_adam_step_prenorm", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups,
                    max_grad_norm, beta1, beta2, eps, bc1, bc2_sqrt, state, nullptr, 0, norm_partials, stream);
+}
+
+extern "C" int ppo_adam_step_prenorm_mirror(float* params, float* grads, float* exp_avg, float* exp_avg_sq,
+                                            const int64_t* group_begin, int32_t num_groups, double max_grad_norm,
+                                            double beta1, double beta2, double eps, double bc1, double bc2_sqrt,
+                                            ppo_device_state* state, const double* norm_partials,
+                                            const ppo_param_mirror* mirrors, int32_t num_mirrors, ppo_stream_t stream) {
+  PPO_REQUIRE(norm_partials != nullptr, "ppo_adam_step_prenorm_mirror: null norm_partials");
+  return adam_step("ppo_adam_step_prenorm_mirror", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups,
+                   max_grad_norm, beta1, beta2, eps, bc1, bc2_sqrt, state, nullptr, 0, norm_partials, stream, mirrors,
+                   num_mirrors);
 }
 
 // The same kernels on the static scratch: the parameter count is checked against the array's capacity before any

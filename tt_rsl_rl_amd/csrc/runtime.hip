@@ -58,4 +58,4 @@ DeviceInfo device_info() {
 
 extern "C" const char* ppo_last_error(void) { return ppo::g_error; }
 
-extern "C" int ppo_abi_version(void) { return 7; }
+extern "C" int ppo_abi_version(void) { return 8; }

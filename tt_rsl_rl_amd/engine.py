@@ -159,8 +159,9 @@ class UpdateEngine:
         self.layout = TableLayout(actor.obs_dim, critic.obs_dim, self.A, keep=self.recurrent)
         self.table = torch.zeros(self.B, self.layout.width, device=self.device)  # padding columns stay zero
         self.scalars = torch.empty(self.B, 4, device=self.device)  # pack_scalars
-        # zero-padded copies of first-layer weights whose input width is not a multiple of 16 (refreshed from the
-        # parameters before every mini-batch's forward by a row gather)
+        # zero-padded copies of first-layer weights whose input width is not a multiple of 16: written by every Adam
+        # step beside the weight itself (mirrors of ppo_adam_step_prenorm_mirror) after a row gather at the start of
+        # each update; without the one-launch Adam, refreshed by a row gather before every mini-batch's forward
         self.w0_pad: dict[int, torch.Tensor] = {}
         if not self.recurrent:
             for model in (actor, critic):
@@ -170,6 +171,14 @@ class UpdateEngine:
             rows = max((w.shape[0] for w in self.w0_pad.values()), default=0)
             self.w0_rows = torch.arange(rows, dtype=torch.int64, device=self.device)
         self.grad_norm = None if self.recurrent else self._grad_norm_plan()
+        self.w0_mirrors: list[tuple] = []
+        self._w0_current = False  # inside run(): the copies were refreshed at its start and every Adam step keeps them
+        if self.grad_norm is not None and len(self.w0_pad) <= L.MAX_PARAM_MIRRORS:
+            for model in (actor, critic):
+                wp = self.w0_pad.get(id(model))
+                if wp is not None:
+                    w = model.linears[0].weight
+                    self.w0_mirrors.append((alg.flat.offsets[id(w)][0], w.shape[0], w.shape[1], wp))
         self.buf_a = ModelBuffers(actor, self.R_max, self.device)
         self.buf_c = ModelBuffers(critic, self.R_max, self.device)
         self.loss_ws = torch.empty(ops.loss_workspace_bytes(self.R_max, self.A), dtype=torch.uint8, device=self.device)
@@ -265,7 +274,7 @@ class UpdateEngine:
                 self.timer.stop(e[1])
             else:
                 name, args = e
-                if name in ("ppo_adam_step", "ppo_adam_step_prenorm"):
+                if name in ("ppo_adam_step", "ppo_adam_step_prenorm", "ppo_adam_step_prenorm_mirror"):
                     bc1, bc2_sqrt = self._bias_corrections(step)
                     args = args[:10] + (float(bc1), float(bc2_sqrt)) + args[12:]
                 L.check(getattr(lib, name)(*args), name)
@@ -342,7 +351,8 @@ class UpdateEngine:
         xa = tab[:, lay.xa:lay.xa + alg.actor.obs_dim]
         xc = tab[:, lay.xc:lay.xc + alg.critic.obs_dim]
         adv_col = self.advantage_column(tab, R)
-        self.refresh_padded_weights()
+        if not (self.w0_mirrors and self._w0_current):  # (a caller may have changed the weights since)
+            self.refresh_padded_weights()
         fa, wa0 = self._first_layer(alg.actor, tab, lay.xa, xa)
         fc, wc0 = self._first_layer(alg.critic, tab, lay.xc, xc)
         self.head_forward(fa, fc, R, w0=(wa0, wc0))
@@ -503,7 +513,8 @@ class UpdateEngine:
         tm = self.timer
         tm.start("adam")
         ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin, alg.max_grad_norm, b1, b2, alg.adam_eps,
-                      bc1, bc2_sqrt, alg.device_state, self.adam_ws, prenorm=prenorm)
+                      bc1, bc2_sqrt, alg.device_state, self.adam_ws, prenorm=prenorm,
+                      mirrors=self.w0_mirrors if prenorm is not None else None)
         tm.stop("adam")
 
     def minibatch_rows(self, i: int) -> tuple[int, int]:
@@ -546,6 +557,9 @@ class UpdateEngine:
 
         self._issue(("gather", 0, None if perm is None else first.numel(), None if perm is None else perm.data_ptr()),
                     gather_first)
+        if self.w0_mirrors:  # (then every Adam step of this run keeps the copies current)
+            self.refresh_padded_weights()
+            self._w0_current = True
         # (no clearing of the trace: the finalize of mini-batch i writes all 5 values of row i, and the host reads
         # back only the rows of this update's mini-batches)
         step = first_step
@@ -569,6 +583,7 @@ class UpdateEngine:
                         self.step_hook(self, r0, r1)
         finally:
             self._frozen = False
+            self._w0_current = False
         self._warm = True
         return step - first_step
 

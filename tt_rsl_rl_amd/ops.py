@@ -563,9 +563,11 @@ def ppo_head(args: L.LossArgs, h_actor: torch.Tensor, w_actor: torch.Tensor, b_a
 
 def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max_grad_norm: float, beta1: float,
               beta2: float, eps: float, bc1: float, bc2_sqrt: float, state: torch.Tensor, ws: Workspace | None,
-              prenorm: torch.Tensor | None = None) -> None:
+              prenorm: torch.Tensor | None = None, mirrors: list[tuple] | None = None) -> None:
     """Clip + Adam over the flat buffers.  prenorm: the GradNorm partials of the weight-grad launch that wrote every
-    gradient of every group (ppo_adam_step_prenorm, one launch); else the norms are computed here (two launches)."""
+    gradient of every group (ppo_adam_step_prenorm, one launch); else the norms are computed here (two launches).
+    mirrors (with prenorm): (begin, rows, cols, dst [rows, >= cols] row-major) -- the updated rows x cols parameters at
+    flat offset begin are also written to dst (ppo_adam_step_prenorm_mirror)."""
     _dev(params, grads, exp_avg, exp_avg_sq)
     n = params.numel()
     for t in (grads, exp_avg, exp_avg_sq):
@@ -580,6 +582,21 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max
         _dev(prenorm, dtype=torch.float64)
         if tuple(prenorm.shape) != (L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS) or not prenorm.is_contiguous():
             raise ValueError("adam_step: prenorm must be a contiguous [DW_NORM_BLOCKS, MAX_PARAM_GROUPS] fp64 tensor")
+        if mirrors:
+            if len(mirrors) > L.MAX_PARAM_MIRRORS:
+                raise ValueError(f"adam_step: at most {L.MAX_PARAM_MIRRORS} mirrors")
+            items = []
+            for begin, rows, cols, dst in mirrors:
+                _dev(dst)
+                ld = _row_major(dst, "mirror dst")
+                if dst.shape[0] < rows or dst.shape[1] < cols or begin < 0 or begin + rows * cols > n:
+                    raise ValueError("adam_step: mirror outside the flat buffer or its destination")
+                items.append(L.ParamMirror(int(begin), int(rows), int(cols), dst.data_ptr(), ld))
+            L.call("ppo_adam_step_prenorm_mirror", params.data_ptr(), grads.data_ptr(), exp_avg.data_ptr(),
+                   exp_avg_sq.data_ptr(), group_begin.data_ptr(), groups, float(max_grad_norm), float(beta1),
+                   float(beta2), float(eps), float(bc1), float(bc2_sqrt), state.data_ptr(), prenorm.data_ptr(),
+                   L.array(L.ParamMirror, items), len(items), _stream())
+            return
         L.call("ppo_adam_step_prenorm", params.data_ptr(), grads.data_ptr(), exp_avg.data_ptr(),
                exp_avg_sq.data_ptr(), group_begin.data_ptr(), groups, float(max_grad_norm), float(beta1),
                float(beta2), float(eps), float(bc1), float(bc2_sqrt), state.data_ptr(), prenorm.data_ptr(),
