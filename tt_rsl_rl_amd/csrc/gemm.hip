@@ -1,6 +1,9 @@
-// A6 linear layers (rsl_rl/modules/mlp.py:27-95; autograd of nn.Linear / nn.ELU) as fp32 MFMA GEMMs for gfx950.
+// A6 linear layers (rsl_rl/modules/mlp.py:27-95; autograd of nn.Linear / nn.ELU) as fp32-accurate MFMA GEMMs for
+// gfx950.  Launches whose operands all have 16-byte rows run the bf16x6 kernels of gemm_core.hpp (each fp32 operand
+// split into three bf16 parts, six bf16 MFMA products per fp32 product, fp32 accumulation); the others run the fp32
+// MFMA kernels described here.
 //
-// Two kernel families, both 256 threads = 4 wavefronts in a 2 x 2 arrangement over a BM x BN output tile, each
+// Two fp32 kernel families, both 256 threads = 4 wavefronts in a 2 x 2 arrangement over a BM x BN output tile, each
 // wave owning (BM/2) x (BN/2) of 32 x 32 v_mfma_f32_32x32x2f32 accumulators, both fed by gfx950's direct
 // global->LDS loads (global_load_lds_dwordx4 / _dword: no register staging, no ds_write) into a two-stage LDS ring
 // with one barrier per BK-deep k-slab:
