@@ -143,13 +143,15 @@ class SplitRandperm:
 
     _pool = None
 
-    def __init__(self, n: int, out: torch.Tensor | None, split: int, normals: list[int] | tuple = ()) -> None:
+    def __init__(self, n: int, out: torch.Tensor | None, split: int, normals: list[int] | tuple = (),
+                 on_rest=None) -> None:
         import ctypes
 
         if n > 0 and (out is None or out.dtype != torch.int64 or out.device.type != "cpu" or out.numel() != n
                       or not out.is_contiguous()):
             raise ValueError("SplitRandperm: out must be a contiguous int64 CPU tensor of n elements")
         self.n, self.out, self.normals = n, out, list(normals)
+        self.on_rest = on_rest  # on_rest(self), on the worker once out[split:] is final (e.g. to enqueue its copy)
         self.split = max(0, min(int(split), n - 1)) if n > 0 else 0
         self._rec = bytearray(torch.get_rng_state().numpy().tobytes())
         self._buf = (ctypes.c_uint8 * len(self._rec)).from_buffer(self._rec)
@@ -177,7 +179,11 @@ class SplitRandperm:
     def _perm_rest(self) -> str | None:
         rc = L.load().ppo_host_randperm_range(self._buf, len(self._rec), self.n, self.split, self.n - 1,
                                               self.out.data_ptr())
-        return None if rc == L.PPO_OK else L.last_error()  # the error text is thread-local: read it here
+        if rc != L.PPO_OK:
+            return L.last_error()  # the error text is thread-local: read it here
+        if self.on_rest is not None:
+            self.on_rest(self)
+        return None
 
     def _skips(self) -> str | None:
         import ctypes

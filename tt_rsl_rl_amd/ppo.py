@@ -222,6 +222,8 @@ class PPO:
         self._engine: UpdateEngine | None = None
         self._adv_ws = ops.Workspace(self.device)
         self._perm_host: torch.Tensor | None = None
+        self._copy_stream = None  # the permutation's second part goes to the device on it (enqueued by the worker)
+        self._rest_copied = None
         self._state_host = ops.pinned_state_buffer()
         self._reset_host = ops.pinned_state_buffer()
         self._trace_rows: list | None = None
@@ -316,14 +318,24 @@ class PPO:
             # torch.randperm(B) on the CPU generator, computed natively (same permutation, same generator state):
             # the first mini-batch's positions now, the rest on a worker thread while its kernels are enqueued
             ready = engine.minibatch_rows(0)[1]
-            shuffle = ops.SplitRandperm(B, self._perm_host, ready, discards)
-            ready = shuffle.split if shuffle.split < B - 1 else B
             perm = self._perm_dev
+            if self._copy_stream is None:
+                self._copy_stream = torch.cuda.Stream(self.device)  # (default priority)
+                self._rest_copied = torch.cuda.Event()
+            copy_stream, rest_copied, host = self._copy_stream, self._rest_copied, self._perm_host
+
+            def copy_rest(sp):  # on the worker, once perm[sp.split:] is final: its copy, beside the update's kernels
+                with torch.cuda.device(self.device), torch.cuda.stream(copy_stream):
+                    perm[sp.split:].copy_(host[sp.split:], non_blocking=True)
+                    rest_copied.record(copy_stream)
+
+            shuffle = ops.SplitRandperm(B, self._perm_host, ready, discards, on_rest=copy_rest)
+            ready = shuffle.split if shuffle.split < B - 1 else B
             perm[:ready].copy_(self._perm_host[:ready], non_blocking=True)
             if ready < B:
                 def rest():
-                    shuffle.perm_ready()
-                    perm[ready:].copy_(self._perm_host[ready:], non_blocking=True)
+                    shuffle.perm_ready()  # (the copy was enqueued on the worker before this returns)
+                    torch.cuda.current_stream(self.device).wait_event(rest_copied)
         try:
             steps = engine.run(perm, self._opt_steps, ready, rest)
         finally:
