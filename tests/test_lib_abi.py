@@ -237,6 +237,36 @@ def test_split_randperm_is_torch_randperm(n, split):
     sh.join()  # idempotent
 
 
+def test_split_randperm_calls_on_rest_once_the_rest_is_final():
+    """on_rest(self) runs on the worker thread after the second piece, with out[split:] already final (the update
+    enqueues that piece's host-to-device copy from it); perm_ready() returns only after it; the permutation and the
+    generator state stay torch.randperm's."""
+    import threading
+
+    from tt_rsl_rl_amd import ops
+
+    n, split = 98304, 24576
+    torch.manual_seed(11)
+    start = torch.get_rng_state()
+    ref = torch.randperm(n)
+    ref_state = torch.get_rng_state()
+    torch.set_rng_state(start)
+    out = torch.empty(n, dtype=torch.int64)
+    seen = {}
+
+    def on_rest(sp):
+        seen["thread"] = threading.get_ident()
+        seen["split"] = sp.split
+        seen["tail"] = sp.out[sp.split:].clone()
+
+    sh = ops.SplitRandperm(n, out, split, on_rest=on_rest)
+    sh.perm_ready()
+    assert seen["split"] == split and seen["thread"] != threading.get_ident()
+    assert torch.equal(seen["tail"], ref[split:])
+    assert torch.equal(sh.join(), ref)
+    assert torch.equal(torch.get_rng_state(), ref_state)
+
+
 def test_host_randperm_range_validation():
     from tt_rsl_rl_amd import _lib
 
