@@ -211,7 +211,8 @@ class UpdateEngine:
         self.replays = 0
         self.replay = os.environ.get("PPO_HIP_LAUNCH_CACHE", "1") != "0" and not self.recurrent
         # inspection hook (None in normal use): called as step_hook(engine, r0, r1) after each mini-batch's launches
-        # are enqueued, before the next mini-batch's; the buffers then hold that mini-batch's activations / gradients
+        # are enqueued, before the next mini-batch's; the buffers then hold that mini-batch's activations / gradients.
+        # It must not change the parameters: within a run the padded first-layer copies follow the Adam steps only
         self.step_hook = None
 
     # -- one update ------------------------------------------------------------------------------------------------
