@@ -487,6 +487,13 @@ int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_
 int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
                      int32_t* sync, int64_t sync_words, ppo_stream_t stream);
 
+/* How long the blocks of a whole-sequence launch wait for each other before they give up and set the status word,
+ * in ticks of the 100 MHz device clock, for every later launch of this process: ticks >= 0 sets that limit, ticks < 0
+ * restores the default (200,000,000 = 2 s).  Returns the limit in force before the call.  A test hook (0 forces the
+ * give-up path from the host; every kernel still runs to its end); no environment variable changes the limit.
+ * No counterpart in the reference (nn.LSTM has no cross-block waits). */
+int64_t ppo_lstm_seq_wait_limit(int64_t ticks);
+
 /* gate-interleaved gradients -> torch-layout gradients (the bias gradient goes to both b_ih and b_hh). */
 typedef struct ppo_lstm_grad_problem {
   const float* dw_ih_g; const float* dw_hh_g; const float* db_g;

@@ -7,7 +7,9 @@ gradients given identical network outputs; 1e-6 for Adam + clipping against torc
 
 from __future__ import annotations
 
+import json
 import math
+import os
 
 import pytest
 import torch
@@ -393,6 +395,94 @@ def test_linear_bwd_dw_narrow_tiles(cuda, rows):
     for dw, db, rw, rb, rb_abs in refs:
         assert rel_err(dw, rw) < 2e-6
         assert ((db.cpu().double() - rb).abs() / rb_abs).max().item() < 1e-6
+
+
+def _gemm_errors(c: torch.Tensor, c64: torch.Tensor, bound: torch.Tensor) -> tuple[float, float]:
+    """(relative Frobenius error against fp64, largest per-element error over the element's |A| |B| bound)."""
+    e = (c.double() - c64).abs()
+    return float(e.norm() / c64.norm()), float((e / bound.clamp(min=1e-300)).max())
+
+
+def _operand(t: torch.Tensor, path: str, cuda) -> torch.Tensor:
+    """t on the device in 16-byte rows (the bf16x6 matrix-core kernels) or one float past a 16-byte boundary (the
+    fp32-MFMA kernels take operands the bf16x6 kernels cannot)."""
+    rows, cols = t.shape
+    if path == "bx6":
+        buf = torch.zeros(rows, -(-cols // 4) * 4, device=cuda)
+        buf[:, :cols].copy_(t)
+        return buf[:, :cols]
+    buf = torch.zeros(rows, cols + 4, device=cuda)
+    buf[:, 1:1 + cols].copy_(t)
+    return buf[:, 1:1 + cols]
+
+
+def _scaled(rows: int, cols: int, wide: bool, g: torch.Generator) -> torch.Tensor:
+    """N(0, 1) entries; wide: times row and column magnitudes log-uniform over [1e-6, 1e6]."""
+    x = torch.randn(rows, cols, generator=g)
+    if wide:
+        x *= 10.0 ** (12 * torch.rand(rows, 1, generator=g) - 6) * 10.0 ** (12 * torch.rand(1, cols, generator=g) - 6)
+    return x
+
+
+@pytest.mark.parametrize("op,rows,wide", [("fwd", 24576, False), ("fwd", 24576, True), ("dx", 24576, False),
+                                          ("dx", 24576, True), ("dw", 24576, False), ("dw", 24576, True),
+                                          ("dw", 393216, False)])
+def test_bx6_error_against_fp32_mfma(cuda, op, rows, wide):
+    """The bf16x6 GEMMs (fp32 operands as three bf16 parts, six bf16 MFMA products, fp32 accumulation) against the
+    fp32-MFMA kernels on identical problems: forward (x w^T), input-grad (dz w) and weight-grad (dz^T x, k = the rows:
+    24,576, and 393,216 as in the 65,536-env mini-batches), N(0, 1) operands and operands whose row and column
+    magnitudes are log-uniform over [1e-6, 1e6].  Both errors are measured against fp64 two ways (relative Frobenius;
+    per element over its |A| |B| bound), and the bf16x6 error must be at most twice the fp32-MFMA one by both, and
+    within the fp32-GEMM bar of 2e-6 (per element over its bound; relative Frobenius up to 24,576 rows).  The two
+    results must differ in some bits (two different kernels ran)."""
+    ops = _ops()
+    g = torch.Generator().manual_seed(rows + 3 * wide + {"fwd": 1, "dx": 2, "dw": 3}[op])
+    fin, fout = 512, 256
+    out = {}
+    if op == "fwd":
+        x, w = _scaled(rows, fin, wide, g), _scaled(fout, fin, wide, g)
+        xd, wd = x.to(cuda).double(), w.to(cuda).double()
+        c64, bound = xd @ wd.t(), xd.abs() @ wd.abs().t()
+        for path in ("bx6", "fp32"):
+            z = torch.empty(rows, fout, device=cuda)
+            ops.linear_fwd([(_operand(x, path, cuda), w.to(cuda), torch.zeros(fout, device=cuda), z, None)], rows,
+                           elu=False)
+            out[path] = z
+    elif op == "dx":
+        dz, w = _scaled(rows, fout, wide, g), _scaled(fout, fin, wide, g)
+        dzd, wd = dz.to(cuda).double(), w.to(cuda).double()
+        c64, bound = dzd @ wd, dzd.abs() @ wd.abs()
+        for path in ("bx6", "fp32"):
+            dx = torch.empty(rows, fin, device=cuda)
+            ops.linear_bwd_dx([(_operand(dz, path, cuda), w.to(cuda), None, dx)], rows)
+            out[path] = dx
+    else:
+        dz, x = _scaled(rows, fout, wide, g), _scaled(rows, fin, wide, g)
+        dzd, xd = dz.to(cuda).double(), x.to(cuda).double()
+        c64, bound = dzd.t() @ xd, dzd.abs().t() @ xd.abs()
+        for path in ("bx6", "fp32"):
+            dw, db = torch.empty(fout, fin, device=cuda), torch.empty(fout, device=cuda)
+            ops.linear_bwd_dw([(_operand(dz, path, cuda), _operand(x, path, cuda), dw, db)], rows)
+            out[path] = dw
+    torch.cuda.synchronize()
+    assert not torch.equal(out["bx6"], out["fp32"]), "both paths ran the same kernel"
+    e6, e32 = _gemm_errors(out["bx6"], c64, bound), _gemm_errors(out["fp32"], c64, bound)
+    print(f"{op} rows={rows} wide={wide}: bf16x6 rel-Frobenius {e6[0]:.3e} per-element/bound {e6[1]:.3e}; "
+          f"fp32 MFMA {e32[0]:.3e} / {e32[1]:.3e}; ratios {e6[0] / e32[0]:.2f} / {e6[1] / e32[1]:.2f}")
+    rec = os.environ.get("PPO_PARITY_RECORD")
+    if rec:
+        os.makedirs(rec, exist_ok=True)
+        with open(os.path.join(rec, f"bx6_vs_fp32_{op}_{rows}_{'wide' if wide else 'randn'}.json"), "w") as f:
+            json.dump({"op": op, "rows": rows, "wide_range": wide, "in": fin, "out": fout,
+                       "bx6": {"rel_frobenius": e6[0], "per_element_over_bound": e6[1]},
+                       "fp32_mfma": {"rel_frobenius": e32[0], "per_element_over_bound": e32[1]},
+                       "ratio": {"rel_frobenius": e6[0] / e32[0], "per_element_over_bound": e6[1] / e32[1]}}, f,
+                      indent=1)
+    assert e6[0] <= 2 * e32[0], (e6, e32)
+    assert e6[1] <= 2 * e32[1], (e6, e32)
+    assert e6[1] < 2e-6
+    if rows <= 24576:  # (a sum of 393,216 products rounds more: both kernels' relative error grows with k)
+        assert e6[0] < 2e-6
 
 
 # ----------------------------------------------------------------------------------------------------------------------

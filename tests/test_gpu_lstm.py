@@ -166,7 +166,7 @@ def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count):
             assert all(torch.equal(x, b["dgates"]) for x, b in zip(first, one))
 
 
-def test_sequence_wait_gives_up_and_the_update_raises(cuda, monkeypatch):
+def test_sequence_wait_gives_up_and_the_update_raises(cuda):
     """A wait limit of 0 ticks, forced from the host, makes the blocks of a one-launch sequence give up waiting for
     each other: every launch still runs to its end, the sticky status word is set (and stays set through a normal
     call, which clears only the counters), and a recurrent update that hit it raises instead of returning results,
@@ -179,11 +179,13 @@ def test_sequence_wait_gives_up_and_the_update_raises(cuda, monkeypatch):
     T, E, H = 24, 1024, 256
     qs = [_outputs(q, T, E, H, dev) for q in _random_sequences(dev, T, E, H, 2, seed=5)]
     sync = torch.zeros(ops.lstm_seq_sync_words(2, E), dtype=torch.int32, device=dev)
-    monkeypatch.setenv("PPO_HIP_SEQ_SPIN_TICKS", "0")
-    ops.lstm_seq_fwd(qs, T, E, sync)
-    torch.cuda.synchronize()
+    ops.lstm_seq_wait_limit(0)
+    try:
+        ops.lstm_seq_fwd(qs, T, E, sync)
+        torch.cuda.synchronize()
+    finally:
+        assert ops.lstm_seq_wait_limit(None) == 0
     assert int(sync[0]) == 1
-    monkeypatch.delenv("PPO_HIP_SEQ_SPIN_TICKS")
     ops.lstm_seq_fwd(qs, T, E, sync)
     torch.cuda.synchronize()
     assert int(sync[0]) == 1
@@ -208,16 +210,18 @@ def test_sequence_wait_gives_up_and_the_update_raises(cuda, monkeypatch):
     hip.compute_returns_from(torch.randn(w["num_envs"], 1, generator=g).to(hip.device))
     before = [t.clone() for t in (hip.flat.param, hip.flat.exp_avg, hip.flat.exp_avg_sq)]
     lr, steps = hip.learning_rate, hip._opt_steps
-    monkeypatch.setenv("PPO_HIP_SEQ_SPIN_TICKS", "0")
-    with pytest.raises(RuntimeError, match="stopped waiting"):
-        hip.update()
+    ops.lstm_seq_wait_limit(0)
+    try:
+        with pytest.raises(RuntimeError, match="stopped waiting"):
+            hip.update()
+    finally:
+        ops.lstm_seq_wait_limit(None)
     # the failed update is rolled back: parameters, moments, learning rate and step count as before, status cleared
     for a, b in zip(before, (hip.flat.param, hip.flat.exp_avg, hip.flat.exp_avg_sq)):
         assert torch.equal(a, b)
     assert hip.learning_rate == lr and hip._opt_steps == steps
     assert int(hip._engine.lstm_sync[0]) == 0
     # and the algorithm stays usable: the same update with the normal wait limit completes
-    monkeypatch.delenv("PPO_HIP_SEQ_SPIN_TICKS")
     out = hip.update()
     assert all(torch.isfinite(torch.tensor(v)) for v in out.values())
     assert hip._opt_steps == steps + hip.num_learning_epochs * hip.num_mini_batches

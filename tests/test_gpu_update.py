@@ -26,18 +26,26 @@ per-row output gradients, exactly zero iff the row's gradient is), lists every r
 must then agree at 1e-4.  The oracle's own spread (its fp32 log-prob sum against an fp64 one) is printed beside:
 it is of the same size as the GPU's distance from the literal oracle (both are one or two such rows' effect).
 
-Two complementary tests:
+Two complementary tests, both on every case (the five workloads at full size included: 4096 envs x 24 steps, and
+65,536 envs x 24 steps with mini-batches of 393,216 rows):
   * test_update_matches_oracle -- the drop-in update() end to end (state threading between steps, schedule,
     normaliser update);
   * test_update_steps_teacher_forced -- every optimiser step replayed on the GPU from the oracle's exact state before
     it (parameters, Adam moments and step, learning rate) against the oracle's state after it: the numerics of every
-    step without compounding; also at 65,536 envs x 24 steps (the first epoch's 4 steps of 393,216 rows).
+    step without compounding.
+
+With PPO_PARITY_RECORD=<dir> in the environment each case also writes what it measured to <dir>/<test>_<case>.json:
+the rows on another clip branch and their distances, every parameter tensor's error against the branch-matched and
+the literal oracle and the oracle's own spread, the function-space figures and the losses.
 """
 
 from __future__ import annotations
 
 import copy
 import functools
+import json
+import os
+import time
 from itertools import chain
 
 import pytest
@@ -96,10 +104,30 @@ CASES = {
                                    "schedule": "fixed", "use_clipped_value_loss": False, "carry_state": True}),
 }
 
-# the 65,536-env update is checked step by step over its first epoch (an end-to-end oracle run of all 20 steps of
-# 393,216 rows takes minutes of CPU time); every other case both ways
-END_TO_END = [n for n in CASES if n != "flat48_65k"]
-TEACHER_FORCED_STEPS = {"flat48_65k": 4}
+# an oracle update of the 65,536-env workload takes ~45 s of CPU time on 16 threads, and the end-to-end test runs it
+# up to three times (literal, branch-matched, fp64 log-prob spread): a limit of its own, progress lines as it goes
+LONG = {"flat48_65k"}
+
+
+def _cases():
+    return [pytest.param(n, marks=pytest.mark.timeout(1200)) if n in LONG else n for n in CASES]
+
+
+def _progress(capsys, name: str, msg: str, t0: list) -> None:
+    """A progress line on the terminal for the long cases (outside pytest's capture)."""
+    if name in LONG:
+        with capsys.disabled():
+            print(f"  [{name} +{time.time() - t0[0]:.0f}s] {msg}", flush=True)
+
+
+def _record(test: str, name: str, data: dict) -> None:
+    """Write a case's measured figures to $PPO_PARITY_RECORD/<test>_<name>.json (nothing without the variable)."""
+    out = os.environ.get("PPO_PARITY_RECORD")
+    if not out:
+        return
+    os.makedirs(out, exist_ok=True)
+    with open(os.path.join(out, f"{test}_{name}.json"), "w") as f:
+        json.dump(data, f, indent=1, sort_keys=True)
 
 # cases whose output layers fall outside the fused head (more than 32 actions, or a last hidden width that is not a
 # multiple of 16)
@@ -143,20 +171,25 @@ def _table_order(ora, hip) -> torch.Tensor:
     return torch.cat([t["indices"] for t in ora.trace[:ora.num_mini_batches]])
 
 
-@pytest.mark.parametrize("name", END_TO_END)
-def test_update_matches_oracle(name):
+@pytest.mark.parametrize("name", _cases())
+def test_update_matches_oracle(name, capsys):
+    t0 = [time.time()]
     w, ora, hip = _pair(name)
+    _progress(capsys, name, "rollout and returns ready", t0)
     st_o, st_h = ora.storage, hip.storage
     assert torch.equal(st_h.returns.cpu(), st_o.returns), "GAE returns must be bit-exact"
-    assert rel_err(st_h.advantages, st_o.advantages) < 1e-6
+    adv_err = rel_err(st_h.advantages, st_o.advantages)
+    assert adv_err < 1e-6
     p0 = param_dict(ora)
     ev = eval_observations(ora)
     lp64, shadow = copy.deepcopy(ora), copy.deepcopy(ora)
     torch.manual_seed(1)
     ref = ora.update()
+    _progress(capsys, name, "oracle update done", t0)
     with oracle_logp_fp64():
         torch.manual_seed(1)
         lp64.update()
+    _progress(capsys, name, "oracle update with fp64 log-prob sums done", t0)
 
     # the drop-in update(), with each mini-batch's clip-branch decisions read back
     engine = hip._get_engine()
@@ -176,11 +209,18 @@ def test_update_matches_oracle(name):
     torch.cuda.synchronize()
     engine.step_hook = None
     assert len(rows) == len(ora.trace)
+    _progress(capsys, name, "GPU update done", t0)
 
-    # the oracle trajectory with the GPU's decisions on the rows where they differ
-    shadow.forced_branches = rows
-    torch.manual_seed(1)
-    ref_s = shadow.update()
+    # the oracle trajectory with the GPU's decisions on the rows where they differ (where the GPU took the oracle's
+    # own decision on every row of every step, forcing changes nothing: that trajectory is the oracle's, bit for bit)
+    same = all(torch.equal(r[kind], own) for r, t in zip(rows, ora.trace) for kind, own in t["branches"].own.items())
+    if same:
+        shadow, ref_s = ora, ref
+    else:
+        shadow.forced_branches = rows
+        torch.manual_seed(1)
+        ref_s = shadow.update()
+        _progress(capsys, name, "branch-matched oracle update done", t0)
     flips = flipped_rows(shadow.trace)
     gaps = []
     for k, (t, q) in enumerate(zip(shadow.trace, quantities)):
@@ -208,19 +248,24 @@ def test_update_matches_oracle(name):
         for k, scale in (("value", 0.0), ("surrogate", 0.1), ("entropy", 0.0)):
             assert abs(out[k] - r[k]) <= 1e-4 * max(abs(r[k]), scale), (k, out[k], r[k])
     # parameters and optimiser moments against the branch-matched oracle
-    worst = 0.0
-    for model_h, model_s, model_o, model_64 in ((hip.actor, shadow.actor, ora.actor, lp64.actor),
-                                                (hip.critic, shadow.critic, ora.critic, lp64.critic)):
+    worst, tensors = 0.0, {}
+    for tag, model_h, model_s, model_o, model_64 in (("actor", hip.actor, shadow.actor, ora.actor, lp64.actor),
+                                                     ("critic", hip.critic, shadow.critic, ora.critic, lp64.critic)):
         for (name_p, p_s), p_h, p_o, p_64 in zip(model_s.named_parameters(), model_h.parameters(),
                                                  model_o.parameters(), model_64.parameters()):
             err = rel_err(p_h, p_s)
             worst = max(worst, err)
-            print(f"{name_p:28s} vs branch-matched oracle {err:.2e}   vs oracle {rel_err(p_h, p_o):.2e}   "
+            s_s, s_h = shadow.optimizer.state[p_s], hip.optimizer.state[p_h]
+            m1 = rel_err(s_h["exp_avg"], s_s["exp_avg"], 1e-12)
+            m2 = rel_err(s_h["exp_avg_sq"], s_s["exp_avg_sq"], 1e-20)
+            tensors[f"{tag}.{name_p}"] = {"vs_branch_matched": err, "vs_literal_oracle": rel_err(p_h, p_o),
+                                          "oracle_spread_lp64_vs_oracle": rel_err(p_64, p_o),
+                                          "exp_avg_vs_branch_matched": m1, "exp_avg_sq_vs_branch_matched": m2}
+            print(f"{tag}.{name_p:28s} vs branch-matched oracle {err:.2e}   vs oracle {rel_err(p_h, p_o):.2e}   "
                   f"(oracle's own spread: lp64 vs oracle {rel_err(p_64, p_o):.2e})")
             assert err < PARAM_BAR, name_p
-            s_s, s_h = shadow.optimizer.state[p_s], hip.optimizer.state[p_h]
-            assert rel_err(s_h["exp_avg"], s_s["exp_avg"], 1e-12) < MOMENT_BAR, name_p
-            assert rel_err(s_h["exp_avg_sq"], s_s["exp_avg_sq"], 1e-20) < MOMENT_BAR, name_p
+            assert m1 < MOMENT_BAR, name_p
+            assert m2 < MOMENT_BAR, name_p
             assert float(s_h["step"]) == float(s_s["step"])
     # function space
     p_h, p_s, p_o, p_64 = param_dict(hip), param_dict(shadow), param_dict(ora), param_dict(lp64)
@@ -228,9 +273,22 @@ def test_update_matches_oracle(name):
     d_ho = function_deviation(p_h, p_o, p0, ora, ev)
     d_so = function_deviation(p_s, p_o, p0, ora, ev)
     spread = function_deviation(p_64, p_o, p0, ora, ev)
+    worst_gap = {kind: max(g.get(kind, 0.0) for g in gaps) for kind in ("surrogate", "value")}
+    _record("update", name, {
+        "case": name, "rows": B, "mini_batches": len(rows), "returns_bit_exact": True, "advantages_rel_err": adv_err,
+        "rows_on_another_branch": [{"step": k, "kind": kind, "row": i, "distance_to_boundary": d}
+                                   for k, kind, i, d in flips],
+        "branch_matched_oracle_replayed": not same,
+        "worst_param_err_vs_branch_matched": worst, "tensors": tensors,
+        "largest_ratio_gap": worst_gap["surrogate"], "largest_value_gap": worst_gap["value"],
+        "function_space": {t: {"gpu_vs_branch_matched": d_hs[t], "gpu_vs_literal_oracle": d_ho[t],
+                               "branch_matched_vs_literal_oracle": d_so[t], "oracle_spread_lp64_vs_oracle": spread[t]}
+                           for t in ("actor", "critic")},
+        "losses": {"gpu": out, "literal_oracle": ref, "branch_matched_oracle": ref_s},
+        "learning_rates_equal": True, "final_learning_rate": hip.learning_rate})
     print(f"{name}: {len(flips)} row(s) on another branch {[(k, kind, round(d, 9)) for k, kind, _, d in flips]}; "
           f"worst parameter error {worst:.2e}; largest ratio gap "
-          f"{max(g['surrogate'] for g in gaps):.2e}, value gap {max(g.get('value', 0.0) for g in gaps):.2e}")
+          f"{worst_gap['surrogate']:.2e}, value gap {worst_gap['value']:.2e}")
     for t in ("actor", "critic"):
         print(f"  {t}: d(gpu, branch-matched) {d_hs[t]:.2e}  d(gpu, oracle) {d_ho[t]:.2e}  "
               f"d(branch-matched, oracle) {d_so[t]:.2e}  oracle spread d(lp64, oracle) {spread[t]:.2e}")
@@ -243,6 +301,34 @@ def test_update_matches_oracle(name):
             assert int(n_h.count) == int(n_o.count)
             assert rel_err(n_h._mean, n_o._mean) < 1e-6
             assert rel_err(n_h._var, n_o._var) < 1e-6
+
+
+@pytest.mark.parametrize("name", ["humanoid_full", "flat48_65k"])
+def test_compute_returns_with_own_bootstrap_full_size(name):
+    """compute_returns as the runner calls it (ppo.py:166-191): the bootstrap value from the plugin's own critic
+    forward on the GPU (observation normaliser included), the GAE scan and the global advantage normalisation, at
+    4096 envs x 24 steps (humanoid) and 65,536 envs x 24 steps, against the oracle's compute_returns with its own CPU
+    critic on the same rollout and weights: returns and advantages within 1e-6 relative (norm-wise), the bootstrap
+    values within 1e-6.  The critic's state is left as it was."""
+    w, over = CASES[name]
+    ora0, roll, last_values = _rollout(name)  # the oracle's returns come from its own critic's bootstrap value
+    hip = make_hip(w, 0, **over)
+    with torch.no_grad():
+        hip.actor.load_state_dict(roll.init_state["actor"])
+        hip.critic.load_state_dict(roll.init_state["critic"])
+    R.feed(hip.storage, roll)
+    obs = {k: v.to(hip.device) for k, v in roll.last_obs.items()}
+    with torch.inference_mode():
+        v_h = hip.critic(obs).detach()
+        hip.compute_returns(obs)
+    torch.cuda.synchronize()
+    st_o, st_h = ora0.storage, hip.storage
+    figures = {"bootstrap_values": rel_err(v_h, last_values), "returns": rel_err(st_h.returns, st_o.returns),
+               "advantages": rel_err(st_h.advantages, st_o.advantages)}
+    _record("compute_returns", name, {"case": name, "envs": w["num_envs"], "steps": w["steps"], "rel_err": figures})
+    print(name, figures)
+    for k, v in figures.items():
+        assert v < 1e-6, (k, v)
 
 
 def test_recorded_launches_match_rebuilt_launches():
@@ -275,6 +361,105 @@ def test_recorded_launches_match_rebuilt_launches():
     assert a._engine.replays > 0 and b._engine.replays == 0
 
 
+def _update_both(algs, seed: int) -> list[dict]:
+    outs = []
+    for alg in algs:
+        alg.storage.step = alg.storage.num_transitions_per_env
+        torch.manual_seed(seed)
+        outs.append(alg.update())
+    torch.cuda.synchronize()
+    return outs
+
+
+def _assert_same_state(a, b, where) -> None:
+    assert a.learning_rate == b.learning_rate, where
+    assert a._opt_steps == b._opt_steps, where
+    for name in ("param", "exp_avg", "exp_avg_sq"):
+        assert torch.equal(getattr(a.flat, name), getattr(b.flat, name)), (where, name)
+    for ma, mb in ((a.actor, b.actor), (a.critic, b.critic)):
+        if ma.obs_normalization:
+            na, nb = ma.obs_normalizer, mb.obs_normalizer
+            for k in ("_mean", "_var", "_std", "count"):
+                assert torch.equal(getattr(na, k), getattr(nb, k)), (where, k)
+            assert na._host_count == nb._host_count == int(na.count), where
+
+
+def test_recorded_launches_follow_a_new_storage():
+    """A RolloutStorage of the same shape swapped in between updates (upstream's update reads whatever alg.storage
+    is): the recorded launches hold the old storage's addresses, so they must be dropped and the updates after the
+    swap read the new storage -- bit for bit the updates of a twin whose every launch is rebuilt -- and record again.
+    The old storages stay alive, so the new ones cannot take their addresses."""
+    from tests.parity import make_pair
+    from tt_rsl_rl_amd.storage import RolloutStorage
+
+    w = R.scaled(R.WORKLOADS["humanoid"], num_envs=256, steps=8, hidden_dims=[64, 32])
+    _, a, _ = make_pair(w, seed=0)
+    _, b, _ = make_pair(w, seed=0)
+    a._get_engine().replay, b._get_engine().replay = True, False
+    for rep in range(3):
+        _update_both((a, b), 1 + rep)
+    _assert_same_state(a, b, "before the swap")
+    replays = a._engine.replays
+    assert replays > 0
+    _, roll2 = R.generate(w, 5)
+    old = [a.storage, b.storage]
+    g = torch.Generator().manual_seed(9)
+    last = torch.randn(w["num_envs"], 1, generator=g)
+    for alg in (a, b):
+        st = RolloutStorage("rl", w["num_envs"], w["steps"], R.zero_obs(w), [w["num_actions"]], alg.device)
+        R.feed(st, roll2)
+        alg.storage = st
+        alg.compute_returns_from(last.to(alg.device))
+    assert all(x.observations["policy"].data_ptr() != y.storage.observations["policy"].data_ptr()
+               for x, y in zip(old, (a, b)))
+    for rep in range(3):
+        outs = _update_both((a, b), 10 + rep)
+        assert outs[0] == outs[1], rep
+        _assert_same_state(a, b, f"update {rep} after the swap")
+    assert a._engine.replays > replays, "the updates after the swap record and replay again"
+    assert b._engine.replays == 0
+
+
+def test_failed_update_is_rolled_back():
+    """An error raised while an update's launches are issued -- here the library rejecting a weight-grad launch of the
+    third mini-batch (asked for -1 rows) after two mini-batches' Adam steps and the normaliser update have run --
+    leaves the algorithm as it was before the update: parameters, Adam moments and step count, learning rate, the
+    observation normalisers' statistics and sample counts (the host mirror the `until` check reads included).  The
+    same update then runs normally and equals, bit for bit, the update of a twin that never failed."""
+    from tests.parity import make_pair
+
+    w = R.scaled(R.WORKLOADS["humanoid"], num_envs=256, steps=8, hidden_dims=[64, 32])
+    assert w["obs_normalization"]
+    _, a, _ = make_pair(w, seed=0)
+    _, b, _ = make_pair(w, seed=0)
+    for alg in (a, b):
+        for m in (alg.actor, alg.critic):
+            m.obs_normalizer.until = 10 ** 9
+    _update_both((a, b), 1)
+    _assert_same_state(a, b, "after the first update")
+    engine = a._get_engine()
+    real, calls = engine.weight_grads, [0]
+
+    def failing(dw, rows, *args, **kw):
+        calls[0] += 1
+        return real(dw, -1 if calls[0] == 3 else rows, *args, **kw)
+
+    engine.weight_grads = failing
+    a.storage.step = a.storage.num_transitions_per_env
+    torch.manual_seed(2)
+    with pytest.raises(ValueError):
+        a.update()
+    assert calls[0] == 3
+    del engine.weight_grads
+    torch.cuda.synchronize()
+    _assert_same_state(a, b, "after the failed update")
+    assert a.storage.step == a.storage.num_transitions_per_env, "the rollout is kept"
+    for rep in range(2):
+        outs = _update_both((a, b), 2 + rep)
+        assert outs[0] == outs[1], rep
+        _assert_same_state(a, b, f"update {rep} after the failure")
+
+
 def _adam_state(opt, p):
     st = opt.state.get(p, {})
     if "exp_avg" not in st:
@@ -305,25 +490,25 @@ def _load_oracle_state(ora, snap: dict) -> None:
         g["lr"] = snap["lr"]
 
 
-@pytest.mark.parametrize("name", list(CASES))
-def test_update_steps_teacher_forced(name):
+@pytest.mark.parametrize("name", _cases())
+def test_update_steps_teacher_forced(name, capsys):
+    t0 = [time.time()]
     w, ora, hip = _pair(name)
     snaps = []
     ora.recorder = lambda phase, alg: snaps.append((phase, _snapshot(alg)))
-    ora.max_steps = TEACHER_FORCED_STEPS.get(name)
     # the normalisers are updated after the epochs; the steps replayed below need the statistics they ran with
     norms = [(m.obs_normalizer, copy.deepcopy(m.obs_normalizer.state_dict()))
              for m in (ora.actor, ora.critic) if m.obs_normalization]
     torch.manual_seed(1)
     ora.update()
+    _progress(capsys, name, "oracle update done", t0)
     ora.recorder = None
     for norm, sd in norms:
         norm.load_state_dict(sd)
     pre = [s for ph, s in snaps if ph == "pre"]
     post = [s for ph, s in snaps if ph == "post"]
     M = ora.num_mini_batches
-    n_steps = ora.max_steps or ora.num_learning_epochs * M
-    assert len(pre) == len(post) == len(ora.trace) == n_steps
+    assert len(pre) == len(post) == len(ora.trace) == ora.num_learning_epochs * M
 
     # the GPU side: the update's packed table (same permutation), then one step at a time from the oracle's state
     engine = hip._get_engine()
@@ -332,7 +517,7 @@ def test_update_steps_teacher_forced(name):
     names = [n for n, _ in chain(ora.actor.named_parameters(), ora.critic.named_parameters())]
     torch.manual_seed(1)
     batches = ora.batches()  # the oracle's mini-batches again, for the steps it replays with the GPU's branches
-    worst, replayed, n_flips, worst_gap = 0.0, 0, 0, {}
+    worst, replayed, n_flips, worst_gap, per_step = 0.0, 0, 0, {}, []
     for k, (a, b) in enumerate(zip(pre, post)):
         batch = next(batches)
         with torch.no_grad():
@@ -361,21 +546,34 @@ def test_update_steps_teacher_forced(name):
             worst_gap[kind] = max(worst_gap.get(kind, 0.0), d)
             assert d < QUANTITY_BAR, (k, kind, d)
         own = t["branches"].own
+        step_flips = []
         if any(not torch.equal(rows[kind], own[kind]) for kind in own):
             _load_oracle_state(ora, a)
             t2 = ora.minibatch_step(batch, rows)
             bad = unexplained_flips(t2["branches"], q, AMBIGUOUS)
             assert not bad, (k, bad)
-            n_flips += len(flipped_rows([t2]))
+            step_flips = flipped_rows([t2])
+            n_flips += len(step_flips)
             assert t2["lr"] == lr
             b = _snapshot(ora)
             replayed += 1
+        step_worst = 0.0
         for n, p, v, m1, m2 in zip(names, params, b["params"], b["exp_avg"], b["exp_avg_sq"]):
             err = rel_err(p, v)
-            worst = max(worst, err)
+            step_worst = max(step_worst, err)
             assert err < PARAM_BAR, (k, n, err)
             assert rel_err(hip.flat.exp_avg_view(p), m1, 1e-12) < MOMENT_BAR, (k, n)
             assert rel_err(hip.flat.exp_avg_sq_view(p), m2, 1e-20) < MOMENT_BAR, (k, n)
+        worst = max(worst, step_worst)
+        per_step.append({"step": k, "worst_param_err": step_worst, "ratio_gap": gap.get("surrogate"),
+                         "value_gap": gap.get("value"),
+                         "rows_on_another_branch": [{"kind": kind, "row": i, "distance_to_boundary": d}
+                                                    for _, kind, i, d in step_flips]})
+        if k % 5 == 4:
+            _progress(capsys, name, f"step {k + 1} of {len(pre)} checked", t0)
+    _record("teacher_forced", name, {"case": name, "steps": len(pre), "replayed_with_gpu_branches": replayed,
+                                     "rows_on_another_branch": n_flips, "worst_param_err": worst,
+                                     "largest_gaps": worst_gap, "per_step": per_step})
     print(f"{name}: {len(pre)} teacher-forced steps, {replayed} with {n_flips} row(s) on another clip branch "
           f"(oracle replayed with the GPU's decisions), worst parameter rel error {worst:.2e}, largest ratio / value "
           f"gap {worst_gap}")

@@ -289,3 +289,18 @@ def test_host_randperm_rejects_unknown_generator_records():
     assert lib.ppo_host_randperm(rec, 5056, 4, out) == _lib.PPO_EINVAL
     assert "not recognised" in _lib.last_error()
     assert lib.ppo_host_randperm(rec, 5000, 4, out) == _lib.PPO_EINVAL
+
+
+def test_sequence_wait_limit_is_set_only_through_its_entry_point(monkeypatch):
+    """The whole-sequence LSTM launches' wait limit: 2 s of the 100 MHz clock by default, changed only by
+    ppo_lstm_seq_wait_limit (no environment variable), which returns the limit it replaces; a negative value restores
+    the default."""
+    from tt_rsl_rl_amd import _lib
+
+    lib = _lib.load()
+    monkeypatch.setenv("PPO_HIP_SEQ_SPIN_TICKS", "0")  # a stray variable of an older build changes nothing
+    assert lib.ppo_lstm_seq_wait_limit(-1) == 200_000_000
+    assert lib.ppo_lstm_seq_wait_limit(0) == 200_000_000
+    assert lib.ppo_lstm_seq_wait_limit(12345) == 0
+    assert lib.ppo_lstm_seq_wait_limit(-7) == 12345
+    assert lib.ppo_lstm_seq_wait_limit(-1) == 200_000_000

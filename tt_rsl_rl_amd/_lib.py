@@ -12,7 +12,8 @@ import ctypes as C
 import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libppo_hip.so"
+# PPO_HIP_LIB names another build of the same library (the host-sanitizer build of sanitize_host.py)
+LIB_PATH = Path(os.environ.get("PPO_HIP_LIB") or Path(__file__).resolve().parent / "libppo_hip.so")
 
 PPO_OK = 0
 PPO_EINVAL = -1
@@ -139,6 +140,7 @@ _SIGNATURES = [
     ("ppo_linear_fwd", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, C.c_void_p]),
     ("ppo_lstm_pack", C.c_int, [C.POINTER(LstmPackProblem), i32, C.c_void_p]),
     ("ppo_lstm_seq_sync_words", i64, [i32, i64]),
+    ("ppo_lstm_seq_wait_limit", i64, [i64]),
     ("ppo_lstm_seq_fwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_seq_bwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),

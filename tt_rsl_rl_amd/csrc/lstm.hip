@@ -156,7 +156,7 @@ constexpr int kSyncHeader = 32;  // int32 words ahead of the row-group lines: [0
 constexpr int kSyncStride = 32;  // one 128-byte line per row group: [0] counter, [16 + j] XCD of block j
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data (gfx9 family)
 constexpr int kDeviceScope = 16;          // buffer-load cache policy: sc1, coherent at device scope
-constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock (PPO_HIP_SEQ_SPIN_TICKS overrides it)
+constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock (ppo_lstm_seq_wait_limit)
 
 struct SeqFwdItem {
   const float* w;  // w_hh_g [4H, H]
@@ -642,11 +642,14 @@ int launch_step(Group& g, int count, hipStream_t s, const char* name) {
 
 int64_t seq_row_groups(int64_t envs) { return ceil_div(envs, static_cast<int64_t>(kSeqRows)); }
 
-// How long a block of a sequence kernel waits for the others before it gives up (100 MHz ticks).  The variable
-// exists so that tests can force the give-up path from the host; every kernel still runs to its end.
+// How long a block of a sequence kernel waits for the others before it gives up (100 MHz ticks): kSeqSpinTicks,
+// unless a caller set another limit through ppo_lstm_seq_wait_limit (tests force the give-up path that way; every
+// kernel still runs to its end).  No environment variable changes it.
+std::atomic<int64_t> g_seq_wait_limit{-1};
+
 uint64_t seq_spin_ticks() {
-  const char* e = std::getenv("PPO_HIP_SEQ_SPIN_TICKS");
-  return e != nullptr ? std::strtoull(e, nullptr, 10) : kSeqSpinTicks;
+  const int64_t v = g_seq_wait_limit.load(std::memory_order_relaxed);
+  return v >= 0 ? static_cast<uint64_t>(v) : kSeqSpinTicks;
 }
 
 // Launches the whole-sequence forward when the shape allows it and the device holds at least one row-group slot
@@ -804,6 +807,11 @@ extern "C" int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int3
 extern "C" int64_t ppo_lstm_seq_sync_words(int32_t count, int64_t envs) {
   if (count < 1 || count > PPO_MAX_LSTM_PROBLEMS || envs < 1) return -1;
   return kSyncHeader + count * seq_row_groups(envs) * kSyncStride;
+}
+
+extern "C" int64_t ppo_lstm_seq_wait_limit(int64_t ticks) {
+  const int64_t previous = g_seq_wait_limit.exchange(ticks < 0 ? -1 : ticks, std::memory_order_relaxed);
+  return previous < 0 ? static_cast<int64_t>(kSeqSpinTicks) : previous;
 }
 
 extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,

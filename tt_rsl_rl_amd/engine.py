@@ -244,10 +244,22 @@ class UpdateEngine:
 
     # -- recorded launch sequences ------------------------------------------------------------------------------------
     def _plan_signature(self):
+        """What the recorded launches hold besides the engine's own buffers: the stream, the hyperparameters passed
+        as values, and every storage tensor the gathers read (address, shape, strides: a storage rebound to other
+        tensors of the same shape, or its distribution parameters replaced, must not replay stale addresses)."""
         a = self.alg
         return (torch.cuda.current_stream(self.device).cuda_stream, a.clip_param, a.value_loss_coef, a.entropy_coef,
                 a.use_clipped_value_loss, a.desired_kl, a.schedule, a.max_grad_norm, tuple(a.betas), a.adam_eps,
-                a.normalize_advantage_per_mini_batch, a.num_learning_epochs)
+                a.normalize_advantage_per_mini_batch, a.num_learning_epochs, self._storage_signature())
+
+    def _storage_signature(self) -> tuple:
+        st = self.alg.storage
+        ts = [*st.observations.values(), st.actions, st.actions_log_prob, st.values, st.returns, st.advantages,
+              st.dones, *(st.distribution_params or ())]
+        if st.act_record is not None:
+            ts.append(st.act_record)
+        return (id(st), self.alg.flat.param.data_ptr()) + tuple(
+            (t.data_ptr(), tuple(t.shape), tuple(t.stride())) for t in ts)
 
     def _issue(self, key, fn, step: int | None = None) -> None:
         """Run fn (which issues launches through the C ABI) the first time for this key, recording its calls;

@@ -687,6 +687,12 @@ def _seq_problem(q: dict, steps: int, envs: int, bwd: bool) -> "L.LstmSeqProblem
                             _ptr(q.get("dgates")), _ptr(q.get("dc")), H, 0)
 
 
+def lstm_seq_wait_limit(ticks: int | None) -> int:
+    """Set how long the blocks of a whole-sequence LSTM launch wait for each other (100 MHz ticks) for every later
+    launch; None restores the default.  Returns the previous limit.  For tests that force the give-up path."""
+    return int(L.load().ppo_lstm_seq_wait_limit(-1 if ticks is None else int(ticks)))
+
+
 def lstm_seq_sync_words(count: int, envs: int) -> int:
     """int32 words of the whole-sequence launches' synchronisation buffer (word 0: sticky status)."""
     n = L.load().ppo_lstm_seq_sync_words(count, envs)

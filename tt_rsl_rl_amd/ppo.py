@@ -228,6 +228,7 @@ class PPO:
         self._reset_host = ops.pinned_state_buffer()
         self._trace_rows: list | None = None
         self._step_tensor: torch.Tensor | None = None
+        self._saved: dict | None = None  # the state before the current update (_save_state)
 
     # -- rollout side ------------------------------------------------------------------------------------------------
     def act(self, obs: Mapping) -> torch.Tensor:
@@ -290,9 +291,10 @@ class PPO:
         if st.distribution_params is None:
             raise RuntimeError("update() called before any transition was stored")
         engine = self._get_engine()
-        # an update whose kernels can report a failure (the recurrent one-launch sequences) starts from a copy of
-        # the state it changes, so a failed update leaves the algorithm as it was
-        saved = self._save_state() if engine.can_fail else None
+        # every update starts from a copy of the state it changes (parameters, Adam moments, normaliser statistics),
+        # so an update that fails -- an error raised while its launches are issued, or a device-side failure the
+        # read-back reports (the recurrent one-launch sequences) -- leaves the algorithm as it was
+        self._save_state()
         # the staging buffer's previous copy (one update ago) completed at that update's read-back
         ops.reset_device_state(self.device_state, self.learning_rate, self._reset_host)
         # The normaliser update (upstream: after the epochs, ppo.py:327-330) reads only the stored raw observations;
@@ -336,11 +338,23 @@ class PPO:
                 def rest():
                     shuffle.perm_ready()  # (the copy was enqueued on the worker before this returns)
                     torch.cuda.current_stream(self.device).wait_event(rest_copied)
+                    consumed[0] = True
+        consumed = [False]
         try:
             steps = engine.run(perm, self._opt_steps, ready, rest)
-        finally:
+        except BaseException:
             if shuffle is not None:
                 shuffle.join()  # idempotent; on an error path it still restores the generator before raising
+            if rest is not None and not consumed[0]:
+                # the worker may have enqueued the copy of perm[split:] from the pinned host buffer, which the next
+                # update's worker rewrites: no stream waits on that copy, so wait for it here
+                self._rest_copied.synchronize()
+            torch.cuda.current_stream(self.device).synchronize()
+            self._restore_state()
+            raise
+        finally:
+            if shuffle is not None:
+                shuffle.join()
 
         # the one host sync of the update: device state and per-mini-batch trace, two async copies, one wait
         self._state_host.copy_(self.device_state, non_blocking=True)
@@ -349,7 +363,7 @@ class PPO:
         torch.cuda.current_stream(self.device).synchronize()
         failure = engine.failure()
         if failure is not None:
-            self._restore_state(saved)
+            self._restore_state()
             engine.clear_status()
             raise RuntimeError(f"{failure}; the update was rolled back (parameters, optimiser state and normaliser "
                                "statistics are those before it, the rollout is kept)")
@@ -365,22 +379,36 @@ class PPO:
         return {"value": state.sum_value_loss / n, "surrogate": state.sum_surrogate_loss / n,
                 "entropy": state.sum_entropy / n}
 
-    def _save_state(self) -> dict:
-        """Device copies of what an update changes: the flat parameters and Adam moments, and the observation
-        normalisers' statistics (a few MB, copied on the update's stream)."""
+    def _save_state(self) -> None:
+        """Device copies of what an update changes, into buffers kept from update to update: the flat parameters and
+        Adam moments, and the observation normalisers' statistics (a few MB, copied on the update's stream), plus
+        each normaliser's host-side sample count."""
         f = self.flat
         norms = [m.obs_normalizer for m in (self.actor, self.critic) if m.obs_normalization]
-        return {"flat": [t.clone() for t in (f.param, f.exp_avg, f.exp_avg_sq)],
-                "norms": [(n, {k: v.clone() for k, v in n.state_dict().items()}) for n in norms]}
+        saved = self._saved
+        if saved is None or saved["flat"][0].numel() != f.param.numel() or \
+                [id(n) for n, _, _ in saved["norms"]] != [id(n) for n in norms]:
+            saved = self._saved = {
+                "flat": [torch.empty_like(t) for t in (f.param, f.exp_avg, f.exp_avg_sq)],
+                "norms": [(n, {k: torch.empty_like(v) for k, v in n.state_dict().items()}, [0]) for n in norms]}
+        with torch.no_grad():
+            for dst, src in zip(saved["flat"], (f.param, f.exp_avg, f.exp_avg_sq)):
+                dst.copy_(src)
+            for norm, bufs, host_count in saved["norms"]:
+                for k, v in bufs.items():
+                    v.copy_(getattr(norm, k))
+                host_count[0] = norm._host_count
 
-    def _restore_state(self, saved: dict) -> None:
+    def _restore_state(self) -> None:
         f = self.flat
+        saved = self._saved
         with torch.no_grad():
             for dst, src in zip((f.param, f.exp_avg, f.exp_avg_sq), saved["flat"]):
                 dst.copy_(src)
-            for norm, sd in saved["norms"]:
-                for k, v in sd.items():
+            for norm, bufs, host_count in saved["norms"]:
+                for k, v in bufs.items():
                     getattr(norm, k).copy_(v)
+                norm._host_count = host_count[0]
 
     @property
     def last_trace(self) -> list[dict]:
