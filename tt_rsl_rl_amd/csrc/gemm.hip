@@ -327,6 +327,15 @@ int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
   int blocks;
   if (int rc = assign_blocks(g, count, 128, bn, name, blocks)) return rc;
   if (blocks == 0) return PPO_OK;
+#ifdef PPO_HIP_TUNING
+  if (std::getenv("PPO_HIP_BX6") == nullptr)
+#endif
+  if (!BKM && 2 * blocks <= 3 * device_info().cus) {
+    // 128 x 128 tiles would fill at most half of the three blocks per CU (a 128-wide output of a 24,576-row
+    // mini-batch: 384 tiles): 128 x 64 tiles, twice as many blocks (humanoid fwd2 32.2 -> 31.3 us)
+    bn = 64;
+    if (int rc = assign_blocks(g, count, 128, bn, name, blocks)) return rc;
+  }
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, s, g);
     return check_launch(name);
@@ -341,6 +350,7 @@ int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
   }
 #endif
   // two LDS stages (48 KiB with 128 x 128 tiles): three blocks per CU
+  if (bn == 64) return go(gemm_nt_bx6_kernel<64, 3, EPI, 2, true>);
   return go(gemm_nt_bx6_kernel<128, 3, EPI, 2, true>);
 }
 

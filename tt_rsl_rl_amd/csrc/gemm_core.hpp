@@ -1625,12 +1625,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         for (int l = 0; l < LD; ++l) sv[(NA + i) * LD + l] = *reinterpret_cast<const u32x4*>(brow[i] + k0 + 4 * l);
     }
   };
-  auto split_store = [&](int stage, int rb) {
+  auto split_piece = [&](int stage, int rb, int o) __attribute__((always_inline)) {
     unsigned char* st = lds + stage * STAGE;
     const u32x4* const sv = stage_v[rb];
-#pragma unroll
-    for (int o = 0; o < NA + NB; ++o) {
-      if (o >= NA && !stage_b) break;
+    {
+      if (o >= NA && !stage_b) return;
       const int i = o < NA ? o : o - NA;
       const int plane = o < NA ? PLANE_A : PLANE_B;
       unsigned char* row = st + (o < NA ? swz[i] : 3 * PLANE_A + (BKM ? boff[i] : swz[i]));
@@ -1653,6 +1652,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
         *reinterpret_cast<u32x4*>(row + 2 * plane) = u32x4{lo[0], lo[1], lo[2], lo[3]};
       }
     }
+  };
+  auto split_store = [&](int stage, int rb) {
+#pragma unroll
+    for (int o = 0; o < NA + NB; ++o) split_piece(stage, rb, o);
   };
 
   f32x16 acc[TM][TN];
@@ -1709,15 +1712,34 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
                         : frag(st + 3 * PLANE_A + pp * PLANE_B, wn * (BN / 2) + 32 * j + fr);
     }
     constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
+    const int next = cs == 0 ? NS - 1 : cs - 1;
+    if constexpr (BN == 128) {
+      // the next slab's split, one staged row piece after each group of MFMAs: the wave's VALU work and LDS writes
+      // issue while its MFMAs run (humanoid, per mini-batch: dx1 94 -> 88 us, fwd1 84 -> 83 us; the 64-wide tiles,
+      // with half the MFMAs per group, measured 1 us slower that way)
 #pragma unroll
-    for (int t = 0; t < 6; ++t)
+      for (int t = 0; t < 6; ++t) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j][pb[t]], fa[i][pa[t]], acc[i][j], 0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    split_store(cs == 0 ? NS - 1 : cs - 1, rb_store);
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j][pb[t]], fa[i][pa[t]], acc[i][j], 0, 0, 0);
+        if (t < NA + NB) split_piece(next, rb_store, t);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int o = 6; o < NA + NB; ++o) split_piece(next, rb_store, o);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 6; ++t)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j][pb[t]], fa[i][pa[t]], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      split_store(next, rb_store);
+    }
     lds_barrier();
   };
   constexpr int RB_EVEN = NS % 2;  // the buffer iteration kt loads into, kt even
