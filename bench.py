@@ -172,9 +172,14 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
     B = T * N
     A = workload["num_actions"]
     ka, kc = alg.actor.linears[-1].in_features, alg.critic.linears[-1].in_features
-    width = sum(seg.src.shape[1] for seg in engine.segments())
+    # the rows' algorithmic floats: every observation group once, actions, old mean, the four per-transition scalars
+    # (the state-independent std counts once per rollout); the kernel copies every segment it is given, the std and
+    # the 16-byte padding of the action records included
+    groups = {g for m in (alg.actor, alg.critic) for g in m.obs_groups}
+    width = sum(st.observations[g].shape[-1] for g in groups) + 2 * A + 4
+    copied = sum(seg.src.shape[1] for seg in engine.segments())
     nbytes = {
-        "gather": B * (2 * 4 * width + 8),                        # every copied float read + written, int64 index
+        "gather": B * (2 * 4 * width + 8),                        # every float read + written once, int64 index
         "loss": R * 4 * (4 * A + 6) + R * 4 * (A + 1),            # per-row inputs + per-row output gradients
         # fused head: last hidden activations in, their gradients out, batch columns in, mean / value and their
         # gradients out
@@ -205,12 +210,15 @@ def hbm_kernels(alg, engine, phases, workload, R: int) -> dict:
             gbs = b / (ms[k] * 1e-3) / 1e9
             out[k] = {"bytes": b, "mean_us": round(ms[k] * 1e3, 2), "GB/s": round(gbs, 1),
                       "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    if "gather" in out:
+        out["gather"]["row_floats"] = width
+        out["gather"]["copied_bytes"] = B * (2 * 4 * copied + 8)
     # Single-launch floor at these sizes: one plain streaming kernel (torch's elementwise y = x * 1, half the bytes
     # read, half written) moving the same bytes as the kernel, and an empty launch (one element), both by graph replay
     empty = torch.ones(1, device=alg.device)
     out["floor"] = {"empty_launch_us": round(graph_ms(lambda: torch.mul(empty, 1.0, out=empty)) * 1e3, 2)}
     for k in ("gae", "adam", "gather"):
-        n = max(1, nbytes[k] // 8)
+        n = max(1, (out["gather"]["copied_bytes"] if k == "gather" else nbytes[k]) // 8)
         x, y = torch.ones(n, device=alg.device), torch.empty(n, device=alg.device)
         us = graph_ms(lambda: torch.mul(x, 1.0, out=y)) * 1e3
         gbs = 8 * n / (us * 1e-6) / 1e9

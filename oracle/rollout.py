@@ -47,6 +47,8 @@ def train_cfg(workload: dict, algorithm_class: str = "PPO", **alg_overrides) -> 
     actor = dict(class_name=model, hidden_dims=list(workload["hidden_dims"]), activation="elu",
                  obs_normalization=workload["obs_normalization"],
                  distribution_cfg=dict(class_name="GaussianDistribution", init_std=1.0, std_type="log"))
+    if workload.get("learn_std") is False:  # a fixed std (distribution.py:166)
+        actor["distribution_cfg"]["learn_std"] = False
     critic = dict(class_name=model, hidden_dims=list(workload["hidden_dims"]), activation="elu",
                   obs_normalization=workload["obs_normalization"])
     if "rnn" in workload:

@@ -485,6 +485,39 @@ def test_bx6_error_against_fp32_mfma(cuda, op, rows, wide):
         assert e6[0] < 2e-6
 
 
+@pytest.mark.parametrize("rows", [24576, 96, 64])
+def test_linear_bwd_dw_partial_tiles(cuda, rows):
+    """Weight-grads whose outputs (384, 300, 29) or inputs (200, 99) leave partial 128-wide tiles, beside full-width and
+    narrow (48-input, 128 x 64) problems in one launch, with whole 32-row slab pairs (rows a multiple of 32: 2 splits of
+    64 and 32 rows at 96); operands in rows padded to 16 bytes with NaN in the padding, fp64 references, bias
+    gradients included (one problem without)."""
+    ops = _ops()
+    torch.manual_seed(rows + 11)
+    shapes = [(200, 384), (99, 300), (96, 512), (512, 256), (48, 256), (128, 29), (256, 128)]
+
+    def dev(t):
+        buf = torch.full((t.shape[0], -(-t.shape[1] // 4) * 4), float("nan"), device=cuda)
+        buf[:, :t.shape[1]].copy_(t)
+        return buf[:, :t.shape[1]]
+
+    probs, refs = [], []
+    for fin, fout in shapes:
+        dz = torch.randn(rows, fout) / rows
+        x = torch.randn(rows, fin)
+        dw = torch.full((fout, fin), float("nan"), device=cuda)
+        db = torch.full((fout,), float("nan"), device=cuda)
+        probs.append((dev(dz), dev(x), dw, db))
+        refs.append((dw, db, dz.double().t() @ x.double(), dz.double().sum(0), dz.double().abs().sum(0)))
+    probs[1] = probs[1][:3] + (None,)
+    ops.linear_bwd_dw(probs, rows)
+    for i, (dw, db, rw, rb, rb_abs) in enumerate(refs):
+        assert rel_err(dw, rw) < 2e-6, shapes[i]
+        if i == 1:
+            assert torch.isnan(db).all()
+        else:
+            assert ((db.cpu().double() - rb).abs() / rb_abs).max().item() < 1e-6, shapes[i]
+
+
 # ----------------------------------------------------------------------------------------------------------------------
 # A8-A11 losses
 # ----------------------------------------------------------------------------------------------------------------------

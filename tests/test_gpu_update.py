@@ -93,6 +93,9 @@ CASES = {
                                  {"normalize_advantage_per_mini_batch": True, "num_mini_batches": 3}),
     "flat48_unclipped_fixed": (R.scaled(R.WORKLOADS["flat48"], num_envs=200, steps=5, hidden_dims=[128, 64, 32]),
                                {"use_clipped_value_loss": False, "schedule": "fixed", "num_learning_epochs": 2}),
+    # a fixed std (learn_std=False): no gradient, no Adam state and no clip-norm share for the std parameter
+    "humanoid_small_fixed_std": (dict(R.scaled(R.WORKLOADS["humanoid"], num_envs=128, steps=8, hidden_dims=[64, 32]),
+                                      learn_std=False), {}),
     # 40 actions on a 48-wide last hidden layer: outside the fused head's shapes, the separate output-layer path
     "flat48_a40_unfused": (dict(R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[64, 48]),
                                 num_actions=40), {}),
@@ -255,6 +258,10 @@ def test_update_matches_oracle(name, capsys):
                                                  model_o.parameters(), model_64.parameters()):
             err = rel_err(p_h, p_s)
             worst = max(worst, err)
+            if not p_s.requires_grad:  # (learn_std=False: untouched, and no optimiser state on either side)
+                assert not p_h.requires_grad and torch.equal(p_h.detach().cpu(), p_s.detach()), name_p
+                assert p_s not in shadow.optimizer.state and p_h not in hip.optimizer.state, name_p
+                continue
             s_s, s_h = shadow.optimizer.state[p_s], hip.optimizer.state[p_h]
             m1 = rel_err(s_h["exp_avg"], s_s["exp_avg"], 1e-12)
             m2 = rel_err(s_h["exp_avg_sq"], s_s["exp_avg_sq"], 1e-20)
@@ -470,8 +477,10 @@ def _adam_state(opt, p):
 def _snapshot(alg) -> dict:
     params = list(chain(alg.actor.parameters(), alg.critic.parameters()))
     moments = [_adam_state(alg.optimizer, p) for p in params]
+    # (the optimiser's step count: a parameter without a gradient -- learn_std=False -- has no state and no count)
     return {"params": [p.detach().clone() for p in params], "lr": alg.learning_rate,
-            "exp_avg": [m[0] for m in moments], "exp_avg_sq": [m[1] for m in moments], "step": moments[0][2]}
+            "exp_avg": [m[0] for m in moments], "exp_avg_sq": [m[1] for m in moments],
+            "step": max(m[2] for m in moments)}
 
 
 def _load_oracle_state(ora, snap: dict) -> None:
@@ -483,6 +492,8 @@ def _load_oracle_state(ora, snap: dict) -> None:
     ora.optimizer.state.clear()
     if snap["step"] > 0:
         for p, m1, m2 in zip(params, snap["exp_avg"], snap["exp_avg_sq"]):
+            if not p.requires_grad:
+                continue
             ora.optimizer.state[p] = {"step": torch.tensor(float(snap["step"])), "exp_avg": m1.clone(),
                                       "exp_avg_sq": m2.clone()}
     ora.learning_rate = snap["lr"]

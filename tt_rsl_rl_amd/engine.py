@@ -182,6 +182,10 @@ class UpdateEngine:
         self.buf_a = ModelBuffers(actor, self.R_max, self.device)
         self.buf_c = ModelBuffers(critic, self.R_max, self.device)
         self.loss_ws = torch.empty(ops.loss_workspace_bytes(self.R_max, self.A), dtype=torch.uint8, device=self.device)
+        # learn_std=False (distribution.py:166): the std parameter takes no gradient; the loss kernels' gradient for it
+        # goes here instead of into the flat gradient, whose slot stays zero, so Adam leaves the parameter (and its
+        # zero moments) as they are and the clip norms do not count it
+        self.std_grad_sink = torch.zeros_like(actor.distribution.param)
         # the output layers, loss and their input-grad as one launch (ppo_gauss_ppo_head) where it takes the shapes
         la, lc = actor.linears, critic.linears
         self.fused_head = (len(la) >= 2 and len(la) == len(lc) and
@@ -422,7 +426,7 @@ class UpdateEngine:
         group = lambda off: max(i for i in range(len(bounds) - 1) if bounds[i] <= off)  # noqa: E731
         extra = []
         for p in f.params:
-            if id(p) not in linear:
+            if id(p) not in linear and p.requires_grad:  # (a fixed std takes no gradient: not in the norms)
                 off, k = f.offsets[id(p)]
                 extra.append((off, off + k, group(off)))
         if len(extra) > L.MAX_EXTRA_GRADS or len(bounds) - 1 > L.MAX_PARAM_GROUPS:
@@ -453,18 +457,19 @@ class UpdateEngine:
                                   ba.dz[-1][:R], bc.dz[-1][:R, 0])
         tm = self.timer
         adaptive = alg.desired_kl is not None and alg.schedule == "adaptive"
+        std_grad = alg.flat.grad_view(dist.param) if dist.param.requires_grad else self.std_grad_sink
         if self.fused_head:
             la, lc = self._layers()
             tm.start("head")
             ops.ppo_head(args, ba.h[-1][:R], la[-1].weight, la[-1].bias, bc.h[-1][:R], lc[-1].weight, lc[-1].bias,
-                         ba.dz[-2][:R], bc.dz[-2][:R], self.head_ws, alg.flat.grad_view(dist.param),
+                         ba.dz[-2][:R], bc.dz[-2][:R], self.head_ws, std_grad,
                          alg.device_state, adaptive, alg.desired_kl, self.trace, mean=ba.out[:R],
                          value=bc.out[:R, 0])
             tm.stop("head")
             return
         tm.start("loss")
         ops.ppo_loss(args, self.loss_ws)
-        ops.ppo_loss_finalize(args, self.loss_ws, alg.flat.grad_view(dist.param), alg.device_state, adaptive,
+        ops.ppo_loss_finalize(args, self.loss_ws, std_grad, alg.device_state, adaptive,
                               alg.desired_kl if alg.desired_kl is not None else 0.0, self.trace)
         tm.stop("loss")
 

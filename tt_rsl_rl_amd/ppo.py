@@ -171,8 +171,6 @@ class PPO:
             raise NotImplementedError("the HIP recurrent update needs both actor and critic recurrent (or neither)")
         if actor.distribution is None:
             raise ValueError("the actor needs a GaussianDistribution (distribution_cfg)")
-        if not actor.distribution.param.requires_grad:
-            raise NotImplementedError("learn_std=False is not supported by the fused update")
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("tt_rsl_rl_amd.ppo.PPO runs on a GPU device (no CPU path)")
@@ -422,12 +420,15 @@ class PPO:
         """Expose the flat Adam moments through torch.optim.Adam's state (views, no copies).  Every parameter takes
         the same number of steps, so they share one step tensor, updated in place."""
         steps = float(self._opt_steps)
+        # a parameter that takes no gradient (learn_std=False) has no Adam state, as in torch.optim.Adam, whose step
+        # skips parameters whose .grad is None
+        learned = [p for p in self.flat.params if p.requires_grad]
         if self._step_tensor is not None and all(
-                self.optimizer.state[p].get("step") is self._step_tensor for p in self.flat.params):
+                self.optimizer.state[p].get("step") is self._step_tensor for p in learned):
             self._step_tensor.fill_(steps)
             return
         self._step_tensor = torch.tensor(steps)
-        for p in self.flat.params:
+        for p in learned:
             s = self.optimizer.state[p]
             s["step"] = self._step_tensor
             s["exp_avg"] = self.flat.exp_avg_view(p)
