@@ -29,8 +29,17 @@ enum {
   PPO_EUNSUPPORTED = -3, /* shape or option outside what the kernels implement */
 };
 
-enum { PPO_ACT_NONE = 0, PPO_ACT_ELU = 1 };
-/* what ppo_linear_bwd_dx's z_prev holds: the ELU input (pre-activation) or its output h = elu(z) */
+/* hidden-layer activations: rsl_rl's resolve_nn_activation names (rsl_rl/utils/utils.py:34-68) with torch's default
+ * arguments: elu, selu, relu, crelu (CELU, alpha 1), lrelu (slope 0.01), tanh, sigmoid, softplus (beta 1, threshold
+ * 20), gelu (erf), swish (SiLU), mish, identity */
+enum {
+  PPO_ACT_NONE = 0, PPO_ACT_ELU = 1, PPO_ACT_SELU = 2, PPO_ACT_RELU = 3, PPO_ACT_CELU = 4, PPO_ACT_LRELU = 5,
+  PPO_ACT_TANH = 6, PPO_ACT_SIGMOID = 7, PPO_ACT_SOFTPLUS = 8, PPO_ACT_GELU = 9, PPO_ACT_SILU = 10, PPO_ACT_MISH = 11,
+  PPO_ACT_IDENTITY = 12
+};
+#define PPO_ACT_COUNT 13
+/* what an input-grad's z_prev holds: the activation's input (pre-activation) or its output h = act(z); the output
+ * serves only the monotone activations (elu, selu, relu, crelu, lrelu, tanh, sigmoid, identity) */
 enum { PPO_ELU_FROM_INPUT = 0, PPO_ELU_FROM_OUTPUT = 1 };
 enum { PPO_STD_SCALAR = 0, PPO_STD_LOG = 1 };
 
@@ -140,9 +149,10 @@ int ppo_host_rng_skip(uint8_t* generator_state, size_t state_bytes, int64_t draw
  * ------------------------------------------------------------------------------------------------------------------ */
 #define PPO_MAX_LINEAR_PROBLEMS 12
 
-/* forward: z = x w^T + b; with PPO_ACT_ELU also h = elu(z) (alpha 1).  Replaces nn.Linear.forward / nn.ELU.forward.
- * With PPO_ACT_ELU either output may be NULL (not both): a backward that takes ELU' from h
- * (PPO_ELU_FROM_OUTPUT) needs only h.  With PPO_ACT_NONE z is required and h is ignored. */
+/* forward: z = x w^T + b; with an activation (PPO_ACT_ELU ... PPO_ACT_IDENTITY) also h = act(z).  Replaces
+ * nn.Linear.forward and the activation module's forward (rsl_rl/modules/mlp.py:91-95).  With an activation either
+ * output may be NULL (not both): a backward that takes act' from h (PPO_ELU_FROM_OUTPUT, monotone activations) needs
+ * only h; the others need z.  With PPO_ACT_NONE z is required and h is ignored. */
 typedef struct ppo_linear_fwd_problem {
   const float* x; int64_t ldx; /* [rows, in] */
   const float* w;              /* [out, in] */
@@ -175,6 +185,13 @@ typedef struct ppo_linear_bwd_dx_problem {
 size_t ppo_linear_bwd_dx_workspace_bytes(const ppo_linear_bwd_dx_problem* problems, int32_t count);
 int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t elu_source,
                       void* workspace, size_t workspace_bytes, ppo_stream_t stream);
+/* the same for any hidden-layer activation: dz_prev = (dz w) * act'(z_prev), z_prev the activation's input, or its
+ * output with source = PPO_ELU_FROM_OUTPUT (monotone activations only; PPO_EINVAL otherwise).  ppo_linear_bwd_dx is
+ * this call with PPO_ACT_ELU.  Replaces autograd's mm backward + the activation's backward (torch's
+ * elu_backward / threshold_backward / leaky_relu_backward / tanh_backward / sigmoid_backward / softplus_backward /
+ * gelu_backward / silu_backward / mish_backward). */
+int ppo_linear_bwd_dx_act(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t activation,
+                          int32_t source, void* workspace, size_t workspace_bytes, ppo_stream_t stream);
 
 /* backward to the parameters: dw = dz^T x, db = sum_rows dz, reduced over rows in fixed-order split-K partials
  * (deterministic: no float atomics).  Replaces autograd's AddmmBackward for weight and bias. */

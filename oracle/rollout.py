@@ -44,12 +44,13 @@ DEFAULT_ALGORITHM = dict(num_learning_epochs=5, num_mini_batches=4, clip_param=0
 def train_cfg(workload: dict, algorithm_class: str = "PPO", **alg_overrides) -> dict:
     """The runner-style config of a workload (upstream layout: algorithm / actor / critic / obs_groups)."""
     model = "RNNModel" if "rnn" in workload else "MLPModel"
-    actor = dict(class_name=model, hidden_dims=list(workload["hidden_dims"]), activation="elu",
+    actor = dict(class_name=model, hidden_dims=list(workload["hidden_dims"]), activation=workload.get("activation", "elu"),
                  obs_normalization=workload["obs_normalization"],
                  distribution_cfg=dict(class_name="GaussianDistribution", init_std=1.0, std_type="log"))
     if workload.get("learn_std") is False:  # a fixed std (distribution.py:166)
         actor["distribution_cfg"]["learn_std"] = False
-    critic = dict(class_name=model, hidden_dims=list(workload["hidden_dims"]), activation="elu",
+    critic = dict(class_name=model, hidden_dims=list(workload["hidden_dims"]),
+                  activation=workload.get("critic_activation", workload.get("activation", "elu")),
                   obs_normalization=workload["obs_normalization"])
     if "rnn" in workload:
         actor.update(workload["rnn"])

@@ -179,6 +179,59 @@ def test_linear_fwd_grouped(cuda, rows, aligned_x):
         assert rel_err(h, _elu64(z64)) < 2e-6
 
 
+_ACT64 = {  # the activations' closed forms in fp64 (torch's modules with their default arguments)
+    "elu": lambda z: torch.where(z > 0, z, torch.expm1(z)),
+    "selu": lambda z: 1.0507009873554805 * torch.where(z > 0, z, 1.6732632423543772 * torch.expm1(z)),
+    "relu": lambda z: z.clamp(min=0),
+    "crelu": lambda z: torch.where(z > 0, z, torch.expm1(z)),
+    "lrelu": lambda z: torch.where(z > 0, z, 0.01 * z),
+    "tanh": torch.tanh,
+    "sigmoid": torch.sigmoid,
+    "softplus": lambda z: torch.where(z > 20, z, torch.log1p(torch.exp(z))),
+    "gelu": lambda z: 0.5 * z * (1 + torch.erf(z / math.sqrt(2))),
+    "swish": lambda z: z * torch.sigmoid(z),
+    "mish": lambda z: z * torch.tanh(torch.log1p(torch.exp(z))),
+    "identity": lambda z: z,
+}
+
+
+@pytest.mark.parametrize("name", list(_ACT64))
+@pytest.mark.parametrize("aligned", [True, False])
+def test_linear_activations(cuda, name, aligned):
+    """Every hidden-layer activation rsl_rl resolves (rsl_rl/utils/utils.py:34-68): the forward's h = act(x w^T + b)
+    and the input-grad's (dz w) * act'(.) from the activation's input z and, for the monotone ones, from its output h,
+    against fp64 (autograd of the closed form for act'), on the bf16x6 kernels (16-byte rows) and on the fp32-MFMA
+    kernels (rows one float off 16 bytes); a plain input-grad (no activation) beside them in the forward test."""
+    from tt_rsl_rl_amd import _lib as L
+
+    ops = _ops()
+    act = L.ACTIVATIONS[name]
+    torch.manual_seed(act + 100 * aligned)
+    rows, fin, fout = 3000, 96, 256
+    x = torch.randn(rows, fin)
+    w = torch.randn(fout, fin) / math.sqrt(fin) * 2
+    b = torch.randn(fout)
+    z64 = x.double() @ w.double().t() + b.double()
+    h64 = _ACT64[name](z64)
+    xd = _operand(x, "bx6" if aligned else "fp32", cuda)
+    z, h = torch.empty(rows, fout, device=cuda), torch.empty(rows, fout, device=cuda)
+    ops.linear_fwd([(xd, w.to(cuda), b.to(cuda), z, h)], rows, act=act)
+    assert rel_err(z, z64) < 2e-6
+    assert rel_err(h, h64) < 2e-6, name
+    # input-grad into that layer: dz_prev = (dz w2) * act'(z)
+    w2 = torch.randn(64, fout) / 8
+    dz = torch.randn(rows, 64)
+    zr = z.detach().double().cpu().requires_grad_(True)
+    g64 = torch.autograd.grad(_ACT64[name](zr).sum(), zr)[0]
+    ref = (dz.double() @ w2.double()) * g64
+    sources = [(False, z)] + ([(True, h)] if act in L.ACT_FROM_OUTPUT else [])
+    for from_output, src in sources:
+        out = torch.empty(rows, fout, device=cuda)
+        ops.linear_bwd_dx([(_operand(dz, "bx6" if aligned else "fp32", cuda), w2.to(cuda), src, out)], rows,
+                          elu_from_output=from_output, act=act)
+        assert rel_err(out, ref) < 2e-6, (name, from_output)
+
+
 @pytest.mark.parametrize("rows", [1, 130, 24576 + 77])
 @pytest.mark.parametrize("elu", [True, False])
 def test_linear_fwd_narrow_inputs(cuda, rows, elu):

@@ -96,6 +96,15 @@ CASES = {
     # a fixed std (learn_std=False): no gradient, no Adam state and no clip-norm share for the std parameter
     "humanoid_small_fixed_std": (dict(R.scaled(R.WORKLOADS["humanoid"], num_envs=128, steps=8, hidden_dims=[64, 32]),
                                       learn_std=False), {}),
+    # other hidden-layer activations (rsl_rl/utils/utils.py:34-68): tanh (act' from the output), gelu (from the
+    # stored input), actor relu with a softplus critic (one launch per model); the separate output-layer path
+    "humanoid_small_tanh": (dict(R.scaled(R.WORKLOADS["humanoid"], num_envs=128, steps=8, hidden_dims=[64, 32]),
+                                 activation="tanh"), {}),
+    "flat48_small_gelu": (dict(R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[128, 64, 32]),
+                               activation="gelu"), {}),
+    "rough235_small_relu_softplus": (dict(R.scaled(R.WORKLOADS["rough235"], num_envs=128, steps=8,
+                                                   hidden_dims=[64, 32]), activation="relu",
+                                          critic_activation="softplus"), {}),
     # 40 actions on a 48-wide last hidden layer: outside the fused head's shapes, the separate output-layer path
     "flat48_a40_unfused": (dict(R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[64, 48]),
                                 num_actions=40), {}),
@@ -134,7 +143,7 @@ def _record(test: str, name: str, data: dict) -> None:
 
 # cases whose output layers fall outside the fused head (more than 32 actions, or a last hidden width that is not a
 # multiple of 16)
-UNFUSED = {"flat48_a40_unfused"}
+UNFUSED = {"flat48_a40_unfused", "humanoid_small_tanh", "flat48_small_gelu", "rough235_small_relu_softplus"}
 
 
 @functools.lru_cache(maxsize=None)

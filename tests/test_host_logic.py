@@ -9,6 +9,7 @@ import copy
 import pytest
 import torch
 
+from oracle import ppo_ref as O
 from oracle import rollout as R
 from tt_rsl_rl_amd import workloads as W
 from tt_rsl_rl_amd.engine import TableLayout
@@ -94,11 +95,21 @@ def test_recurrent_options_outside_the_kernels_are_rejected():
         PPO(actor, critic, None, device="cuda")
 
 
-def test_non_elu_activation_is_rejected():
+@pytest.mark.parametrize("name", ["elu", "selu", "relu", "crelu", "lrelu", "tanh", "sigmoid", "softplus", "gelu",
+                                  "swish", "mish", "identity", "ELU"])
+def test_activations_resolve_to_upstream_modules_and_kernel_codes(name):
+    """Every activation name upstream resolves (rsl_rl/utils/utils.py:34-68) builds the model with upstream's module in
+    every hidden slot and the kernels' code for it; unknown names raise upstream's ValueError."""
+    from tt_rsl_rl_amd import _lib as L
+
     w = R.scaled(R.WORKLOADS["flat48"], num_envs=8)
     cfg = W.train_cfg(w)
-    with pytest.raises(NotImplementedError):
-        MLPModel(R.zero_obs(w), cfg["obs_groups"], "critic", 1, hidden_dims=[8], activation="tanh")
+    m = MLPModel(R.zero_obs(w), cfg["obs_groups"], "critic", 1, hidden_dims=[8, 4], activation=name)
+    ref = O.activation_module(name)
+    assert [type(x) for x in m.mlp] == [torch.nn.Linear, type(ref), torch.nn.Linear, type(ref), torch.nn.Linear]
+    assert m.act_code == L.ACTIVATIONS[name.lower()]
+    with pytest.raises(ValueError, match="Invalid activation"):
+        MLPModel(R.zero_obs(w), cfg["obs_groups"], "critic", 1, hidden_dims=[8], activation="swishy")
 
 
 @pytest.mark.parametrize("da, dc, a", [(96, 99, 29), (48, 48, 12), (235, 235, 12), (3, 5, 1)])

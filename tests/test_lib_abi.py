@@ -118,6 +118,19 @@ def test_argument_validation_reports_errors_without_a_gpu():
     with pytest.raises(ValueError, match="num_actions"):
         args = _lib.LossArgs(rows=10, num_actions=65)
         _lib.call("ppo_gauss_ppo_loss", ctypes.byref(args), None, 0, None)
+    # activations: codes in [0, PPO_ACT_COUNT), and act' from the output only for the monotone ones
+    prob = _lib.LinearFwdProblem(x=16, ldx=96, w=16, b=16, z=16, ldz=256, in_features=96, out_features=256)
+    with pytest.raises(ValueError, match="activation=13"):
+        _lib.call("ppo_linear_fwd", ctypes.byref(prob), 1, 10, 13, None)
+    dx = _lib.LinearBwdDxProblem(dz=16, lddz=64, w=16, z_prev=16, ldz_prev=256, dz_prev=16, lddz_prev=256,
+                                 in_features=256, out_features=64)
+    for name in ("softplus", "gelu", "swish", "mish"):
+        with pytest.raises(ValueError, match="needs the activation's input"):
+            _lib.call("ppo_linear_bwd_dx_act", ctypes.byref(dx), 1, 10, _lib.ACTIVATIONS[name],
+                      _lib.PPO_ELU_FROM_OUTPUT, None, 0, None)
+    with pytest.raises(ValueError, match="activation=0"):
+        _lib.call("ppo_linear_bwd_dx_act", ctypes.byref(dx), 1, 10, 0, _lib.PPO_ELU_FROM_INPUT, None, 0, None)
+    assert sorted(_lib.ACTIVATIONS.values()) == list(range(1, 13))
     # workspace queries are pure host arithmetic
     assert lib.ppo_adv_normalize_workspace_bytes(98304) > 0
     assert lib.ppo_loss_workspace_bytes(24576, 29) > 0

@@ -109,3 +109,33 @@ def test_running_moments_equal_pooled_moments():
     assert torch.allclose(n._mean.double().view(-1), pooled.mean(0), rtol=1e-5, atol=1e-6)
     assert torch.allclose(n._var.double().view(-1), pooled.var(0, unbiased=False), rtol=1e-5)
     assert int(n.count) == 3500
+
+
+def test_activation_modules_are_the_closed_forms():
+    """rsl_rl/utils/utils.py:34-68: every name resolves to the module whose output is the textbook function (torch's
+    default arguments: SELU's alpha / scale, LeakyReLU slope 0.01, CELU alpha 1, Softplus beta 1 with threshold 20,
+    exact-erf GELU), checked in fp64 on values across every branch; unknown names raise ValueError."""
+    import math
+
+    from oracle import ppo_ref as O
+
+    x = torch.linspace(-30.0, 30.0, 2001, dtype=torch.float64)
+    e = lambda v: torch.tensor([math.exp(t) for t in v.tolist()], dtype=torch.float64)  # noqa: E731
+    sig = 1.0 / (1.0 + e(-x))
+    sp = torch.where(x > 20, x, torch.log(1.0 + e(x)))
+    want = {
+        "elu": torch.where(x > 0, x, e(x) - 1), "crelu": torch.where(x > 0, x, e(x) - 1),
+        "selu": 1.0507009873554805 * torch.where(x > 0, x, 1.6732632423543772 * (e(x) - 1)),
+        "relu": torch.where(x > 0, x, torch.zeros_like(x)), "lrelu": torch.where(x > 0, x, 0.01 * x),
+        "tanh": torch.tensor([math.tanh(t) for t in x.tolist()], dtype=torch.float64), "sigmoid": sig,
+        "softplus": sp, "gelu": torch.tensor([0.5 * t * (1 + math.erf(t / math.sqrt(2))) for t in x.tolist()],
+                                             dtype=torch.float64),
+        "swish": x * sig, "mish": x * torch.tensor([math.tanh(t) for t in torch.log(1.0 + e(x)).tolist()],
+                                                     dtype=torch.float64),
+        "identity": x,
+    }
+    for name, ref in want.items():
+        got = O.activation_module(name)(x)
+        assert torch.allclose(got, ref, rtol=1e-12, atol=1e-12), name
+    with pytest.raises(ValueError):
+        O.activation_module("swishy")

@@ -21,6 +21,11 @@ PPO_EHIP = -2
 PPO_EUNSUPPORTED = -3
 PPO_ACT_NONE = 0
 PPO_ACT_ELU = 1
+# rsl_rl's activation names (rsl_rl/utils/utils.py:34-68) -> the library's codes
+ACTIVATIONS = {"elu": 1, "selu": 2, "relu": 3, "crelu": 4, "lrelu": 5, "tanh": 6, "sigmoid": 7, "softplus": 8,
+               "gelu": 9, "swish": 10, "mish": 11, "identity": 12}
+# activations whose derivative the input-grad can take from the activation's output (the rest need its input)
+ACT_FROM_OUTPUT = {1, 2, 3, 4, 5, 6, 7, 12}
 PPO_ELU_FROM_INPUT = 0
 PPO_ELU_FROM_OUTPUT = 1
 PPO_STD_SCALAR = 0
@@ -146,6 +151,8 @@ _SIGNATURES = [
     ("ppo_lstm_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
     ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),
     ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, C.c_void_p, C.c_size_t,
+                                    C.c_void_p]),
+    ("ppo_linear_bwd_dx_act", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, i32, C.c_void_p, C.c_size_t,
                                     C.c_void_p]),
     ("ppo_linear_bwd_dw_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDwProblem), i32, i64]),
     ("ppo_linear_bwd_dw", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, C.c_void_p]),

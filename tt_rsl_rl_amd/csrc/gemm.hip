@@ -418,12 +418,12 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS,
               "ppo_linear_fwd: count=%d outside [1, %d]", count, PPO_MAX_LINEAR_PROBLEMS);
   PPO_REQUIRE(rows_ok(rows), "ppo_linear_fwd: rows=%lld", (long long)rows);
-  PPO_REQUIRE(activation == PPO_ACT_NONE || activation == PPO_ACT_ELU, "ppo_linear_fwd: activation=%d", activation);
+  PPO_REQUIRE(activation >= PPO_ACT_NONE && activation < PPO_ACT_COUNT, "ppo_linear_fwd: activation=%d", activation);
+  const bool elu = activation != PPO_ACT_NONE;  // (any activation: the bias + activation epilogue)
   Group g{};
   int max_n = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_linear_fwd_problem& q = problems[i];
-    const bool elu = activation == PPO_ACT_ELU;
     PPO_REQUIRE(q.x && q.w && q.b && (q.z || (elu && q.h)), "ppo_linear_fwd: problem %d has a null pointer", i);
     PPO_REQUIRE(q.in_features > 0 && q.out_features > 0, "ppo_linear_fwd: problem %d features", i);
     PPO_REQUIRE(q.ldx >= q.in_features && (q.z == nullptr || q.ldz >= q.out_features) &&
@@ -441,20 +441,21 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
     p.splits = 1; p.k_chunk = q.in_features;
     p.c_vec = (q.z == nullptr || w16_ok(q.z, q.ldz)) && (!elu || q.h == nullptr || w16_ok(q.h, q.ldh));
     if (!elu) p.C2 = nullptr;
+    p.act = activation;
     max_n = std::max(max_n, q.out_features);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   // measured on MI355X for 24576-row mini-batches: outputs wider than 128 like 128x128 tiles with 16-deep slabs,
   // narrower ones 128x64
-  const int brc = activation == PPO_ACT_ELU ? launch_nt_bx6<EPI_BIAS_ELU>(g, count, s, "linear_fwd_elu")
-                                            : launch_nt_bx6<EPI_BIAS>(g, count, s, "linear_fwd");
+  const int brc = elu ? launch_nt_bx6<EPI_BIAS_ELU>(g, count, s, "linear_fwd_act")
+                      : launch_nt_bx6<EPI_BIAS>(g, count, s, "linear_fwd");
   if (brc != PPO_EUNSUPPORTED) return brc;
   const int pt = pipe_tile("PPO_HIP_PIPE_FWD", max_n > 128 ? 1 : 2);
-  const int prc = activation == PPO_ACT_ELU ? launch_nt_pipe_tile<EPI_BIAS_ELU>(pt, g, count, s, "linear_fwd_elu")
-                                            : launch_nt_pipe_tile<EPI_BIAS>(pt, g, count, s, "linear_fwd");
+  const int prc = elu ? launch_nt_pipe_tile<EPI_BIAS_ELU>(pt, g, count, s, "linear_fwd_act")
+                      : launch_nt_pipe_tile<EPI_BIAS>(pt, g, count, s, "linear_fwd");
   if (prc != PPO_EUNSUPPORTED) return prc;
   const Tile t = pick_tile(max_n > 128 ? T128x128k16s2o3 : T128x64k32s2o4);
-  if (activation == PPO_ACT_ELU) return launch_nt_tile<EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_elu");
+  if (elu) return launch_nt_tile<EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_act");
   return launch_nt_tile<EPI_BIAS>(t, g, count, s, "linear_fwd");
 }
 
@@ -498,12 +499,22 @@ int launch_transposes(const ppo_linear_bwd_dx_problem* problems, int count, floa
 }
 
 // w^T of every problem into the workspace, then the input-grad GEMMs on those copies.
-int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t elu_source,
-            void* workspace, size_t workspace_bytes, ppo_stream_t stream, const char* who) {
+// act' can be evaluated from the activation's output (monotone activations: the output determines the input)
+bool act_from_output_ok(int act) {
+  return act == PPO_ACT_ELU || act == PPO_ACT_SELU || act == PPO_ACT_RELU || act == PPO_ACT_CELU ||
+         act == PPO_ACT_LRELU || act == PPO_ACT_TANH || act == PPO_ACT_SIGMOID || act == PPO_ACT_IDENTITY;
+}
+
+int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t activation,
+            int32_t elu_source, void* workspace, size_t workspace_bytes, ppo_stream_t stream, const char* who) {
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS, "%s: count=%d outside [1, %d]",
               who, count, PPO_MAX_LINEAR_PROBLEMS);
-  PPO_REQUIRE(elu_source == PPO_ELU_FROM_INPUT || elu_source == PPO_ELU_FROM_OUTPUT, "%s: elu_source=%d", who,
+  PPO_REQUIRE(activation > PPO_ACT_NONE && activation < PPO_ACT_COUNT, "%s: activation=%d", who, activation);
+  PPO_REQUIRE(elu_source == PPO_ELU_FROM_INPUT || elu_source == PPO_ELU_FROM_OUTPUT, "%s: source=%d", who,
               elu_source);
+  PPO_REQUIRE(elu_source == PPO_ELU_FROM_INPUT || act_from_output_ok(activation),
+              "%s: activation %d: its derivative needs the activation's input (source PPO_ELU_FROM_INPUT)", who,
+              activation);
   PPO_REQUIRE(rows_ok(rows), "%s: rows=%lld", who, (long long)rows);
   bool any_act = false, any_plain = false;
   for (int i = 0; i < count; ++i) {
@@ -535,6 +546,7 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
     p.splits = 1; p.k_chunk = q.out_features;
     p.c_vec = w16_ok(q.dz_prev, q.lddz_prev) && (q.z_prev == nullptr || w16_ok(q.z_prev, q.ldz_prev));
     p.elu_from_output = elu_source == PPO_ELU_FROM_OUTPUT;
+    p.act = activation;
     max_n = std::max(max_n, q.in_features);
   }
   // the bf16x6 kernel reads the weights as stored (k-major, 16-byte rows): no transpose
@@ -565,7 +577,15 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
 
 extern "C" int ppo_linear_bwd_dx(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
                                  int32_t elu_source, void* workspace, size_t workspace_bytes, ppo_stream_t stream) {
-  return dx_gemm(problems, count, rows, elu_source, workspace, workspace_bytes, stream, "ppo_linear_bwd_dx");
+  return dx_gemm(problems, count, rows, PPO_ACT_ELU, elu_source, workspace, workspace_bytes, stream,
+                 "ppo_linear_bwd_dx");
+}
+
+extern "C" int ppo_linear_bwd_dx_act(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
+                                     int32_t activation, int32_t source, void* workspace, size_t workspace_bytes,
+                                     ppo_stream_t stream) {
+  return dx_gemm(problems, count, rows, activation, source, workspace, workspace_bytes, stream,
+                 "ppo_linear_bwd_dx_act");
 }
 
 extern "C" size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_problem* problems, int32_t count,

@@ -77,7 +77,8 @@ struct Problem {
   int32_t tiles_m, tiles_n, splits, k_chunk;
   int32_t block_begin;
   int32_t c_vec;            // NT epilogue: C (and C2 / aux when used) allow 16-byte accesses
-  int32_t elu_from_output;  // input-grad: aux holds h = elu(z) (ELU' = 1 if h > 0 else h + 1), else z
+  int32_t elu_from_output;  // input-grad: aux holds h = act(z) (act' from the output), else z
+  int32_t act;              // EPI_BIAS_ELU / EPI_ELU_GRAD: the hidden layers' activation (PPO_ACT_*)
   int32_t b16;              // NT: B allows 16-byte direct loads (set by launch_nt)
   int32_t tn64;             // TN bf16x6: 128 x 64 output tiles (problems at most 64 columns wide)
   LstmArgs lstm;            // EPI_LSTM_*
@@ -108,6 +109,98 @@ __device__ __forceinline__ float elu_fwd(float x) {
   const float near0 = fmaf(x * x, p, x);
   const float far = __builtin_amdgcn_exp2f(x * 1.4426950408889634f) - 1.0f;
   return x > 0.0f ? x : (x > -0.7f ? near0 : far);
+}
+
+// The hidden-layer activations of rsl_rl's MLP (rsl_rl/utils/utils.py:34-68, torch's modules with their default
+// arguments) and their derivatives, as torch's CPU kernels evaluate them: SELU = scale (x or alpha (e^x - 1)),
+// LeakyReLU slope 0.01, CELU alpha 1 = ELU, Softplus beta 1 threshold 20, GELU on erf, SiLU x sigma(x),
+// Mish x tanh(softplus(x)).  act_grad(src) is act'(z) from the layer's input z, or, where the derivative is a
+// function of the output h (every monotone one), from h: ELU / CELU h + 1 (h <= 0), SELU h + alpha scale, tanh
+// 1 - h^2, sigmoid (1 - h) h.  ELU itself keeps elu_fwd (the epilogues test for it first).
+constexpr float kSeluAlpha = 1.6732632423543772f, kSeluScale = 1.0507009873554805f;
+constexpr float kSeluAS = kSeluAlpha * kSeluScale;
+
+__device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float act_fwd(int act, float x) {
+  switch (act) {
+    case PPO_ACT_SELU: return x > 0.0f ? x * kSeluScale : (expf(x) - 1.0f) * kSeluAS;
+    case PPO_ACT_RELU: return x > 0.0f ? x : 0.0f;
+    case PPO_ACT_LRELU: return x > 0.0f ? x : x * 0.01f;
+    case PPO_ACT_TANH: return tanhf(x);
+    case PPO_ACT_SIGMOID: return sigmoid_ref(x);
+    case PPO_ACT_SOFTPLUS: return x > 20.0f ? x : log1pf(expf(x));
+    case PPO_ACT_GELU: return x * 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+    case PPO_ACT_SILU: return x / (1.0f + expf(-x));
+    case PPO_ACT_MISH: return x * tanhf(log1pf(expf(x)));
+    case PPO_ACT_IDENTITY: return x;
+    default: return elu_fwd(x);  // PPO_ACT_ELU, PPO_ACT_CELU
+  }
+}
+
+// act'(.) of `src`: the output h when from_output (monotone activations only: the host checks), else the input z.
+__device__ __forceinline__ float act_grad(int act, float src, bool from_output) {
+  switch (act) {
+    case PPO_ACT_SELU:
+      return src > 0.0f ? kSeluScale : (from_output ? src + kSeluAS : kSeluAS * expf(src));
+    case PPO_ACT_RELU: return src > 0.0f ? 1.0f : 0.0f;
+    case PPO_ACT_LRELU: return src > 0.0f ? 1.0f : 0.01f;
+    case PPO_ACT_TANH: {
+      const float t = from_output ? src : tanhf(src);
+      return 1.0f - t * t;
+    }
+    case PPO_ACT_SIGMOID: {
+      const float y = from_output ? src : sigmoid_ref(src);
+      return (1.0f - y) * y;
+    }
+    case PPO_ACT_SOFTPLUS: {
+      const float z = expf(src);
+      return src > 20.0f ? 1.0f : z / (z + 1.0f);
+    }
+    case PPO_ACT_GELU: {
+      const float cdf = 0.5f * (1.0f + erff(src * 0.70710678118654752f));
+      const float pdf = expf(-0.5f * src * src) * 0.39894228040143268f;
+      return cdf + src * pdf;
+    }
+    case PPO_ACT_SILU: {
+      const float sg = sigmoid_ref(src);
+      return sg * (1.0f + src * (1.0f - sg));
+    }
+    case PPO_ACT_MISH: {
+      const float sg = sigmoid_ref(src);
+      const float ts = tanhf(log1pf(expf(src)));
+      return ts + src * sg * (1.0f - ts * ts);
+    }
+    case PPO_ACT_IDENTITY: return 1.0f;
+    default: return src > 0.0f ? 1.0f : (from_output ? src + 1.0f : expf(src));  // ELU, CELU
+  }
+}
+
+// Four outputs of an epilogue: o2 = act(o); ELU (the default of every workload here) on its own path.
+__device__ __forceinline__ void act_fwd4(int act, const f32x4& o, f32x4& o2) {
+  if (act == PPO_ACT_ELU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o2[e] = elu_fwd(o[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o2[e] = act_fwd(act, o[e]);
+  }
+}
+
+// o = x * act'(src); ELU's exactly as before the other activations existed (x itself where act' = 1).
+__device__ __forceinline__ void act_grad4(int act, int from_output, const f32x4& x, const f32x4& src, f32x4& o) {
+  if (act == PPO_ACT_ELU) {
+    if (from_output) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = src[e] > 0.0f ? x[e] : x[e] * (src[e] + 1.0f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = src[e] > 0.0f ? x[e] : x[e] * expf(src[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = x[e] * act_grad(act, src[e], from_output != 0);
+  }
 }
 
 struct Group {
@@ -589,10 +682,8 @@ __device__ __forceinline__ void gemm_nt_tile(const Group& g, const TileCoord& tc
         f32x4 o, o2;
         if (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[e] = x[e] + bias[e];
-            o2[e] = elu_fwd(o[e]);
-          }
+          for (int e = 0; e < 4; ++e) o[e] = x[e] + bias[e];
+          if (EPI == EPI_BIAS_ELU) act_fwd4(P.act, o, o2);
         } else if (EPI == EPI_ELU_GRAD) {
           f32x4 zp;
           if (full) {
@@ -601,13 +692,7 @@ __device__ __forceinline__ void gemm_nt_tile(const Group& g, const TileCoord& tc
 #pragma unroll
             for (int e = 0; e < 4; ++e) zp[e] = n + e < N ? P.aux[mm * P.ldaux + n + e] : 0.0f;
           }
-          if (P.elu_from_output) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * (zp[e] + 1.0f);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * expf(zp[e]);
-          }
+          act_grad4(P.act, P.elu_from_output, x, zp, o);
         } else {
           o = x;
         }
@@ -750,19 +835,10 @@ __device__ __forceinline__ void nt_pipe_epilogue(const Problem& P, const f32x16 
         f32x4 o, o2;
         if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[e] = x[e] + bias[j][e];
-            o2[e] = elu_fwd(o[e]);
-          }
+          for (int e = 0; e < 4; ++e) o[e] = x[e] + bias[j][e];
+          if constexpr (EPI == EPI_BIAS_ELU) act_fwd4(P.act, o, o2);
         } else if constexpr (EPI == EPI_ELU_GRAD) {
-          const f32x4 zp = zsrc[i][j][rr];
-          if (P.elu_from_output) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * (zp[e] + 1.0f);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = zp[e] > 0.0f ? x[e] : x[e] * expf(zp[e]);
-          }
+          act_grad4(P.act, P.elu_from_output, x, zsrc[i][j][rr], o);
         } else {
           o = x;
         }

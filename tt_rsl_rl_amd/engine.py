@@ -66,13 +66,22 @@ class ModelBuffers:
     def __init__(self, model, rows: int, device) -> None:
         lin = model.linears
         self.widths = [l.out_features for l in lin]
+        self.act = model.act_code
+        # the input-grad takes act' from h = act(z) where the activation allows it (ELU and the other monotone ones);
+        # the others (softplus, gelu, swish, mish) keep z as well
+        self.from_output = self.act in L.ACT_FROM_OUTPUT
 
         def buf(w: int) -> torch.Tensor:
             return torch.empty(rows, -(-w // 4) * 4, device=device)[:, :w]
 
         self.out = buf(self.widths[-1])                 # output layer (no activation): mean / value
-        self.h = [buf(w) for w in self.widths[:-1]]     # hidden layers keep only elu(z); ELU' is taken from it
+        self.h = [buf(w) for w in self.widths[:-1]]     # hidden layers' act(z)
+        self.z = None if self.from_output else [buf(w) for w in self.widths[:-1]]
         self.dz = [buf(w) for w in self.widths]
+
+    def act_src(self, i: int, R: int) -> torch.Tensor:
+        """What the input-grad below hidden layer i reads for act': h (from the output) or z."""
+        return (self.h if self.from_output else self.z)[i][:R]
 
 
 class PhaseTimer:
@@ -189,6 +198,7 @@ class UpdateEngine:
         # the output layers, loss and their input-grad as one launch (ppo_gauss_ppo_head) where it takes the shapes
         la, lc = actor.linears, critic.linears
         self.fused_head = (len(la) >= 2 and len(la) == len(lc) and
+                           actor.act_code == critic.act_code == L.PPO_ACT_ELU and  # (its ELU' of the last hidden layer)
                            ops.head_supported(self.A, la[-1].in_features, lc[-1].in_features) and
                            os.environ.get("PPO_HIP_FUSED_HEAD", "1") != "0")
         if self.fused_head:
@@ -404,10 +414,18 @@ class UpdateEngine:
         for i in range(nl - 1 if self.fused_head else nl):
             last = i == nl - 1
             wa, wc = w0 if i == 0 and w0 is not None else (la[i].weight, lc[i].weight)
-            probs = [(ins_a[-1], wa, la[i].bias, ba.out[:R] if last else None, None if last else ba.h[i][:R]),
-                     (ins_c[-1], wc, lc[i].bias, bc.out[:R] if last else None, None if last else bc.h[i][:R])]
+            probs = []
+            for b, x, w, lin in ((ba, ins_a[-1], wa, la[i]), (bc, ins_c[-1], wc, lc[i])):
+                z = b.out[:R] if last else (b.z[i][:R] if b.z is not None else None)
+                probs.append((x, w, lin.bias, z, None if last else b.h[i][:R]))
             tm.start(f"fwd{i}")
-            ops.linear_fwd(probs, R, elu=not last)
+            if last:
+                ops.linear_fwd(probs, R, act=L.PPO_ACT_NONE)
+            elif ba.act == bc.act:
+                ops.linear_fwd(probs, R, act=ba.act)
+            else:  # (actor and critic with different activations: one launch each)
+                ops.linear_fwd(probs[:1], R, act=ba.act)
+                ops.linear_fwd(probs[1:], R, act=bc.act)
             tm.stop(f"fwd{i}")
             if not last:
                 ins_a.append(ba.h[i][:R])
@@ -473,22 +491,28 @@ class UpdateEngine:
                               alg.desired_kl if alg.desired_kl is not None else 0.0, self.trace)
         tm.stop("loss")
 
-    def dx_layers(self, R: int) -> list[tuple[int, list[tuple], bool]]:
-        """The head's input-gradients, top layer first: (layer, grouped actor / critic problems, ELU' taken from the
-        layer below's output).  Layer 0 has none (no gradient into the observations)."""
+    def dx_layers(self, R: int) -> list[tuple[int, list[tuple], bool, int]]:
+        """The head's input-gradients, top layer first: (layer, grouped actor / critic problems, act' taken from the
+        layer below's output, the activation).  Layer 0 has none (no gradient into the observations)."""
         la, lc = self._layers()
         ba, bc = self.buf_a, self.buf_c
         top = len(la) - 2 if self.fused_head else len(la) - 1  # the fused head produced the output layer's
-        return [(i, [(ba.dz[i][:R], la[i].weight, ba.h[i - 1][:R], ba.dz[i - 1][:R]),
-                     (bc.dz[i][:R], lc[i].weight, bc.h[i - 1][:R], bc.dz[i - 1][:R])], True)
-                for i in range(top, 0, -1)]
+        out = []
+        for i in range(top, 0, -1):
+            pa = (ba.dz[i][:R], la[i].weight, ba.act_src(i - 1, R), ba.dz[i - 1][:R])
+            pc = (bc.dz[i][:R], lc[i].weight, bc.act_src(i - 1, R), bc.dz[i - 1][:R])
+            if (ba.act, ba.from_output) == (bc.act, bc.from_output):
+                out.append((i, [pa, pc], ba.from_output, ba.act))
+            else:
+                out += [(i, [pa], ba.from_output, ba.act), (i, [pc], bc.from_output, bc.act)]
+        return out
 
     def head_backward(self, R: int) -> None:
         """Input gradients down the chain (actor and critic grouped)."""
         tm = self.timer
-        for i, probs, from_output in self.dx_layers(R):
+        for i, probs, from_output, act in self.dx_layers(R):
             tm.start(f"dx{i}")
-            ops.linear_bwd_dx(probs, R, self.dx_ws, elu_from_output=from_output)
+            ops.linear_bwd_dx(probs, R, self.dx_ws, elu_from_output=from_output, act=act)
             tm.stop(f"dx{i}")
 
     def head_dw(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> list[tuple]:
@@ -702,7 +726,8 @@ class RecurrentUpdateEngine(UpdateEngine):
         the LSTM outputs' gradient dh."""
         la, lc = self._layers()
         return super().dx_layers(R) + [(0, [(self.buf_a.dz[0][:R], la[0].weight, None, self.seq_a.dh[:R]),
-                                            (self.buf_c.dz[0][:R], lc[0].weight, None, self.seq_c.dh[:R])], False)]
+                                            (self.buf_c.dz[0][:R], lc[0].weight, None, self.seq_c.dh[:R])], False,
+                                        L.PPO_ACT_ELU)]
 
     @property
     def can_fail(self) -> bool:

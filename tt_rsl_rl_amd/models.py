@@ -263,9 +263,8 @@ class MLPModel(nn.Module):
         else:
             self.distribution = None
             mlp_out = output_dim
-        if activation.lower() != "elu":
-            raise NotImplementedError(f"activation '{activation}': the HIP MLP kernels implement ELU")
         act = resolve_nn_activation(activation)
+        self.act_code = L.ACTIVATIONS[activation.lower()]  # the hidden layers' activation in the HIP kernels
         dims = [self._get_latent_dim() if d == -1 else d for d in hidden_dims]
         layers: list[nn.Module] = [nn.Linear(self._get_latent_dim(), dims[0]), act]
         for a, b in zip(dims[:-1], dims[1:]):
@@ -318,11 +317,11 @@ class MLPModel(nn.Module):
         bufs = self._fwd.get(rows, widths, latent.device)
         x = latent
         for i, l in enumerate(lin[:-1]):
-            h = bufs[i]  # hidden layers: only elu(z) is needed
-            ops.linear_fwd([(x, l.weight, l.bias, None, h)], rows, elu=True)
+            h = bufs[i]  # hidden layers: only act(z) is needed
+            ops.linear_fwd([(x, l.weight, l.bias, None, h)], rows, act=self.act_code)
             x = h
         out = torch.empty(rows, lin[-1].out_features, device=latent.device)
-        ops.linear_fwd([(x, lin[-1].weight, lin[-1].bias, out, None)], rows, elu=False)
+        ops.linear_fwd([(x, lin[-1].weight, lin[-1].bias, out, None)], rows, act=L.PPO_ACT_NONE)
         return out
 
     def get_latent(self, obs: Mapping, masks=None, hidden_state=None) -> torch.Tensor:

@@ -301,9 +301,12 @@ def _check_weight(w: torch.Tensor, b: torch.Tensor | None) -> tuple[int, int]:
     return out_f, in_f
 
 
-def linear_fwd(problems: list[tuple], rows: int, elu: bool) -> None:
+def linear_fwd(problems: list[tuple], rows: int, elu: bool = False, act: int | None = None) -> None:
     """problems: (x [rows, in], w [out, in], b [out], z [rows, out] or None, h [rows, out] or None).
-    Without ELU z is required; with ELU at least one of z / h."""
+    act: the hidden-layer activation (an L.ACTIVATIONS code; elu=True is L.PPO_ACT_ELU), h = act(z); without one z is
+    required, with one at least one of z / h."""
+    act = (L.PPO_ACT_ELU if elu else L.PPO_ACT_NONE) if act is None else int(act)
+    elu = act != L.PPO_ACT_NONE
     items = []
     for x, w, b, z, h in problems:
         _dev(x, w, b, z, h)
@@ -324,8 +327,7 @@ def linear_fwd(problems: list[tuple], rows: int, elu: bool) -> None:
                 raise ValueError("linear_fwd: h too small")
         items.append(L.LinearFwdProblem(x.data_ptr(), ldx, w.data_ptr(), b.data_ptr(), _ptr(z), ldz,
                                         _ptr(h) if elu else None, ldh, in_f, out_f))
-    L.call("ppo_linear_fwd", L.array(L.LinearFwdProblem, items), len(items), rows,
-           L.PPO_ACT_ELU if elu else L.PPO_ACT_NONE, _stream())
+    L.call("ppo_linear_fwd", L.array(L.LinearFwdProblem, items), len(items), rows, act, _stream())
 
 
 def _dx_problems(problems: list[tuple], rows: int):
@@ -348,14 +350,14 @@ def _dx_problems(problems: list[tuple], rows: int):
     return arr, len(items), nbytes
 
 
-def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None, elu_from_output: bool = False
-                  ) -> None:
-    """problems: (dz [rows, out], w [out, in], act [rows, in] or None, dz_prev [rows, in]); act is the ELU input z
-    of the layer below, or its output h = elu(z) with elu_from_output."""
+def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None, elu_from_output: bool = False,
+                  act: int = L.PPO_ACT_ELU) -> None:
+    """problems: (dz [rows, out], w [out, in], src [rows, in] or None, dz_prev [rows, in]); src is the activation's
+    input z of the layer below, or its output h = act(z) with elu_from_output (monotone activations only)."""
     arr, count, nbytes = _dx_problems(problems, rows)
     buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
     src = L.PPO_ELU_FROM_OUTPUT if elu_from_output else L.PPO_ELU_FROM_INPUT
-    L.call("ppo_linear_bwd_dx", arr, count, rows, src, buf.data_ptr(), buf.numel(), _stream())
+    L.call("ppo_linear_bwd_dx_act", arr, count, rows, int(act), src, buf.data_ptr(), buf.numel(), _stream())
 
 
 @dataclass
