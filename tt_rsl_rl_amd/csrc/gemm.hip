@@ -274,9 +274,9 @@ int launch_nt_pipe(Group& g, int count, hipStream_t s, const char* name) {
   for (int i = 0; i < count; ++i) {
     const Problem& p = g.p[i];
     if (!w16_ok(p.A, p.lda) || !w16_ok(p.B, p.ldb) || p.K % BK != 0 || p.N % 4 != 0) return PPO_EUNSUPPORTED;
-    if (!fits(p.C, p.M, p.ldc) || (EPI == EPI_BIAS_ELU && !fits(p.C2, p.M, p.ldc2))) return PPO_EUNSUPPORTED;
-    if (EPI == EPI_ELU_GRAD && !w16_ok(p.aux, p.ldaux)) return PPO_EUNSUPPORTED;
-    if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && reinterpret_cast<uintptr_t>(p.vec) % 16 != 0)
+    if (!fits(p.C, p.M, p.ldc) || (epi_fwd_act(EPI) && !fits(p.C2, p.M, p.ldc2))) return PPO_EUNSUPPORTED;
+    if (epi_act_grad(EPI) && !w16_ok(p.aux, p.ldaux)) return PPO_EUNSUPPORTED;
+    if ((EPI == EPI_BIAS || epi_fwd_act(EPI)) && reinterpret_cast<uintptr_t>(p.vec) % 16 != 0)
       return PPO_EUNSUPPORTED;
   }
   int tiles;
@@ -305,12 +305,13 @@ int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
   for (int i = 0; i < count; ++i) {
     const Problem& p = g.p[i];
     if (!w16_ok(p.A, p.lda) || !w16_ok(p.B, p.ldb) || p.K % 16 != 0 || p.N % 4 != 0) return PPO_EUNSUPPORTED;
-    if (!fits(p.C, p.M, p.ldc) || (EPI == EPI_BIAS_ELU && !fits(p.C2, p.M, p.ldc2))) return PPO_EUNSUPPORTED;
-    if (EPI == EPI_ELU_GRAD && !w16_ok(p.aux, p.ldaux)) return PPO_EUNSUPPORTED;
-    if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && reinterpret_cast<uintptr_t>(p.vec) % 16 != 0)
+    if (!fits(p.C, p.M, p.ldc) || (epi_fwd_act(EPI) && !fits(p.C2, p.M, p.ldc2))) return PPO_EUNSUPPORTED;
+    if (epi_act_grad(EPI) && !w16_ok(p.aux, p.ldaux)) return PPO_EUNSUPPORTED;
+    if ((EPI == EPI_BIAS || epi_fwd_act(EPI)) && reinterpret_cast<uintptr_t>(p.vec) % 16 != 0)
       return PPO_EUNSUPPORTED;
   }
-  int bn = 128, ns = 2, q4 = 1;
+  int bn = 128;
+  [[maybe_unused]] int ns = 2, q4 = 1;
 #ifdef PPO_HIP_TUNING
   if (const char* e = std::getenv("PPO_HIP_BX6")) {  // "bn[:ns[:q4]]"
     bn = std::atoi(e);
@@ -369,7 +370,7 @@ template <int EPI>
 int launch_nt_pipe_tile(int t, Group& g, int count, hipStream_t s, const char* name) {
   switch (t) {
     case 1:  // (its ELU'-source registers would not fit 3 blocks per CU: not for the input-grads)
-      if constexpr (EPI == EPI_ELU_GRAD) {
+      if constexpr (epi_act_grad(EPI)) {
         return PPO_EUNSUPPORTED;
       } else {
         return launch_nt_pipe<128, 128, 16, 3, EPI>(g, count, s, name);
@@ -382,7 +383,7 @@ int launch_nt_pipe_tile(int t, Group& g, int count, hipStream_t s, const char* n
     case 4:
       return launch_nt_pipe<64, 64, 32, 3, EPI>(g, count, s, name);
     case 5:
-      if constexpr (EPI == EPI_ELU_GRAD) {
+      if constexpr (epi_act_grad(EPI)) {
         return PPO_EUNSUPPORTED;
       } else {
         return launch_nt_pipe<128, 128, 32, 2, EPI>(g, count, s, name);
@@ -447,16 +448,17 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
   hipStream_t s = static_cast<hipStream_t>(stream);
   // measured on MI355X for 24576-row mini-batches: outputs wider than 128 like 128x128 tiles with 16-deep slabs,
   // narrower ones 128x64
-  const int brc = elu ? launch_nt_bx6<EPI_BIAS_ELU>(g, count, s, "linear_fwd_act")
-                      : launch_nt_bx6<EPI_BIAS>(g, count, s, "linear_fwd");
-  if (brc != PPO_EUNSUPPORTED) return brc;
-  const int pt = pipe_tile("PPO_HIP_PIPE_FWD", max_n > 128 ? 1 : 2);
-  const int prc = elu ? launch_nt_pipe_tile<EPI_BIAS_ELU>(pt, g, count, s, "linear_fwd_act")
-                      : launch_nt_pipe_tile<EPI_BIAS>(pt, g, count, s, "linear_fwd");
-  if (prc != PPO_EUNSUPPORTED) return prc;
-  const Tile t = pick_tile(max_n > 128 ? T128x128k16s2o3 : T128x64k32s2o4);
-  if (elu) return launch_nt_tile<EPI_BIAS_ELU>(t, g, count, s, "linear_fwd_act");
-  return launch_nt_tile<EPI_BIAS>(t, g, count, s, "linear_fwd");
+  auto run = [&](auto epi_c, const char* name) {
+    constexpr int EPI = decltype(epi_c)::value;
+    const int brc = launch_nt_bx6<EPI>(g, count, s, name);
+    if (brc != PPO_EUNSUPPORTED) return brc;
+    const int prc = launch_nt_pipe_tile<EPI>(pipe_tile("PPO_HIP_PIPE_FWD", max_n > 128 ? 1 : 2), g, count, s, name);
+    if (prc != PPO_EUNSUPPORTED) return prc;
+    return launch_nt_tile<EPI>(pick_tile(max_n > 128 ? T128x128k16s2o3 : T128x64k32s2o4), g, count, s, name);
+  };
+  if (!elu) return run(IntC<EPI_BIAS>{}, "linear_fwd");
+  if (activation == PPO_ACT_ELU) return run(IntC<EPI_BIAS_ELU>{}, "linear_fwd_elu");
+  return run(IntC<EPI_BIAS_ACT>{}, "linear_fwd_act");
 }
 
 extern "C" size_t ppo_linear_bwd_dx_workspace_bytes(const ppo_linear_bwd_dx_problem* problems, int32_t count) {
@@ -549,27 +551,27 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
     p.act = activation;
     max_n = std::max(max_n, q.in_features);
   }
-  // the bf16x6 kernel reads the weights as stored (k-major, 16-byte rows): no transpose
-  const int krc = any_act ? launch_nt_bx6<EPI_ELU_GRAD, true>(g, count, s, "linear_bwd_dx_elu")
-                          : launch_nt_bx6<EPI_STORE, true>(g, count, s, "linear_bwd_dx");
-  if (krc != PPO_EUNSUPPORTED) return krc;
-  // else w^T (k-contiguous) into the workspace for the other kernels
-  if (int rc = launch_transposes(problems, count, ws, offs, s)) return rc;
-  for (int i = 0; i < count; ++i) {
-    g.p[i].B = ws + offs[i];
-    g.p[i].ldb = round4(problems[i].out_features);
-  }
-  const int brc = any_act ? launch_nt_bx6<EPI_ELU_GRAD>(g, count, s, "linear_bwd_dx_elu")
-                          : launch_nt_bx6<EPI_STORE>(g, count, s, "linear_bwd_dx");
-  if (brc != PPO_EUNSUPPORTED) return brc;
-  // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
-  const int pt = pipe_tile("PPO_HIP_PIPE_DX", max_n > 128 ? 3 : 2);
-  const int prc = any_act ? launch_nt_pipe_tile<EPI_ELU_GRAD>(pt, g, count, s, "linear_bwd_dx_elu")
-                          : launch_nt_pipe_tile<EPI_STORE>(pt, g, count, s, "linear_bwd_dx");
-  if (prc != PPO_EUNSUPPORTED) return prc;
-  const Tile t = pick_tile(max_n > 128 ? T64x64k32s2o4 : T128x64k32s2o4);
-  if (any_act) return launch_nt_tile<EPI_ELU_GRAD>(t, g, count, s, "linear_bwd_dx_elu");
-  return launch_nt_tile<EPI_STORE>(t, g, count, s, "linear_bwd_dx");
+  auto run = [&](auto epi_c, const char* name) {
+    constexpr int EPI = decltype(epi_c)::value;
+    // the bf16x6 kernel reads the weights as stored (k-major, 16-byte rows): no transpose
+    const int krc = launch_nt_bx6<EPI, true>(g, count, s, name);
+    if (krc != PPO_EUNSUPPORTED) return krc;
+    // else w^T (k-contiguous) into the workspace for the other kernels
+    if (int rc = launch_transposes(problems, count, ws, offs, s)) return rc;
+    for (int i = 0; i < count; ++i) {
+      g.p[i].B = ws + offs[i];
+      g.p[i].ldb = round4(problems[i].out_features);
+    }
+    const int brc = launch_nt_bx6<EPI>(g, count, s, name);
+    if (brc != PPO_EUNSUPPORTED) return brc;
+    // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
+    const int prc = launch_nt_pipe_tile<EPI>(pipe_tile("PPO_HIP_PIPE_DX", max_n > 128 ? 3 : 2), g, count, s, name);
+    if (prc != PPO_EUNSUPPORTED) return prc;
+    return launch_nt_tile<EPI>(pick_tile(max_n > 128 ? T64x64k32s2o4 : T128x64k32s2o4), g, count, s, name);
+  };
+  if (!any_act) return run(IntC<EPI_STORE>{}, "linear_bwd_dx");
+  if (activation == PPO_ACT_ELU) return run(IntC<EPI_ELU_GRAD>{}, "linear_bwd_dx_elu");
+  return run(IntC<EPI_ACT_GRAD>{}, "linear_bwd_dx_act");
 }
 
 }  // namespace

@@ -44,7 +44,16 @@ enum Epilogue : int {
   EPI_PARTIAL = 4,
   EPI_LSTM_FWD = 5,  // one LSTM step: gates -> cell / hidden state (lstm.hip)
   EPI_LSTM_BWD = 6,  // one LSTM backward step: hidden-state gradient -> gate gradients (lstm.hip)
+  EPI_BIAS_ACT = 7,  // EPI_BIAS_ELU for the other activations (Problem::act)
+  EPI_ACT_GRAD = 8,  // EPI_ELU_GRAD for the other activations
 };
+// The forward epilogues that add the bias and apply an activation, and the input-grad epilogues that multiply by its
+// derivative: ELU's own (the kernels every workload here runs, unchanged by the others' existence) and the generic
+// ones, which evaluate Problem::act per element.
+constexpr bool epi_fwd_act(int e) { return e == EPI_BIAS_ELU || e == EPI_BIAS_ACT; }
+constexpr bool epi_act_grad(int e) { return e == EPI_ELU_GRAD || e == EPI_ACT_GRAD; }
+constexpr bool epi_generic(int e) { return e == EPI_BIAS_ACT || e == EPI_ACT_GRAD; }
+
 
 // Per-step operands of the LSTM epilogues.  Rows are envs; gate-interleaved columns (4u + q = gate q of unit u).
 struct LstmArgs {
@@ -122,7 +131,8 @@ constexpr float kSeluAS = kSeluAlpha * kSeluScale;
 
 __device__ __forceinline__ float sigmoid_ref(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-__device__ __forceinline__ float act_fwd(int act, float x) {
+// (called, not inlined: one copy of every activation's code instead of one per output element)
+__device__ __attribute__((noinline)) float act_fwd(int act, float x) {
   switch (act) {
     case PPO_ACT_SELU: return x > 0.0f ? x * kSeluScale : (expf(x) - 1.0f) * kSeluAS;
     case PPO_ACT_RELU: return x > 0.0f ? x : 0.0f;
@@ -139,7 +149,7 @@ __device__ __forceinline__ float act_fwd(int act, float x) {
 }
 
 // act'(.) of `src`: the output h when from_output (monotone activations only: the host checks), else the input z.
-__device__ __forceinline__ float act_grad(int act, float src, bool from_output) {
+__device__ __attribute__((noinline)) float act_grad(int act, float src, bool from_output) {
   switch (act) {
     case PPO_ACT_SELU:
       return src > 0.0f ? kSeluScale : (from_output ? src + kSeluAS : kSeluAS * expf(src));
@@ -176,20 +186,28 @@ __device__ __forceinline__ float act_grad(int act, float src, bool from_output) 
   }
 }
 
-// Four outputs of an epilogue: o2 = act(o); ELU (the default of every workload here) on its own path.
+template <bool V>
+struct BoolC {
+  static constexpr bool value = V;
+};
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
+// Four outputs of an epilogue: o2 = act(o).  GEN = false: ELU (every workload here); GEN = true: any activation,
+// chosen per element by `act` (a call: with every activation's code inlined per group of four outputs, the forward
+// kernels grew 7x and ran 10x slower, measured).
+template <bool GEN>
 __device__ __forceinline__ void act_fwd4(int act, const f32x4& o, f32x4& o2) {
-  if (act == PPO_ACT_ELU) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o2[e] = elu_fwd(o[e]);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o2[e] = act_fwd(act, o[e]);
-  }
+  for (int e = 0; e < 4; ++e) o2[e] = GEN ? act_fwd(act, o[e]) : elu_fwd(o[e]);
 }
 
 // o = x * act'(src); ELU's exactly as before the other activations existed (x itself where act' = 1).
+template <bool GEN>
 __device__ __forceinline__ void act_grad4(int act, int from_output, const f32x4& x, const f32x4& src, f32x4& o) {
-  if (act == PPO_ACT_ELU) {
+  if constexpr (!GEN) {
     if (from_output) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = src[e] > 0.0f ? x[e] : x[e] * (src[e] + 1.0f);
@@ -202,6 +220,7 @@ __device__ __forceinline__ void act_grad4(int act, int from_output, const f32x4&
     for (int e = 0; e < 4; ++e) o[e] = x[e] * act_grad(act, src[e], from_output != 0);
   }
 }
+
 
 struct Group {
   Problem p[PPO_MAX_LINEAR_PROBLEMS];
@@ -647,6 +666,7 @@ __device__ __forceinline__ void gemm_nt_tile(const Group& g, const TileCoord& tc
   float* patch = lds + wave * 32 * PS;
   const int h = lane >> 5;
   const int pr = lane >> 3, pc = 4 * (lane & 7);  // read-back: row pr (+8 per step), columns pc .. pc + 3
+  constexpr bool GEN = epi_generic(EPI);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -660,7 +680,7 @@ __device__ __forceinline__ void gemm_nt_tile(const Group& g, const TileCoord& tc
       const bool n_in = n < N;
       const bool full = P.c_vec && n + 3 < N;
       f32x4 bias = {0.0f, 0.0f, 0.0f, 0.0f};
-      if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && n_in) {
+      if ((EPI == EPI_BIAS || epi_fwd_act(EPI)) && n_in) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) bias[e] = n + e < N ? P.vec[n + e] : 0.0f;
       }
@@ -680,11 +700,11 @@ __device__ __forceinline__ void gemm_nt_tile(const Group& g, const TileCoord& tc
           continue;
         }
         f32x4 o, o2;
-        if (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) {
+        if (EPI == EPI_BIAS || epi_fwd_act(EPI)) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = x[e] + bias[e];
-          if (EPI == EPI_BIAS_ELU) act_fwd4(P.act, o, o2);
-        } else if (EPI == EPI_ELU_GRAD) {
+          if (epi_fwd_act(EPI)) act_fwd4<GEN>(P.act, o, o2);
+        } else if (epi_act_grad(EPI)) {
           f32x4 zp;
           if (full) {
             zp = *reinterpret_cast<const f32x4*>(P.aux + mm * P.ldaux + n);
@@ -692,13 +712,13 @@ __device__ __forceinline__ void gemm_nt_tile(const Group& g, const TileCoord& tc
 #pragma unroll
             for (int e = 0; e < 4; ++e) zp[e] = n + e < N ? P.aux[mm * P.ldaux + n + e] : 0.0f;
           }
-          act_grad4(P.act, P.elu_from_output, x, zp, o);
+          act_grad4<GEN>(P.act, P.elu_from_output, x, zp, o);
         } else {
           o = x;
         }
         // with ELU either output may be absent (h alone feeds the next layer and the input-grad)
-        const bool st_c = EPI != EPI_BIAS_ELU || P.C != nullptr;
-        const bool st_c2 = EPI == EPI_BIAS_ELU && P.C2 != nullptr;
+        const bool st_c = !epi_fwd_act(EPI) || P.C != nullptr;
+        const bool st_c2 = epi_fwd_act(EPI) && P.C2 != nullptr;
         if (full) {
           if (st_c) *reinterpret_cast<f32x4*>(P.C + mm * P.ldc + n) = o;
           if (st_c2) *reinterpret_cast<f32x4*>(P.C2 + mm * P.ldc2 + n) = o2;
@@ -783,15 +803,15 @@ __device__ __forceinline__ void store_b128(__amdgpu_buffer_rsrc_t r, uint32_t of
 
 // The epilogue of one wave's (TM x TN) 32 x 32 accumulator tiles (layout as in gemm_nt_tile): each tile through the
 // wave's own LDS patch, finished in row order, TM * TN * 4 * OUTS buffer stores in every lane.
-template <int TM, int TN, int EPI>
-__device__ __forceinline__ void nt_pipe_epilogue(const Problem& P, const f32x16 (&acc)[TM][TN], int row0w, int col0w,
-                                                 float* patch, int lane) {
+template <int TM, int TN, int EPI, bool GEN>
+__device__ __forceinline__ void nt_pipe_epilogue_t(const Problem& P, const f32x16 (&acc)[TM][TN], int row0w,
+                                                   int col0w, float* patch, int lane) {
   constexpr int PS = 36;
   const int h = lane >> 5;
   const int pr = lane >> 3, pc = 4 * (lane & 7);
   const int M = P.M, N = P.N;
-  const __amdgpu_buffer_rsrc_t rc = out_buffer(EPI == EPI_BIAS_ELU && P.C == nullptr ? nullptr : P.C, M, P.ldc);
-  const __amdgpu_buffer_rsrc_t rc2 = out_buffer(EPI == EPI_BIAS_ELU ? P.C2 : nullptr, M, P.ldc2);
+  const __amdgpu_buffer_rsrc_t rc = out_buffer(epi_fwd_act(EPI) && P.C == nullptr ? nullptr : P.C, M, P.ldc);
+  const __amdgpu_buffer_rsrc_t rc2 = out_buffer(epi_fwd_act(EPI) ? P.C2 : nullptr, M, P.ldc2);
   // every load of the epilogue before its first store: a wait for a load issued after a store would wait for the
   // store as well (in-order retirement)
   f32x4 bias[TN];
@@ -799,10 +819,10 @@ __device__ __forceinline__ void nt_pipe_epilogue(const Problem& P, const f32x16 
   for (int j = 0; j < TN; ++j) {
     bias[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int n = col0w + j * 32 + pc;
-    if ((EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) && n < N) bias[j] = *reinterpret_cast<const f32x4*>(P.vec + n);
+    if ((EPI == EPI_BIAS || epi_fwd_act(EPI)) && n < N) bias[j] = *reinterpret_cast<const f32x4*>(P.vec + n);
   }
-  f32x4 zsrc[EPI == EPI_ELU_GRAD ? TM : 1][EPI == EPI_ELU_GRAD ? TN : 1][4];
-  if constexpr (EPI == EPI_ELU_GRAD) {
+  f32x4 zsrc[epi_act_grad(EPI) ? TM : 1][epi_act_grad(EPI) ? TN : 1][4];
+  if constexpr (epi_act_grad(EPI)) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -833,27 +853,33 @@ __device__ __forceinline__ void nt_pipe_epilogue(const Problem& P, const f32x16 
         const bool ok = m < M && n_in;
         const int64_t mm = ok ? m : 0;
         f32x4 o, o2;
-        if constexpr (EPI == EPI_BIAS || EPI == EPI_BIAS_ELU) {
+        if constexpr (EPI == EPI_BIAS || epi_fwd_act(EPI)) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = x[e] + bias[j][e];
-          if constexpr (EPI == EPI_BIAS_ELU) act_fwd4(P.act, o, o2);
-        } else if constexpr (EPI == EPI_ELU_GRAD) {
-          act_grad4(P.act, P.elu_from_output, x, zsrc[i][j][rr], o);
+          if constexpr (epi_fwd_act(EPI)) act_fwd4<GEN>(P.act, o, o2);
+        } else if constexpr (epi_act_grad(EPI)) {
+          act_grad4<GEN>(P.act, P.elu_from_output, x, zsrc[i][j][rr], o);
         } else {
           o = x;
         }
         store_b128(rc, ok ? static_cast<uint32_t>((mm * P.ldc + n) * 4) : kDropOffset, o);
-        if constexpr (EPI == EPI_BIAS_ELU)
+        if constexpr (epi_fwd_act(EPI))
           store_b128(rc2, ok ? static_cast<uint32_t>((mm * P.ldc2 + n) * 4) : kDropOffset, o2);
       }
     }
   }
 }
 
+template <int TM, int TN, int EPI>
+__device__ __forceinline__ void nt_pipe_epilogue(const Problem& P, const f32x16 (&acc)[TM][TN], int row0w, int col0w,
+                                                 float* patch, int lane) {
+  nt_pipe_epilogue_t<TM, TN, EPI, epi_generic(EPI)>(P, acc, row0w, col0w, patch, lane);
+}
+
 template <int BM, int BN, int BK, int OCC, int EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_pipe_kernel(
     const Group g, int tiles) {
-  static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_ELU || EPI == EPI_ELU_GRAD || EPI == EPI_STORE,
+  static_assert(EPI == EPI_BIAS || epi_fwd_act(EPI) || epi_act_grad(EPI) || EPI == EPI_STORE,
                 "persistent NT: forward / input-grad epilogues");
   constexpr int S = 2;
   constexpr int WM = BM / 2, WN = BN / 2;
@@ -861,7 +887,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
   constexpr int STAGE = (BM + BN) * BK;
   constexpr int G = BK / 8;
   constexpr int PS = 36;
-  constexpr int NSTORE = TM * TN * 4 * (EPI == EPI_BIAS_ELU ? 2 : 1);
+  constexpr int NSTORE = TM * TN * 4 * (epi_fwd_act(EPI) ? 2 : 1);
   static_assert(TM >= 1 && TN >= 1 && NSTORE < 63, "tile");
   __shared__ __align__(16) float lds[S * STAGE + 4 * 32 * PS];
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -1346,14 +1372,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 // split into the free one of two stages runs between the MFMA groups of the slab before it, so each wave's VALU
 // work overlaps its own MFMAs.  The fp64 bias sums come from the staged A values.
 // ------------------------------------------------------------------------------------------------------------------
-template <bool V>
-struct BoolC {
-  static constexpr bool value = V;
-};
-template <int V>
-struct IntC {
-  static constexpr int value = V;
-};
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -1617,7 +1635,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 template <int BN, int OCC, int EPI, int NS, bool Q4, bool BKM = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_bx6_kernel(
     const Group g) {
-  static_assert(EPI == EPI_BIAS || EPI == EPI_BIAS_ELU || EPI == EPI_ELU_GRAD || EPI == EPI_STORE,
+  static_assert(EPI == EPI_BIAS || epi_fwd_act(EPI) || epi_act_grad(EPI) || EPI == EPI_STORE,
                 "bf16x6 NT: forward / input-grad epilogues");
   static_assert(BN == 128 || BN == 64, "tile");
   static_assert(!BKM || (BN == 128 && Q4), "k-major B: 128-wide tiles, four lanes per A row");
