@@ -99,6 +99,50 @@ def test_gather_rows_bit_exact(cuda):
     assert torch.isnan(out[:, 133]).all() and torch.isnan(out[:, 135:]).all(), "gather wrote outside its columns"
 
 
+@pytest.mark.parametrize("vec_width,odd_width", [(4, 0), (96, 99), (200, 1), (256, 130), (512, 190), (1020, 255),
+                                                 (1100, 3)])
+def test_gather_rows_float4_segments(cuda, vec_width, odd_width):
+    """Segments that are whole 16-byte aligned float4 runs (aligned sources with a leading dimension and width that are
+    multiples of 4, destination columns multiples of 4) move as float4 chunks beside segments that are not (a 99- or
+    odd-wide source, a keep column): one 16-byte aligned segment with the normaliser fused, split in two, next to
+    4-byte ones, for every chunk-slot class (1 to 4 slots of 64 chunks per lane, and 1100 floats: the float path);
+    bit-exact against torch on a ragged row count, nothing written outside the columns."""
+    ops = _ops()
+    torch.manual_seed(vec_width + odd_width)
+    src_rows, rows = 5003, 4999
+    half = vec_width // 8 * 4
+    a = torch.randn(src_rows, half + 4, device=cuda)[:, :half] if half else None     # leading dim half + 4
+    b = torch.randn(src_rows, vec_width - half, device=cuda)                           # contiguous, width % 4 == 0
+    mean, std = torch.randn(vec_width - half, device=cuda), torch.rand(vec_width - half, device=cuda) + 0.5
+    odd = torch.randn(src_rows, odd_width, device=cuda) if odd_width else None
+    dones = (torch.rand(src_rows, 1) < 0.5).to(torch.uint8).to(cuda)
+    perm = torch.randperm(src_rows)[:rows].to(cuda)
+    W = -(-(vec_width + odd_width + 16) // 4) * 4
+    dst = torch.full((rows, W), float("nan"), device=cuda)
+    segs, col, checks = [], 0, []
+    if a is not None:
+        segs.append(ops.Segment(a, col))
+        checks.append((col, a[perm]))
+        col += half
+    segs.append(ops.Segment(b, col, mean, std, 1e-2))
+    checks.append((col, (b[perm] - mean) / (std + 1e-2)))
+    col += vec_width - half
+    if odd is not None:
+        col += 1  # (a column that is not a multiple of 4)
+        segs.append(ops.Segment(odd, col))
+        checks.append((col, odd[perm]))
+        col += odd_width
+    segs.append(ops.Segment(dones, col, keep=True))
+    checks.append((col, 1.0 - dones[perm].float()))
+    ops.gather_rows(perm, segs, dst)
+    torch.cuda.synchronize()
+    written = torch.zeros(W, dtype=torch.bool)
+    for c, ref in checks:
+        assert torch.equal(dst[:, c:c + ref.shape[1]], ref), c
+        written[c:c + ref.shape[1]] = True
+    assert torch.isnan(dst[:, ~written.to(cuda)]).all(), "gather wrote outside its columns"
+
+
 @pytest.mark.parametrize("width", [1, 63, 64, 65, 130, 190, 250, 300, 380, 420, 511, 600, 1100])
 def test_gather_rows_every_slot_count(cuda, width):
     """Rows of every width class the launcher distinguishes (1 to 8 slots of 64 floats per lane, and rows wider than

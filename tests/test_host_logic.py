@@ -125,6 +125,16 @@ def test_table_layout_is_aligned_and_disjoint(da, dc, a):
     assert lay.width % 4 == 0 and lay.width >= ends[-1][1]
     rec = TableLayout(da, dc, a, keep=True)
     assert rec.keep >= ends[-1][1] and rec.width % 4 == 0 and rec.width > rec.keep
+    if da == dc:  # one latent block for both models
+        sh = TableLayout(da, dc, a, shared_obs=True)
+        assert sh.xc == sh.xa == 0 and sh.actions == _round4(da) and sh.width == lay.width - _round4(dc)
+    else:
+        with pytest.raises(ValueError):
+            TableLayout(da, dc, a, shared_obs=True)
+
+
+def _round4(n: int) -> int:
+    return (n + 3) // 4 * 4
 
 
 def test_gemm_flop_counts():

@@ -22,11 +22,16 @@ struct GatherArgs {
   ppo_gather_segment seg[PPO_MAX_GATHER_SEGMENTS];
   int32_t prefix[PPO_MAX_GATHER_SEGMENTS + 1];  // first flat column of each segment; prefix[num_segments] = total
   int32_t num_segments;
+  // gather_rows_vec_kernel: segments [0, num_vec) move as float4 chunks (vprefix: first chunk of each, vprefix[num_vec]
+  // = the chunk count), segments [num_vec, num_segments) as floats (prefix, from 0 at segment num_vec)
+  int32_t vprefix[PPO_MAX_GATHER_SEGMENTS + 1];
+  int32_t num_vec;
 };
 
 // Source pointers are global memory; read back from the LDS copy of the segment table they would otherwise be
 // generic (flat) pointers, whose loads also count as LDS operations and defeat the wait counters.
 typedef const uint32_t __attribute__((address_space(1))) global_u32;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGatherThreads = 256;
 constexpr int kWavesPerBlock = kGatherThreads / kWave;
@@ -116,6 +121,128 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_kernel(const int64
 #pragma unroll
         for (int k = 0; k < kSlots; ++k)
           if (sr[r] >= 0 && valid[k]) dst[(j0 + r) * dst_stride + dcol[k]] = v[r][k];
+    }
+  }
+}
+
+// Rows whose segments are mostly whole, 16-byte aligned float4 runs (fp32 source 16-byte aligned with a leading
+// dimension a multiple of 4, width and destination column multiples of 4, in a 16-byte aligned table whose stride is
+// a multiple of 4): lane l owns the float4 chunks l, l + 64, ... of those segments (kV slots, one 16-byte load and
+// store each) and the flat columns l, l + 64, ... of the others (kS slots, 4-byte), every row in one pass.  A wave
+// moves kRowsPerIter rows per iteration with all their loads in flight before the arithmetic and the stores, as in
+// gather_rows_kernel, whose results it reproduces bit for bit (the same (x - mean) / (std + eps) per float).
+template <int kV, int kS, int kRowsPerIter>
+__global__ __launch_bounds__(kGatherThreads) void gather_rows_vec_kernel(const int64_t* __restrict__ perm,
+                                                                         int64_t rows, int64_t src_rows,
+                                                                         GatherArgs args, float* __restrict__ dst,
+                                                                         int64_t dst_stride) {
+  __shared__ ppo_gather_segment seg[PPO_MAX_GATHER_SEGMENTS];
+  if (threadIdx.x < args.num_segments) seg[threadIdx.x] = args.seg[threadIdx.x];
+  __syncthreads();
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+  const int nv = args.num_vec, ns = args.num_segments;
+  const int vtotal = args.vprefix[nv], stotal = args.prefix[ns];
+  // the lane's chunks: source address, row stride (bytes), destination column, normaliser (4 columns each)
+  uintptr_t vsrc[kV];
+  int64_t vstride[kV];
+  int vcol[kV];
+  bool vvalid[kV];
+  f32x4 vmu[kV], vden[kV];
+#pragma unroll
+  for (int k = 0; k < kV; ++k) {
+    const int fc = lane + kWave * k;
+    int s = 0;
+    for (int i = 1; i < nv; ++i) s = fc >= args.vprefix[i] ? i : s;
+    const ppo_gather_segment& g = seg[s];
+    const bool in = fc < vtotal;
+    const int col = in ? 4 * (fc - args.vprefix[s]) : 0;
+    vvalid[k] = in;
+    vsrc[k] = reinterpret_cast<uintptr_t>(in ? g.src : seg[0].src) + col * 4;
+    vstride[k] = in ? g.src_stride * 4 : 0;
+    vcol[k] = g.dst_col + col;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool norm = in && g.norm_mean != nullptr;
+      vmu[k][e] = norm ? g.norm_mean[col + e] : 0.0f;
+      vden[k][e] = norm ? g.norm_std[col + e] + g.norm_eps : 1.0f;
+    }
+  }
+  // the lane's single floats (as gather_rows_kernel's)
+  uintptr_t src[kS > 0 ? kS : 1];
+  int64_t stride[kS > 0 ? kS : 1];
+  int dcol[kS > 0 ? kS : 1];
+  bool valid[kS > 0 ? kS : 1], keep[kS > 0 ? kS : 1];
+  float mu[kS > 0 ? kS : 1], den[kS > 0 ? kS : 1];
+#pragma unroll
+  for (int k = 0; k < kS; ++k) {
+    const int fc = lane + kWave * k;
+    int s = nv;
+    for (int i = nv + 1; i < ns; ++i) s = fc >= args.prefix[i] ? i : s;
+    const bool in = fc < stotal && ns > nv;
+    const ppo_gather_segment& g = seg[in ? s : 0];
+    const int col = in ? fc - args.prefix[s] : 0;
+    const bool u8 = in && g.kind == PPO_GATHER_KEEP_U8;
+    const int esz = u8 ? 1 : 4;
+    src[k] = reinterpret_cast<uintptr_t>(in ? g.src : seg[0].src) + (in ? col * esz : 0);
+    valid[k] = in;
+    keep[k] = u8;
+    stride[k] = in ? g.src_stride * esz : 0;
+    dcol[k] = g.dst_col + col;
+    const bool norm = in && g.norm_mean != nullptr;
+    mu[k] = norm ? g.norm_mean[col] : 0.0f;
+    den[k] = norm ? g.norm_std[col] + g.norm_eps : 1.0f;
+  }
+  typedef const f32x4 __attribute__((address_space(1))) global_f32x4;
+  for (int64_t j0 = wave_id * kRowsPerIter; j0 < rows; j0 += wave_count * kRowsPerIter) {
+    int64_t sr[kRowsPerIter];
+#pragma unroll
+    for (int r = 0; r < kRowsPerIter; ++r) {
+      const int64_t j = j0 + r;
+      const int64_t p = j < rows ? perm[j] : -1;
+      sr[r] = p >= 0 && p < src_rows ? p : -1;  // never read outside the source (the host checks perm)
+    }
+    f32x4 vv[kRowsPerIter][kV];
+    uint32_t word[kRowsPerIter][kS > 0 ? kS : 1];
+    int shift[kRowsPerIter][kS > 0 ? kS : 1];
+#pragma unroll
+    for (int r = 0; r < kRowsPerIter; ++r) {
+      const int64_t row = sr[r] >= 0 ? sr[r] : 0;
+#pragma unroll
+      for (int k = 0; k < kV; ++k) vv[r][k] = *reinterpret_cast<global_f32x4*>(vsrc[k] + row * vstride[k]);
+#pragma unroll
+      for (int k = 0; k < kS; ++k) {
+        const uintptr_t a = src[k] + row * stride[k];
+        word[r][k] = *reinterpret_cast<global_u32*>(a & ~static_cast<uintptr_t>(3));
+        shift[r][k] = static_cast<int>(a & 3) * 8;
+      }
+    }
+    float v[kRowsPerIter][kS > 0 ? kS : 1];
+#pragma unroll
+    for (int r = 0; r < kRowsPerIter; ++r) {
+#pragma unroll
+      for (int k = 0; k < kV; ++k)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vv[r][k][e] = (vv[r][k][e] - vmu[k][e]) / vden[k][e];
+#pragma unroll
+      for (int k = 0; k < kS; ++k) {
+        const float x = keep[k] ? 1.0f - static_cast<float>((word[r][k] >> shift[r][k]) & 0xffu)
+                                : __uint_as_float(word[r][k]);
+        v[r][k] = (x - mu[k]) / den[k];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the arithmetic above the (predicated) stores
+#pragma unroll
+    for (int r = 0; r < kRowsPerIter; ++r) {
+      if (sr[r] < 0) continue;
+      float* const drow = dst + (j0 + r) * dst_stride;
+#pragma unroll
+      for (int k = 0; k < kV; ++k)
+        if (vvalid[k]) *reinterpret_cast<f32x4*>(drow + vcol[k]) = vv[r][k];
+#pragma unroll
+      for (int k = 0; k < kS; ++k)
+        if (valid[k]) drow[dcol[k]] = v[r][k];
     }
   }
 }
@@ -218,6 +345,64 @@ extern "C" int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_ro
     PPO_REQUIRE(total <= INT32_MAX / 2, "ppo_gather_rows: rows of %lld floats are too wide", (long long)total);
   }
   args.prefix[num_segments] = static_cast<int32_t>(total);
+  // float4 chunks for the segments that allow them (16-byte aligned sources of a stride and width that are multiples
+  // of 4, destination columns multiples of 4 in a 16-byte aligned table of such a stride), when each lane's share of
+  // a row fits 4 chunk slots and 4 float slots (one pass)
+  {
+    const bool dst16 = reinterpret_cast<uintptr_t>(dst) % 16 == 0 && dst_stride % 4 == 0;
+    auto vec_ok = [&](const ppo_gather_segment& g) {
+      return dst16 && g.kind == PPO_GATHER_FLOAT && reinterpret_cast<uintptr_t>(g.src) % 16 == 0 &&
+             g.src_stride % 4 == 0 && g.width % 4 == 0 && g.dst_col % 4 == 0;
+    };
+    GatherArgs va{};
+    int n = 0;
+    int64_t chunks = 0, floats = 0;
+    for (int pass = 0; pass < 2; ++pass)
+      for (int s = 0; s < num_segments; ++s) {
+        const ppo_gather_segment& g = segments[s];
+        if (vec_ok(g) != (pass == 0)) continue;
+        va.seg[n] = g;
+        if (pass == 0) {
+          va.vprefix[n] = static_cast<int32_t>(chunks);
+          chunks += g.width / 4;
+        } else {
+          va.prefix[n] = static_cast<int32_t>(floats);
+          floats += g.width;
+        }
+        if (pass == 0) va.num_vec = n + 1;
+        ++n;
+      }
+    va.num_segments = num_segments;
+    va.vprefix[va.num_vec] = static_cast<int32_t>(chunks);
+    va.prefix[num_segments] = static_cast<int32_t>(floats);
+    const int kv = static_cast<int>(ceil_div(chunks, static_cast<int64_t>(kWave)));
+    const int ks = static_cast<int>(ceil_div(floats, static_cast<int64_t>(kWave)));
+    if (va.num_vec > 0 && kv <= 4 && ks <= 4) {
+      auto gov = [&](auto kernel) {
+        constexpr int R = kGatherRowsPerIter;
+        const int64_t blocks = std::min<int64_t>(ceil_div(rows, static_cast<int64_t>(kWavesPerBlock) * R), 65536);
+        hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGatherThreads), 0,
+                           static_cast<hipStream_t>(stream), perm, rows, src_rows, va, dst, dst_stride);
+        return check_launch("gather_rows_vec_kernel");
+      };
+      constexpr int R = kGatherRowsPerIter;
+#define PPO_GATHER_VEC(V)                                         \
+  switch (ks) {                                                   \
+    case 0: return gov(gather_rows_vec_kernel<V, 0, R>);          \
+    case 1: return gov(gather_rows_vec_kernel<V, 1, R>);          \
+    case 2: return gov(gather_rows_vec_kernel<V, 2, R>);          \
+    case 3: return gov(gather_rows_vec_kernel<V, 3, R>);          \
+    default: return gov(gather_rows_vec_kernel<V, 4, R>);         \
+  }
+      switch (kv) {
+        case 1: PPO_GATHER_VEC(1)
+        case 2: PPO_GATHER_VEC(2)
+        case 3: PPO_GATHER_VEC(3)
+        default: PPO_GATHER_VEC(4)
+      }
+#undef PPO_GATHER_VEC
+    }
+  }
   // the fewest slots that cover a row (a slot past the row still issues its load), 8 for wider rows (more passes)
   const int slots = static_cast<int>(std::min<int64_t>(ceil_div(total, static_cast<int64_t>(kWave)), 8));
   auto go = [&](auto kernel, int r) {

@@ -40,12 +40,20 @@ def _pad16(n: int) -> int:
 
 
 class TableLayout:
-    def __init__(self, actor_dim: int, critic_dim: int, num_actions: int, keep: bool = False) -> None:
+    """Column blocks of the packed table.  shared_obs: the critic reads the actor's latent block (the same observation
+    groups and neither model normalises: identical latents), so the gather copies each observation once."""
+
+    def __init__(self, actor_dim: int, critic_dim: int, num_actions: int, keep: bool = False,
+                 shared_obs: bool = False) -> None:
+        if shared_obs and actor_dim != critic_dim:
+            raise ValueError("TableLayout: shared latents need equal widths")
         c = 0
         self.xa = c
         c = _align4(c + actor_dim)
-        self.xc = c
-        c = _align4(c + critic_dim)
+        self.shared_obs = shared_obs
+        self.xc = self.xa if shared_obs else c
+        if not shared_obs:
+            c = _align4(c + critic_dim)
         self.actions = c
         c = _align4(c + num_actions)
         self.old_mean = c
@@ -165,7 +173,9 @@ class UpdateEngine:
         self.R_max = self.max_rows()
         actor, critic = alg.actor, alg.critic
         self.A = actor.distribution.output_dim
-        self.layout = TableLayout(actor.obs_dim, critic.obs_dim, self.A, keep=self.recurrent)
+        shared = (list(actor.obs_groups) == list(critic.obs_groups) and not actor.obs_normalization and
+                  not critic.obs_normalization)
+        self.layout = TableLayout(actor.obs_dim, critic.obs_dim, self.A, keep=self.recurrent, shared_obs=shared)
         self.table = torch.zeros(self.B, self.layout.width, device=self.device)  # padding columns stay zero
         self.scalars = torch.empty(self.B, 4, device=self.device)  # pack_scalars
         # zero-padded copies of first-layer weights whose input width is not a multiple of 16: written by every Adam
@@ -320,7 +330,8 @@ class UpdateEngine:
         """The packed table's column blocks and their storage sources ([T * N, width] views)."""
         alg, st, lay = self.alg, self.alg.storage, self.layout
         segs: list[ops.Segment] = []
-        for model, base in ((alg.actor, lay.xa), (alg.critic, lay.xc)):
+        models = ((alg.actor, lay.xa),) if lay.shared_obs else ((alg.actor, lay.xa), (alg.critic, lay.xc))
+        for model, base in models:
             col = 0
             norm = model.obs_normalizer if model.obs_normalization else None
             for g in model.obs_groups:
@@ -631,10 +642,11 @@ class UpdateEngine:
 
 
 class LstmBuffers:
-    """Sequence buffers of one LSTM for mini-batches of up to ``rows`` = T x envs rows (t-major)."""
+    """Sequence buffers of one LSTM layer for mini-batches of up to ``rows`` = T x envs rows (t-major)."""
 
-    def __init__(self, rnn, rows: int, envs: int, device) -> None:
-        H, D = rnn.hidden_size, rnn.input_size
+    def __init__(self, rnn, layer: int, rows: int, envs: int, device) -> None:
+        H, D = rnn.hidden_size, rnn.layer_input_size(layer)
+        self.layer = layer
         e = lambda *shape: torch.empty(*shape, device=device)
         self.packed = ops.LstmPacked(D, H, device)
         self.gx, self.gates, self.dgates = e(rows, 4 * H), e(rows, 4 * H), e(rows, 4 * H)
