@@ -48,10 +48,10 @@ def dw_arith(engine, R: int) -> str:
     xa = tab[:, lay.xa:lay.xa + alg.actor.obs_dim]
     xc = tab[:, lay.xc:lay.xc + alg.critic.obs_dim]
     if engine.recurrent:
-        sa, sc = engine.seq_a, engine.seq_c
-        ops = [(s.dgates[:R], h) for s, x in ((sa, xa), (sc, xc)) for h in (s.hs[:R], x)]
+        ops = [(b.dgates[:R], h) for row in engine._layer_inputs(xa, xc, R) for _, _, b, x in row
+               for h in (b.hs[:R], x)]
         if engine.lstm_sync is not None:
-            ops += [(dz, x) for dz, x, *_ in engine.head_dw(sa.h[:R], sc.h[:R], R)]
+            ops += [(dz, x) for dz, x, *_ in engine.head_dw(engine.seq_a.h[:R], engine.seq_c.h[:R], R)]
     else:
         ops = [(dz, x) for dz, x, *_ in engine.head_dw(xa, xc, R)]
     aligned = all(t.data_ptr() % 16 == 0 and t.stride(0) % 4 == 0 for pair in ops for t in pair)

@@ -112,9 +112,9 @@ def generate(workload: dict, seed: int = 0, carry_state: bool = False, **alg_ove
                                "critic": copy.deepcopy(alg.critic.state_dict())})
     n = workload["num_envs"]
     if carry_state and "rnn" in workload:
-        H = workload["rnn"]["rnn_hidden_dim"]
+        H, layers = workload["rnn"]["rnn_hidden_dim"], workload["rnn"].get("rnn_num_layers", 1)
         for model in (alg.actor, alg.critic):
-            model.reset(hidden_state=tuple(0.5 * torch.randn(1, n, H) for _ in range(2)))
+            model.reset(hidden_state=tuple(0.5 * torch.randn(layers, n, H) for _ in range(2)))
     with torch.inference_mode():
         obs = sample_obs(workload)
         for _ in range(workload["steps"]):

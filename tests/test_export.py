@@ -19,10 +19,10 @@ GROUPS = {"actor": ["policy", "extra"], "critic": ["policy"]}
 DIST = {"class_name": "GaussianDistribution", "init_std": 1.0, "std_type": "log"}
 
 
-def _pair(recurrent: bool, normalization: bool):
+def _pair(recurrent: bool, normalization: bool, layers: int = 1):
     kw = dict(hidden_dims=[32, 16], activation="elu", obs_normalization=normalization, distribution_cfg=DIST)
     if recurrent:
-        kw.update(rnn_type="lstm", rnn_hidden_dim=24)
+        kw.update(rnn_type="lstm", rnn_hidden_dim=24, rnn_num_layers=layers)
     torch.manual_seed(0)
     ora = (O.RNNModel if recurrent else O.MLPModel)(OBS, GROUPS, "actor", 5, **kw)
     torch.manual_seed(0)
@@ -110,8 +110,9 @@ def _oracle_steps(ora, seq: list[dict], dones: list[torch.Tensor]) -> list[torch
     return outs
 
 
-def test_lstm_jit_and_onnx_exports_step_like_upstream():
-    ora, hip = _pair(True, True)
+@pytest.mark.parametrize("layers", [1, 2])
+def test_lstm_jit_and_onnx_exports_step_like_upstream(layers):
+    ora, hip = _pair(True, True, layers)
     jit = hip.as_jit()
     # upstream's copy: its state buffers, then the normaliser, the torch LSTM (the wrapper's inner nn.LSTM) and the
     # MLP, in that order
@@ -121,7 +122,7 @@ def test_lstm_jit_and_onnx_exports_step_like_upstream():
                 [k for k in sd if k.startswith("mlp.")])
     assert list(jit.state_dict().keys()) == expected
     assert list(hip.as_onnx().state_dict().keys()) == expected[2:]
-    assert jit.hidden_state.shape == jit.cell_state.shape == (1, 1, 24)
+    assert jit.hidden_state.shape == jit.cell_state.shape == (layers, 1, 24)
     scripted = torch.jit.script(jit)
     seq = [_obs(1, 10 + t) for t in range(6)]
     dones = [torch.tensor([1.0 if t == 2 else 0.0]) for t in range(6)]

@@ -21,9 +21,9 @@ from tests.parity import make_hip, rel_err
 pytestmark = pytest.mark.gpu
 
 
-def _workload():
+def _workload(layers: int = 1):
     w = R.scaled(R.WORKLOADS["lstm256"], num_envs=96, steps=6, hidden_dims=[64, 32])
-    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=64)
+    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=64, rnn_num_layers=layers)
     w["obs_normalization"] = True
     return w
 
@@ -77,8 +77,9 @@ def _rollout(alg, env: list[dict], dev, seed: int) -> list[dict]:
     return rec, r_state
 
 
-def test_recurrent_rollout_matches_oracle():
-    w = _workload()
+@pytest.mark.parametrize("layers", [1, 2])
+def test_recurrent_rollout_matches_oracle(layers):
+    w = _workload(layers)
     ora = R.make_oracle(w, seed=0)
     ora.train_mode()
     hip = make_hip(w, seed=0)
@@ -102,12 +103,12 @@ def test_recurrent_rollout_matches_oracle():
                 assert sh is None and so is None
                 continue
             for x, y in zip(sh, so):
-                assert x.shape == y.shape == (1, n, w["rnn"]["rnn_hidden_dim"])
+                assert x.shape == y.shape == (layers, n, w["rnn"]["rnn_hidden_dim"])
                 assert rel_err(x, y) < 1e-5, (step, side)
         dones = env[step + 1]["dones"]
         for x, y in zip(a["carried"], b["carried"]):
             for xs, ys in zip(x, y):
-                assert torch.equal(xs[0][dones == 1], torch.zeros_like(ys[0, dones == 1]))
+                assert torch.equal(xs[:, dones == 1], torch.zeros_like(ys[:, dones == 1]))
                 assert rel_err(xs, ys) < 1e-5, step
     with torch.inference_mode():
         # the stored states: step 0 stays zero (no state yet), later steps the state before that step

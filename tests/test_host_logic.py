@@ -22,11 +22,13 @@ def test_workload_table_matches_the_oracle_copy():
     assert W.ALGORITHM == R.DEFAULT_ALGORITHM
 
 
-@pytest.mark.parametrize("name", ["flat48", "humanoid", "rough235", "lstm256"])
+@pytest.mark.parametrize("name", ["flat48", "humanoid", "rough235", "lstm256", "lstm256x3"])
 def test_initial_weights_and_state_dict_layout_equal_upstream(name):
-    """Same seed -> same default nn.Linear (and nn.LSTM) init as upstream (actor then critic), same keys, same
-    parameter order."""
-    w = R.scaled(R.WORKLOADS[name], num_envs=8)
+    """Same seed -> same default nn.Linear (and nn.LSTM, of one or several layers) init as upstream (actor then
+    critic), same keys, same parameter order."""
+    w = R.scaled(R.WORKLOADS[name.split("x")[0]], num_envs=8)
+    if "x" in name:
+        w["rnn"] = dict(w["rnn"], rnn_num_layers=int(name.split("x")[1]))
     ora = R.make_oracle(w, seed=3)
     torch.manual_seed(3)
     cfg = W.train_cfg(w)
@@ -82,8 +84,8 @@ def test_recurrent_options_outside_the_kernels_are_rejected():
     obs, groups = R.zero_obs(w), w["obs_groups"]
     with pytest.raises(NotImplementedError, match="LSTM"):
         RNNModel(obs, groups, "actor", 12, rnn_type="gru")
-    with pytest.raises(NotImplementedError, match="one layer"):
-        RNNModel(obs, groups, "actor", 12, rnn_num_layers=2)
+    with pytest.raises(ValueError, match="rnn_num_layers"):
+        RNNModel(obs, groups, "actor", 12, rnn_num_layers=0)
     with pytest.raises(NotImplementedError, match="multiple of 4"):
         RNNModel(obs, groups, "actor", 12, rnn_hidden_dim=30)
     # a recurrent actor with a feed-forward critic

@@ -95,16 +95,19 @@ def _masked_lstm_fp64(x, h0, c0, dones, w_ih, w_hh, b_ih, b_hh):
     return torch.stack(outs)
 
 
-@pytest.mark.parametrize("num_envs,num_steps,num_batches", [(6, 5, 2), (9, 7, 3)])
-def test_padded_trajectories_equal_the_masked_per_env_sequence(num_envs, num_steps, num_batches):
+@pytest.mark.parametrize("num_envs,num_steps,num_batches,layers", [(6, 5, 2, 1), (9, 7, 3, 1), (9, 7, 3, 2),
+                                                                   (5, 6, 1, 3)])
+def test_padded_trajectories_equal_the_masked_per_env_sequence(num_envs, num_steps, num_batches, layers):
     """The oracle's upstream-style evaluation (split at dones, pad, LSTM from each trajectory's saved start state,
-    unpad) equals one sequence per env from the state saved at step 0 with the state zeroed after every done."""
+    unpad) equals one sequence per env from the state saved at step 0 with the state zeroed after every done; with
+    stacked layers, layer by layer, each from its own saved state and on the h sequence of the layer below."""
     torch.manual_seed(3)
     D, H = 4, 5
-    rnn = O.RNN(D, hidden_dim=H, num_layers=1, type="lstm").double()
+    rnn = O.RNN(D, hidden_dim=H, num_layers=layers, type="lstm").double()
     obs = {"policy": torch.zeros(num_envs, D)}
     st = O.RolloutStorage(num_envs, num_steps, obs, [1])
-    state = (torch.randn(1, num_envs, H), torch.randn(1, num_envs, H))  # a state carried in from a previous rollout
+    # a state carried in from a previous rollout
+    state = (torch.randn(layers, num_envs, H), torch.randn(layers, num_envs, H))
     for step in range(num_steps):
         t = O.Transition()
         t.observations = {"policy": torch.randn(num_envs, D)}
@@ -123,11 +126,12 @@ def test_padded_trajectories_equal_the_masked_per_env_sequence(num_envs, num_ste
         lo, hi = i * num_envs // num_batches, (i + 1) * num_envs // num_batches
         hs = tuple(s.double() for s in b.hidden_states[0])
         got = rnn(b.observations["policy"].double(), b.masks, hs)
-        x = st.observations["policy"][:, lo:hi]
-        h0 = st.saved_hidden_state_a[0][0, 0, lo:hi]
-        c0 = st.saved_hidden_state_a[1][0, 0, lo:hi]
-        want = _masked_lstm_fp64(x, h0, c0, st.dones[:, lo:hi, 0], w.weight_ih_l0, w.weight_hh_l0, w.bias_ih_l0,
-                                 w.bias_hh_l0)
+        want = st.observations["policy"][:, lo:hi]
+        for k in range(layers):
+            h0 = st.saved_hidden_state_a[0][0, k, lo:hi]
+            c0 = st.saved_hidden_state_a[1][0, k, lo:hi]
+            want = _masked_lstm_fp64(want, h0, c0, st.dones[:, lo:hi, 0], *(getattr(w, f"{n}_l{k}") for n in
+                                     ("weight_ih", "weight_hh", "bias_ih", "bias_hh")))
         assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
 
 

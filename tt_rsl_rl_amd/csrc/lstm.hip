@@ -1,4 +1,5 @@
-// A15 LSTM of the recurrent models (torch nn.LSTM, one layer; rsl_rl/modules/rnn.py:22-86) on gfx950.
+// A15 LSTM of the recurrent models (torch nn.LSTM; rsl_rl/modules/rnn.py:22-86) on gfx950.  Every entry point
+// works on one layer; stacked layers are run one after another by the caller (layer k's input = layer k-1's h).
 //
 // The input projection x w_ih^T + b of all T steps is one GEMM (ppo_linear_fwd on the gate-interleaved weights).
 // The recurrence is one kernel per step: the NT GEMM of gemm_core.hpp computes hs[t] w_hh_g^T (rows = envs,

@@ -683,8 +683,12 @@ class RecurrentUpdateEngine(UpdateEngine):
         # the heads' weight-grads run on a second stream (default priority) beside the LSTM backward steps
         self.side = torch.cuda.Stream(device=self.device)
         self.side_dw_ws = ops.Workspace(self.device)
-        self.seq_a = LstmBuffers(actor.rnn, self.R_max, self.E_max, self.device)
-        self.seq_c = LstmBuffers(critic.rnn, self.R_max, self.E_max, self.device)
+        # per layer, bottom first; seq_a / seq_c: the top layers, whose outputs feed the heads
+        self.lay_a = [LstmBuffers(actor.rnn, k, self.R_max, self.E_max, self.device)
+                      for k in range(actor.rnn.num_layers)]
+        self.lay_c = [LstmBuffers(critic.rnn, k, self.R_max, self.E_max, self.device)
+                      for k in range(critic.rnn.num_layers)]
+        self.seq_a, self.seq_c = self.lay_a[-1], self.lay_c[-1]
         # synchronisation words of the one-launch sequences (word 0: sticky status, read back with every update);
         # PPO_HIP_LSTM_SEQ=0 selects one launch per step (same results)
         self.lstm_sync = None
@@ -720,15 +724,16 @@ class RecurrentUpdateEngine(UpdateEngine):
         return super().segments() + [ops.Segment(self.alg.storage.dones.reshape(-1, 1), self.layout.keep,
                                                  keep=True)]
 
-    def _initial_state(self, model, side: str, e0: int, e1: int, buf: LstmBuffers):
+    def _initial_state(self, side: str, e0: int, e1: int, buf: LstmBuffers):
         saved = getattr(self.alg.storage, f"saved_hidden_state_{side}")
         if saved is None:  # no state was recorded (a first rollout of one step): nn.LSTM's zero default
             return buf.zero[:e1 - e0], buf.zero[:e1 - e0]
-        return saved[0][0, 0, e0:e1], saved[1][0, 0, e0:e1]
+        # [T, layers, N, H]: the state of this layer before step 0
+        return saved[0][0, buf.layer, e0:e1], saved[1][0, buf.layer, e0:e1]
 
-    def _seq(self, model, side: str, buf: LstmBuffers, x: torch.Tensor, e0: int, e1: int, tab: torch.Tensor) -> dict:
+    def _seq(self, model, side: str, buf: LstmBuffers, e0: int, e1: int, tab: torch.Tensor) -> dict:
         R = self.T * (e1 - e0)
-        h0, c0 = self._initial_state(model, side, e0, e1, buf)
+        h0, c0 = self._initial_state(side, e0, e1, buf)
         return dict(packed=buf.packed, hidden=model.rnn.hidden_size, gx=buf.gx[:R], h0=h0, c0=c0,
                     keep=tab[:, self.layout.keep], h=buf.h[:R], hs=buf.hs[:R + e1 - e0], c=buf.c[:R],
                     gates=buf.gates[:R], dh=buf.dh[:R], dgates=buf.dgates[:R], dc=buf.dc[:e1 - e0])
@@ -759,12 +764,26 @@ class RecurrentUpdateEngine(UpdateEngine):
         if self.lstm_sync is not None:
             self.lstm_sync.zero_()
 
-    def _grouped(self, fn, qa: dict, qc: dict, E: int) -> None:
-        if qa["hidden"] == qc["hidden"]:
-            fn([qa, qc], self.T, E, self.lstm_sync)
+    def _grouped(self, fn, qs: list[dict], E: int) -> None:
+        """One launch for the actor's and the critic's sequences of one layer when their hidden sizes agree."""
+        if len(qs) == 2 and qs[0]["hidden"] == qs[1]["hidden"]:
+            fn(qs, self.T, E, self.lstm_sync)
         else:
-            fn([qa], self.T, E, self.lstm_sync)
-            fn([qc], self.T, E, self.lstm_sync)
+            for q in qs:
+                fn([q], self.T, E, self.lstm_sync)
+
+    def _layer_inputs(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> list[list[tuple]]:
+        """Per layer k (bottom first): (model, side, buffers, the layer's input rows) of each model that has layer k;
+        layer 0 reads the observations, layer k > 0 the h of layer k - 1."""
+        alg = self.alg
+        out = []
+        for k in range(max(len(self.lay_a), len(self.lay_c))):
+            row = []
+            for model, side, lays, x in ((alg.actor, "a", self.lay_a, xa), (alg.critic, "c", self.lay_c, xc)):
+                if k < len(lays):
+                    row.append((model, side, lays[k], x if k == 0 else lays[k - 1].h[:R]))
+            out.append(row)
+        return out
 
     def minibatch(self, r0: int, r1: int, step: int) -> None:
         alg, lay, tm = self.alg, self.layout, self.timer
@@ -778,14 +797,19 @@ class RecurrentUpdateEngine(UpdateEngine):
         sa, sc = self.seq_a, self.seq_c
         adv_col = self.advantage_column(tab, R)
 
-        # LSTM forward: packed weights, input projection for all T x E rows at once, then the T recurrent steps
+        # LSTM forward, layer after layer: packed weights, input projection for all T x E rows at once, then the T
+        # recurrent steps
         tm.start("lstm_fwd")
-        ops.lstm_pack([(*actor.rnn.weights, sa.packed), (*critic.rnn.weights, sc.packed)])
-        ops.linear_fwd([(xa, sa.packed.w_ih_g, sa.packed.b_g, sa.gx[:R], None),
-                        (xc, sc.packed.w_ih_g, sc.packed.b_g, sc.gx[:R], None)], R, elu=False)
-        qa = self._seq(actor, "a", sa, xa, e0, e0 + E, tab)
-        qc = self._seq(critic, "c", sc, xc, e0, e0 + E, tab)
-        self._grouped(ops.lstm_seq_fwd, qa, qc, E)
+        ops.lstm_pack([(*m.rnn.layer_weights(b.layer), b.packed)
+                       for m, lays in ((actor, self.lay_a), (critic, self.lay_c)) for b in lays])
+        layers = self._layer_inputs(xa, xc, R)
+        seqs = []
+        for row in layers:
+            ops.linear_fwd([(x, b.packed.w_ih_g, b.packed.b_g, b.gx[:R], None) for _, _, b, x in row], R,
+                           act=L.PPO_ACT_NONE)
+            qs = [self._seq(m, side, b, e0, e0 + E, tab) for m, side, b, _ in row]
+            self._grouped(ops.lstm_seq_fwd, qs, E)
+            seqs.append(qs)
         tm.stop("lstm_fwd")
 
         self.head_forward(sa.h[:R], sc.h[:R], R)
@@ -801,18 +825,26 @@ class RecurrentUpdateEngine(UpdateEngine):
             with torch.cuda.stream(self.side):
                 self.weight_grads(head_dw, R, ws=self.side_dw_ws)
             head_dw = []
+        # LSTM backward, top layer first: each layer's sequence, then the input-gradient of its projection into the
+        # outputs' gradient dh of the layer below (no activation between the layers)
         tm.start("lstm_bwd")
-        self._grouped(ops.lstm_seq_bwd, qa, qc, E)
+        below = {"a": self.lay_a, "c": self.lay_c}
+        for k in range(len(layers) - 1, -1, -1):
+            self._grouped(ops.lstm_seq_bwd, seqs[k], E)
+            if k > 0:
+                ops.linear_bwd_dx([(b.dgates[:R], b.packed.w_ih_g, None, below[side][k - 1].dh[:R])
+                                   for _, side, b, _ in layers[k]], R, self.dx_ws)
         tm.stop("lstm_bwd")
 
         dw = []
-        for s, x in ((sa, xa), (sc, xc)):
-            dw.append((s.dgates[:R], s.hs[:R], s.dw_hh_g, s.db_g))
-            dw.append((s.dgates[:R], x, s.dw_ih_g, None))  # same operand dgates: its column sums once
+        for row in layers:
+            for _, _, b, x in row:
+                dw.append((b.dgates[:R], b.hs[:R], b.dw_hh_g, b.db_g))
+                dw.append((b.dgates[:R], x, b.dw_ih_g, None))  # same operand dgates: its column sums once
         self.weight_grads(dw + head_dw, R, "lstm_dw")
         grad = alg.flat.grad_view
-        ops.lstm_unpack_grads([(s.dw_ih_g, s.dw_hh_g, s.db_g, *(grad(p) for p in m.rnn.weights))
-                               for s, m in ((sa, actor), (sc, critic))])
+        ops.lstm_unpack_grads([(b.dw_ih_g, b.dw_hh_g, b.db_g, *(grad(p) for p in m.rnn.layer_weights(b.layer)))
+                               for m, lays in ((actor, self.lay_a), (critic, self.lay_c)) for b in lays])
         if self.lstm_sync is None:
             main.wait_stream(self.side)
         self.adam(step)

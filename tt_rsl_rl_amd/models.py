@@ -408,75 +408,90 @@ class MLPModel(nn.Module):
 
 
 class RNN(nn.Module):
-    """rsl_rl/modules/rnn.py:22-86 for a one-layer LSTM, in rollout mode on the GPU.
+    """rsl_rl/modules/rnn.py:22-86 for an LSTM of one or more layers, in rollout mode on the GPU.
 
-    The parameters carry nn.LSTM's names (``rnn.weight_ih_l0``, ``rnn.weight_hh_l0``, ``rnn.bias_ih_l0``,
-    ``rnn.bias_hh_l0`` under this module) and its initial values: an ``nn.LSTM`` is built on the CPU (drawing from
-    the global generator exactly as upstream's constructor does) and its tensors are adopted, so no torch RNN
-    kernel ever runs.  ``hidden_state`` is upstream's tuple ``(h, c)`` of [1, N, H] tensors, or None before the
-    first step; every step writes fresh tensors, so a state captured with ``get_hidden_state`` stays valid (upstream
-    relies on that in ``compute_returns``)."""
+    The parameters carry nn.LSTM's names (``rnn.weight_ih_l<k>``, ``rnn.weight_hh_l<k>``, ``rnn.bias_ih_l<k>``,
+    ``rnn.bias_hh_l<k>`` under this module, layer after layer) and its initial values: an ``nn.LSTM`` is built on the
+    CPU (drawing from the global generator exactly as upstream's constructor does) and its tensors are adopted, so no
+    torch RNN kernel ever runs.  ``hidden_state`` is upstream's tuple ``(h, c)`` of [layers, N, H] tensors, or None
+    before the first step; every step writes fresh tensors, so a state captured with ``get_hidden_state`` stays valid
+    (upstream relies on that in ``compute_returns``).  Layer k > 0 takes layer k - 1's new h as its input."""
 
     def __init__(self, input_size: int, hidden_dim: int = 256, num_layers: int = 1, type: str = "lstm") -> None:
         super().__init__()
         if type.lower() != "lstm":
             raise NotImplementedError(f"rnn_type '{type}': the HIP recurrent path implements the LSTM")
-        if num_layers != 1:
-            raise NotImplementedError("the HIP LSTM kernels implement one layer (rnn_num_layers=1)")
+        if num_layers < 1:
+            raise ValueError(f"rnn_num_layers={num_layers}")
         if hidden_dim % 4 != 0:
             raise NotImplementedError(f"rnn_hidden_dim={hidden_dim}: the HIP LSTM kernels need a multiple of 4")
-        ref = nn.LSTM(input_size=input_size, hidden_size=hidden_dim, num_layers=1)
+        ref = nn.LSTM(input_size=input_size, hidden_size=hidden_dim, num_layers=num_layers)
         self.rnn = nn.Module()
-        for name in ("weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0"):
-            self.rnn.register_parameter(name, nn.Parameter(getattr(ref, name).detach().clone()))
+        for k in range(num_layers):
+            for name in (f"weight_ih_l{k}", f"weight_hh_l{k}", f"bias_ih_l{k}", f"bias_hh_l{k}"):
+                self.rnn.register_parameter(name, nn.Parameter(getattr(ref, name).detach().clone()))
         self.input_size = input_size
         self.hidden_size = hidden_dim
+        self.num_layers = num_layers
         self.hidden_state: tuple[torch.Tensor, torch.Tensor] | None = None
-        self._packed: ops.LstmPacked | None = None
+        self._packed: list[ops.LstmPacked] = []
         self._fwd = _ForwardBuffers()
         self._hs = _ForwardBuffers()
         self._const = _ForwardBuffers()
 
+    def layer_input_size(self, k: int) -> int:
+        return self.input_size if k == 0 else self.hidden_size
+
+    def layer_weights(self, k: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        r = self.rnn
+        return (getattr(r, f"weight_ih_l{k}"), getattr(r, f"weight_hh_l{k}"), getattr(r, f"bias_ih_l{k}"),
+                getattr(r, f"bias_hh_l{k}"))
+
     @property
     def weights(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-        r = self.rnn
-        return r.weight_ih_l0, r.weight_hh_l0, r.bias_ih_l0, r.bias_hh_l0
+        """Layer 0's weights."""
+        return self.layer_weights(0)
 
-    def packed(self, device) -> ops.LstmPacked:
-        """The gate-interleaved weight copies the kernels read (buffers only; ``ops.lstm_pack`` fills them)."""
-        pk = self._packed
-        if pk is None or pk.w_ih_g.device != torch.device(device):
-            self._packed = pk = ops.LstmPacked(self.input_size, self.hidden_size, device)
-        return pk
+    def packed(self, device, k: int = 0) -> ops.LstmPacked:
+        """Layer k's gate-interleaved weight copies the kernels read (buffers only; ``ops.lstm_pack`` fills them)."""
+        if len(self._packed) != self.num_layers or self._packed[0].w_ih_g.device != torch.device(device):
+            self._packed = [ops.LstmPacked(self.layer_input_size(i), self.hidden_size, device)
+                            for i in range(self.num_layers)]
+        return self._packed[k]
 
     def forward(self, x: torch.Tensor, masks=None, hidden_state=None) -> torch.Tensor:
-        """rnn.py:35-52, rollout mode: one step for every env of ``x`` [N, input_size]; returns h' [N, H]."""
+        """rnn.py:35-52, rollout mode: one step for every env of ``x`` [N, input_size], layer after layer; returns the
+        last layer's h' [N, H]."""
         if masks is not None:
             raise NotImplementedError("padded trajectory batches: the recurrent update evaluates them on the GPU "
                                       "inside PPO.update()")
         _require_gpu(x, "RNN.forward")
-        N, H, dev = x.shape[0], self.hidden_size, x.device
-        pk = self.packed(dev)
-        ops.lstm_pack([(*self.weights, pk)])
+        N, H, layers, dev = x.shape[0], self.hidden_size, self.num_layers, x.device
         gx, gates = self._fwd.get(N, [4 * H, 4 * H], dev)
         zero, ones = self._const.get(N, [H, 1], dev)
+        ones.fill_(1.0)
         if self.hidden_state is None:
             zero.zero_()
-            h0 = c0 = zero
-        else:
-            h0, c0 = (s.reshape(N, H) for s in self.hidden_state)
-            if h0.stride(0) != H or c0.stride(0) != H:
-                h0, c0 = h0.contiguous(), c0.contiguous()
-        ones.fill_(1.0)
-        ops.linear_fwd([(x, pk.w_ih_g, pk.b_g, gx, None)], N, elu=False)
-        h_new = torch.empty(1, N, H, device=dev)
-        c_new = torch.empty(1, N, H, device=dev)
+        h_new = torch.empty(layers, N, H, device=dev)
+        c_new = torch.empty(layers, N, H, device=dev)
         # hs: the per-step input states the backward reads ([T + 1 blocks of N rows]); unused in rollout mode
         hs = self._hs.get(2 * N, [H], dev)[0]
-        ops.lstm_seq_fwd([dict(packed=pk, hidden=H, gx=gx, h0=h0, c0=c0, keep=ones.view(-1), h=h_new[0], hs=hs,
-                               c=c_new[0], gates=gates)], 1, N)
+        inp = x
+        for k in range(layers):
+            pk = self.packed(dev, k)
+            ops.lstm_pack([(*self.layer_weights(k), pk)])
+            if self.hidden_state is None:
+                h0 = c0 = zero
+            else:
+                h0, c0 = (s[k].reshape(N, H) for s in self.hidden_state)
+                if h0.stride(0) != H or c0.stride(0) != H:
+                    h0, c0 = h0.contiguous(), c0.contiguous()
+            ops.linear_fwd([(inp, pk.w_ih_g, pk.b_g, gx, None)], N, act=L.PPO_ACT_NONE)
+            ops.lstm_seq_fwd([dict(packed=pk, hidden=H, gx=gx, h0=h0, c0=c0, keep=ones.view(-1), h=h_new[k], hs=hs,
+                                   c=c_new[k], gates=gates)], 1, N)
+            inp = h_new[k]
         self.hidden_state = (h_new, c_new)
-        return h_new[0]
+        return h_new[layers - 1]
 
     def reset(self, dones: torch.Tensor | None = None, hidden_state=None) -> None:
         """rnn.py:54-71."""
@@ -573,10 +588,13 @@ def _export_parts(model) -> tuple[nn.Module, nn.Module, nn.Module]:
 
 
 def _cpu_lstm(model: RNNModel) -> nn.LSTM:
-    lstm = nn.LSTM(model.rnn.input_size, model.rnn.hidden_size)
+    rnn = model.rnn
+    lstm = nn.LSTM(rnn.input_size, rnn.hidden_size, num_layers=rnn.num_layers)
     with torch.no_grad():
-        for name, p in zip(("weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0"), model.rnn.weights):
-            getattr(lstm, name).copy_(p.detach().cpu())
+        for k in range(rnn.num_layers):
+            for name, p in zip((f"weight_ih_l{k}", f"weight_hh_l{k}", f"bias_ih_l{k}", f"bias_hh_l{k}"),
+                               rnn.layer_weights(k)):
+                getattr(lstm, name).copy_(p.detach().cpu())
     return lstm
 
 

@@ -641,7 +641,8 @@ class LstmPacked:
 
 
 def lstm_pack(items: list[tuple]) -> None:
-    """items: (w_ih [4H, D], w_hh [4H, H], b_ih [4H], b_hh [4H], LstmPacked)."""
+    """items: (w_ih [4H, D], w_hh [4H, H], b_ih [4H], b_hh [4H], LstmPacked), any number (launches of up to
+    MAX_LSTM_PROBLEMS each)."""
     probs = []
     for w_ih, w_hh, b_ih, b_hh, pk in items:
         _dev(w_ih, w_hh, b_ih, b_hh)
@@ -655,7 +656,9 @@ def lstm_pack(items: list[tuple]) -> None:
         probs.append(L.LstmPackProblem(w_ih.data_ptr(), w_hh.data_ptr(), b_ih.data_ptr(), b_hh.data_ptr(),
                                        pk.w_ih_g.data_ptr(), pk.w_hh_g.data_ptr(), pk.w_hh_gt.data_ptr(),
                                        pk.b_g.data_ptr(), pk.input_size, pk.hidden))
-    L.call("ppo_lstm_pack", L.array(L.LstmPackProblem, probs), len(probs), _stream())
+    for i in range(0, len(probs), L.MAX_LSTM_PROBLEMS):
+        part = probs[i:i + L.MAX_LSTM_PROBLEMS]
+        L.call("ppo_lstm_pack", L.array(L.LstmPackProblem, part), len(part), _stream())
 
 
 def _seq_problem(q: dict, steps: int, envs: int, bwd: bool) -> "L.LstmSeqProblem":
@@ -727,7 +730,8 @@ def lstm_seq_bwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor
 
 
 def lstm_unpack_grads(items: list[tuple]) -> None:
-    """items: (dw_ih_g [4H, D], dw_hh_g [4H, H], db_g [4H], dw_ih, dw_hh, db_ih, db_hh (torch layout views))."""
+    """items: (dw_ih_g [4H, D], dw_hh_g [4H, H], db_g [4H], dw_ih, dw_hh, db_ih, db_hh (torch layout views)), any
+    number (launches of up to MAX_LSTM_PROBLEMS each)."""
     probs = []
     for dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh in items:
         _dev(dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh)
@@ -738,4 +742,6 @@ def lstm_unpack_grads(items: list[tuple]) -> None:
                 raise ValueError("lstm_unpack_grads: gradient buffers do not match [4H, D] / [4H, H] / [4H]")
         probs.append(L.LstmGradProblem(dw_ih_g.data_ptr(), dw_hh_g.data_ptr(), db_g.data_ptr(), dw_ih.data_ptr(),
                                        dw_hh.data_ptr(), db_ih.data_ptr(), db_hh.data_ptr(), dw_ih.shape[1], H))
-    L.call("ppo_lstm_unpack_grads", L.array(L.LstmGradProblem, probs), len(probs), _stream())
+    for i in range(0, len(probs), L.MAX_LSTM_PROBLEMS):
+        part = probs[i:i + L.MAX_LSTM_PROBLEMS]
+        L.call("ppo_lstm_unpack_grads", L.array(L.LstmGradProblem, part), len(part), _stream())

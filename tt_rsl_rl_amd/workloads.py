@@ -80,18 +80,24 @@ def gemm_flops_per_update(workload: dict, epochs: int = 5) -> float:
 
 
 def lstm_gemm_flops_per_update(workload: dict, epochs: int = 5) -> float:
-    """Recurrent models (one LSTM layer of hidden H on D observation columns, then the MLP head), per model and
-    sample-visit: LSTM forward 2*4H*(D+H) (input projection + recurrent product), weight-grad 2*4H*(D+H), the
-    recurrent input-grad 2*4H*H on all but the last step of each sequence (no gradient flows into the saved initial
-    state or the observations); the head: forward, input-grad and weight-grad of every layer (its first layer's
-    input-grad feeds the LSTM)."""
+    """Recurrent models (LSTM layers of hidden H, the first on D observation columns and each later one on the h of
+    the layer below, then the MLP head), per model, layer and sample-visit: LSTM forward 2*4H*(D_k+H) (input
+    projection + recurrent product), weight-grad 2*4H*(D_k+H), the recurrent input-grad 2*4H*H on all but the last
+    step of each sequence (no gradient flows into the saved initial state), for a layer above the first the
+    input-grad 2*4H*H into the lower layer's outputs (none into the observations); the head: forward, input-grad and
+    weight-grad of every layer (its first layer's input-grad feeds the top LSTM layer)."""
     N, T = workload["num_envs"], workload["steps"]
     B = N * T
     H = workload["rnn"]["rnn_hidden_dim"]
+    layers_rnn = workload["rnn"].get("rnn_num_layers", 1)
     dims, groups = workload["obs"], workload["obs_groups"]
     total = 0
     for layers, model in zip(linear_shapes(workload), ("actor", "critic")):
         D = sum(dims[g][1] for g in groups[model])
-        total += B * (sum(3 * 2 * i * o for i, o in layers) + 2 * 2 * 4 * H * (D + H))
-        total += (B - N) * 2 * 4 * H * H
+        total += B * sum(3 * 2 * i * o for i, o in layers)
+        for k in range(layers_rnn):
+            Dk = D if k == 0 else H
+            total += B * 2 * 2 * 4 * H * (Dk + H) + (B - N) * 2 * 4 * H * H
+            if k > 0:
+                total += B * 2 * 4 * H * H
     return float(total) * epochs
