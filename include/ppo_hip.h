@@ -438,7 +438,8 @@ int ppo_adam_step_static(float* params, float* grads, float* exp_avg, float* exp
                          double bc2_sqrt, ppo_device_state* state, ppo_stream_t stream);
 
 /* ------------------------------------------------------------------------------------------------------------------
- * A15  LSTM of the recurrent models (torch nn.LSTM, one layer, gates i, f, g, o): rsl_rl/modules/rnn.py:22-86,
+ * A15  LSTM / GRU of the recurrent models (torch nn.LSTM: gates i, f, g, o; torch nn.GRU: gates r, z, n; one layer
+ * per call, stacked layers call again on the h of the layer below): rsl_rl/modules/rnn.py:22-86,
  * rsl_rl/models/rnn_model.py:76-84, the recurrent mini-batches of rsl_rl/storage/rollout_storage.py:262-331 and the
  * trajectory padding of rsl_rl/utils/utils.py:395-463.
  *
@@ -448,11 +449,17 @@ int ppo_adam_step_static(float* params, float* grads, float* exp_avg, float* exp
  * from the state saved at step 0, with the state multiplied by keep_t = 1 - done_t after step t.  That is the form
  * evaluated here: rows are t * E + e (step-major), the envs of a mini-batch being E consecutive envs.
  *
- * Gate-interleaved layout ("_g"): row (or column) 4u + q holds gate q (i, f, g, o) of hidden unit u, so that one
- * 16-byte group holds the four gates of a unit.  H must be a multiple of 4; every pointer 16-byte aligned and
- * every leading dimension a multiple of 4.
+ * Gate-interleaved layout ("_g"): row (or column) 4u + q holds slot q of hidden unit u, so that one 16-byte group
+ * holds the four slots of a unit.  LSTM: slot q = gate q (i, f, g, o).  GRU: slots r, z, the hidden part of n
+ * (W_hn h + b_hn) and the input part of n (W_in x + b_in); w_ih_g is zero in slot 2 and w_hh_g in slot 3, so the
+ * input projection and the recurrent product are the LSTM's, and the cell n = tanh(slot 3 + r * slot 2),
+ * h' = n + z (h - n) (torch's order) reads them apart.  The GRU's state h takes the place of the LSTM's cell state c
+ * in every buffer (c0 = h0, c = h).  H must be a multiple of 4; every pointer 16-byte aligned and every leading
+ * dimension a multiple of 4.
  * ------------------------------------------------------------------------------------------------------------------ */
 #define PPO_MAX_LSTM_PROBLEMS 2
+#define PPO_CELL_LSTM 0
+#define PPO_CELL_GRU 1
 
 /* torch-layout weights -> gate-interleaved copies: w_ih_g [4H, D], w_hh_g [4H, H], w_hh_gt = w_hh_g^T [H, 4H],
  * b_g = b_ih + b_hh [4H] (the gates' bias, nn.LSTM adds both). */
@@ -464,6 +471,9 @@ typedef struct ppo_lstm_pack_problem {
 } ppo_lstm_pack_problem;
 
 int ppo_lstm_pack(const ppo_lstm_pack_problem* problems, int32_t count, ppo_stream_t stream);
+/* The same for torch nn.GRU weights ([3H, D], [3H, H], [3H], [3H]; gates r, z, n) into the four-slot layout:
+ * b_g = (b_ir + b_hr, b_iz + b_hz, b_hn, b_in) per unit. */
+int ppo_gru_pack(const ppo_lstm_pack_problem* problems, int32_t count, ppo_stream_t stream);
 
 /* One model's sequence over T steps x E envs.  The forward consumes gx = x w_ih_g^T + b_g for every row (from
  * ppo_linear_fwd) and writes, per step, the gate activations, the cell and hidden states, and hs (the state entering
@@ -485,7 +495,7 @@ typedef struct ppo_lstm_seq_problem {
   float* dgates;                             /* backward: [T*E, 4H], ld 4H */
   float* dc;                                 /* backward: [E, H] scratch, ld H */
   int32_t hidden;
-  int32_t reserved;
+  int32_t cell;                              /* PPO_CELL_LSTM or PPO_CELL_GRU; one value for all problems of a call */
 } ppo_lstm_seq_problem;
 
 /* Synchronisation buffer of the whole-sequence launches: int32 words for `count` problems of `envs` rows (-1 for an
@@ -520,6 +530,9 @@ typedef struct ppo_lstm_grad_problem {
 } ppo_lstm_grad_problem;
 
 int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream);
+/* The same into torch nn.GRU's layout ([3H, D], [3H, H], [3H], [3H]): the r and z bias gradients go to both biases,
+ * slot 2's to b_hn and slot 3's to b_in. */
+int ppo_gru_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream);
 
 #ifdef __cplusplus
 }

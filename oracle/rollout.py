@@ -113,8 +113,10 @@ def generate(workload: dict, seed: int = 0, carry_state: bool = False, **alg_ove
     n = workload["num_envs"]
     if carry_state and "rnn" in workload:
         H, layers = workload["rnn"]["rnn_hidden_dim"], workload["rnn"].get("rnn_num_layers", 1)
+        gru = workload["rnn"].get("rnn_type", "lstm").lower() == "gru"
         for model in (alg.actor, alg.critic):
-            model.reset(hidden_state=tuple(0.5 * torch.randn(layers, n, H) for _ in range(2)))
+            state = tuple(0.5 * torch.randn(layers, n, H) for _ in range(1 if gru else 2))
+            model.reset(hidden_state=state[0] if gru else state)
     with torch.inference_mode():
         obs = sample_obs(workload)
         for _ in range(workload["steps"]):

@@ -133,7 +133,10 @@ def function_outputs(params: dict, ora, eval_obs: dict) -> dict[str, torch.Tenso
                 continue
             saved = model.get_hidden_state()
             h0 = eval_obs["h0_" + tag]
-            model.reset(hidden_state=None if h0 is None else tuple(h.clone() for h in h0))
+            state = None if h0 is None else tuple(h.clone() for h in h0)
+            if state is not None and len(state) == 1:  # the GRU's state is one tensor
+                state = state[0]
+            model.reset(hidden_state=state)
             ys = []
             for t, obs_t in enumerate(eval_obs["seq"]):
                 ys.append(torch.func.functional_call(model, p, (obs_t,)))

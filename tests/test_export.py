@@ -19,10 +19,10 @@ GROUPS = {"actor": ["policy", "extra"], "critic": ["policy"]}
 DIST = {"class_name": "GaussianDistribution", "init_std": 1.0, "std_type": "log"}
 
 
-def _pair(recurrent: bool, normalization: bool, layers: int = 1):
+def _pair(recurrent: bool, normalization: bool, layers: int = 1, rnn_type: str = "lstm"):
     kw = dict(hidden_dims=[32, 16], activation="elu", obs_normalization=normalization, distribution_cfg=DIST)
     if recurrent:
-        kw.update(rnn_type="lstm", rnn_hidden_dim=24, rnn_num_layers=layers)
+        kw.update(rnn_type=rnn_type, rnn_hidden_dim=24, rnn_num_layers=layers)
     torch.manual_seed(0)
     ora = (O.RNNModel if recurrent else O.MLPModel)(OBS, GROUPS, "actor", 5, **kw)
     torch.manual_seed(0)
@@ -110,46 +110,65 @@ def _oracle_steps(ora, seq: list[dict], dones: list[torch.Tensor]) -> list[torch
     return outs
 
 
-@pytest.mark.parametrize("layers", [1, 2])
-def test_lstm_jit_and_onnx_exports_step_like_upstream(layers):
-    ora, hip = _pair(True, True, layers)
+class _TensorOutputs(torch.nn.Module):
+    def __init__(self, m: torch.nn.Module) -> None:
+        super().__init__()
+        self.m = m
+
+    def forward(self, obs: torch.Tensor, h: torch.Tensor):
+        return self.m(obs, h)[:2]
+
+
+@pytest.mark.parametrize("rnn_type,layers", [("lstm", 1), ("lstm", 2), ("gru", 1), ("gru", 2)])
+def test_recurrent_jit_and_onnx_exports_step_like_upstream(rnn_type, layers):
+    ora, hip = _pair(True, True, layers, rnn_type)
+    lstm = rnn_type == "lstm"
     jit = hip.as_jit()
-    # upstream's copy: its state buffers, then the normaliser, the torch LSTM (the wrapper's inner nn.LSTM) and the
-    # MLP, in that order
+    # upstream's copy: its state buffers (the GRU has no cell state), then the normaliser, the torch RNN (the
+    # wrapper's inner nn.LSTM / nn.GRU) and the MLP, in that order
     sd = ora.state_dict()
-    expected = (["hidden_state", "cell_state"] + [k for k in sd if k.startswith("obs_normalizer.")] +
+    states = ["hidden_state", "cell_state"] if lstm else ["hidden_state"]
+    expected = (states + [k for k in sd if k.startswith("obs_normalizer.")] +
                 [k.replace("rnn.rnn.", "rnn.") for k in sd if k.startswith("rnn.")] +
                 [k for k in sd if k.startswith("mlp.")])
     assert list(jit.state_dict().keys()) == expected
-    assert list(hip.as_onnx().state_dict().keys()) == expected[2:]
-    assert jit.hidden_state.shape == jit.cell_state.shape == (layers, 1, 24)
+    assert list(hip.as_onnx().state_dict().keys()) == expected[len(states):]
+    assert isinstance(jit.rnn, torch.nn.LSTM if lstm else torch.nn.GRU)
+    for name in states:
+        assert getattr(jit, name).shape == (layers, 1, 24)
     scripted = torch.jit.script(jit)
     seq = [_obs(1, 10 + t) for t in range(6)]
     dones = [torch.tensor([1.0 if t == 2 else 0.0]) for t in range(6)]
     ref = _oracle_steps(ora, seq, dones)
     onnx_model = hip.as_onnx()
-    assert onnx_model.input_names == ["obs", "h_in", "c_in"]
-    assert onnx_model.output_names == ["actions", "h_out", "c_out"]
-    _, h, c = onnx_model.get_dummy_inputs()
+    assert onnx_model.input_names == (["obs", "h_in", "c_in"] if lstm else ["obs", "h_in"])
+    assert onnx_model.output_names == (["actions", "h_out", "c_out"] if lstm else ["actions", "h_out"])
+    dummy = onnx_model.get_dummy_inputs()
+    assert len(dummy) == (3 if lstm else 2)
+    state = list(dummy[1:])
     with torch.no_grad():
         for t, (obs, d) in enumerate(zip(seq, dones)):
             assert torch.allclose(scripted(_flat(obs)), ref[t], rtol=1e-6, atol=1e-7), t
-            out, h, c = onnx_model(_flat(obs), h, c)
+            out, h, c = onnx_model(_flat(obs), *state)
+            assert (c is None) == (not lstm)
+            state = [h, c] if lstm else [h]
             assert torch.allclose(out, ref[t], rtol=1e-6, atol=1e-7), t
             if d.item() == 1.0:  # a done: the exported models start the next step from the zero state
                 scripted.reset()
-                h, c = torch.zeros_like(h), torch.zeros_like(c)
-        traced = torch.jit.trace(onnx_model, onnx_model.get_dummy_inputs())
-        out, _, _ = traced(*onnx_model.get_dummy_inputs())
+                state = [torch.zeros_like(x) for x in state]
+        # the GRU's (out, h, None) as upstream's: torch.jit.trace takes tensor outputs only, so trace the two tensors
+        fn = onnx_model if lstm else _TensorOutputs(onnx_model)
+        traced = torch.jit.trace(fn, onnx_model.get_dummy_inputs())
+        out = traced(*onnx_model.get_dummy_inputs())[0]
         assert out.shape == (1, 5)
     _maybe_onnx_export(onnx_model)
 
 
-@pytest.mark.parametrize("recurrent", [False, True])
+@pytest.mark.parametrize("recurrent", [False, "lstm", "gru"])
 def test_to_cpu_gives_an_inference_copy(recurrent):
     """model.to("cpu") returns a plain-torch copy with upstream's forward on observation dicts (the deterministic
     mean; recurrent models carry a per-env state that reset(dones) zeroes) and leaves the model itself alone."""
-    ora, hip = _pair(recurrent, True)
+    ora, hip = _pair(bool(recurrent), True, rnn_type=recurrent or "lstm")
     before = [p.data_ptr() for p in hip.parameters()]
     pol = hip.to("cpu")
     assert isinstance(pol, M.TorchPolicy) and pol is not hip

@@ -1,6 +1,7 @@
-"""The LSTM kernels through the C ABI (ppo_lstm_pack / _seq_fwd / _seq_bwd / _unpack_grads, plus the input projection
-and weight gradients through the linear entry points) against an fp64 reference of torch.nn.LSTM's cell equations
-over the masked per-env sequence (state multiplied by 1 - done after each step) with autograd gradients.  The
+"""The LSTM and GRU kernels through the C ABI (ppo_lstm_pack / ppo_gru_pack, _seq_fwd / _seq_bwd, _unpack_grads,
+plus the input projection and weight gradients through the linear entry points) against an fp64 reference of
+torch.nn.LSTM's / torch.nn.GRU's cell equations over the masked per-env sequence (state multiplied by 1 - done after
+each step) with autograd gradients.  The
 equivalence of that sequence with upstream's padded trajectories is pinned on the CPU
 (tests/test_oracle_recurrent.py)."""
 
@@ -84,21 +85,97 @@ def test_lstm_sequence_forward_and_backward(cuda, T, E, D, H, one_launch):
         assert int(sync[0]) == 0
 
 
-def _random_sequences(dev, T, E, H, count, seed):
+def _reference_gru(x, h0, dones, w_ih, w_hh, b_ih, b_hh, dh):
+    """fp64 over torch.nn.GRU's cell equations (gates r, z, n; n = tanh(W_in x + b_in + r (W_hn h + b_hn)),
+    h' = (1 - z) n + z h): outputs [T, E, H] and d(sum(out * dh))/d(w_ih, w_hh, b_ih, b_hh)."""
+    params = [p.detach().double().requires_grad_(True) for p in (w_ih, w_hh, b_ih, b_hh)]
+    w_ih, w_hh, b_ih, b_hh = params
+    H = h0.shape[1]
+    h = h0.double()
+    outs = []
+    for t in range(x.shape[0]):
+        gi = x[t].double() @ w_ih.t() + b_ih
+        gh = h @ w_hh.t() + b_hh
+        r = torch.sigmoid(gi[:, :H] + gh[:, :H])
+        z = torch.sigmoid(gi[:, H:2 * H] + gh[:, H:2 * H])
+        n = torch.tanh(gi[:, 2 * H:] + r * gh[:, 2 * H:])
+        h = (1.0 - z) * n + z * h
+        outs.append(h)
+        h = h * (1.0 - dones[t].double())[:, None]
+    out = torch.stack(outs)
+    (out * dh.double()).sum().backward()
+    return out.detach(), [p.grad for p in params]
+
+
+@pytest.mark.parametrize("one_launch", [False, True], ids=["per_step", "one_launch"])
+@pytest.mark.parametrize("T,E,D,H", [(7, 64, 48, 256), (5, 200, 13, 8), (24, 1024, 48, 256), (6, 100, 20, 96),
+                                     (9, 130, 7, 32)])
+def test_gru_sequence_forward_and_backward(cuda, T, E, D, H, one_launch):
+    """The GRU on the LSTM's kernels (ppo_gru_pack's four-slot layout, cell = PPO_CELL_GRU, ppo_gru_unpack_grads)
+    against nn.GRU's equations in fp64 with autograd gradients; per-step and whole-sequence launches."""
+    from tt_rsl_rl_amd import ops
+
+    torch.manual_seed(T * 1000 + H + 7)
+    gru = torch.nn.GRU(D, H)
+    w_ih, w_hh, b_ih, b_hh = (p.detach() for p in (gru.weight_ih_l0, gru.weight_hh_l0, gru.bias_ih_l0,
+                                                    gru.bias_hh_l0))
+    # biases of the size the weights have, so a bias mapped to the wrong slot shows
+    b_ih, b_hh = torch.randn_like(b_ih) * 0.3, torch.randn_like(b_hh) * 0.3
+    x = torch.randn(T, E, D)
+    h0 = torch.randn(E, H) * 0.5
+    dones = (torch.rand(T, E) < 0.2).float()
+    dh = torch.randn(T, E, H) / math.sqrt(H)
+    ref_out, ref_grads = _reference_gru(x, h0, dones, w_ih, w_hh, b_ih, b_hh, dh)
+
+    dev = cuda
+    g = lambda t: t.contiguous().to(dev)
+    pk = ops.LstmPacked(D, H, dev)
+    wd = [g(w) for w in (w_ih, w_hh, b_ih, b_hh)]
+    ops.lstm_pack([(*wd, pk)], gru=True)
+    R = T * E
+    xf = g(x.reshape(R, D))
+    gx = torch.empty(R, 4 * H, device=dev)
+    ops.linear_fwd([(xf, pk.w_ih_g, pk.b_g, gx, None)], R, elu=False)
+    keep = g(1.0 - dones.reshape(R))
+    h0d = g(h0)
+    q = dict(packed=pk, hidden=H, gx=gx, h0=h0d, c0=h0d, keep=keep, h=torch.empty(R, H, device=dev),
+             hs=torch.empty(R + E, H, device=dev), c=torch.empty(R, H, device=dev),
+             gates=torch.empty(R, 4 * H, device=dev), dh=g(dh.reshape(R, H)),
+             dgates=torch.empty(R, 4 * H, device=dev), dc=torch.empty(E, H, device=dev), gru=True)
+    sync = torch.zeros(ops.lstm_seq_sync_words(1, E), dtype=torch.int32, device=dev) if one_launch else None
+    ops.lstm_seq_fwd([q], T, E, sync)
+    assert rel_err(q["h"].view(T, E, H), ref_out) < 1e-5
+    assert torch.equal(q["c"], q["h"])  # the GRU's state is h
+    ops.lstm_seq_bwd([q], T, E, sync)
+    dw_ih_g, dw_hh_g = torch.empty(4 * H, D, device=dev), torch.empty(4 * H, H, device=dev)
+    db_g = torch.empty(4 * H, device=dev)
+    ops.linear_bwd_dw([(q["dgates"], q["hs"][:R], dw_hh_g, db_g), (q["dgates"], xf, dw_ih_g, None)], R)
+    grads = [torch.empty_like(t) for t in wd]
+    ops.lstm_unpack_grads([(dw_ih_g, dw_hh_g, db_g, *grads)], gru=True)
+    torch.cuda.synchronize()
+    for name, got, want in zip(("w_ih", "w_hh", "b_ih", "b_hh"), grads, ref_grads):
+        assert rel_err(got, want) < 1e-5, name
+    if sync is not None:
+        assert int(sync[0]) == 0
+
+
+def _random_sequences(dev, T, E, H, count, seed, gru=False):
     from tt_rsl_rl_amd import ops
 
     gen = torch.Generator().manual_seed(seed)
+    G = (3 if gru else 4) * H
     qs = []
     for _ in range(count):
         pk = ops.LstmPacked(8, H, dev)
-        w = [torch.randn(4 * H, 8, generator=gen) * 0.3, torch.randn(4 * H, H, generator=gen) / math.sqrt(H),
-             torch.randn(4 * H, generator=gen) * 0.1, torch.randn(4 * H, generator=gen) * 0.1]
-        ops.lstm_pack([(*(t.to(dev) for t in w), pk)])
+        w = [torch.randn(G, 8, generator=gen) * 0.3, torch.randn(G, H, generator=gen) / math.sqrt(H),
+             torch.randn(G, generator=gen) * 0.1, torch.randn(G, generator=gen) * 0.1]
+        ops.lstm_pack([(*(t.to(dev) for t in w), pk)], gru=gru)
         R = T * E
         dones = (torch.rand(R, generator=gen) < 0.05).float()
-        qs.append(dict(packed=pk, hidden=H, gx=torch.randn(R, 4 * H, generator=gen).to(dev),
-                       h0=(torch.randn(E, H, generator=gen) * 0.5).to(dev),
-                       c0=(torch.randn(E, H, generator=gen) * 0.5).to(dev), keep=(1.0 - dones).to(dev)))
+        h0 = (torch.randn(E, H, generator=gen) * 0.5).to(dev)
+        c0 = h0 if gru else (torch.randn(E, H, generator=gen) * 0.5).to(dev)
+        qs.append(dict(packed=pk, hidden=H, gx=torch.randn(R, 4 * H, generator=gen).to(dev), h0=h0, c0=c0,
+                       keep=(1.0 - dones).to(dev), gru=gru))
     return qs
 
 
@@ -108,16 +185,17 @@ def _outputs(q, T, E, H, dev):
                 c=torch.full((R, H), float("nan"), device=dev), gates=torch.full((R, 4 * H), float("nan"), device=dev))
 
 
+@pytest.mark.parametrize("gru", [False, True], ids=["lstm", "gru"])
 @pytest.mark.parametrize("T,E,H,count", [(24, 1024, 256, 2), (9, 200, 64, 1), (5, 70, 96, 2), (4, 8192, 256, 2),
                                          (3, 64, 512, 1), (1, 100, 256, 2), (6, 65, 32, 2)])
-def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count):
+def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count, gru):
     """The whole-sequence forward (row groups of 64 envs synchronised through the sync buffer; 8192 envs need more
     row groups than the device holds at once, so blocks take several in turn; H = 512 and T = 1 take the per-step
     launches) gives bit-identical outputs to one launch per step, and leaves the status word clear."""
     from tt_rsl_rl_amd import ops
 
     dev = cuda
-    qs = _random_sequences(dev, T, E, H, count, seed=T * 7919 + E + H)
+    qs = _random_sequences(dev, T, E, H, count, seed=T * 7919 + E + H, gru=gru)
     per_step = [_outputs(q, T, E, H, dev) for q in qs]
     ops.lstm_seq_fwd(per_step, T, E)
     sync = torch.zeros(ops.lstm_seq_sync_words(count, E), dtype=torch.int32, device=dev)
@@ -132,16 +210,17 @@ def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count):
             assert torch.equal(a["hs"], b["hs"]), ("hs", rep)
 
 
+@pytest.mark.parametrize("gru", [False, True], ids=["lstm", "gru"])
 @pytest.mark.parametrize("T,E,H,count", [(24, 1024, 256, 2), (9, 200, 64, 1), (5, 70, 96, 2), (4, 8192, 256, 2),
                                          (3, 64, 512, 1), (6, 65, 32, 2)])
-def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count):
+def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count, gru):
     """The whole-sequence backward against one launch per step on the same forward: dgates of every step agree to
     fp32 rounding (the recurrent product sums its 4H terms in another order), the status word stays clear, and a
     second call on the same buffer gives the same bits."""
     from tt_rsl_rl_amd import ops
 
     dev = cuda
-    qs = _random_sequences(dev, T, E, H, count, seed=T * 31 + E + H)
+    qs = _random_sequences(dev, T, E, H, count, seed=T * 31 + E + H, gru=gru)
     gen = torch.Generator().manual_seed(E + H)
     qs = [_outputs(q, T, E, H, dev) for q in qs]
     ops.lstm_seq_fwd(qs, T, E)

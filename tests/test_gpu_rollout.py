@@ -21,9 +21,9 @@ from tests.parity import make_hip, rel_err
 pytestmark = pytest.mark.gpu
 
 
-def _workload(layers: int = 1):
+def _workload(layers: int = 1, rnn_type: str = "lstm"):
     w = R.scaled(R.WORKLOADS["lstm256"], num_envs=96, steps=6, hidden_dims=[64, 32])
-    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=64, rnn_num_layers=layers)
+    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=64, rnn_num_layers=layers, rnn_type=rnn_type)
     w["obs_normalization"] = True
     return w
 
@@ -51,6 +51,11 @@ def _env_inputs(w: dict, seed: int, time_outs: bool = False) -> list[dict]:
     return steps
 
 
+def _states(h) -> tuple:
+    """A recurrent model's state as a tuple: (h, c) for the LSTM, (h,) for the GRU."""
+    return h if isinstance(h, tuple) else (h,)
+
+
 def _rollout(alg, env: list[dict], dev, seed: int) -> list[dict]:
     """One rollout of alg on the recorded env inputs after torch.manual_seed(seed); per step the transition's
     tensors (on the CPU) and the models' carried states after the step."""
@@ -64,22 +69,23 @@ def _rollout(alg, env: list[dict], dev, seed: int) -> list[dict]:
             r = {"actions": tr.actions.cpu().clone(), "values": tr.values.cpu().clone(),
                  "logp": tr.actions_log_prob.cpu().clone(),
                  "params": [p.cpu().clone() for p in tr.distribution_params],
-                 "hidden": [None if h is None else [x.cpu().clone() for x in h] for h in tr.hidden_states]}
+                 "hidden": [None if h is None else [x.cpu().clone() for x in _states(h)] for h in tr.hidden_states]}
             e = env[step + 1]
             extras = {"time_outs": e["time_outs"].to(dev) if dev is not None else e["time_outs"]} \
                 if "time_outs" in e else {}
             alg.process_env_step(to(e["obs"]), e["rewards"].to(dev) if dev is not None else e["rewards"],
                                  e["dones"].to(dev) if dev is not None else e["dones"], extras)
-            r["carried"] = [None if m.get_hidden_state() is None else [x.cpu().clone() for x in m.get_hidden_state()]
-                            for m in (alg.actor, alg.critic)]
+            r["carried"] = [None if m.get_hidden_state() is None else
+                            [x.cpu().clone() for x in _states(m.get_hidden_state())] for m in (alg.actor, alg.critic)]
             rec.append(r)
     r_state = torch.get_rng_state()
     return rec, r_state
 
 
-@pytest.mark.parametrize("layers", [1, 2])
-def test_recurrent_rollout_matches_oracle(layers):
-    w = _workload(layers)
+@pytest.mark.parametrize("rnn_type,layers", [("lstm", 1), ("lstm", 2), ("gru", 1), ("gru", 2)])
+def test_recurrent_rollout_matches_oracle(rnn_type, layers):
+    w = _workload(layers, rnn_type)
+    states = 2 if rnn_type == "lstm" else 1
     ora = R.make_oracle(w, seed=0)
     ora.train_mode()
     hip = make_hip(w, seed=0)
@@ -102,6 +108,7 @@ def test_recurrent_rollout_matches_oracle(layers):
             if step == 0:
                 assert sh is None and so is None
                 continue
+            assert len(sh) == len(so) == states
             for x, y in zip(sh, so):
                 assert x.shape == y.shape == (layers, n, w["rnn"]["rnn_hidden_dim"])
                 assert rel_err(x, y) < 1e-5, (step, side)
@@ -119,10 +126,10 @@ def test_recurrent_rollout_matches_oracle(layers):
                 assert rel_err(a, b) < 1e-5
         # the bootstrap forward leaves the critic's rollout state as it was
         obs = env[-1]["obs"]
-        before = [t.clone() for t in hip.critic.get_hidden_state()]
+        before = [t.clone() for t in _states(hip.critic.get_hidden_state())]
         hip.compute_returns({k: v.to(dev) for k, v in obs.items()})
         ora.compute_returns(obs)
-        for a, b in zip(hip.critic.get_hidden_state(), before):
+        for a, b in zip(_states(hip.critic.get_hidden_state()), before):
             assert torch.equal(a, b)
         assert rel_err(hip.storage.returns, ora.storage.returns) < 1e-5
 

@@ -71,9 +71,10 @@ MOMENT_BAR = 1e-3
 FUNCTION_BAR = 1e-4
 
 
-def _lstm(num_envs: int, steps: int, hidden: int, hidden_dims: list[int], layers: int = 1, **kw) -> dict:
+def _lstm(num_envs: int, steps: int, hidden: int, hidden_dims: list[int], layers: int = 1, rnn_type: str = "lstm",
+          **kw) -> dict:
     w = R.scaled(R.WORKLOADS["lstm256"], num_envs=num_envs, steps=steps, hidden_dims=hidden_dims)
-    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=hidden, rnn_num_layers=layers)
+    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=hidden, rnn_num_layers=layers, rnn_type=rnn_type)
     w.update(kw)
     return w
 
@@ -117,6 +118,11 @@ CASES = {
     # two stacked LSTM layers (layer 1 reads layer 0's h): the hidden size of the workload and a small one
     "lstm256x2_512": (_lstm(512, 24, 256, [256, 128], layers=2), {"carry_state": True}),
     "lstm32x3_ragged": (_lstm(200, 10, 32, [32, 16], layers=3), {"num_mini_batches": 3, "carry_state": True}),
+    # GRU (rsl_rl/modules/rnn.py:29): the workload's shape, a normalised small one, two layers on ragged slices
+    "gru256_512": (_lstm(512, 24, 256, [256, 128], rnn_type="gru"), {"carry_state": True}),
+    "gru64_norm": (_lstm(128, 16, 64, [64, 32], rnn_type="gru", obs_normalization=True), {}),
+    "gru32x2_ragged_permb": (_lstm(200, 10, 32, [32, 16], layers=2, rnn_type="gru"),
+                             {"num_mini_batches": 3, "normalize_advantage_per_mini_batch": True, "carry_state": True}),
 }
 
 # an oracle update of the 65,536-env workload takes ~45 s of CPU time on 16 threads, and the end-to-end test runs it

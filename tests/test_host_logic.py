@@ -22,11 +22,14 @@ def test_workload_table_matches_the_oracle_copy():
     assert W.ALGORITHM == R.DEFAULT_ALGORITHM
 
 
-@pytest.mark.parametrize("name", ["flat48", "humanoid", "rough235", "lstm256", "lstm256x3"])
+@pytest.mark.parametrize("name", ["flat48", "humanoid", "rough235", "lstm256", "lstm256x3", "gru256", "gru256x2"])
 def test_initial_weights_and_state_dict_layout_equal_upstream(name):
-    """Same seed -> same default nn.Linear (and nn.LSTM, of one or several layers) init as upstream (actor then
-    critic), same keys, same parameter order."""
-    w = R.scaled(R.WORKLOADS[name.split("x")[0]], num_envs=8)
+    """Same seed -> same default nn.Linear (and nn.LSTM / nn.GRU, of one or several layers) init as upstream (actor
+    then critic), same keys, same parameter order."""
+    base = name.split("x")[0]
+    w = R.scaled(R.WORKLOADS[base.replace("gru", "lstm")], num_envs=8)
+    if base.startswith("gru"):
+        w["rnn"] = dict(w["rnn"], rnn_type="gru")
     if "x" in name:
         w["rnn"] = dict(w["rnn"], rnn_num_layers=int(name.split("x")[1]))
     ora = R.make_oracle(w, seed=3)
@@ -82,8 +85,9 @@ def test_unsupported_options_are_rejected_before_touching_the_gpu(kwargs, exc):
 def test_recurrent_options_outside_the_kernels_are_rejected():
     w = R.scaled(R.WORKLOADS["lstm256"], num_envs=8)
     obs, groups = R.zero_obs(w), w["obs_groups"]
-    with pytest.raises(NotImplementedError, match="LSTM"):
-        RNNModel(obs, groups, "actor", 12, rnn_type="gru")
+    # upstream's rule (rsl_rl/modules/rnn.py:29): "gru" in any case is the GRU, any other name the LSTM
+    assert RNNModel(obs, groups, "actor", 12, rnn_type="GRU").rnn.gru
+    assert not RNNModel(obs, groups, "actor", 12, rnn_type="rnn").rnn.gru
     with pytest.raises(ValueError, match="rnn_num_layers"):
         RNNModel(obs, groups, "actor", 12, rnn_num_layers=0)
     with pytest.raises(NotImplementedError, match="multiple of 4"):

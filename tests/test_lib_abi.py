@@ -63,7 +63,7 @@ STRUCTS = {
                                                   "b_g", "input_size", "hidden"]),
     "ppo_lstm_seq_problem": ("LstmSeqProblem", ["w_hh_g", "w_hh_gt", "gx", "ldgx", "h0", "c0", "ld0", "keep",
                                                 "keep_stride", "h", "ldh", "hs", "c", "gates", "dh", "lddh",
-                                                "dgates", "dc", "hidden"]),
+                                                "dgates", "dc", "hidden", "cell"]),
     "ppo_lstm_grad_problem": ("LstmGradProblem", ["dw_ih_g", "dw_hh_g", "db_g", "dw_ih", "dw_hh", "db_ih", "db_hh",
                                                   "input_size", "hidden"]),
 }
@@ -162,6 +162,18 @@ def test_argument_validation_reports_errors_without_a_gpu():
     pack = _lib.LstmPackProblem(8, 8, 8, 8, 8, 8, 8, 8, 48, 250)
     with pytest.raises(ValueError, match="sizes"):
         _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)
+    with pytest.raises(ValueError, match="ppo_gru_pack: problem 0 sizes"):
+        _lib.call("ppo_gru_pack", ctypes.byref(pack), 1, None)
+    grad = _lib.LstmGradProblem(8, 8, 8, 8, 8, 8, 8, 48, 6)
+    with pytest.raises(ValueError, match="ppo_gru_unpack_grads: problem 0 sizes"):
+        _lib.call("ppo_gru_unpack_grads", ctypes.byref(grad), 1, None)
+    # the cell type: LSTM (0) or GRU (1), one type per call
+    bad = _lib.LstmSeqProblem(hidden=256, cell=2)
+    with pytest.raises(ValueError, match="cell=2"):
+        _lib.call("ppo_lstm_seq_fwd", ctypes.byref(bad), 1, 24, 64, None, 0, None)
+    mixed = _lib.array(_lib.LstmSeqProblem, [full, _lib.LstmSeqProblem(hidden=256, cell=_lib.CELL_GRU)])
+    with pytest.raises(ValueError, match="share the cell type"):
+        _lib.call("ppo_lstm_seq_fwd", mixed, 2, 24, 64, None, 0, None)
     probs = _lib.array(_lib.LinearBwdDwProblem, [_lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512)])
     assert lib.ppo_linear_bwd_dw_workspace_bytes(probs, 1, 24576) >= 4 * 512 * 96
     # column interleave: at most MAX_INTERLEAVE_FLOATS per row, a destination wide enough, 32-bit element count

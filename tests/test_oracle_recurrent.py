@@ -95,19 +95,42 @@ def _masked_lstm_fp64(x, h0, c0, dones, w_ih, w_hh, b_ih, b_hh):
     return torch.stack(outs)
 
 
+def _masked_gru_fp64(x, h0, dones, w_ih, w_hh, b_ih, b_hh):
+    """The same for torch.nn.GRU's cell equations as its documentation states them (gates r, z, n):
+    r = sigma(W_ir x + b_ir + W_hr h + b_hr), z likewise, n = tanh(W_in x + b_in + r (W_hn h + b_hn)),
+    h' = (1 - z) n + z h."""
+    H = h0.shape[-1]
+    h = h0.double()
+    outs = []
+    for t in range(x.shape[0]):
+        gi = x[t].double() @ w_ih.double().t() + b_ih.double()
+        gh = h @ w_hh.double().t() + b_hh.double()
+        r = torch.sigmoid(gi[:, :H] + gh[:, :H])
+        z = torch.sigmoid(gi[:, H:2 * H] + gh[:, H:2 * H])
+        n = torch.tanh(gi[:, 2 * H:] + r * gh[:, 2 * H:])
+        h = (1.0 - z) * n + z * h
+        outs.append(h)
+        h = h * (1.0 - dones[t].double())[:, None]
+    return torch.stack(outs)
+
+
+@pytest.mark.parametrize("rnn_type", ["lstm", "gru"])
 @pytest.mark.parametrize("num_envs,num_steps,num_batches,layers", [(6, 5, 2, 1), (9, 7, 3, 1), (9, 7, 3, 2),
                                                                    (5, 6, 1, 3)])
-def test_padded_trajectories_equal_the_masked_per_env_sequence(num_envs, num_steps, num_batches, layers):
-    """The oracle's upstream-style evaluation (split at dones, pad, LSTM from each trajectory's saved start state,
-    unpad) equals one sequence per env from the state saved at step 0 with the state zeroed after every done; with
-    stacked layers, layer by layer, each from its own saved state and on the h sequence of the layer below."""
+def test_padded_trajectories_equal_the_masked_per_env_sequence(num_envs, num_steps, num_batches, layers, rnn_type):
+    """The oracle's upstream-style evaluation (split at dones, pad, nn.LSTM / nn.GRU from each trajectory's saved
+    start state, unpad) equals one sequence per env from the state saved at step 0 with the state zeroed after every
+    done, evaluated with the cell equations written out; with stacked layers, layer by layer, each from its own saved
+    state and on the h sequence of the layer below."""
     torch.manual_seed(3)
     D, H = 4, 5
-    rnn = O.RNN(D, hidden_dim=H, num_layers=layers, type="lstm").double()
+    gru = rnn_type == "gru"
+    rnn = O.RNN(D, hidden_dim=H, num_layers=layers, type=rnn_type).double()
     obs = {"policy": torch.zeros(num_envs, D)}
     st = O.RolloutStorage(num_envs, num_steps, obs, [1])
-    # a state carried in from a previous rollout
-    state = (torch.randn(layers, num_envs, H), torch.randn(layers, num_envs, H))
+    # a state carried in from a previous rollout (the GRU's: one tensor)
+    state = (torch.randn(layers, num_envs, H),) if gru else (torch.randn(layers, num_envs, H),
+                                                              torch.randn(layers, num_envs, H))
     for step in range(num_steps):
         t = O.Transition()
         t.observations = {"policy": torch.randn(num_envs, D)}
@@ -117,21 +140,24 @@ def test_padded_trajectories_equal_the_masked_per_env_sequence(num_envs, num_ste
         t.distribution_params = (torch.zeros(num_envs, 1), torch.ones(num_envs, 1))
         t.rewards = torch.zeros(num_envs)
         t.dones = (torch.rand(num_envs) < 0.3).float()
-        t.hidden_states = (state, state)
+        t.hidden_states = (state[0], state[0]) if gru else (state, state)
         st.add_transition(t)
         # what the rollout does: the policy's state after the step (any value), zeroed for done envs
         state = tuple(s.clone().normal_() * (1 - t.dones)[None, :, None] for s in state)
     w = rnn.rnn
     for b, i in zip(st.recurrent_mini_batch_generator(num_batches, 1), range(num_batches)):
         lo, hi = i * num_envs // num_batches, (i + 1) * num_envs // num_batches
-        hs = tuple(s.double() for s in b.hidden_states[0])
+        hs = b.hidden_states[0].double() if gru else tuple(s.double() for s in b.hidden_states[0])
         got = rnn(b.observations["policy"].double(), b.masks, hs)
         want = st.observations["policy"][:, lo:hi]
         for k in range(layers):
             h0 = st.saved_hidden_state_a[0][0, k, lo:hi]
-            c0 = st.saved_hidden_state_a[1][0, k, lo:hi]
-            want = _masked_lstm_fp64(want, h0, c0, st.dones[:, lo:hi, 0], *(getattr(w, f"{n}_l{k}") for n in
-                                     ("weight_ih", "weight_hh", "bias_ih", "bias_hh")))
+            weights = [getattr(w, f"{n}_l{k}") for n in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+            if gru:
+                want = _masked_gru_fp64(want, h0, st.dones[:, lo:hi, 0], *weights)
+            else:
+                c0 = st.saved_hidden_state_a[1][0, k, lo:hi]
+                want = _masked_lstm_fp64(want, h0, c0, st.dones[:, lo:hi, 0], *weights)
         assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
 
 

@@ -116,6 +116,7 @@ class DeviceState(C.Structure):
 
 DEVICE_STATE_BYTES = C.sizeof(DeviceState)
 MAX_LSTM_PROBLEMS = 2
+CELL_LSTM, CELL_GRU = 0, 1
 vp = C.c_void_p
 
 
@@ -127,7 +128,7 @@ class LstmPackProblem(C.Structure):
 class LstmSeqProblem(C.Structure):
     _fields_ = [("w_hh_g", vp), ("w_hh_gt", vp), ("gx", vp), ("ldgx", i64), ("h0", vp), ("c0", vp), ("ld0", i64),
                 ("keep", vp), ("keep_stride", i64), ("h", vp), ("ldh", i64), ("hs", vp), ("c", vp), ("gates", vp),
-                ("dh", vp), ("lddh", i64), ("dgates", vp), ("dc", vp), ("hidden", i32), ("reserved", i32)]
+                ("dh", vp), ("lddh", i64), ("dgates", vp), ("dc", vp), ("hidden", i32), ("cell", i32)]
 
 
 class LstmGradProblem(C.Structure):
@@ -144,11 +145,13 @@ _SIGNATURES = [
     ("ppo_gather_rows", C.c_int, [C.c_void_p, i64, i64, C.POINTER(GatherSegment), i32, f32p, i64, C.c_void_p]),
     ("ppo_linear_fwd", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, C.c_void_p]),
     ("ppo_lstm_pack", C.c_int, [C.POINTER(LstmPackProblem), i32, C.c_void_p]),
+    ("ppo_gru_pack", C.c_int, [C.POINTER(LstmPackProblem), i32, C.c_void_p]),
     ("ppo_lstm_seq_sync_words", i64, [i32, i64]),
     ("ppo_lstm_seq_wait_limit", i64, [i64]),
     ("ppo_lstm_seq_fwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_seq_bwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
+    ("ppo_gru_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
     ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),
     ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, C.c_void_p, C.c_size_t,
                                     C.c_void_p]),

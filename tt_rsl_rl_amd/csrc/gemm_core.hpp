@@ -70,6 +70,7 @@ struct LstmArgs {
   float* dc;               // bwd: [E, H] cell gradient carried to the previous step (read unless first)
   int64_t ldgx, ldcp, ldh, lddh, keep_stride;
   int32_t hidden, first, last;  // bwd: first = no carried cell gradient yet, last = do not write dc
+  int32_t cell;                 // PPO_CELL_LSTM or PPO_CELL_GRU (see gru_cell_fwd for the GRU's use of the buffers)
 };
 
 struct Problem {
@@ -511,10 +512,37 @@ __device__ __forceinline__ LstmCellFwd lstm_cell_fwd(const f32x4& x, const f32x4
   return o;
 }
 
+// GRU cell (torch nn.GRU: r = sigma(W_ir x + b_ir + W_hr h + b_hr), z likewise, n = tanh(W_in x + b_in + r (W_hn h +
+// b_hn)), h' = (1 - z) n + z h, evaluated as torch's cell does: n + z (h - n)) on the LSTM's four-slot layout.  Slot q
+// of unit u holds r, z, the hidden part of n (W_hn h + b_hn) and its input part (W_in x + b_in): w_ih_g has zero rows
+// in slot 2, w_hh_g in slot 3, and b_g = (b_ir + b_hr, b_iz + b_hz, b_hn, b_in), so the input projection and the
+// recurrent product are the LSTM's GEMMs.  x = the recurrent product (slot 3 exactly zero), gx = the projection (slot
+// 2 exactly b_hn), hp = h_{t-1} of the unit multiplied by keep_prev.  The state the LSTM keeps in c is h itself here:
+// c = h = h', act = (r, z, W_hn h + b_hn, n) for the backward.
+__device__ __forceinline__ LstmCellFwd gru_cell_fwd(const f32x4& x, const f32x4& gx, float hp) {
+  LstmCellFwd o;
+  const float r = sigmoid_hw(x[0] + gx[0]), z = sigmoid_hw(x[1] + gx[1]);
+  const float a = x[2] + gx[2];
+  const float n = tanh_hw((x[3] + gx[3]) + r * a);
+  o.h = n + z * (hp - n);
+  o.c = o.h;
+  o.act = f32x4{r, z, a, n};
+  return o;
+}
+
+template <bool GRU>
+__device__ __forceinline__ LstmCellFwd rnn_cell_fwd(const f32x4& x, const f32x4& gx, float cp) {
+  if constexpr (GRU) {
+    return gru_cell_fwd(x, gx, cp);
+  } else {
+    return lstm_cell_fwd(x, gx, cp);
+  }
+}
+
 __device__ __forceinline__ void lstm_fwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, const f32x4& gx,
                                                 float cp) {
   const int64_t H = L.hidden, u = n >> 2;
-  const LstmCellFwd o = lstm_cell_fwd(x, gx, cp);
+  const LstmCellFwd o = L.cell == PPO_CELL_GRU ? gru_cell_fwd(x, gx, cp) : lstm_cell_fwd(x, gx, cp);
   *reinterpret_cast<f32x4*>(L.gates + m * 4 * H + n) = o.act;
   L.c[m * H + u] = o.c;
   L.h[m * L.ldh + u] = o.h;
@@ -539,12 +567,45 @@ __device__ __forceinline__ void lstm_cell_bwd(const f32x4& x, float keep, float 
   }
 }
 
+// GRU backward cell for env m, hidden units n .. n+3 (slots and act as gru_cell_fwd).  The state h_t reaches step
+// t + 1 through the recurrent product (x, masked by keep) and directly through z h_t: dcin carries the latter,
+// dh_{t+1} z_{t+1} keep_t, as the LSTM carries dL/dc.  dpre = (dr r (1 - r), dz z (1 - z), dn' r, dn') with
+// dn' = dh (1 - z) (1 - n^2), dr = dn' (W_hn h + b_hn), dz = dh (h_{t-1} - n).
+__device__ __forceinline__ void gru_cell_bwd(const f32x4& x, float keep, float keep_prev, const f32x4& dhu,
+                                             const f32x4& cp, const f32x4& dcin, const f32x4 (&gt)[4],
+                                             f32x4 (&dpre)[4], f32x4& dcout) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float r = gt[e][0], z = gt[e][1], a = gt[e][2], nn = gt[e][3];
+    const float dh = (dhu[e] + keep * x[e]) + dcin[e];
+    const float dn = dh * (1.0f - z) * (1.0f - nn * nn);
+    const float dz = dh * (cp[e] * keep_prev - nn);
+    dpre[e] = f32x4{dn * a * r * (1.0f - r), dz * z * (1.0f - z), dn * r, dn};
+    dcout[e] = dh * z * keep_prev;
+  }
+}
+
+template <bool GRU>
+__device__ __forceinline__ void rnn_cell_bwd(const f32x4& x, float keep, float keep_prev, const f32x4& dhu,
+                                             const f32x4& ct, const f32x4& cp, const f32x4& dcin,
+                                             const f32x4 (&gt)[4], f32x4 (&dpre)[4], f32x4& dcout) {
+  if constexpr (GRU) {
+    gru_cell_bwd(x, keep, keep_prev, dhu, cp, dcin, gt, dpre, dcout);
+  } else {
+    lstm_cell_bwd(x, keep, keep_prev, dhu, ct, cp, dcin, gt, dpre, dcout);
+  }
+}
+
 __device__ __forceinline__ void lstm_bwd_finish(const LstmArgs& L, int64_t m, int n, const f32x4& x, float keep,
                                                 float keep_prev, const f32x4& dhu, const f32x4& ct, const f32x4& cp,
                                                 const f32x4& dcin, const f32x4 (&gt)[4]) {
   const int64_t H = L.hidden;
   f32x4 dpre[4], dcout;
-  lstm_cell_bwd(x, keep, keep_prev, dhu, ct, cp, dcin, gt, dpre, dcout);
+  if (L.cell == PPO_CELL_GRU) {
+    gru_cell_bwd(x, keep, keep_prev, dhu, cp, dcin, gt, dpre, dcout);
+  } else {
+    lstm_cell_bwd(x, keep, keep_prev, dhu, ct, cp, dcin, gt, dpre, dcout);
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) *reinterpret_cast<f32x4*>(L.dgates + m * 4 * H + 4 * (n + e)) = dpre[e];
   if (!L.last) *reinterpret_cast<f32x4*>(L.dc + m * H + n) = dcout;

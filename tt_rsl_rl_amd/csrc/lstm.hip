@@ -19,9 +19,6 @@
 namespace ppo {
 namespace {
 
-// Gate-interleaved index of torch row r = q*H + u is 4u + q.
-__device__ __forceinline__ int64_t interleave(int64_t r, int64_t H) { return 4 * (r % H) + r / H; }
-
 struct PackItem {
   const float* w_ih;
   const float* w_hh;
@@ -32,6 +29,7 @@ struct PackItem {
   float* w_hh_gt;
   float* b_g;
   int64_t D, H, begin;  // begin: first flat element of this problem in the launch
+  int32_t gru;          // torch nn.GRU weights (r, z, n) into the four-slot layout of gru_cell_fwd
 };
 struct PackGroup {
   PackItem it[PPO_MAX_LSTM_PROBLEMS];
@@ -47,26 +45,34 @@ __global__ __launch_bounds__(256) void lstm_pack_kernel(const PackGroup g) {
     const PackItem& P = g.it[(g.count > 1 && e >= g.it[1].begin) ? 1 : 0];
     int64_t k = e - P.begin;
     const int64_t H = P.H, D = P.D, G = 4 * H;
-    if (k < G * D) {  // w_ih_g[4u+q][d] = w_ih[qH+u][d]
-      const int64_t n = k / D, d = k % D;
-      P.w_ih_g[k] = P.w_ih[((n & 3) * H + (n >> 2)) * D + d];
+    // torch gate of slot q (-1: a zero row).  LSTM: slot q = gate q (i, f, g, o) of both weights.  GRU: slots r, z
+    // of both weights, slot 2 = n of w_hh only, slot 3 = n of w_ih only.
+    auto gate_ih = [&](int64_t q) -> int64_t { return P.gru ? (q < 2 ? q : q == 3 ? 2 : -1) : q; };
+    auto gate_hh = [&](int64_t q) -> int64_t { return P.gru ? (q < 3 ? q : -1) : q; };
+    if (k < G * D) {  // w_ih_g[4u+q][d] = w_ih[gate(q) H + u][d]
+      const int64_t n = k / D, d = k % D, q = gate_ih(n & 3);
+      P.w_ih_g[k] = q < 0 ? 0.0f : P.w_ih[(q * H + (n >> 2)) * D + d];
       continue;
     }
     k -= G * D;
-    if (k < G * H) {  // w_hh_g[4u+q][j] = w_hh[qH+u][j]
-      const int64_t n = k / H, j = k % H;
-      P.w_hh_g[k] = P.w_hh[((n & 3) * H + (n >> 2)) * H + j];
+    if (k < G * H) {  // w_hh_g[4u+q][j] = w_hh[gate(q) H + u][j]
+      const int64_t n = k / H, j = k % H, q = gate_hh(n & 3);
+      P.w_hh_g[k] = q < 0 ? 0.0f : P.w_hh[(q * H + (n >> 2)) * H + j];
       continue;
     }
     k -= G * H;
-    if (k < G * H) {  // w_hh_gt[j][4u+q] = w_hh[qH+u][j]
-      const int64_t j = k / G, n = k % G;
-      P.w_hh_gt[k] = P.w_hh[((n & 3) * H + (n >> 2)) * H + j];
+    if (k < G * H) {  // w_hh_gt[j][4u+q] = w_hh_g[4u+q][j]
+      const int64_t j = k / G, n = k % G, q = gate_hh(n & 3);
+      P.w_hh_gt[k] = q < 0 ? 0.0f : P.w_hh[(q * H + (n >> 2)) * H + j];
       continue;
     }
-    k -= G * H;  // b_g[4u+q] = b_ih[qH+u] + b_hh[qH+u]
-    const int64_t r = (k & 3) * H + (k >> 2);
-    P.b_g[k] = P.b_ih[r] + P.b_hh[r];
+    k -= G * H;  // b_g[4u+q] = b_ih[gate_ih(q) H + u] + b_hh[gate_hh(q) H + u] (a missing gate adds nothing)
+    const int64_t u = k >> 2, qi = gate_ih(k & 3), qh = gate_hh(k & 3);
+    if (qi >= 0 && qh >= 0) {
+      P.b_g[k] = P.b_ih[qi * H + u] + P.b_hh[qh * H + u];
+    } else {
+      P.b_g[k] = qi >= 0 ? P.b_ih[qi * H + u] : P.b_hh[qh * H + u];
+    }
   }
 }
 
@@ -79,6 +85,7 @@ struct GradItem {
   float* db_ih;
   float* db_hh;
   int64_t D, H, begin;
+  int32_t gru;  // torch nn.GRU layout ([3H, D], [3H, H], [3H]) from the four-slot layout of gru_cell_fwd
 };
 struct GradGroup {
   GradItem it[PPO_MAX_LSTM_PROBLEMS];
@@ -86,29 +93,35 @@ struct GradGroup {
   int64_t total;
 };
 
-// Flat element e of a problem: [0, 4HD) dw_ih, [.., +4HH) dw_hh, [.., +4H) db_ih and db_hh (torch layout, written
-// once each).
+// Flat element e of a problem: [0, GD) dw_ih, [.., +GH) dw_hh, [.., +G) db_ih and db_hh (torch layout, written once
+// each; G = 4H rows for the LSTM, 3H for the GRU).  The LSTM's bias gradient goes to both b_ih and b_hh; the GRU's n
+// gate has separate input and hidden biases (slots 3 and 2).
 __global__ __launch_bounds__(256) void lstm_unpack_kernel(const GradGroup g) {
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < g.total;
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const GradItem& P = g.it[(g.count > 1 && e >= g.it[1].begin) ? 1 : 0];
     int64_t k = e - P.begin;
-    const int64_t H = P.H, D = P.D, G = 4 * H;
+    const int64_t H = P.H, D = P.D, G = (P.gru ? 3 : 4) * H;
+    // torch row r = q H + u -> interleaved row 4u + slot
+    auto slot_ih = [&](int64_t r) -> int64_t {
+      const int64_t q = r / H;
+      return 4 * (r % H) + (P.gru && q == 2 ? 3 : q);
+    };
+    auto slot_hh = [&](int64_t r) -> int64_t { return 4 * (r % H) + r / H; };
     if (k < G * D) {
       const int64_t r = k / D, d = k % D;
-      P.dw_ih[k] = P.dw_ih_g[interleave(r, H) * D + d];
+      P.dw_ih[k] = P.dw_ih_g[slot_ih(r) * D + d];
       continue;
     }
     k -= G * D;
     if (k < G * H) {
       const int64_t r = k / H, j = k % H;
-      P.dw_hh[k] = P.dw_hh_g[interleave(r, H) * H + j];
+      P.dw_hh[k] = P.dw_hh_g[slot_hh(r) * H + j];
       continue;
     }
     k -= G * H;
-    const float v = P.db_g[interleave(k, H)];
-    P.db_ih[k] = v;
-    P.db_hh[k] = v;
+    P.db_ih[k] = P.db_g[slot_ih(k)];
+    P.db_hh[k] = P.db_g[slot_hh(k)];
   }
 }
 
@@ -268,7 +281,7 @@ __device__ __forceinline__ void seq_signal(int32_t* ctr) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NS>
+template <int NS, bool GRU>
 __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
   constexpr int BK = kSeqBK, WSLAB = kSeqCols * BK, ASLAB = kSeqRows * BK;
   __shared__ __align__(16) float wl[NS * WSLAB];
@@ -301,7 +314,7 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
     const int64_t m = m0 + wm * 32 + (lane & 31);
     const bool in = m < E;
     const int64_t mc = in ? m : E - 1;
-    float cp[4];  // c_{t-1} * keep_{t-1} of the lane's units; step 0: c0
+    float cp[4];  // c_{t-1} * keep_{t-1} of the lane's units (the GRU: h_{t-1} * keep_{t-1}); step 0: c0
 #pragma unroll
     for (int q = 0; q < 4; ++q) cp[q] = S.c0[mc * S.ld0 + ((ncol + 8 * q) >> 2)];
     // this thread's two 16-byte chunks of every 64 x 32 slab of hs[t]: rows clamped to E - 1
@@ -374,7 +387,7 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const f32x4 x = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
-        const LstmCellFwd o = lstm_cell_fwd(x, gx[q], cp[q]);
+        const LstmCellFwd o = rnn_cell_fwd<GRU>(x, gx[q], cp[q]);
         act[q] = o.act;
         cv[q] = o.c;
         hv[q] = o.h;
@@ -441,7 +454,7 @@ struct SeqBwdArgs {
   int32_t xcds;
 };
 
-template <int NS>
+template <int NS, bool GRU>
 __global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
   constexpr int K = kSeqBwdKS * NS, KC = K / 4, U = kSeqBwdUnits, AH = kSeqBwdAhead < NS ? kSeqBwdAhead : NS;
   __shared__ __align__(16) float wl[U * K];
@@ -554,7 +567,7 @@ __global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
       for (int ti = 0; ti < 2; ++ti) {
         const f32x4 x = (acc[ti][0] + acc[ti][1]) + (acc[ti][2] + acc[ti][3]);
         f32x4 dcout;
-        lstm_cell_bwd(x, keep, kp, dhu[ti], ct[ti], cp[ti], dc[ti], gt[ti], dpre[ti], dcout);
+        rnn_cell_bwd<GRU>(x, keep, kp, dhu[ti], ct[ti], cp[ti], dc[ti], gt[ti], dpre[ti], dcout);
         dc[ti] = dcout;
       }
       // dgates[t]: the next step's operand (through this XCD's L2 when every writer of the row group runs here, else
@@ -594,6 +607,8 @@ int check_seq(const ppo_lstm_seq_problem* probs, int32_t count, int64_t steps, i
     const int64_t H = q.hidden;
     PPO_REQUIRE(H >= 4 && H % 4 == 0 && H <= 4096, "%s: problem %d hidden=%d must be a positive multiple of 4", who,
                 i, q.hidden);
+    PPO_REQUIRE(q.cell == PPO_CELL_LSTM || q.cell == PPO_CELL_GRU, "%s: problem %d cell=%d", who, i, q.cell);
+    PPO_REQUIRE(q.cell == probs[0].cell, "%s: the problems of one call must share the cell type", who);
     PPO_REQUIRE(q.w_hh_g && q.gx && q.h0 && q.c0 && q.keep && q.h && q.hs && q.c && q.gates,
                 "%s: problem %d has a null pointer", who, i);
     PPO_REQUIRE(!bwd || (q.w_hh_gt && q.dh && q.dgates && q.dc), "%s: problem %d: backward buffers missing", who, i);
@@ -655,10 +670,10 @@ uint64_t seq_spin_ticks() {
 
 // Launches the whole-sequence forward when the shape allows it and the device holds at least one row-group slot
 // (count * ncb blocks) at once.  Returns PPO_OK, an error, or PPO_EUNSUPPORTED to ask for the per-step launches.
-template <int NS>
+template <int NS, bool GRU>
 int launch_seq_fwd(SeqFwdArgs& a, int count, hipStream_t s) {
   static std::atomic<int> cache[kMaxDevices];
-  const int resident = resident_blocks(lstm_seq_fwd_kernel<NS>, cache);
+  const int resident = resident_blocks(lstm_seq_fwd_kernel<NS, GRU>, cache);
   const int per_slot = count * a.ncb;
   const int slots = std::min(a.nrg, resident / per_slot);
   if (slots < 1) return PPO_EUNSUPPORTED;
@@ -666,8 +681,22 @@ int launch_seq_fwd(SeqFwdArgs& a, int count, hipStream_t s) {
   hipLaunchKernelGGL(seq_sync_reset_kernel, dim3(1), dim3(256), 0, s, a.sync,
                      static_cast<int32_t>(kSyncHeader + count * a.nrg * kSyncStride));
   if (int rc = check_launch("seq_sync_reset_kernel")) return rc;
-  hipLaunchKernelGGL((lstm_seq_fwd_kernel<NS>), dim3(count * slots * a.ncb), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((lstm_seq_fwd_kernel<NS, GRU>), dim3(count * slots * a.ncb), dim3(256), 0, s, a);
   return check_launch("lstm_seq_fwd_kernel");
+}
+
+template <bool GRU>
+int seq_fwd_slabs(SeqFwdArgs& a, int64_t H, int count, hipStream_t s) {
+  switch (H / kSeqBK) {
+    case 1: return launch_seq_fwd<1, GRU>(a, count, s);
+    case 2: return launch_seq_fwd<2, GRU>(a, count, s);
+    case 3: return launch_seq_fwd<3, GRU>(a, count, s);
+    case 4: return launch_seq_fwd<4, GRU>(a, count, s);
+    case 5: return launch_seq_fwd<5, GRU>(a, count, s);
+    case 6: return launch_seq_fwd<6, GRU>(a, count, s);
+    case 7: return launch_seq_fwd<7, GRU>(a, count, s);
+    default: return launch_seq_fwd<8, GRU>(a, count, s);
+  }
 }
 
 int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t envs, int32_t* sync,
@@ -690,22 +719,13 @@ int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
   a.T = static_cast<int32_t>(steps);
   a.nrg = static_cast<int32_t>(seq_row_groups(envs));
   a.ncb = static_cast<int32_t>(4 * H / kSeqCols);
-  switch (H / kSeqBK) {
-    case 1: return launch_seq_fwd<1>(a, count, s);
-    case 2: return launch_seq_fwd<2>(a, count, s);
-    case 3: return launch_seq_fwd<3>(a, count, s);
-    case 4: return launch_seq_fwd<4>(a, count, s);
-    case 5: return launch_seq_fwd<5>(a, count, s);
-    case 6: return launch_seq_fwd<6>(a, count, s);
-    case 7: return launch_seq_fwd<7>(a, count, s);
-    default: return launch_seq_fwd<8>(a, count, s);
-  }
+  return probs[0].cell == PPO_CELL_GRU ? seq_fwd_slabs<true>(a, H, count, s) : seq_fwd_slabs<false>(a, H, count, s);
 }
 
-template <int NS>
+template <int NS, bool GRU>
 int launch_seq_bwd(SeqBwdArgs& a, int count, hipStream_t s) {
   static std::atomic<int> cache[kMaxDevices];
-  const int resident = resident_blocks(lstm_seq_bwd_kernel<NS>, cache);
+  const int resident = resident_blocks(lstm_seq_bwd_kernel<NS, GRU>, cache);
   const int per_slot = count * a.nub;
   const int slots = std::min(a.nrg, resident / per_slot);
   if (slots < 1) return PPO_EUNSUPPORTED;
@@ -713,8 +733,22 @@ int launch_seq_bwd(SeqBwdArgs& a, int count, hipStream_t s) {
   hipLaunchKernelGGL(seq_sync_reset_kernel, dim3(1), dim3(256), 0, s, a.sync,
                      static_cast<int32_t>(kSyncHeader + count * a.nrg * kSyncStride));
   if (int rc = check_launch("seq_sync_reset_kernel")) return rc;
-  hipLaunchKernelGGL((lstm_seq_bwd_kernel<NS>), dim3(count * slots * a.nub), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((lstm_seq_bwd_kernel<NS, GRU>), dim3(count * slots * a.nub), dim3(256), 0, s, a);
   return check_launch("lstm_seq_bwd_kernel");
+}
+
+template <bool GRU>
+int seq_bwd_slabs(SeqBwdArgs& a, int64_t H, int count, hipStream_t s) {
+  switch (4 * H / kSeqBwdKS) {
+    case 2: return launch_seq_bwd<2, GRU>(a, count, s);
+    case 4: return launch_seq_bwd<4, GRU>(a, count, s);
+    case 6: return launch_seq_bwd<6, GRU>(a, count, s);
+    case 8: return launch_seq_bwd<8, GRU>(a, count, s);
+    case 10: return launch_seq_bwd<10, GRU>(a, count, s);
+    case 12: return launch_seq_bwd<12, GRU>(a, count, s);
+    case 14: return launch_seq_bwd<14, GRU>(a, count, s);
+    default: return launch_seq_bwd<16, GRU>(a, count, s);
+  }
 }
 
 int seq_bwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t envs, int32_t* sync,
@@ -736,16 +770,7 @@ int seq_bwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
   a.T = static_cast<int32_t>(steps);
   a.nrg = static_cast<int32_t>(seq_row_groups(envs));
   a.nub = static_cast<int32_t>(H / kSeqBwdUnits);
-  switch (4 * H / kSeqBwdKS) {
-    case 2: return launch_seq_bwd<2>(a, count, s);
-    case 4: return launch_seq_bwd<4>(a, count, s);
-    case 6: return launch_seq_bwd<6>(a, count, s);
-    case 8: return launch_seq_bwd<8>(a, count, s);
-    case 10: return launch_seq_bwd<10>(a, count, s);
-    case 12: return launch_seq_bwd<12>(a, count, s);
-    case 14: return launch_seq_bwd<14>(a, count, s);
-    default: return launch_seq_bwd<16>(a, count, s);
-  }
+  return probs[0].cell == PPO_CELL_GRU ? seq_bwd_slabs<true>(a, H, count, s) : seq_bwd_slabs<false>(a, H, count, s);
 }
 
 int check_sync(int32_t* sync, int64_t sync_words, int count, int64_t envs, const char* who) {
@@ -762,19 +787,22 @@ int check_sync(int32_t* sync, int64_t sync_words, int count, int64_t envs, const
 
 using namespace ppo;
 
-extern "C" int ppo_lstm_pack(const ppo_lstm_pack_problem* problems, int32_t count, ppo_stream_t stream) {
-  PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LSTM_PROBLEMS, "ppo_lstm_pack: count=%d", count);
+namespace ppo {
+namespace {
+
+int pack(const ppo_lstm_pack_problem* problems, int32_t count, bool gru, ppo_stream_t stream, const char* who) {
+  PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LSTM_PROBLEMS, "%s: count=%d", who, count);
   PackGroup g{};
   int64_t total = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_lstm_pack_problem& q = problems[i];
     PPO_REQUIRE(q.w_ih && q.w_hh && q.b_ih && q.b_hh && q.w_ih_g && q.w_hh_g && q.w_hh_gt && q.b_g,
-                "ppo_lstm_pack: problem %d has a null pointer", i);
-    PPO_REQUIRE(q.input_size >= 1 && q.hidden >= 4 && q.hidden % 4 == 0, "ppo_lstm_pack: problem %d sizes", i);
+                "%s: problem %d has a null pointer", who, i);
+    PPO_REQUIRE(q.input_size >= 1 && q.hidden >= 4 && q.hidden % 4 == 0, "%s: problem %d sizes", who, i);
     PackItem& P = g.it[i];
     P.w_ih = q.w_ih; P.w_hh = q.w_hh; P.b_ih = q.b_ih; P.b_hh = q.b_hh;
     P.w_ih_g = q.w_ih_g; P.w_hh_g = q.w_hh_g; P.w_hh_gt = q.w_hh_gt; P.b_g = q.b_g;
-    P.D = q.input_size; P.H = q.hidden; P.begin = total;
+    P.D = q.input_size; P.H = q.hidden; P.begin = total; P.gru = gru;
     total += 4 * P.H * P.D + 8 * P.H * P.H + 4 * P.H;
   }
   g.count = count;
@@ -783,26 +811,44 @@ extern "C" int ppo_lstm_pack(const ppo_lstm_pack_problem* problems, int32_t coun
   return check_launch("lstm_pack_kernel");
 }
 
-extern "C" int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream) {
-  PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LSTM_PROBLEMS, "ppo_lstm_unpack_grads: count=%d",
-              count);
+int unpack(const ppo_lstm_grad_problem* problems, int32_t count, bool gru, ppo_stream_t stream, const char* who) {
+  PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LSTM_PROBLEMS, "%s: count=%d", who, count);
   GradGroup g{};
   int64_t total = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_lstm_grad_problem& q = problems[i];
     PPO_REQUIRE(q.dw_ih_g && q.dw_hh_g && q.db_g && q.dw_ih && q.dw_hh && q.db_ih && q.db_hh,
-                "ppo_lstm_unpack_grads: problem %d has a null pointer", i);
-    PPO_REQUIRE(q.input_size >= 1 && q.hidden >= 4 && q.hidden % 4 == 0, "ppo_lstm_unpack_grads: problem %d sizes", i);
+                "%s: problem %d has a null pointer", who, i);
+    PPO_REQUIRE(q.input_size >= 1 && q.hidden >= 4 && q.hidden % 4 == 0, "%s: problem %d sizes", who, i);
     GradItem& P = g.it[i];
     P.dw_ih_g = q.dw_ih_g; P.dw_hh_g = q.dw_hh_g; P.db_g = q.db_g;
     P.dw_ih = q.dw_ih; P.dw_hh = q.dw_hh; P.db_ih = q.db_ih; P.db_hh = q.db_hh;
-    P.D = q.input_size; P.H = q.hidden; P.begin = total;
-    total += 4 * P.H * P.D + 4 * P.H * P.H + 4 * P.H;
+    P.D = q.input_size; P.H = q.hidden; P.begin = total; P.gru = gru;
+    total += (gru ? 3 : 4) * P.H * (P.D + P.H + 1);
   }
   g.count = count;
   g.total = total;
   hipLaunchKernelGGL(lstm_unpack_kernel, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream), g);
   return check_launch("lstm_unpack_kernel");
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_lstm_pack(const ppo_lstm_pack_problem* problems, int32_t count, ppo_stream_t stream) {
+  return pack(problems, count, false, stream, "ppo_lstm_pack");
+}
+
+extern "C" int ppo_gru_pack(const ppo_lstm_pack_problem* problems, int32_t count, ppo_stream_t stream) {
+  return pack(problems, count, true, stream, "ppo_gru_pack");
+}
+
+extern "C" int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream) {
+  return unpack(problems, count, false, stream, "ppo_lstm_unpack_grads");
+}
+
+extern "C" int ppo_gru_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream) {
+  return unpack(problems, count, true, stream, "ppo_gru_unpack_grads");
 }
 
 extern "C" int64_t ppo_lstm_seq_sync_words(int32_t count, int64_t envs) {
@@ -863,6 +909,7 @@ extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t co
       L.h = q.h + t * E * q.ldh; L.ldh = q.ldh;
       L.hs = q.hs + (t + 1) * E * H;
       L.hidden = static_cast<int>(H);
+      L.cell = q.cell;
     }
     if (int rc = launch_step<EPI_LSTM_FWD>(g, count, s, "lstm_step_fwd")) return rc;
   }
@@ -905,6 +952,7 @@ extern "C" int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t co
       L.hidden = static_cast<int>(H);
       L.first = t + 1 == steps;
       L.last = t == 0;
+      L.cell = q.cell;
     }
     if (int rc = launch_step<EPI_LSTM_BWD>(g, count, s, "lstm_step_bwd")) return rc;
   }

@@ -642,11 +642,13 @@ class UpdateEngine:
 
 
 class LstmBuffers:
-    """Sequence buffers of one LSTM layer for mini-batches of up to ``rows`` = T x envs rows (t-major)."""
+    """Sequence buffers of one LSTM or GRU layer for mini-batches of up to ``rows`` = T x envs rows (t-major); the
+    GRU's state h takes the place of the LSTM's cell state c."""
 
     def __init__(self, rnn, layer: int, rows: int, envs: int, device) -> None:
         H, D = rnn.hidden_size, rnn.layer_input_size(layer)
         self.layer = layer
+        self.gru = rnn.gru
         e = lambda *shape: torch.empty(*shape, device=device)
         self.packed = ops.LstmPacked(D, H, device)
         self.gx, self.gates, self.dgates = e(rows, 4 * H), e(rows, 4 * H), e(rows, 4 * H)
@@ -659,7 +661,8 @@ class LstmBuffers:
 
 
 class RecurrentUpdateEngine(UpdateEngine):
-    """The recurrent update (upstream ppo.py:204-236 with rollout_storage.py:262-331 and rnn.py:35-52).
+    """The recurrent update (upstream ppo.py:204-236 with rollout_storage.py:262-331 and rnn.py:35-52), for LSTM and
+    GRU models of one or more layers.
 
     Upstream splits each env's rollout at dones, pads the trajectories, runs nn.LSTM from the hidden state saved at
     each trajectory start and unpads.  Here every env of a mini-batch is ONE sequence of T steps started from the
@@ -728,15 +731,16 @@ class RecurrentUpdateEngine(UpdateEngine):
         saved = getattr(self.alg.storage, f"saved_hidden_state_{side}")
         if saved is None:  # no state was recorded (a first rollout of one step): nn.LSTM's zero default
             return buf.zero[:e1 - e0], buf.zero[:e1 - e0]
-        # [T, layers, N, H]: the state of this layer before step 0
-        return saved[0][0, buf.layer, e0:e1], saved[1][0, buf.layer, e0:e1]
+        # [T, layers, N, H]: the state of this layer before step 0 (the GRU's h is also the kernels' c0)
+        h0 = saved[0][0, buf.layer, e0:e1]
+        return (h0, h0) if buf.gru else (h0, saved[1][0, buf.layer, e0:e1])
 
     def _seq(self, model, side: str, buf: LstmBuffers, e0: int, e1: int, tab: torch.Tensor) -> dict:
         R = self.T * (e1 - e0)
         h0, c0 = self._initial_state(side, e0, e1, buf)
         return dict(packed=buf.packed, hidden=model.rnn.hidden_size, gx=buf.gx[:R], h0=h0, c0=c0,
                     keep=tab[:, self.layout.keep], h=buf.h[:R], hs=buf.hs[:R + e1 - e0], c=buf.c[:R],
-                    gates=buf.gates[:R], dh=buf.dh[:R], dgates=buf.dgates[:R], dc=buf.dc[:e1 - e0])
+                    gates=buf.gates[:R], dh=buf.dh[:R], dgates=buf.dgates[:R], dc=buf.dc[:e1 - e0], gru=buf.gru)
 
     def dx_layers(self, R: int) -> list[tuple[int, list[tuple], bool]]:
         """As the feed-forward head's, plus layer 0: it has no activation below it, so a plain input-gradient into
@@ -765,8 +769,9 @@ class RecurrentUpdateEngine(UpdateEngine):
             self.lstm_sync.zero_()
 
     def _grouped(self, fn, qs: list[dict], E: int) -> None:
-        """One launch for the actor's and the critic's sequences of one layer when their hidden sizes agree."""
-        if len(qs) == 2 and qs[0]["hidden"] == qs[1]["hidden"]:
+        """One launch for the actor's and the critic's sequences of one layer when their hidden sizes and cell types
+        agree."""
+        if len(qs) == 2 and qs[0]["hidden"] == qs[1]["hidden"] and qs[0]["gru"] == qs[1]["gru"]:
             fn(qs, self.T, E, self.lstm_sync)
         else:
             for q in qs:
@@ -800,8 +805,11 @@ class RecurrentUpdateEngine(UpdateEngine):
         # LSTM forward, layer after layer: packed weights, input projection for all T x E rows at once, then the T
         # recurrent steps
         tm.start("lstm_fwd")
-        ops.lstm_pack([(*m.rnn.layer_weights(b.layer), b.packed)
-                       for m, lays in ((actor, self.lay_a), (critic, self.lay_c)) for b in lays])
+        packs = [(m, b) for m, lays in ((actor, self.lay_a), (critic, self.lay_c)) for b in lays]
+        for gru in (False, True):
+            items = [(*m.rnn.layer_weights(b.layer), b.packed) for m, b in packs if b.gru == gru]
+            if items:
+                ops.lstm_pack(items, gru=gru)
         layers = self._layer_inputs(xa, xc, R)
         seqs = []
         for row in layers:
@@ -843,8 +851,11 @@ class RecurrentUpdateEngine(UpdateEngine):
                 dw.append((b.dgates[:R], x, b.dw_ih_g, None))  # same operand dgates: its column sums once
         self.weight_grads(dw + head_dw, R, "lstm_dw")
         grad = alg.flat.grad_view
-        ops.lstm_unpack_grads([(b.dw_ih_g, b.dw_hh_g, b.db_g, *(grad(p) for p in m.rnn.layer_weights(b.layer)))
-                               for m, lays in ((actor, self.lay_a), (critic, self.lay_c)) for b in lays])
+        for gru in (False, True):
+            items = [(b.dw_ih_g, b.dw_hh_g, b.db_g, *(grad(p) for p in m.rnn.layer_weights(b.layer)))
+                     for m, b in packs if b.gru == gru]
+            if items:
+                ops.lstm_unpack_grads(items, gru=gru)
         if self.lstm_sync is None:
             main.wait_stream(self.side)
         self.adam(step)

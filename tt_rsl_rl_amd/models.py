@@ -408,24 +408,25 @@ class MLPModel(nn.Module):
 
 
 class RNN(nn.Module):
-    """rsl_rl/modules/rnn.py:22-86 for an LSTM of one or more layers, in rollout mode on the GPU.
+    """rsl_rl/modules/rnn.py:22-86 for an LSTM or a GRU of one or more layers, in rollout mode on the GPU.
 
-    The parameters carry nn.LSTM's names (``rnn.weight_ih_l<k>``, ``rnn.weight_hh_l<k>``, ``rnn.bias_ih_l<k>``,
-    ``rnn.bias_hh_l<k>`` under this module, layer after layer) and its initial values: an ``nn.LSTM`` is built on the
-    CPU (drawing from the global generator exactly as upstream's constructor does) and its tensors are adopted, so no
-    torch RNN kernel ever runs.  ``hidden_state`` is upstream's tuple ``(h, c)`` of [layers, N, H] tensors, or None
-    before the first step; every step writes fresh tensors, so a state captured with ``get_hidden_state`` stays valid
-    (upstream relies on that in ``compute_returns``).  Layer k > 0 takes layer k - 1's new h as its input."""
+    As upstream, ``type`` "gru" (any case) selects the GRU and anything else the LSTM.  The parameters carry the torch
+    module's names (``rnn.weight_ih_l<k>``, ``rnn.weight_hh_l<k>``, ``rnn.bias_ih_l<k>``, ``rnn.bias_hh_l<k>`` under
+    this module, layer after layer) and its initial values: an ``nn.LSTM`` / ``nn.GRU`` is built on the CPU (drawing
+    from the global generator exactly as upstream's constructor does) and its tensors are adopted, so no torch RNN
+    kernel ever runs.  ``hidden_state`` is upstream's: the LSTM's tuple ``(h, c)``, the GRU's tensor ``h``, each
+    [layers, N, H], or None before the first step; every step writes fresh tensors, so a state captured with
+    ``get_hidden_state`` stays valid (upstream relies on that in ``compute_returns``).  Layer k > 0 takes layer
+    k - 1's new h as its input."""
 
     def __init__(self, input_size: int, hidden_dim: int = 256, num_layers: int = 1, type: str = "lstm") -> None:
         super().__init__()
-        if type.lower() != "lstm":
-            raise NotImplementedError(f"rnn_type '{type}': the HIP recurrent path implements the LSTM")
         if num_layers < 1:
             raise ValueError(f"rnn_num_layers={num_layers}")
         if hidden_dim % 4 != 0:
-            raise NotImplementedError(f"rnn_hidden_dim={hidden_dim}: the HIP LSTM kernels need a multiple of 4")
-        ref = nn.LSTM(input_size=input_size, hidden_size=hidden_dim, num_layers=num_layers)
+            raise NotImplementedError(f"rnn_hidden_dim={hidden_dim}: the HIP recurrent kernels need a multiple of 4")
+        self.gru = type.lower() == "gru"
+        ref = (nn.GRU if self.gru else nn.LSTM)(input_size=input_size, hidden_size=hidden_dim, num_layers=num_layers)
         self.rnn = nn.Module()
         for k in range(num_layers):
             for name in (f"weight_ih_l{k}", f"weight_hh_l{k}", f"bias_ih_l{k}", f"bias_hh_l{k}"):
@@ -433,11 +434,16 @@ class RNN(nn.Module):
         self.input_size = input_size
         self.hidden_size = hidden_dim
         self.num_layers = num_layers
-        self.hidden_state: tuple[torch.Tensor, torch.Tensor] | None = None
+        self.hidden_state: tuple[torch.Tensor, torch.Tensor] | torch.Tensor | None = None
         self._packed: list[ops.LstmPacked] = []
         self._fwd = _ForwardBuffers()
         self._hs = _ForwardBuffers()
         self._const = _ForwardBuffers()
+
+    def states(self, hidden_state=None) -> tuple:
+        """``hidden_state`` (default: the module's) as a tuple of tensors: (h, c) for the LSTM, (h,) for the GRU."""
+        hs = self.hidden_state if hidden_state is None else hidden_state
+        return hs if isinstance(hs, tuple) else (hs,)
 
     def layer_input_size(self, k: int) -> int:
         return self.input_size if k == 0 else self.hidden_size
@@ -473,24 +479,25 @@ class RNN(nn.Module):
         if self.hidden_state is None:
             zero.zero_()
         h_new = torch.empty(layers, N, H, device=dev)
+        # the LSTM's new cell state; the GRU's kernels write the state h into this buffer too (unused)
         c_new = torch.empty(layers, N, H, device=dev)
         # hs: the per-step input states the backward reads ([T + 1 blocks of N rows]); unused in rollout mode
         hs = self._hs.get(2 * N, [H], dev)[0]
         inp = x
         for k in range(layers):
             pk = self.packed(dev, k)
-            ops.lstm_pack([(*self.layer_weights(k), pk)])
+            ops.lstm_pack([(*self.layer_weights(k), pk)], gru=self.gru)
             if self.hidden_state is None:
                 h0 = c0 = zero
             else:
-                h0, c0 = (s[k].reshape(N, H) for s in self.hidden_state)
-                if h0.stride(0) != H or c0.stride(0) != H:
-                    h0, c0 = h0.contiguous(), c0.contiguous()
+                st = [s[k].reshape(N, H) for s in self.states()]
+                st = [t if t.stride(0) == H else t.contiguous() for t in st]
+                h0, c0 = (st[0], st[0]) if self.gru else st
             ops.linear_fwd([(inp, pk.w_ih_g, pk.b_g, gx, None)], N, act=L.PPO_ACT_NONE)
             ops.lstm_seq_fwd([dict(packed=pk, hidden=H, gx=gx, h0=h0, c0=c0, keep=ones.view(-1), h=h_new[k], hs=hs,
-                                   c=c_new[k], gates=gates)], 1, N)
+                                   c=c_new[k], gates=gates, gru=self.gru)], 1, N)
             inp = h_new[k]
-        self.hidden_state = (h_new, c_new)
+        self.hidden_state = h_new if self.gru else (h_new, c_new)
         return h_new[layers - 1]
 
     def reset(self, dones: torch.Tensor | None = None, hidden_state=None) -> None:
@@ -501,7 +508,7 @@ class RNN(nn.Module):
             if hidden_state is not None:
                 raise NotImplementedError("Resetting the hidden state of done environments with a custom hidden state "
                                           "is not implemented")
-            for s in self.hidden_state:
+            for s in self.states():
                 s[..., dones == 1, :] = 0.0
 
     def detach_hidden_state(self, dones: torch.Tensor | None = None) -> None:
@@ -509,20 +516,18 @@ class RNN(nn.Module):
 
 
 class RNNModel(MLPModel):
-    """rsl_rl/models/rnn_model.py:18-107: LSTM on the (normalised) observations, then the MLP head.
+    """rsl_rl/models/rnn_model.py:18-107: LSTM or GRU on the (normalised) observations, then the MLP head.
 
     Registration order as upstream (normaliser, distribution, mlp, then ``rnn``), so the parameter order is
     [distribution, mlp.*, rnn.rnn.weight_ih_l0, weight_hh_l0, bias_ih_l0, bias_hh_l0] and a seed gives upstream's
-    initial weights.  Rollout forwards step the LSTM on the GPU; the update evaluates whole mini-batches of
-    trajectories inside ``PPO.update()``."""
+    initial weights.  Rollout forwards step the recurrent layers on the GPU; the update evaluates whole mini-batches
+    of trajectories inside ``PPO.update()``."""
 
     is_recurrent: bool = True
 
     def __init__(self, obs: Mapping, obs_groups: dict, obs_set: str, output_dim: int, hidden_dims=(256, 256, 256),
                  activation: str = "elu", obs_normalization: bool = False, distribution_cfg: dict | None = None,
                  rnn_type: str = "lstm", rnn_hidden_dim: int = 256, rnn_num_layers: int = 1) -> None:
-        if rnn_type.lower() != "lstm":
-            raise NotImplementedError(f"rnn_type '{rnn_type}': the HIP recurrent path implements the LSTM")
         self.latent_dim = rnn_hidden_dim
         super().__init__(obs, obs_groups, obs_set, output_dim, hidden_dims, activation, obs_normalization,
                          distribution_cfg)
@@ -557,9 +562,9 @@ class RNNModel(MLPModel):
         self.rnn.detach_hidden_state(dones)
 
     def as_jit(self) -> nn.Module:
-        """Export copy with plain torch modules (rsl_rl/models/rnn_model.py:98-105, 147-175) -- export, not the hot
+        """Export copy with plain torch modules (rsl_rl/models/rnn_model.py:98-105, 116-175) -- export, not the hot
         path."""
-        return _TorchLSTMModel(self)
+        return _TorchGRUModel(self) if self.rnn.gru else _TorchLSTMModel(self)
 
     def as_onnx(self) -> nn.Module:
         """rsl_rl/models/rnn_model.py:107-109, 178-247."""
@@ -587,15 +592,16 @@ def _export_parts(model) -> tuple[nn.Module, nn.Module, nn.Module]:
     return norm, copy.deepcopy(model.mlp).cpu(), det
 
 
-def _cpu_lstm(model: RNNModel) -> nn.LSTM:
+def _cpu_rnn(model: RNNModel) -> nn.Module:
+    """The model's recurrent layers as a CPU nn.GRU / nn.LSTM with its current weights."""
     rnn = model.rnn
-    lstm = nn.LSTM(rnn.input_size, rnn.hidden_size, num_layers=rnn.num_layers)
+    out = (nn.GRU if rnn.gru else nn.LSTM)(rnn.input_size, rnn.hidden_size, num_layers=rnn.num_layers)
     with torch.no_grad():
         for k in range(rnn.num_layers):
             for name, p in zip((f"weight_ih_l{k}", f"weight_hh_l{k}", f"bias_ih_l{k}", f"bias_hh_l{k}"),
                                rnn.layer_weights(k)):
-                getattr(lstm, name).copy_(p.detach().cpu())
-    return lstm
+                getattr(out, name).copy_(p.detach().cpu())
+    return out
 
 
 class _TorchMLPModel(nn.Module):
@@ -650,7 +656,7 @@ class _TorchLSTMModel(nn.Module):
         super().__init__()
         norm, mlp, det = _export_parts(model)
         self.obs_normalizer = norm  # upstream's attribute order: normaliser, rnn, mlp, deterministic output
-        self.rnn = _cpu_lstm(model)
+        self.rnn = _cpu_rnn(model)
         self.mlp, self.deterministic_output = mlp, det
         self.register_buffer("hidden_state", torch.zeros(self.rnn.num_layers, 1, self.rnn.hidden_size))
         self.register_buffer("cell_state", torch.zeros(self.rnn.num_layers, 1, self.rnn.hidden_size))
@@ -670,9 +676,35 @@ class _TorchLSTMModel(nn.Module):
         self.cell_state[:] = 0.0
 
 
+class _TorchGRUModel(nn.Module):
+    """TorchScript export copy, rsl_rl/models/rnn_model.py:116-144: one GRU step per call on a batch-1 state kept in
+    the ``hidden_state`` buffer, ``reset()`` zeroes it."""
+
+    def __init__(self, model: RNNModel) -> None:
+        super().__init__()
+        norm, mlp, det = _export_parts(model)
+        self.obs_normalizer = norm
+        self.rnn = _cpu_rnn(model)
+        self.mlp, self.deterministic_output = mlp, det
+        self.register_buffer("hidden_state", torch.zeros(self.rnn.num_layers, 1, self.rnn.hidden_size))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = self.obs_normalizer(x)
+        x, h = self.rnn(x.unsqueeze(0), self.hidden_state)
+        self.hidden_state[:] = h
+        x = x.squeeze(0)
+        out = self.mlp(x)
+        return self.deterministic_output(out)
+
+    @torch.jit.export
+    def reset(self) -> None:
+        self.hidden_state[:] = 0.0
+
+
 class _OnnxRNNModel(nn.Module):
-    """ONNX export copy of the LSTM model, rsl_rl/models/rnn_model.py:178-247: the state is an explicit input and
-    output (inputs "obs", "h_in", "c_in"; outputs "actions", "h_out", "c_out")."""
+    """ONNX export copy of the recurrent model, rsl_rl/models/rnn_model.py:178-247: the state is an explicit input
+    and output (LSTM: inputs "obs", "h_in", "c_in", outputs "actions", "h_out", "c_out"; GRU: without the cell
+    state, and None in its output slot)."""
 
     is_recurrent: bool = True
 
@@ -680,41 +712,46 @@ class _OnnxRNNModel(nn.Module):
         super().__init__()
         norm, mlp, det = _export_parts(model)
         self.obs_normalizer = norm
-        self.rnn = _cpu_lstm(model)
+        self.rnn = _cpu_rnn(model)
         self.mlp, self.deterministic_output = mlp, det
-        self.rnn_type = "lstm"
+        self.rnn_type = "gru" if model.rnn.gru else "lstm"
         self.input_size = model.obs_dim
         self.hidden_size = self.rnn.hidden_size
         self.num_layers = self.rnn.num_layers
 
-    def forward(self, obs: torch.Tensor, h_in: torch.Tensor, c_in: torch.Tensor):
+    def forward(self, obs: torch.Tensor, h_in: torch.Tensor, c_in: torch.Tensor | None = None):
         x = self.obs_normalizer(obs)
-        x, (h, c) = self.rnn(x.unsqueeze(0), (h_in, c_in))
+        if self.rnn_type == "lstm":
+            x, (h, c) = self.rnn(x.unsqueeze(0), (h_in, c_in))
+            x = x.squeeze(0)
+            out = self.deterministic_output(self.mlp(x))
+            return out, h, c
+        x, h = self.rnn(x.unsqueeze(0), h_in)
         x = x.squeeze(0)
-        out = self.mlp(x)
-        out = self.deterministic_output(out)
-        return out, h, c
+        out = self.deterministic_output(self.mlp(x))
+        return out, h, None
 
     def get_dummy_inputs(self) -> tuple[torch.Tensor, ...]:
         obs = torch.zeros(1, self.input_size)
         h_in = torch.zeros(self.num_layers, 1, self.hidden_size)
-        c_in = torch.zeros(self.num_layers, 1, self.hidden_size)
-        return (obs, h_in, c_in)
+        if self.rnn_type == "lstm":
+            return (obs, h_in, torch.zeros(self.num_layers, 1, self.hidden_size))
+        return (obs, h_in)
 
     @property
     def input_names(self) -> list[str]:
-        return ["obs", "h_in", "c_in"]
+        return ["obs", "h_in", "c_in"] if self.rnn_type == "lstm" else ["obs", "h_in"]
 
     @property
     def output_names(self) -> list[str]:
-        return ["actions", "h_out", "c_out"]
+        return ["actions", "h_out", "c_out"] if self.rnn_type == "lstm" else ["actions", "h_out"]
 
 
 class TorchPolicy(nn.Module):
     """Plain-torch inference copy of a plugin model on a device the HIP kernels do not run on (what
     ``model.to("cpu")``, and so upstream's ``runner.get_inference_policy("cpu")``, returns: the plugin model itself
     stays on the GPU, its parameters views of the update's flat buffers).  Upstream's MLPModel / RNNModel forward for
-    observation dicts: concatenated groups -> normaliser -> (LSTM, state carried per env and zeroed by
+    observation dicts: concatenated groups -> normaliser -> (LSTM / GRU, state carried per env and zeroed by
     ``reset(dones)``) -> MLP -> the distribution's mean.  A copy: later updates do not reach it."""
 
     def __init__(self, model, device) -> None:
@@ -722,7 +759,7 @@ class TorchPolicy(nn.Module):
         self.obs_groups = list(model.obs_groups)
         self.is_recurrent = bool(model.is_recurrent)
         self.obs_normalizer, self.mlp, self.deterministic_output = _export_parts(model)
-        self.rnn = _cpu_lstm(model) if self.is_recurrent else None
+        self.rnn = _cpu_rnn(model) if self.is_recurrent else None
         self.hidden_state = None
         self.to(device)
 
@@ -739,7 +776,8 @@ class TorchPolicy(nn.Module):
         if dones is None:
             self.hidden_state = hidden_state
         elif self.hidden_state is not None:
-            for s in self.hidden_state:
+            states = self.hidden_state if isinstance(self.hidden_state, tuple) else (self.hidden_state,)
+            for s in states:
                 s[..., dones == 1, :] = 0.0
 
     def get_hidden_state(self):

@@ -624,12 +624,13 @@ def C_ref(struct):
 
 
 # ----------------------------------------------------------------------------------------------------------------------
-# A15 LSTM
+# A15 LSTM / GRU
 # ----------------------------------------------------------------------------------------------------------------------
 
 
 class LstmPacked:
-    """Gate-interleaved copies of one nn.LSTM layer's weights (row 4u + q = gate q of unit u)."""
+    """Gate-interleaved copies of one nn.LSTM (or nn.GRU) layer's weights (row 4u + q = slot q of unit u: the LSTM's
+    gates i, f, g, o; the GRU's r, z, hidden part of n, input part of n)."""
 
     def __init__(self, input_size: int, hidden: int, device) -> None:
         H, D = hidden, input_size
@@ -640,9 +641,9 @@ class LstmPacked:
         self.b_g = torch.empty(4 * H, device=device)
 
 
-def lstm_pack(items: list[tuple]) -> None:
-    """items: (w_ih [4H, D], w_hh [4H, H], b_ih [4H], b_hh [4H], LstmPacked), any number (launches of up to
-    MAX_LSTM_PROBLEMS each)."""
+def lstm_pack(items: list[tuple], gru: bool = False) -> None:
+    """items: (w_ih [G, D], w_hh [G, H], b_ih [G], b_hh [G], LstmPacked) with G = 4H (nn.LSTM) or, with gru, 3H
+    (nn.GRU, ppo_gru_pack); any number (launches of up to MAX_LSTM_PROBLEMS each)."""
     probs = []
     for w_ih, w_hh, b_ih, b_hh, pk in items:
         _dev(w_ih, w_hh, b_ih, b_hh)
@@ -650,15 +651,17 @@ def lstm_pack(items: list[tuple]) -> None:
             if not t.is_contiguous():
                 raise ValueError("lstm_pack: weights must be contiguous")
         H, D = pk.hidden, pk.input_size
-        if (tuple(w_ih.shape) != (4 * H, D) or tuple(w_hh.shape) != (4 * H, H) or b_ih.numel() != 4 * H
-                or b_hh.numel() != 4 * H):
+        G = (3 if gru else 4) * H
+        if (tuple(w_ih.shape) != (G, D) or tuple(w_hh.shape) != (G, H) or b_ih.numel() != G
+                or b_hh.numel() != G):
             raise ValueError("lstm_pack: weight shapes do not match the packed buffers")
         probs.append(L.LstmPackProblem(w_ih.data_ptr(), w_hh.data_ptr(), b_ih.data_ptr(), b_hh.data_ptr(),
                                        pk.w_ih_g.data_ptr(), pk.w_hh_g.data_ptr(), pk.w_hh_gt.data_ptr(),
                                        pk.b_g.data_ptr(), pk.input_size, pk.hidden))
+    name = "ppo_gru_pack" if gru else "ppo_lstm_pack"
     for i in range(0, len(probs), L.MAX_LSTM_PROBLEMS):
         part = probs[i:i + L.MAX_LSTM_PROBLEMS]
-        L.call("ppo_lstm_pack", L.array(L.LstmPackProblem, part), len(part), _stream())
+        L.call(name, L.array(L.LstmPackProblem, part), len(part), _stream())
 
 
 def _seq_problem(q: dict, steps: int, envs: int, bwd: bool) -> "L.LstmSeqProblem":
@@ -689,7 +692,8 @@ def _seq_problem(q: dict, steps: int, envs: int, bwd: bool) -> "L.LstmSeqProblem
                             _row_major(gx, "gx"), h0.data_ptr(), c0.data_ptr(), _row_major(h0, "h0"), keep.data_ptr(),
                             keep.stride(0), h.data_ptr(), _row_major(h, "h"), q["hs"].data_ptr(), q["c"].data_ptr(),
                             q["gates"].data_ptr(), _ptr(dh), _row_major(dh, "dh") if dh is not None else 0,
-                            _ptr(q.get("dgates")), _ptr(q.get("dc")), H, 0)
+                            _ptr(q.get("dgates")), _ptr(q.get("dc")), H,
+                            L.CELL_GRU if q.get("gru") else L.CELL_LSTM)
 
 
 def lstm_seq_wait_limit(ticks: int | None) -> int:
@@ -716,7 +720,8 @@ def _sync_args(sync: torch.Tensor | None, count: int, envs: int) -> tuple[int, i
 
 def lstm_seq_fwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor | None = None) -> None:
     """problems: dicts with packed (LstmPacked), hidden, gx [T*E, 4H], h0 / c0 [E, H], keep [T*E] (stride = row
-    step), h [T*E, H], hs [(T+1)*E, H], c [T*E, H], gates [T*E, 4H].  sync: int32 device buffer of
+    step), h [T*E, H], hs [(T+1)*E, H], c [T*E, H], gates [T*E, 4H], and gru=True for a GRU (c0 = h0; c receives
+    the state h).  sync: int32 device buffer of
     lstm_seq_sync_words(len(problems), envs) words (zeroed once by the caller) for the one-launch sequence, or None
     for one launch per step."""
     arr = L.array(L.LstmSeqProblem, [_seq_problem(q, steps, envs, False) for q in problems])
@@ -729,19 +734,22 @@ def lstm_seq_bwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor
     L.call("ppo_lstm_seq_bwd", arr, len(problems), steps, envs, *_sync_args(sync, len(problems), envs), _stream())
 
 
-def lstm_unpack_grads(items: list[tuple]) -> None:
-    """items: (dw_ih_g [4H, D], dw_hh_g [4H, H], db_g [4H], dw_ih, dw_hh, db_ih, db_hh (torch layout views)), any
-    number (launches of up to MAX_LSTM_PROBLEMS each)."""
+def lstm_unpack_grads(items: list[tuple], gru: bool = False) -> None:
+    """items: (dw_ih_g [4H, D], dw_hh_g [4H, H], db_g [4H], dw_ih, dw_hh, db_ih, db_hh (torch layout views: 4H rows,
+    or 3H with gru, ppo_gru_unpack_grads)), any number (launches of up to MAX_LSTM_PROBLEMS each)."""
     probs = []
     for dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh in items:
         _dev(dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh)
         H, D = dw_hh.shape[1], dw_ih.shape[1]
-        for t, n in ((dw_ih_g, 4 * H * D), (dw_ih, 4 * H * D), (dw_hh_g, 4 * H * H), (dw_hh, 4 * H * H), (db_g, 4 * H),
-                     (db_ih, 4 * H), (db_hh, 4 * H)):
+        G = (3 if gru else 4) * H
+        for t, n in ((dw_ih_g, 4 * H * D), (dw_ih, G * D), (dw_hh_g, 4 * H * H), (dw_hh, G * H), (db_g, 4 * H),
+                     (db_ih, G), (db_hh, G)):
             if t.numel() != n or not t.is_contiguous():
-                raise ValueError("lstm_unpack_grads: gradient buffers do not match [4H, D] / [4H, H] / [4H]")
+                raise ValueError("lstm_unpack_grads: gradient buffers do not match [4H, D] / [4H, H] / [4H] "
+                                 "(torch layout: [G, D] / [G, H] / [G])")
         probs.append(L.LstmGradProblem(dw_ih_g.data_ptr(), dw_hh_g.data_ptr(), db_g.data_ptr(), dw_ih.data_ptr(),
                                        dw_hh.data_ptr(), db_ih.data_ptr(), db_hh.data_ptr(), dw_ih.shape[1], H))
+    name = "ppo_gru_unpack_grads" if gru else "ppo_lstm_unpack_grads"
     for i in range(0, len(probs), L.MAX_LSTM_PROBLEMS):
         part = probs[i:i + L.MAX_LSTM_PROBLEMS]
-        L.call("ppo_lstm_unpack_grads", L.array(L.LstmGradProblem, part), len(part), _stream())
+        L.call(name, L.array(L.LstmGradProblem, part), len(part), _stream())
