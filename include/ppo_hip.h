@@ -437,6 +437,34 @@ int ppo_adam_step_static(float* params, float* grads, float* exp_avg, float* exp
                          int32_t num_groups, double max_grad_norm, double beta1, double beta2, double eps, double bc1,
                          double bc2_sqrt, ppo_device_state* state, ppo_stream_t stream);
 
+/* The optimisers upstream resolves by name (rsl_rl/utils/utils.py:71-96, constructed at rsl_rl/algorithms/ppo.py:99-102
+ * with the learning rate only, so every other hyperparameter is torch's default), each with the same per-group clip
+ * and in torch's single-tensor fp32 order:
+ *   PPO_OPTIM_ADAM     ppo_adam_step's update (state0 = exp_avg, state1 = exp_avg_sq);
+ *   PPO_OPTIM_ADAMW    p = p * fl(1 - lr * weight_decay), then Adam's update (torch.optim.AdamW, weight_decay 1e-2);
+ *   PPO_OPTIM_SGD      p = p + g' * (-lr) as one fused multiply-add (torch.optim.SGD without momentum; no state);
+ *   PPO_OPTIM_RMSPROP  sq = sq * alpha + ((1 - alpha) g') g';  p = p + ((-lr) g') / (sqrt(sq) + eps)
+ *                      (torch.optim.RMSprop, alpha 0.99, eps 1e-8, no momentum, not centred; state0 = square_avg).
+ * norm_partials != NULL: the group norms from ppo_linear_bwd_dw_norm's partial rows (as ppo_adam_step_prenorm, one
+ * launch); else from a pass over the gradients into workspace (ppo_adam_workspace_bytes).  Up to
+ * PPO_MAX_PARAM_MIRRORS mirrored parameters either way.  bc1 / bc2_sqrt: Adam and AdamW only (ignored otherwise). */
+#define PPO_OPTIM_ADAM 0
+#define PPO_OPTIM_ADAMW 1
+#define PPO_OPTIM_SGD 2
+#define PPO_OPTIM_RMSPROP 3
+typedef struct ppo_optim_config {
+  int32_t kind;        /* PPO_OPTIM_* */
+  int32_t reserved;
+  double beta1, beta2; /* Adam / AdamW */
+  double eps;          /* Adam / AdamW / RMSprop */
+  double weight_decay; /* AdamW */
+  double alpha;        /* RMSprop */
+} ppo_optim_config;
+int ppo_optim_step(float* params, float* grads, float* state0, float* state1, const int64_t* group_begin,
+                   int32_t num_groups, double max_grad_norm, const ppo_optim_config* config, double bc1,
+                   double bc2_sqrt, ppo_device_state* state, const double* norm_partials, void* workspace,
+                   size_t workspace_bytes, const ppo_param_mirror* mirrors, int32_t num_mirrors, ppo_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------------------------
  * A15  LSTM / GRU of the recurrent models (torch nn.LSTM: gates i, f, g, o; torch nn.GRU: gates r, z, n; one layer
  * per call, stacked layers call again on the h of the layer below): rsl_rl/modules/rnn.py:22-86,

@@ -646,6 +646,16 @@ def adaptive_lr(kl_mean: torch.Tensor, learning_rate: float, desired_kl: float) 
 # ----------------------------------------------------------------------------------------------------------------------
 
 
+def resolve_optimizer(name: str):
+    """rsl_rl/utils/utils.py:71-96: the torch optimiser class of a name (adam, adamw, sgd, rmsprop; any case)."""
+    table = {"adam": torch.optim.Adam, "adamw": torch.optim.AdamW, "sgd": torch.optim.SGD,
+             "rmsprop": torch.optim.RMSprop}
+    name = name.lower()
+    if name not in table:
+        raise ValueError(f"Invalid optimizer '{name}'. Valid optimizers are: {list(table.keys())}")
+    return table[name]
+
+
 class PPO:
     """rsl_rl/algorithms/ppo.py:27-465 on one CPU process (no RND, no symmetry, no multi-GPU)."""
 
@@ -659,13 +669,11 @@ class PPO:
                  grad_reduce_bucket_mb: float = 25) -> None:
         if rnd_cfg or symmetry_cfg or multi_gpu_cfg is not None:
             raise NotImplementedError("RND, symmetry and multi-GPU are outside this oracle")
-        if optimizer.lower() != "adam":
-            raise NotImplementedError("the PPO path is checked with Adam only")
         self.device = "cpu"
         self.actor = actor
         self.critic = critic
-        self.optimizer = torch.optim.Adam(list(dict.fromkeys(chain(actor.parameters(), critic.parameters()))),
-                                          lr=learning_rate)
+        self.optimizer = resolve_optimizer(optimizer)(
+            list(dict.fromkeys(chain(actor.parameters(), critic.parameters()))), lr=learning_rate)
         self.storage = storage
         self.transition = Transition()
         self.clip_param = clip_param

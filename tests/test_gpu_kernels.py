@@ -1010,6 +1010,78 @@ def test_adam_prenorm_mirror_matches_prenorm(cuda):
             assert torch.isnan(d[:, c:]).all(), "columns past cols written"
 
 
+@pytest.mark.parametrize("name", ["adam", "adamw", "sgd", "rmsprop"])
+@pytest.mark.parametrize("aligned,prenorm", [(False, False), (True, False), (True, True)])
+def test_optim_step_matches_torch(cuda, name, aligned, prenorm):
+    """ppo_optim_step against torch's own optimiser of that name with its defaults (rsl_rl/utils/utils.py:71-96;
+    upstream passes the learning rate only), after clip_grad_norm_ per group, over learning rates the adaptive
+    schedule could set: parameters, state and the clipped gradients to 1e-6.  Adam through ppo_optim_step equals
+    ppo_adam_step bit for bit.  With prenorm the group norms come from partial rows summing to the same squares."""
+    ops = _ops()
+    from tt_rsl_rl_amd import _lib as L
+
+    torch.manual_seed(31)
+    shapes_a = [(32,) if aligned else (29,), (256, 96), (256,), (128, 256)]
+    shapes_c = [(256, 99), (256,), (1, 128), (4,) if aligned else (1,)]
+    pa = [torch.nn.Parameter(torch.randn(s) * 0.1) for s in shapes_a]
+    pc = [torch.nn.Parameter(torch.randn(s) * 0.1) for s in shapes_c]
+    cls = {"adam": torch.optim.Adam, "adamw": torch.optim.AdamW, "sgd": torch.optim.SGD,
+           "rmsprop": torch.optim.RMSprop}[name]
+    opt = cls(pa + pc, lr=1e-3)
+    d = opt.defaults
+    kind = L.OPTIMIZERS[name]
+    cfg = L.OptimConfig(kind=kind, beta1=d.get("betas", (0.9, 0.999))[0], beta2=d.get("betas", (0.9, 0.999))[1],
+                        eps=d.get("eps", 1e-8), weight_decay=d.get("weight_decay", 0.0), alpha=d.get("alpha", 0.0))
+    flat = torch.cat([p.detach().reshape(-1) for p in pa + pc]).to(cuda)
+    n_a = sum(p.numel() for p in pa)
+    grad = torch.zeros_like(flat)
+    s0, s1 = torch.zeros_like(flat), torch.zeros_like(flat)
+    twin = [flat.clone(), grad.clone(), s0.clone(), s1.clone()]  # ppo_adam_step on the same inputs (Adam only)
+    gb = torch.tensor([0, n_a, flat.numel()], dtype=torch.int64)
+    state = ops.new_device_state(1e-3, cuda)
+    ws = ops.Workspace(cuda)
+    partials = ops.grad_norm_partials(cuda)
+    lrs = [1e-3, 6.7e-4, 2e-3, 1e-5, 1e-2, 3e-3]
+    for step, lr in enumerate(lrs, start=1):
+        scale = 10.0 if step % 3 == 0 else 0.01  # both sides of the clip threshold
+        for p in pa + pc:
+            p.grad = torch.randn_like(p) * scale
+        grad.copy_(torch.cat([p.grad.reshape(-1) for p in pa + pc]).to(cuda))
+        twin[1].copy_(grad)
+        pre = None
+        if prenorm:  # each group's squared norm spread over the partial rows (in halves: exact in fp64)
+            g64 = grad.double()
+            partials.zero_()
+            for g in (0, 1):
+                sq = float((g64[gb[g]:gb[g + 1]] ** 2).sum())
+                partials[0, g], partials[1, g] = sq / 2, sq - sq / 2
+            pre = partials
+        for group in opt.param_groups:
+            group["lr"] = lr
+        torch.nn.utils.clip_grad_norm_(pa, 1.0)
+        torch.nn.utils.clip_grad_norm_(pc, 1.0)
+        opt.step()
+        bc1, bc2 = 1 - 0.9 ** step, (1 - 0.999 ** step) ** 0.5
+        ops.reset_device_state(state, lr)
+        ops.optim_step(cfg, flat, grad, None if name == "sgd" else s0, s1 if name in ("adam", "adamw") else None, gb,
+                       1.0, bc1, bc2, state, ws, prenorm=pre)
+        ref = torch.cat([p.detach().reshape(-1) for p in pa + pc])
+        assert rel_err(flat, ref) < 1e-6, step
+        ref_g = torch.cat([p.grad.reshape(-1) for p in pa + pc])
+        assert rel_err(grad, ref_g) < 1e-6, "clipped gradients are left in the gradient buffer like upstream"
+        keys = {"adam": ("exp_avg", "exp_avg_sq"), "adamw": ("exp_avg", "exp_avg_sq"), "sgd": (),
+                "rmsprop": ("square_avg",)}[name]
+        for buf, key in zip((s0, s1), keys):
+            assert rel_err(buf, torch.cat([opt.state[p][key].reshape(-1) for p in pa + pc])) < 1e-6, (step, key)
+        if name == "sgd":
+            assert not any(opt.state[p] for p in pa + pc) and float(s0.abs().sum()) == 0.0
+        if name == "adam":
+            st = ops.new_device_state(lr, cuda)
+            ops.adam_step(*twin, gb, 1.0, 0.9, 0.999, 1e-8, bc1, bc2, st, ws, prenorm=pre)
+            for x, y in zip(twin, (flat, grad, s0, s1)):
+                assert torch.equal(x, y), step
+
+
 def test_adam_first_step_moves_by_lr(cuda):
     """tests/algorithms/test_ppo.py:492-505: the first Adam step moves every parameter by lr."""
     ops = _ops()

@@ -118,6 +118,14 @@ CASES = {
     # two stacked LSTM layers (layer 1 reads layer 0's h): the hidden size of the workload and a small one
     "lstm256x2_512": (_lstm(512, 24, 256, [256, 128], layers=2), {"carry_state": True}),
     "lstm32x3_ragged": (_lstm(200, 10, 32, [32, 16], layers=3), {"num_mini_batches": 3, "carry_state": True}),
+    # the other optimisers upstream resolves (rsl_rl/utils/utils.py:71-96), each with torch's defaults
+    "humanoid_small_adamw": (R.scaled(R.WORKLOADS["humanoid"], num_envs=128, steps=8, hidden_dims=[64, 32]),
+                             {"optimizer": "adamw"}),
+    "flat48_small_sgd": (R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[128, 64, 32]),
+                         {"optimizer": "sgd", "learning_rate": 1e-2}),
+    "rough235_small_rmsprop": (R.scaled(R.WORKLOADS["rough235"], num_envs=128, steps=8, hidden_dims=[64, 32]),
+                               {"optimizer": "RMSprop", "schedule": "fixed", "learning_rate": 3e-4}),
+    "lstm64_adamw": (_lstm(128, 16, 64, [64, 32]), {"optimizer": "adamw"}),
     # GRU (rsl_rl/modules/rnn.py:29): the workload's shape, a normalised small one, two layers on ragged slices
     "gru256_512": (_lstm(512, 24, 256, [256, 128], rnn_type="gru"), {"carry_state": True}),
     "gru64_norm": (_lstm(128, 16, 64, [64, 32], rnn_type="gru", obs_normalization=True), {}),
@@ -280,18 +288,20 @@ def test_update_matches_oracle(name, capsys):
                 assert not p_h.requires_grad and torch.equal(p_h.detach().cpu(), p_s.detach()), name_p
                 assert p_s not in shadow.optimizer.state and p_h not in hip.optimizer.state, name_p
                 continue
-            s_s, s_h = shadow.optimizer.state[p_s], hip.optimizer.state[p_h]
-            m1 = rel_err(s_h["exp_avg"], s_s["exp_avg"], 1e-12)
-            m2 = rel_err(s_h["exp_avg_sq"], s_s["exp_avg_sq"], 1e-20)
-            tensors[f"{tag}.{name_p}"] = {"vs_branch_matched": err, "vs_literal_oracle": rel_err(p_h, p_o),
-                                          "oracle_spread_lp64_vs_oracle": rel_err(p_64, p_o),
-                                          "exp_avg_vs_branch_matched": m1, "exp_avg_sq_vs_branch_matched": m2}
+            # the optimiser's state (Adam / AdamW: exp_avg, exp_avg_sq; RMSprop: square_avg; SGD: none), same keys
+            s_s, s_h = shadow.optimizer.state.get(p_s, {}), hip.optimizer.state.get(p_h, {})
+            assert set(s_h) == set(s_s), (name_p, set(s_h), set(s_s))
+            rec = {"vs_branch_matched": err, "vs_literal_oracle": rel_err(p_h, p_o),
+                   "oracle_spread_lp64_vs_oracle": rel_err(p_64, p_o)}
+            for key in sorted(k for k in s_s if k != "step"):
+                rec[f"{key}_vs_branch_matched"] = rel_err(s_h[key], s_s[key], _STATE_FLOOR.get(key, 1e-20))
+                assert rec[f"{key}_vs_branch_matched"] < MOMENT_BAR, (name_p, key)
+            tensors[f"{tag}.{name_p}"] = rec
             print(f"{tag}.{name_p:28s} vs branch-matched oracle {err:.2e}   vs oracle {rel_err(p_h, p_o):.2e}   "
                   f"(oracle's own spread: lp64 vs oracle {rel_err(p_64, p_o):.2e})")
             assert err < PARAM_BAR, name_p
-            assert m1 < MOMENT_BAR, name_p
-            assert m2 < MOMENT_BAR, name_p
-            assert float(s_h["step"]) == float(s_s["step"])
+            if "step" in s_s:
+                assert float(s_h["step"]) == float(s_s["step"])
     # function space
     p_h, p_s, p_o, p_64 = param_dict(hip), param_dict(shadow), param_dict(ora), param_dict(lp64)
     d_hs = function_deviation(p_h, p_s, p0, ora, ev)
@@ -485,38 +495,46 @@ def test_failed_update_is_rolled_back():
         _assert_same_state(a, b, f"update {rep} after the failure")
 
 
-def _adam_state(opt, p):
+# denominators' floor of the state comparisons: first moments (gradient scale), second moments (squared)
+_STATE_FLOOR = {"exp_avg": 1e-12}
+
+
+def _opt_state(opt, p) -> tuple[dict, int]:
+    """A parameter's optimiser state tensors (Adam / AdamW: exp_avg, exp_avg_sq; RMSprop: square_avg; SGD: none)
+    and its step count (0 without state)."""
     st = opt.state.get(p, {})
-    if "exp_avg" not in st:
-        return torch.zeros_like(p), torch.zeros_like(p), 0
-    return st["exp_avg"].clone(), st["exp_avg_sq"].clone(), int(st["step"])
+    tensors = {k: v.detach().clone() for k, v in st.items() if k != "step" and torch.is_tensor(v)}
+    return tensors, int(st["step"]) if "step" in st else 0
 
 
 def _snapshot(alg) -> dict:
     params = list(chain(alg.actor.parameters(), alg.critic.parameters()))
-    moments = [_adam_state(alg.optimizer, p) for p in params]
-    # (the optimiser's step count: a parameter without a gradient -- learn_std=False -- has no state and no count)
+    states = [_opt_state(alg.optimizer, p) for p in params]
+    # (the optimiser's step count: a parameter without a gradient -- learn_std=False -- has no state and no count;
+    # SGD keeps none at all, and only Adam's bias corrections read the count)
     return {"params": [p.detach().clone() for p in params], "lr": alg.learning_rate,
-            "exp_avg": [m[0] for m in moments], "exp_avg_sq": [m[1] for m in moments],
-            "step": max(m[2] for m in moments)}
+            "state": [st for st, _ in states], "step": max(n for _, n in states)}
 
 
 def _load_oracle_state(ora, snap: dict) -> None:
-    """Put the oracle back into a recorded state (parameters, Adam moments and step, learning rate)."""
+    """Put the oracle back into a recorded state (parameters, optimiser state and step, learning rate)."""
     params = list(chain(ora.actor.parameters(), ora.critic.parameters()))
     with torch.no_grad():
         for p, v in zip(params, snap["params"]):
             p.copy_(v)
     ora.optimizer.state.clear()
-    if snap["step"] > 0:
-        for p, m1, m2 in zip(params, snap["exp_avg"], snap["exp_avg_sq"]):
-            if not p.requires_grad:
-                continue
-            ora.optimizer.state[p] = {"step": torch.tensor(float(snap["step"])), "exp_avg": m1.clone(),
-                                      "exp_avg_sq": m2.clone()}
+    for p, st in zip(params, snap["state"]):
+        if st and p.requires_grad:
+            ora.optimizer.state[p] = {"step": torch.tensor(float(snap["step"])), **{k: v.clone() for k, v in st.items()}}
     ora.learning_rate = snap["lr"]
     for g in ora.optimizer.param_groups:
         g["lr"] = snap["lr"]
+
+
+def _flat_state_matches(hip, p, want: dict) -> dict[str, float]:
+    """The GPU's flat optimiser state of p against a recorded state (zero where the optimiser kept none)."""
+    return {k: rel_err(view, want[k] if k in want else torch.zeros_like(view), _STATE_FLOOR.get(k, 1e-20))
+            for k, view in hip._state_views(p).items()}
 
 
 @pytest.mark.parametrize("name", _cases())
@@ -550,10 +568,10 @@ def test_update_steps_teacher_forced(name, capsys):
     for k, (a, b) in enumerate(zip(pre, post)):
         batch = next(batches)
         with torch.no_grad():
-            for p, v, m1, m2 in zip(params, a["params"], a["exp_avg"], a["exp_avg_sq"]):
+            for p, v, st in zip(params, a["params"], a["state"]):
                 p.copy_(v.to(hip.device))
-                hip.flat.exp_avg_view(p).copy_(m1.to(hip.device))
-                hip.flat.exp_avg_sq_view(p).copy_(m2.to(hip.device))
+                for key, view in hip._state_views(p).items():
+                    view.copy_(st[key].to(hip.device)) if key in st else view.zero_()
         ops.reset_device_state(hip.device_state, a["lr"])
         r0, r1 = engine.minibatch_rows(k % M)
         engine.minibatch(r0, r1, a["step"] + 1)
@@ -587,12 +605,12 @@ def test_update_steps_teacher_forced(name, capsys):
             b = _snapshot(ora)
             replayed += 1
         step_worst = 0.0
-        for n, p, v, m1, m2 in zip(names, params, b["params"], b["exp_avg"], b["exp_avg_sq"]):
+        for n, p, v, st in zip(names, params, b["params"], b["state"]):
             err = rel_err(p, v)
             step_worst = max(step_worst, err)
             assert err < PARAM_BAR, (k, n, err)
-            assert rel_err(hip.flat.exp_avg_view(p), m1, 1e-12) < MOMENT_BAR, (k, n)
-            assert rel_err(hip.flat.exp_avg_sq_view(p), m2, 1e-20) < MOMENT_BAR, (k, n)
+            for key, e in _flat_state_matches(hip, p, st).items():
+                assert e < MOMENT_BAR, (k, n, key, e)
         worst = max(worst, step_worst)
         per_step.append({"step": k, "worst_param_err": step_worst, "ratio_gap": gap.get("surrogate"),
                          "value_gap": gap.get("value"),

@@ -167,6 +167,13 @@ def test_argument_validation_reports_errors_without_a_gpu():
     grad = _lib.LstmGradProblem(8, 8, 8, 8, 8, 8, 8, 48, 6)
     with pytest.raises(ValueError, match="ppo_gru_unpack_grads: problem 0 sizes"):
         _lib.call("ppo_gru_unpack_grads", ctypes.byref(grad), 1, None)
+    # the optimiser step: a known kind and a config
+    cfg = _lib.OptimConfig(kind=7)
+    with pytest.raises(ValueError, match="kind=7"):
+        _lib.call("ppo_optim_step", 16, 16, 16, 16, None, 1, 1.0, ctypes.byref(cfg), 1.0, 1.0, 16, 16, None, 0, None,
+                  0, None)
+    with pytest.raises(ValueError, match="null config"):
+        _lib.call("ppo_optim_step", 16, 16, 16, 16, None, 1, 1.0, None, 1.0, 1.0, 16, 16, None, 0, None, 0, None)
     # the cell type: LSTM (0) or GRU (1), one type per call
     bad = _lib.LstmSeqProblem(hidden=256, cell=2)
     with pytest.raises(ValueError, match="cell=2"):

@@ -79,6 +79,15 @@ class ParamMirror(C.Structure):
     _fields_ = [("begin", i64), ("rows", i32), ("cols", i32), ("dst", C.c_void_p), ("ld_dst", i64)]
 
 
+class OptimConfig(C.Structure):
+    _fields_ = [("kind", i32), ("reserved", i32), ("beta1", C.c_double), ("beta2", C.c_double), ("eps", C.c_double),
+                ("weight_decay", C.c_double), ("alpha", C.c_double)]
+
+
+OPTIM_ADAM, OPTIM_ADAMW, OPTIM_SGD, OPTIM_RMSPROP = 0, 1, 2, 3
+OPTIMIZERS = {"adam": OPTIM_ADAM, "adamw": OPTIM_ADAMW, "sgd": OPTIM_SGD, "rmsprop": OPTIM_RMSPROP}
+
+
 class ColumnBlock(C.Structure):
     _fields_ = [("src", C.c_void_p), ("stride", i64), ("width", i32), ("reserved", i32)]
 
@@ -191,6 +200,9 @@ _SIGNATURES = [
     ("ppo_adam_step_prenorm_mirror", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.c_double,
                                                C.c_double, C.c_double, C.c_double, C.c_double, C.c_void_p, C.c_void_p,
                                                C.c_void_p, i32, C.c_void_p]),
+    ("ppo_optim_step", C.c_int, [f32p, f32p, f32p, f32p, C.c_void_p, i32, C.c_double, C.POINTER(OptimConfig),
+                                 C.c_double, C.c_double, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
+                                 i32, C.c_void_p]),
 ]
 
 EXPORTED_SYMBOLS = [name for name, _, _ in _SIGNATURES]

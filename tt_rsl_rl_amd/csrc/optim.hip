@@ -1,6 +1,6 @@
 // A12 + A13: per-group gradient-norm clipping (torch.nn.utils.clip_grad_norm_, rsl_rl/algorithms/ppo.py:309-310)
 // fused with Adam (torch.optim.Adam, single-tensor path, ppo.py:311) over flat parameter / gradient / moment
-// buffers.  ppo_adam_step, two launches:
+// buffers; ppo_optim_step runs the same launches with the other optimisers upstream resolves (AdamW, SGD, RMSprop).  ppo_adam_step, two launches:
 //   1. sum of squares of the gradient, one fp64 partial per 1024-element chunk (chunks never straddle groups);
 //   2. every block re-reduces its group's partials in the same fixed order (so all blocks agree bit for bit),
 //      derives the clip coefficient and streams p, g, m, v once: 16 B read + 12 B written per parameter
@@ -102,6 +102,8 @@ __device__ __forceinline__ void mirror_store(const MirrorTable& mt, int64_t i, f
 struct AdamScalars {
   float max_norm, w1, b2, c2, eps, bc2_sqrt;
   double bc1;
+  double weight_decay;  // AdamW: decoupled decay, p *= 1 - lr * weight_decay before the step
+  float alpha, c_alpha;  // RMSprop: square_avg = alpha square_avg + (1 - alpha) g^2
 };
 
 // One parameter's update in torch's fp32 operation order.
@@ -115,14 +117,36 @@ __device__ __forceinline__ void adam_elem(float& p, float& g, float& m, float& v
   p = p + (neg_step * m) / denom;
 }
 
+// The other optimisers upstream resolves (rsl_rl/utils/utils.py:71-96), torch's single-tensor update with the
+// defaults upstream leaves them (torch/optim/{adamw,sgd,rmsprop}.py): AdamW = p *= fl(1 - lr wd) (Python double,
+// rounded once), then Adam's update; SGD (no momentum, no decay) p = p - lr g (torch's vectorised add: one fused
+// multiply-add); RMSprop (no momentum, not centred) square_avg = square_avg alpha + (1 - alpha) g g, p = p - lr g /
+// (sqrt(square_avg) + eps).  m holds square_avg for RMSprop; SGD keeps no state.
+__device__ __forceinline__ void sgd_elem(float& p, float& g, float coef, float neg_lr) {
+  g = g * coef;
+  p = fmaf(g, neg_lr, p);
+}
+
+__device__ __forceinline__ void rmsprop_elem(float& p, float& g, float& sa, float coef, float neg_lr,
+                                             const AdamScalars& s) {
+  g = g * coef;
+  sa = sa * s.alpha;
+  sa = sa + (s.c_alpha * g) * g;
+  const float avg = sqrtf(sa) + s.eps;
+  p = p + (neg_lr * g) / avg;
+}
+
 // PRE: the group's squared norm is the sum of column g of the PPO_DW_NORM_BLOCKS partial rows the weight-grad reduce
-// wrote (ppo_adam_step_prenorm); else the sum of the group's per-chunk partials from grad_sqnorm_kernel.
-template <bool VEC, bool PRE>
+// wrote (ppo_adam_step_prenorm); else the sum of the group's per-chunk partials from grad_sqnorm_kernel.  KIND: the
+// update rule (PPO_OPTIM_*); the Adam instantiations are the plain Adam kernel.
+template <bool VEC, bool PRE, int KIND = PPO_OPTIM_ADAM>
 __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ params, float* __restrict__ grads,
                                                             float* __restrict__ exp_avg,
                                                             float* __restrict__ exp_avg_sq, GroupTable t,
                                                             AdamScalars s, const double* __restrict__ partials,
                                                             ppo_device_state* __restrict__ state, MirrorTable mt) {
+  constexpr bool kAdam = KIND == PPO_OPTIM_ADAM || KIND == PPO_OPTIM_ADAMW;
+  constexpr bool kState0 = KIND != PPO_OPTIM_SGD, kState1 = kAdam;
   __shared__ double red[kAdamThreads / 64];
   const int chunk = blockIdx.x;
   const int g = group_of_chunk(t, chunk);
@@ -136,11 +160,25 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
   const float total = static_cast<float>(sqrt(sq));
   const float coef = fminf(s.max_norm / (total + 1e-6f), 1.0f);
   const double lr = state->learning_rate;
-  const float neg_step = static_cast<float>(-(lr / s.bc1));
+  const float neg_step = static_cast<float>(kAdam ? -(lr / s.bc1) : -lr);
+  const float decay = static_cast<float>(1.0 - lr * s.weight_decay);
   if (chunk == t.first_chunk[g] && threadIdx.x == 0 && g < 4) {
     state->total_norm[g] = total;
     state->clip_coef[g] = coef;
   }
+  // one element: p, its gradient and the state this rule keeps
+  auto update = [&](float& p, float& gr, float& m, float& v) {
+    if constexpr (KIND == PPO_OPTIM_ADAM) {
+      adam_elem(p, gr, m, v, coef, neg_step, s);
+    } else if constexpr (KIND == PPO_OPTIM_ADAMW) {
+      p = p * decay;
+      adam_elem(p, gr, m, v, coef, neg_step, s);
+    } else if constexpr (KIND == PPO_OPTIM_SGD) {
+      sgd_elem(p, gr, coef, neg_step);
+    } else {
+      rmsprop_elem(p, gr, m, coef, neg_step, s);
+    }
+  };
   const int64_t lo = t.begin[g] + static_cast<int64_t>(chunk - t.first_chunk[g]) * kChunk;
   const int64_t hi = min(lo + kChunk, t.begin[g + 1]);
   if constexpr (VEC) {
@@ -148,16 +186,17 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
     if (i < hi) {
       float4 p = *reinterpret_cast<const float4*>(params + i);
       float4 gr = *reinterpret_cast<const float4*>(grads + i);
-      float4 m = *reinterpret_cast<const float4*>(exp_avg + i);
-      float4 v = *reinterpret_cast<const float4*>(exp_avg_sq + i);
-      adam_elem(p.x, gr.x, m.x, v.x, coef, neg_step, s);
-      adam_elem(p.y, gr.y, m.y, v.y, coef, neg_step, s);
-      adam_elem(p.z, gr.z, m.z, v.z, coef, neg_step, s);
-      adam_elem(p.w, gr.w, m.w, v.w, coef, neg_step, s);
+      float4 m = {0.0f, 0.0f, 0.0f, 0.0f}, v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (kState0) m = *reinterpret_cast<const float4*>(exp_avg + i);
+      if constexpr (kState1) v = *reinterpret_cast<const float4*>(exp_avg_sq + i);
+      update(p.x, gr.x, m.x, v.x);
+      update(p.y, gr.y, m.y, v.y);
+      update(p.z, gr.z, m.z, v.z);
+      update(p.w, gr.w, m.w, v.w);
       *reinterpret_cast<float4*>(params + i) = p;
       *reinterpret_cast<float4*>(grads + i) = gr;
-      *reinterpret_cast<float4*>(exp_avg + i) = m;
-      *reinterpret_cast<float4*>(exp_avg_sq + i) = v;
+      if constexpr (kState0) *reinterpret_cast<float4*>(exp_avg + i) = m;
+      if constexpr (kState1) *reinterpret_cast<float4*>(exp_avg_sq + i) = v;
       if (mt.count > 0) {  // (a float4 may straddle a mirror's first or last element: per element)
         mirror_store(mt, i, p.x);
         mirror_store(mt, i + 1, p.y);
@@ -167,12 +206,14 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(float* __restrict__ 
     }
   } else {
     for (int64_t i = lo + threadIdx.x; i < hi; i += kAdamThreads) {
-      float p = params[i], gr = grads[i], m = exp_avg[i], v = exp_avg_sq[i];
-      adam_elem(p, gr, m, v, coef, neg_step, s);
+      float p = params[i], gr = grads[i], m = 0.0f, v = 0.0f;
+      if constexpr (kState0) m = exp_avg[i];
+      if constexpr (kState1) v = exp_avg_sq[i];
+      update(p, gr, m, v);
       params[i] = p;
       grads[i] = gr;
-      exp_avg[i] = m;
-      exp_avg_sq[i] = v;
+      if constexpr (kState0) exp_avg[i] = m;
+      if constexpr (kState1) exp_avg_sq[i] = v;
       if (mt.count > 0) mirror_store(mt, i, p);
     }
   }
@@ -226,12 +267,42 @@ int static_scratch(double** out) {
 
 // prenorm != nullptr: one launch taking the norms from the weight-grad reduce's partial rows; else the per-chunk
 // norm pass into `workspace`, then the update.
+// The rule-specific hyperparameters of ppo_optim_step (Adam: kind only).
+struct OptimRule {
+  int kind = PPO_OPTIM_ADAM;
+  double weight_decay = 0.0, alpha = 0.0;
+};
+
+template <int KIND>
+void launch_update(bool vec, bool pre, int chunks, hipStream_t st, float* params, float* grads, float* s0, float* s1,
+                   const GroupTable& t, const AdamScalars& s, const double* partials, ppo_device_state* state,
+                   const MirrorTable& mt) {
+  if (pre) {
+    if (vec) {
+      hipLaunchKernelGGL((adam_kernel<true, true, KIND>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, s0,
+                         s1, t, s, partials, state, mt);
+    } else {
+      hipLaunchKernelGGL((adam_kernel<false, true, KIND>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads,
+                         s0, s1, t, s, partials, state, mt);
+    }
+  } else if (vec) {
+    hipLaunchKernelGGL((adam_kernel<true, false, KIND>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, s0,
+                       s1, t, s, partials, state, mt);
+  } else {
+    hipLaunchKernelGGL((adam_kernel<false, false, KIND>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, s0,
+                       s1, t, s, partials, state, mt);
+  }
+}
+
 int adam_step(const char* who, float* params, float* grads, float* exp_avg, float* exp_avg_sq,
               const int64_t* group_begin, int32_t num_groups, double max_grad_norm, double beta1, double beta2,
               double eps, double bc1, double bc2_sqrt, ppo_device_state* state, void* workspace,
               size_t workspace_bytes, const double* prenorm, ppo_stream_t stream,
-              const ppo_param_mirror* mirrors = nullptr, int num_mirrors = 0) {
-  PPO_REQUIRE(params && grads && exp_avg && exp_avg_sq && state, "%s: null pointer", who);
+              const ppo_param_mirror* mirrors = nullptr, int num_mirrors = 0, const OptimRule& rule = OptimRule{}) {
+  const bool adam = rule.kind == PPO_OPTIM_ADAM || rule.kind == PPO_OPTIM_ADAMW;
+  PPO_REQUIRE(rule.kind >= PPO_OPTIM_ADAM && rule.kind <= PPO_OPTIM_RMSPROP, "%s: optimizer kind %d", who, rule.kind);
+  PPO_REQUIRE(params && grads && state && (rule.kind == PPO_OPTIM_SGD || exp_avg) && (!adam || exp_avg_sq),
+              "%s: null pointer", who);
   GroupTable t;
   int chunks = 0;
   int rc = build_table(group_begin, num_groups, t, chunks);
@@ -260,45 +331,53 @@ int adam_step(const char* who, float* params, float* grads, float* exp_avg, floa
     PPO_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace too small (%zu < %zu)", who,
                 workspace_bytes, need);
   }
-  PPO_REQUIRE(bc1 > 0.0 && bc2_sqrt > 0.0, "%s: bias corrections must be positive", who);
-  AdamScalars s;
+  PPO_REQUIRE(!adam || (bc1 > 0.0 && bc2_sqrt > 0.0), "%s: bias corrections must be positive", who);
+  AdamScalars s{};
   // torch passes max_norm, 1 - beta1, beta2, 1 - beta2 and eps as Python doubles that the fp32 kernels round once
   s.max_norm = static_cast<float>(max_grad_norm);
   s.w1 = static_cast<float>(1.0 - beta1);
   s.b2 = static_cast<float>(beta2);
   s.c2 = static_cast<float>(1.0 - beta2);
   s.eps = static_cast<float>(eps);
-  s.bc1 = bc1;
-  s.bc2_sqrt = static_cast<float>(bc2_sqrt);
+  s.bc1 = adam ? bc1 : 1.0;
+  s.bc2_sqrt = static_cast<float>(adam ? bc2_sqrt : 1.0);
+  s.weight_decay = rule.kind == PPO_OPTIM_ADAMW ? rule.weight_decay : 0.0;
+  s.alpha = static_cast<float>(rule.alpha);
+  s.c_alpha = static_cast<float>(1.0 - rule.alpha);
   hipStream_t st = static_cast<hipStream_t>(stream);
   bool vec = true;
   const void* bufs[] = {params, grads, exp_avg, exp_avg_sq};
   for (const void* b : bufs) vec = vec && reinterpret_cast<uintptr_t>(b) % 16 == 0;
   for (int g = 0; g <= num_groups; ++g) vec = vec && group_begin[g] % 4 == 0;
-  if (prenorm != nullptr) {
+  const double* partials = prenorm;
+  if (prenorm == nullptr) {
+    double* ws = static_cast<double*>(workspace);
     if (vec) {
-      hipLaunchKernelGGL((adam_kernel<true, true>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
-                         exp_avg_sq, t, s, prenorm, state, mt);
+      hipLaunchKernelGGL(grad_sqnorm_kernel<true>, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, ws);
     } else {
-      hipLaunchKernelGGL((adam_kernel<false, true>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads,
-                         exp_avg, exp_avg_sq, t, s, prenorm, state, mt);
+      hipLaunchKernelGGL(grad_sqnorm_kernel<false>, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, ws);
     }
-    return check_launch("adam_kernel");
+    rc = check_launch("grad_sqnorm_kernel");
+    if (rc != PPO_OK) return rc;
+    partials = ws;
   }
-  double* partials = static_cast<double*>(workspace);
-  if (vec) {
-    hipLaunchKernelGGL(grad_sqnorm_kernel<true>, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, partials);
-  } else {
-    hipLaunchKernelGGL(grad_sqnorm_kernel<false>, dim3(chunks), dim3(kAdamThreads), 0, st, grads, t, partials);
-  }
-  rc = check_launch("grad_sqnorm_kernel");
-  if (rc != PPO_OK) return rc;
-  if (vec) {
-    hipLaunchKernelGGL((adam_kernel<true, false>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads, exp_avg,
-                       exp_avg_sq, t, s, partials, state, mt);
-  } else {
-    hipLaunchKernelGGL((adam_kernel<false, false>), dim3(chunks), dim3(kAdamThreads), 0, st, params, grads,
-                       exp_avg, exp_avg_sq, t, s, partials, state, mt);
+  const bool pre = prenorm != nullptr;
+  switch (rule.kind) {
+    case PPO_OPTIM_ADAMW:
+      launch_update<PPO_OPTIM_ADAMW>(vec, pre, chunks, st, params, grads, exp_avg, exp_avg_sq, t, s, partials, state,
+                                     mt);
+      break;
+    case PPO_OPTIM_SGD:
+      launch_update<PPO_OPTIM_SGD>(vec, pre, chunks, st, params, grads, exp_avg, exp_avg_sq, t, s, partials, state,
+                                   mt);
+      break;
+    case PPO_OPTIM_RMSPROP:
+      launch_update<PPO_OPTIM_RMSPROP>(vec, pre, chunks, st, params, grads, exp_avg, exp_avg_sq, t, s, partials,
+                                       state, mt);
+      break;
+    default:
+      launch_update<PPO_OPTIM_ADAM>(vec, pre, chunks, st, params, grads, exp_avg, exp_avg_sq, t, s, partials, state,
+                                    mt);
   }
   return check_launch("adam_kernel");
 }
@@ -357,4 +436,24 @@ extern "C" int ppo_adam_step_static(float* params, float* grads, float* exp_avg,
   return adam_step("ppo_adam_step_static", params, grads, exp_avg, exp_avg_sq, group_begin, num_groups,
                    max_grad_norm, beta1, beta2, eps, bc1, bc2_sqrt, state, ws,
                    sizeof(double) * PPO_ADAM_STATIC_SCRATCH_DOUBLES, nullptr, stream);
+}
+
+extern "C" int ppo_optim_step(float* params, float* grads, float* state0, float* state1, const int64_t* group_begin,
+                              int32_t num_groups, double max_grad_norm, const ppo_optim_config* config, double bc1,
+                              double bc2_sqrt, ppo_device_state* state, const double* norm_partials, void* workspace,
+                              size_t workspace_bytes, const ppo_param_mirror* mirrors, int32_t num_mirrors,
+                              ppo_stream_t stream) {
+  PPO_REQUIRE(config != nullptr, "ppo_optim_step: null config");
+  const ppo_optim_config& c = *config;
+  PPO_REQUIRE(c.kind >= PPO_OPTIM_ADAM && c.kind <= PPO_OPTIM_RMSPROP, "ppo_optim_step: kind=%d", c.kind);
+  PPO_REQUIRE(c.kind != PPO_OPTIM_RMSPROP || (c.alpha >= 0.0 && c.alpha <= 1.0), "ppo_optim_step: alpha=%g",
+              c.alpha);
+  PPO_REQUIRE(c.weight_decay >= 0.0, "ppo_optim_step: weight_decay=%g", c.weight_decay);
+  OptimRule rule;
+  rule.kind = c.kind;
+  rule.weight_decay = c.weight_decay;
+  rule.alpha = c.alpha;
+  return adam_step("ppo_optim_step", params, grads, state0, state1, group_begin, num_groups, max_grad_norm, c.beta1,
+                   c.beta2, c.eps, bc1, bc2_sqrt, state, workspace, workspace_bytes, norm_partials, stream, mirrors,
+                   num_mirrors, rule);
 }

@@ -274,6 +274,7 @@ class UpdateEngine:
         a = self.alg
         return (torch.cuda.current_stream(self.device).cuda_stream, a.clip_param, a.value_loss_coef, a.entropy_coef,
                 a.use_clipped_value_loss, a.desired_kl, a.schedule, a.max_grad_norm, tuple(a.betas), a.adam_eps,
+                a.optim_kind, a.optim_config.weight_decay, a.optim_config.alpha,
                 a.normalize_advantage_per_mini_batch, a.num_learning_epochs, self._storage_signature())
 
     def _storage_signature(self) -> tuple:
@@ -314,6 +315,9 @@ class UpdateEngine:
                 if name in ("ppo_adam_step", "ppo_adam_step_prenorm", "ppo_adam_step_prenorm_mirror"):
                     bc1, bc2_sqrt = self._bias_corrections(step)
                     args = args[:10] + (float(bc1), float(bc2_sqrt)) + args[12:]
+                elif name == "ppo_optim_step":
+                    bc1, bc2_sqrt = self._bias_corrections(step)
+                    args = args[:8] + (float(bc1), float(bc2_sqrt)) + args[10:]
                 L.check(getattr(lib, name)(*args), name)
 
     def gather(self, perm: torch.Tensor, row0: int = 0) -> None:
@@ -565,9 +569,15 @@ class UpdateEngine:
         f = alg.flat
         tm = self.timer
         tm.start("adam")
-        ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin, alg.max_grad_norm, b1, b2, alg.adam_eps,
-                      bc1, bc2_sqrt, alg.device_state, self.adam_ws, prenorm=prenorm,
-                      mirrors=self.w0_mirrors if prenorm is not None else None)
+        mirrors = self.w0_mirrors if prenorm is not None else None
+        if alg.optim_kind == L.OPTIM_ADAM:
+            ops.adam_step(f.param, f.grad, f.exp_avg, f.exp_avg_sq, f.group_begin, alg.max_grad_norm, b1, b2,
+                          alg.adam_eps, bc1, bc2_sqrt, alg.device_state, self.adam_ws, prenorm=prenorm, mirrors=mirrors)
+        else:  # AdamW / SGD / RMSprop: the same launches with their update rule
+            s0 = None if alg.optim_kind == L.OPTIM_SGD else f.exp_avg
+            s1 = f.exp_avg_sq if alg.optim_kind == L.OPTIM_ADAMW else None
+            ops.optim_step(alg.optim_config, f.param, f.grad, s0, s1, f.group_begin, alg.max_grad_norm, bc1, bc2_sqrt,
+                           alg.device_state, self.adam_ws, prenorm=prenorm, mirrors=mirrors)
         tm.stop("adam")
 
     def minibatch_rows(self, i: int) -> tuple[int, int]:

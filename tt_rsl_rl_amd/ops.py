@@ -569,6 +569,41 @@ def ppo_head(args: L.LossArgs, h_actor: torch.Tensor, w_actor: torch.Tensor, b_a
            _trace_rows(trace), _stream())
 
 
+def optim_step(config: "L.OptimConfig", params, grads, state0, state1, group_begin: torch.Tensor,
+               max_grad_norm: float, bc1: float, bc2_sqrt: float, state: torch.Tensor, ws: Workspace | None,
+               prenorm: torch.Tensor | None = None, mirrors: list[tuple] | None = None) -> None:
+    """Clip + the update of config.kind (L.OPTIM_*: Adam, AdamW, SGD, RMSprop) over the flat buffers
+    (ppo_optim_step): state0 / state1 are Adam's moments, RMSprop's square_avg (state1 unused), nothing for SGD (both
+    unused).  prenorm / mirrors as adam_step's."""
+    import ctypes
+
+    _dev(params, grads, state0, state1)
+    n = params.numel()
+    for t in (grads, state0, state1):
+        if t is not None and (t.numel() != n or not t.is_contiguous()):
+            raise ValueError("optim_step: flat buffers must be contiguous and equally long")
+    if group_begin.device.type != "cpu" or group_begin.dtype != torch.int64 or int(group_begin[-1]) != n:
+        raise ValueError("optim_step: group_begin is a host int64 tensor covering the flat buffer")
+    items = []
+    for begin, rows, cols, dst in mirrors or []:
+        _dev(dst)
+        ld = _row_major(dst, "mirror dst")
+        if dst.shape[0] < rows or dst.shape[1] < cols or begin < 0 or begin + rows * cols > n:
+            raise ValueError("optim_step: mirror outside the flat buffer or its destination")
+        items.append(L.ParamMirror(int(begin), int(rows), int(cols), dst.data_ptr(), ld))
+    buf = None
+    if prenorm is not None:
+        _dev(prenorm, dtype=torch.float64)
+        if tuple(prenorm.shape) != (L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS) or not prenorm.is_contiguous():
+            raise ValueError("optim_step: prenorm must be a contiguous [DW_NORM_BLOCKS, MAX_PARAM_GROUPS] fp64 tensor")
+    else:
+        buf = ws.get(L.load().ppo_adam_workspace_bytes(n))
+    L.call("ppo_optim_step", params.data_ptr(), grads.data_ptr(), _ptr(state0), _ptr(state1), group_begin.data_ptr(),
+           group_begin.numel() - 1, float(max_grad_norm), ctypes.byref(config), float(bc1), float(bc2_sqrt),
+           state.data_ptr(), _ptr(prenorm), _ptr(buf), 0 if buf is None else buf.numel(),
+           L.array(L.ParamMirror, items) if items else None, len(items), _stream())
+
+
 def adam_step(params, grads, exp_avg, exp_avg_sq, group_begin: torch.Tensor, max_grad_norm: float, beta1: float,
               beta2: float, eps: float, bc1: float, bc2_sqrt: float, state: torch.Tensor, ws: Workspace | None,
               prenorm: torch.Tensor | None = None, mirrors: list[tuple] | None = None) -> None:

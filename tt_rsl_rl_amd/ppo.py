@@ -29,6 +29,7 @@ from typing import Mapping
 import torch
 import torch.nn as nn
 
+from . import _lib as L
 from . import ops
 from .engine import RecurrentUpdateEngine, UpdateEngine
 from .models import MLPModel, RNNModel
@@ -163,8 +164,8 @@ class PPO:
             raise NotImplementedError("symmetry augmentation is not on the HIP PPO path")
         if multi_gpu_cfg is not None:
             raise NotImplementedError("multi-GPU training is not implemented by the HIP PPO plugin (single GPU)")
-        if optimizer.lower() != "adam":
-            raise NotImplementedError(f"optimizer '{optimizer}': the fused update implements Adam")
+        if optimizer.lower() not in L.OPTIMIZERS:  # upstream's resolve_optimizer (rsl_rl/utils/utils.py:71-96)
+            raise ValueError(f"Invalid optimizer '{optimizer.lower()}'. Valid optimizers are: {list(L.OPTIMIZERS)}")
         if use_mixed_precision:
             raise NotImplementedError("the HIP update computes in fp32; use_mixed_precision is not supported")
         if actor.is_recurrent != critic.is_recurrent:
@@ -195,9 +196,21 @@ class PPO:
         actor_params = list(dict.fromkeys(self.actor.parameters()))
         critic_params = [p for p in dict.fromkeys(self.critic.parameters()) if p not in set(actor_params)]
         self.flat = FlatParams([actor_params, critic_params], self.device)
-        self.optimizer = torch.optim.Adam(actor_params + critic_params, lr=learning_rate)
-        self.betas = tuple(self.optimizer.defaults["betas"])
-        self.adam_eps = float(self.optimizer.defaults["eps"])
+        # upstream passes the learning rate only (ppo.py:99-102): every other hyperparameter is torch's default
+        self.optim_kind = L.OPTIMIZERS[optimizer.lower()]
+        opt_cls = {L.OPTIM_ADAM: torch.optim.Adam, L.OPTIM_ADAMW: torch.optim.AdamW, L.OPTIM_SGD: torch.optim.SGD,
+                   L.OPTIM_RMSPROP: torch.optim.RMSprop}[self.optim_kind]
+        self.optimizer = opt_cls(actor_params + critic_params, lr=learning_rate)
+        d = self.optimizer.defaults
+        if d.get("momentum", 0) != 0 or d.get("centered", False) or d.get("nesterov", False) or d.get("amsgrad", False):
+            raise NotImplementedError("optimizer defaults outside the fused update (momentum / centered / amsgrad)")
+        if self.optim_kind != L.OPTIM_ADAMW and d.get("weight_decay", 0) != 0:
+            raise NotImplementedError("coupled weight decay is outside the fused update")
+        self.betas = tuple(d.get("betas", (0.9, 0.999)))
+        self.adam_eps = float(d.get("eps", 1e-8))
+        self.optim_config = L.OptimConfig(kind=self.optim_kind, beta1=self.betas[0], beta2=self.betas[1],
+                                          eps=self.adam_eps, weight_decay=float(d.get("weight_decay", 0.0)),
+                                          alpha=float(d.get("alpha", 0.0)))
         self._opt_steps = 0
 
         self.storage = storage
@@ -416,12 +429,23 @@ class PPO:
         return [dict(kl_mean=t[0], lr=t[1], surrogate=t[2], value=t[3], entropy=t[4])
                 for t in self._trace_rows.tolist()]
 
+    def _state_views(self, p) -> dict:
+        """The torch optimiser's per-parameter state tensors as views of the flat buffers the kernels update: Adam /
+        AdamW exp_avg and exp_avg_sq, RMSprop square_avg; SGD without momentum keeps none."""
+        if self.optim_kind == L.OPTIM_SGD:
+            return {}
+        if self.optim_kind == L.OPTIM_RMSPROP:
+            return {"square_avg": self.flat.exp_avg_view(p)}
+        return {"exp_avg": self.flat.exp_avg_view(p), "exp_avg_sq": self.flat.exp_avg_sq_view(p)}
+
     def _sync_optimizer_state(self) -> None:
-        """Expose the flat Adam moments through torch.optim.Adam's state (views, no copies).  Every parameter takes
-        the same number of steps, so they share one step tensor, updated in place."""
+        """Expose the flat optimiser state through the torch optimiser's state (views, no copies).  Every parameter
+        takes the same number of steps, so they share one step tensor, updated in place."""
+        if self.optim_kind == L.OPTIM_SGD:
+            return
         steps = float(self._opt_steps)
-        # a parameter that takes no gradient (learn_std=False) has no Adam state, as in torch.optim.Adam, whose step
-        # skips parameters whose .grad is None
+        # a parameter that takes no gradient (learn_std=False) has no optimiser state, as in torch's optimisers, whose
+        # step skips parameters whose .grad is None
         learned = [p for p in self.flat.params if p.requires_grad]
         if self._step_tensor is not None and all(
                 self.optimizer.state[p].get("step") is self._step_tensor for p in learned):
@@ -431,8 +455,7 @@ class PPO:
         for p in learned:
             s = self.optimizer.state[p]
             s["step"] = self._step_tensor
-            s["exp_avg"] = self.flat.exp_avg_view(p)
-            s["exp_avg_sq"] = self.flat.exp_avg_sq_view(p)
+            s.update(self._state_views(p))
 
     # -- bookkeeping -------------------------------------------------------------------------------------------------
     def train_mode(self) -> None:
@@ -463,13 +486,13 @@ class PPO:
             with torch.no_grad():
                 for p in self.flat.params:
                     s = self.optimizer.state.get(p, {})
-                    if "exp_avg" in s:
-                        self.flat.exp_avg_view(p).copy_(s["exp_avg"])
-                        self.flat.exp_avg_sq_view(p).copy_(s["exp_avg_sq"])
+                    views = self._state_views(p)
+                    self.flat.exp_avg_view(p).zero_()
+                    self.flat.exp_avg_sq_view(p).zero_()
+                    if views and all(k in s for k in views):
+                        for k, v in views.items():
+                            v.copy_(s[k])
                         steps = max(steps, int(float(s["step"])))
-                    else:
-                        self.flat.exp_avg_view(p).zero_()
-                        self.flat.exp_avg_sq_view(p).zero_()
             self._opt_steps = steps
             if steps > 0:
                 self._sync_optimizer_state()
