@@ -18,11 +18,11 @@ def _flat(w, obs, groups):
     return torch.cat([obs[g] for g in groups], dim=-1)
 
 
-@pytest.mark.parametrize("recurrent", [False, True])
+@pytest.mark.parametrize("recurrent", [False, "lstm", "gru"])
 def test_inference_policies_and_exports_after_an_update(recurrent):
     if recurrent:
         w = R.scaled(R.WORKLOADS["lstm256"], num_envs=64, steps=8, hidden_dims=[64, 32])
-        w["rnn"] = dict(w["rnn"], rnn_hidden_dim=32)
+        w["rnn"] = dict(w["rnn"], rnn_hidden_dim=32, rnn_type=recurrent, rnn_num_layers=2 if recurrent == "gru" else 1)
         w["obs_normalization"] = True
     else:
         w = R.scaled(R.WORKLOADS["humanoid"], num_envs=64, steps=8, hidden_dims=[64, 32])
@@ -60,12 +60,13 @@ def test_inference_policies_and_exports_after_an_update(recurrent):
                 # the exports are batch-1 steppers: follow env 0 (reset after its dones)
                 out_j = jit(x[:1])
                 if h is None:
-                    _, h, c = onnx_model.get_dummy_inputs()
-                out_o, h, c = onnx_model(x[:1], h, c)
+                    state = list(onnx_model.get_dummy_inputs()[1:])  # (h, c) for the LSTM, (h,) for the GRU
+                out_o, h, c = onnx_model(x[:1], *state)
+                state = [h, c] if c is not None else [h]
                 assert rel_err(out_j, ref[:1]) < 1e-5 and rel_err(out_o, ref[:1]) < 1e-5, t
                 if d[0] == 1.0:
                     jit.reset()
-                    h, c = torch.zeros_like(h), torch.zeros_like(c)
+                    state = [torch.zeros_like(v) for v in state]
             else:
                 assert rel_err(jit(x), ref) < 1e-5 and rel_err(onnx_model(x), ref) < 1e-5, t
             actor.reset(d.to(dev))

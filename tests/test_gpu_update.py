@@ -131,6 +131,10 @@ CASES = {
     "gru64_norm": (_lstm(128, 16, 64, [64, 32], rnn_type="gru", obs_normalization=True), {}),
     "gru32x2_ragged_permb": (_lstm(200, 10, 32, [32, 16], layers=2, rnn_type="gru"),
                              {"num_mini_batches": 3, "normalize_advantage_per_mini_batch": True, "carry_state": True}),
+    # the recurrent update with one launch per step (PPO_HIP_LSTM_SEQ=0: the heads' weight-grads on a second stream)
+    "lstm64_per_step_launches": (_lstm(128, 16, 64, [64, 32]), {"carry_state": True, "per_step_launches": True}),
+    "gru32x2_per_step_launches": (_lstm(200, 10, 32, [32, 16], layers=2, rnn_type="gru"),
+                                  {"num_mini_batches": 3, "per_step_launches": True}),
 }
 
 # an oracle update of the 65,536-env workload takes ~45 s of CPU time on 16 threads, and the end-to-end test runs it
@@ -169,6 +173,7 @@ def _rollout(name: str):
     w, over = CASES[name]
     over = dict(over)
     carry = over.pop("carry_state", False)
+    over.pop("per_step_launches", None)
     ora, roll = R.generate(w, 0, carry_state=carry, **over)
     with torch.inference_mode():
         last_values = ora.critic(roll.last_obs).detach()
@@ -179,7 +184,8 @@ def _rollout(name: str):
 def _pair(name: str):
     """A fresh copy of the case's oracle and a HIP plugin with the same weights, rollout and returns."""
     w, over = CASES[name]
-    over = {k: v for k, v in over.items() if k != "carry_state"}
+    per_step = over.get("per_step_launches", False)
+    over = {k: v for k, v in over.items() if k not in ("carry_state", "per_step_launches")}
     ora0, roll, last_values = _rollout(name)
     ora = copy.deepcopy(ora0)
     hip = make_hip(w, 0, **over)
@@ -188,6 +194,16 @@ def _pair(name: str):
         hip.critic.load_state_dict(roll.init_state["critic"])
     R.feed(hip.storage, roll)
     hip.compute_returns_from(last_values.to(hip.device).contiguous())
+    if per_step:  # the recurrent engine reads the switch when it is built: one launch per step, head dw beside them
+        old = os.environ.get("PPO_HIP_LSTM_SEQ")
+        os.environ["PPO_HIP_LSTM_SEQ"] = "0"
+        try:
+            assert hip._get_engine().lstm_sync is None
+        finally:
+            if old is None:
+                del os.environ["PPO_HIP_LSTM_SEQ"]
+            else:
+                os.environ["PPO_HIP_LSTM_SEQ"] = old
     return w, ora, hip
 
 
