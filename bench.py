@@ -70,7 +70,7 @@ def _sample_obs(workload, n, device, gen):
     return out
 
 
-def build_gpu_alg(workload, seed: int = 0):
+def build_gpu_alg(workload, seed: int = 0, mixed_precision: bool = False):
     """Construct the plugin the way upstream's runner does and collect one synthetic rollout on the GPU."""
     import torch
 
@@ -79,7 +79,7 @@ def build_gpu_alg(workload, seed: int = 0):
 
     dev = torch.device("cuda:0")
     torch.manual_seed(seed)
-    cfg = W.train_cfg(workload)
+    cfg = W.train_cfg(workload, **({"use_mixed_precision": True} if mixed_precision else {}))
     env = SimpleNamespace(num_envs=workload["num_envs"], num_actions=workload["num_actions"])
     n = workload["num_envs"]
     obs0 = {k: torch.zeros(n, w) for k, (_, w) in workload["obs"].items()}
@@ -367,6 +367,9 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=None,
                     help="timed oracle updates for cpu_baseline (default 3; 1 for recurrent workloads)")
     ap.add_argument("--no-phase-events", action="store_true", help="do not record per-launch HIP events")
+    ap.add_argument("--mixed-precision", action="store_true",
+                    help="upstream's use_mixed_precision: the layers' GEMMs with bf16 operands (not the default "
+                         "configuration: a separate line, dtype bf16)")
     ap.add_argument("--census", type=int, default=None, metavar="N",
                     help="only collect the rollout and run N updates (no timing; for a kernel census under rocprofv3: "
                          "the kernels of N updates = this run's minus the run with N = 0)")
@@ -399,7 +402,7 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 2
     workload = W.WORKLOADS[args.workload]
-    alg = build_gpu_alg(workload)
+    alg = build_gpu_alg(workload, mixed_precision=args.mixed_precision)
     B = workload["num_envs"] * workload["steps"]
     M = alg.num_mini_batches
     R = B // M if "rnn" not in workload else workload["steps"] * (workload["num_envs"] // M)
@@ -470,11 +473,14 @@ def main() -> int:
         n, t = timer.summary()[dom]
         ach = flops[dom] / (t * 1e-3) / 1e12
         arith = dw_arith(engine, R) if dom in ("dw", "lstm_dw") else "fp32"
-        peak = PEAK_BX6_TFLOPS if arith == "bf16x6" else PEAK_FP32_MFMA_TFLOPS
+        if arith == "bf16x6" and args.mixed_precision:
+            arith = "bf16"  # (the same kernels at one bf16 product per k-group)
+        peak = {"bf16x6": PEAK_BX6_TFLOPS, "bf16": PEAK_BF16_MFMA_TFLOPS}.get(arith, PEAK_FP32_MFMA_TFLOPS)
         roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": round(peak, 2), "unit": "TFLOP/s",
                     "frac": round(ach / peak, 4), "traffic": load_traffic(args.workload, dom), "kernel": dom,
-                    "arith": arith, "peak_basis": ("bf16 dense MFMA 2.5 PFLOP/s / 6 products per fp32 product"
-                                                   if arith == "bf16x6" else "fp32 dense MFMA"),
+                    "arith": arith, "peak_basis": {"bf16x6": "bf16 dense MFMA 2.5 PFLOP/s / 6 products per fp32 "
+                                                             "product", "bf16": "bf16 dense MFMA 2.5 PFLOP/s"}.get(
+                                                       arith, "fp32 dense MFMA"),
                     "frac_of_fp32_mfma_peak": round(ach / PEAK_FP32_MFMA_TFLOPS, 4),
                     "flops_per_launch": flops[dom], "mean_launch_ms": round(t, 5), "launches_timed": n}
     # compute_returns() (bootstrap critic forward, GAE, advantage normalisation) on the stored rollout, timed after
@@ -499,8 +505,11 @@ def main() -> int:
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "samples/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-        "gemm_arith": ("fp32 operands and results; GEMMs with 16-byte aligned operand rows as bf16x6 (three bf16 "
+        "vs_baseline": None, "dtype": "bf16" if args.mixed_precision else "fp32", "data": "synthetic",
+        "gemm_arith": ("use_mixed_precision: the layers' GEMMs with bf16 operands (rounded to nearest even), one bf16 "
+                       "MFMA product, fp32 accumulation and results; loss, head and optimiser in fp32"
+                       if args.mixed_precision else
+                       "fp32 operands and results; GEMMs with 16-byte aligned operand rows as bf16x6 (three bf16 "
                        "parts per operand, six bf16 MFMA products, fp32 accumulation), the rest on fp32 MFMA"),
         "config": {"workload": f"{args.workload}: {lstm}{len(W.linear_shapes(workload)[0])}-layer actor/critic MLPs "
                                f"{W.linear_shapes(workload)}, {workload['num_envs']} envs x {workload['steps']} steps, "

@@ -229,6 +229,24 @@ int ppo_linear_bwd_dw_norm(const ppo_linear_bwd_dw_problem* problems, int32_t co
                            size_t workspace_bytes, const float* extra_grads, const ppo_grad_range* extra,
                            int32_t num_extra, double* norm_partials, ppo_stream_t stream);
 
+/* The same three GEMMs with launch flags (all problems of a call share them):
+ *   PPO_GEMM_BF16_OPERANDS  bf16 operands: every operand element rounded to bf16 (to nearest even), the products
+ *       of those exact in fp32 accumulation, fp32 outputs and epilogues -- the matrix products of upstream's
+ *       use_mixed_precision (rsl_rl/algorithms/ppo.py:222-224: torch.autocast to bfloat16 over the forward and the
+ *       loss, so their backward too), on the bf16 matrix cores at one product per k-group instead of bf16x6's six.
+ *       Operands the bf16 kernels do not take (rows that are not 16-byte multiples, k not a multiple of 16) run on
+ *       the fp32 kernels, i.e. at higher precision.  The bias gradient's column sums stay fp64 over the fp32 values.
+ * flags = 0 is the plain entry point.  ppo_linear_bwd_dw_ex: norm_partials NULL (and no extra ranges) is
+ * ppo_linear_bwd_dw, else ppo_linear_bwd_dw_norm. */
+#define PPO_GEMM_BF16_OPERANDS 1
+int ppo_linear_fwd_ex(const ppo_linear_fwd_problem* problems, int32_t count, int64_t rows, int32_t activation,
+                      int32_t flags, ppo_stream_t stream);
+int ppo_linear_bwd_dx_ex(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t activation,
+                         int32_t source, int32_t flags, void* workspace, size_t workspace_bytes, ppo_stream_t stream);
+int ppo_linear_bwd_dw_ex(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows, int32_t flags,
+                         void* workspace, size_t workspace_bytes, const float* extra_grads,
+                         const ppo_grad_range* extra, int32_t num_extra, double* norm_partials, ppo_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------------------------
  * A7  Empirical observation normaliser, rsl_rl/modules/normalization.py:46-78.
  * ppo_obs_normalize: y = (x - mean) / (std + eps) over [rows, width] (forward, :46-48).

@@ -73,7 +73,7 @@ def _models(w):
     ({"device": "cuda", "symmetry_cfg": {"use_data_augmentation": True}}, NotImplementedError),
     ({"device": "cuda", "multi_gpu_cfg": {"global_rank": 0, "world_size": 2}}, NotImplementedError),
     ({"device": "cuda", "optimizer": "lamb"}, ValueError),  # upstream's resolve_optimizer error
-    ({"device": "cuda", "use_mixed_precision": True}, NotImplementedError),
+    ({"device": "cpu", "use_mixed_precision": True}, RuntimeError),  # (accepted: rejected for the device only)
 ])
 def test_unsupported_options_are_rejected_before_touching_the_gpu(kwargs, exc):
     w = R.scaled(R.WORKLOADS["flat48"], num_envs=8)

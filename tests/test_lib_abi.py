@@ -130,6 +130,20 @@ def test_argument_validation_reports_errors_without_a_gpu():
                       _lib.PPO_ELU_FROM_OUTPUT, None, 0, None)
     with pytest.raises(ValueError, match="activation=0"):
         _lib.call("ppo_linear_bwd_dx_act", ctypes.byref(dx), 1, 10, 0, _lib.PPO_ELU_FROM_INPUT, None, 0, None)
+    # the GEMM launch flags: PPO_GEMM_BF16_OPERANDS is the only bit, anything else is refused before any launch
+    assert _lib.GEMM_BF16_OPERANDS == 1
+    for flags in (2, -1, 1 | 8):
+        with pytest.raises(ValueError, match=f"flags={flags}"):
+            _lib.call("ppo_linear_fwd_ex", ctypes.byref(prob), 1, 10, 1, flags, None)
+        with pytest.raises(ValueError, match=f"flags={flags}"):
+            _lib.call("ppo_linear_bwd_dx_ex", ctypes.byref(dx), 1, 10, 1, _lib.PPO_ELU_FROM_INPUT, flags, None, 0,
+                      None)
+    dwp = _lib.LinearBwdDwProblem(8, 512, 8, 96, 8, 8, 96, 512, 0, 0)
+    with pytest.raises(ValueError, match="flags=4"):
+        _lib.call("ppo_linear_bwd_dw_ex", ctypes.byref(dwp), 1, 24576, 4, 16, 1 << 30, None, None, 0, None, None)
+    rng1 = _lib.array(_lib.GradRange, [_lib.GradRange(0, 5, 0, 0)])
+    with pytest.raises(ValueError, match="norm_partials"):
+        _lib.call("ppo_linear_bwd_dw_ex", ctypes.byref(dwp), 1, 24576, 1, 16, 1 << 30, 16, rng1, 1, None, None)
     assert sorted(_lib.ACTIVATIONS.values()) == list(range(1, 13))
     # workspace queries are pure host arithmetic
     assert lib.ppo_adv_normalize_workspace_bytes(98304) > 0

@@ -85,6 +85,7 @@ class OptimConfig(C.Structure):
 
 
 OPTIM_ADAM, OPTIM_ADAMW, OPTIM_SGD, OPTIM_RMSPROP = 0, 1, 2, 3
+GEMM_BF16_OPERANDS = 1
 OPTIMIZERS = {"adam": OPTIM_ADAM, "adamw": OPTIM_ADAMW, "sgd": OPTIM_SGD, "rmsprop": OPTIM_RMSPROP}
 
 
@@ -171,6 +172,11 @@ _SIGNATURES = [
     ("ppo_interleave_columns", C.c_int, [C.POINTER(ColumnBlock), i32, i64, f32p, i64, C.c_void_p]),
     ("ppo_linear_bwd_dw_norm", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, C.c_void_p, C.c_size_t, f32p,
                                          C.POINTER(GradRange), i32, C.c_void_p, C.c_void_p]),
+    ("ppo_linear_fwd_ex", C.c_int, [C.POINTER(LinearFwdProblem), i32, i64, i32, i32, C.c_void_p]),
+    ("ppo_linear_bwd_dx_ex", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, i32, i32, C.c_void_p,
+                                       C.c_size_t, C.c_void_p]),
+    ("ppo_linear_bwd_dw_ex", C.c_int, [C.POINTER(LinearBwdDwProblem), i32, i64, i32, C.c_void_p, C.c_size_t, f32p,
+                                       C.POINTER(GradRange), i32, C.c_void_p, C.c_void_p]),
     ("ppo_obs_normalize", C.c_int, [f32p, i64, f32p, i64, i64, i32, f32p, f32p, C.c_float, C.c_void_p]),
     ("ppo_normalizer_update_workspace_bytes", C.c_size_t, [i64, i32]),
     ("ppo_normalizer_update", C.c_int, [C.POINTER(ColumnBlock), i32, i64, f32p, f32p, f32p, C.c_void_p, C.c_void_p,

@@ -298,7 +298,7 @@ int launch_nt_pipe(Group& g, int count, hipStream_t s, const char* name) {
 // row and 11.4 with 128 x 64 tiles.  A PPO_HIP_TUNING build reads "PPO_HIP_BX6" = "bn[:stages[:four_lanes]]"
 // (0: off).
 template <int EPI, bool BKM = false>
-int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
+int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name, bool bf16 = false) {
   auto fits = [](const float* c, int64_t rows, int64_t ld) {
     return c == nullptr || (w16_ok(c, ld) && rows * ld * 4 < (int64_t(1) << 31));
   };
@@ -341,6 +341,11 @@ int launch_nt_bx6(Group& g, int count, hipStream_t s, const char* name) {
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), 0, s, g);
     return check_launch(name);
   };
+  if (bf16) {  // the bf16-operand mode: one product per k-group, the default tiles
+    if constexpr (BKM) return go(gemm_nt_bx6_kernel<128, 3, EPI, 2, true, true, true>);
+    if (bn == 64) return go(gemm_nt_bx6_kernel<64, 3, EPI, 2, true, false, true>);
+    return go(gemm_nt_bx6_kernel<128, 3, EPI, 2, true, false, true>);
+  }
   if constexpr (BKM) return go(gemm_nt_bx6_kernel<128, 3, EPI, 2, true, true>);
 #ifdef PPO_HIP_TUNING
   if (bn == 64 || ns == 3 || !q4) {
@@ -414,8 +419,23 @@ bool span_ok(int64_t rows, int64_t ld) { return rows * ld < (int64_t(1) << 30); 
 
 using namespace ppo;
 
+namespace ppo {
+namespace {
+
+bool flags_ok(int32_t flags) { return (flags & ~PPO_GEMM_BF16_OPERANDS) == 0; }
+
+}  // namespace
+}  // namespace ppo
+
 extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t count, int64_t rows, int32_t activation,
                               ppo_stream_t stream) {
+  return ppo_linear_fwd_ex(problems, count, rows, activation, 0, stream);
+}
+
+extern "C" int ppo_linear_fwd_ex(const ppo_linear_fwd_problem* problems, int32_t count, int64_t rows,
+                                 int32_t activation, int32_t flags, ppo_stream_t stream) {
+  PPO_REQUIRE(flags_ok(flags), "ppo_linear_fwd: flags=%d", flags);
+  const bool bf16 = (flags & PPO_GEMM_BF16_OPERANDS) != 0;
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS,
               "ppo_linear_fwd: count=%d outside [1, %d]", count, PPO_MAX_LINEAR_PROBLEMS);
   PPO_REQUIRE(rows_ok(rows), "ppo_linear_fwd: rows=%lld", (long long)rows);
@@ -450,7 +470,7 @@ extern "C" int ppo_linear_fwd(const ppo_linear_fwd_problem* problems, int32_t co
   // narrower ones 128x64
   auto run = [&](auto epi_c, const char* name) {
     constexpr int EPI = decltype(epi_c)::value;
-    const int brc = launch_nt_bx6<EPI>(g, count, s, name);
+    const int brc = launch_nt_bx6<EPI>(g, count, s, name, bf16);
     if (brc != PPO_EUNSUPPORTED) return brc;
     const int prc = launch_nt_pipe_tile<EPI>(pipe_tile("PPO_HIP_PIPE_FWD", max_n > 128 ? 1 : 2), g, count, s, name);
     if (prc != PPO_EUNSUPPORTED) return prc;
@@ -508,7 +528,10 @@ bool act_from_output_ok(int act) {
 }
 
 int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows, int32_t activation,
-            int32_t elu_source, void* workspace, size_t workspace_bytes, ppo_stream_t stream, const char* who) {
+            int32_t elu_source, void* workspace, size_t workspace_bytes, ppo_stream_t stream, const char* who,
+            int32_t flags = 0) {
+  PPO_REQUIRE(flags_ok(flags), "%s: flags=%d", who, flags);
+  const bool bf16 = (flags & PPO_GEMM_BF16_OPERANDS) != 0;
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS, "%s: count=%d outside [1, %d]",
               who, count, PPO_MAX_LINEAR_PROBLEMS);
   PPO_REQUIRE(activation > PPO_ACT_NONE && activation < PPO_ACT_COUNT, "%s: activation=%d", who, activation);
@@ -554,7 +577,7 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
   auto run = [&](auto epi_c, const char* name) {
     constexpr int EPI = decltype(epi_c)::value;
     // the bf16x6 kernel reads the weights as stored (k-major, 16-byte rows): no transpose
-    const int krc = launch_nt_bx6<EPI, true>(g, count, s, name);
+    const int krc = launch_nt_bx6<EPI, true>(g, count, s, name, bf16);
     if (krc != PPO_EUNSUPPORTED) return krc;
     // else w^T (k-contiguous) into the workspace for the other kernels
     if (int rc = launch_transposes(problems, count, ws, offs, s)) return rc;
@@ -562,7 +585,7 @@ int dx_gemm(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t ro
       g.p[i].B = ws + offs[i];
       g.p[i].ldb = round4(problems[i].out_features);
     }
-    const int brc = launch_nt_bx6<EPI>(g, count, s, name);
+    const int brc = launch_nt_bx6<EPI>(g, count, s, name, bf16);
     if (brc != PPO_EUNSUPPORTED) return brc;
     // measured on MI355X: 64x64 tiles for the 256..512-wide input grads, 128x64 for narrower ones
     const int prc = launch_nt_pipe_tile<EPI>(pipe_tile("PPO_HIP_PIPE_DX", max_n > 128 ? 3 : 2), g, count, s, name);
@@ -590,6 +613,13 @@ extern "C" int ppo_linear_bwd_dx_act(const ppo_linear_bwd_dx_problem* problems, 
                  "ppo_linear_bwd_dx_act");
 }
 
+extern "C" int ppo_linear_bwd_dx_ex(const ppo_linear_bwd_dx_problem* problems, int32_t count, int64_t rows,
+                                    int32_t activation, int32_t source, int32_t flags, void* workspace,
+                                    size_t workspace_bytes, ppo_stream_t stream) {
+  return dx_gemm(problems, count, rows, activation, source, workspace, workspace_bytes, stream,
+                 "ppo_linear_bwd_dx_ex", flags);
+}
+
 extern "C" size_t ppo_linear_bwd_dw_workspace_bytes(const ppo_linear_bwd_dw_problem* problems, int32_t count,
                                                     int64_t rows) {
   if (problems == nullptr || count < 1 || count > PPO_MAX_LINEAR_PROBLEMS || !rows_ok(rows)) return 0;
@@ -603,7 +633,9 @@ namespace {
 
 int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows, void* workspace,
             size_t workspace_bytes, const float* extra_grads, const ppo_grad_range* extra, int32_t num_extra,
-            double* norm, ppo_stream_t stream) {
+            double* norm, ppo_stream_t stream, int32_t flags = 0) {
+  PPO_REQUIRE(flags_ok(flags), "ppo_linear_bwd_dw: flags=%d", flags);
+  const bool bf16 = (flags & PPO_GEMM_BF16_OPERANDS) != 0;
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LINEAR_PROBLEMS,
               "ppo_linear_bwd_dw: count=%d outside [1, %d]", count, PPO_MAX_LINEAR_PROBLEMS);
   PPO_REQUIRE(rows_ok(rows), "ppo_linear_bwd_dw: rows=%lld", (long long)rows);
@@ -691,7 +723,7 @@ int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t ro
   } else
 #endif
   if (bx6) {
-    rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw");
+    rc = launch_tn_bx6<kDwBlocksPerCu>(g, count, s, "linear_bwd_dw", bf16);
   } else {
     rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwF32BlocksPerCu>(g, count, s, "linear_bwd_dw");
   }
@@ -716,4 +748,13 @@ extern "C" int ppo_linear_bwd_dw_norm(const ppo_linear_bwd_dw_problem* problems,
   PPO_REQUIRE(norm_partials != nullptr, "ppo_linear_bwd_dw_norm: null norm_partials");
   return dw_gemm(problems, count, rows, workspace, workspace_bytes, extra_grads, extra, num_extra, norm_partials,
                  stream);
+}
+
+extern "C" int ppo_linear_bwd_dw_ex(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t rows,
+                                    int32_t flags, void* workspace, size_t workspace_bytes, const float* extra_grads,
+                                    const ppo_grad_range* extra, int32_t num_extra, double* norm_partials,
+                                    ppo_stream_t stream) {
+  PPO_REQUIRE(norm_partials != nullptr || num_extra == 0, "ppo_linear_bwd_dw_ex: extra ranges need norm_partials");
+  return dw_gemm(problems, count, rows, workspace, workspace_bytes, extra_grads, extra, num_extra, norm_partials,
+                 stream, flags);
 }

@@ -1451,6 +1451,12 @@ __device__ __forceinline__ void split_bf16x3(float x0, float x1, uint32_t& hi, u
   lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{r0, r1}), bf16x2));
 }
 
+// Two floats rounded to bf16 (to nearest even), packed (element 0 in the low half): the operands of the bf16-operand
+// mode (PPO_GEMM_BF16_OPERANDS), whose products are the hi-part products of the bf16x6 scheme alone.
+__device__ __forceinline__ uint32_t round_bf16x2(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x0, x1}), bf16x2));
+}
+
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 // Byte offset of the 8-byte chunk c (4 bf16 columns) of row k in a k-major plane of W bf16 columns: the chunk index
@@ -1465,7 +1471,8 @@ __device__ __forceinline__ int tn_chunk_off(int k, int c) {
 
 // One BM x BN tile (BN = 128, or 64 for narrow problems: then each wave owns 64 x 32 and B is staged one row per
 // thread) of one split of the weight-grad.
-template <int BN, bool FULL>
+// BF16: operands rounded to bf16 and one product per k-group (the bf16-operand mode); only part plane 0 is used.
+template <int BN, bool FULL, bool BF16 = false>
 __device__ __forceinline__ void tn_bx6_tile(const Group& g, const TileCoord tc, unsigned char* lds) {
   constexpr int BM = 128, BK = 16;
   constexpr int TN = BN / 64;                  // 32-column accumulator tiles per wave
@@ -1547,14 +1554,19 @@ __device__ __forceinline__ void tn_bx6_tile(const Group& g, const TileCoord tc, 
   };
   // q: A row sk, A row sk + 8, B row bsk (, B row bsk + 8)
   auto split_row = [&](const f32x4& v, int q, unsigned char* st) {
-    uint32_t h[2], md[2], l[2];
-    split_bf16x3(v[0], v[1], h[0], md[0], l[0]);
-    split_bf16x3(v[2], v[3], h[1], md[1], l[1]);
-    const int pl = q < 2 ? PLANE : PLANE_B;
     unsigned char* c = st + (q < 2 ? ((q & 1) ? w_off1 : w_off0) : 3 * PLANE + ((q & 1) ? wb_off1 : wb_off0));
-    *reinterpret_cast<uint64_t*>(c) = (static_cast<uint64_t>(h[1]) << 32) | h[0];
-    *reinterpret_cast<uint64_t*>(c + pl) = (static_cast<uint64_t>(md[1]) << 32) | md[0];
-    *reinterpret_cast<uint64_t*>(c + 2 * pl) = (static_cast<uint64_t>(l[1]) << 32) | l[0];
+    if constexpr (BF16) {
+      const uint32_t h0 = round_bf16x2(v[0], v[1]), h1 = round_bf16x2(v[2], v[3]);
+      *reinterpret_cast<uint64_t*>(c) = (static_cast<uint64_t>(h1) << 32) | h0;
+    } else {
+      uint32_t h[2], md[2], l[2];
+      split_bf16x3(v[0], v[1], h[0], md[0], l[0]);
+      split_bf16x3(v[2], v[3], h[1], md[1], l[1]);
+      const int pl = q < 2 ? PLANE : PLANE_B;
+      *reinterpret_cast<uint64_t*>(c) = (static_cast<uint64_t>(h[1]) << 32) | h[0];
+      *reinterpret_cast<uint64_t*>(c + pl) = (static_cast<uint64_t>(md[1]) << 32) | md[0];
+      *reinterpret_cast<uint64_t*>(c + 2 * pl) = (static_cast<uint64_t>(l[1]) << 32) | l[0];
+    }
   };
   double colsum_acc[4] = {0.0, 0.0, 0.0, 0.0};  // columns 4 sc + e of A over rows sk, sk + 8 of every slab, in order
   auto add_colsum = [&](const f32x4 (&v)[2 + NBR]) {
@@ -1610,15 +1622,29 @@ __device__ __forceinline__ void tn_bx6_tile(const Group& g, const TileCoord tc, 
       __builtin_amdgcn_sched_barrier(0);
       const unsigned char* st = lds + u * STAGE;
       unsigned char* nst = lds + (u ^ 1) * STAGE;
+      constexpr int NP = BF16 ? 1 : 3;  // part planes read
       bf16x8 fa[2][3], fb[TN][3];
 #pragma unroll
-      for (int pp = 0; pp < 3; ++pp) {
+      for (int pp = 0; pp < NP; ++pp) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) fa[i][pp] = frag(IntC<BM>{}, st + pp * PLANE, wm * 64 + 32 * i);
 #pragma unroll
         for (int j = 0; j < TN; ++j) fb[j][pp] = frag(IntC<BN>{}, st + 3 * PLANE + pp * PLANE_B, wn * (BN / 2) + 32 * j);
       }
       if constexpr (!FULL) zero_tail(kt + 1, stage_v[u ^ 1]);
+      if constexpr (BF16) {  // the one product, then the next slab's rounding and its column sums
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][0], fb[j][0], acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 2 + NBR; ++q) split_row(stage_v[u ^ 1][q], q, nst);
+        if (CS && (!FULL || kt + 1 < 2 * nk2)) add_colsum(stage_v[u ^ 1]);
+        lds_barrier();
+        continue;
+      }
       constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
       for (int t = 0; t < 6; ++t) {
@@ -1670,15 +1696,15 @@ __device__ __forceinline__ void tn_bx6_tile(const Group& g, const TileCoord tc, 
   }
 }
 
-template <int OCC, bool FULL>
+template <int OCC, bool FULL, bool BF16 = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_tn_bx6_kernel(
     const Group g) {
   __shared__ __align__(16) unsigned char lds[2 * 6 * 16 * 128 * 2];  // two stages of the 128 x 128 tile's planes
   const TileCoord tc = locate(g);
   if (g.p[tc.pi].tn64) {
-    tn_bx6_tile<64, FULL>(g, tc, lds);
+    tn_bx6_tile<64, FULL, BF16>(g, tc, lds);
   } else {
-    tn_bx6_tile<128, FULL>(g, tc, lds);
+    tn_bx6_tile<128, FULL, BF16>(g, tc, lds);
   }
 }
 
@@ -1693,7 +1719,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
 // the fp32 NT kernels' layout (B fragment first), so the persistent kernel's epilogues finish the tile, through
 // patches in the (then free) stage memory.
 // ------------------------------------------------------------------------------------------------------------------
-template <int BN, int OCC, int EPI, int NS, bool Q4, bool BKM = false>
+// BF16: operands rounded to bf16 and one product per k-group (the bf16-operand mode); only part plane 0 is used.
+template <int BN, int OCC, int EPI, int NS, bool Q4, bool BKM = false, bool BF16 = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, OCC))) void gemm_nt_bx6_kernel(
     const Group g) {
   static_assert(EPI == EPI_BIAS || epi_fwd_act(EPI) || epi_act_grad(EPI) || EPI == EPI_STORE,
@@ -1786,13 +1813,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     {
       if (o >= NA && !stage_b) return;
       const int i = o < NA ? o : o - NA;
-      const int plane = o < NA ? PLANE_A : PLANE_B;
+      [[maybe_unused]] const int plane = o < NA ? PLANE_A : PLANE_B;
       unsigned char* row = st + (o < NA ? swz[i] : 3 * PLANE_A + (BKM ? boff[i] : swz[i]));
       uint32_t w[4 * LD];
 #pragma unroll
       for (int l = 0; l < LD; ++l)
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[4 * l + e] = sv[o * LD + l][e];
+      if constexpr (BF16) {
+        uint32_t h[2 * LD];
+#pragma unroll
+        for (int q = 0; q < 2 * LD; ++q)
+          h[q] = round_bf16x2(__builtin_bit_cast(float, w[2 * q]), __builtin_bit_cast(float, w[2 * q + 1]));
+        if constexpr (Q4) {
+          *reinterpret_cast<u32x2*>(row) = u32x2{h[0], h[1]};
+        } else {
+          *reinterpret_cast<u32x4*>(row) = u32x4{h[0], h[1], h[2], h[3]};
+        }
+        return;
+      }
       uint32_t h[2 * LD], md[2 * LD], lo[2 * LD];
 #pragma unroll
       for (int q = 0; q < 2 * LD; ++q)
@@ -1856,9 +1895,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     load_slab(kt + NS, rb_load);
     __builtin_amdgcn_sched_barrier(0);  // (the compiler would sink the loads to their use)
     const unsigned char* st = lds + cs * STAGE;
+    constexpr int NP = BF16 ? 1 : 3;  // part planes read
     bf16x8 fa[TM][3], fb[TN][3];
 #pragma unroll
-    for (int pp = 0; pp < 3; ++pp) {
+    for (int pp = 0; pp < NP; ++pp) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[i][pp] = frag(st + pp * PLANE_A, wm * 64 + 32 * i + fr);
 #pragma unroll
@@ -1868,7 +1908,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(OCC, O
     }
     constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
     const int next = cs == 0 ? NS - 1 : cs - 1;
-    if constexpr (BN == 128) {
+    if constexpr (BF16) {  // the one product, then the next slab's rounding
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j][0], fa[i][0], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      split_store(next, rb_store);
+    } else if constexpr (BN == 128) {
       // the next slab's split, one staged row piece after each group of MFMAs: the wave's VALU work and LDS writes
       // issue while its MFMAs run (humanoid, per mini-batch: dx1 94 -> 88 us, fwd1 84 -> 83 us; the 64-wide tiles,
       // with half the MFMAs per group, measured 1 us slower that way)
@@ -2006,7 +2054,7 @@ int launch_tn(Group& g, int count, hipStream_t s, const char* name) {
 // The bf16x6 weight-grad when every problem's operands allow 16-byte loads (16-byte aligned, leading dimension a
 // multiple of 4); PPO_EUNSUPPORTED otherwise.
 template <int OCC>
-int launch_tn_bx6(Group& g, int count, hipStream_t s, const char* name) {
+int launch_tn_bx6(Group& g, int count, hipStream_t s, const char* name, bool bf16 = false) {
   bool full = true;  // every split chunk whole slab pairs, 16 rows of an operand under 2^31 bytes
   for (int i = 0; i < count; ++i) {
     const Problem& p = g.p[i];
@@ -2025,7 +2073,14 @@ int launch_tn_bx6(Group& g, int count, hipStream_t s, const char* name) {
     blocks += p.tiles_m * p.tiles_n * p.splits;  // (at most the 128 x 128 count assign_blocks checked)
   }
   if (blocks == 0) return PPO_OK;
-  if (full) {
+  if (bf16) {  // the bf16-operand mode: one product per k-group
+    if (full) {
+      hipLaunchKernelGGL((gemm_tn_bx6_kernel<OCC, true, true>), dim3(blocks), dim3(kThreads), 0, s, g);
+    } else {
+      hipLaunchKernelGGL((gemm_tn_bx6_kernel<(OCC < 2 ? OCC : 2), false, true>), dim3(blocks), dim3(kThreads), 0, s,
+                         g);
+    }
+  } else if (full) {
     hipLaunchKernelGGL((gemm_tn_bx6_kernel<OCC, true>), dim3(blocks), dim3(kThreads), 0, s, g);
   } else {  // (the clamped, zeroed rows need more registers than three blocks per CU leave: two)
     hipLaunchKernelGGL((gemm_tn_bx6_kernel<(OCC < 2 ? OCC : 2), false>), dim3(blocks), dim3(kThreads), 0, s, g);

@@ -275,7 +275,8 @@ class UpdateEngine:
         return (torch.cuda.current_stream(self.device).cuda_stream, a.clip_param, a.value_loss_coef, a.entropy_coef,
                 a.use_clipped_value_loss, a.desired_kl, a.schedule, a.max_grad_norm, tuple(a.betas), a.adam_eps,
                 a.optim_kind, a.optim_config.weight_decay, a.optim_config.alpha,
-                a.normalize_advantage_per_mini_batch, a.num_learning_epochs, self._storage_signature())
+                a.normalize_advantage_per_mini_batch, a.num_learning_epochs, a.use_mixed_precision,
+                self._storage_signature())
 
     def _storage_signature(self) -> tuple:
         st = self.alg.storage
@@ -434,13 +435,14 @@ class UpdateEngine:
                 z = b.out[:R] if last else (b.z[i][:R] if b.z is not None else None)
                 probs.append((x, w, lin.bias, z, None if last else b.h[i][:R]))
             tm.start(f"fwd{i}")
+            bf16 = self.alg.use_mixed_precision
             if last:
-                ops.linear_fwd(probs, R, act=L.PPO_ACT_NONE)
+                ops.linear_fwd(probs, R, act=L.PPO_ACT_NONE, bf16=bf16)
             elif ba.act == bc.act:
-                ops.linear_fwd(probs, R, act=ba.act)
+                ops.linear_fwd(probs, R, act=ba.act, bf16=bf16)
             else:  # (actor and critic with different activations: one launch each)
-                ops.linear_fwd(probs[:1], R, act=ba.act)
-                ops.linear_fwd(probs[1:], R, act=bc.act)
+                ops.linear_fwd(probs[:1], R, act=ba.act, bf16=bf16)
+                ops.linear_fwd(probs[1:], R, act=bc.act, bf16=bf16)
             tm.stop(f"fwd{i}")
             if not last:
                 ins_a.append(ba.h[i][:R])
@@ -527,7 +529,8 @@ class UpdateEngine:
         tm = self.timer
         for i, probs, from_output, act in self.dx_layers(R):
             tm.start(f"dx{i}")
-            ops.linear_bwd_dx(probs, R, self.dx_ws, elu_from_output=from_output, act=act)
+            ops.linear_bwd_dx(probs, R, self.dx_ws, elu_from_output=from_output, act=act,
+                              bf16=self.alg.use_mixed_precision)
             tm.stop(f"dx{i}")
 
     def head_dw(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> list[tuple]:
@@ -546,13 +549,14 @@ class UpdateEngine:
         sums the squares for the clip norms)."""
         tm = self.timer
         tm.start(phase)
+        bf16 = self.alg.use_mixed_precision
         if norm is not None:
             if len(dw) > L.MAX_LINEAR_PROBLEMS:
                 raise RuntimeError("weight_grads: the norm partials need all problems in one launch")
-            ops.linear_bwd_dw(dw, R, ws if ws is not None else self.dw_ws, norm=norm)
+            ops.linear_bwd_dw(dw, R, ws if ws is not None else self.dw_ws, norm=norm, bf16=bf16)
         else:
             for i in range(0, len(dw), L.MAX_LINEAR_PROBLEMS):
-                ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, ws if ws is not None else self.dw_ws)
+                ops.linear_bwd_dw(dw[i:i + L.MAX_LINEAR_PROBLEMS], R, ws if ws is not None else self.dw_ws, bf16=bf16)
         tm.stop(phase)
 
     def _bias_corrections(self, step: int) -> tuple[float, float]:
@@ -824,7 +828,7 @@ class RecurrentUpdateEngine(UpdateEngine):
         seqs = []
         for row in layers:
             ops.linear_fwd([(x, b.packed.w_ih_g, b.packed.b_g, b.gx[:R], None) for _, _, b, x in row], R,
-                           act=L.PPO_ACT_NONE)
+                           act=L.PPO_ACT_NONE, bf16=alg.use_mixed_precision)
             qs = [self._seq(m, side, b, e0, e0 + E, tab) for m, side, b, _ in row]
             self._grouped(ops.lstm_seq_fwd, qs, E)
             seqs.append(qs)
@@ -851,7 +855,7 @@ class RecurrentUpdateEngine(UpdateEngine):
             self._grouped(ops.lstm_seq_bwd, seqs[k], E)
             if k > 0:
                 ops.linear_bwd_dx([(b.dgates[:R], b.packed.w_ih_g, None, below[side][k - 1].dh[:R])
-                                   for _, side, b, _ in layers[k]], R, self.dx_ws)
+                                   for _, side, b, _ in layers[k]], R, self.dx_ws, bf16=alg.use_mixed_precision)
         tm.stop("lstm_bwd")
 
         dw = []

@@ -301,10 +301,11 @@ def _check_weight(w: torch.Tensor, b: torch.Tensor | None) -> tuple[int, int]:
     return out_f, in_f
 
 
-def linear_fwd(problems: list[tuple], rows: int, elu: bool = False, act: int | None = None) -> None:
+def linear_fwd(problems: list[tuple], rows: int, elu: bool = False, act: int | None = None,
+               bf16: bool = False) -> None:
     """problems: (x [rows, in], w [out, in], b [out], z [rows, out] or None, h [rows, out] or None).
     act: the hidden-layer activation (an L.ACTIVATIONS code; elu=True is L.PPO_ACT_ELU), h = act(z); without one z is
-    required, with one at least one of z / h."""
+    required, with one at least one of z / h.  bf16: bf16 operands (ppo_linear_fwd_ex, PPO_GEMM_BF16_OPERANDS)."""
     act = (L.PPO_ACT_ELU if elu else L.PPO_ACT_NONE) if act is None else int(act)
     elu = act != L.PPO_ACT_NONE
     items = []
@@ -327,7 +328,11 @@ def linear_fwd(problems: list[tuple], rows: int, elu: bool = False, act: int | N
                 raise ValueError("linear_fwd: h too small")
         items.append(L.LinearFwdProblem(x.data_ptr(), ldx, w.data_ptr(), b.data_ptr(), _ptr(z), ldz,
                                         _ptr(h) if elu else None, ldh, in_f, out_f))
-    L.call("ppo_linear_fwd", L.array(L.LinearFwdProblem, items), len(items), rows, act, _stream())
+    if bf16:
+        L.call("ppo_linear_fwd_ex", L.array(L.LinearFwdProblem, items), len(items), rows, act, L.GEMM_BF16_OPERANDS,
+               _stream())
+    else:
+        L.call("ppo_linear_fwd", L.array(L.LinearFwdProblem, items), len(items), rows, act, _stream())
 
 
 def _dx_problems(problems: list[tuple], rows: int):
@@ -351,13 +356,18 @@ def _dx_problems(problems: list[tuple], rows: int):
 
 
 def linear_bwd_dx(problems: list[tuple], rows: int, ws: Workspace | None = None, elu_from_output: bool = False,
-                  act: int = L.PPO_ACT_ELU) -> None:
+                  act: int = L.PPO_ACT_ELU, bf16: bool = False) -> None:
     """problems: (dz [rows, out], w [out, in], src [rows, in] or None, dz_prev [rows, in]); src is the activation's
-    input z of the layer below, or its output h = act(z) with elu_from_output (monotone activations only)."""
+    input z of the layer below, or its output h = act(z) with elu_from_output (monotone activations only).  bf16:
+    bf16 operands (ppo_linear_bwd_dx_ex, PPO_GEMM_BF16_OPERANDS)."""
     arr, count, nbytes = _dx_problems(problems, rows)
     buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
     src = L.PPO_ELU_FROM_OUTPUT if elu_from_output else L.PPO_ELU_FROM_INPUT
-    L.call("ppo_linear_bwd_dx_act", arr, count, rows, int(act), src, buf.data_ptr(), buf.numel(), _stream())
+    if bf16:
+        L.call("ppo_linear_bwd_dx_ex", arr, count, rows, int(act), src, L.GEMM_BF16_OPERANDS, buf.data_ptr(),
+               buf.numel(), _stream())
+    else:
+        L.call("ppo_linear_bwd_dx_act", arr, count, rows, int(act), src, buf.data_ptr(), buf.numel(), _stream())
 
 
 @dataclass
@@ -376,9 +386,11 @@ def grad_norm_partials(device) -> torch.Tensor:
     return torch.zeros(L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS, dtype=torch.float64, device=device)
 
 
-def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None, norm: GradNorm | None = None) -> None:
+def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None, norm: GradNorm | None = None,
+                  bf16: bool = False) -> None:
     """problems: (dz [rows, out], x [rows, in], dw [out, in], db [out] or None for no bias gradient).  With `norm`
-    the launch also writes the per-group sums of squares of what it stores (ppo_linear_bwd_dw_norm)."""
+    the launch also writes the per-group sums of squares of what it stores (ppo_linear_bwd_dw_norm).  bf16: bf16
+    operands (ppo_linear_bwd_dw_ex, PPO_GEMM_BF16_OPERANDS)."""
     items = []
     for i, (dz, x, dw, db) in enumerate(problems):
         _dev(dz, x, dw, db)
@@ -397,7 +409,11 @@ def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None,
         raise ValueError("linear_bwd_dw: invalid problem set")
     buf = (ws or Workspace(problems[0][0].device)).get(nbytes)
     if norm is None:
-        L.call("ppo_linear_bwd_dw", arr, len(items), rows, buf.data_ptr(), buf.numel(), _stream())
+        if bf16:
+            L.call("ppo_linear_bwd_dw_ex", arr, len(items), rows, L.GEMM_BF16_OPERANDS, buf.data_ptr(), buf.numel(),
+                   None, None, 0, None, _stream())
+        else:
+            L.call("ppo_linear_bwd_dw", arr, len(items), rows, buf.data_ptr(), buf.numel(), _stream())
         return
     p = norm.partials
     _dev(p, dtype=torch.float64)
@@ -408,9 +424,14 @@ def linear_bwd_dw(problems: list[tuple], rows: int, ws: Workspace | None = None,
         _dev(norm.extra_grads)
         if any(r.begin < 0 or r.end > norm.extra_grads.numel() for r in extra):
             raise ValueError("linear_bwd_dw: extra gradient range outside its buffer")
-    L.call("ppo_linear_bwd_dw_norm", arr, len(items), rows, buf.data_ptr(), buf.numel(),
-           _ptr(norm.extra_grads) if extra else None, L.array(L.GradRange, extra) if extra else None, len(extra),
-           p.data_ptr(), _stream())
+    if bf16:
+        L.call("ppo_linear_bwd_dw_ex", arr, len(items), rows, L.GEMM_BF16_OPERANDS, buf.data_ptr(), buf.numel(),
+               _ptr(norm.extra_grads) if extra else None, L.array(L.GradRange, extra) if extra else None, len(extra),
+               p.data_ptr(), _stream())
+    else:
+        L.call("ppo_linear_bwd_dw_norm", arr, len(items), rows, buf.data_ptr(), buf.numel(),
+               _ptr(norm.extra_grads) if extra else None, L.array(L.GradRange, extra) if extra else None, len(extra),
+               p.data_ptr(), _stream())
 
 
 # ----------------------------------------------------------------------------------------------------------------------

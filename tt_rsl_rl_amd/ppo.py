@@ -166,8 +166,6 @@ class PPO:
             raise NotImplementedError("multi-GPU training is not implemented by the HIP PPO plugin (single GPU)")
         if optimizer.lower() not in L.OPTIMIZERS:  # upstream's resolve_optimizer (rsl_rl/utils/utils.py:71-96)
             raise ValueError(f"Invalid optimizer '{optimizer.lower()}'. Valid optimizers are: {list(L.OPTIMIZERS)}")
-        if use_mixed_precision:
-            raise NotImplementedError("the HIP update computes in fp32; use_mixed_precision is not supported")
         if actor.is_recurrent != critic.is_recurrent:
             raise NotImplementedError("the HIP recurrent update needs both actor and critic recurrent (or neither)")
         if actor.distribution is None:
