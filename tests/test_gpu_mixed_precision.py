@@ -26,7 +26,7 @@ import pytest
 import torch
 
 from oracle import rollout as R
-from tests.parity import eval_observations, function_deviation, make_hip, make_pair, param_dict, rel_err
+from tests.parity import eval_observations, function_deviation, make_hip, param_dict, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -166,11 +166,21 @@ def test_bf16_flag_on_operands_outside_the_bf16_kernels_runs_fp32(cuda):
 # the update
 # ---------------------------------------------------------------------------------------------------------------------
 
+def _rnn(num_envs: int, steps: int, hidden: int, hidden_dims: list[int], layers: int = 1, rnn_type: str = "lstm"):
+    w = R.scaled(R.WORKLOADS["lstm256"], num_envs=num_envs, steps=steps, hidden_dims=hidden_dims)
+    w["rnn"] = dict(w["rnn"], rnn_hidden_dim=hidden, rnn_num_layers=layers, rnn_type=rnn_type)
+    return w
+
+
 MP_CASES = {
     "humanoid_1k": (R.scaled(R.WORKLOADS["humanoid"], num_envs=1024), {}),
     "rough235_512": (R.scaled(R.WORKLOADS["rough235"], num_envs=512), {}),
     "flat48_small_fixed": (R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[128, 64, 32]),
                            {"schedule": "fixed"}),
+    # recurrent: autocast also runs upstream's nn.LSTM / nn.GRU in bf16 (input and recurrent products); the plugin
+    # takes bf16 operands in the input projections and the heads, and keeps the recurrent product fp32
+    "lstm64_512": (_rnn(512, 16, 64, [64, 32]), {}),
+    "gru32x2_256_fixed": (_rnn(256, 10, 32, [32, 16], layers=2, rnn_type="gru"), {"schedule": "fixed"}),
 }
 
 
@@ -194,12 +204,13 @@ def test_mixed_precision_update_against_the_oracle(name):
     every trained one moved; and the same update without the flag is closer to the fp32 oracle, so the switch
     reached the kernels."""
     w, over = MP_CASES[name]
-    ora, hip, roll = make_pair(w, 0, use_mixed_precision=True, **over)
-    assert hip.use_mixed_precision and ora.use_mixed_precision
-    ora.use_mixed_precision = False
-    with torch.inference_mode():
+    ora, roll = R.generate(w, 0, **over)
+    with torch.inference_mode():  # (once: a recurrent critic's forward advances its hidden state)
         last_values = ora.critic(roll.last_obs).detach()
+    ora.compute_returns(roll.last_obs, last_values=last_values)
+    hip = _hip_twin(w, roll, last_values, use_mixed_precision=True, **over)
     hip32 = _hip_twin(w, roll, last_values, **over)
+    assert hip.use_mixed_precision and not hip32.use_mixed_precision and not ora.use_mixed_precision
     assert torch.equal(hip32.storage.advantages, hip.storage.advantages)
     p0, ev = param_dict(ora), eval_observations(ora)
     amp = copy.deepcopy(ora)
