@@ -560,6 +560,25 @@ int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_
 int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
                      int32_t* sync, int64_t sync_words, ppo_stream_t stream);
 
+/* The layer's input projection for ppo_lstm_seq_fwd_proj: gx = x w_ih_g^T + b_g over all T*E rows (the
+ * nn.LSTM / nn.GRU input products of rsl_rl/modules/rnn.py:35-52 in the gate-interleaved layout). */
+typedef struct ppo_lstm_input_projection {
+  const float* x; int64_t ldx;               /* [T*E, input_size] the layer's input, row t*E + e */
+  const float* w_ih_g;                       /* [4H, input_size] gate-interleaved (ppo_lstm_pack / ppo_gru_pack) */
+  const float* b_g;                          /* [4H] */
+  int32_t input_size;
+  int32_t reserved;
+} ppo_lstm_input_projection;
+
+/* ppo_lstm_seq_fwd with the input projection done by the call itself: gx is computed as ppo_linear_fwd_ex(x, w_ih_g,
+ * b_g, no activation, flags) would compute it (flags: 0 or PPO_GEMM_BF16_OPERANDS), bit for bit.  For inputs of up to
+ * 48 columns (a multiple of 16) with 16-byte rows, in a one-launch sequence, it runs inside that launch (each step's
+ * products in the time its blocks wait for each other) and gx is left unwritten; otherwise as its own launch into gx
+ * before the steps.  The problems' gx is scratch: its contents afterwards are unspecified. */
+int ppo_lstm_seq_fwd_proj(const ppo_lstm_seq_problem* problems, const ppo_lstm_input_projection* proj, int32_t count,
+                          int64_t steps, int64_t envs, int32_t flags, int32_t* sync, int64_t sync_words,
+                          ppo_stream_t stream);
+
 /* How long the blocks of a whole-sequence launch wait for each other before they give up and set the status word,
  * in ticks of the 100 MHz device clock, for every later launch of this process: ticks >= 0 sets that limit, ticks < 0
  * restores the default (200,000,000 = 2 s).  Returns the limit in force before the call.  A test hook (0 forces the

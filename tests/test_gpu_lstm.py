@@ -305,3 +305,49 @@ def test_sequence_wait_gives_up_and_the_update_raises(cuda):
     assert all(torch.isfinite(torch.tensor(v)) for v in out.values())
     assert hip._opt_steps == steps + hip.num_learning_epochs * hip.num_mini_batches
     assert not torch.equal(before[0], hip.flat.param)
+
+
+@pytest.mark.parametrize("T,E,H,D,count,gru,bf16", [
+    (24, 1024, 256, 48, 2, False, False), (24, 1024, 256, 48, 2, True, True), (9, 200, 64, 32, 1, False, False),
+    (5, 70, 96, 16, 2, False, True), (4, 8192, 256, 48, 2, False, False), (6, 65, 32, 64, 2, True, False),
+    (7, 100, 64, 20, 1, False, False), (1, 100, 128, 48, 2, False, False)])
+def test_sequence_with_input_projection_matches_the_separate_projection(cuda, T, E, H, D, count, gru, bf16):
+    """ppo_lstm_seq_fwd_proj (the input projection done by the sequence call: inside the one-launch sequence for
+    inputs of up to 48 columns in 16-column slabs, else as its own launch) gives bit for bit the outputs of
+    ppo_linear_fwd(_ex) into gx followed by ppo_lstm_seq_fwd, in the one-launch and the per-step modes, with fp32
+    and bf16 operands; x read as a column block of a wider table, as the update reads it.  64 and 20 columns and a
+    single step take the separate launch inside the call."""
+    from tt_rsl_rl_amd import _lib as L
+    from tt_rsl_rl_amd import ops
+
+    dev = cuda
+    gen = torch.Generator().manual_seed(T * 13 + E + H + D)
+    G = (3 if gru else 4) * H
+    R = T * E
+    qs, xs = [], []
+    for i in range(count):
+        pk = ops.LstmPacked(D, H, dev)
+        w = [torch.randn(G, D, generator=gen) / math.sqrt(D), torch.randn(G, H, generator=gen) / math.sqrt(H),
+             torch.randn(G, generator=gen) * 0.1, torch.randn(G, generator=gen) * 0.1]
+        ops.lstm_pack([(*(t.to(dev) for t in w), pk)], gru=gru)
+        table = torch.randn(R, 8 + (D + 3) // 4 * 4 + 12, generator=gen).to(dev)
+        xs.append(table[:, 8:8 + D])
+        dones = (torch.rand(R, generator=gen) < 0.05).float()
+        h0 = (torch.randn(E, H, generator=gen) * 0.5).to(dev)
+        c0 = h0 if gru else (torch.randn(E, H, generator=gen) * 0.5).to(dev)
+        qs.append(dict(packed=pk, hidden=H, gx=torch.full((R, 4 * H), float("nan"), device=dev), h0=h0, c0=c0,
+                       keep=(1.0 - dones).to(dev), gru=gru))
+    # reference: the projection as its own GEMM launch, then the sequence on gx
+    ref = [_outputs(q, T, E, H, dev) for q in qs]
+    ops.linear_fwd([(x, q["packed"].w_ih_g, q["packed"].b_g, q["gx"], None) for q, x in zip(ref, xs)], R,
+                   act=L.PPO_ACT_NONE, bf16=bf16)
+    sync = torch.zeros(ops.lstm_seq_sync_words(count, E), dtype=torch.int32, device=dev)
+    ops.lstm_seq_fwd(ref, T, E, sync)
+    for mode in ("one_launch", "per_step"):
+        got = [_outputs(dict(q, gx=torch.full((R, 4 * H), float("nan"), device=dev)), T, E, H, dev) for q in qs]
+        ops.lstm_seq_fwd(got, T, E, sync if mode == "one_launch" else None, proj=xs, bf16=bf16)
+        torch.cuda.synchronize()
+        assert int(sync[0]) == 0
+        for a, b in zip(ref, got):
+            for k in ("h", "c", "gates", "hs"):
+                assert torch.equal(a[k], b[k]), (mode, k)

@@ -64,6 +64,7 @@ STRUCTS = {
     "ppo_lstm_seq_problem": ("LstmSeqProblem", ["w_hh_g", "w_hh_gt", "gx", "ldgx", "h0", "c0", "ld0", "keep",
                                                 "keep_stride", "h", "ldh", "hs", "c", "gates", "dh", "lddh",
                                                 "dgates", "dc", "hidden", "cell"]),
+    "ppo_lstm_input_projection": ("LstmInputProjection", ["x", "ldx", "w_ih_g", "b_g", "input_size", "reserved"]),
     "ppo_lstm_grad_problem": ("LstmGradProblem", ["dw_ih_g", "dw_hh_g", "db_g", "dw_ih", "dw_hh", "db_ih", "db_hh",
                                                   "input_size", "hidden"]),
 }
@@ -73,7 +74,8 @@ STRUCTS = {
 CONSTANTS = {"PPO_MAX_GATHER_SEGMENTS": "MAX_GATHER_SEGMENTS", "PPO_MAX_INTERLEAVE_FLOATS": "MAX_INTERLEAVE_FLOATS", "PPO_MAX_LINEAR_PROBLEMS": "MAX_LINEAR_PROBLEMS",
              "PPO_MAX_PARAM_GROUPS": "MAX_PARAM_GROUPS", "PPO_DW_NORM_BLOCKS": "DW_NORM_BLOCKS",
              "PPO_MAX_EXTRA_GRADS": "MAX_EXTRA_GRADS", "PPO_ADAM_STATIC_SCRATCH_DOUBLES": "ADAM_STATIC_SCRATCH_DOUBLES",
-             "PPO_ADAM_STATIC_MAX_PARAMS": "ADAM_STATIC_MAX_PARAMS", "PPO_MAX_PARAM_MIRRORS": "MAX_PARAM_MIRRORS"}
+             "PPO_ADAM_STATIC_MAX_PARAMS": "ADAM_STATIC_MAX_PARAMS", "PPO_MAX_PARAM_MIRRORS": "MAX_PARAM_MIRRORS",
+             "PPO_GEMM_BF16_OPERANDS": "GEMM_BF16_OPERANDS"}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
@@ -173,6 +175,20 @@ def test_argument_validation_reports_errors_without_a_gpu():
                                keep_stride=1, h=16, ldh=256, hs=16, c=16, gates=16, hidden=256)
     with pytest.raises(ValueError, match="sync buffer"):
         _lib.call("ppo_lstm_seq_fwd", ctypes.byref(full), 1, 24, 1024, 16, 32 + 16 * 32 - 1, None)
+    # with the input projection: the projections, a known flag, pointers, input size and leading dimension, all
+    # checked before any launch
+    with pytest.raises(ValueError, match="projections are required"):
+        _lib.call("ppo_lstm_seq_fwd_proj", ctypes.byref(full), None, 1, 24, 1024, 0, None, 0, None)
+    proj = _lib.LstmInputProjection(x=16, ldx=48, w_ih_g=16, b_g=16, input_size=48)
+    with pytest.raises(ValueError, match="flags=2"):
+        _lib.call("ppo_lstm_seq_fwd_proj", ctypes.byref(full), ctypes.byref(proj), 1, 24, 1024, 2, None, 0, None)
+    for bad_proj, msg in ((_lib.LstmInputProjection(x=16, ldx=48, w_ih_g=16, b_g=None, input_size=48), "null pointer"),
+                          (_lib.LstmInputProjection(x=16, ldx=32, w_ih_g=16, b_g=16, input_size=48),
+                           "input_size=48 ldx=32"),
+                          (_lib.LstmInputProjection(x=16, ldx=48, w_ih_g=16, b_g=16, input_size=0), "input_size=0")):
+        with pytest.raises(ValueError, match=msg):
+            _lib.call("ppo_lstm_seq_fwd_proj", ctypes.byref(full), ctypes.byref(bad_proj), 1, 24, 1024, 0, None, 0,
+                      None)
     pack = _lib.LstmPackProblem(8, 8, 8, 8, 8, 8, 8, 8, 48, 250)
     with pytest.raises(ValueError, match="sizes"):
         _lib.call("ppo_lstm_pack", ctypes.byref(pack), 1, None)

@@ -141,6 +141,10 @@ class LstmSeqProblem(C.Structure):
                 ("dh", vp), ("lddh", i64), ("dgates", vp), ("dc", vp), ("hidden", i32), ("cell", i32)]
 
 
+class LstmInputProjection(C.Structure):
+    _fields_ = [("x", vp), ("ldx", i64), ("w_ih_g", vp), ("b_g", vp), ("input_size", i32), ("reserved", i32)]
+
+
 class LstmGradProblem(C.Structure):
     _fields_ = [("dw_ih_g", vp), ("dw_hh_g", vp), ("db_g", vp), ("dw_ih", vp), ("dw_hh", vp), ("db_ih", vp),
                 ("db_hh", vp), ("input_size", i32), ("hidden", i32)]
@@ -160,6 +164,8 @@ _SIGNATURES = [
     ("ppo_lstm_seq_wait_limit", i64, [i64]),
     ("ppo_lstm_seq_fwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_seq_bwd", C.c_int, [C.POINTER(LstmSeqProblem), i32, i64, i64, C.c_void_p, i64, C.c_void_p]),
+    ("ppo_lstm_seq_fwd_proj", C.c_int, [C.POINTER(LstmSeqProblem), C.POINTER(LstmInputProjection), i32, i64, i64, i32,
+                                        C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
     ("ppo_gru_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
     ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),

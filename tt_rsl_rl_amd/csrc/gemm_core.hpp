@@ -100,7 +100,7 @@ struct Problem {
 __device__ __forceinline__ float sigmoid_hw(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.44269504088896341f));
 }
-__device__ __forceinline__ float tanh_hw(float x) { return 2.0f * sigmoid_hw(2.0f * x) - 1.0f; }
+__device__ __forceinline__ float tanh_hw(float x) { return __builtin_fmaf(2.0f, sigmoid_hw(2.0f * x), -1.0f); }
 
 // ELU (alpha 1) of the forward epilogue: x for x > 0, else expm1(x), from two published pieces: on [-0.7, 0] the
 // Taylor series of expm1 to degree 9 (x + x^2 (1/2! + x/3! + ... + x^7/9!), truncation below 1e-8 relative), below
@@ -506,7 +506,7 @@ __device__ __forceinline__ LstmCellFwd lstm_cell_fwd(const f32x4& x, const f32x4
   LstmCellFwd o;
   const float ig = sigmoid_hw(x[0] + gx[0]), fg = sigmoid_hw(x[1] + gx[1]);
   const float gg = tanh_hw(x[2] + gx[2]), og = sigmoid_hw(x[3] + gx[3]);
-  o.c = fg * cp + ig * gg;
+  o.c = __builtin_fmaf(fg, cp, ig * gg);  // (explicit: every kernel that inlines the cell rounds it the same way)
   o.h = og * tanh_hw(o.c);
   o.act = f32x4{ig, fg, gg, og};
   return o;
@@ -523,8 +523,8 @@ __device__ __forceinline__ LstmCellFwd gru_cell_fwd(const f32x4& x, const f32x4&
   LstmCellFwd o;
   const float r = sigmoid_hw(x[0] + gx[0]), z = sigmoid_hw(x[1] + gx[1]);
   const float a = x[2] + gx[2];
-  const float n = tanh_hw((x[3] + gx[3]) + r * a);
-  o.h = n + z * (hp - n);
+  const float n = tanh_hw(__builtin_fmaf(r, a, x[3] + gx[3]));
+  o.h = __builtin_fmaf(z, hp - n, n);
   o.c = o.h;
   o.act = f32x4{r, z, a, n};
   return o;

@@ -1,7 +1,8 @@
 // A15 LSTM of the recurrent models (torch nn.LSTM; rsl_rl/modules/rnn.py:22-86) on gfx950.  Every entry point
 // works on one layer; stacked layers are run one after another by the caller (layer k's input = layer k-1's h).
 //
-// The input projection x w_ih^T + b of all T steps is one GEMM (ppo_linear_fwd on the gate-interleaved weights).
+// The input projection x w_ih^T + b of all T steps is one GEMM (ppo_linear_fwd on the gate-interleaved weights), or,
+// for inputs of at most 64 columns, part of the whole-sequence forward launch (ppo_lstm_seq_fwd_proj).
 // The recurrence is one kernel per step: the NT GEMM of gemm_core.hpp computes hs[t] w_hh_g^T (rows = envs,
 // columns = gates of 4 hidden units per 16-byte group) and its LSTM epilogue applies the cell equations
 // (i, f, o = sigmoid, g = tanh; c_t = f c_{t-1} + i g; h_t = o tanh(c_t)), writing the activations for the backward
@@ -164,8 +165,16 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 //
 // The MFMA sequence per accumulator (32-deep k slabs, k-groups of 8, element s of the f32x4 fragments) and the cell
 // arithmetic are those of the per-step kernel on 64 x 64 tiles, so both paths give identical results.
+//
+// PROJ: the input projection gx = x w_ih_g^T + b_g of the lane's cell outputs is computed in the launch with the
+// projection GEMM's own arithmetic (gemm_nt_bx6_kernel: each operand element split into three bf16 parts, or rounded
+// to bf16 alone in the bf16-operand mode; the six products of a 16-deep k-slab in that kernel's order with the
+// weights as the first operand, slabs in order, then + b_g), so gx is bit for bit what ppo_linear_fwd(_ex) writes.
+// A step's x rows and the block's w_ih_g rows (L2-resident) are loaded at the top of the previous step, split and
+// multiplied after that step's signal, in the time the row group's blocks take to see each other's counts.
 constexpr int kSeqRows = 64, kSeqCols = 64, kSeqBK = 32;
 constexpr int kSeqMaxSlabs = 8;  // H <= 256: the w_hh_g slice is 64 KB of LDS, two blocks per CU
+constexpr int kSeqProjSlabs = 3;  // fused input projection: inputs of at most 3 16-deep k-slabs (48 columns)
 constexpr int kSyncHeader = 32;  // int32 words ahead of the row-group lines: [0] status (sticky), [1] abort
 constexpr int kSyncStride = 32;  // one 128-byte line per row group: [0] counter, [16 + j] XCD of block j
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data (gfx9 family)
@@ -175,6 +184,11 @@ constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock (p
 struct SeqFwdItem {
   const float* w;  // w_hh_g [4H, H]
   const float* gx;
+  const float* x;    // fused projection: the layer input [T*E, D] (ld ldx), w_ih_g [4H, D], b_g [4H]
+  const float* wih;
+  const float* bg;
+  int64_t ldx;
+  int32_t kp;        // D / 16
   const float* c0;
   const float* keep;
   float* gates;
@@ -189,6 +203,7 @@ struct SeqFwdArgs {
   uint64_t spin_ticks;
   int32_t H, E, T, nrg, ncb, slots;
   int32_t xcds;  // XCDs of the device (block b runs on XCD b % xcds)
+  int32_t bf16;  // fused projection with bf16 operands (PPO_GEMM_BF16_OPERANDS)
 };
 
 // Zeroes the abort word and the counters of one sequence call (the status word stays).
@@ -233,6 +248,19 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x4 trade_halves(const float (&x)[4], int hl) {
   const float r0 = __shfl_xor(hl ? x[0] : x[2], 32), r1 = __shfl_xor(hl ? x[1] : x[3], 32);
   return hl ? f32x4{r0, x[2], r1, x[3]} : f32x4{x[0], r0, x[1], r1};
+}
+
+// Eight consecutive k of one MFMA operand row (v0: k 0..3, v1: k 4..7) as a 32x32x16 bf16 fragment in each of its
+// three bf16 parts, split as the bf16x6 GEMMs' staging splits them (split_bf16x3 on consecutive pairs).
+__device__ __forceinline__ void split_frag(const f32x4& v0, const f32x4& v1, bf16x8 (&part)[3]) {
+  uint32_t h[4], m[4], l[4];
+  split_bf16x3(v0[0], v0[1], h[0], m[0], l[0]);
+  split_bf16x3(v0[2], v0[3], h[1], m[1], l[1]);
+  split_bf16x3(v1[0], v1[1], h[2], m[2], l[2]);
+  split_bf16x3(v1[2], v1[3], h[3], m[3], l[3]);
+  part[0] = __builtin_bit_cast(bf16x8, u32x4{h[0], h[1], h[2], h[3]});
+  part[1] = __builtin_bit_cast(bf16x8, u32x4{m[0], m[1], m[2], m[3]});
+  part[2] = __builtin_bit_cast(bf16x8, u32x4{l[0], l[1], l[2], l[3]});
 }
 
 // This wave's XCD (accelerator complex die): the hardware register XCC_ID.
@@ -281,7 +309,7 @@ __device__ __forceinline__ void seq_signal(int32_t* ctr) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NS, bool GRU>
+template <int NS, bool GRU, bool PROJ>
 __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
   constexpr int BK = kSeqBK, WSLAB = kSeqCols * BK, ASLAB = kSeqRows * BK;
   __shared__ __align__(16) float wl[NS * WSLAB];
@@ -303,6 +331,10 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
   }
   // the lane's cell outputs: env row wm*32 + lane%32 of the tile, gate columns ncol + 8q (q = 0..3) = 4 units
   const int ncol = n0 + wn * 32 + 4 * hl;
+  // PROJ: the wave's w_ih_g rows (gate columns n0 + wn*32 + lane%32), k 8 (lane/32) .. + 7 of each 16-deep slab
+  constexpr int KPM = PROJ ? kSeqProjSlabs : 1;
+  [[maybe_unused]] const float* const wr =
+      PROJ ? S.wih + static_cast<int64_t>(n0 + wn * 32 + (lane & 31)) * (16 * S.kp) + 8 * hl : nullptr;
   int32_t* const ctr0 = a.sync + kSyncHeader + p * a.nrg * kSyncStride;
   volatile float* const flag = al + ASLAB;  // free between a step's last barrier and the next wait's barrier
   for (int rg = g; rg < a.nrg; rg += a.slots) {
@@ -326,11 +358,62 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
       aoff[j] = std::min<int64_t>(m0 + row, E - 1) * H + 4 * cc;
       lofs[j] = row * BK + 4 * (cc ^ nt_swz<BK>(row));
     }
+    // PROJ: the operands of a step's input projection (its x row of the lane, the block's w_ih_g rows, the bias) are
+    // loaded a step ahead, at the top of the previous step (whose hs stores and signal then find them landed), and
+    // multiplied after that step's signal, while the row group's other blocks pick the signal up
+    [[maybe_unused]] f32x4 xr[KPM][2], wv[KPM][2], pbias[4];
+    auto proj_load = [&](int64_t row) __attribute__((always_inline)) {
+      const float* const xp = S.x + row * S.ldx + 8 * hl;
+#pragma unroll
+      for (int kt = 0; kt < KPM; ++kt) {
+        if (kt < S.kp) {
+          xr[kt][0] = *reinterpret_cast<const f32x4*>(xp + 16 * kt);
+          xr[kt][1] = *reinterpret_cast<const f32x4*>(xp + 16 * kt + 4);
+          wv[kt][0] = *reinterpret_cast<const f32x4*>(wr + 16 * kt);
+          wv[kt][1] = *reinterpret_cast<const f32x4*>(wr + 16 * kt + 4);
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pbias[q] = *reinterpret_cast<const f32x4*>(S.bg + ncol + 8 * q);
+    };
+    auto proj_compute = [&](f32x4 (&out)[4]) __attribute__((always_inline)) {
+      f32x16 pacc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) pacc[v] = 0.0f;
+      constexpr int pa[6] = {2, 1, 0, 1, 0, 0}, pb[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+      for (int kt = 0; kt < KPM; ++kt) {
+        if (kt < S.kp) {
+          bf16x8 xpl[3], wpl[3];
+          split_frag(xr[kt][0], xr[kt][1], xpl);
+          split_frag(wv[kt][0], wv[kt][1], wpl);
+          if (a.bf16) {
+            pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wpl[0], xpl[0], pacc, 0, 0, 0);
+          } else {
+#pragma unroll
+            for (int u = 0; u < 6; ++u)
+              pacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wpl[pb[u]], xpl[pa[u]], pacc, 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[q][e] = pacc[4 * q + e] + pbias[q][e];
+    };
+    f32x4 gx[4];
+    if constexpr (PROJ) {  // step 0's
+      proj_load(mc);
+      proj_compute(gx);
+    }
     for (int t = 0; t < a.T; ++t) {
       const int64_t rowt = static_cast<int64_t>(t) * E + mc;
-      f32x4 gx[4];
+      if constexpr (PROJ) {
+        if (t + 1 < a.T) proj_load(rowt + E);
+      } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) gx[q] = *reinterpret_cast<const f32x4*>(S.gx + rowt * S.ldgx + ncol + 8 * q);
+        for (int q = 0; q < 4; ++q) gx[q] = *reinterpret_cast<const f32x4*>(S.gx + rowt * S.ldgx + ncol + 8 * q);
+      }
       const float keep = S.keep[rowt * S.keep_stride];
       if (t > 0) {
         if (!seq_wait(a.sync, line, a.ncb * t, flag, a.spin_ticks)) return;
@@ -410,6 +493,9 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
         }
       }
       if (t + 1 < a.T) seq_signal(line);
+      if constexpr (PROJ) {
+        if (t + 1 < a.T) proj_compute(gx);  // the next step's (the cell is done with this one's)
+      }
       if (in) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) *reinterpret_cast<f32x4*>(S.gates + rowt * 4 * H + ncol + 8 * q) = act[q];
@@ -670,10 +756,10 @@ uint64_t seq_spin_ticks() {
 
 // Launches the whole-sequence forward when the shape allows it and the device holds at least one row-group slot
 // (count * ncb blocks) at once.  Returns PPO_OK, an error, or PPO_EUNSUPPORTED to ask for the per-step launches.
-template <int NS, bool GRU>
+template <int NS, bool GRU, bool PROJ>
 int launch_seq_fwd(SeqFwdArgs& a, int count, hipStream_t s) {
   static std::atomic<int> cache[kMaxDevices];
-  const int resident = resident_blocks(lstm_seq_fwd_kernel<NS, GRU>, cache);
+  const int resident = resident_blocks(lstm_seq_fwd_kernel<NS, GRU, PROJ>, cache);
   const int per_slot = count * a.ncb;
   const int slots = std::min(a.nrg, resident / per_slot);
   if (slots < 1) return PPO_EUNSUPPORTED;
@@ -681,26 +767,27 @@ int launch_seq_fwd(SeqFwdArgs& a, int count, hipStream_t s) {
   hipLaunchKernelGGL(seq_sync_reset_kernel, dim3(1), dim3(256), 0, s, a.sync,
                      static_cast<int32_t>(kSyncHeader + count * a.nrg * kSyncStride));
   if (int rc = check_launch("seq_sync_reset_kernel")) return rc;
-  hipLaunchKernelGGL((lstm_seq_fwd_kernel<NS, GRU>), dim3(count * slots * a.ncb), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((lstm_seq_fwd_kernel<NS, GRU, PROJ>), dim3(count * slots * a.ncb), dim3(256), 0, s, a);
   return check_launch("lstm_seq_fwd_kernel");
 }
 
-template <bool GRU>
+template <bool GRU, bool PROJ>
 int seq_fwd_slabs(SeqFwdArgs& a, int64_t H, int count, hipStream_t s) {
   switch (H / kSeqBK) {
-    case 1: return launch_seq_fwd<1, GRU>(a, count, s);
-    case 2: return launch_seq_fwd<2, GRU>(a, count, s);
-    case 3: return launch_seq_fwd<3, GRU>(a, count, s);
-    case 4: return launch_seq_fwd<4, GRU>(a, count, s);
-    case 5: return launch_seq_fwd<5, GRU>(a, count, s);
-    case 6: return launch_seq_fwd<6, GRU>(a, count, s);
-    case 7: return launch_seq_fwd<7, GRU>(a, count, s);
-    default: return launch_seq_fwd<8, GRU>(a, count, s);
+    case 1: return launch_seq_fwd<1, GRU, PROJ>(a, count, s);
+    case 2: return launch_seq_fwd<2, GRU, PROJ>(a, count, s);
+    case 3: return launch_seq_fwd<3, GRU, PROJ>(a, count, s);
+    case 4: return launch_seq_fwd<4, GRU, PROJ>(a, count, s);
+    case 5: return launch_seq_fwd<5, GRU, PROJ>(a, count, s);
+    case 6: return launch_seq_fwd<6, GRU, PROJ>(a, count, s);
+    case 7: return launch_seq_fwd<7, GRU, PROJ>(a, count, s);
+    default: return launch_seq_fwd<8, GRU, PROJ>(a, count, s);
   }
 }
 
-int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t envs, int32_t* sync,
-            hipStream_t s) {
+// proj: the problems' input projections computed in the launch (nullptr: gx is read); bf16: their operands in bf16
+int seq_fwd(const ppo_lstm_seq_problem* probs, const ppo_lstm_input_projection* proj, bool bf16, int count,
+            int64_t steps, int64_t envs, int32_t* sync, hipStream_t s) {
   const int64_t H = probs[0].hidden;
   if (H % kSeqBK != 0 || H / kSeqBK > kSeqMaxSlabs) return PPO_EUNSUPPORTED;
   SeqFwdArgs a{};
@@ -710,7 +797,12 @@ int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
     it.w = q.w_hh_g; it.gx = q.gx; it.c0 = q.c0; it.keep = q.keep;
     it.gates = q.gates; it.c = q.c; it.h = q.h; it.hs = q.hs;
     it.ldgx = q.ldgx; it.ld0 = q.ld0; it.keep_stride = q.keep_stride; it.ldh = q.ldh;
+    if (proj != nullptr) {
+      it.x = proj[i].x; it.ldx = proj[i].ldx; it.wih = proj[i].w_ih_g; it.bg = proj[i].b_g;
+      it.kp = proj[i].input_size / 16;
+    }
   }
+  a.bf16 = bf16 ? 1 : 0;
   a.sync = sync;
   a.spin_ticks = seq_spin_ticks();
   a.xcds = std::max(device_info().xcds, 1);
@@ -719,7 +811,9 @@ int seq_fwd(const ppo_lstm_seq_problem* probs, int count, int64_t steps, int64_t
   a.T = static_cast<int32_t>(steps);
   a.nrg = static_cast<int32_t>(seq_row_groups(envs));
   a.ncb = static_cast<int32_t>(4 * H / kSeqCols);
-  return probs[0].cell == PPO_CELL_GRU ? seq_fwd_slabs<true>(a, H, count, s) : seq_fwd_slabs<false>(a, H, count, s);
+  const bool gru = probs[0].cell == PPO_CELL_GRU;
+  if (proj != nullptr) return gru ? seq_fwd_slabs<true, true>(a, H, count, s) : seq_fwd_slabs<false, true>(a, H, count, s);
+  return gru ? seq_fwd_slabs<true, false>(a, H, count, s) : seq_fwd_slabs<false, false>(a, H, count, s);
 }
 
 template <int NS, bool GRU>
@@ -861,11 +955,57 @@ extern "C" int64_t ppo_lstm_seq_wait_limit(int64_t ticks) {
   return previous < 0 ? static_cast<int64_t>(kSeqSpinTicks) : previous;
 }
 
-extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
-                                int32_t* sync, int64_t sync_words, ppo_stream_t stream) {
-  if (int rc = check_seq(problems, count, steps, envs, false, "ppo_lstm_seq_fwd")) return rc;
-  if (int rc = check_sync(sync, sync_words, count, envs, "ppo_lstm_seq_fwd")) return rc;
+namespace ppo {
+namespace {
+
+// The input projections can be computed inside the whole-sequence launch with exactly the arithmetic of the
+// projection GEMM: inputs of 16..64 columns (a multiple of 16) and every operand as the bf16x6 GEMM takes it
+// (16-byte rows: x, w_ih_g, b_g, gx), so that ppo_linear_fwd(_ex) would run the bf16x6 kernel on them.
+bool proj_fusable(const ppo_lstm_seq_problem* probs, const ppo_lstm_input_projection* proj, int count,
+                  int64_t steps, int64_t envs) {
+  for (int i = 0; i < count; ++i) {
+    const ppo_lstm_input_projection& r = proj[i];
+    const int64_t rows = steps * envs;
+    if (r.input_size % 16 != 0 || r.input_size > 16 * kSeqProjSlabs) return false;
+    if (!w16_ok(r.x, r.ldx) || !w16_ok(r.w_ih_g, r.input_size) || !aligned16(r.b_g)) return false;
+    if (!w16_ok(probs[i].gx, probs[i].ldgx) || rows * probs[i].ldgx * 4 >= (int64_t(1) << 31)) return false;
+    if (rows * r.ldx >= (int64_t(1) << 30)) return false;
+  }
+  return true;
+}
+
+// gx = x w_ih_g^T + b_g for every problem, as ppo_linear_fwd_ex.
+int launch_projections(const ppo_lstm_seq_problem* probs, const ppo_lstm_input_projection* proj, int count,
+                       int64_t rows, int32_t flags, ppo_stream_t stream) {
+  ppo_linear_fwd_problem lp[PPO_MAX_LSTM_PROBLEMS]{};
+  for (int i = 0; i < count; ++i) {
+    lp[i].x = proj[i].x; lp[i].ldx = proj[i].ldx;
+    lp[i].w = proj[i].w_ih_g; lp[i].b = proj[i].b_g;
+    lp[i].z = const_cast<float*>(probs[i].gx); lp[i].ldz = probs[i].ldgx;
+    lp[i].in_features = proj[i].input_size;
+    lp[i].out_features = static_cast<int32_t>(4 * probs[i].hidden);
+  }
+  return ppo_linear_fwd_ex(lp, count, rows, PPO_ACT_NONE, flags, stream);
+}
+
+int seq_fwd_entry(const ppo_lstm_seq_problem* problems, const ppo_lstm_input_projection* proj, int32_t flags,
+                  int32_t count, int64_t steps, int64_t envs, int32_t* sync, int64_t sync_words,
+                  ppo_stream_t stream, const char* who) {
+  if (int rc = check_seq(problems, count, steps, envs, false, who)) return rc;
+  if (int rc = check_sync(sync, sync_words, count, envs, who)) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  bool fuse = false;
+  if (proj != nullptr) {
+    PPO_REQUIRE((flags & ~PPO_GEMM_BF16_OPERANDS) == 0, "%s: flags=%d", who, flags);
+    for (int i = 0; i < count; ++i) {
+      const ppo_lstm_input_projection& r = proj[i];
+      PPO_REQUIRE(r.x != nullptr && r.w_ih_g != nullptr && r.b_g != nullptr, "%s: projection %d has a null pointer",
+                  who, i);
+      PPO_REQUIRE(r.input_size > 0 && r.ldx >= r.input_size, "%s: projection %d: input_size=%d ldx=%lld", who, i,
+                  r.input_size, (long long)r.ldx);
+    }
+    fuse = sync != nullptr && steps > 1 && proj_fusable(problems, proj, count, steps, envs);
+  }
   const int64_t E = envs;
   CopyGroup cg{};
   int64_t total = 0;
@@ -882,8 +1022,15 @@ extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t co
   cg.total = total;
   hipLaunchKernelGGL(lstm_copy_state_kernel, dim3(grid_for(total)), dim3(256), 0, s, cg);
   if (int rc = check_launch("lstm_copy_state_kernel")) return rc;
+  if (fuse) {
+    const int rc = seq_fwd(problems, proj, (flags & PPO_GEMM_BF16_OPERANDS) != 0, count, steps, envs, sync, s);
+    if (rc != PPO_EUNSUPPORTED) return rc;
+  }
+  if (proj != nullptr) {  // the projections as their own launch, then the sequence on gx
+    if (int rc = launch_projections(problems, proj, count, steps * E, flags, stream)) return rc;
+  }
   if (sync != nullptr && steps > 1) {
-    const int rc = seq_fwd(problems, count, steps, envs, sync, s);
+    const int rc = seq_fwd(problems, nullptr, false, count, steps, envs, sync, s);
     if (rc != PPO_EUNSUPPORTED) return rc;
   }
   for (int64_t t = 0; t < steps; ++t) {
@@ -914,6 +1061,21 @@ extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t co
     if (int rc = launch_step<EPI_LSTM_FWD>(g, count, s, "lstm_step_fwd")) return rc;
   }
   return PPO_OK;
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_lstm_seq_fwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,
+                                int32_t* sync, int64_t sync_words, ppo_stream_t stream) {
+  return seq_fwd_entry(problems, nullptr, 0, count, steps, envs, sync, sync_words, stream, "ppo_lstm_seq_fwd");
+}
+
+extern "C" int ppo_lstm_seq_fwd_proj(const ppo_lstm_seq_problem* problems, const ppo_lstm_input_projection* proj,
+                                     int32_t count, int64_t steps, int64_t envs, int32_t flags, int32_t* sync,
+                                     int64_t sync_words, ppo_stream_t stream) {
+  PPO_REQUIRE(proj != nullptr, "ppo_lstm_seq_fwd_proj: projections are required");
+  return seq_fwd_entry(problems, proj, flags, count, steps, envs, sync, sync_words, stream, "ppo_lstm_seq_fwd_proj");
 }
 
 extern "C" int ppo_lstm_seq_bwd(const ppo_lstm_seq_problem* problems, int32_t count, int64_t steps, int64_t envs,

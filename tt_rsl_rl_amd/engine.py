@@ -791,6 +791,15 @@ class RecurrentUpdateEngine(UpdateEngine):
             for q in qs:
                 fn([q], self.T, E, self.lstm_sync)
 
+    def _grouped_fwd(self, qs: list[dict], xs: list[torch.Tensor], E: int, bf16: bool) -> None:
+        """The forward sequences of one layer with their input projections (x_i: problem i's layer input), grouped
+        as _grouped groups them."""
+        if len(qs) == 2 and qs[0]["hidden"] == qs[1]["hidden"] and qs[0]["gru"] == qs[1]["gru"]:
+            ops.lstm_seq_fwd(qs, self.T, E, self.lstm_sync, proj=xs, bf16=bf16)
+        else:
+            for q, x in zip(qs, xs):
+                ops.lstm_seq_fwd([q], self.T, E, self.lstm_sync, proj=[x], bf16=bf16)
+
     def _layer_inputs(self, xa: torch.Tensor, xc: torch.Tensor, R: int) -> list[list[tuple]]:
         """Per layer k (bottom first): (model, side, buffers, the layer's input rows) of each model that has layer k;
         layer 0 reads the observations, layer k > 0 the h of layer k - 1."""
@@ -827,10 +836,10 @@ class RecurrentUpdateEngine(UpdateEngine):
         layers = self._layer_inputs(xa, xc, R)
         seqs = []
         for row in layers:
-            ops.linear_fwd([(x, b.packed.w_ih_g, b.packed.b_g, b.gx[:R], None) for _, _, b, x in row], R,
-                           act=L.PPO_ACT_NONE, bf16=alg.use_mixed_precision)
+            # the input projection gx = x w_ih_g^T + b_g goes with the sequence call (inside the one-launch sequence
+            # for narrow inputs, else its own launch first: the same values either way)
             qs = [self._seq(m, side, b, e0, e0 + E, tab) for m, side, b, _ in row]
-            self._grouped(ops.lstm_seq_fwd, qs, E)
+            self._grouped_fwd(qs, [x for _, _, _, x in row], E, alg.use_mixed_precision)
             seqs.append(qs)
         tm.stop("lstm_fwd")
 

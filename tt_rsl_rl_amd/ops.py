@@ -774,14 +774,30 @@ def _sync_args(sync: torch.Tensor | None, count: int, envs: int) -> tuple[int, i
     return sync.data_ptr(), sync.numel()
 
 
-def lstm_seq_fwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor | None = None) -> None:
+def lstm_seq_fwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor | None = None,
+                 proj: list[torch.Tensor] | None = None, bf16: bool = False) -> None:
     """problems: dicts with packed (LstmPacked), hidden, gx [T*E, 4H], h0 / c0 [E, H], keep [T*E] (stride = row
     step), h [T*E, H], hs [(T+1)*E, H], c [T*E, H], gates [T*E, 4H], and gru=True for a GRU (c0 = h0; c receives
     the state h).  sync: int32 device buffer of
     lstm_seq_sync_words(len(problems), envs) words (zeroed once by the caller) for the one-launch sequence, or None
-    for one launch per step."""
+    for one launch per step.  proj: each problem's layer input x [T*E, D]: the call computes gx = x w_ih_g^T + b_g
+    itself (ppo_lstm_seq_fwd_proj; inside the sequence launch when it can, gx is then scratch), with bf16 operands
+    when bf16."""
     arr = L.array(L.LstmSeqProblem, [_seq_problem(q, steps, envs, False) for q in problems])
-    L.call("ppo_lstm_seq_fwd", arr, len(problems), steps, envs, *_sync_args(sync, len(problems), envs), _stream())
+    if proj is None:
+        L.call("ppo_lstm_seq_fwd", arr, len(problems), steps, envs, *_sync_args(sync, len(problems), envs), _stream())
+        return
+    items = []
+    for q, x in zip(problems, proj, strict=True):
+        pk = q["packed"]
+        _dev(x)
+        if x.dim() != 2 or x.shape[0] < steps * envs or x.shape[1] != pk.input_size or x.stride(1) != 1:
+            raise ValueError(f"lstm projection: x {tuple(x.shape)} must be a row-major view of [{steps * envs}, "
+                             f"{pk.input_size}]")
+        items.append(L.LstmInputProjection(x.data_ptr(), x.stride(0), pk.w_ih_g.data_ptr(), pk.b_g.data_ptr(),
+                                           pk.input_size, 0))
+    L.call("ppo_lstm_seq_fwd_proj", arr, L.array(L.LstmInputProjection, items), len(problems), steps, envs,
+           L.GEMM_BF16_OPERANDS if bf16 else 0, *_sync_args(sync, len(problems), envs), _stream())
 
 
 def lstm_seq_bwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor | None = None) -> None:
