@@ -126,7 +126,8 @@ __global__ __launch_bounds__(256) void lstm_unpack_kernel(const GradGroup g) {
   }
 }
 
-// hs[0] = h0 for every problem (rows E, H floats each).
+// hs[0] = h0 for every problem (rows E, H floats each); with a sync buffer, block 0 also clears its words 1 ..
+// sync_words - 1 for the whole-sequence launch that follows (the status word 0 stays).
 struct CopyItem {
   const float* src;
   float* dst;
@@ -136,9 +137,13 @@ struct CopyGroup {
   CopyItem it[PPO_MAX_LSTM_PROBLEMS];
   int32_t count;
   int64_t H, total;
+  int32_t* sync;
+  int32_t sync_words;
 };
 
 __global__ __launch_bounds__(256) void lstm_copy_state_kernel(const CopyGroup g) {
+  if (g.sync != nullptr && blockIdx.x == 0)
+    for (int i = 1 + threadIdx.x; i < g.sync_words; i += blockDim.x) g.sync[i] = 0;
   for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < g.total;
        e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const CopyItem& C = g.it[(g.count > 1 && e >= g.it[1].begin) ? 1 : 0];
@@ -763,10 +768,7 @@ int launch_seq_fwd(SeqFwdArgs& a, int count, hipStream_t s) {
   const int per_slot = count * a.ncb;
   const int slots = std::min(a.nrg, resident / per_slot);
   if (slots < 1) return PPO_EUNSUPPORTED;
-  a.slots = slots;
-  hipLaunchKernelGGL(seq_sync_reset_kernel, dim3(1), dim3(256), 0, s, a.sync,
-                     static_cast<int32_t>(kSyncHeader + count * a.nrg * kSyncStride));
-  if (int rc = check_launch("seq_sync_reset_kernel")) return rc;
+  a.slots = slots;  // (the state-copy launch before this one cleared the sync words)
   hipLaunchKernelGGL((lstm_seq_fwd_kernel<NS, GRU, PROJ>), dim3(count * slots * a.ncb), dim3(256), 0, s, a);
   return check_launch("lstm_seq_fwd_kernel");
 }
@@ -1020,6 +1022,10 @@ int seq_fwd_entry(const ppo_lstm_seq_problem* problems, const ppo_lstm_input_pro
   cg.count = count;
   cg.H = problems[0].hidden;
   cg.total = total;
+  if (sync != nullptr && steps > 1) {  // the counters of the whole-sequence launch, cleared in the same launch
+    cg.sync = sync;
+    cg.sync_words = static_cast<int32_t>(kSyncHeader + count * seq_row_groups(envs) * kSyncStride);
+  }
   hipLaunchKernelGGL(lstm_copy_state_kernel, dim3(grid_for(total)), dim3(256), 0, s, cg);
   if (int rc = check_launch("lstm_copy_state_kernel")) return rc;
   if (fuse) {
