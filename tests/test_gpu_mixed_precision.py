@@ -177,6 +177,9 @@ MP_CASES = {
     "rough235_512": (R.scaled(R.WORKLOADS["rough235"], num_envs=512), {}),
     "flat48_small_fixed": (R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[128, 64, 32]),
                            {"schedule": "fixed"}),
+    # 40 actions: the output layers outside the fused head (their own GEMMs, bf16 operands too, and the loss kernel)
+    "flat48_a40_unfused_fixed": (dict(R.scaled(R.WORKLOADS["flat48"], num_envs=256, steps=8, hidden_dims=[64, 48]),
+                                      num_actions=40), {"schedule": "fixed"}),
     # recurrent: autocast also runs upstream's nn.LSTM / nn.GRU in bf16 (input and recurrent products); the plugin
     # takes bf16 operands in the input projections and the heads, and keeps the recurrent product fp32
     "lstm64_512": (_rnn(512, 16, 64, [64, 32]), {}),
