@@ -547,8 +547,10 @@ typedef struct ppo_lstm_seq_problem {
 /* Synchronisation buffer of the whole-sequence launches: int32 words for `count` problems of `envs` rows (-1 for an
  * invalid count or envs).  Word 0 is a sticky status: the library sets it non-zero when the blocks of a
  * whole-sequence launch stopped waiting for each other (after about 2 s; the outputs of that call are then invalid).
- * The caller zeroes the buffer once and reads word 0 whenever it checks for errors; the library clears the other
- * words itself at the start of every call.  Calls that share a buffer must not overlap. */
+ * The caller zeroes the buffer once and reads word 0 whenever it checks for errors; a call that completes leaves the
+ * other words at zero for the next one (and a forward call clears them before it starts).  After word 0 was found
+ * non-zero the caller zeroes the whole buffer again: a backward call on the words a failed call left returns at
+ * once with invalid outputs (word 0 stays set).  Calls that share a buffer must not overlap. */
 int64_t ppo_lstm_seq_sync_words(int32_t count, int64_t envs);
 
 /* sync = NULL: one launch per step.  sync != NULL (sync_words >= ppo_lstm_seq_sync_words(count, envs)): all steps
@@ -598,6 +600,17 @@ int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, 
 /* The same into torch nn.GRU's layout ([3H, D], [3H, H], [3H], [3H]): the r and z bias gradients go to both biases,
  * slot 2's to b_hn and slot 3's to b_in. */
 int ppo_gru_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream);
+
+/* ppo_lstm_unpack_grads / ppo_gru_unpack_grads that also add the fp64 sums of squares of the torch-layout gradients
+ * they write to the norm_partials of the ppo_linear_bwd_dw_norm call before them on the same stream (problem i's to
+ * group groups[i], 0 .. PPO_MAX_PARAM_GROUPS - 1; each partial row gets at most one addition per problem, in a fixed
+ * order), so one ppo_adam_step_prenorm covers a recurrent model whose weight gradients the GEMM writes in the
+ * gate-interleaved layout.  No counterpart in the reference (upstream's clip_grad_norm_ reads the gradients once
+ * more). */
+int ppo_lstm_unpack_grads_norm(const ppo_lstm_grad_problem* problems, const int32_t* groups, int32_t count,
+                               double* norm_partials, ppo_stream_t stream);
+int ppo_gru_unpack_grads_norm(const ppo_lstm_grad_problem* problems, const int32_t* groups, int32_t count,
+                              double* norm_partials, ppo_stream_t stream);
 
 #ifdef __cplusplus
 }

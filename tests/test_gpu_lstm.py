@@ -159,6 +159,47 @@ def test_gru_sequence_forward_and_backward(cuda, T, E, D, H, one_launch):
         assert int(sync[0]) == 0
 
 
+@pytest.mark.parametrize("gru", [False, True], ids=["lstm", "gru"])
+@pytest.mark.parametrize("D,H,groups", [(48, 256, (0, 1)), (13, 96, (2, 2)), (7, 8, (3,))])
+def test_unpack_grads_norm_adds_the_torch_layout_squares(cuda, D, H, groups, gru):
+    """ppo_lstm_unpack_grads_norm / ppo_gru_unpack_grads_norm write the same gradients as the plain unpack (bit for
+    bit) and add, per parameter group, the fp64 sum of squares of the torch-layout gradients (both biases of the
+    LSTM, the GRU's separate n biases) to the partial rows already there; twice in a row gives the same rows."""
+    from tt_rsl_rl_amd import _lib as L, ops
+
+    dev = cuda
+    gen = torch.Generator().manual_seed(D * 100 + H + gru)
+    G = (3 if gru else 4) * H
+    items, plain = [], []
+    for _ in groups:
+        packed = [torch.randn(4 * H, D, generator=gen).to(dev), torch.randn(4 * H, H, generator=gen).to(dev),
+                  torch.randn(4 * H, generator=gen).to(dev)]
+        out = [torch.full((G, D), float("nan"), device=dev), torch.full((G, H), float("nan"), device=dev),
+               torch.full((G,), float("nan"), device=dev), torch.full((G,), float("nan"), device=dev)]
+        ref = [torch.empty_like(t) for t in out]
+        items.append((*packed, *out))
+        plain.append((*packed, *ref))
+    ops.lstm_unpack_grads(plain, gru=gru)
+    start = torch.rand(L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS, generator=gen, dtype=torch.float64).to(dev)
+    runs = []
+    for _ in range(2):
+        partials = start.clone()
+        ops.lstm_unpack_grads(items, gru=gru, norm=(partials, list(groups)))
+        runs.append(partials)
+    torch.cuda.synchronize()
+    for it, ref in zip(items, plain):
+        for got, want in zip(it[3:], ref[3:]):
+            assert torch.equal(got, want)
+    want = start.sum(0).clone()
+    for grp, it in zip(groups, items):
+        want[grp] += sum(float((t.double() ** 2).sum()) for t in it[3:])
+    got = runs[0].sum(0)
+    assert torch.allclose(got, want, rtol=1e-12, atol=0), (got, want)
+    assert torch.equal(runs[0], runs[1])
+    blocks = min(-(-len(groups) * G * (D + H + 1) // 256), L.DW_NORM_BLOCKS)  # (one launch: at most two problems)
+    assert torch.equal(runs[0][blocks:], start[blocks:])  # rows past the launch's blocks keep their values
+
+
 def _random_sequences(dev, T, E, H, count, seed, gru=False):
     from tt_rsl_rl_amd import ops
 
@@ -199,11 +240,12 @@ def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count, gru
     per_step = [_outputs(q, T, E, H, dev) for q in qs]
     ops.lstm_seq_fwd(per_step, T, E)
     sync = torch.zeros(ops.lstm_seq_sync_words(count, E), dtype=torch.int32, device=dev)
-    for rep in range(2):  # a second call reuses the buffer (the library clears its counters)
+    for rep in range(2):  # a second call reuses the buffer
         one = [_outputs(q, T, E, H, dev) for q in qs]
         ops.lstm_seq_fwd(one, T, E, sync)
         torch.cuda.synchronize()
         assert int(sync[0]) == 0
+        assert int(sync[1]) == 0 and not sync[32::32].any()  # abort word and every row group's counter at zero
         for a, b in zip(per_step, one):
             for k in ("h", "c", "gates"):
                 assert torch.equal(a[k], b[k]), (k, rep)
@@ -215,8 +257,9 @@ def test_one_launch_sequence_matches_per_step_launches(cuda, T, E, H, count, gru
                                          (3, 64, 512, 1), (6, 65, 32, 2)])
 def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count, gru):
     """The whole-sequence backward against one launch per step on the same forward: dgates of every step agree to
-    fp32 rounding (the recurrent product sums its 4H terms in another order), the status word stays clear, and a
-    second call on the same buffer gives the same bits."""
+    fp32 rounding (the recurrent product sums its 4H terms in another order), the status word stays clear, every
+    call leaves the row groups' counters at zero (no clearing launch before the backward), and a second call on the
+    same buffer gives the same bits."""
     from tt_rsl_rl_amd import ops
 
     dev = cuda
@@ -236,6 +279,7 @@ def test_one_launch_backward_matches_per_step_launches(cuda, T, E, H, count, gru
         ops.lstm_seq_bwd(one, T, E, sync)
         torch.cuda.synchronize()
         assert int(sync[0]) == 0
+        assert int(sync[1]) == 0 and not sync[32::32].any()
         for a, b in zip(per_step, one):
             assert torch.isfinite(b["dgates"]).all()
             assert rel_err(b["dgates"], a["dgates"]) < 1e-5, rep

@@ -197,6 +197,15 @@ def test_argument_validation_reports_errors_without_a_gpu():
     grad = _lib.LstmGradProblem(8, 8, 8, 8, 8, 8, 8, 48, 6)
     with pytest.raises(ValueError, match="ppo_gru_unpack_grads: problem 0 sizes"):
         _lib.call("ppo_gru_unpack_grads", ctypes.byref(grad), 1, None)
+    # the norm-writing unpack: partials, a group per problem in range
+    ok_grad = _lib.LstmGradProblem(8, 8, 8, 8, 8, 8, 8, 48, 256)
+    grp = (ctypes.c_int32 * 1)(4)
+    with pytest.raises(ValueError, match="null norm_partials"):
+        _lib.call("ppo_lstm_unpack_grads_norm", ctypes.byref(ok_grad), grp, 1, None, None)
+    with pytest.raises(ValueError, match=r"groups\[0\]=4"):
+        _lib.call("ppo_lstm_unpack_grads_norm", ctypes.byref(ok_grad), grp, 1, 8, None)
+    with pytest.raises(ValueError, match="null groups"):
+        _lib.call("ppo_gru_unpack_grads_norm", ctypes.byref(ok_grad), None, 1, 8, None)
     # the optimiser step: a known kind and a config
     cfg = _lib.OptimConfig(kind=7)
     with pytest.raises(ValueError, match="kind=7"):

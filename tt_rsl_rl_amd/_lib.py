@@ -168,6 +168,10 @@ _SIGNATURES = [
                                         C.c_void_p, i64, C.c_void_p]),
     ("ppo_lstm_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
     ("ppo_gru_unpack_grads", C.c_int, [C.POINTER(LstmGradProblem), i32, C.c_void_p]),
+    ("ppo_lstm_unpack_grads_norm", C.c_int, [C.POINTER(LstmGradProblem), C.POINTER(i32), i32, C.c_void_p,
+                                             C.c_void_p]),
+    ("ppo_gru_unpack_grads_norm", C.c_int, [C.POINTER(LstmGradProblem), C.POINTER(i32), i32, C.c_void_p,
+                                            C.c_void_p]),
     ("ppo_linear_bwd_dx_workspace_bytes", C.c_size_t, [C.POINTER(LinearBwdDxProblem), i32]),
     ("ppo_linear_bwd_dx", C.c_int, [C.POINTER(LinearBwdDxProblem), i32, i64, i32, C.c_void_p, C.c_size_t,
                                     C.c_void_p]),

@@ -68,7 +68,8 @@ __device__ __forceinline__ void add_sq(double (&sq)[PPO_MAX_PARAM_GROUPS], int g
     if (group == k + 1) sq[k] += x;
 }
 
-__global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
+template <int THREADS>
+__global__ __launch_bounds__(THREADS) void dw_reduce_kernel(const ReduceGroup g) {
   double sq[PPO_MAX_PARAM_GROUPS];
 #pragma unroll
   for (int k = 0; k < PPO_MAX_PARAM_GROUPS; ++k) sq[k] = 0.0;
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
         add_sq(sq, g.extra[r].group + 1, x * x);
       }
   }
-  __shared__ double red[256 / 64][PPO_MAX_PARAM_GROUPS];
+  __shared__ double red[THREADS / 64][PPO_MAX_PARAM_GROUPS];
 #pragma unroll
   for (int k = 0; k < PPO_MAX_PARAM_GROUPS; ++k) {
     double x = sq[k];
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const ReduceGroup g) {
   __syncthreads();
   if (threadIdx.x < PPO_MAX_PARAM_GROUPS) {
     double x = 0.0;
-    for (int w = 0; w < 256 / 64; ++w) x += red[w][threadIdx.x];
+    for (int w = 0; w < THREADS / 64; ++w) x += red[w][threadIdx.x];
     g.norm[static_cast<int64_t>(blockIdx.x) * PPO_MAX_PARAM_GROUPS + threadIdx.x] = x;
   }
 }
@@ -728,8 +729,13 @@ int dw_gemm(const ppo_linear_bwd_dw_problem* problems, int32_t count, int64_t ro
     rc = launch_tn<kDwBM, kDwBN, 32, 2, kDwF32BlocksPerCu>(g, count, s, "linear_bwd_dw");
   }
   if (rc != PPO_OK) return rc;
-  const int64_t blocks = norm != nullptr ? PPO_DW_NORM_BLOCKS : std::min<int64_t>(ceil_div(total, 256), 4096);
-  hipLaunchKernelGGL(dw_reduce_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);
+  if (norm != nullptr && total > PPO_DW_NORM_BLOCKS * 256) {
+    // the norm rows fix the block count: wider blocks keep one work item per thread (the LSTMs' weight-grads)
+    hipLaunchKernelGGL(dw_reduce_kernel<1024>, dim3(PPO_DW_NORM_BLOCKS), dim3(1024), 0, s, rg);
+  } else {
+    const int64_t blocks = norm != nullptr ? PPO_DW_NORM_BLOCKS : std::min<int64_t>(ceil_div(total, 256), 4096);
+    hipLaunchKernelGGL(dw_reduce_kernel<256>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, rg);
+  }
   return check_launch("dw_reduce_kernel");
 }
 

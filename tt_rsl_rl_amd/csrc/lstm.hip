@@ -39,36 +39,41 @@ struct PackGroup {
 };
 
 // Flat element e of a problem: [0, 4HD) w_ih_g, [.., +4HH) w_hh_g, [.., +4HH) w_hh_gt, [.., +4H) b_g; each output
-// element is written by exactly one thread (reads are gathers from the torch layout).
+// element is written by exactly one thread (reads are gathers from the torch layout).  32-bit index arithmetic (the
+// host checks that a launch has fewer than 2^31 elements): a 64-bit division is a long subroutine per element.
 __global__ __launch_bounds__(256) void lstm_pack_kernel(const PackGroup g) {
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < g.total;
-       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const PackItem& P = g.it[(g.count > 1 && e >= g.it[1].begin) ? 1 : 0];
-    int64_t k = e - P.begin;
-    const int64_t H = P.H, D = P.D, G = 4 * H;
+  const uint32_t total = static_cast<uint32_t>(g.total), b1 = static_cast<uint32_t>(g.it[1].begin);
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const PackItem& P = g.it[(g.count > 1 && e >= b1) ? 1 : 0];
+    uint32_t k = e - static_cast<uint32_t>(P.begin);
+    const uint32_t H = static_cast<uint32_t>(P.H), D = static_cast<uint32_t>(P.D), G = 4 * H;
     // torch gate of slot q (-1: a zero row).  LSTM: slot q = gate q (i, f, g, o) of both weights.  GRU: slots r, z
     // of both weights, slot 2 = n of w_hh only, slot 3 = n of w_ih only.
-    auto gate_ih = [&](int64_t q) -> int64_t { return P.gru ? (q < 2 ? q : q == 3 ? 2 : -1) : q; };
-    auto gate_hh = [&](int64_t q) -> int64_t { return P.gru ? (q < 3 ? q : -1) : q; };
+    auto gate_ih = [&](uint32_t q) -> int { return P.gru ? (q < 2 ? static_cast<int>(q) : q == 3 ? 2 : -1) : static_cast<int>(q); };
+    auto gate_hh = [&](uint32_t q) -> int { return P.gru ? (q < 3 ? static_cast<int>(q) : -1) : static_cast<int>(q); };
     if (k < G * D) {  // w_ih_g[4u+q][d] = w_ih[gate(q) H + u][d]
-      const int64_t n = k / D, d = k % D, q = gate_ih(n & 3);
+      const uint32_t n = k / D, d = k - n * D;
+      const int q = gate_ih(n & 3);
       P.w_ih_g[k] = q < 0 ? 0.0f : P.w_ih[(q * H + (n >> 2)) * D + d];
       continue;
     }
     k -= G * D;
     if (k < G * H) {  // w_hh_g[4u+q][j] = w_hh[gate(q) H + u][j]
-      const int64_t n = k / H, j = k % H, q = gate_hh(n & 3);
+      const uint32_t n = k / H, j = k - n * H;
+      const int q = gate_hh(n & 3);
       P.w_hh_g[k] = q < 0 ? 0.0f : P.w_hh[(q * H + (n >> 2)) * H + j];
       continue;
     }
     k -= G * H;
     if (k < G * H) {  // w_hh_gt[j][4u+q] = w_hh_g[4u+q][j]
-      const int64_t j = k / G, n = k % G, q = gate_hh(n & 3);
+      const uint32_t j = k / G, n = k - j * G;
+      const int q = gate_hh(n & 3);
       P.w_hh_gt[k] = q < 0 ? 0.0f : P.w_hh[(q * H + (n >> 2)) * H + j];
       continue;
     }
     k -= G * H;  // b_g[4u+q] = b_ih[gate_ih(q) H + u] + b_hh[gate_hh(q) H + u] (a missing gate adds nothing)
-    const int64_t u = k >> 2, qi = gate_ih(k & 3), qh = gate_hh(k & 3);
+    const uint32_t u = k >> 2;
+    const int qi = gate_ih(k & 3), qh = gate_hh(k & 3);
     if (qi >= 0 && qh >= 0) {
       P.b_g[k] = P.b_ih[qi * H + u] + P.b_hh[qh * H + u];
     } else {
@@ -92,37 +97,75 @@ struct GradGroup {
   GradItem it[PPO_MAX_LSTM_PROBLEMS];
   int32_t count;
   int64_t total;
+  double* norm;                          // NORM: [PPO_DW_NORM_BLOCKS][PPO_MAX_PARAM_GROUPS] partial rows, added to
+  int32_t group[PPO_MAX_LSTM_PROBLEMS];  // problem i's parameter group
 };
 
 // Flat element e of a problem: [0, GD) dw_ih, [.., +GH) dw_hh, [.., +G) db_ih and db_hh (torch layout, written once
 // each; G = 4H rows for the LSTM, 3H for the GRU).  The LSTM's bias gradient goes to both b_ih and b_hh; the GRU's n
 // gate has separate input and hidden biases (slots 3 and 2).
+//
+// NORM: the launch has at most PPO_DW_NORM_BLOCKS blocks and block b adds the fp64 sums of squares of the values it
+// wrote (per problem: the thread's elements in order, then a fixed-order block reduction) to row b of the partials
+// the weight-gradient launch before it wrote (problem 0's sum first, then problem 1's), so the optimiser's clip norms
+// cover the torch-layout gradients (each bias gradient of an LSTM counted for both b_ih and b_hh, as torch sees them).
+template <bool NORM>
 __global__ __launch_bounds__(256) void lstm_unpack_kernel(const GradGroup g) {
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < g.total;
-       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const GradItem& P = g.it[(g.count > 1 && e >= g.it[1].begin) ? 1 : 0];
-    int64_t k = e - P.begin;
-    const int64_t H = P.H, D = P.D, G = (P.gru ? 3 : 4) * H;
-    // torch row r = q H + u -> interleaved row 4u + slot
-    auto slot_ih = [&](int64_t r) -> int64_t {
-      const int64_t q = r / H;
-      return 4 * (r % H) + (P.gru && q == 2 ? 3 : q);
+  const uint32_t total = static_cast<uint32_t>(g.total), b1 = static_cast<uint32_t>(g.it[1].begin);
+  double sq[PPO_MAX_LSTM_PROBLEMS] = {};
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const int pi = (g.count > 1 && e >= b1) ? 1 : 0;
+    const GradItem& P = g.it[pi];
+    auto put = [&](float* dst, float v) {
+      *dst = v;
+      if constexpr (NORM) {
+        const double x = static_cast<double>(v) * v;
+        if (pi == 0) sq[0] += x; else sq[1] += x;
+      }
     };
-    auto slot_hh = [&](int64_t r) -> int64_t { return 4 * (r % H) + r / H; };
+    uint32_t k = e - static_cast<uint32_t>(P.begin);
+    const uint32_t H = static_cast<uint32_t>(P.H), D = static_cast<uint32_t>(P.D), G = (P.gru ? 3 : 4) * H;
+    // torch row r = q H + u -> interleaved row 4u + slot
+    auto slot_ih = [&](uint32_t r) -> uint32_t {
+      const uint32_t q = r / H;
+      return 4 * (r - q * H) + (P.gru && q == 2 ? 3 : q);
+    };
+    auto slot_hh = [&](uint32_t r) -> uint32_t {
+      const uint32_t q = r / H;
+      return 4 * (r - q * H) + q;
+    };
     if (k < G * D) {
-      const int64_t r = k / D, d = k % D;
-      P.dw_ih[k] = P.dw_ih_g[slot_ih(r) * D + d];
+      const uint32_t r = k / D, d = k - r * D;
+      put(P.dw_ih + k, P.dw_ih_g[slot_ih(r) * D + d]);
       continue;
     }
     k -= G * D;
     if (k < G * H) {
-      const int64_t r = k / H, j = k % H;
-      P.dw_hh[k] = P.dw_hh_g[slot_hh(r) * H + j];
+      const uint32_t r = k / H, j = k - r * H;
+      put(P.dw_hh + k, P.dw_hh_g[slot_hh(r) * H + j]);
       continue;
     }
     k -= G * H;
-    P.db_ih[k] = P.db_g[slot_ih(k)];
-    P.db_hh[k] = P.db_g[slot_hh(k)];
+    put(P.db_ih + k, P.db_g[slot_ih(k)]);
+    put(P.db_hh + k, P.db_g[slot_hh(k)]);
+  }
+  if constexpr (NORM) {
+    __shared__ double red[256 / 64][PPO_MAX_LSTM_PROBLEMS];
+#pragma unroll
+    for (int p = 0; p < PPO_MAX_LSTM_PROBLEMS; ++p) {
+      double x = sq[p];
+      for (int off = 32; off > 0; off >>= 1) x += __shfl_down(x, off, 64);
+      if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][p] = x;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double* row = g.norm + static_cast<int64_t>(blockIdx.x) * PPO_MAX_PARAM_GROUPS;
+      for (int p = 0; p < g.count; ++p) {
+        double x = 0.0;
+        for (int w = 0; w < 256 / 64; ++w) x += red[w][p];
+        row[g.group[p]] += x;
+      }
+    }
   }
 }
 
@@ -144,11 +187,12 @@ struct CopyGroup {
 __global__ __launch_bounds__(256) void lstm_copy_state_kernel(const CopyGroup g) {
   if (g.sync != nullptr && blockIdx.x == 0)
     for (int i = 1 + threadIdx.x; i < g.sync_words; i += blockDim.x) g.sync[i] = 0;
-  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < g.total;
-       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const CopyItem& C = g.it[(g.count > 1 && e >= g.it[1].begin) ? 1 : 0];
-    const int64_t k = e - C.begin, row = k / g.H, col = k % g.H;
-    C.dst[k] = C.src[row * C.ld_src + col];
+  const uint32_t total = static_cast<uint32_t>(g.total), b1 = static_cast<uint32_t>(g.it[1].begin);
+  const uint32_t H = static_cast<uint32_t>(g.H);
+  for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+    const CopyItem& C = g.it[(g.count > 1 && e >= b1) ? 1 : 0];
+    const uint32_t k = e - static_cast<uint32_t>(C.begin), row = k / H, col = k - row * H;
+    C.dst[k] = C.src[static_cast<int64_t>(row) * C.ld_src + col];
   }
 }
 
@@ -163,8 +207,10 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 // (the usual case, see writers_on_xcd), else with device-scope (sc1) accesses, which the XCDs' separate L2 caches
 // keep coherent; neither needs a whole-cache write-back or invalidate.  After its stores have completed (vmcnt 0) a
 // block adds 1 to the row group's counter (word 0 of the row group's 128-byte line), and before step t a block polls
-// the counter until it reaches ncb t.  The host sizes the grid to the blocks the device holds at once (occupancy query), so the peers of
-// a row group are resident together.  A wait still gives up after kSeqSpinTicks of the 100 MHz real-time clock: it
+// the counter until it reaches ncb t; after its last step a block counts out (seq_count_out), and the last block of
+// the row group to do so zeroes the counter, so a call that completes leaves its counters at zero for the next call
+// (the forward's state-copy launch clears them too).  The host sizes the grid to the blocks the device holds at once
+// (occupancy query), so the peers of a row group are resident together.  A wait still gives up after kSeqSpinTicks of the 100 MHz real-time clock: it
 // sets the sticky status word and the abort word, every block then leaves at its next wait, and the caller sees
 // status != 0 (no hang).
 //
@@ -181,7 +227,7 @@ constexpr int kSeqRows = 64, kSeqCols = 64, kSeqBK = 32;
 constexpr int kSeqMaxSlabs = 8;  // H <= 256: the w_hh_g slice is 64 KB of LDS, two blocks per CU
 constexpr int kSeqProjSlabs = 3;  // fused input projection: inputs of at most 3 16-deep k-slabs (48 columns)
 constexpr int kSyncHeader = 32;  // int32 words ahead of the row-group lines: [0] status (sticky), [1] abort
-constexpr int kSyncStride = 32;  // one 128-byte line per row group: [0] counter, [16 + j] XCD of block j
+constexpr int kSyncStride = 32;  // one 128-byte line per row group: [0] counter, [1 + j] XCD of block j
 constexpr int kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data (gfx9 family)
 constexpr int kDeviceScope = 16;          // buffer-load cache policy: sc1, coherent at device scope
 constexpr uint64_t kSeqSpinTicks = 200000000ull;  // 2 s of the 100 MHz clock (ppo_lstm_seq_wait_limit)
@@ -210,11 +256,6 @@ struct SeqFwdArgs {
   int32_t xcds;  // XCDs of the device (block b runs on XCD b % xcds)
   int32_t bf16;  // fused projection with bf16 operands (PPO_GEMM_BF16_OPERANDS)
 };
-
-// Zeroes the abort word and the counters of one sequence call (the status word stays).
-__global__ __launch_bounds__(256) void seq_sync_reset_kernel(int32_t* sync, int32_t words) {
-  for (int i = 1 + threadIdx.x; i < words; i += blockDim.x) sync[i] = 0;
-}
 
 // Waits until *ctr >= target; every thread of the block returns the same verdict (false: the sequence was aborted).
 // `flag` is an LDS word that no wave touches between the previous workgroup barrier and this one.  The data the
@@ -312,6 +353,17 @@ __device__ __forceinline__ void seq_signal(int32_t* ctr) {
   wait_vmcnt<0>();
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Counts the block out of its row group's pass, after its last wait (only thread 0 reads the counter): one more
+// increment per block on top of the step counts, so the block whose increment brings the counter to `total` (the
+// blocks' T - 1 step counts and one count-out each) comes after every read of the counter in this call, and it
+// zeroes the counter for the next call on the same buffer.  Every wait's target is at most the final step count,
+// which the counter has reached before any block counts out, so the extra increments release no wait early.  A call
+// that gave up leaves its counters as they were (the caller zeroes the buffer after reading a non-zero status).
+__device__ __forceinline__ void seq_count_out(int32_t* ctr, int total) {
+  if (threadIdx.x == 0 && __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1)
+    __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int NS, bool GRU, bool PROJ>
@@ -508,6 +560,7 @@ __global__ __launch_bounds__(256) void lstm_seq_fwd_kernel(const SeqFwdArgs a) {
         *reinterpret_cast<f32x4*>(S.h + rowt * S.ldh + ub) = h4;
       }
     }
+    seq_count_out(line, a.ncb * a.T);
   }
 }
 
@@ -681,6 +734,7 @@ __global__ __launch_bounds__(256) void lstm_seq_bwd_kernel(const SeqBwdArgs a) {
       }
       if (t > 0) seq_signal(line);
     }
+    seq_count_out(line, a.nub * a.T);
     __syncthreads();  // flag_word is reused by the next row group's first wait
   }
 }
@@ -826,9 +880,7 @@ int launch_seq_bwd(SeqBwdArgs& a, int count, hipStream_t s) {
   const int slots = std::min(a.nrg, resident / per_slot);
   if (slots < 1) return PPO_EUNSUPPORTED;
   a.slots = slots;
-  hipLaunchKernelGGL(seq_sync_reset_kernel, dim3(1), dim3(256), 0, s, a.sync,
-                     static_cast<int32_t>(kSyncHeader + count * a.nrg * kSyncStride));
-  if (int rc = check_launch("seq_sync_reset_kernel")) return rc;
+  // (the counters start at zero: a zeroed buffer, or the previous call's count-outs)
   hipLaunchKernelGGL((lstm_seq_bwd_kernel<NS, GRU>), dim3(count * slots * a.nub), dim3(256), 0, s, a);
   return check_launch("lstm_seq_bwd_kernel");
 }
@@ -901,15 +953,27 @@ int pack(const ppo_lstm_pack_problem* problems, int32_t count, bool gru, ppo_str
     P.D = q.input_size; P.H = q.hidden; P.begin = total; P.gru = gru;
     total += 4 * P.H * P.D + 8 * P.H * P.H + 4 * P.H;
   }
+  PPO_REQUIRE(total <= INT32_MAX, "%s: %lld elements (at most 2^31 - 1 per call)", who, (long long)total);
   g.count = count;
   g.total = total;
   hipLaunchKernelGGL(lstm_pack_kernel, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream), g);
   return check_launch("lstm_pack_kernel");
 }
 
-int unpack(const ppo_lstm_grad_problem* problems, int32_t count, bool gru, ppo_stream_t stream, const char* who) {
+int unpack(const ppo_lstm_grad_problem* problems, int32_t count, bool gru, const int32_t* groups, double* norm,
+           ppo_stream_t stream, const char* who) {
   PPO_REQUIRE(problems != nullptr && count >= 1 && count <= PPO_MAX_LSTM_PROBLEMS, "%s: count=%d", who, count);
   GradGroup g{};
+  if (norm != nullptr) {
+    PPO_REQUIRE(groups != nullptr, "%s: null groups", who);
+    PPO_REQUIRE(reinterpret_cast<uintptr_t>(norm) % 8 == 0, "%s: norm_partials must be 8-byte aligned", who);
+    for (int i = 0; i < count; ++i) {
+      PPO_REQUIRE(groups[i] >= 0 && groups[i] < PPO_MAX_PARAM_GROUPS, "%s: groups[%d]=%d (0 .. %d)", who, i,
+                  groups[i], PPO_MAX_PARAM_GROUPS - 1);
+      g.group[i] = groups[i];
+    }
+    g.norm = norm;
+  }
   int64_t total = 0;
   for (int i = 0; i < count; ++i) {
     const ppo_lstm_grad_problem& q = problems[i];
@@ -922,9 +986,16 @@ int unpack(const ppo_lstm_grad_problem* problems, int32_t count, bool gru, ppo_s
     P.D = q.input_size; P.H = q.hidden; P.begin = total; P.gru = gru;
     total += (gru ? 3 : 4) * P.H * (P.D + P.H + 1);
   }
+  PPO_REQUIRE(total <= INT32_MAX, "%s: %lld elements (at most 2^31 - 1 per call)", who, (long long)total);
   g.count = count;
   g.total = total;
-  hipLaunchKernelGGL(lstm_unpack_kernel, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream), g);
+  if (norm != nullptr) {
+    const int64_t blocks = std::min<int64_t>(grid_for(total), PPO_DW_NORM_BLOCKS);
+    hipLaunchKernelGGL(lstm_unpack_kernel<true>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), g);
+  } else {
+    hipLaunchKernelGGL(lstm_unpack_kernel<false>, dim3(grid_for(total)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), g);
+  }
   return check_launch("lstm_unpack_kernel");
 }
 
@@ -940,11 +1011,25 @@ extern "C" int ppo_gru_pack(const ppo_lstm_pack_problem* problems, int32_t count
 }
 
 extern "C" int ppo_lstm_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream) {
-  return unpack(problems, count, false, stream, "ppo_lstm_unpack_grads");
+  return unpack(problems, count, false, nullptr, nullptr, stream, "ppo_lstm_unpack_grads");
 }
 
 extern "C" int ppo_gru_unpack_grads(const ppo_lstm_grad_problem* problems, int32_t count, ppo_stream_t stream) {
-  return unpack(problems, count, true, stream, "ppo_gru_unpack_grads");
+  return unpack(problems, count, true, nullptr, nullptr, stream, "ppo_gru_unpack_grads");
+}
+
+extern "C" int ppo_lstm_unpack_grads_norm(const ppo_lstm_grad_problem* problems, const int32_t* groups, int32_t count,
+                                          double* norm_partials, ppo_stream_t stream) {
+  static const char* who = "ppo_lstm_unpack_grads_norm";
+  PPO_REQUIRE(norm_partials != nullptr, "%s: null norm_partials", who);
+  return unpack(problems, count, false, groups, norm_partials, stream, who);
+}
+
+extern "C" int ppo_gru_unpack_grads_norm(const ppo_lstm_grad_problem* problems, const int32_t* groups, int32_t count,
+                                         double* norm_partials, ppo_stream_t stream) {
+  static const char* who = "ppo_gru_unpack_grads_norm";
+  PPO_REQUIRE(norm_partials != nullptr, "%s: null norm_partials", who);
+  return unpack(problems, count, true, groups, norm_partials, stream, who);
 }
 
 extern "C" int64_t ppo_lstm_seq_sync_words(int32_t count, int64_t envs) {
@@ -1019,6 +1104,7 @@ int seq_fwd_entry(const ppo_lstm_seq_problem* problems, const ppo_lstm_input_pro
     cg.it[i].begin = total;
     total += E * problems[i].hidden;
   }
+  PPO_REQUIRE(total <= INT32_MAX, "%s: %lld state elements (at most 2^31 - 1 per call)", who, (long long)total);
   cg.count = count;
   cg.H = problems[0].hidden;
   cg.total = total;

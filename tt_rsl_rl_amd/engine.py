@@ -713,6 +713,10 @@ class RecurrentUpdateEngine(UpdateEngine):
             self.lstm_sync = torch.zeros(ops.lstm_seq_sync_words(2, self.E_max), dtype=torch.int32,
                                          device=self.device)
             self._status_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        # one clip + optimiser launch (prenorm): the weight-grad launch of the recurrent layers and heads writes the
+        # norm partials of the heads' gradients and the extra ranges, the gradient unpack adds the recurrent layers'.
+        # Only with the one-launch sequences, where the heads' weight-grads share that launch
+        self.rnn_norm = self._recurrent_norm_plan() if self.lstm_sync is not None else None
         # row order of the table: per env slice, t-major
         order = []
         idx = torch.arange(self.T * self.N).view(self.T, self.N)
@@ -722,6 +726,39 @@ class RecurrentUpdateEngine(UpdateEngine):
         self.order = torch.cat(order).to(self.device)
 
     recurrent = True
+
+    def _recurrent_norm_plan(self) -> dict | None:
+        """The clip norms from the weight-grad launch and the gradient unpack (one optimiser launch), when that one
+        launch holds both weight-grads of every recurrent layer and every head layer, and the remaining gradients
+        (the std parameter) fit as extra ranges; else None (the optimiser computes the norms itself)."""
+        alg, f = self.alg, self.alg.flat
+        la, lc = self._layers()
+        n_rnn = len(self.lay_a) + len(self.lay_c)
+        if 2 * n_rnn + len(la) + len(lc) > L.MAX_LINEAR_PROBLEMS or any(lin.bias is None for lin in (*la, *lc)):
+            return None
+        bounds = f.group_begin.tolist()
+        if len(bounds) - 1 > L.MAX_PARAM_GROUPS:
+            return None
+        group = lambda off: max(i for i in range(len(bounds) - 1) if bounds[i] <= off)  # noqa: E731
+        covered = {id(p) for lin in (*la, *lc) for p in (lin.weight, lin.bias)}
+        rnn = {}
+        for m, lays in ((alg.actor, self.lay_a), (alg.critic, self.lay_c)):
+            for b in lays:
+                ps = m.rnn.layer_weights(b.layer)
+                covered |= {id(p) for p in ps}
+                gs = {group(f.offsets[id(p)][0]) for p in ps}
+                if len(gs) != 1:
+                    return None
+                rnn[id(b)] = gs.pop()
+        extra = []
+        for p in f.params:
+            if id(p) not in covered and p.requires_grad:
+                off, k = f.offsets[id(p)]
+                extra.append((off, off + k, group(off)))
+        if len(extra) > L.MAX_EXTRA_GRADS:
+            return None
+        head = [group(f.offsets[id(lin.weight)][0]) for lin in (*la, *lc)]
+        return {"partials": ops.grad_norm_partials(self.device), "head": head, "extra": tuple(extra), "rnn": rnn}
 
     def max_rows(self) -> int:
         return self.T * self.E_max
@@ -872,13 +909,17 @@ class RecurrentUpdateEngine(UpdateEngine):
             for _, _, b, x in row:
                 dw.append((b.dgates[:R], b.hs[:R], b.dw_hh_g, b.db_g))
                 dw.append((b.dgates[:R], x, b.dw_ih_g, None))  # same operand dgates: its column sums once
-        self.weight_grads(dw + head_dw, R, "lstm_dw")
+        rn = self.rnn_norm
+        norm = None if rn is None else ops.GradNorm(rn["partials"], [None] * len(dw) + rn["head"], alg.flat.grad,
+                                                    rn["extra"])
+        self.weight_grads(dw + head_dw, R, "lstm_dw", norm=norm)
         grad = alg.flat.grad_view
         for gru in (False, True):
-            items = [(b.dw_ih_g, b.dw_hh_g, b.db_g, *(grad(p) for p in m.rnn.layer_weights(b.layer)))
-                     for m, b in packs if b.gru == gru]
+            sel = [(m, b) for m, b in packs if b.gru == gru]
+            items = [(b.dw_ih_g, b.dw_hh_g, b.db_g, *(grad(p) for p in m.rnn.layer_weights(b.layer))) for m, b in sel]
             if items:
-                ops.lstm_unpack_grads(items, gru=gru)
+                ops.lstm_unpack_grads(items, gru=gru,
+                                      norm=None if rn is None else (rn["partials"], [rn["rnn"][id(b)] for _, b in sel]))
         if self.lstm_sync is None:
             main.wait_stream(self.side)
-        self.adam(step)
+        self.adam(step, prenorm=None if rn is None else rn["partials"])

@@ -806,9 +806,20 @@ def lstm_seq_bwd(problems: list[dict], steps: int, envs: int, sync: torch.Tensor
     L.call("ppo_lstm_seq_bwd", arr, len(problems), steps, envs, *_sync_args(sync, len(problems), envs), _stream())
 
 
-def lstm_unpack_grads(items: list[tuple], gru: bool = False) -> None:
+def lstm_unpack_grads(items: list[tuple], gru: bool = False, norm: tuple | None = None) -> None:
     """items: (dw_ih_g [4H, D], dw_hh_g [4H, H], db_g [4H], dw_ih, dw_hh, db_ih, db_hh (torch layout views: 4H rows,
-    or 3H with gru, ppo_gru_unpack_grads)), any number (launches of up to MAX_LSTM_PROBLEMS each)."""
+    or 3H with gru, ppo_gru_unpack_grads)), any number (launches of up to MAX_LSTM_PROBLEMS each).  norm =
+    (partials, groups): also add the sums of squares of the written gradients, item i's to parameter group groups[i],
+    to the norm partials of the weight-grad launch before (ppo_lstm_unpack_grads_norm / ppo_gru_unpack_grads_norm)."""
+    if norm is not None:
+        partials, groups = norm
+        _dev(partials, dtype=torch.float64)
+        if (partials.dtype != torch.float64 or tuple(partials.shape) != (L.DW_NORM_BLOCKS, L.MAX_PARAM_GROUPS)
+                or not partials.is_contiguous()):
+            raise ValueError("lstm_unpack_grads: norm partials must be contiguous float64 [DW_NORM_BLOCKS, "
+                             "MAX_PARAM_GROUPS]")
+        if len(groups) != len(items):
+            raise ValueError("lstm_unpack_grads: one parameter group per item")
     probs = []
     for dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh in items:
         _dev(dw_ih_g, dw_hh_g, db_g, dw_ih, dw_hh, db_ih, db_hh)
@@ -824,4 +835,9 @@ def lstm_unpack_grads(items: list[tuple], gru: bool = False) -> None:
     name = "ppo_gru_unpack_grads" if gru else "ppo_lstm_unpack_grads"
     for i in range(0, len(probs), L.MAX_LSTM_PROBLEMS):
         part = probs[i:i + L.MAX_LSTM_PROBLEMS]
-        L.call(name, L.array(L.LstmGradProblem, part), len(part), _stream())
+        if norm is None:
+            L.call(name, L.array(L.LstmGradProblem, part), len(part), _stream())
+        else:
+            import ctypes
+            grp = (ctypes.c_int32 * len(part))(*norm[1][i:i + L.MAX_LSTM_PROBLEMS])
+            L.call(name + "_norm", L.array(L.LstmGradProblem, part), grp, len(part), norm[0].data_ptr(), _stream())
