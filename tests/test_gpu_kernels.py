@@ -788,19 +788,22 @@ def test_fused_head_matches_autograd_and_the_separate_launches(cuda, rows, A, ka
         lo, hi, st = 1e-6, 1e6, L.PPO_STD_SCALAR
     buf = lambda w: torch.full((rows, pad(w)), float("nan"), device=cuda)[:, :w]
 
-    def run(fused):
+    def run(fused, reps=1):
         mean, value = buf(A), buf(1)
         d_mean, d_value = buf(A), buf(1)
         dz_a, dz_c = buf(ka), buf(kc)
         d_param = torch.empty(A, device=cuda)
         state = ops.new_device_state(1e-3, cuda)
-        trace = torch.zeros(5, dtype=torch.float64, device=cuda)
+        trace = torch.zeros(5 * reps, dtype=torch.float64, device=cuda)
         args = ops.make_loss_args(rows, mean, value[:, 0], batch, param, st, lo, hi, 0.2, 1.0, 0.01, clipped, d_mean,
                                   d_value[:, 0])
         if fused:
             ws = torch.empty(ops.head_workspace_bytes(rows, A), dtype=torch.uint8, device=cuda)
-            ops.ppo_head(args, dv["h_a"], dv["w_a"], dv["b_a"], dv["h_c"], dv["w_c"], dv["b_c"], dz_a, dz_c, ws,
-                         d_param, state, True, 0.01, trace, mean=mean, value=value[:, 0])
+            for _ in range(reps):  # (the same state: one mini-batch after another)
+                ops.ppo_head(args, dv["h_a"], dv["w_a"], dv["b_a"], dv["h_c"], dv["w_c"], dv["b_c"], dz_a, dz_c, ws,
+                             d_param, state, True, 0.01, trace, mean=mean, value=value[:, 0])
+            torch.cuda.synchronize()
+            assert ops.read_device_state(state).num_minibatches == reps
         else:
             ops.linear_fwd([(dv["h_a"], dv["w_a"], dv["b_a"], mean, None), (dv["h_c"], dv["w_c"], dv["b_c"], value,
                                                                              None)], rows, elu=False)
@@ -814,6 +817,17 @@ def test_fused_head_matches_autograd_and_the_separate_launches(cuda, rows, A, ka
                     d_param=d_param, trace=trace.cpu().tolist())
 
     got, sep = run(True), run(False)
+    # three calls in a row on one state give the same losses and gradients each time, and the learning rate follows
+    # the rule from call to call
+    again = run(True, reps=3)
+    for key in ("d_mean", "dz_a", "dz_c", "d_param"):
+        assert torch.equal(again[key], got[key]), key
+    lr = 1e-3
+    for i in range(3):
+        row = again["trace"][5 * i:5 * i + 5]
+        assert row[0] == got["trace"][0] and row[2:] == got["trace"][2:], i
+        lr = O.adaptive_lr(torch.tensor(row[0], dtype=torch.float32), lr, 0.01)
+        assert row[1] == lr, i
     for key in ("mean", "value"):
         assert rel_err(got[key], ref[key]) < 2e-6, key
     # gradients: fp32 noise of the fp64 truth (the loss-gradient bar), and the separate launches' within the same
