@@ -109,8 +109,8 @@ struct GradGroup {
 // wrote (per problem: the thread's elements in order, then a fixed-order block reduction) to row b of the partials
 // the weight-gradient launch before it wrote (problem 0's sum first, then problem 1's), so the optimiser's clip norms
 // cover the torch-layout gradients (each bias gradient of an LSTM counted for both b_ih and b_hh, as torch sees them).
-template <bool NORM>
-__global__ __launch_bounds__(256) void lstm_unpack_kernel(const GradGroup g) {
+template <bool NORM, int THREADS = 256>
+__global__ __launch_bounds__(THREADS) void lstm_unpack_kernel(const GradGroup g) {
   const uint32_t total = static_cast<uint32_t>(g.total), b1 = static_cast<uint32_t>(g.it[1].begin);
   double sq[PPO_MAX_LSTM_PROBLEMS] = {};
   for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void lstm_unpack_kernel(const GradGroup g) {
     put(P.db_hh + k, P.db_g[slot_hh(k)]);
   }
   if constexpr (NORM) {
-    __shared__ double red[256 / 64][PPO_MAX_LSTM_PROBLEMS];
+    __shared__ double red[THREADS / 64][PPO_MAX_LSTM_PROBLEMS];
 #pragma unroll
     for (int p = 0; p < PPO_MAX_LSTM_PROBLEMS; ++p) {
       double x = sq[p];
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256) void lstm_unpack_kernel(const GradGroup g) {
       double* row = g.norm + static_cast<int64_t>(blockIdx.x) * PPO_MAX_PARAM_GROUPS;
       for (int p = 0; p < g.count; ++p) {
         double x = 0.0;
-        for (int w = 0; w < 256 / 64; ++w) x += red[w][p];
+        for (int w = 0; w < THREADS / 64; ++w) x += red[w][p];
         row[g.group[p]] += x;
       }
     }
@@ -989,9 +989,13 @@ int unpack(const ppo_lstm_grad_problem* problems, int32_t count, bool gru, const
   PPO_REQUIRE(total <= INT32_MAX, "%s: %lld elements (at most 2^31 - 1 per call)", who, (long long)total);
   g.count = count;
   g.total = total;
-  if (norm != nullptr) {
-    const int64_t blocks = std::min<int64_t>(grid_for(total), PPO_DW_NORM_BLOCKS);
-    hipLaunchKernelGGL(lstm_unpack_kernel<true>, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), g);
+  if (norm != nullptr && total > PPO_DW_NORM_BLOCKS * 256) {
+    // the norm rows cap the block count: wider blocks keep about one element per thread
+    hipLaunchKernelGGL((lstm_unpack_kernel<true, 1024>), dim3(PPO_DW_NORM_BLOCKS), dim3(1024), 0,
+                       static_cast<hipStream_t>(stream), g);
+  } else if (norm != nullptr) {
+    hipLaunchKernelGGL(lstm_unpack_kernel<true>, dim3(grid_for(total)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), g);
   } else {
     hipLaunchKernelGGL(lstm_unpack_kernel<false>, dim3(grid_for(total)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), g);
