@@ -51,10 +51,11 @@ def test_sample_is_a_standard_normal_scaled():
     assert torch.equal(a, b) and torch.equal(st_a, torch.get_rng_state())
 
 
+@pytest.mark.parametrize("first_on_worker", [False, True], ids=["first_here", "first_on_worker"])
 @pytest.mark.parametrize("n,split,normals", [(98304, 24576, [24576 * 29] * 20),
                                              (1000, 250, [250 * 12, 3, 250 * 12, 7, 250 * 12]),
                                              (0, 0, [1024 * 24 * 12] * 20)])
-def test_update_draws_match_upstream_order(n, split, normals):
+def test_update_draws_match_upstream_order(n, split, normals, first_on_worker):
     """randperm(n) then one discarded sample per mini-batch (sizes in order; tiny ones included), as upstream's update
     draws them, against torch doing exactly that."""
     def upstream():
@@ -68,7 +69,7 @@ def test_update_draws_match_upstream_order(n, split, normals):
     st_ref = torch.get_rng_state()
     torch.manual_seed(5)
     out = torch.empty(n, dtype=torch.int64) if n else None
-    job = ops.SplitRandperm(n, out, split, normals)
+    job = ops.SplitRandperm(n, out, split, normals, first_on_worker=first_on_worker)
     p = job.join()
     assert torch.equal(st_ref, torch.get_rng_state())
     if n:

@@ -283,12 +283,13 @@ def test_host_randperm_is_torch_randperm(seed, n, pre):
     assert torch.equal(torch.rand(4), ref_next)
 
 
+@pytest.mark.parametrize("first_on_worker", [False, True], ids=["first_here", "first_on_worker"])
 @pytest.mark.parametrize("n, split", [(98304, 24576), (1000, 0), (1000, 999), (1000, 5000), (2, 1), (1, 0),
                                       (1572864, 393216)])
-def test_split_randperm_is_torch_randperm(n, split):
-    """The permutation drawn in two pieces (the first mini-batch's positions, then the rest on a worker thread)
-    equals torch.randperm(n) and leaves the generator where torch.randperm leaves it; positions [0, split) are
-    already final after the first piece."""
+def test_split_randperm_is_torch_randperm(n, split, first_on_worker):
+    """The permutation drawn in two pieces (the first mini-batch's positions, on the calling thread or ahead of the
+    rest on the worker thread, then the rest on the worker) equals torch.randperm(n) and leaves the generator where
+    torch.randperm leaves it; positions [0, split) are final after the first piece."""
     from tt_rsl_rl_amd import ops
 
     torch.manual_seed(n + split)
@@ -298,7 +299,8 @@ def test_split_randperm_is_torch_randperm(n, split):
     ref_state, ref_next = torch.get_rng_state(), torch.rand(4)
     torch.set_rng_state(start)
     out = torch.empty(n, dtype=torch.int64)
-    sh = ops.SplitRandperm(n, out, split)
+    sh = ops.SplitRandperm(n, out, split, first_on_worker=first_on_worker)
+    sh.wait_first()
     k = sh.split
     assert torch.equal(out[:k], ref[:k]), "the first piece's positions must be final"
     got = sh.join()
@@ -306,6 +308,31 @@ def test_split_randperm_is_torch_randperm(n, split):
     assert torch.equal(torch.get_rng_state(), ref_state)
     assert torch.equal(torch.rand(4), ref_next)
     sh.join()  # idempotent
+
+
+@pytest.mark.parametrize("first_on_worker", [False, True], ids=["first_here", "first_on_worker"])
+def test_split_randperm_falls_back_to_torch_on_an_unknown_generator_record(monkeypatch, first_on_worker):
+    """A generator record this library does not read (here: one byte longer) leaves the whole draw to torch itself:
+    the permutation and the samples after it are torch's, from the same generator state."""
+    from tt_rsl_rl_amd import ops
+
+    n, split, normals = 5000, 1000, [7, 40]
+    torch.manual_seed(3)
+    start = torch.get_rng_state()
+    ref = torch.randperm(n)
+    for k in normals:
+        torch.randn(k)
+    ref_state = torch.get_rng_state()
+    torch.set_rng_state(start)
+    real = torch.get_rng_state
+    monkeypatch.setattr(torch, "get_rng_state", lambda: torch.cat([real(), torch.zeros(1, dtype=torch.uint8)]))
+    out = torch.empty(n, dtype=torch.int64)
+    sh = ops.SplitRandperm(n, out, split, normals, first_on_worker=first_on_worker)
+    sh.wait_first()
+    assert sh.split == n
+    assert torch.equal(sh.join(), ref)
+    monkeypatch.undo()
+    assert torch.equal(torch.get_rng_state(), ref_state)
 
 
 def test_split_randperm_calls_on_rest_once_the_rest_is_final():

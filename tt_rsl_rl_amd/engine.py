@@ -253,12 +253,15 @@ class UpdateEngine:
         """Copy the normalisers' current statistics (device to device, on the stream) for this update's gather, so
         the normaliser update (upstream runs it after the epochs, ppo.py:327-330) can be launched first and run
         while the host draws the permutation."""
+        dsts, srcs = [], []
         for model in (self.alg.actor, self.alg.critic):
             if model.obs_normalization:
                 norm = model.obs_normalizer
                 mean, std = self._norm_frozen[id(norm)]
-                mean.copy_(norm._mean.view(-1))
-                std.copy_(norm._std.view(-1))
+                dsts += [mean, std]
+                srcs += [norm._mean.view(-1), norm._std.view(-1)]
+        if dsts:
+            torch._foreach_copy_(dsts, srcs)
         self._frozen = True
 
     def _norm_stats(self, norm) -> tuple[torch.Tensor, torch.Tensor]:

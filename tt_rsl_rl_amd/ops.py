@@ -139,12 +139,14 @@ class SplitRandperm:
     elements.  n = 0: no permutation (the recurrent update).  ``join()`` waits and writes the generator state back;
     between ``__init__`` and ``join()`` nothing else may draw from the CPU generator.  The permutation and the final
     generator state are bit-identical to torch's.  A generator record of an unexpected layout falls back to torch
-    itself."""
+    itself.  ``first_on_worker``: iterations [0, split) run on the worker too, ahead of the rest, so the caller can do
+    other work first; ``wait_first()`` then waits until positions [0, split) are final (and ``split`` is n after a
+    fallback to torch)."""
 
     _pool = None
 
     def __init__(self, n: int, out: torch.Tensor | None, split: int, normals: list[int] | tuple = (),
-                 on_rest=None) -> None:
+                 on_rest=None, first_on_worker: bool = False) -> None:
         import ctypes
 
         if n > 0 and (out is None or out.dtype != torch.int64 or out.device.type != "cpu" or out.numel() != n
@@ -155,28 +157,66 @@ class SplitRandperm:
         self.split = max(0, min(int(split), n - 1)) if n > 0 else 0
         self._rec = bytearray(torch.get_rng_state().numpy().tobytes())
         self._buf = (ctypes.c_uint8 * len(self._rec)).from_buffer(self._rec)
-        self._perm_future = self._future = None
+        self._perm_future = self._future = self._first_future = None
+        self._first_error = None  # (first_on_worker) the first range's error: the record is not one this library reads
+        if n > 0 and first_on_worker:
+            pool = self._worker()
+            self._first_future = pool.submit(self._perm_first)
+            if self.split < n - 1:
+                self._perm_future = pool.submit(self._perm_rest)
+            if self.normals:
+                self._future = pool.submit(self._skips)
+            return
         lib = L.load()
         if n > 0 and lib.ppo_host_randperm_range(self._buf, len(self._rec), n, 0, self.split,
                                                  out.data_ptr()) != L.PPO_OK:
-            out.copy_(torch.randperm(n))
-            for k in self.normals:
-                torch.randn(k)
-            self._rec = None
-            self.split = n
+            self._torch_fallback()
             return
         if (n > 0 and self.split < n - 1) or self.normals:
-            if SplitRandperm._pool is None:
-                from concurrent.futures import ThreadPoolExecutor
-
-                SplitRandperm._pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="ppo-host-rng")
+            pool = self._worker()
             # one worker: the skips run after the permutation's rest, in stream order
             if n > 0 and self.split < n - 1:
-                self._perm_future = SplitRandperm._pool.submit(self._perm_rest)
+                self._perm_future = pool.submit(self._perm_rest)
             if self.normals:
-                self._future = SplitRandperm._pool.submit(self._skips)
+                self._future = pool.submit(self._skips)
+
+    @staticmethod
+    def _worker():
+        if SplitRandperm._pool is None:
+            from concurrent.futures import ThreadPoolExecutor
+
+            SplitRandperm._pool = ThreadPoolExecutor(max_workers=1, thread_name_prefix="ppo-host-rng")
+        return SplitRandperm._pool
+
+    def _torch_fallback(self) -> None:
+        """torch itself draws the permutation and the samples (a generator record this library does not read)."""
+        self.out.copy_(torch.randperm(self.n))
+        for k in self.normals:
+            torch.randn(k)
+        self._rec = None
+        self.split = self.n
+
+    def _perm_first(self) -> None:
+        if L.load().ppo_host_randperm_range(self._buf, len(self._rec), self.n, 0, self.split,
+                                            self.out.data_ptr()) != L.PPO_OK:
+            self._first_error = L.last_error()
+
+    def wait_first(self) -> None:
+        """(first_on_worker) Wait until positions [0, split) of the permutation are final."""
+        if self._first_future is None:
+            return
+        self._first_future.result()
+        self._first_future = None
+        if self._first_error is not None:  # the queued rest and skips returned at once: torch draws everything
+            for f in (self._perm_future, self._future):
+                if f is not None:
+                    f.result()
+            self._perm_future = self._future = None
+            self._torch_fallback()
 
     def _perm_rest(self) -> str | None:
+        if self._first_error is not None:
+            return None
         rc = L.load().ppo_host_randperm_range(self._buf, len(self._rec), self.n, self.split, self.n - 1,
                                               self.out.data_ptr())
         if rc != L.PPO_OK:
@@ -189,6 +229,8 @@ class SplitRandperm:
         import ctypes
 
         lib = L.load()
+        if self._first_error is not None:
+            return None  # (wait_first() hands everything to torch)
         if self._perm_future is not None and self._perm_future.result() is not None:
             return None  # the permutation failed: reported by join()
         pending = 0
@@ -220,6 +262,8 @@ class SplitRandperm:
 
     def join(self) -> torch.Tensor | None:
         errs = []
+        if self._first_future is not None:
+            self.wait_first()
         for f in (self._perm_future, self._future):
             if f is not None:
                 e = f.result()

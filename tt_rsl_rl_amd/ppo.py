@@ -300,35 +300,16 @@ class PPO:
         if st.distribution_params is None:
             raise RuntimeError("update() called before any transition was stored")
         engine = self._get_engine()
-        # every update starts from a copy of the state it changes (parameters, Adam moments, normaliser statistics),
-        # so an update that fails -- an error raised while its launches are issued, or a device-side failure the
-        # read-back reports (the recurrent one-launch sequences) -- leaves the algorithm as it was
-        self._save_state()
-        # the staging buffer's previous copy (one update ago) completed at that update's read-back
-        ops.reset_device_state(self.device_state, self.learning_rate, self._reset_host)
-        # The normaliser update (upstream: after the epochs, ppo.py:327-330) reads only the stored raw observations;
-        # launched first, on the frozen pre-update statistics the gather uses, it runs while the host draws the
-        # permutation.  The epochs see the same statistics as upstream's.
-        engine.freeze_normalizers()
-        obs = st.observations
-        self.actor.update_normalization(obs)
-        self.critic.update_normalization(obs)
         # feed-forward: one permutation of the batch for all epochs (ppo.py:207, rollout_storage.py:210-260);
         # recurrent: fixed env slices, no permutation drawn (rollout_storage.py:262-331).  Then the samples upstream's
         # stochastic forward draws and discards, one [rows, A] Normal sample per mini-batch (mlp_model.py:103-106 via
         # ppo.py:228-233): skipped on the CPU generator by the same worker, beside the GPU update
         discards = engine.discard_sizes() if self.rng_stream == "cpu" else []
         perm, ready, rest, shuffle = None, None, None, None
-        if self.is_recurrent:
-            if discards:
-                shuffle = ops.SplitRandperm(0, None, 0, discards)
-        else:
+        if not self.is_recurrent:
             if self._perm_host is None or self._perm_host.numel() != B:
                 self._perm_host = torch.empty(B, dtype=torch.int64, pin_memory=True)
                 self._perm_dev = torch.empty(B, dtype=torch.int64, device=self.device)
-            # torch.randperm(B) on the CPU generator, computed natively (same permutation, same generator state):
-            # the first mini-batch's positions now, the rest on a worker thread while its kernels are enqueued
-            ready = engine.minibatch_rows(0)[1]
             perm = self._perm_dev
             if self._copy_stream is None:
                 self._copy_stream = torch.cuda.Stream(self.device)  # (default priority)
@@ -340,7 +321,35 @@ class PPO:
                     perm[sp.split:].copy_(host[sp.split:], non_blocking=True)
                     rest_copied.record(copy_stream)
 
-            shuffle = ops.SplitRandperm(B, self._perm_host, ready, discards, on_rest=copy_rest)
+            # torch.randperm(B) on the CPU generator, computed natively (same permutation, same generator state) on a
+            # worker thread from here on: the first mini-batch's positions while this thread copies the state and
+            # launches the normaliser update below (none of which draws from the generator), then the rest while
+            # the first mini-batch's kernels are enqueued
+            shuffle = ops.SplitRandperm(B, self._perm_host, engine.minibatch_rows(0)[1], discards, on_rest=copy_rest,
+                                        first_on_worker=True)
+        try:
+            # every update starts from a copy of the state it changes (parameters, Adam moments, normaliser
+            # statistics), so an update that fails -- an error raised while its launches are issued, or a device-side
+            # failure the read-back reports (the recurrent one-launch sequences) -- leaves the algorithm as it was
+            self._save_state()
+            # the staging buffer's previous copy (one update ago) completed at that update's read-back
+            ops.reset_device_state(self.device_state, self.learning_rate, self._reset_host)
+            # The normaliser update (upstream: after the epochs, ppo.py:327-330) reads only the stored raw
+            # observations; launched first, on the frozen pre-update statistics the gather uses, it runs while the
+            # host draws the permutation.  The epochs see the same statistics as upstream's.
+            engine.freeze_normalizers()
+            obs = st.observations
+            self.actor.update_normalization(obs)
+            self.critic.update_normalization(obs)
+        except BaseException:
+            if shuffle is not None:
+                shuffle.join()
+            raise
+        if self.is_recurrent:
+            if discards:
+                shuffle = ops.SplitRandperm(0, None, 0, discards)
+        else:
+            shuffle.wait_first()
             ready = shuffle.split if shuffle.split < B - 1 else B
             perm[:ready].copy_(self._perm_host[:ready], non_blocking=True)
             if ready < B:
@@ -400,13 +409,14 @@ class PPO:
             saved = self._saved = {
                 "flat": [torch.empty_like(t) for t in (f.param, f.exp_avg, f.exp_avg_sq)],
                 "norms": [(n, {k: torch.empty_like(v) for k, v in n.state_dict().items()}, [0]) for n in norms]}
-        with torch.no_grad():
-            for dst, src in zip(saved["flat"], (f.param, f.exp_avg, f.exp_avg_sq)):
-                dst.copy_(src)
+        with torch.no_grad():  # (grouped copies: fewer launches and less host time ahead of the first gather)
+            dsts, srcs = list(saved["flat"]), [f.param, f.exp_avg, f.exp_avg_sq]
             for norm, bufs, host_count in saved["norms"]:
                 for k, v in bufs.items():
-                    v.copy_(getattr(norm, k))
+                    dsts.append(v)
+                    srcs.append(getattr(norm, k))
                 host_count[0] = norm._host_count
+            torch._foreach_copy_(dsts, srcs)
 
     def _restore_state(self) -> None:
         f = self.flat
