@@ -238,6 +238,13 @@ def test_update_matches_oracle(name, capsys):
 
     # the drop-in update(), with each mini-batch's clip-branch decisions read back
     engine = hip._get_engine()
+    if engine.recurrent:  # one optimiser launch where one weight-grad launch holds every layer's and head's problems
+        n_rnn = len(engine.lay_a) + len(engine.lay_c)
+        n_head = len(hip.actor.linears) + len(hip.critic.linears)
+        from tt_rsl_rl_amd import _lib as L
+
+        fits = engine.lstm_sync is not None and 2 * n_rnn + n_head <= L.MAX_LINEAR_PROBLEMS
+        assert (engine.rnn_norm is not None) == fits, name
     std_param = hip.actor.distribution.param
     rows: list[dict] = []
     quantities: list[dict] = []
