@@ -9,6 +9,7 @@
 // segment widths: each wave derives it once per pass (from a copy of the segment table in LDS) and then moves
 // kRowsPerIter rows per iteration, issuing all their loads before any store so a wave waits for memory once per
 // iteration rather than once per segment.
+#include <atomic>
 #include <cstdlib>
 
 #include "common.hpp"
@@ -37,6 +38,10 @@ constexpr int kGatherThreads = 256;
 constexpr int kWavesPerBlock = kGatherThreads / kWave;
 
 constexpr int kGatherRowsPerIter = 4;
+// Row iterations per wave of gather_rows_vec_kernel at most (measured, gather alone: humanoid's 98,304 rows 54.5 us
+// with one iteration per wave, 49.9 with two, 48.2 with eight; flat48_65k's 1,572,864 rows 413 / 412 / 423 us: an
+// iteration's loads wait for the previous iteration's stores to have read their registers)
+constexpr int64_t kGatherMaxIters = 2;
 
 // kSlots: flat columns per lane per pass (64 kSlots floats of a row; the launcher takes the fewest that cover a row,
 // up to 8); kRowsPerIter: rows whose loads a wave has in flight at once (4: 96 against 105 us with 2 for the humanoid
@@ -140,7 +145,10 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_vec_kernel(const i
   if (threadIdx.x < args.num_segments) seg[threadIdx.x] = args.seg[threadIdx.x];
   __syncthreads();
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+  // (wave-uniform as far as the compiler can see, so the permutation entries below are scalar loads, which wait on
+  // their own counter instead of behind this wave's row stores)
+  const int64_t wave_id = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock +
+                          __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
   const int nv = args.num_vec, ns = args.num_segments;
   const int vtotal = args.vprefix[nv], stotal = args.prefix[ns];
@@ -195,14 +203,26 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_vec_kernel(const i
     den[k] = norm ? g.norm_std[col] + g.norm_eps : 1.0f;
   }
   typedef const f32x4 __attribute__((address_space(1))) global_f32x4;
-  for (int64_t j0 = wave_id * kRowsPerIter; j0 < rows; j0 += wave_count * kRowsPerIter) {
-    int64_t sr[kRowsPerIter];
+  // The grid holds about the blocks the device keeps resident, so a wave walks several iterations; the permutation
+  // entries of its next iteration are loaded right after this iteration's row loads, and an iteration waits for one
+  // memory round trip instead of two (the entry, then the row it names).
+  // (32-bit row indices, rows < 2^30 (the launcher checks): the loop's compares stay scalar, and no vector register
+  // that a row store of the iteration still reads is taken for them)
+  const int rows32 = static_cast<int>(rows), step = static_cast<int>(wave_count) * kRowsPerIter;
+  int64_t pn[kRowsPerIter];
+  auto load_perm = [&](int j0) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < kRowsPerIter; ++r) {
-      const int64_t j = j0 + r;
-      const int64_t p = j < rows ? perm[j] : -1;
-      sr[r] = p >= 0 && p < src_rows ? p : -1;  // never read outside the source (the host checks perm)
+      const int j = j0 + r;
+      pn[r] = j < rows32 ? perm[j] : -1;
     }
+  };
+  load_perm(static_cast<int>(wave_id) * kRowsPerIter);
+  for (int j0 = static_cast<int>(wave_id) * kRowsPerIter; j0 < rows32; j0 += step) {
+    int64_t sr[kRowsPerIter];
+#pragma unroll
+    for (int r = 0; r < kRowsPerIter; ++r)
+      sr[r] = pn[r] >= 0 && pn[r] < src_rows ? pn[r] : -1;  // never read outside the source (the host checks perm)
     f32x4 vv[kRowsPerIter][kV];
     uint32_t word[kRowsPerIter][kS > 0 ? kS : 1];
     int shift[kRowsPerIter][kS > 0 ? kS : 1];
@@ -218,6 +238,8 @@ __global__ __launch_bounds__(kGatherThreads) void gather_rows_vec_kernel(const i
         shift[r][k] = static_cast<int>(a & 3) * 8;
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // (the next entries' loads after the rows', so the wait below skips them)
+    load_perm(j0 + step);
     float v[kRowsPerIter][kS > 0 ? kS : 1];
 #pragma unroll
     for (int r = 0; r < kRowsPerIter; ++r) {
@@ -280,6 +302,27 @@ __global__ __launch_bounds__(256) void interleave_kernel(const InterleaveArgs a,
       if (i < a.num_cols && c >= a.first[i]) b = i;
     dst[static_cast<int64_t>(r) * dst_stride + c] = a.col[b].src[static_cast<int64_t>(r) * a.col[b].stride + (c - a.first[b])];
   }
+}
+
+// Blocks of a gather kernel the current device holds at once (0 when unknown), queried once per instantiation and
+// device.
+template <typename K>
+int64_t resident_gather_blocks(K kernel) {
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kGatherThreads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    v = std::max(per_cu, 0) * std::max(cus, 0) + 1;  // stored + 1: 0 marks "not queried yet"
+    cache[dev].store(v, std::memory_order_relaxed);
+  }
+  return v - 1;
 }
 
 }  // namespace
@@ -377,10 +420,15 @@ extern "C" int ppo_gather_rows(const int64_t* perm, int64_t rows, int64_t src_ro
     va.prefix[num_segments] = static_cast<int32_t>(floats);
     const int kv = static_cast<int>(ceil_div(chunks, static_cast<int64_t>(kWave)));
     const int ks = static_cast<int>(ceil_div(floats, static_cast<int64_t>(kWave)));
-    if (va.num_vec > 0 && kv <= 4 && ks <= 4) {
+    if (va.num_vec > 0 && kv <= 4 && ks <= 4 && rows < (int64_t(1) << 30)) {
       auto gov = [&](auto kernel) {
         constexpr int R = kGatherRowsPerIter;
-        const int64_t blocks = std::min<int64_t>(ceil_div(rows, static_cast<int64_t>(kWavesPerBlock) * R), 65536);
+        // the blocks the device holds at once, or more where a wave would otherwise take more than kGatherMaxIters
+        // iterations
+        const int64_t need = ceil_div(rows, static_cast<int64_t>(kWavesPerBlock) * R);
+        const int64_t res = resident_gather_blocks(kernel);
+        const int64_t blocks = std::min<int64_t>(
+            res > 0 ? std::max<int64_t>(std::min(need, res), ceil_div(need, kGatherMaxIters)) : need, 65536);
         hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kGatherThreads), 0,
                            static_cast<hipStream_t>(stream), perm, rows, src_rows, va, dst, dst_stride);
         return check_launch("gather_rows_vec_kernel");
